@@ -1,0 +1,347 @@
+/* oracle.c — TEST INFRASTRUCTURE ONLY (see oracle.h).
+ *
+ * A scalar restatement of the reference's kernels in their float32 order.  Built with -ffp-contract=off and no
+ * fast-math, so every float operation below is one IEEE binary32 operation rounded to nearest-even, as WebAssembly's
+ * f32 / f32x4 operations are.  Integer sums are computed as the WASM SIMD instructions compute them (including the
+ * int16 pair sums of kernels/kernel/matmul.ts:68-72 and the wrap of i32x4.add in quantize_x).
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdatomic.h>
+#include <string.h>
+#include <time.h>
+
+#define GS 32 /* kernels/kernel/math.ts:4 */
+
+/* ---- helpers ------------------------------------------------------------------------------------------------ */
+
+/* f32x4.max lane semantics: NaN if either operand is NaN, and -0 below +0 (kernels/kernel/quantize.ts:10-19) */
+static float wasm_max(float a, float b) {
+  if (a != a) return a;
+  if (b != b) return b;
+  if (a == b) return signbit(a) ? b : a;
+  return a > b ? a : b;
+}
+
+/* i32x4.trunc_sat_f32x4_s: NaN -> 0, saturating at the int32 ends */
+static int32_t trunc_sat(float v) {
+  if (v != v) return 0;
+  if (v >= 2147483648.0f) return INT32_MAX;
+  if (v <= -2147483648.0f) return INT32_MIN;
+  return (int32_t)v;
+}
+
+static int32_t wrap16(int32_t v) { return (int32_t)(int16_t)(uint16_t)(uint32_t)v; }
+
+/* kernels/kernel/halves.ts:317-326: ((h sign-extended) << 13 & 0x8fffffff) as float, times 2^112 */
+float o_half(uint16_t h) {
+  int32_t bits = ((int32_t)(int16_t)h * 8192) & (int32_t)0x8fffffff;
+  float f;
+  memcpy(&f, &bits, 4);
+  return f * 5.192296858534828e33f;
+}
+
+/* ---- quantize_x: kernels/kernel/quantize.ts:124-151 --------------------------------------------------------- */
+void o_quantize_x(void *xq_, float *xs, const float *x, int32_t n, int32_t bias) {
+  uint8_t *xq = (uint8_t *)xq_;
+  const float qmax = bias == 0 ? 127.0f : 63.0f;
+  for (int32_t g = 0; g < n; g += GS) {
+    /* groupMax (quantize.ts:10-19): lane j holds the max over values 4i + j, then lanes 1..3 compared in order */
+    float m[4];
+    for (int j = 0; j < 4; j++) {
+      float v = fabsf(x[g + j]);
+      for (int i = 1; i < 8; i++) v = wasm_max(v, fabsf(x[g + 4 * i + j]));
+      m[j] = v;
+    }
+    float amax = m[0];
+    if (m[1] > amax) amax = m[1];
+    if (m[2] > amax) amax = m[2];
+    if (m[3] > amax) amax = m[3];
+    const float scale = amax / qmax;
+    xs[g / GS] = scale;
+    const float inv = scale > 0 ? 1.0f / scale : 0.0f;
+    for (int j = 0; j < GS; j++) {
+      const float p = x[g + j] * inv;
+      const int32_t t = trunc_sat(rintf(p));
+      int32_t q = (int32_t)((uint32_t)t + (uint32_t)bias); /* i32x4.add wraps */
+      if (q > 127) q = 127;                                /* narrow i32->i16->i8 with saturation */
+      if (q < -128) q = -128;
+      xq[g + j] = (uint8_t)(int8_t)q;
+    }
+  }
+}
+
+/* ---- corrections: kernels/kernel/matmul.ts:38-58 ------------------------------------------------------------ */
+void o_int8_sums(int32_t *out, const int8_t *w, int32_t groups) {
+  for (int32_t g = 0; g < groups; g++) {
+    int32_t s = 0;
+    for (int j = 0; j < GS; j++) s += w[(int64_t)g * GS + j];
+    out[g] = -64 * s;
+  }
+}
+
+/* kernels/six.ts:1-31, layout of src/python/engine/packing.py:56-70: value j's low nibble in byte j (j < 16) or the
+ * high nibble of byte j - 16; its top two bits at bits 2 (j / 8) of byte 16 + j % 8; the int8 is the six bits << 2 */
+void o_six_unpack(int8_t *out, const uint8_t *p) {
+  for (int j = 0; j < 32; j++) {
+    const int low = j < 16 ? (p[j] & 15) : (p[j - 16] >> 4);
+    const int top = (p[16 + (j & 7)] >> (2 * (j >> 3))) & 3;
+    out[j] = (int8_t)(uint8_t)((low | (top << 4)) << 2);
+  }
+}
+
+void o_six_sums(int32_t *out, const uint8_t *w, int32_t groups) {
+  int8_t v[32];
+  for (int32_t g = 0; g < groups; g++) {
+    o_six_unpack(v, w + (int64_t)g * 24);
+    int32_t s = 0;
+    for (int j = 0; j < 32; j++) s += v[j];
+    out[g] = -64 * s;
+  }
+}
+
+/* ---- interleave: kernels/kernel/matmul.ts:107-146 ----------------------------------------------------------- */
+void o_interleave(int8_t *xq, float *xs, int32_t n) {
+  int32_t *sums = (int32_t *)(xs + (n >> 5));
+  int8_t a[64];
+  for (int32_t b = 0; b < n; b += 64) {
+    memcpy(a, xq + b, 64);
+    int32_t s0 = 0, s1 = 0;
+    for (int j = 0; j < 32; j++) s0 += a[j];
+    for (int j = 32; j < 64; j++) s1 += a[j];
+    sums[(b >> 5)] = -s0;
+    sums[(b >> 5) + 1] = -s1;
+    for (int p = 0; p < 4; p++)
+      for (int c = 0; c < 16; c++) xq[b + 16 * p + c] = a[4 * c + p];
+  }
+}
+
+/* ---- int8 products ------------------------------------------------------------------------------------------ */
+
+/* the group's exact integer sum with the correction in it: relaxed/int8.ts:29-37 (relaxed_dot with activations
+ * 0..127, int8.ts:6-11) */
+static int32_t dot_relaxed(const int8_t *w, const uint8_t *q) {
+  int32_t s = 0;
+  for (int j = 0; j < GS; j++) s += (int32_t)w[j] * (int32_t)q[j];
+  return s;
+}
+
+/* relaxed/int8.ts:17-50 over one row's int8 values (w, ng groups), scales srow, corrections crow */
+static float q8r_row(const int8_t *w, const uint8_t *xq, const float *xs, const float *srow, const int32_t *crow,
+                     int32_t ng) {
+  const int32_t ng4 = ng & ~3;
+  float lane[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  int32_t g = 0;
+  for (; g < ng4; g++) { /* lane g & 3 adds the groups 4j + (g & 3) in order (int8.ts:26-39) */
+    const float s = srow[g] * xs[g];
+    const int32_t d = dot_relaxed(w + g * GS, xq + g * GS) + crow[g];
+    const float p = (float)d * s;
+    lane[g & 3] = lane[g & 3] + p;
+  }
+  float sum = ((lane[0] + lane[1]) + lane[2]) + lane[3]; /* hsum, math.ts:7-9 */
+  for (; g < ng; g++) {                                /* the groups past the fours (int8.ts:41-47) */
+    const int32_t d = dot_relaxed(w + g * GS, xq + g * GS) + crow[g];
+    const float s = srow[g] * xs[g];
+    const float p = (float)d * s;
+    sum = sum + p;
+  }
+  return sum;
+}
+
+void o_matmul_q8r(float *xout, const uint8_t *xq, const float *xs, const int8_t *wq, const float *ws,
+                  const int32_t *wc, int32_t n, int32_t r0, int32_t r1) {
+  const int32_t ng = n / GS;
+  for (int32_t i = r0; i < r1; i++)
+    xout[i] = q8r_row(wq + (int64_t)i * n, xq, xs, ws + (int64_t)i * ng, wc + (int64_t)i * ng, ng);
+}
+
+/* dot32 (kernel/matmul.ts:68-72): lane k holds products 2k, 2k+1, 2k+8, 2k+9 of each 16-byte half, two products
+ * added in int16 first (i16x8.add of the low and high extmuls, which wraps) */
+static void dot32_lanes(int32_t lane[4], const int8_t *w, const int8_t *x) {
+  for (int k = 0; k < 4; k++) {
+    int32_t s = 0;
+    for (int half = 0; half < 32; half += 16) {
+      const int32_t a = wrap16((int32_t)w[half + 2 * k] * x[half + 2 * k] + (int32_t)w[half + 2 * k + 8] * x[half + 2 * k + 8]);
+      const int32_t b = wrap16((int32_t)w[half + 2 * k + 1] * x[half + 2 * k + 1] +
+                               (int32_t)w[half + 2 * k + 9] * x[half + 2 * k + 9]);
+      s += a + b;
+    }
+    lane[k] = s;
+  }
+}
+
+/* kernel/matmul.ts:77-97 over one row's int8 values: each lane times the scales' product into its own float32
+ * lane, group by group; the four lanes added in order at the end */
+static float q8_row(const int8_t *w, const int8_t *xq, const float *xs, const float *srow, int32_t ng) {
+  float lane[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  int32_t d[4];
+  for (int32_t g = 0; g < ng; g++) {
+    const float s = srow[g] * xs[g];
+    dot32_lanes(d, w + g * GS, xq + g * GS);
+    for (int k = 0; k < 4; k++) {
+      const float p = (float)d[k] * s;
+      lane[k] = lane[k] + p;
+    }
+  }
+  return ((lane[0] + lane[1]) + lane[2]) + lane[3];
+}
+
+void o_matmul_q8(float *xout, const int8_t *xq, const float *xs, const int8_t *wq, const float *ws, int32_t n,
+                 int32_t r0, int32_t r1) {
+  const int32_t ng = n / GS;
+  for (int32_t i = r0; i < r1; i++) xout[i] = q8_row(wq + (int64_t)i * n, xq, xs, ws + (int64_t)i * ng, ng);
+}
+
+/* relaxed/int8.ts:147-166: every (row, token) is matmul_q8r's number to the bit (int8.ts:60-65), token t's
+ * activations and scales at xq + t frame, xs + t frame, its outputs at xout + t os */
+void o_matmul_q8r_tile(void *xout, const void *xq, const void *xs, const int8_t *wq, const float *ws,
+                       const int32_t *wc, int32_t n, int32_t r0, int32_t r1, int32_t count, int32_t os,
+                       int32_t frame) {
+  for (int32_t t = 0; t < count; t++)
+    o_matmul_q8r((float *)((char *)xout + (int64_t)t * os), (const uint8_t *)((const char *)xq + (int64_t)t * frame),
+                 (const float *)((const char *)xs + (int64_t)t * frame), wq, ws, wc, n, r0, r1);
+}
+
+/* ---- int6 products: relaxed/six.ts:146-175, kernel/matmul.ts:227-244 ---------------------------------------- */
+void o_matmul_q6r(float *xout, const uint8_t *xq, const float *xs, const uint8_t *wq, const float *ws,
+                  const int32_t *wc, int32_t n, int32_t r0, int32_t r1) {
+  const int32_t ng = n / GS;
+  int8_t row[32 * 2048]; /* rows up to 65536 values: matmul_q8r's order on the widened row */
+  if (ng > 2048) return;
+  for (int32_t i = r0; i < r1; i++) {
+    const uint8_t *packed = wq + (int64_t)i * ng * 24;
+    for (int32_t g = 0; g < ng; g++) o_six_unpack(row + g * GS, packed + g * 24);
+    xout[i] = q8r_row(row, xq, xs, ws + (int64_t)i * ng, wc + (int64_t)i * ng, ng);
+  }
+}
+
+void o_matmul_q6(float *xout, const int8_t *xq, const float *xs, const uint8_t *wq, const float *ws, int32_t n,
+                 int32_t r0, int32_t r1) {
+  const int32_t ng = n / GS;
+  int8_t v[32];
+  int32_t d[4];
+  for (int32_t i = r0; i < r1; i++) {
+    const uint8_t *packed = wq + (int64_t)i * ng * 24;
+    float lane[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int32_t g = 0; g < ng; g++) {
+      o_six_unpack(v, packed + g * 24);
+      dot32_lanes(d, v, xq + g * GS);
+      const float s = ws[(int64_t)i * ng + g] * xs[g];
+      for (int k = 0; k < 4; k++) lane[k] = lane[k] + (float)d[k] * s;
+    }
+    xout[i] = ((lane[0] + lane[1]) + lane[2]) + lane[3];
+  }
+}
+
+/* ---- ternary products: kernels/ternary.ts:54-65, relaxed/signs.ts:185-230 ------------------------------------- */
+
+/* codes(v, p, three) (ternary.ts:56-58): i16x8.shr_u by 2p, then the mask; byte c of a 16-byte vector */
+static int32_t code_of(const uint8_t *v16, int c, int p, int32_t three) {
+  if (p == 0) return v16[c] & three;
+  const int lo = c & ~1;
+  const uint32_t lane = (uint32_t)v16[lo] | ((uint32_t)v16[lo + 1] << 8);
+  const uint32_t shifted = (lane >> (2 * p)) & 0xffff;
+  const uint32_t byte = (c & 1) ? (shifted >> 8) : (shifted & 0xff);
+  return (int32_t)(int8_t)(uint8_t)(byte & (uint32_t)three);
+}
+
+/* one row of matmul_t2r / matmul_t2: lane k adds sub-group k (activations 32k..32k+31) of every group of 128, in
+ * order: f(f(whole * xs) * d) (tests/ternary-check.ts:129-139) */
+static float t2_row(const uint8_t *row, const uint16_t *srow, const int8_t *xq, const float *xs,
+                    const int32_t *sums, int32_t groups, int32_t three) {
+  float lane[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int32_t g = 0; g < groups; g++) {
+    const float d = o_half(srow[g]);
+    for (int k = 0; k < 4; k++) {
+      const int h = k >> 1, s = k & 1;
+      const uint8_t *v = row + (int64_t)g * 32 + 16 * h;
+      const int8_t *x = xq + (int64_t)g * 128 + 64 * h;
+      int32_t dot = 0;
+      for (int p = 0; p < 4; p++)
+        for (int c = 8 * s; c < 8 * s + 8; c++) dot += code_of(v, c, p, three) * (int32_t)x[16 * p + c];
+      const int32_t whole = dot + sums[4 * g + k];
+      const float a = (float)whole * xs[4 * g + k];
+      const float b = a * d;
+      lane[k] = lane[k] + b;
+    }
+  }
+  return ((lane[0] + lane[1]) + lane[2]) + lane[3];
+}
+
+void o_matmul_t2r(float *xout, const int8_t *xq, const float *xs, const uint8_t *wq, const uint16_t *ws,
+                  int32_t n, int32_t r0, int32_t r1, int32_t three) {
+  const int32_t groups = n >> 7;
+  const int32_t *sums = (const int32_t *)(xs + (n >> 5));
+  for (int32_t i = r0; i < r1; i++)
+    xout[i] = t2_row(wq + (int64_t)i * (n >> 2), ws + (int64_t)i * groups, xq, xs, sums, groups, three);
+}
+
+void o_matmul_t2r_tile(void *xout, const void *xq, const void *xs, const uint8_t *wq, const uint16_t *ws,
+                       int32_t n, int32_t r0, int32_t r1, int32_t count, int32_t os, int32_t frame,
+                       int32_t three) {
+  for (int32_t t = 0; t < count; t++)
+    o_matmul_t2r((float *)((char *)xout + (int64_t)t * os), (const int8_t *)((const char *)xq + (int64_t)t * frame),
+                 (const float *)((const char *)xs + (int64_t)t * frame), wq, ws, n, r0, r1, three);
+}
+
+/* ---- CPU baseline: phase()-style row chunks over host threads ------------------------------------------------ */
+typedef struct {
+  int32_t kind;
+  float *xout;
+  const void *xq, *xs, *wq, *ws, *wc;
+  int32_t n, rows, chunk, chunks;
+  atomic_int next;
+} gemv_job;
+
+static void run_rows(gemv_job *j, int32_t r0, int32_t r1) {
+  switch (j->kind) {
+  case 0: o_matmul_q8r(j->xout, j->xq, j->xs, j->wq, j->ws, j->wc, j->n, r0, r1); break;
+  case 1: o_matmul_q8(j->xout, j->xq, j->xs, j->wq, j->ws, j->n, r0, r1); break;
+  case 2: o_matmul_q6r(j->xout, j->xq, j->xs, j->wq, j->ws, j->wc, j->n, r0, r1); break;
+  case 3: o_matmul_q6(j->xout, j->xq, j->xs, j->wq, j->ws, j->n, r0, r1); break;
+  default: o_matmul_t2r(j->xout, j->xq, j->xs, j->wq, j->ws, j->n, r0, r1, 3); break;
+  }
+}
+
+static void *worker(void *arg) {
+  gemv_job *j = (gemv_job *)arg;
+  for (;;) {
+    const int32_t c = atomic_fetch_add(&j->next, 1);
+    if (c >= j->chunks) break;
+    const int32_t r0 = c * j->chunk;
+    const int32_t r1 = r0 + j->chunk < j->rows ? r0 + j->chunk : j->rows;
+    run_rows(j, r0, r1);
+  }
+  return NULL;
+}
+
+static double now_s(void) {
+  struct timespec t;
+  clock_gettime(CLOCK_MONOTONIC, &t);
+  return (double)t.tv_sec + 1e-9 * (double)t.tv_nsec;
+}
+
+double o_time_gemv(int32_t kind, float *xout, const void *xq, const void *xs, const void *wq, const void *ws,
+                   const void *wc, int32_t n, int32_t rows, int32_t threads, int32_t reps) {
+  if (threads < 1) threads = 1;
+  if (threads > 256) threads = 256;
+  pthread_t tid[256];
+  double best = 1e30;
+  for (int32_t r = 0; r < reps; r++) {
+    gemv_job j = {kind, xout, xq, xs, wq, ws, wc, n, rows, 0, 0, 0};
+    int32_t want = threads * 4; /* CHUNKS_PER_THREAD, threads.ts:45 */
+    j.chunk = (rows + want - 1) / want;
+    if (j.chunk < 1) j.chunk = 1;
+    j.chunks = (rows + j.chunk - 1) / j.chunk;
+    atomic_init(&j.next, 0);
+    const double t0 = now_s();
+    for (int32_t t = 1; t < threads; t++) pthread_create(&tid[t], NULL, worker, &j);
+    worker(&j);
+    for (int32_t t = 1; t < threads; t++) pthread_join(tid[t], NULL);
+    const double dt = now_s() - t0;
+    if (dt < best) best = dt;
+  }
+  return best;
+}

@@ -1,0 +1,67 @@
+/* oracle.h — TEST INFRASTRUCTURE ONLY.
+ *
+ * A scalar C restatement of the reference's quantized-matmul arithmetic (takano32/pyodide-llm, kernels/ .ts files),
+ * in the reference's own float32 order, used as the parity checker for the HIP library and as the timed CPU
+ * baseline ("port").  Nothing on the product path may link, load or call it: only tests/, the smoke check of
+ * __graft_entry__.py and bench.py's cpu_baseline leg do.
+ *
+ * Each function names the reference lines it follows.  Pointers are host pointers; byte strides (os, frame) are
+ * bytes, as in the reference.  Every function is reentrant and touches only the rows / tokens it is given.
+ */
+#ifndef HQ_ORACLE_H
+#define HQ_ORACLE_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* kernels/kernel/quantize.ts:124-151 */
+void o_quantize_x(void *xq, float *xs, const float *x, int32_t n, int32_t bias);
+/* kernels/kernel/matmul.ts:50-58 */
+void o_int8_sums(int32_t *out, const int8_t *w, int32_t groups);
+/* kernels/kernel/matmul.ts:38-46 (six.ts:16-31 widening) */
+void o_six_sums(int32_t *out, const uint8_t *w, int32_t groups);
+/* kernels/six.ts:16-31: one 24-byte group -> its 32 int8 values */
+void o_six_unpack(int8_t *out32, const uint8_t *group24);
+/* kernels/kernel/matmul.ts:134-146 */
+void o_interleave(int8_t *xq, float *xs, int32_t n);
+/* kernels/kernel/halves.ts:320-326 (half) */
+float o_half(uint16_t h);
+
+/* kernels/relaxed/int8.ts:17-50 */
+void o_matmul_q8r(float *xout, const uint8_t *xq, const float *xs, const int8_t *wq, const float *ws,
+                  const int32_t *wc, int32_t n, int32_t r0, int32_t r1);
+/* kernels/kernel/matmul.ts:77-104 */
+void o_matmul_q8(float *xout, const int8_t *xq, const float *xs, const int8_t *wq, const float *ws, int32_t n,
+                 int32_t r0, int32_t r1);
+/* kernels/relaxed/int8.ts:147-166 (every (row, token) is matmul_q8r's number, int8.ts:60-65) */
+void o_matmul_q8r_tile(void *xout, const void *xq, const void *xs, const int8_t *wq, const float *ws,
+                       const int32_t *wc, int32_t n, int32_t r0, int32_t r1, int32_t count, int32_t os,
+                       int32_t frame);
+/* kernels/relaxed/six.ts:152-175 */
+void o_matmul_q6r(float *xout, const uint8_t *xq, const float *xs, const uint8_t *wq, const float *ws,
+                  const int32_t *wc, int32_t n, int32_t r0, int32_t r1);
+/* kernels/kernel/matmul.ts:227-244 */
+void o_matmul_q6(float *xout, const int8_t *xq, const float *xs, const uint8_t *wq, const float *ws, int32_t n,
+                 int32_t r0, int32_t r1);
+/* kernels/relaxed/signs.ts:203-230, 292-294 (matmul_t2r) and kernels/kernel/matmul.ts:196-220 (matmul_t2): the
+ * same numbers to the bit (tests/ternary-check.ts:7-10) */
+void o_matmul_t2r(float *xout, const int8_t *xq, const float *xs, const uint8_t *wq, const uint16_t *ws,
+                  int32_t n, int32_t r0, int32_t r1, int32_t three);
+/* kernels/relaxed/signs.ts:252-289, 295-297 */
+void o_matmul_t2r_tile(void *xout, const void *xq, const void *xs, const uint8_t *wq, const uint16_t *ws,
+                       int32_t n, int32_t r0, int32_t r1, int32_t count, int32_t os, int32_t frame,
+                       int32_t three);
+
+/* CPU baseline: the GEMV above over rows [0, rows) on `threads` host threads, rows handed out in chunks as the
+ * reference's phase() does (src/runtime/forward/threads.ts:45, 90-137: 4 chunks a thread, a shared counter).
+ * kind: 0 matmul_q8r, 1 matmul_q8, 2 matmul_q6r, 3 matmul_q6, 4 matmul_t2r.  Runs `reps` times, returns seconds
+ * of the fastest run. */
+double o_time_gemv(int32_t kind, float *xout, const void *xq, const void *xs, const void *wq, const void *ws,
+                   const void *wc, int32_t n, int32_t rows, int32_t threads, int32_t reps);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,175 @@
+"""oracle.py — TEST INFRASTRUCTURE ONLY.
+
+ctypes bindings of liboracle.so (oracle.c: a scalar C restatement of the reference's quantized-matmul arithmetic,
+in the reference's float32 order) for the tests, the smoke check and bench.py's CPU baseline.  Nothing on the
+product path imports this module.
+
+Every function takes NumPy arrays (C-contiguous, of the dtype the reference's memory holds) and returns NumPy
+arrays; byte strides follow the reference (os, frame in bytes).
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIBRARY = os.path.join(HERE, "liboracle.so")
+
+
+def build():
+    """Compile liboracle.so with the committed Makefile."""
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIBRARY):
+            build()
+        L = ctypes.CDLL(LIBRARY)
+        p, i32 = ctypes.c_void_p, ctypes.c_int32
+        sigs = {
+            "o_quantize_x": [p, p, p, i32, i32],
+            "o_int8_sums": [p, p, i32],
+            "o_six_sums": [p, p, i32],
+            "o_six_unpack": [p, p],
+            "o_interleave": [p, p, i32],
+            "o_matmul_q8r": [p, p, p, p, p, p, i32, i32, i32],
+            "o_matmul_q8": [p, p, p, p, p, i32, i32, i32],
+            "o_matmul_q8r_tile": [p, p, p, p, p, p, i32, i32, i32, i32, i32, i32],
+            "o_matmul_q6r": [p, p, p, p, p, p, i32, i32, i32],
+            "o_matmul_q6": [p, p, p, p, p, i32, i32, i32],
+            "o_matmul_t2r": [p, p, p, p, p, i32, i32, i32, i32],
+            "o_matmul_t2r_tile": [p, p, p, p, p, i32, i32, i32, i32, i32, i32, i32],
+        }
+        for name, argtypes in sigs.items():
+            fn = getattr(L, name)
+            fn.argtypes, fn.restype = argtypes, None
+        L.o_half.argtypes, L.o_half.restype = [ctypes.c_uint16], ctypes.c_float
+        L.o_time_gemv.argtypes = [i32, p, p, p, p, p, p, i32, i32, i32, i32]
+        L.o_time_gemv.restype = ctypes.c_double
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data
+
+
+def _c(a, dtype):
+    a = np.ascontiguousarray(a, dtype=dtype)
+    return a
+
+
+def quantize_x(x, bias):
+    """kernels/kernel/quantize.ts:124-151: float32 x (n) -> (uint8 xq (n), float32 xs (n/32))."""
+    x = _c(x, np.float32)
+    n = x.shape[-1]
+    xq, xs = np.zeros(n, np.uint8), np.zeros(n // 32, np.float32)
+    lib().o_quantize_x(_p(xq), _p(xs), _p(x), n, bias)
+    return xq, xs
+
+
+def int8_sums(w):
+    w = _c(w, np.int8).reshape(-1)
+    out = np.zeros(w.size // 32, np.int32)
+    lib().o_int8_sums(_p(out), _p(w), out.size)
+    return out
+
+
+def six_sums(w):
+    w = _c(w, np.uint8).reshape(-1)
+    out = np.zeros(w.size // 24, np.int32)
+    lib().o_six_sums(_p(out), _p(w), out.size)
+    return out
+
+
+def six_unpack(packed):
+    """24 bytes a group -> the groups' int8 values (flattened)."""
+    packed = _c(packed, np.uint8).reshape(-1, 24)
+    out = np.zeros((packed.shape[0], 32), np.int8)
+    for g in range(packed.shape[0]):
+        lib().o_six_unpack(out[g].ctypes.data, packed[g].ctypes.data)
+    return out.reshape(-1)
+
+
+def interleave(xq, xs):
+    """kernels/kernel/matmul.ts:134-146: returns (permuted int8 xq, the 8 bytes a group of xs: scales then sums)."""
+    xq = _c(xq, np.int8).copy()
+    n = xq.size
+    area = np.zeros(2 * (n // 32), np.float32)
+    area[: n // 32] = np.asarray(xs, np.float32)
+    lib().o_interleave(_p(xq), _p(area), n)
+    return xq, area
+
+
+def half(bits):
+    return lib().o_half(int(bits) & 0xFFFF)
+
+
+def matmul_q8r(xq, xs, wq, ws, wc, n, r0=0, r1=None):
+    rows = wq.size // n
+    r1 = rows if r1 is None else r1
+    out = np.zeros(rows, np.float32)
+    lib().o_matmul_q8r(_p(out), _p(_c(xq, np.uint8)), _p(_c(xs, np.float32)), _p(_c(wq, np.int8)),
+                       _p(_c(ws, np.float32)), _p(_c(wc, np.int32)), n, r0, r1)
+    return out
+
+
+def matmul_q8(xq, xs, wq, ws, n, r0=0, r1=None):
+    rows = wq.size // n
+    r1 = rows if r1 is None else r1
+    out = np.zeros(rows, np.float32)
+    lib().o_matmul_q8(_p(out), _p(_c(xq, np.int8)), _p(_c(xs, np.float32)), _p(_c(wq, np.int8)),
+                      _p(_c(ws, np.float32)), n, r0, r1)
+    return out
+
+
+def matmul_q6r(xq, xs, wq, ws, wc, n, r0=0, r1=None):
+    rows = wq.size // (n // 32 * 24)
+    r1 = rows if r1 is None else r1
+    out = np.zeros(rows, np.float32)
+    lib().o_matmul_q6r(_p(out), _p(_c(xq, np.uint8)), _p(_c(xs, np.float32)), _p(_c(wq, np.uint8)),
+                       _p(_c(ws, np.float32)), _p(_c(wc, np.int32)), n, r0, r1)
+    return out
+
+
+def matmul_q6(xq, xs, wq, ws, n, r0=0, r1=None):
+    rows = wq.size // (n // 32 * 24)
+    r1 = rows if r1 is None else r1
+    out = np.zeros(rows, np.float32)
+    lib().o_matmul_q6(_p(out), _p(_c(xq, np.int8)), _p(_c(xs, np.float32)), _p(_c(wq, np.uint8)),
+                      _p(_c(ws, np.float32)), n, r0, r1)
+    return out
+
+
+def matmul_t2r(xq, area, wq, ws_bits, n, r0=0, r1=None, three=3):
+    """xq: interleaved int8 activations; area: xs then the int32 sums (interleave's 8 bytes a group)."""
+    rows = wq.size // (n // 4)
+    r1 = rows if r1 is None else r1
+    out = np.zeros(rows, np.float32)
+    lib().o_matmul_t2r(_p(out), _p(_c(xq, np.int8)), _p(_c(area, np.float32)), _p(_c(wq, np.uint8)),
+                       _p(_c(ws_bits, np.uint16)), n, r0, r1, three)
+    return out
+
+
+def matmul_q8r_tokens(xq, xs, wq, ws, wc, n):
+    """matmul_q8r for each token (rows of xq / xs): (count, rows) outputs."""
+    return np.stack([matmul_q8r(xq[t], xs[t], wq, ws, wc, n) for t in range(xq.shape[0])])
+
+
+def matmul_t2r_tokens(xq, area, wq, ws_bits, n):
+    return np.stack([matmul_t2r(xq[t], area[t], wq, ws_bits, n) for t in range(xq.shape[0])])
+
+
+KINDS = {"matmul_q8r": 0, "matmul_q8": 1, "matmul_q6r": 2, "matmul_q6": 3, "matmul_t2r": 4}
+
+
+def time_gemv(kind, xq, xs, wq, ws, wc, n, rows, threads, reps):
+    """The oracle's GEMV over all rows on `threads` host threads (phase()-style chunks); fastest of reps, seconds."""
+    out = np.zeros(rows, np.float32)
+    return lib().o_time_gemv(KINDS[kind], _p(out), _p(xq), _p(xs), _p(wq), _p(ws), _p(wc), n, rows, threads, reps)

@@ -1,0 +1,506 @@
+"""The oracle (oracle/oracle.c) pinned without trusting its own formulas.
+
+Each check is one the reference's arithmetic fixes independently of how the oracle is written:
+  * closed forms: quantize_x's scalar steps (tests/int8-check.ts:248-257, and NumPy's packing.quantize at bias 0),
+    int8_sums/six_sums = -64 * sum, interleave's byte map and sums (tests/ternary-check.ts:95-103), float16 widening
+    against IEEE binary16 over all 65536 halves;
+  * round trips: pack6 -> six unpack (tests/test_int6.py), hand-derived bytes of the int6 layout;
+  * hand-derived float32 answers of order-revealing inputs: big/small products that tell the reference's lane
+    chains, the order of the horizontal sum, the place of the tail groups and the separate (unfused) roundings apart
+    from every plausible alternative (relaxed/int8.ts:26-47, kernel/matmul.ts:60-97, relaxed/signs.ts:198-228);
+  * the lane membership of matmul_q8's integer partial sums, found position by position;
+  * exact float64 sums of the same integers within a bound, and power-of-two scales where every order is exact;
+  * the reference tests' own models (int8-check.ts:65-90, ternary-check.ts:129-139) on their LCG streams, bit for bit.
+"""
+import numpy as np
+import pytest
+
+import models
+from models import F
+from streams import LCG, pack6, pack_ternary, scale_rule, uninterleave_index
+
+
+# ---- quantize_x ---------------------------------------------------------------------------------------------
+def quantize_cases():
+    rng = LCG(644)
+    groups = 12
+    x = np.zeros(groups * 32, F)
+    for g in range(groups):
+        size = [1, 3.0000002, 1e-30, 65504, 1.5e-5, 2 ** -140][g % 6]
+        for j in range(32):
+            x[g * 32 + j] = 0 if g == 4 else (-0.0 if g == 5 else F(((rng.next() % 2001) - 1000) * 1e-3 * size))
+    x[6 * 32], x[6 * 32 + 31] = F(-3), F(3)
+    for j in range(1, 31):
+        x[7 * 32 + j] = F((j - 15) * 0.5)
+    x[7 * 32], x[7 * 32 + 31] = F(63), F(-63)
+    return x
+
+
+@pytest.mark.parametrize("bias", [0, 64])
+def test_quantize_x_scalar_steps(oracle, bias):
+    """tests/int8-check.ts:232-265's cases: every scale size, zeros, -0, the ends, half steps, 1/scale overflow."""
+    x = quantize_cases()
+    xq, xs = oracle.quantize_x(x, bias)
+    want_q, want_s = models.quantize_x_model(x, bias)
+    assert np.array_equal(xs.view(np.uint32), want_s.view(np.uint32))
+    assert np.array_equal(xq, want_q)
+
+
+def test_quantize_x_matches_numpy_packing_at_bias0(oracle):
+    """At bias 0 quantize_x is the converter's NumPy quantize() (src/python/engine/packing.py:40-45, quantize.ts:125-128),
+    written here as that one expression: scales max|x|/127, values rint(x * (1/scale))."""
+    rng = np.random.default_rng(1)
+    x = (rng.standard_normal(64 * 32) * rng.choice([1e-3, 1, 50], 64 * 32)).astype(F)
+    xq, xs = oracle.quantize_x(x, 0)
+    groups = x.reshape(-1, 32)
+    scales = (np.abs(groups).max(axis=1) / 127.0).astype(F)
+    inverse = np.divide(F(1.0), scales, out=np.zeros_like(scales), where=scales > 0)
+    want = np.rint(groups * inverse[:, None]).astype(np.int8).reshape(-1)
+    assert np.array_equal(xs, scales)
+    assert np.array_equal(xq.view(np.int8), want)
+
+
+def test_quantize_x_bounds(oracle):
+    """bias 64 writes 1..127 and bias 0 -127..127 wherever 1/scale is finite (int8-check.ts:258-260); the value
+    (q - bias) * scale is within half a step of x."""
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal(4096).astype(F)
+    for bias, lo, hi in [(64, 1, 127), (0, -127, 127)]:
+        xq, xs = oracle.quantize_x(x, bias)
+        q = xq.astype(np.int32) if bias else xq.view(np.int8).astype(np.int32)
+        assert q.min() >= lo and q.max() <= hi
+        back = (q - bias).reshape(-1, 32) * xs[:, None].astype(np.float64)
+        assert np.all(np.abs(back - x.reshape(-1, 32)) <= xs[:, None] * 0.5 * (1 + 1e-6))
+
+
+def test_quantize_x_nan_lane_rule(oracle):
+    """quantize.ts:10-19: a NaN in lane 0 (values 4i) makes the scale NaN; a NaN elsewhere is passed over by the
+    scalar comparisons of lanes 1..3 (the NaN lane's maximum is NaN, and NaN > amax is false)."""
+    x = np.ones(64, F)
+    x[0] = np.nan          # group 0: lane 0
+    x[32 + 5] = np.nan     # group 1: lane 1
+    x[32 + 1] = F(2.0)     # group 1's largest is in lane 1 too: lost with the NaN
+    x[32 + 2] = F(1.5)     # lane 2
+    xq, xs = oracle.quantize_x(x, 0)
+    assert np.isnan(xs[0])
+    assert xs[1] == F(F(1.5) / F(127.0))
+    assert np.all(xq[:32] == 0)  # inv = 0 where the scale is NaN
+
+
+# ---- corrections, int6 layout, interleave, halves ----------------------------------------------------------
+def test_int8_sums_closed_form(oracle):
+    rng = np.random.default_rng(3)
+    w = rng.integers(-128, 128, 32 * 37).astype(np.int8)
+    w[:32] = 127
+    w[32:64] = -128
+    want = -64 * w.astype(np.int64).reshape(-1, 32).sum(axis=1)
+    assert np.array_equal(oracle.int8_sums(w), want.astype(np.int32))
+
+
+def test_six_unpack_round_trip_and_bytes(oracle):
+    rng = np.random.default_rng(4)
+    v = (4 * rng.integers(-32, 32, 32 * 29)).astype(np.int8)
+    assert np.array_equal(oracle.six_unpack(pack6(v)), v)
+    # hand-derived bytes: -128 = six bits 100000 (low nibble 0, top 10): bytes 0..15 = 0x00, tops 0b10101010;
+    # 124 = 011111 (low 1111, top 01): 0xff and 0b01010101
+    assert np.array_equal(pack6(np.full(32, -128, np.int8)), [0] * 16 + [0xAA] * 8)
+    assert np.array_equal(pack6(np.full(32, 124, np.int8)), [0xFF] * 16 + [0x55] * 8)
+    assert np.array_equal(oracle.six_unpack(np.array([0] * 16 + [0xAA] * 8, np.uint8)), [-128] * 32)
+    assert np.array_equal(oracle.six_unpack(np.array([0xFF] * 16 + [0x55] * 8, np.uint8)), [124] * 32)
+    # one value at a time: value j alone nonzero lands at j
+    for j in range(32):
+        one = np.zeros(32, np.int8)
+        one[j] = -4
+        assert np.array_equal(oracle.six_unpack(pack6(one)), one)
+
+
+def test_six_sums_closed_form(oracle):
+    rng = np.random.default_rng(5)
+    v = (4 * rng.integers(-32, 32, 32 * 19)).astype(np.int8)
+    want = -64 * v.astype(np.int64).reshape(-1, 32).sum(axis=1)
+    assert np.array_equal(oracle.six_sums(pack6(v)), want.astype(np.int32))
+
+
+@pytest.mark.parametrize("n", [128, 256, 384, 640, 1152])
+def test_interleave_byte_map(oracle, n):
+    """tests/ternary-check.ts:84-106."""
+    rng = LCG(231)
+    a = np.array([(rng.next() & 255) - 128 for _ in range(n)], np.int8)
+    a[:32], a[32:64] = 127, -128
+    xs = (np.arange(n // 32) + 0.5).astype(F)
+    got, area = oracle.interleave(a, xs)
+    want_bytes, want_sums = models.interleave_model(a)
+    assert np.array_equal(got, want_bytes)
+    assert np.array_equal(area[: n // 32], xs)
+    assert np.array_equal(area[n // 32:].view(np.int32), want_sums)
+
+
+def test_half_all_65536(oracle):
+    """kernels/kernel/halves.ts: exact IEEE binary16 -> binary32 for every finite half; an infinity reads as 65536."""
+    import ctypes
+    L = oracle.lib()
+    bits = np.arange(65536, dtype=np.uint32)
+    got = np.array([L.o_half(ctypes.c_uint16(int(b))) for b in bits], F)
+    halves = bits.astype(np.uint16).view(np.float16)
+    finite = np.isfinite(halves)
+    assert np.array_equal(got[finite].view(np.uint32), halves[finite].astype(F).view(np.uint32))
+    assert got[0x7C00] == 65536.0 and got[0xFC00] == -65536.0
+
+
+# ---- matmul_q8r: order-revealing inputs ----------------------------------------------------------------------
+BIG = 24  # 2^24: adding 1 to it is lost (16777217 rounds to 16777216, ties to even)
+
+
+def q8r_one(oracle, ds, es):
+    xq, xs, w, ws, wc, n = models.crafted_q8r(ds, es)
+    return oracle.matmul_q8r(xq, xs, w, ws, wc, n)[0]
+
+
+def test_q8r_lanes_are_g_mod_4(oracle):
+    """relaxed/int8.ts:26-39: lane k adds groups 4j + k.  p0 = 2^24, p1 = 1, p4 = -2^24 (12 groups): lane 0 is
+    2^24 - 2^24 = 0 and lane 1 keeps the 1 -> 1.  One accumulator in group order gives 0 (2^24 + 1 -> 2^24), and
+    lanes of consecutive blocks (g // 3) give 0 too."""
+    ds = [1, 1, 0, 0, -1, 0, 0, 0, 0, 0, 0, 0]
+    es = [BIG, 0, 0, 0, BIG, 0, 0, 0, 0, 0, 0, 0]
+    assert q8r_one(oracle, ds, es) == F(1.0)
+
+
+def test_q8r_lane_chain_in_order(oracle):
+    """lane 0 takes groups 0, 4, 8 in that order: (2^24 + 1) + -2^24 = 0, where (2^24 + -2^24) + 1 would be 1."""
+    ds = [1, 0, 0, 0, 1, 0, 0, 0, -1, 0, 0, 0]
+    es = [BIG, 0, 0, 0, 0, 0, 0, 0, BIG, 0, 0, 0]
+    assert q8r_one(oracle, ds, es) == F(0.0)
+
+
+def test_q8r_hsum_order(oracle):
+    """math.ts:7-9: ((l0 + l1) + l2) + l3.  l0 = 2^24, l1 = 1, l2 = 1, l3 = -2^24: ((2^24 + 1) + 1) - 2^24 = 0,
+    where (l0 + l1) + (l2 + l3) = 2^24 + (1 - 2^24) = 1."""
+    ds = [1, 1, 1, -1]
+    es = [BIG, 0, 0, BIG]
+    assert q8r_one(oracle, ds, es) == F(0.0)
+
+
+def test_q8r_tail_after_hsum(oracle):
+    """relaxed/int8.ts:40-47: groups past the fours are added one at a time after hsum.  5 groups: p0 = 2^24,
+    p1 = -2^24, p4 = 1: hsum 0, then + 1 = 1.  Folding group 4 into lane 0 would give (2^24 + 1) - 2^24 = 0."""
+    ds = [1, -1, 0, 0, 1]
+    es = [BIG, BIG, 0, 0, 0]
+    assert q8r_one(oracle, ds, es) == F(1.0)
+    # the tail groups one at a time, in order: ng = 7 -> groups 4, 5, 6: (0 + 2^24) + 1 + -2^24 = 0
+    ds = [0, 0, 0, 0, 1, 1, -1]
+    es = [0, 0, 0, 0, BIG, 0, BIG]
+    assert q8r_one(oracle, ds, es) == F(0.0)
+
+
+def test_q8r_scale_product_rounded_first(oracle):
+    """f(d * f(ws * xs)): the scales' product is rounded before the integer meets it.  d = 3, ws = xs = 1 + 2^-12:
+    ws * xs = 1 + 2^-11 + 2^-24 rounds (a tie, to even) to 1 + 2^-11, and 3 (1 + 2^-11) is exact; multiplying the
+    unrounded product would give 3 + 3 * 2^-11 + 2^-22 instead."""
+    xq, xs, w, ws, wc, n = models.crafted_q8r([3], [0])
+    ws[0] = xs[0] = F(1 + 2.0 ** -12)
+    got = oracle.matmul_q8r(xq, xs, w, ws, wc, n)[0]
+    assert got == F(3 + 3 * 2.0 ** -11)
+    assert got != F(3 + 3 * 2.0 ** -11 + 2.0 ** -22)
+
+
+def test_q8r_no_fused_multiply_add(oracle):
+    """f(lane + f(d * s)): the product is rounded before it is added.  Lane 0 takes group 0 (-3) then group 4
+    (d = 3, s = 1 + 2^-23): 3 s = 3 + 1.5 ulp rounds to 3 + 2^-21, and -3 + that = 2^-21; a fused multiply-add would
+    give 3 * 2^-23."""
+    ds = [-3, 0, 0, 0, 3, 0, 0, 0]
+    xq, xs, w, ws, wc, n = models.crafted_q8r(ds, [0] * 8)
+    ws[4] = F(1 + 2.0 ** -23)
+    got = oracle.matmul_q8r(xq, xs, w, ws, wc, n)[0]
+    assert got == F(2.0 ** -21)
+    assert got != F(3 * 2.0 ** -23)
+
+
+def test_q8r_wc_enters_the_integer(oracle):
+    """relaxed/int8.ts:37, 45: the correction is added to the group's integer before it is scaled: with wc = 0 the
+    integer is dot(w, q) itself (here 65 * d), with int8_sums' wc it is dot(w, q - 64) (= d)."""
+    xq, xs, w, ws, wc, n = models.crafted_q8r([5, -7, 2, 1, 3], [0, 0, 0, 0, 0])
+    assert oracle.matmul_q8r(xq, xs, w, ws, wc, n)[0] == F(5 - 7 + 2 + 1 + 3)
+    assert oracle.matmul_q8r(xq, xs, w, ws, np.zeros_like(wc), n)[0] == F(65 * (5 - 7 + 2 + 1 + 3))
+
+
+# ---- matmul_q8: lane membership and order ---------------------------------------------------------------------
+def q8_groups(ds_by_pos, es):
+    """one row; group g holds a single nonzero product ds_by_pos[g] = (position, d) (activation 1 there), scale 2^e"""
+    ng = len(ds_by_pos)
+    n = ng * 32
+    w = np.zeros(n, np.int8)
+    xq = np.zeros(n, np.int8)
+    for g, (pos, d) in enumerate(ds_by_pos):
+        if d:
+            w[g * 32 + pos] = d
+            xq[g * 32 + pos] = 1
+    ws = np.array([F(2.0 ** e) for e in es], F)
+    return xq, np.ones(ng, F), w, ws, n
+
+
+def test_q8_lane_membership(oracle):
+    """kernel/matmul.ts:60-66: lane k holds products 2k, 2k+1, 2k+8, 2k+9 of each half.  Group 0 puts 2^24 at
+    position 0 (lane 0), group 1 puts 1 at position p, group 2 puts -2^24 at position 0: the 1 is lost exactly when
+    position p is in lane 0's chain."""
+    lane0 = {0, 1, 8, 9, 16, 17, 24, 25}
+    for p in range(32):
+        xq, xs, w, ws, n = q8_groups([(0, 1), (p, 1), (0, -1)], [BIG, 0, BIG])
+        got = oracle.matmul_q8(xq, xs, w, ws, n)[0]
+        assert got == (F(0.0) if p in lane0 else F(1.0)), p
+
+
+def test_q8_lane_of_each_position(oracle):
+    """and which lane: with 2^24 in lane k0 and -2^24 in lane k1 != k0 after it, a 1 in lane L survives unless
+    L == k0 ((2^24 + 1) - 2^24 in one lane is 0; in two lanes 2^24 + (1 - 2^24)... the hsum order decides)."""
+    lane_of = lambda p: (p % 8) // 2
+    for p in range(32):
+        for k0 in range(4):
+            pos0 = 2 * k0
+            xq, xs, w, ws, n = q8_groups([(pos0, 1), (p, 1), (pos0, -1)], [BIG, 0, BIG])
+            got = oracle.matmul_q8(xq, xs, w, ws, n)[0]
+            assert got == (F(0.0) if lane_of(p) == k0 else F(1.0)), (p, k0)
+
+
+def test_q8_all_groups_in_lanes(oracle):
+    """kernel/matmul.ts:84-95: matmul_q8 has no tail rule: group 4 (of 5) goes into the lanes like the others.
+    p0 = 2^24 (lane 0), p4 = 1 (lane 0), p1 = -2^24 (lane 0): 2^24 + (-2^24) + 1 in lane 0's order 0, 1, 4 = 1;
+    lane 0 order is groups 0, 1, 4: ((2^24 - 2^24) + 1) = 1."""
+    xq, xs, w, ws, n = q8_groups([(0, 1), (0, -1), (0, 0), (0, 0), (0, 1)], [BIG, BIG, 0, 0, 0])
+    assert oracle.matmul_q8(xq, xs, w, ws, n)[0] == F(1.0)
+    # and groups 0, 4, 1 would differ: put the 1 first among the big ones
+    xq, xs, w, ws, n = q8_groups([(0, 1), (0, 1), (0, 0), (0, 0), (0, -1)], [BIG, 0, 0, 0, BIG])
+    assert oracle.matmul_q8(xq, xs, w, ws, n)[0] == F(0.0)
+
+
+def test_q8_int16_pairs(oracle):
+    """dot32 adds products 2k and 2k+8 in int16 before widening (matmul.ts:60-72): -128 * -128 twice wraps to
+    -32768 (only where quantize_x's scale is 0: the reference's note); -128 * 127 + -128 * -128 stays exact."""
+    n = 32
+    w = np.zeros(n, np.int8)
+    xq = np.zeros(n, np.int8)
+    w[0], xq[0], w[8], xq[8] = -128, -128, -128, -128
+    got = oracle.matmul_q8(xq, np.ones(1, F), w, np.ones(1, F), n)[0]
+    assert got == F(-32768.0)
+    xq[8] = 127
+    assert oracle.matmul_q8(xq, np.ones(1, F), w, np.ones(1, F), n)[0] == F(16384 - 16256)
+
+
+# ---- matmul_t2r: order-revealing inputs --------------------------------------------------------------------
+def t2_crafted(terms, groups):
+    """one ternary row: terms[(g, k)] = (w, e): sub-group k of group g holds one weight w (code w + 1) against an
+    activation 1, and the activation scale xs[4g + k] = 2^e; every group scale d = 1 (half 0x3c00)."""
+    n = groups * 128
+    codes = np.ones(n, np.uint8)
+    a = np.zeros(n, np.int8)
+    xs = np.ones(n // 32, F)
+    for (g, k), (wv, e) in terms.items():
+        j = g * 128 + k * 32
+        codes[j] = wv + 1
+        a[j] = 1
+        xs[4 * g + k] = F(2.0 ** e)
+    wq = pack_ternary(codes)
+    ws = np.full(groups, 0x3C00, np.uint16)
+    return a, xs, wq, ws, n
+
+
+def t2_run(oracle, a, xs, wq, ws, n):
+    xq, area = oracle.interleave(a, xs)
+    return oracle.matmul_t2r(xq, area, wq, ws, n)[0]
+
+
+def test_t2r_lane_is_subgroup(oracle):
+    """relaxed/signs.ts:198-228: lane k adds sub-group k (activations 32k..32k+31) of every group in order.
+    2^24 (g0 k0), 1 (g0 k1), -2^24 (g1 k0): lane 0 cancels, lane 1 keeps 1."""
+    a, xs, wq, ws, n = t2_crafted({(0, 0): (1, BIG), (0, 1): (1, 0), (1, 0): (-1, BIG)}, 2)
+    assert t2_run(oracle, a, xs, wq, ws, n) == F(1.0)
+    a, xs, wq, ws, n = t2_crafted({(0, 0): (1, BIG), (1, 0): (1, 0), (2, 0): (-1, BIG)}, 3)
+    assert t2_run(oracle, a, xs, wq, ws, n) == F(0.0)
+
+
+def test_t2r_hsum_order(oracle):
+    a, xs, wq, ws, n = t2_crafted({(0, 0): (1, BIG), (0, 1): (1, 0), (0, 2): (1, 0), (0, 3): (-1, BIG)}, 1)
+    assert t2_run(oracle, a, xs, wq, ws, n) == F(0.0)
+
+
+def test_t2r_scales_twice_rounded(oracle):
+    """f(f(whole * xs) * d): two roundings.  whole = 1 (a weight 1 against 1), xs = 1 + 2^-23, d = half 1 + 2^-10
+    (0x3c01): f(1 + 2^-23) * (1 + 2^-10) = 1 + 2^-10 + 2^-23 + 2^-33 -> 1 + 2^-10 + 2^-23 (one rounding of the
+    product, which the double product's exact value also rounds to here); the second rounding is what matters for
+    a larger whole: whole = 3: f(3 + 3 * 2^-23) = 3 + 2^-21 (1.5 ulp rounds to even: 2 ulp), times (1 + 2^-10)."""
+    n = 128
+    codes = np.ones(n, np.uint8)
+    a = np.zeros(n, np.int8)
+    codes[0], a[0] = 2, 3
+    xs = np.ones(4, F)
+    xs[0] = F(1 + 2.0 ** -23)
+    wq = pack_ternary(codes)
+    ws = np.array([0x3C01], np.uint16)
+    got = t2_run(oracle, a, xs, wq, ws, n)
+    first = F(F(3.0) * xs[0])
+    assert first == F(3 + 2.0 ** -21)
+    assert got == F(first * F(1 + 2.0 ** -10))
+
+
+def test_t2r_fourth_code(oracle):
+    """ternary.ts:54-58 / ternary-check.ts:7-10: code 3 (PQ2_0's fourth, weight 2) passes the mask."""
+    n = 128
+    codes = np.ones(n, np.uint8)
+    a = np.zeros(n, np.int8)
+    codes[5], a[5] = 3, 7
+    a[6] = -1
+    got = t2_run(oracle, a, np.ones(4, F), pack_ternary(codes), np.array([0x3C00], np.uint16), n)
+    assert got == F(14.0)
+
+
+# ---- exact sums, power-of-two scales, float64 bound ----------------------------------------------------------
+def test_q8r_power_of_two_scales_exact(oracle):
+    """With every scale a power of two and small integers, every partial sum is exact: the result is the exact
+    integer sum, whatever the order (pins the indexing of w, q, ws, wc over rows and groups)."""
+    rng = np.random.default_rng(6)
+    rows, ng = 7, 13
+    n = ng * 32
+    # |dot| <= 32 * 4 * 8 = 1024 and scale products 2^-6..2^0: every partial sum is a multiple of 2^-6 below
+    # 2^14, exact in float32
+    w = rng.integers(-4, 5, rows * n).astype(np.int8)
+    xq = rng.integers(56, 73, n).astype(np.uint8)
+    ws = (2.0 ** rng.integers(-3, 1, rows * ng)).astype(F)
+    xs = (2.0 ** rng.integers(-3, 1, ng)).astype(F)
+    wc = oracle.int8_sums(w)
+    got = oracle.matmul_q8r(xq, xs, w, ws, wc, n)
+    dots = (w.reshape(rows, ng, 32).astype(np.int64) * (xq.reshape(ng, 32).astype(np.int64) - 64)).sum(-1)
+    want = (dots * ws.reshape(rows, ng).astype(np.float64) * xs.astype(np.float64)).sum(-1)
+    assert np.array_equal(got.astype(np.float64), want)
+
+
+def test_q8r_float64_bound(oracle):
+    rng = np.random.default_rng(7)
+    rows, n = 64, 4096
+    ng = n // 32
+    x = rng.standard_normal(n).astype(F)
+    xq, xs = oracle.quantize_x(x, 64)
+    w = rng.integers(-127, 128, rows * n).astype(np.int8)
+    ws = (np.abs(rng.standard_normal(rows * ng)) * 0.02 / 127).astype(F)
+    got = oracle.matmul_q8r(xq, xs, w, ws, oracle.int8_sums(w), n)
+    dots = (w.reshape(rows, ng, 32).astype(np.int64) * (xq.reshape(ng, 32).astype(np.int64) - 64)).sum(-1)
+    exact = (dots * (ws.reshape(rows, ng).astype(np.float64) * xs.astype(np.float64))).sum(-1)
+    assert np.max(np.abs(got - exact)) <= 1e-5 * np.max(np.abs(exact))
+
+
+def test_q6_is_q8_on_widened_weights(oracle):
+    """relaxed/six.ts:142-175, kernel/matmul.ts:226-244: the int6 products are the int8 ones on the widened
+    groups (six.ts:1-11), scale and order alike."""
+    rng = np.random.default_rng(8)
+    rows, ng = 9, 11
+    n = ng * 32
+    v = (4 * rng.integers(-32, 32, rows * n)).astype(np.int8)
+    packed = pack6(v)
+    ws = rng.random(rows * ng).astype(F)
+    x = rng.standard_normal(n).astype(F)
+    xq, xs = oracle.quantize_x(x, 64)
+    assert np.array_equal(oracle.matmul_q6r(xq, xs, packed, ws, oracle.six_sums(packed), n),
+                          oracle.matmul_q8r(xq, xs, v, ws, oracle.int8_sums(v), n))
+    xq0, xs0 = oracle.quantize_x(x, 0)
+    assert np.array_equal(oracle.matmul_q6(xq0, xs0, packed, ws, n), oracle.matmul_q8(xq0, xs0, v, ws, n))
+
+
+def test_t2r_float64_bound_and_identity(oracle):
+    """The integer of sub-group k is dot(code - 1, a) exactly (ternary.ts:37-43): power-of-two scales give the
+    exact float64 sum; random scales stay within 1e-5 of max |y|."""
+    rng = np.random.default_rng(9)
+    rows, groups = 6, 5
+    n = groups * 128
+    codes = rng.integers(0, 4, rows * n).astype(np.uint8)
+    a = rng.integers(-128, 128, n).astype(np.int8)
+    wq = pack_ternary(codes)
+    for power in (True, False):
+        if power:
+            xs = (2.0 ** rng.integers(-6, 0, n // 32)).astype(F)
+            d = (2.0 ** rng.integers(-6, 0, rows * groups)).astype(np.float16)
+        else:
+            xs = (rng.random(n // 32) * 0.01).astype(F)
+            d = (rng.random(rows * groups) * 0.01).astype(np.float16)
+        got = t2_run_all(oracle, a, xs, wq, d.view(np.uint16), n)
+        whole = ((codes.reshape(rows, n // 32, 32).astype(np.int64) - 1) * a.reshape(n // 32, 32)).sum(-1)
+        exact = (whole * xs.astype(np.float64) * np.repeat(d.astype(np.float64).reshape(rows, groups), 4, axis=1)).sum(-1)
+        if power:
+            assert np.array_equal(got.astype(np.float64), exact)
+        else:
+            assert np.max(np.abs(got - exact)) <= 1e-5 * np.max(np.abs(exact))
+
+
+def t2_run_all(oracle, a, xs, wq, ws, n):
+    xq, area = oracle.interleave(a, xs)
+    return oracle.matmul_t2r(xq, area, wq, ws, n)
+
+
+# ---- the reference tests' own models on their streams ---------------------------------------------------------
+def int8_check_case(ng, rows=13, tokens=4):
+    """tests/int8-check.ts:129-171's inputs for one group count (tokens 0..2 the fixed patterns, 3 random)."""
+    rng = LCG(644 + ng)
+    n = ng * 32
+    w8 = np.array([(rng.next() & 255) - 128 for _ in range(rows * n)], np.int8)
+    w8[:n], w8[n:2 * n] = 127, -128
+    w8[2 * n:3 * n] = np.where(np.arange(n) & 1, 127, -128)
+    wsv = np.array([scale_rule(rng, i) for i in range(rows * ng)], F)
+    acts, scales = [], []
+    for t in range(tokens):
+        if t < 3:
+            q = [127, 0, None][t]
+            u = np.full(n, q, np.uint8) if q is not None else np.where(np.arange(n) & 1, 127, 0).astype(np.uint8)
+        else:
+            u = np.array([rng.next() & 127 for _ in range(n)], np.uint8)
+        acts.append(u)
+        scales.append(np.array([scale_rule(rng, g + t) for g in range(ng)], F))
+    return w8, wsv, acts, scales, n
+
+
+@pytest.mark.parametrize("ng", [1, 2, 3, 4, 5, 7, 9, 12, 13, 80, 81])
+def test_q8r_reference_model(oracle, ng):
+    w8, wsv, acts, scales, n = int8_check_case(ng)
+    rows = w8.size // n
+    wc = oracle.int8_sums(w8)
+    for q, xs in zip(acts, scales):
+        got = oracle.matmul_q8r(q, xs, w8, wsv, wc, n)
+        for i in range(rows):
+            want = models.q8r_model(w8[i * n:(i + 1) * n], q, wsv[i * ng:(i + 1) * ng], xs, ng)
+            assert got[i].view(np.uint32) == want.view(np.uint32), (ng, i)
+
+
+@pytest.mark.parametrize("ng", [1, 3, 4, 9, 13])
+def test_q8_reference_model(oracle, ng):
+    rng = LCG(77 + ng)
+    n, rows = ng * 32, 5
+    w8 = np.array([(rng.next() & 255) - 128 for _ in range(rows * n)], np.int8)
+    q = np.array([(rng.next() % 255) - 127 for _ in range(n)], np.int8)
+    wsv = np.array([scale_rule(rng, i) for i in range(rows * ng)], F)
+    xs = np.array([scale_rule(rng, g + 1) for g in range(ng)], F)
+    got = oracle.matmul_q8(q, xs, w8, wsv, n)
+    for i in range(rows):
+        want = models.q8_model(w8[i * n:(i + 1) * n], q, wsv[i * ng:(i + 1) * ng], xs, ng)
+        assert got[i].view(np.uint32) == want.view(np.uint32)
+
+
+@pytest.mark.parametrize("groups", [1, 2, 3, 4, 5, 7, 9])
+def test_t2r_reference_model(oracle, groups):
+    """tests/ternary-check.ts:108-139, its stream and fixed rows (row 0's first group all +1, row 1's second all
+    -1, activations at int8's ends)."""
+    rng = LCG(231 + groups)
+    rows, n = 13, groups * 128
+    codes = np.array([rng.next() & 3 for _ in range(rows * n)], np.uint8)
+    codes[:128] = 2
+    if groups > 1:
+        codes[n + 128:n + 256] = 0
+    halves = []
+    for g in range(rows * groups):
+        v = 2.0 ** -20 * (1 + rng.next() % 1000) if g % 11 == 7 else (0 if g % 13 == 5 else 1e-3 * (1 + rng.next() % 1000))
+        halves.append(np.float16(v))
+    hs = np.array(halves, np.float16)
+    a = np.array([(rng.next() & 255) - 128 for _ in range(n)], np.int8)
+    a[:64], a[64:128] = 127, -128
+    if groups > 1:
+        a[128:256] = -128
+    xs = np.array([F(1e-2 * (1 + rng.next() % 1000)) for _ in range(n // 32)], F)
+    got = t2_run_all(oracle, a, xs, pack_ternary(codes), hs.view(np.uint16), n)
+    for i in range(rows):
+        want = models.t2_model(codes[i * n:(i + 1) * n], a, xs, hs[i * groups:(i + 1) * groups].astype(F), groups)
+        assert got[i].view(np.uint32) == want.view(np.uint32), (groups, i)
