@@ -1,0 +1,148 @@
+/* hq.h — the C-ABI of libhq.so: pyodide-llm's quantized-matmul kernels on one AMD Instinct MI355X (gfx950).
+ *
+ * The first block exports the reference kernels under their own names, arguments and order
+ * (takano32/pyodide-llm src/runtime/jobs.ts:101-140, the `Arguments` type; src/python/engine/kernels.py:42-51 for
+ * the ctypes form of the same table: usize -> pointer, i32 -> int32_t, f32 -> float).  A host that binds the
+ * WebAssembly exports by name (bun:ffi, N-API, ctypes) binds these instead.  What differs from the WebAssembly
+ * module:
+ *   - every pointer is a DEVICE address (hipMalloc'd, managed, or mapped pinned host memory), passed as a 64-bit
+ *     integer where the host language has no pointer type (bun:ffi `u64` / `ptr`);
+ *   - every call is stream-ordered: it is enqueued on the library's current stream (hq_set_stream; the null stream
+ *     until one is set) and returns before the GPU has finished.  The results are visible to later work on that
+ *     stream, and to the host after hq_synchronize() or a synchronous copy;
+ *   - a call whose arguments break a precondition launches nothing and records an error code and message for
+ *     hq_last_error() / hq_last_error_message() (per host thread), where the WebAssembly kernels (compiled
+ *     --noAssert) would write wrong memory.  Preconditions: n > 0, n % 32 == 0 (int8, int6) or n % 128 == 0
+ *     (ternary), 0 <= r0 <= r1, count >= 0, three == 3; device pointers of the weights (int8, ternary) and of the
+ *     activations 16-byte aligned, int6 weights 8-byte aligned, scales / corrections / outputs 4-byte aligned;
+ *     frame a multiple of 16 and os a multiple of 4 where count > 1.
+ *   - matmul_q8r / matmul_q6r / matmul_q8r_tile accept wc == NULL (no counterpart in the reference): the group's
+ *     integer is then dot(w, q - 64) computed directly, which is what the reference's integer is whenever wc is
+ *     int8_sums' / six_sums' (relaxed/int8.ts:6-11), without reading wc (12.5 % fewer bytes for int8).
+ * Every (row, token) output is the reference kernel's float32 number to the bit: the integer of each group is exact
+ * and the float32 operations run in the reference's order (see each declaration's citation).
+ *
+ * The second block (hq_*) is the library's own: stream and error handling, the status-returning `_ex` forms of the
+ * kernels (an explicit stream; a failure is also kept for hq_last_error()), the batched activation preparation of a
+ * prompt, and
+ * hq_phase(), which runs a whole phase of jobs written in the reference's job-table form in as few launches as the
+ * jobs allow (src/runtime/jobs.ts:36-46 for the table, 456-477 for what runner() does with each job).
+ */
+#ifndef HQ_H
+#define HQ_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- the reference's kernels, drop-in (device pointers, stream-ordered, errors via hq_last_error) ------------ */
+
+/* kernels/kernel/quantize.ts:124-151: x (n float32) -> xq (n int8, with the bias added: 0 -> -127..127, 64 ->
+ * 1..127) and xs (n/32 float32 scales) */
+void quantize_x(void *xq, void *xs, const void *x, int32_t n, int32_t bias);
+/* kernels/kernel/matmul.ts:50-58: out[g] = -64 * sum of the 32 int8 of group g (the corrections of matmul_q8r) */
+void int8_sums(void *out, const void *w, int32_t groups);
+/* kernels/kernel/matmul.ts:38-46: the same of int6 groups (24 bytes each, kernels/six.ts) */
+void six_sums(void *out, const void *w, int32_t groups);
+/* kernels/kernel/matmul.ts:134-146: the activations of quantize_x(bias 0) laid out in planes for the ternary
+ * products, in place, and after the n/32 scales at xs one int32 a group: minus the group's sum */
+void interleave(void *xq, void *xs, int32_t n);
+
+/* kernels/relaxed/int8.ts:17-50: rows [r0, r1) of int8 weights (wq: rows of n, ws: n/32 float32 a row, wc: n/32
+ * int32 a row) times the activations of quantize_x(bias 64) -> xout[r0..r1) */
+void matmul_q8r(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, const void *wc,
+                int32_t n, int32_t r0, int32_t r1);
+/* kernels/kernel/matmul.ts:77-104: the same with the activations of quantize_x(bias 0) and no corrections */
+void matmul_q8(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, int32_t n, int32_t r0,
+               int32_t r1);
+/* kernels/relaxed/int8.ts:147-166: matmul_q8r for `count` tokens: token t's activations and scales at xq + t frame
+ * and xs + t frame (bytes), its outputs at xout + t os (bytes); every (row, token) is matmul_q8r's number */
+void matmul_q8r_tile(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, const void *wc,
+                     int32_t n, int32_t r0, int32_t r1, int32_t count, int32_t os, int32_t frame);
+/* kernels/relaxed/six.ts:152-175: int6 weights (24 bytes a group of 32, kernels/six.ts), as matmul_q8r */
+void matmul_q6r(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, const void *wc,
+                int32_t n, int32_t r0, int32_t r1);
+/* kernels/kernel/matmul.ts:227-244: int6 weights, as matmul_q8 */
+void matmul_q6(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, int32_t n, int32_t r0,
+               int32_t r1);
+/* kernels/relaxed/signs.ts:292-294: ternary weights (32 bytes a group of 128, kernels/ternary.ts; ws: float16
+ * scales, one a group) times the activations interleave() left (xs: scales, then the sums) */
+void matmul_t2r(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, int32_t n, int32_t r0,
+                int32_t r1, int32_t three);
+/* kernels/kernel/matmul.ts:218-220: the same numbers (tests/ternary-check.ts:7-10) */
+void matmul_t2(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, int32_t n, int32_t r0,
+               int32_t r1, int32_t three);
+/* kernels/relaxed/signs.ts:295-297: matmul_t2r for `count` tokens, strides as matmul_q8r_tile's */
+void matmul_t2r_tile(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, int32_t n,
+                     int32_t r0, int32_t r1, int32_t count, int32_t os, int32_t frame, int32_t three);
+
+/* ---- the library's own ----------------------------------------------------------------------------------------- */
+
+enum {
+  HQ_OK = 0,
+  HQ_ERR_ARGUMENT = 1,  /* a size, range, count or constant the kernel does not take */
+  HQ_ERR_ALIGNMENT = 2, /* a pointer or stride not aligned as the kernel reads it */
+  HQ_ERR_NULL = 3,      /* a required pointer is NULL */
+  HQ_ERR_HIP = 4,       /* the HIP runtime refused the launch or reported an earlier asynchronous error */
+  HQ_ERR_KIND = 5,      /* hq_phase: a job kind this library does not run */
+  HQ_ERR_DEVICE = 6     /* no gfx950 device */
+};
+
+/* the version string, e.g. "hq 1.0 gfx950" */
+const char *hq_version(void);
+/* sets up the current HIP device (checks it is gfx950); optional, the first call does it; HQ_* status */
+int32_t hq_init(void);
+/* the stream the drop-in calls enqueue on, process-wide (a hipStream_t; NULL: the null stream) */
+int32_t hq_set_stream(void *stream);
+void *hq_get_stream(void);
+/* waits for the current stream; HQ_OK or HQ_ERR_HIP */
+int32_t hq_synchronize(void);
+/* the status of the last failed call of this host thread (HQ_OK when none), its message, and a reset */
+int32_t hq_last_error(void);
+const char *hq_last_error_message(void);
+void hq_clear_error(void);
+
+/* status-returning forms of the drop-in kernels, on an explicit stream (NULL: the null stream) */
+int32_t hq_quantize_x_ex(void *xq, void *xs, const void *x, int32_t n, int32_t bias, void *stream);
+int32_t hq_int8_sums_ex(void *out, const void *w, int32_t groups, void *stream);
+int32_t hq_six_sums_ex(void *out, const void *w, int32_t groups, void *stream);
+int32_t hq_interleave_ex(void *xq, void *xs, int32_t n, void *stream);
+int32_t hq_matmul_q8r_ex(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, const void *wc,
+                         int32_t n, int32_t r0, int32_t r1, void *stream);
+int32_t hq_matmul_q8_ex(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, int32_t n,
+                        int32_t r0, int32_t r1, void *stream);
+int32_t hq_matmul_q8r_tile_ex(void *xout, const void *xq, const void *xs, const void *wq, const void *ws,
+                              const void *wc, int32_t n, int32_t r0, int32_t r1, int32_t count, int32_t os,
+                              int32_t frame, void *stream);
+int32_t hq_matmul_q6r_ex(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, const void *wc,
+                         int32_t n, int32_t r0, int32_t r1, void *stream);
+int32_t hq_matmul_q6_ex(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, int32_t n,
+                        int32_t r0, int32_t r1, void *stream);
+int32_t hq_matmul_t2r_ex(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, int32_t n,
+                         int32_t r0, int32_t r1, int32_t three, void *stream);
+int32_t hq_matmul_t2r_tile_ex(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, int32_t n,
+                              int32_t r0, int32_t r1, int32_t count, int32_t os, int32_t frame, int32_t three,
+                              void *stream);
+
+/* The activations of `count` tokens prepared in one launch (src/runtime/forward/engine.ts:405 calls ready() once a
+ * token): token t's float32 values at x + t x_stride (bytes) -> xq + t frame and xs + t frame, as quantize_x; and,
+ * for the ternary packing, interleave() of each (src/runtime/jobs.ts:421-424). */
+int32_t hq_quantize_x_batch(void *xq, void *xs, const void *x, int32_t n, int32_t bias, int32_t count, int32_t frame,
+                            int32_t x_stride, void *stream);
+int32_t hq_interleave_batch(void *xq, void *xs, int32_t n, int32_t count, int32_t frame, void *stream);
+
+/* One phase of jobs (src/runtime/forward/threads.ts:90-137, src/runtime/jobs.ts:36-46): `jobs` holds `count` jobs
+ * of `stride` float64 each (the reference's table has JOB = 16: the first 14 are used), each
+ *   [kind, out, a, b, a4, a5, a6, a7, a8, rows, count, os, as, bs]
+ * with kind the place of its line in jobs.ts's WORK (0 matmul_q8r, 1 matmul_q8, 5 matmul_q6r, 6 matmul_q6,
+ * 8 matmul_t2r, 9 matmul_t2), the eight arguments as WORK's `one` reads them, and every row [0, rows) of every one
+ * of `count` tokens run (a job's out / a / b advance by os / as / bs bytes a token).  The addresses are device
+ * addresses held exactly in the doubles (below 2^53).  Jobs of one kind and token count share a launch. */
+int32_t hq_phase(const double *jobs, int32_t count, int32_t stride, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,64 @@
+"""Builds libhq.so (the HIP kernels and their C-ABI, include/hq.h) in-tree for gfx950 with hipcc.
+
+    python pyodide-llm_amd/build.py [--jobs N]
+
+Every source is compiled again on every call.  Flags: -ffp-contract=off (every float operation written in the
+kernels is one IEEE operation, as the reference's are), denormals kept, and packed FP32 instructions off.
+"""
+import argparse
+import concurrent.futures
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+INCLUDE = os.path.join(ROOT, "include")
+OBJ = os.path.join(HERE, "_build")
+LIBRARY = os.path.join(HERE, "libhq.so")
+SOURCES = ["quantize.hip", "gemv.hip", "gemm.hip", "abi.cpp"]
+
+HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+FLAGS = [
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-result",
+    "-ffp-contract=off", "-fno-gpu-flush-denormals-to-zero",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-I", CSRC, "-I", INCLUDE,
+]
+
+
+def _compile(src):
+    obj = os.path.join(OBJ, os.path.splitext(src)[0] + ".o")
+    cmd = [HIPCC, *FLAGS, "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
+    run = subprocess.run(cmd, capture_output=True, text=True)
+    # hipcc's host pass does not know the packed-fp32 feature and says so: harmless
+    noise = "is not a recognized feature for this target"
+    err = "\n".join(line for line in run.stderr.splitlines() if noise not in line)
+    if run.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {src}:\n{err}")
+    if err.strip():
+        print(err, file=sys.stderr)
+    return obj
+
+
+def build(jobs=None):
+    """Compile every source and link libhq.so; returns its path."""
+    os.makedirs(OBJ, exist_ok=True)
+    jobs = jobs or min(len(SOURCES), os.cpu_count() or 1)
+    with concurrent.futures.ThreadPoolExecutor(jobs) as pool:
+        objects = list(pool.map(_compile, SOURCES))
+    tmp = LIBRARY + ".tmp"
+    run = subprocess.run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objects],
+                         capture_output=True, text=True)
+    if run.returncode != 0:
+        raise RuntimeError(f"link failed:\n{run.stderr}")
+    os.replace(tmp, LIBRARY)
+    return LIBRARY
+
+
+if __name__ == "__main__":
+    parser = argparse.ArgumentParser()
+    parser.add_argument("--jobs", type=int, default=None)
+    print(build(parser.parse_args().jobs))

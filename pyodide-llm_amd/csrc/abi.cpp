@@ -1,0 +1,351 @@
+// abi.cpp — libhq.so's C-ABI (include/hq.h): argument checks, the error state, the stream, and which kernel each
+// call takes.  No kernel is here; the launchers are in quantize.hip, gemv.hip and gemm.hip.
+#include "hq.h"
+
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <vector>
+
+#include "launch.hpp"
+
+namespace {
+
+thread_local int32_t g_error = HQ_OK;
+thread_local char g_message[512] = "";
+std::atomic<void *> g_stream{nullptr};
+
+// more tokens than this take the matrix cores (fewer: the token kernel, the weights read once a 4 tokens)
+constexpr int32_t kGemmMinTokens = 16;
+
+int32_t fail(int32_t code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_message, sizeof g_message, fmt, ap);
+  va_end(ap);
+  g_error = code;
+  return code;
+}
+
+int32_t hip_status(hipError_t e, const char *what) {
+  if (e == hipSuccess) return HQ_OK;
+  return fail(HQ_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+// the device check, once a device
+std::mutex g_init_mutex;
+int8_t g_device_ok[64];  // 0 unknown, 1 gfx950, -1 not
+
+int32_t ensure_device() {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(HQ_ERR_DEVICE, "no HIP device: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= 64) return fail(HQ_ERR_DEVICE, "device %d out of range", dev);
+  if (g_device_ok[dev] == 1) return HQ_OK;
+  std::lock_guard<std::mutex> lock(g_init_mutex);
+  if (g_device_ok[dev] == 0) {
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, dev);
+    if (e != hipSuccess) return fail(HQ_ERR_DEVICE, "hipGetDeviceProperties: %s", hipGetErrorString(e));
+    g_device_ok[dev] = std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : -1;
+    if (g_device_ok[dev] != 1) {
+      return fail(HQ_ERR_DEVICE, "device %d is %s: libhq.so holds gfx950 code only", dev, prop.gcnArchName);
+    }
+  }
+  return g_device_ok[dev] == 1 ? HQ_OK : fail(HQ_ERR_DEVICE, "device %d is not gfx950", dev);
+}
+
+bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+hipStream_t stream_of(void *s) { return (hipStream_t)s; }
+
+const char *kind_name(hq::Kind k) {
+  switch (k) {
+  case hq::Q8R: return "matmul_q8r";
+  case hq::Q8: return "matmul_q8";
+  case hq::Q6R: return "matmul_q6r";
+  case hq::Q6: return "matmul_q6";
+  case hq::T2R: return "matmul_t2r";
+  case hq::T2: return "matmul_t2";
+  }
+  return "?";
+}
+
+bool ternary(hq::Kind k) { return k == hq::T2R || k == hq::T2; }
+bool relaxed(hq::Kind k) { return k == hq::Q8R || k == hq::Q6R; }
+bool six(hq::Kind k) { return k == hq::Q6R || k == hq::Q6; }
+
+// the preconditions of a matrix job (include/hq.h's list)
+int32_t check_job(hq::Kind kind, const hq::Job &j, int32_t three) {
+  const char *name = kind_name(kind);
+  const int32_t unit = ternary(kind) ? 128 : 32;
+  if (j.n <= 0 || j.n % unit) return fail(HQ_ERR_ARGUMENT, "%s: n = %d is not a positive multiple of %d", name, j.n, unit);
+  if (j.r0 < 0 || j.r1 < j.r0) return fail(HQ_ERR_ARGUMENT, "%s: rows %d..%d", name, j.r0, j.r1);
+  if (j.count < 0) return fail(HQ_ERR_ARGUMENT, "%s: count = %d", name, j.count);
+  if (ternary(kind) && three != 3) return fail(HQ_ERR_ARGUMENT, "%s: three = %d, not 3", name, three);
+  if (j.r1 == j.r0 || j.count == 0) return HQ_OK;
+  if (!j.out || !j.xq || !j.xs || !j.wq || !j.ws) return fail(HQ_ERR_NULL, "%s: a NULL pointer", name);
+  const uintptr_t wa = six(kind) ? 8 : 16;
+  if (!aligned(j.wq, wa)) return fail(HQ_ERR_ALIGNMENT, "%s: wq not %d-byte aligned", name, (int)wa);
+  if (!aligned(j.xq, 16)) return fail(HQ_ERR_ALIGNMENT, "%s: xq not 16-byte aligned", name);
+  if (!aligned(j.xs, ternary(kind) ? 16 : 4)) return fail(HQ_ERR_ALIGNMENT, "%s: xs misaligned", name);
+  if (!aligned(j.ws, ternary(kind) ? 2 : 4)) return fail(HQ_ERR_ALIGNMENT, "%s: ws misaligned", name);
+  if (j.wc && !aligned(j.wc, 4)) return fail(HQ_ERR_ALIGNMENT, "%s: wc not 4-byte aligned", name);
+  if (!aligned(j.out, 4)) return fail(HQ_ERR_ALIGNMENT, "%s: xout not 4-byte aligned", name);
+  if (j.count > 1) {
+    if (j.os < 0 || j.os % 4) return fail(HQ_ERR_ALIGNMENT, "%s: os = %lld is not a multiple of 4", name, (long long)j.os);
+    if (j.frame < 0 || j.frame % 16) return fail(HQ_ERR_ALIGNMENT, "%s: frame = %lld is not a multiple of 16", name, (long long)j.frame);
+    if (j.sframe < 0 || j.sframe % (ternary(kind) ? 16 : 4))
+      return fail(HQ_ERR_ALIGNMENT, "%s: the scales' stride %lld is misaligned", name, (long long)j.sframe);
+  }
+  return HQ_OK;
+}
+
+// runs jobs of one kind: GEMV jobs (up to 4 tokens; more in slices of 4) batched in launches of up to kMaxJobs,
+// GEMM jobs one a launch
+int32_t run_jobs(hq::Kind kind, const std::vector<hq::Job> &jobs, hipStream_t s) {
+  std::vector<hq::Job> gemv[hq::kGemvMaxTokens + 1][2];  // by token count, by wc-ness
+  for (const hq::Job &j : jobs) {
+    if (j.r1 == j.r0 || j.count == 0) continue;
+    if (j.count >= kGemmMinTokens && hq::gemm_supported(kind)) {
+      const int32_t st = hip_status(hq::launch_gemm(kind, j, s), kind_name(kind));
+      if (st) return st;
+      continue;
+    }
+    for (int32_t t0 = 0; t0 < j.count; t0 += hq::kGemvMaxTokens) {
+      hq::Job part = j;
+      part.count = j.count - t0 < hq::kGemvMaxTokens ? j.count - t0 : hq::kGemvMaxTokens;
+      part.out = j.out + t0 * j.os;
+      part.xq = j.xq + t0 * j.frame;
+      part.xs = j.xs + t0 * j.sframe;
+      gemv[part.count][part.wc != nullptr].push_back(part);
+    }
+  }
+  for (int c = 1; c <= hq::kGemvMaxTokens; c++)
+    for (int w = 0; w < 2; w++) {
+      const auto &list = gemv[c][w];
+      for (size_t i = 0; i < list.size(); i += hq::kMaxJobs) {
+        const int32_t m = (int32_t)(list.size() - i < (size_t)hq::kMaxJobs ? list.size() - i : hq::kMaxJobs);
+        const int32_t st = hip_status(hq::launch_gemv(kind, &list[i], m, s), kind_name(kind));
+        if (st) return st;
+      }
+    }
+  return HQ_OK;
+}
+
+int32_t matmul(hq::Kind kind, void *xout, const void *xq, const void *xs, const void *wq, const void *ws,
+               const void *wc, int32_t n, int32_t r0, int32_t r1, int32_t count, int32_t os, int32_t frame,
+               int32_t three, void *stream) {
+  g_error = HQ_OK;
+  hq::Job j{(char *)xout, (const char *)xq, (const char *)xs, (const char *)wq, (const char *)ws,
+            relaxed(kind) ? (const char *)wc : nullptr, n, r0, r1, count, os, frame, frame};
+  if (int32_t st = check_job(kind, j, three)) return st;
+  if (j.r1 == j.r0 || j.count == 0) return HQ_OK;
+  if (int32_t st = ensure_device()) return st;
+  return run_jobs(kind, {j}, stream_of(stream));
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *hq_version(void) { return "hq 1.0 gfx950"; }
+
+int32_t hq_init(void) {
+  g_error = HQ_OK;
+  return ensure_device();
+}
+
+int32_t hq_set_stream(void *stream) {
+  g_stream.store(stream);
+  return HQ_OK;
+}
+
+void *hq_get_stream(void) { return g_stream.load(); }
+
+int32_t hq_synchronize(void) {
+  return hip_status(hipStreamSynchronize(stream_of(g_stream.load())), "hipStreamSynchronize");
+}
+
+int32_t hq_last_error(void) { return g_error; }
+const char *hq_last_error_message(void) { return g_error ? g_message : ""; }
+void hq_clear_error(void) {
+  g_error = HQ_OK;
+  g_message[0] = 0;
+}
+
+// ---- activations and corrections -----------------------------------------------------------------------------
+int32_t hq_quantize_x_batch(void *xq, void *xs, const void *x, int32_t n, int32_t bias, int32_t count, int32_t frame,
+                            int32_t x_stride, void *stream) {
+  g_error = HQ_OK;
+  if (n <= 0 || n % 32) return fail(HQ_ERR_ARGUMENT, "quantize_x: n = %d is not a positive multiple of 32", n);
+  if (count < 0) return fail(HQ_ERR_ARGUMENT, "quantize_x: count = %d", count);
+  if (count == 0) return HQ_OK;
+  if (!xq || !xs || !x) return fail(HQ_ERR_NULL, "quantize_x: a NULL pointer");
+  if (!aligned(xs, 4) || !aligned(x, 4)) return fail(HQ_ERR_ALIGNMENT, "quantize_x: xs or x not 4-byte aligned");
+  if (count > 1 && (frame < 0 || frame % 4 || x_stride < 0 || x_stride % 4))
+    return fail(HQ_ERR_ALIGNMENT, "quantize_x: frame or x_stride not a multiple of 4");
+  if (int32_t st = ensure_device()) return st;
+  return hip_status(hq::launch_quantize_x((char *)xq, (char *)xs, (const char *)x, n, bias, count, frame, x_stride,
+                                          stream_of(stream)),
+                    "quantize_x");
+}
+
+int32_t hq_quantize_x_ex(void *xq, void *xs, const void *x, int32_t n, int32_t bias, void *stream) {
+  return hq_quantize_x_batch(xq, xs, x, n, bias, 1, 0, 0, stream);
+}
+
+int32_t hq_interleave_batch(void *xq, void *xs, int32_t n, int32_t count, int32_t frame, void *stream) {
+  g_error = HQ_OK;
+  if (n <= 0 || n % 64) return fail(HQ_ERR_ARGUMENT, "interleave: n = %d is not a positive multiple of 64", n);
+  if (count < 0) return fail(HQ_ERR_ARGUMENT, "interleave: count = %d", count);
+  if (count == 0) return HQ_OK;
+  if (!xq || !xs) return fail(HQ_ERR_NULL, "interleave: a NULL pointer");
+  if (!aligned(xq, 16) || !aligned(xs, 4)) return fail(HQ_ERR_ALIGNMENT, "interleave: xq not 16- or xs not 4-byte aligned");
+  if (count > 1 && (frame < 0 || frame % 16)) return fail(HQ_ERR_ALIGNMENT, "interleave: frame not a multiple of 16");
+  if (int32_t st = ensure_device()) return st;
+  return hip_status(hq::launch_interleave((char *)xq, (char *)xs, n, count, frame, stream_of(stream)), "interleave");
+}
+
+int32_t hq_interleave_ex(void *xq, void *xs, int32_t n, void *stream) {
+  return hq_interleave_batch(xq, xs, n, 1, 0, stream);
+}
+
+int32_t hq_int8_sums_ex(void *out, const void *w, int32_t groups, void *stream) {
+  g_error = HQ_OK;
+  if (groups < 0) return fail(HQ_ERR_ARGUMENT, "int8_sums: groups = %d", groups);
+  if (groups == 0) return HQ_OK;
+  if (!out || !w) return fail(HQ_ERR_NULL, "int8_sums: a NULL pointer");
+  if (!aligned(w, 16) || !aligned(out, 4)) return fail(HQ_ERR_ALIGNMENT, "int8_sums: w not 16- or out not 4-byte aligned");
+  if (int32_t st = ensure_device()) return st;
+  return hip_status(hq::launch_int8_sums((int32_t *)out, (const char *)w, groups, stream_of(stream)), "int8_sums");
+}
+
+int32_t hq_six_sums_ex(void *out, const void *w, int32_t groups, void *stream) {
+  g_error = HQ_OK;
+  if (groups < 0) return fail(HQ_ERR_ARGUMENT, "six_sums: groups = %d", groups);
+  if (groups == 0) return HQ_OK;
+  if (!out || !w) return fail(HQ_ERR_NULL, "six_sums: a NULL pointer");
+  if (!aligned(w, 8) || !aligned(out, 4)) return fail(HQ_ERR_ALIGNMENT, "six_sums: w not 8- or out not 4-byte aligned");
+  if (int32_t st = ensure_device()) return st;
+  return hip_status(hq::launch_six_sums((int32_t *)out, (const char *)w, groups, stream_of(stream)), "six_sums");
+}
+
+// ---- the products ---------------------------------------------------------------------------------------------
+int32_t hq_matmul_q8r_ex(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, const void *wc,
+                         int32_t n, int32_t r0, int32_t r1, void *stream) {
+  return matmul(hq::Q8R, xout, xq, xs, wq, ws, wc, n, r0, r1, 1, 0, 0, 3, stream);
+}
+int32_t hq_matmul_q8_ex(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, int32_t n,
+                        int32_t r0, int32_t r1, void *stream) {
+  return matmul(hq::Q8, xout, xq, xs, wq, ws, nullptr, n, r0, r1, 1, 0, 0, 3, stream);
+}
+int32_t hq_matmul_q8r_tile_ex(void *xout, const void *xq, const void *xs, const void *wq, const void *ws,
+                              const void *wc, int32_t n, int32_t r0, int32_t r1, int32_t count, int32_t os,
+                              int32_t frame, void *stream) {
+  return matmul(hq::Q8R, xout, xq, xs, wq, ws, wc, n, r0, r1, count, os, frame, 3, stream);
+}
+int32_t hq_matmul_q6r_ex(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, const void *wc,
+                         int32_t n, int32_t r0, int32_t r1, void *stream) {
+  return matmul(hq::Q6R, xout, xq, xs, wq, ws, wc, n, r0, r1, 1, 0, 0, 3, stream);
+}
+int32_t hq_matmul_q6_ex(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, int32_t n,
+                        int32_t r0, int32_t r1, void *stream) {
+  return matmul(hq::Q6, xout, xq, xs, wq, ws, nullptr, n, r0, r1, 1, 0, 0, 3, stream);
+}
+int32_t hq_matmul_t2r_ex(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, int32_t n,
+                         int32_t r0, int32_t r1, int32_t three, void *stream) {
+  return matmul(hq::T2R, xout, xq, xs, wq, ws, nullptr, n, r0, r1, 1, 0, 0, three, stream);
+}
+int32_t hq_matmul_t2r_tile_ex(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, int32_t n,
+                              int32_t r0, int32_t r1, int32_t count, int32_t os, int32_t frame, int32_t three,
+                              void *stream) {
+  return matmul(hq::T2R, xout, xq, xs, wq, ws, nullptr, n, r0, r1, count, os, frame, three, stream);
+}
+
+// ---- a phase of jobs in the reference's table form ------------------------------------------------------------
+int32_t hq_phase(const double *jobs, int32_t count, int32_t stride, void *stream) {
+  g_error = HQ_OK;
+  if (count < 0 || (count > 0 && (!jobs || stride < 14)))
+    return fail(HQ_ERR_ARGUMENT, "hq_phase: count %d, stride %d (a job has 14 numbers at least)", count, stride);
+  std::vector<hq::Job> by_kind[10];
+  for (int32_t i = 0; i < count; i++) {
+    const double *e = jobs + (int64_t)i * stride;
+    for (int q = 0; q < 14; q++) {
+      if (!(e[q] >= 0.0 && e[q] < 9007199254740992.0 && e[q] == std::floor(e[q])))
+        return fail(HQ_ERR_ARGUMENT, "hq_phase: job %d's number %d (%g) is not an address or count", i, q, e[q]);
+    }
+    const int32_t kind = (int32_t)e[0];
+    auto at = [&](int q) { return (const char *)(uintptr_t)(uint64_t)e[q]; };
+    // [kind, out, a, b, a4, a5, a6, a7, a8, rows, count, os, as, bs] (src/runtime/jobs.ts:46, 207-333)
+    hq::Job j{(char *)at(1), at(2), at(3), at(4), at(5), nullptr, (int32_t)e[7], 0, (int32_t)e[9], (int32_t)e[10],
+              (int64_t)e[11], (int64_t)e[12], (int64_t)e[13]};
+    hq::Kind k;
+    switch (kind) {
+    case hq::Q8R: k = hq::Q8R; j.wc = at(6); j.sframe = j.count > 1 ? j.frame : j.sframe; break;  // its tile
+    case hq::Q8: k = hq::Q8; break;
+    case hq::Q6R: k = hq::Q6R; j.wc = at(6); break;
+    case hq::Q6: k = hq::Q6; break;
+    case hq::T2R: k = hq::T2R; j.sframe = j.count > 1 ? j.frame : j.sframe; break;  // its tile
+    case hq::T2: k = hq::T2; break;
+    default: return fail(HQ_ERR_KIND, "hq_phase: job %d is of kind %d, which this library does not run", i, kind);
+    }
+    if (int32_t st = check_job(k, j, 3)) return st;
+    by_kind[kind].push_back(j);
+  }
+  if (count > 0) {
+    if (int32_t st = ensure_device()) return st;
+  }
+  for (int kind = 0; kind < 10; kind++) {
+    if (by_kind[kind].empty()) continue;
+    if (int32_t st = run_jobs((hq::Kind)kind, by_kind[kind], stream_of(stream))) return st;
+  }
+  return HQ_OK;
+}
+
+// ---- the drop-in names: the library's stream, errors kept for hq_last_error() ---------------------------------
+void quantize_x(void *xq, void *xs, const void *x, int32_t n, int32_t bias) {
+  hq_quantize_x_ex(xq, xs, x, n, bias, g_stream.load());
+}
+void int8_sums(void *out, const void *w, int32_t groups) { hq_int8_sums_ex(out, w, groups, g_stream.load()); }
+void six_sums(void *out, const void *w, int32_t groups) { hq_six_sums_ex(out, w, groups, g_stream.load()); }
+void interleave(void *xq, void *xs, int32_t n) { hq_interleave_ex(xq, xs, n, g_stream.load()); }
+void matmul_q8r(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, const void *wc, int32_t n,
+                int32_t r0, int32_t r1) {
+  hq_matmul_q8r_ex(xout, xq, xs, wq, ws, wc, n, r0, r1, g_stream.load());
+}
+void matmul_q8(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, int32_t n, int32_t r0,
+               int32_t r1) {
+  hq_matmul_q8_ex(xout, xq, xs, wq, ws, n, r0, r1, g_stream.load());
+}
+void matmul_q8r_tile(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, const void *wc,
+                     int32_t n, int32_t r0, int32_t r1, int32_t count, int32_t os, int32_t frame) {
+  hq_matmul_q8r_tile_ex(xout, xq, xs, wq, ws, wc, n, r0, r1, count, os, frame, g_stream.load());
+}
+void matmul_q6r(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, const void *wc, int32_t n,
+                int32_t r0, int32_t r1) {
+  hq_matmul_q6r_ex(xout, xq, xs, wq, ws, wc, n, r0, r1, g_stream.load());
+}
+void matmul_q6(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, int32_t n, int32_t r0,
+               int32_t r1) {
+  hq_matmul_q6_ex(xout, xq, xs, wq, ws, n, r0, r1, g_stream.load());
+}
+void matmul_t2r(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, int32_t n, int32_t r0,
+                int32_t r1, int32_t three) {
+  hq_matmul_t2r_ex(xout, xq, xs, wq, ws, n, r0, r1, three, g_stream.load());
+}
+void matmul_t2(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, int32_t n, int32_t r0,
+               int32_t r1, int32_t three) {
+  matmul(hq::T2, xout, xq, xs, wq, ws, nullptr, n, r0, r1, 1, 0, 0, three, g_stream.load());
+}
+void matmul_t2r_tile(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, int32_t n,
+                     int32_t r0, int32_t r1, int32_t count, int32_t os, int32_t frame, int32_t three) {
+  hq_matmul_t2r_tile_ex(xout, xq, xs, wq, ws, n, r0, r1, count, os, frame, three, g_stream.load());
+}
+
+}  // extern "C"

@@ -1,0 +1,383 @@
+// gemv.hip — the token kernels (decode, 1..4 tokens a launch, the weights read once for all of them):
+//   matmul_q8r / matmul_q6r   (kernels/relaxed/int8.ts:17-50, relaxed/six.ts:152-175; the tile's numbers for
+//                              2..4 tokens, relaxed/int8.ts:52-166)
+//   matmul_q8 / matmul_q6     (kernels/kernel/matmul.ts:77-104, 227-244)
+//   matmul_t2r / matmul_t2    (kernels/relaxed/signs.ts:203-230, kernel/matmul.ts:196-220; the same numbers)
+//
+// Layout (all kinds): a block is 4 waves, a wave 4 rows, a row 16 lanes.  Lane l of a row takes the groups
+// 16 i + l (i = 0, 1, ...): a group's bytes (32 int8, 24 int6 or 32 ternary) are one lane's, so its integer sum is
+// exact in that lane (v_dot4_i32_i8) and the row's 16 lanes read 512 (384) contiguous bytes a step.
+//
+// The float32 order is the reference's, so every output is its number to the bit:
+//   relaxed int8 / int6: lane k (k = 0..3) of the reference's accumulator adds the groups 4 j + k in order.  Those
+//     are lanes k, k + 4, k + 8, k + 12 of a step here: lane k adds them in that order with DPP moves (no LDS),
+//     then lane 0 adds the four lanes ((l0 + l1) + l2) + l3 and the groups past the last four one at a time.
+//   plain int8 / int6 and ternary: the reference's lane k adds part k of EVERY group in order (matmul_q8: the
+//     products 2k, 2k+1, 2k+8, 2k+9 of each half; ternary: the k-th 32 of each 128).  A step's 16 groups x 4 parts
+//     are written to LDS and lane k of the row adds its part of the 16 groups in order.
+// Rows past r1 in a block compute on a clamped row and store nothing (DPP needs the whole row of lanes live).
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace hq {
+
+namespace {
+
+struct GemvBatch {
+  Job job[kMaxJobs];
+  int32_t block0[kMaxJobs + 1];  // the first block of each job
+  int32_t njobs;
+};
+
+constexpr int kRowsPerBlock = 16;
+
+HQ_DEV int job_of(const GemvBatch &b, int blk) {
+  int j = 0;
+  while (j + 1 < b.njobs && blk >= b.block0[j + 1]) ++j;
+  return j;
+}
+
+HQ_DEV uint4 ld16(const char *p) { return *(const uint4 *)p; }
+HQ_DEV uint2 ld8(const char *p) { return *(const uint2 *)p; }
+
+// the 32 weight bytes of group g of a row, as eight dwords of int8 (int6 groups widened, kernels/six.ts)
+template <int PACK>
+HQ_DEV void load_group(const char *wrow, int g, uint32_t w[8]) {
+  if (PACK == 8) {
+    const uint4 a = ld16(wrow + g * 32), b = ld16(wrow + g * 32 + 16);
+    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+    w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+  } else {
+    const char *p = wrow + g * 24;
+    const uint2 a = ld8(p), b = ld8(p + 8), c = ld8(p + 16);
+    const uint32_t d[6] = {a.x, a.y, b.x, b.y, c.x, c.y};
+    six_widen(d, w);
+  }
+}
+
+HQ_DEV void load_acts(const char *xq, int g, uint32_t x[8]) {
+  const uint4 a = ld16(xq + g * 32), b = ld16(xq + g * 32 + 16);
+  x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+  x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// relaxed int8 / int6 (matmul_q8r, matmul_q6r; T tokens of the tile)
+// ---------------------------------------------------------------------------------------------------------------
+// the group's integer dot(w, q - 64): with the caller's correction (wc: dot(w, q) + wc, relaxed/int8.ts:37), or
+// with -64 sum(w) made here when wc is NULL (the same integer whenever wc is int8_sums' / six_sums')
+template <int T, bool WC>
+HQ_DEV void relaxed_terms(const uint32_t w[8], const char *const xq[T], const char *const xs[T], float ws, int32_t wc,
+                          int g, float p[T]) {
+  int32_t wsum = 0;
+  if (!WC) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) wsum = sdot4((int32_t)w[i], 0x01010101, wsum);
+  }
+#pragma unroll
+  for (int t = 0; t < T; t++) {
+    uint32_t x[8];
+    load_acts(xq[t], g, x);
+    int32_t d = WC ? wc : -64 * wsum;
+#pragma unroll
+    for (int i = 0; i < 8; i++) d = sdot4((int32_t)w[i], (int32_t)x[i], d);
+    const float s = fmul(ws, ((const float *)xs[t])[g]);
+    p[t] = fmul((float)d, s);
+  }
+}
+
+template <int PACK, int T, bool WC>
+__global__ __launch_bounds__(256) void gemv_relaxed(GemvBatch batch) {
+  const int jb = job_of(batch, blockIdx.x);
+  const Job &J = batch.job[jb];
+  const int lane = threadIdx.x & 15;
+  const int row_u = J.r0 + (blockIdx.x - batch.block0[jb]) * kRowsPerBlock + (threadIdx.x >> 4);
+  const bool live = row_u < J.r1;
+  const int row = live ? row_u : J.r1 - 1;
+  const int ng = J.n >> 5, ng4 = ng & ~3;
+  constexpr int GB = PACK == 8 ? 32 : 24;
+  const char *wrow = J.wq + (int64_t)row * ng * GB;
+  const float *srow = (const float *)J.ws + (int64_t)row * ng;
+  const int32_t *crow = WC ? (const int32_t *)J.wc + (int64_t)row * ng : nullptr;
+  const char *xq[T];
+  const char *xs[T];
+#pragma unroll
+  for (int t = 0; t < T; t++) {
+    xq[t] = J.xq + t * J.frame;
+    xs[t] = J.xs + t * J.sframe;
+  }
+
+  float acc[T];
+#pragma unroll
+  for (int t = 0; t < T; t++) acc[t] = 0.0f;
+  const int steps = (ng4 + 15) >> 4;
+  for (int it = 0; it < steps; ++it) {
+    const int g = it * 16 + lane;
+    const bool valid = g < ng4;
+    const int gl = valid ? g : 0;
+    uint32_t w[8];
+    load_group<PACK>(wrow, gl, w);
+    float p[T];
+    relaxed_terms<T, WC>(w, xq, xs, srow[gl], WC ? crow[gl] : 0, gl, p);
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+      const float q = valid ? p[t] : 0.0f;  // +0 leaves a lane as it is: a lane is never -0
+      // lane k: groups 16 it + k, + 4, + 8, + 12 in order (relaxed/int8.ts:26-39)
+      float a = fadd(acc[t], q);
+      a = fadd(a, from_lane_plus<4>(q));
+      a = fadd(a, from_lane_plus<8>(q));
+      acc[t] = fadd(a, from_lane_plus<12>(q));
+    }
+  }
+  // lane 0: ((l0 + l1) + l2) + l3 (math.ts:7-9), then the groups past the fours one at a time (int8.ts:40-47)
+  float sum[T];
+#pragma unroll
+  for (int t = 0; t < T; t++)
+    sum[t] = fadd(fadd(fadd(acc[t], from_lane_plus<1>(acc[t])), from_lane_plus<2>(acc[t])), from_lane_plus<3>(acc[t]));
+  const int tail = ng - ng4;
+  if (tail > 0) {
+    const int g = ng4 + (lane < tail ? lane : 0);
+    uint32_t w[8];
+    load_group<PACK>(wrow, g, w);
+    float p[T];
+    relaxed_terms<T, WC>(w, xq, xs, srow[g], WC ? crow[g] : 0, g, p);
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+      sum[t] = fadd(sum[t], p[t]);
+      if (tail > 1) sum[t] = fadd(sum[t], from_lane_plus<1>(p[t]));
+      if (tail > 2) sum[t] = fadd(sum[t], from_lane_plus<2>(p[t]));
+    }
+  }
+  if (live && lane == 0) {
+#pragma unroll
+    for (int t = 0; t < T; t++) ((float *)(J.out + t * J.os))[row] = sum[t];
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// the LDS fold of the kinds whose four lanes take part of every group
+// ---------------------------------------------------------------------------------------------------------------
+// per wave: 4 rows x T tokens x 4 parts x 16 groups, twice (a step's and the next one's)
+template <int T>
+struct Fold {
+  float v[2][4][T][4][16];
+};
+
+// after the wave wrote its step's parts: lane k (k < 4) of each row adds part k of the 16 groups in order
+template <int T>
+HQ_DEV void fold_step(const Fold<T> &f, int buf, int slot, int lane, float acc[T]) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const int k = lane & 3;
+#pragma unroll
+  for (int t = 0; t < T; t++) {
+    const float4 *src = (const float4 *)f.v[buf][slot][t][k];
+    float a = acc[t];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const float4 v = src[q];
+      a = fadd(fadd(fadd(fadd(a, v.x), v.y), v.z), v.w);
+    }
+    acc[t] = a;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// plain int8 / int6 (matmul_q8, matmul_q6)
+// ---------------------------------------------------------------------------------------------------------------
+// dot32's lanes (kernel/matmul.ts:60-72): part k of a group is the products at 2k, 2k+1, 2k+8, 2k+9 of each half.
+// In dwords: part 0 is bytes 0-1 of dwords 0 and 2, part 1 bytes 2-3 of them, part 2 bytes 0-1 of dwords 1 and 3,
+// part 3 bytes 2-3 of those (and the same of dwords 4..7).  v_perm_b32 gathers a part's four bytes of each half.
+HQ_DEV void parts_of(const uint32_t v[8], uint32_t out[8]) {
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    out[0 + h] = perm(v[4 * h + 2], v[4 * h + 0], 0x05040100u);
+    out[2 + h] = perm(v[4 * h + 2], v[4 * h + 0], 0x07060302u);
+    out[4 + h] = perm(v[4 * h + 3], v[4 * h + 1], 0x05040100u);
+    out[6 + h] = perm(v[4 * h + 3], v[4 * h + 1], 0x07060302u);
+  }
+}
+
+template <int PACK, int T>
+__global__ __launch_bounds__(256) void gemv_plain(GemvBatch batch) {
+  __shared__ Fold<T> fold[4];
+  const int jb = job_of(batch, blockIdx.x);
+  const Job &J = batch.job[jb];
+  const int lane = threadIdx.x & 15;
+  const int wave = threadIdx.x >> 6, slot = (threadIdx.x >> 4) & 3;
+  const int row_u = J.r0 + (blockIdx.x - batch.block0[jb]) * kRowsPerBlock + (threadIdx.x >> 4);
+  const bool live = row_u < J.r1;
+  const int row = live ? row_u : J.r1 - 1;
+  const int ng = J.n >> 5;
+  constexpr int GB = PACK == 8 ? 32 : 24;
+  const char *wrow = J.wq + (int64_t)row * ng * GB;
+  const float *srow = (const float *)J.ws + (int64_t)row * ng;
+  Fold<T> &f = fold[wave];
+
+  float acc[T];
+#pragma unroll
+  for (int t = 0; t < T; t++) acc[t] = 0.0f;
+  const int steps = (ng + 15) >> 4;
+  for (int it = 0; it < steps; ++it) {
+    const int g = it * 16 + lane;
+    const bool valid = g < ng;
+    const int gl = valid ? g : 0;
+    uint32_t w[8], wp[8];
+    load_group<PACK>(wrow, gl, w);
+    parts_of(w, wp);
+    const float ws = srow[gl];
+    const int buf = it & 1;
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+      uint32_t x[8], xp[8];
+      load_acts(J.xq + t * J.frame, gl, x);
+      parts_of(x, xp);
+      const float s = fmul(ws, ((const float *)(J.xs + t * J.sframe))[gl]);
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const int32_t d = sdot4((int32_t)wp[2 * k + 1], (int32_t)xp[2 * k + 1], sdot4((int32_t)wp[2 * k], (int32_t)xp[2 * k], 0));
+        f.v[buf][slot][t][k][lane] = valid ? fmul((float)d, s) : 0.0f;
+      }
+    }
+    fold_step<T>(f, buf, slot, lane, acc);
+  }
+  // lanes 0..3 hold the four parts' sums: ((l0 + l1) + l2) + l3 in lane 0
+  float sum[T];
+#pragma unroll
+  for (int t = 0; t < T; t++)
+    sum[t] = fadd(fadd(fadd(acc[t], from_lane_plus<1>(acc[t])), from_lane_plus<2>(acc[t])), from_lane_plus<3>(acc[t]));
+  if (live && lane == 0) {
+#pragma unroll
+    for (int t = 0; t < T; t++) ((float *)(J.out + t * J.os))[row] = sum[t];
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// ternary (matmul_t2r == matmul_t2)
+// ---------------------------------------------------------------------------------------------------------------
+// A group of 128 weights is 32 bytes: block h (bytes 16h..16h+15) holds the codes of weights 64h + 4c + p in byte c,
+// bits 2p.  The activations are interleave()'s: byte 16p + c of block (2g + h) is activation 4c + p of it.  Part k
+// (the reference's lane k: activations 32k..32k+31 of the group) is block h = k / 2, c in 8 (k % 2) .. + 7: weight
+// dwords 4h + 2(k%2) + {0,1} and, for every plane p, activation dwords 4p + 2(k%2) + {0,1} of the block.  Its
+// integer is sum(code * a) + (minus the sum of its 32 activations) = sum((code - 1) a) exactly (ternary.ts:37-43).
+template <int T>
+__global__ __launch_bounds__(256) void gemv_ternary(GemvBatch batch) {
+  __shared__ Fold<T> fold[4];
+  const int jb = job_of(batch, blockIdx.x);
+  const Job &J = batch.job[jb];
+  const int lane = threadIdx.x & 15;
+  const int wave = threadIdx.x >> 6, slot = (threadIdx.x >> 4) & 3;
+  const int row_u = J.r0 + (blockIdx.x - batch.block0[jb]) * kRowsPerBlock + (threadIdx.x >> 4);
+  const bool live = row_u < J.r1;
+  const int row = live ? row_u : J.r1 - 1;
+  const int groups = J.n >> 7;
+  const char *wrow = J.wq + (int64_t)row * groups * 32;
+  const uint16_t *srow = (const uint16_t *)J.ws + (int64_t)row * groups;
+  Fold<T> &f = fold[wave];
+
+  float acc[T];
+#pragma unroll
+  for (int t = 0; t < T; t++) acc[t] = 0.0f;
+  const int steps = (groups + 15) >> 4;
+  for (int it = 0; it < steps; ++it) {
+    const int g = it * 16 + lane;
+    const bool valid = g < groups;
+    const int gl = valid ? g : 0;
+    const uint4 wa = ld16(wrow + gl * 32), wb = ld16(wrow + gl * 32 + 16);
+    const uint32_t w[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+    const float d = half_to_float(srow[gl]);
+    const int buf = it & 1;
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+      const char *xb = J.xq + t * J.frame + (int64_t)gl * 128;
+      const float *xs = (const float *)(J.xs + t * J.sframe);
+      const float4 sc = *(const float4 *)(xs + 4 * gl);
+      const int4 su = *(const int4 *)((const int32_t *)(xs + (J.n >> 5)) + 4 * gl);
+      const float scale[4] = {sc.x, sc.y, sc.z, sc.w};
+      const int32_t sums[4] = {su.x, su.y, su.z, su.w};
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        uint32_t a[16];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const uint4 v = ld16(xb + 64 * h + 16 * q);
+          a[4 * q] = v.x; a[4 * q + 1] = v.y; a[4 * q + 2] = v.z; a[4 * q + 3] = v.w;
+        }
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+          const uint32_t w0 = w[4 * h + 2 * s], w1 = w[4 * h + 2 * s + 1];
+          int32_t dot = sums[2 * h + s];
+          dot = sdot4((int32_t)codes<0>(w0), (int32_t)a[0 + 2 * s], dot);
+          dot = sdot4((int32_t)codes<0>(w1), (int32_t)a[1 + 2 * s], dot);
+          dot = sdot4((int32_t)codes<1>(w0), (int32_t)a[4 + 2 * s], dot);
+          dot = sdot4((int32_t)codes<1>(w1), (int32_t)a[5 + 2 * s], dot);
+          dot = sdot4((int32_t)codes<2>(w0), (int32_t)a[8 + 2 * s], dot);
+          dot = sdot4((int32_t)codes<2>(w1), (int32_t)a[9 + 2 * s], dot);
+          dot = sdot4((int32_t)codes<3>(w0), (int32_t)a[12 + 2 * s], dot);
+          dot = sdot4((int32_t)codes<3>(w1), (int32_t)a[13 + 2 * s], dot);
+          const int k = 2 * h + s;
+          // f(f(whole * xs) * d) (relaxed/signs.ts:206)
+          f.v[buf][slot][t][k][lane] = valid ? fmul(fmul((float)dot, scale[k]), d) : 0.0f;
+        }
+      }
+    }
+    fold_step<T>(f, buf, slot, lane, acc);
+  }
+  float sum[T];
+#pragma unroll
+  for (int t = 0; t < T; t++)
+    sum[t] = fadd(fadd(fadd(acc[t], from_lane_plus<1>(acc[t])), from_lane_plus<2>(acc[t])), from_lane_plus<3>(acc[t]));
+  if (live && lane == 0) {
+#pragma unroll
+    for (int t = 0; t < T; t++) ((float *)(J.out + t * J.os))[row] = sum[t];
+  }
+}
+
+template <int T>
+hipError_t launch_t(Kind kind, const GemvBatch &b, int blocks, bool wc, hipStream_t s) {
+  dim3 grid(blocks), block(256);
+  switch (kind) {
+  case Q8R:
+    if (wc) hipLaunchKernelGGL((gemv_relaxed<8, T, true>), grid, block, 0, s, b);
+    else hipLaunchKernelGGL((gemv_relaxed<8, T, false>), grid, block, 0, s, b);
+    break;
+  case Q6R:
+    if (wc) hipLaunchKernelGGL((gemv_relaxed<6, T, true>), grid, block, 0, s, b);
+    else hipLaunchKernelGGL((gemv_relaxed<6, T, false>), grid, block, 0, s, b);
+    break;
+  case Q8: hipLaunchKernelGGL((gemv_plain<8, T>), grid, block, 0, s, b); break;
+  case Q6: hipLaunchKernelGGL((gemv_plain<6, T>), grid, block, 0, s, b); break;
+  case T2R:
+  case T2: hipLaunchKernelGGL((gemv_ternary<T>), grid, block, 0, s, b); break;
+  default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+// jobs: one kind, one token count (1..4), one wc-ness (all with corrections or all without)
+hipError_t launch_gemv(Kind kind, const Job *jobs, int32_t njobs, hipStream_t s) {
+  if (njobs < 1 || njobs > kMaxJobs) return hipErrorInvalidValue;
+  GemvBatch b{};
+  int blocks = 0;
+  for (int j = 0; j < njobs; j++) {
+    b.job[j] = jobs[j];
+    b.block0[j] = blocks;
+    blocks += (jobs[j].r1 - jobs[j].r0 + kRowsPerBlock - 1) / kRowsPerBlock;
+  }
+  b.block0[njobs] = blocks;
+  b.njobs = njobs;
+  if (blocks == 0) return hipSuccess;
+  const bool wc = jobs[0].wc != nullptr;
+  switch (jobs[0].count) {
+  case 1: return launch_t<1>(kind, b, blocks, wc, s);
+  case 2: return launch_t<2>(kind, b, blocks, wc, s);
+  case 3: return launch_t<3>(kind, b, blocks, wc, s);
+  case 4: return launch_t<4>(kind, b, blocks, wc, s);
+  default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace hq

@@ -1,0 +1,39 @@
+// launch.hpp — the host-side launchers of libhq.so's kernels (defined in quantize.hip, gemv.hip, gemm.hip) and
+// the job descriptors they take.  abi.cpp validates the C-ABI's arguments and calls these; they only launch.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace hq {
+
+// one matrix-times-activations job: rows [r0, r1) of the weights at wq (scales ws, corrections wc or NULL) for
+// `count` tokens (activations at xq + t frame, their scales at xs + t sframe; outputs at out + t os, row i at + 4 i)
+struct Job {
+  char *out;
+  const char *xq, *xs, *wq, *ws, *wc;
+  int32_t n, r0, r1, count;
+  int64_t os, frame, sframe;
+};
+
+enum Kind : int32_t { Q8R = 0, Q8 = 1, Q6R = 5, Q6 = 6, T2R = 8, T2 = 9 };
+
+// activations: count tokens of n values (x + t x_stride) -> xq + t frame, xs + t frame
+hipError_t launch_quantize_x(char *xq, char *xs, const char *x, int32_t n, int32_t bias, int32_t count,
+                             int64_t frame, int64_t x_stride, hipStream_t s);
+hipError_t launch_interleave(char *xq, char *xs, int32_t n, int32_t count, int64_t frame, hipStream_t s);
+hipError_t launch_int8_sums(int32_t *out, const char *w, int32_t groups, hipStream_t s);
+hipError_t launch_six_sums(int32_t *out, const char *w, int32_t groups, hipStream_t s);
+
+// GEMV-shaped products (every job of one kind and one token count, 1..4; up to kMaxJobs jobs a launch)
+constexpr int kMaxJobs = 8;
+hipError_t launch_gemv(Kind kind, const Job *jobs, int32_t njobs, hipStream_t s);
+
+// MFMA GEMM-shaped products (one job a launch; count > 4 tokens): the tiles of matmul_q8r_tile, matmul_q6r and
+// matmul_t2r_tile over a prompt.  Returns hipErrorNotSupported for a kind that has none.
+hipError_t launch_gemm(Kind kind, const Job &job, hipStream_t s);
+
+// which path a job of `count` tokens takes
+constexpr int kGemvMaxTokens = 4;
+bool gemm_supported(Kind kind);
+
+}  // namespace hq

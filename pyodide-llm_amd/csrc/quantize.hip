@@ -1,0 +1,143 @@
+// quantize.hip — the activations' preparation and the weights' corrections:
+//   quantize_x (kernels/kernel/quantize.ts:124-151), interleave (kernels/kernel/matmul.ts:107-146),
+//   int8_sums (matmul.ts:50-58), six_sums (matmul.ts:38-46).
+// Byte-for-byte the reference's outputs; small, latency-bound kernels (a token's activations are a few KB).
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace hq {
+
+// quantize_x: one group of 32 values a half-wave, lane j its value j.  Lane j belongs to WebAssembly lane j % 4 of
+// groupMax (quantize.ts:10-19): the maxima of each residue are reduced first (NaN kept), then lanes 1..3 compared
+// with lane 0's in order (a NaN there is passed over).
+__global__ __launch_bounds__(256) void quantize_kernel(char *xq, char *xs, const char *x, int32_t n, int32_t bias,
+                                                       int64_t total_groups, int64_t frame, int64_t x_stride) {
+  const int32_t ng = n >> 5;
+  const int64_t gi = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
+  const int j = threadIdx.x & 31;
+  const bool live = gi < total_groups;
+  const int64_t gg = live ? gi : 0;
+  const int64_t t = gg / ng;
+  const int32_t g = (int32_t)(gg - t * ng);
+  const float v = ((const float *)(x + t * x_stride))[g * GS + j];
+
+  float m = fabsf(v);
+  m = wasm_max_abs(m, from_lane_plus<4>(m));  // values 4i + r of this row of 16
+  m = wasm_max_abs(m, from_lane_plus<8>(m));
+  m = wasm_max_abs(m, __shfl_xor(m, 16, 64));  // and of the other row of the group
+  const float m0 = quad_lane<0>(m), m1 = quad_lane<1>(m), m2 = quad_lane<2>(m), m3 = quad_lane<3>(m);
+  float amax = m0;
+  if (m1 > amax) amax = m1;
+  if (m2 > amax) amax = m2;
+  if (m3 > amax) amax = m3;
+
+  const float qmax = bias == 0 ? 127.0f : 63.0f;
+  const float scale = fdiv(amax, qmax);
+  const float inv = scale > 0.0f ? fdiv(1.0f, scale) : 0.0f;
+  const int32_t tq = trunc_sat(rintf(fmul(v, inv)));
+  int32_t q = (int32_t)((uint32_t)tq + (uint32_t)bias);  // i32x4.add wraps
+  q = q > 127 ? 127 : (q < -128 ? -128 : q);             // the two saturating narrowings
+  if (live) {
+    xq[t * frame + g * GS + j] = (char)(int8_t)q;
+    if (j == 0) ((float *)(xs + t * frame))[g] = scale;
+  }
+}
+
+hipError_t launch_quantize_x(char *xq, char *xs, const char *x, int32_t n, int32_t bias, int32_t count,
+                             int64_t frame, int64_t x_stride, hipStream_t s) {
+  const int64_t groups = (int64_t)count * (n >> 5);
+  const int64_t blocks = (groups + 7) / 8;
+  hipLaunchKernelGGL(quantize_kernel, dim3((uint32_t)blocks), dim3(256), 0, s, xq, xs, x, n, bias, groups, frame,
+                     x_stride);
+  return hipGetLastError();
+}
+
+// interleave: one block of 64 activations a thread, in place.  Byte 16 p + c of the block becomes activation
+// 4 c + p (byte p of the block's dword c), and after the n / 32 scales come the blocks' two group sums, negated.
+__global__ __launch_bounds__(256) void interleave_kernel(char *xq, char *xs, int32_t n, int64_t total_blocks,
+                                                         int64_t frame) {
+  const int64_t bi = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (bi >= total_blocks) return;
+  const int32_t nb = n >> 6;
+  const int64_t t = bi / nb;
+  const int32_t b = (int32_t)(bi - t * nb);
+  uint4 *p = (uint4 *)(xq + t * frame + (int64_t)b * 64);
+  const uint4 q0 = p[0], q1 = p[1], q2 = p[2], q3 = p[3];
+  const uint32_t d[16] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w,
+                          q2.x, q2.y, q2.z, q2.w, q3.x, q3.y, q3.z, q3.w};
+  int32_t s0 = 0, s1 = 0;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    s0 = sdot4((int32_t)d[i], 0x01010101, s0);
+    s1 = sdot4((int32_t)d[8 + i], 0x01010101, s1);
+  }
+  uint32_t o[16];
+#pragma unroll
+  for (int pl = 0; pl < 4; pl++) {
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+      // bytes c = 4m..4m+3 of plane pl: byte pl of dwords 4m..4m+3
+      const uint32_t lo = perm(d[4 * m + 1], d[4 * m], (uint32_t)pl | ((uint32_t)(4 + pl) << 8));
+      const uint32_t hi = perm(d[4 * m + 3], d[4 * m + 2], (uint32_t)pl | ((uint32_t)(4 + pl) << 8));
+      o[4 * pl + m] = perm(hi, lo, 0x05040100u);
+    }
+  }
+  p[0] = make_uint4(o[0], o[1], o[2], o[3]);
+  p[1] = make_uint4(o[4], o[5], o[6], o[7]);
+  p[2] = make_uint4(o[8], o[9], o[10], o[11]);
+  p[3] = make_uint4(o[12], o[13], o[14], o[15]);
+  int32_t *sums = (int32_t *)(xs + t * frame) + (n >> 5);
+  sums[2 * b] = -s0;
+  sums[2 * b + 1] = -s1;
+}
+
+hipError_t launch_interleave(char *xq, char *xs, int32_t n, int32_t count, int64_t frame, hipStream_t s) {
+  const int64_t blocks = (int64_t)count * (n >> 6);
+  hipLaunchKernelGGL(interleave_kernel, dim3((uint32_t)((blocks + 255) / 256)), dim3(256), 0, s, xq, xs, n, blocks,
+                     frame);
+  return hipGetLastError();
+}
+
+// int8_sums / six_sums: a group a thread, -64 times the sum of its int8 values (exact in int32)
+__global__ __launch_bounds__(256) void int8_sums_kernel(int32_t *out, const char *w, int32_t groups) {
+  const int32_t g = blockIdx.x * 256 + threadIdx.x;
+  if (g >= groups) return;
+  const uint4 *p = (const uint4 *)(w + (int64_t)g * 32);
+  const uint4 a = p[0], b = p[1];
+  int32_t s = 0;
+  s = sdot4((int32_t)a.x, 0x01010101, s);
+  s = sdot4((int32_t)a.y, 0x01010101, s);
+  s = sdot4((int32_t)a.z, 0x01010101, s);
+  s = sdot4((int32_t)a.w, 0x01010101, s);
+  s = sdot4((int32_t)b.x, 0x01010101, s);
+  s = sdot4((int32_t)b.y, 0x01010101, s);
+  s = sdot4((int32_t)b.z, 0x01010101, s);
+  s = sdot4((int32_t)b.w, 0x01010101, s);
+  out[g] = -64 * s;
+}
+
+__global__ __launch_bounds__(256) void six_sums_kernel(int32_t *out, const char *w, int32_t groups) {
+  const int32_t g = blockIdx.x * 256 + threadIdx.x;
+  if (g >= groups) return;
+  const uint2 *p = (const uint2 *)(w + (int64_t)g * 24);
+  const uint2 a = p[0], b = p[1], c = p[2];
+  const uint32_t d[6] = {a.x, a.y, b.x, b.y, c.x, c.y};
+  uint32_t v[8];
+  six_widen(d, v);
+  int32_t s = 0;
+#pragma unroll
+  for (int i = 0; i < 8; i++) s = sdot4((int32_t)v[i], 0x01010101, s);
+  out[g] = -64 * s;
+}
+
+hipError_t launch_int8_sums(int32_t *out, const char *w, int32_t groups, hipStream_t s) {
+  hipLaunchKernelGGL(int8_sums_kernel, dim3((groups + 255) / 256), dim3(256), 0, s, out, w, groups);
+  return hipGetLastError();
+}
+
+hipError_t launch_six_sums(int32_t *out, const char *w, int32_t groups, hipStream_t s) {
+  hipLaunchKernelGGL(six_sums_kernel, dim3((groups + 255) / 256), dim3(256), 0, s, out, w, groups);
+  return hipGetLastError();
+}
+
+}  // namespace hq

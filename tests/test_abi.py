@@ -1,0 +1,111 @@
+"""The C-ABI (include/hq.h) without a GPU: the library loads, exports every declared symbol with the reference
+kernels' argument lists, and refuses bad arguments on the host before anything reaches a device."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "hq.h")
+
+
+def declared():
+    """(name, argument count) of every function include/hq.h declares."""
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for m in re.finditer(r"^\s*(?:const\s+)?[\w\s]+?\*?\s*(\w+)\s*\(([^;{]*?)\)\s*;", text, flags=re.M):
+        name, args = m.group(1), m.group(2).strip()
+        out[name] = 0 if args in ("", "void") else len(args.split(","))
+    return out
+
+
+def test_every_declared_symbol_is_exported(pkg):
+    lib = pkg.library()
+    names = declared()
+    assert len(names) >= 30
+    for name in names:
+        assert hasattr(lib, name), name
+
+
+def test_reference_names_and_arities(pkg):
+    """The reference kernels keep their names and argument counts (src/runtime/jobs.ts:101-140)."""
+    names = declared()
+    reference = {"quantize_x": 5, "int8_sums": 3, "six_sums": 3, "interleave": 3, "matmul_q8r": 9, "matmul_q8": 8,
+                 "matmul_q8r_tile": 12, "matmul_q6r": 9, "matmul_q6": 8, "matmul_t2r": 9, "matmul_t2": 9,
+                 "matmul_t2r_tile": 12}
+    for name, arity in reference.items():
+        assert names[name] == arity, name
+        assert len(pkg.REFERENCE_SIGNATURES[name]) == arity, name
+    for name, (argtypes, _) in pkg.OWN_SIGNATURES.items():
+        assert names[name] == len(argtypes), name
+
+
+def test_version(pkg):
+    assert pkg.library().hq_version().startswith(b"hq ")
+
+
+@pytest.mark.parametrize("call, code, words", [
+    (lambda L: L.hq_matmul_q8r_ex(None, None, None, None, None, None, 33, 0, 1, None), 1, "multiple of 32"),
+    (lambda L: L.hq_matmul_q8r_ex(None, None, None, None, None, None, 64, 3, 2, None), 1, "rows 3..2"),
+    (lambda L: L.hq_matmul_q8r_ex(None, None, None, None, None, None, 64, 0, 2, None), 3, "NULL"),
+    (lambda L: L.hq_matmul_t2r_ex(16, 16, 16, 16, 16, 128, 0, 1, 2, None), 1, "three"),
+    (lambda L: L.hq_matmul_t2r_ex(16, 16, 16, 16, 16, 96, 0, 1, 3, None), 1, "multiple of 128"),
+    (lambda L: L.hq_matmul_q8_ex(16, 17, 16, 16, 16, 64, 0, 1, None), 2, "xq"),
+    (lambda L: L.hq_matmul_q6_ex(16, 16, 16, 12, 16, 64, 0, 1, None), 2, "wq"),
+    (lambda L: L.hq_matmul_q8r_tile_ex(16, 16, 16, 16, 16, 16, 64, 0, 1, 3, 4, 8, None), 2, "frame"),
+    (lambda L: L.hq_matmul_q8r_tile_ex(16, 16, 16, 16, 16, 16, 64, 0, 1, 3, 6, 16, None), 2, "os"),
+    (lambda L: L.hq_quantize_x_ex(16, 16, 16, 48, 0, None), 1, "multiple of 32"),
+    (lambda L: L.hq_interleave_ex(16, 16, 96, None), 1, "multiple of 64"),
+    (lambda L: L.hq_int8_sums_ex(16, 8, 4, None), 2, "aligned"),
+])
+def test_argument_errors_on_host(pkg, call, code, words):
+    L = pkg.library()
+    L.hq_clear_error()
+    assert call(L) == code
+    assert L.hq_last_error() == code
+    assert words in L.hq_last_error_message().decode()
+    L.hq_clear_error()
+    assert L.hq_last_error() == 0
+
+
+def test_empty_ranges_launch_nothing(pkg):
+    """Zero rows or zero tokens: nothing to do, no device needed, no error (the reference's loops run zero times)."""
+    L = pkg.library()
+    assert L.hq_matmul_q8r_ex(None, None, None, None, None, None, 64, 5, 5, None) == 0
+    assert L.hq_matmul_q8r_tile_ex(None, None, None, None, None, None, 64, 0, 9, 0, 0, 0, None) == 0
+    assert L.hq_quantize_x_batch(None, None, None, 64, 64, 0, 0, 0, None) == 0
+
+
+def test_drop_in_records_errors(pkg):
+    """The drop-in names return nothing and keep the error for hq_last_error (Kernels raises HQError)."""
+    k = pkg.load_kernels()
+    with pytest.raises(pkg.HQError) as e:
+        k.matmul_q8r(0, 0, 0, 0, 0, 0, 100, 0, 4)
+    assert e.value.code == pkg.HQ_ERR_ARGUMENT
+    assert pkg.library().hq_last_error() == 0  # cleared once raised
+
+
+def test_phase_refuses_other_kinds_and_bad_numbers(pkg):
+    from pyodide_llm_amd import jobs
+    L = pkg.library()
+    attention = jobs.job("attention", 16, 16, 16, 16, 16, 0, 64, rows=4)
+    assert jobs.phase(L, [attention]) == pkg.HQ_ERR_KIND
+    assert "kind 3" in L.hq_last_error_message().decode()
+    bad = jobs.job("matmul_q8r", 16.5, 16, 16, 16, 16, 16, 64, rows=4)
+    assert jobs.phase(L, [bad]) == pkg.HQ_ERR_ARGUMENT
+    odd = jobs.job("matmul_t2r", 16, 16, 16, 16, 16, 0, 100, rows=4)
+    assert jobs.phase(L, [odd]) == pkg.HQ_ERR_ARGUMENT
+    assert jobs.phase(L, []) == 0
+
+
+def test_work_numbers_match_the_reference():
+    """KIND is each kind's place in jobs.ts's WORK (jobs.ts:207-336); hq.h names 0, 1, 5, 6, 8, 9."""
+    from pyodide_llm_amd import jobs
+    assert [jobs.KIND[k] for k in ("matmul_q8r", "matmul_q8", "matmul_q6r", "matmul_q6", "matmul_t2r", "matmul_t2")] \
+        == [0, 1, 5, 6, 8, 9]
+    assert jobs.PACKED["int8"].weight_bytes() == 1.125
+    assert jobs.PACKED["int6"].weight_bytes() == 0.875
+    assert jobs.PACKED["ternary"].weight_bytes() == 0.265625

@@ -1,0 +1,443 @@
+"""Parity of libhq.so's HIP kernels with the oracle (the reference's arithmetic), through the C-ABI, on cuda:0.
+
+Integers and bytes exact, every float32 output to the bit (the kernels keep the reference's float32 order), and
+nothing written outside the rows / tokens of a call (outputs start at -7, as tests/int8-check.ts:176-181 checks).
+The cases are the reference tests' (tests/int8-check.ts, tests/ternary-check.ts: their group counts, row ranges,
+token counts, int8 ends, zero and subnormal scales, the largest sums), the order-revealing inputs of
+test_oracle.py, and the BASELINE.json shapes at full size.
+"""
+import numpy as np
+import pytest
+
+import models
+from gpu_util import Arena, first_difference, same_bits
+from models import F
+from streams import LCG, pack6, pack_ternary, scale_rule
+from test_oracle import quantize_cases
+
+pytestmark = pytest.mark.gpu
+
+ROWS = 13
+RANGES = [(0, ROWS), (0, 1), (0, 3), (ROWS - 1, ROWS), (1, 6), (3, 8), (5, 5), (4, 12)]
+GROUPS = [1, 2, 3, 4, 5, 6, 7, 8, 9, 12, 13, 80, 81]
+
+
+@pytest.fixture(scope="module")
+def k(pkg):
+    import torch
+    assert torch.cuda.is_available(), "the GPU tests need a GPU"
+    return pkg.load_kernels()
+
+
+@pytest.fixture(scope="module")
+def arena():
+    return Arena(1 << 30)
+
+
+@pytest.fixture(autouse=True)
+def fresh(arena):
+    arena.reset()
+    yield
+
+
+def expect_range(full, r0, r1, rows=ROWS):
+    want = np.full(rows + 1, F(-7), F)
+    want[r0:r1] = full[r0:r1]
+    return want
+
+
+# ---- activations and corrections ------------------------------------------------------------------------------
+@pytest.mark.parametrize("bias", [0, 64])
+def test_quantize_x(k, arena, oracle, bias):
+    x = quantize_cases()
+    rng = np.random.default_rng(bias)
+    x = np.concatenate([x, rng.standard_normal(32 * 50).astype(F) * 3])
+    n = x.size
+    ax = arena.put(x)
+    xq = arena.alloc(n + 64, fill=np.full(n + 64, 0xAA, np.uint8))
+    xs = arena.alloc(4 * (n // 32) + 64, fill=np.full(n // 8 + 64, 0xAA, np.uint8))
+    k.quantize_x(xq, xs, ax, n, bias)
+    want_q, want_s = oracle.quantize_x(x, bias)
+    got_q = arena.get(xq, np.uint8, n + 64)
+    got_s = arena.get(xs, F, n // 32 + 16)
+    assert np.array_equal(got_q[:n], want_q)
+    assert same_bits(got_s[: n // 32], want_s)
+    assert np.all(got_q[n:] == 0xAA) and np.all(got_s[n // 32:].view(np.uint32) == 0xAAAAAAAA)
+
+
+def test_quantize_x_nan_groups(k, arena, oracle):
+    x = np.ones(96, F)
+    x[0] = np.nan
+    x[32 + 5] = np.nan
+    x[32 + 1] = F(2.0)
+    x[64 + 3] = np.inf
+    xq, xs = arena.alloc(96), arena.alloc(12)
+    k.quantize_x(xq, xs, arena.put(x), 96, 64)
+    want_q, want_s = oracle.quantize_x(x, 64)
+    assert np.array_equal(arena.get(xq, np.uint8, 96), want_q)
+    got_s = arena.get(xs, F, 3)
+    assert np.array_equal(np.isnan(got_s), np.isnan(want_s))
+    assert got_s[1] == want_s[1]
+
+
+def test_quantize_x_batch(pkg, arena, oracle):
+    rng = np.random.default_rng(11)
+    n, count, frame = 1024, 7, 2048
+    x = rng.standard_normal((count, n)).astype(F)
+    ax = arena.put(x)
+    xq = arena.alloc(count * frame)
+    L = pkg.library()
+    assert L.hq_quantize_x_batch(xq, xq + n, ax, n, 64, count, frame, 4 * n, None) == 0
+    for t in range(count):
+        want_q, want_s = oracle.quantize_x(x[t], 64)
+        assert np.array_equal(arena.get(xq + t * frame, np.uint8, n), want_q)
+        assert same_bits(arena.get(xq + t * frame + n, F, n // 32), want_s)
+
+
+def test_int8_and_six_sums(k, arena, oracle):
+    rng = np.random.default_rng(3)
+    w = rng.integers(-128, 128, 32 * 777).astype(np.int8)
+    w[:32], w[32:64] = 127, -128
+    out = arena.alloc(4 * 780, fill=np.full(780, -7, np.int32))
+    k.int8_sums(out, arena.put(w), 777)
+    got = arena.get(out, np.int32, 778)
+    assert np.array_equal(got[:777], oracle.int8_sums(w)) and got[777] == -7
+    v = (4 * rng.integers(-32, 32, 32 * 333)).astype(np.int8)
+    v[:32], v[32:64] = 124, -128
+    packed = pack6(v)
+    out6 = arena.alloc(4 * 340, fill=np.full(340, -7, np.int32))
+    k.six_sums(out6, arena.put(packed), 333)
+    got6 = arena.get(out6, np.int32, 334)
+    assert np.array_equal(got6[:333], oracle.six_sums(packed)) and got6[333] == -7
+
+
+@pytest.mark.parametrize("n", [128, 256, 384, 640, 1152, 17408])
+def test_interleave(k, arena, oracle, n):
+    rng = LCG(231 + n)
+    a = np.array([(rng.next() & 255) - 128 for _ in range(n)], np.int8)
+    a[:32], a[32:64] = 127, -128
+    xs = (np.arange(n // 32) + 0.5).astype(F)
+    xq = arena.put(np.concatenate([a, np.full(64, 55, np.int8)]))
+    area = arena.put(np.concatenate([xs, np.full(n // 32 + 2, -7, np.int32).view(F)]))
+    k.interleave(xq, area, n)
+    want_bytes, want_area = oracle.interleave(a, xs)
+    assert np.array_equal(arena.get(xq, np.int8, n + 64), np.concatenate([want_bytes, np.full(64, 55, np.int8)]))
+    got_area = arena.get(area, F, 2 * (n // 32) + 2)
+    assert same_bits(got_area[: 2 * (n // 32)], want_area)
+    assert np.all(got_area[2 * (n // 32):].view(np.int32) == -7)
+
+
+def test_interleave_batch(pkg, arena, oracle):
+    rng = np.random.default_rng(5)
+    n, count, frame = 5120, 5, 8192
+    a = rng.integers(-128, 128, (count, n)).astype(np.int8)
+    xs = rng.random((count, n // 32)).astype(F)
+    buf = arena.alloc(count * frame)
+    for t in range(count):
+        arena.write(buf + t * frame, a[t])
+        arena.write(buf + t * frame + n, xs[t])
+    assert pkg.library().hq_interleave_batch(buf, buf + n, n, count, frame, None) == 0
+    for t in range(count):
+        want_bytes, want_area = oracle.interleave(a[t], xs[t])
+        assert np.array_equal(arena.get(buf + t * frame, np.int8, n), want_bytes)
+        assert same_bits(arena.get(buf + t * frame + n, F, 2 * (n // 32)), want_area)
+
+
+# ---- int8 / int6 token kernels --------------------------------------------------------------------------------
+def int8_case(ng, tokens=9):
+    """tests/int8-check.ts:129-171: int8 weights (-128 too, rows 0/1 at the ends, row 2 alternating), int6 ones,
+    scales of every size, activations: token 0 all 127, 1 all 0, 2 alternating, 3 quantize_x of floats, others
+    random (relaxed, 0..127); and the plain form's -127..127 patterns."""
+    rng = LCG(644 + 7 * ng)
+    n = ng * 32
+    w8 = np.array([(rng.next() & 255) - 128 for _ in range(ROWS * n)], np.int8)
+    v6 = np.array([4 * ((rng.next() & 63) - 32) for _ in range(ROWS * n)], np.int8)
+    w8[:n], w8[n:2 * n] = 127, -128
+    v6[:n], v6[n:2 * n] = 124, -128
+    w8[2 * n:3 * n] = np.where(np.arange(n) & 1, 127, -128)
+    v6[2 * n:3 * n] = np.where(np.arange(n) & 1, 124, -128)
+    ws = np.array([scale_rule(rng, i) for i in range(ROWS * ng)], F)
+    xf = np.array([F(((rng.next() % 2001) - 1000) * 1e-3 * (1 + j % 5)) for j in range(n)], F)
+    relaxed, plain = [], []
+    for t in range(tokens):
+        s = np.array([scale_rule(rng, g + t) for g in range(ng)], F)
+        if t == 3:  # quantize_x of the floats xf, at the form's bias
+            relaxed.append((None, None))
+            plain.append((None, None))
+            continue
+        if t == 0:
+            u, i8 = np.full(n, 127, np.uint8), np.full(n, 127, np.int8)
+        elif t == 1:
+            u, i8 = np.zeros(n, np.uint8), np.full(n, -127, np.int8)
+        elif t == 2:
+            u = np.where(np.arange(n) & 1, 127, 0).astype(np.uint8)
+            i8 = np.where(np.arange(n) & 1, 127, -127).astype(np.int8)
+        else:
+            u = np.array([rng.next() & 127 for _ in range(n)], np.uint8)
+            i8 = np.array([(rng.next() % 255) - 127 for _ in range(n)], np.int8)
+        relaxed.append((u, s))
+        plain.append((i8, s))
+    return n, w8, v6, ws, xf, relaxed, plain
+
+
+def quantized_tokens(oracle, xf, toks, bias):
+    out = []
+    for (q, s) in toks:
+        if q is None:
+            q, s = oracle.quantize_x(xf, bias)
+            if bias == 0:
+                q = q.view(np.int8)
+        out.append((q, s))
+    return out
+
+
+def run_token_kernel(k, arena, name, n, wq_addr, ws_addr, wc_addr, q, s, r0, r1):
+    xq = arena.put(q)
+    xs = arena.put(s)
+    out = arena.alloc(4 * (ROWS + 1), fill=np.full(ROWS + 1, -7, F))
+    fn = getattr(k, name)
+    if name in ("matmul_q8r", "matmul_q6r"):
+        fn(out, xq, xs, wq_addr, ws_addr, wc_addr, n, r0, r1)
+    else:
+        fn(out, xq, xs, wq_addr, ws_addr, n, r0, r1)
+    return arena.get(out, F, ROWS + 1)
+
+
+@pytest.mark.parametrize("ng", GROUPS)
+@pytest.mark.parametrize("form", ["matmul_q8r", "matmul_q8r_derived", "matmul_q6r", "matmul_q8", "matmul_q6"])
+def test_token_kernels(k, arena, oracle, ng, form):
+    n, w8, v6, ws, xf, relaxed, plain = int8_case(ng)
+    six = form in ("matmul_q6r", "matmul_q6")
+    wbytes = pack6(v6) if six else w8
+    wq = arena.put(wbytes)
+    wsa = arena.put(ws)
+    is_relaxed = form.startswith("matmul_q8r") or form == "matmul_q6r"
+    toks = quantized_tokens(oracle, xf, relaxed if is_relaxed else plain, 64 if is_relaxed else 0)
+    wc = (oracle.six_sums(wbytes) if six else oracle.int8_sums(w8)) if is_relaxed else None
+    wca = arena.put(wc) if form in ("matmul_q8r", "matmul_q6r") else 0
+    name = "matmul_q8r" if form == "matmul_q8r_derived" else form
+    for t, (q, s) in enumerate(toks):
+        if is_relaxed:
+            full = (oracle.matmul_q6r if six else oracle.matmul_q8r)(q, s, wbytes, ws, wc, n)
+        else:
+            full = (oracle.matmul_q6 if six else oracle.matmul_q8)(q, s, wbytes, ws, n)
+        for r0, r1 in RANGES:
+            got = run_token_kernel(k, arena, name, n, wq, wsa, wca, q, s, r0, r1)
+            want = expect_range(full, r0, r1)
+            assert same_bits(got, want), f"{form} ng {ng} token {t} rows {r0}..{r1}: {first_difference(got, want)}"
+
+
+# ---- the tile: every (row, token) is matmul_q8r's number ------------------------------------------------------
+def tile_inputs(oracle, rng, n, count, frame, rows):
+    x = rng.standard_normal((count, n)).astype(F)
+    x[0, :32] = 0  # a group of zeros: scale 0
+    q = np.zeros((count, frame), np.uint8)
+    for t in range(count):
+        qq, ss = oracle.quantize_x(x[t], 64)
+        q[t, :n] = qq
+        q[t, n:n + 4 * (n // 32)] = ss.view(np.uint8)
+    return q
+
+
+@pytest.mark.parametrize("count", [1, 2, 3, 4, 5, 7, 8, 9, 16, 17, 33, 64, 65, 100])
+@pytest.mark.parametrize("ng", [1, 3, 4, 9, 13, 80])
+def test_q8r_tile(k, arena, oracle, count, ng):
+    rng = np.random.default_rng(1000 * ng + count)
+    n = 32 * ng
+    rows = 70
+    frame = ((n + 4 * ng + 15) // 16) * 16
+    os_ = 4 * (rows + 3)
+    w = rng.integers(-128, 128, rows * n).astype(np.int8)
+    ws = (rng.random(rows * ng) * 1e-3).astype(F)
+    ws[::11] = F(2.0 ** -130)
+    ws[5::13] = 0
+    wc = oracle.int8_sums(w)
+    q = tile_inputs(oracle, rng, n, count, frame, rows)
+    wq, wsa, wca, xq = arena.put(w), arena.put(ws), arena.put(wc), arena.put(q)
+    for derived in (False, True):
+        for r0, r1 in [(0, rows), (3, 64 + 3), (5, 6)]:
+            out = arena.alloc(os_ * count, fill=np.full(os_ * count // 4, -7, F))
+            k.matmul_q8r_tile(out, xq, xq + n, wq, wsa, 0 if derived else wca, n, r0, r1, count, os_, frame)
+            got = arena.get(out, F, os_ * count // 4).reshape(count, -1)
+            for t in range(count):
+                full = oracle.matmul_q8r(q[t, :n], q[t, n:n + 4 * ng].view(F), w, ws, wc, n)
+                want = np.full(os_ // 4, F(-7), F)
+                want[r0:r1] = full[r0:r1]
+                assert same_bits(got[t], want), f"count {count} ng {ng} rows {r0}..{r1} token {t} derived {derived}: " \
+                                                f"{first_difference(got[t], want)}"
+
+
+@pytest.mark.parametrize("count", [2, 4, 5, 16, 40])
+def test_q6r_many_tokens(pkg, arena, oracle, count):
+    """matmul_q6r over a prompt (no tile in the reference: a call a token, jobs.ts:471-475) through hq_phase."""
+    from pyodide_llm_amd import jobs
+    rng = np.random.default_rng(77 + count)
+    rows, ng = 90, 13
+    n = 32 * ng
+    frame = ((n + 4 * ng + 15) // 16) * 16
+    v = (4 * rng.integers(-32, 32, rows * n)).astype(np.int8)
+    packed = pack6(v)
+    ws = (rng.random(rows * ng) * 1e-3).astype(F)
+    wc = oracle.six_sums(packed)
+    q = tile_inputs(oracle, rng, n, count, frame, rows)
+    wq, wsa, wca, xq = arena.put(packed, align=256), arena.put(ws), arena.put(wc), arena.put(q)
+    out = arena.alloc(4 * rows * count, fill=np.full(rows * count, -7, F))
+    job = jobs.job("matmul_q6r", out, xq, xq + n, wq, wsa, wca, n, rows=rows, count=count, os=4 * rows, as_=frame,
+                   bs=frame)
+    assert jobs.phase(pkg.library(), [job]) == 0, pkg.library().hq_last_error_message()
+    got = arena.get(out, F, rows * count).reshape(count, rows)
+    for t in range(count):
+        want = oracle.matmul_q6r(q[t, :n], q[t, n:n + 4 * ng].view(F), packed, ws, wc, n)
+        assert same_bits(got[t], want), f"token {t}: {first_difference(got[t], want)}"
+
+
+# ---- ternary -------------------------------------------------------------------------------------------------
+def ternary_case(groups, rows=ROWS, seed=231):
+    rng = LCG(seed + groups)
+    n = groups * 128
+    codes = np.array([rng.next() & 3 for _ in range(rows * n)], np.uint8)
+    codes[:128] = 2
+    if groups > 1:
+        codes[n + 128:n + 256] = 0
+    halves = []
+    for g in range(rows * groups):
+        v = 2.0 ** -20 * (1 + rng.next() % 1000) if g % 11 == 7 else (0 if g % 13 == 5 else 1e-3 * (1 + rng.next() % 1000))
+        halves.append(np.float16(v))
+    return n, codes, np.array(halves, np.float16).view(np.uint16), rng
+
+
+def ternary_acts(rng, oracle, n, pattern=None):
+    if pattern is None:
+        a = np.array([(rng.next() & 255) - 128 for _ in range(n)], np.int8)
+    else:
+        a = pattern
+    xs = np.array([F(1e-2 * (1 + rng.next() % 1000)) for _ in range(n // 32)], F)
+    return oracle.interleave(a, xs)
+
+
+@pytest.mark.parametrize("groups", [1, 2, 3, 4, 5, 7, 9, 40])
+@pytest.mark.parametrize("name", ["matmul_t2r", "matmul_t2"])
+def test_ternary_token(k, arena, oracle, groups, name):
+    n, codes, halves, rng = ternary_case(groups)
+    wq = arena.put(pack_ternary(codes))
+    wsa = arena.put(halves)
+    for t in range(3):
+        if t == 0:
+            pat = np.full(n, 127, np.int8)
+            pat[64:128] = -128
+        else:
+            pat = None
+        xq_b, area = ternary_acts(rng, oracle, n, pat)
+        xq, xs = arena.put(xq_b), arena.put(area)
+        full = oracle.matmul_t2r(xq_b, area, pack_ternary(codes), halves, n)
+        for r0, r1 in [(0, ROWS), (0, 1), (ROWS - 1, ROWS), (3, 8), (5, 5)]:
+            out = arena.alloc(4 * (ROWS + 1), fill=np.full(ROWS + 1, -7, F))
+            getattr(k, name)(out, xq, xs, wq, wsa, n, r0, r1, 3)
+            got = arena.get(out, F, ROWS + 1)
+            want = expect_range(full, r0, r1)
+            assert same_bits(got, want), f"{name} groups {groups} token {t} rows {r0}..{r1}: {first_difference(got, want)}"
+
+
+def test_ternary_largest_sums(k, arena, oracle):
+    """tests/ternary-check.ts:184-248: rows of one code (0..3) against activations at int8's ends."""
+    groups, rows = 9, ROWS
+    n = groups * 128
+    codes = np.zeros(rows * n, np.uint8)
+    for i in range(rows):
+        codes[i * n:(i + 1) * n] = i & 3
+    halves = np.array([np.float16(0.5 + 0.01 * g) for g in range(rows * groups)], np.float16).view(np.uint16)
+    wq, wsa = arena.put(pack_ternary(codes)), arena.put(halves)
+    patterns = [lambda j: -128, lambda j: 127, lambda j: 127 if j & 1 else -128, lambda j: -128 if j & 32 else 127,
+                lambda j: 0, lambda j: -127]
+    for pi, pattern in enumerate(patterns):
+        for t in range(5):
+            a = np.array([max(-128, min(127, -pattern(j) if t % 2 else pattern(j + t))) for j in range(n)], np.int8)
+            xs = np.array([F(1e-2 * (1 + ((g + t) % 7))) for g in range(n // 32)], F)
+            xq_b, area = oracle.interleave(a, xs)
+            want = oracle.matmul_t2r(xq_b, area, pack_ternary(codes), halves, n)
+            out = arena.alloc(4 * rows)
+            k.matmul_t2r(out, arena.put(xq_b), arena.put(area), wq, wsa, n, 0, rows, 3)
+            got = arena.get(out, F, rows)
+            assert same_bits(got, want), f"pattern {pi} token {t}: {first_difference(got, want)}"
+
+
+@pytest.mark.parametrize("count", [1, 2, 3, 4, 5, 7, 8, 9, 16, 17, 64, 65, 100])
+@pytest.mark.parametrize("groups", [1, 3, 9])
+def test_t2r_tile(k, arena, oracle, count, groups):
+    n, codes, halves, rng = ternary_case(groups, rows=70, seed=500 + count)
+    rows = 70
+    wbytes = pack_ternary(codes)
+    wq, wsa = arena.put(wbytes), arena.put(halves)
+    frame = ((n + 8 * (n // 32) + 15) // 16) * 16
+    buf = np.zeros((count, frame), np.uint8)
+    areas = []
+    for t in range(count):
+        xq_b, area = ternary_acts(rng, oracle, n)
+        buf[t, :n] = xq_b.view(np.uint8)
+        buf[t, n:n + area.nbytes] = area.view(np.uint8)
+        areas.append((xq_b, area))
+    xq = arena.put(buf)
+    os_ = 4 * (rows + 5)
+    for r0, r1 in [(0, rows), (2, 9), (rows - 1, rows), (3, 67)]:
+        out = arena.alloc(os_ * count, fill=np.full(os_ * count // 4, -7, F))
+        k.matmul_t2r_tile(out, xq, xq + n, wq, wsa, n, r0, r1, count, os_, frame, 3)
+        got = arena.get(out, F, os_ * count // 4).reshape(count, -1)
+        for t in range(count):
+            full = oracle.matmul_t2r(areas[t][0], areas[t][1], wbytes, halves, n)
+            want = np.full(os_ // 4, F(-7), F)
+            want[r0:r1] = full[r0:r1]
+            assert same_bits(got[t], want), f"count {count} groups {groups} rows {r0}..{r1} token {t}: " \
+                                            f"{first_difference(got[t], want)}"
+
+
+# ---- the order-revealing inputs of test_oracle.py, on the GPU ------------------------------------------------
+@pytest.mark.parametrize("ds, es, want", [
+    ([1, 1, 0, 0, -1, 0, 0, 0, 0, 0, 0, 0], [24, 0, 0, 0, 24, 0, 0, 0, 0, 0, 0, 0], 1.0),
+    ([1, 0, 0, 0, 1, 0, 0, 0, -1, 0, 0, 0], [24, 0, 0, 0, 0, 0, 0, 0, 24, 0, 0, 0], 0.0),
+    ([1, 1, 1, -1], [24, 0, 0, 24], 0.0),
+    ([1, -1, 0, 0, 1], [24, 24, 0, 0, 0], 1.0),
+    ([0, 0, 0, 0, 1, 1, -1], [0, 0, 0, 0, 24, 0, 24], 0.0),
+    ([1] + [0] * 15 + [1] + [0] * 15 + [-1], [24] + [0] * 31 + [24], 0.0),
+    ([1, 0, 0, 0] * 8 + [-1, 0, 0, 0], [24] + [0] * 31 + [24, 0, 0, 0], 0.0),  # each +1 lost to 2^24
+])
+def test_q8r_order_cases(k, arena, ds, es, want):
+    xq, xs, w, ws, wc, n = models.crafted_q8r(ds, es)
+    for wc_addr in (arena.put(wc), 0):
+        out = arena.alloc(4)
+        k.matmul_q8r(out, arena.put(xq), arena.put(xs), arena.put(w), arena.put(ws), wc_addr, n, 0, 1)
+        assert arena.get(out, F, 1)[0] == F(want)
+        # and through the matrix cores: the same row against 20 tokens
+        count, frame = 20, ((n + 4 * len(ds) + 15) // 16) * 16
+        buf = np.zeros((count, frame), np.uint8)
+        buf[:, :n] = xq
+        buf[:, n:n + 4 * len(ds)] = xs.view(np.uint8)
+        outs = arena.alloc(4 * count)
+        k.matmul_q8r_tile(outs, arena.put(buf), arena.put(buf) + n, arena.put(w), arena.put(ws), wc_addr, n, 0, 1,
+                          count, 4, frame)
+        assert np.all(arena.get(outs, F, count) == F(want))
+
+
+# ---- a phase: several jobs, mixed kinds, one call -------------------------------------------------------------
+def test_phase_matches_single_calls(pkg, k, arena, oracle):
+    from pyodide_llm_amd import jobs
+    rng = np.random.default_rng(21)
+    n = 1024
+    ng = n // 32
+    x = rng.standard_normal(n).astype(F)
+    q64, s64 = oracle.quantize_x(x, 64)
+    q0, s0 = oracle.quantize_x(x, 0)
+    xq64, xs64, xq0, xs0 = arena.put(q64), arena.put(s64), arena.put(q0), arena.put(s0)
+    mats, table, wants = [], [], []
+    for rows in (1536, 1024, 96):
+        w = rng.integers(-127, 128, rows * n).astype(np.int8)
+        ws = (np.abs(rng.standard_normal(rows * ng)) * 0.02 / 127).astype(F)
+        wc = oracle.int8_sums(w)
+        wq, wsa, wca = arena.put(w), arena.put(ws), arena.put(wc)
+        o1, o2 = arena.alloc(4 * rows), arena.alloc(4 * rows)
+        table.append(jobs.job("matmul_q8r", o1, xq64, xs64, wq, wsa, wca, n, rows=rows))
+        table.append(jobs.job("matmul_q8", o2, xq0, xs0, wq, wsa, 0, n, rows=rows))
+        wants.append((o1, oracle.matmul_q8r(q64, s64, w, ws, wc, n)))
+        wants.append((o2, oracle.matmul_q8(q0.view(np.int8), s0, w, ws, n)))
+    assert jobs.phase(pkg.library(), table) == 0, pkg.library().hq_last_error_message()
+    for addr, want in wants:
+        assert same_bits(arena.get(addr, F, want.size), want)
