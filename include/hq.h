@@ -142,6 +142,23 @@ int32_t hq_interleave_batch(void *xq, void *xs, int32_t n, int32_t count, int32_
  * addresses held exactly in the doubles (below 2^53).  Jobs of one kind and token count share a launch. */
 int32_t hq_phase(const double *jobs, int32_t count, int32_t stride, void *stream);
 
+/* src/runtime/forward/engine.ts:381-407 (matmulsAlike): the phase of jobs of one input, from its float32
+ * activations: every job takes the same n and token count, token t's n values at x + t x_stride (bytes; x and
+ * x_stride 16-byte aligned).  The relaxed int8 / int6 jobs of up to 4 tokens run with quantize_x in the products'
+ * own launch (each block quantizes the input into its LDS: one launch a phase, the jobs' a / b not written); the
+ * others are readied into their a / b (quantize_x at their bias, and interleave for ternary; jobs.ts:376-379,
+ * 421-424) and then run as hq_phase runs them.  Every output is the number quantize_x + the kernel give. */
+int32_t hq_matmuls(const void *x, int32_t x_stride, const double *jobs, int32_t count, int32_t stride, void *stream);
+
+/* The ceilings the kernels are measured against (no counterpart on this path: the reference's CPU ceiling loops,
+ * kernels/ceilings.ts:12-25 and ceilings_relaxed.ts:34-52, are its model).  hq_ceiling_read reads every byte of
+ * [p, p + bytes) once (bytes a multiple of 16): time it for the achievable HBM read bandwidth of a buffer past the
+ * caches.  hq_ceiling_mfma runs `iterations` x 8 v_mfma_i32_32x32x32_i8 (32768 MACs each) in every wave of `blocks`
+ * blocks of 4 waves, on registers: the achievable dense int8 rate.  sink: 256 int32 of scratch, almost never
+ * written. */
+int32_t hq_ceiling_read(const void *p, int64_t bytes, void *sink, void *stream);
+int32_t hq_ceiling_mfma(int32_t blocks, int32_t iterations, void *sink, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -18,7 +18,7 @@ CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 OBJ = os.path.join(HERE, "_build")
 LIBRARY = os.path.join(HERE, "libhq.so")
-SOURCES = ["quantize.hip", "gemv.hip", "gemm.hip", "abi.cpp"]
+SOURCES = ["quantize.hip", "gemv.hip", "gemm.hip", "ceilings.hip", "abi.cpp"]
 
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 FLAGS = [

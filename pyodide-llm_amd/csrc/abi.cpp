@@ -269,20 +269,23 @@ int32_t hq_matmul_t2r_tile_ex(void *xout, const void *xq, const void *xs, const 
 }
 
 // ---- a phase of jobs in the reference's table form ------------------------------------------------------------
-int32_t hq_phase(const double *jobs, int32_t count, int32_t stride, void *stream) {
-  g_error = HQ_OK;
+}  // extern "C"
+
+namespace {
+
+// [kind, out, a, b, a4, a5, a6, a7, a8, rows, count, os, as, bs] (src/runtime/jobs.ts:46, 207-333) -> a Job
+int32_t parse_jobs(const double *jobs, int32_t count, int32_t stride, std::vector<hq::Job> by_kind[10],
+                   const char *who) {
   if (count < 0 || (count > 0 && (!jobs || stride < 14)))
-    return fail(HQ_ERR_ARGUMENT, "hq_phase: count %d, stride %d (a job has 14 numbers at least)", count, stride);
-  std::vector<hq::Job> by_kind[10];
+    return fail(HQ_ERR_ARGUMENT, "%s: count %d, stride %d (a job has 14 numbers at least)", who, count, stride);
   for (int32_t i = 0; i < count; i++) {
     const double *e = jobs + (int64_t)i * stride;
     for (int q = 0; q < 14; q++) {
       if (!(e[q] >= 0.0 && e[q] < 9007199254740992.0 && e[q] == std::floor(e[q])))
-        return fail(HQ_ERR_ARGUMENT, "hq_phase: job %d's number %d (%g) is not an address or count", i, q, e[q]);
+        return fail(HQ_ERR_ARGUMENT, "%s: job %d's number %d (%g) is not an address or count", who, i, q, e[q]);
     }
     const int32_t kind = (int32_t)e[0];
     auto at = [&](int q) { return (const char *)(uintptr_t)(uint64_t)e[q]; };
-    // [kind, out, a, b, a4, a5, a6, a7, a8, rows, count, os, as, bs] (src/runtime/jobs.ts:46, 207-333)
     hq::Job j{(char *)at(1), at(2), at(3), at(4), at(5), nullptr, (int32_t)e[7], 0, (int32_t)e[9], (int32_t)e[10],
               (int64_t)e[11], (int64_t)e[12], (int64_t)e[13]};
     hq::Kind k;
@@ -293,11 +296,22 @@ int32_t hq_phase(const double *jobs, int32_t count, int32_t stride, void *stream
     case hq::Q6: k = hq::Q6; break;
     case hq::T2R: k = hq::T2R; j.sframe = j.count > 1 ? j.frame : j.sframe; break;  // its tile
     case hq::T2: k = hq::T2; break;
-    default: return fail(HQ_ERR_KIND, "hq_phase: job %d is of kind %d, which this library does not run", i, kind);
+    default: return fail(HQ_ERR_KIND, "%s: job %d is of kind %d, which this library does not run", who, i, kind);
     }
     if (int32_t st = check_job(k, j, 3)) return st;
     by_kind[kind].push_back(j);
   }
+  return HQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t hq_phase(const double *jobs, int32_t count, int32_t stride, void *stream) {
+  g_error = HQ_OK;
+  std::vector<hq::Job> by_kind[10];
+  if (int32_t st = parse_jobs(jobs, count, stride, by_kind, "hq_phase")) return st;
   if (count > 0) {
     if (int32_t st = ensure_device()) return st;
   }
@@ -306,6 +320,88 @@ int32_t hq_phase(const double *jobs, int32_t count, int32_t stride, void *stream
     if (int32_t st = run_jobs((hq::Kind)kind, by_kind[kind], stream_of(stream))) return st;
   }
   return HQ_OK;
+}
+
+int32_t hq_matmuls(const void *x, int32_t x_stride, const double *jobs, int32_t count, int32_t stride, void *stream) {
+  g_error = HQ_OK;
+  std::vector<hq::Job> by_kind[10];
+  if (int32_t st = parse_jobs(jobs, count, stride, by_kind, "hq_matmuls")) return st;
+  if (count == 0) return HQ_OK;
+  // one input: every job of one n and one token count
+  int32_t n = -1, tokens = -1;
+  for (auto &list : by_kind)
+    for (const hq::Job &j : list) {
+      if (n < 0) n = j.n, tokens = j.count;
+      if (j.n != n || j.count != tokens)
+        return fail(HQ_ERR_ARGUMENT, "hq_matmuls: the jobs take one input (n %d and %d tokens, and %d, %d)", n,
+                    tokens, j.n, j.count);
+    }
+  if (tokens == 0) return HQ_OK;
+  if (!x) return fail(HQ_ERR_NULL, "hq_matmuls: x is NULL");
+  if (!aligned(x, 16) || (tokens > 1 && (x_stride < 0 || x_stride % 16)))
+    return fail(HQ_ERR_ALIGNMENT, "hq_matmuls: x or x_stride not 16-byte aligned");
+  if (int32_t st = ensure_device()) return st;
+  const hipStream_t s = stream_of(stream);
+  for (int kind = 0; kind < 10; kind++) {
+    auto &list = by_kind[kind];
+    if (list.empty()) continue;
+    const hq::Kind k = (hq::Kind)kind;
+    if (relaxed(k) && tokens <= hq::kGemvMaxTokens) {
+      // quantize_x in every block of the products (tokens split where their activations do not fit the LDS)
+      const int32_t per = (int64_t)tokens * (n + n / 8) <= 65536 ? tokens : 1;
+      for (int32_t t0 = 0; t0 < tokens; t0 += per)
+        for (int w = 0; w < 2; w++) {
+          std::vector<hq::Job> part;
+          for (const hq::Job &j : list)
+            if ((j.wc != nullptr) == (w == 1)) {
+              hq::Job q = j;
+              q.count = per;
+              q.out = j.out + t0 * j.os;
+              part.push_back(q);
+            }
+          for (size_t i = 0; i < part.size(); i += hq::kMaxJobs) {
+            const int32_t m = (int32_t)(part.size() - i < (size_t)hq::kMaxJobs ? part.size() - i : hq::kMaxJobs);
+            const int32_t st = hip_status(
+                hq::launch_gemv_fused(k, &part[i], m, (const char *)x + (int64_t)t0 * x_stride, x_stride, s),
+                kind_name(k));
+            if (st) return st;
+          }
+        }
+      continue;
+    }
+    // the others: ready() into each job's xq / xs (jobs.ts:376-379, 421-424), then the phase
+    for (const hq::Job &j : list) {
+      const int32_t bias = relaxed(k) ? 64 : 0;
+      if (int32_t st = hip_status(hq::launch_quantize_x((char *)j.xq, (char *)j.xs, (const char *)x, n, bias, tokens,
+                                                        j.frame, x_stride, s),
+                                  "quantize_x"))
+        return st;
+      if (ternary(k)) {
+        if (int32_t st = hip_status(hq::launch_interleave((char *)j.xq, (char *)j.xs, n, tokens, j.frame, s), "interleave"))
+          return st;
+      }
+    }
+    if (int32_t st = run_jobs(k, list, s)) return st;
+  }
+  return HQ_OK;
+}
+
+// ---- the ceilings ---------------------------------------------------------------------------------------------
+int32_t hq_ceiling_read(const void *p, int64_t bytes, void *sink, void *stream) {
+  g_error = HQ_OK;
+  if (bytes <= 0 || bytes % 16) return fail(HQ_ERR_ARGUMENT, "hq_ceiling_read: bytes = %lld", (long long)bytes);
+  if (!p || !sink) return fail(HQ_ERR_NULL, "hq_ceiling_read: a NULL pointer");
+  if (!aligned(p, 16) || !aligned(sink, 4)) return fail(HQ_ERR_ALIGNMENT, "hq_ceiling_read: misaligned");
+  if (int32_t st = ensure_device()) return st;
+  return hip_status(hq::launch_ceiling_read((const char *)p, bytes, (uint32_t *)sink, stream_of(stream)), "ceiling_read");
+}
+
+int32_t hq_ceiling_mfma(int32_t blocks, int32_t iterations, void *sink, void *stream) {
+  g_error = HQ_OK;
+  if (blocks <= 0 || iterations <= 0) return fail(HQ_ERR_ARGUMENT, "hq_ceiling_mfma: %d blocks, %d iterations", blocks, iterations);
+  if (!sink || !aligned(sink, 4)) return fail(HQ_ERR_NULL, "hq_ceiling_mfma: sink");
+  if (int32_t st = ensure_device()) return st;
+  return hip_status(hq::launch_ceiling_mfma(blocks, iterations, (int32_t *)sink, stream_of(stream)), "ceiling_mfma");
 }
 
 // ---- the drop-in names: the library's stream, errors kept for hq_last_error() ---------------------------------

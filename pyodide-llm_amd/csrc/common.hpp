@@ -60,6 +60,44 @@ HQ_DEV int32_t trunc_sat(float v) {
   return (int32_t)v;
 }
 
+// kernels/kernel/quantize.ts:124-151 for one group of 32 float32 values at p (16-byte aligned): its 32 bytes (eight
+// dwords, values 4i..4i+3 in dword i) and its scale.  groupMax (quantize.ts:10-19): lane j's maximum of |values 4i + j|
+// with a NaN kept (a non-negative float's bits order as the float does, and every NaN's bits are above +inf's), then
+// lanes 1..3 compared with lane 0's in order, where a NaN is passed over.
+HQ_DEV void quantize_group(const float *p, int32_t bias, uint32_t q[8], float &scale) {
+  float v[32];
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const float4 f = ((const float4 *)p)[i];
+    v[4 * i] = f.x; v[4 * i + 1] = f.y; v[4 * i + 2] = f.z; v[4 * i + 3] = f.w;
+  }
+  uint32_t m[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int i = 0; i < 8; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) m[j] = max(m[j], __float_as_uint(v[4 * i + j]) & 0x7fffffffu);
+  float amax = __uint_as_float(m[0]);
+#pragma unroll
+  for (int j = 1; j < 4; j++) {
+    const float mj = __uint_as_float(m[j]);
+    if (mj > amax) amax = mj;
+  }
+  scale = fdiv(amax, bias == 0 ? 127.0f : 63.0f);
+  const float inv = scale > 0.0f ? fdiv(1.0f, scale) : 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    uint32_t d = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int32_t t = trunc_sat(rintf(fmul(v[4 * i + j], inv)));
+      int32_t r = (int32_t)((uint32_t)t + (uint32_t)bias);  // i32x4.add wraps
+      r = min(max(r, -128), 127);                           // the two saturating narrowings
+      d |= ((uint32_t)r & 0xffu) << (8 * j);
+    }
+    q[i] = d;
+  }
+}
+
 // v_perm_b32: byte i of the result is byte sel.i of {hi:lo} (0..3 from lo, 4..7 from hi)
 HQ_DEV uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) { return __builtin_amdgcn_perm(hi, lo, sel); }
 

@@ -19,6 +19,8 @@
 #include "common.hpp"
 #include "launch.hpp"
 
+#define HQ_HOST_DEV __host__ __device__
+
 namespace hq {
 
 namespace {
@@ -27,7 +29,42 @@ struct GemvBatch {
   Job job[kMaxJobs];
   int32_t block0[kMaxJobs + 1];  // the first block of each job
   int32_t njobs;
+  int32_t bias;          // FUSED: the activations' bias (quantize_x's)
+  const char *x;         // FUSED: token t's n float32 activations at x + t x_stride, shared by every job
+  int64_t x_stride;
 };
+
+// where a kernel's activations come from: the caller's xq / xs in global memory (read through the L1), a copy of
+// them the block makes in LDS, or the block's own quantize_x of the float32 activations into LDS (one launch a
+// phase, as the reference's matmulsAlike quantizes once and runs the phase, src/runtime/forward/engine.ts:398-407)
+enum Src { GLOBAL = 0, STAGED = 1, FUSED = 2 };
+
+// the LDS a block needs for T tokens of n activations (bytes, then float32 scales)
+HQ_HOST_DEV constexpr int64_t act_lds_bytes(int T, int n) { return (int64_t)T * (n + 4 * (n / 32)); }
+
+// STAGED / FUSED: fill the block's LDS with the activations of T tokens: bytes of token t at lq + t n, scales at
+// ls + t (n / 32).  Every thread takes groups of 32 in turn; the block synchronizes after.
+template <int T, int SRC>
+HQ_DEV void fill_acts(const GemvBatch &b, const Job &J, char *lq, float *ls) {
+  const int n = J.n, ng = n >> 5;
+  for (int idx = threadIdx.x; idx < T * ng; idx += blockDim.x) {
+    const int t = idx / ng, g = idx - t * ng;
+    uint32_t q[8];
+    float sc;
+    if (SRC == FUSED) {
+      quantize_group((const float *)(b.x + t * b.x_stride) + g * GS, b.bias, q, sc);
+    } else {
+      const uint4 a = *(const uint4 *)(J.xq + t * J.frame + g * GS), c = *(const uint4 *)(J.xq + t * J.frame + g * GS + 16);
+      q[0] = a.x; q[1] = a.y; q[2] = a.z; q[3] = a.w; q[4] = c.x; q[5] = c.y; q[6] = c.z; q[7] = c.w;
+      sc = ((const float *)(J.xs + t * J.sframe))[g];
+    }
+    uint4 *dst = (uint4 *)(lq + t * n + g * GS);
+    dst[0] = make_uint4(q[0], q[1], q[2], q[3]);
+    dst[1] = make_uint4(q[4], q[5], q[6], q[7]);
+    ls[t * ng + g] = sc;
+  }
+  __syncthreads();
+}
 
 constexpr int kRowsPerBlock = 16;
 
@@ -40,11 +77,26 @@ HQ_DEV int job_of(const GemvBatch &b, int blk) {
 HQ_DEV uint4 ld16(const char *p) { return *(const uint4 *)p; }
 HQ_DEV uint2 ld8(const char *p) { return *(const uint2 *)p; }
 
+// the weights are read once a launch: loads that do not keep them in the caches (HQ_GEMV_NT) leave the caches to
+// the activations
+#ifndef HQ_GEMV_NT
+#define HQ_GEMV_NT 0
+#endif
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+HQ_DEV uint4 ldw16(const char *p) {
+#if HQ_GEMV_NT
+  const u32x4 v = __builtin_nontemporal_load((const u32x4 *)p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+#else
+  return *(const uint4 *)p;
+#endif
+}
+
 // the 32 weight bytes of group g of a row, as eight dwords of int8 (int6 groups widened, kernels/six.ts)
 template <int PACK>
 HQ_DEV void load_group(const char *wrow, int g, uint32_t w[8]) {
   if (PACK == 8) {
-    const uint4 a = ld16(wrow + g * 32), b = ld16(wrow + g * 32 + 16);
+    const uint4 a = ldw16(wrow + g * 32), b = ldw16(wrow + g * 32 + 16);
     w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
     w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
   } else {
@@ -64,30 +116,100 @@ HQ_DEV void load_acts(const char *xq, int g, uint32_t x[8]) {
 // ---------------------------------------------------------------------------------------------------------------
 // relaxed int8 / int6 (matmul_q8r, matmul_q6r; T tokens of the tile)
 // ---------------------------------------------------------------------------------------------------------------
-// the group's integer dot(w, q - 64): with the caller's correction (wc: dot(w, q) + wc, relaxed/int8.ts:37), or
-// with -64 sum(w) made here when wc is NULL (the same integer whenever wc is int8_sums' / six_sums')
-template <int T, bool WC>
-HQ_DEV void relaxed_terms(const uint32_t w[8], const char *const xq[T], const char *const xs[T], float ws, int32_t wc,
-                          int g, float p[T]) {
-  int32_t wsum = 0;
-  if (!WC) {
-#pragma unroll
-    for (int i = 0; i < 8; i++) wsum = sdot4((int32_t)w[i], 0x01010101, wsum);
+// Memory-level parallelism: a lane's steps are taken U at a time (a chunk: its weights and scales, and from global
+// memory its activations, loaded into registers together), and the next chunk's loads are issued before the current
+// chunk is computed, so a wave keeps two chunks of loads in flight.  The compiler cannot unroll the step loop itself
+// (the DPP moves are convergent), so the two chunk buffers alternate by hand.
+template <int T, int SRC>
+struct ActSource {
+  const char *xq[T];
+  const char *xs[T];
+  const char *lq;  // LDS: token t's bytes at lq + t n, scales at ls + t ng
+  const float *ls;
+  int n, ng;
+  HQ_DEV void get(int t, int g, uint32_t x[8]) const {
+    const char *p = SRC == GLOBAL ? xq[t] + g * 32 : lq + t * n + g * 32;
+    const uint4 a = *(const uint4 *)p, b = *(const uint4 *)(p + 16);
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
   }
-#pragma unroll
-  for (int t = 0; t < T; t++) {
-    uint32_t x[8];
-    load_acts(xq[t], g, x);
-    int32_t d = WC ? wc : -64 * wsum;
-#pragma unroll
-    for (int i = 0; i < 8; i++) d = sdot4((int32_t)w[i], (int32_t)x[i], d);
-    const float s = fmul(ws, ((const float *)xs[t])[g]);
-    p[t] = fmul((float)d, s);
-  }
-}
+  HQ_DEV float scale(int t, int g) const { return SRC == GLOBAL ? ((const float *)xs[t])[g] : ls[t * ng + g]; }
+};
 
-template <int PACK, int T, bool WC>
+template <int PACK, int T, bool WC, int SRC>
+struct RelaxedChunk {
+  static constexpr bool ACTS = SRC == GLOBAL;  // activations prefetched with the weights (else read from LDS)
+#ifndef HQ_GEMV_U
+#define HQ_GEMV_U 4
+#endif
+  static constexpr int U = ACTS ? (T == 1 ? HQ_GEMV_U : (T == 2 ? 2 : 1)) : (T == 1 ? 2 * HQ_GEMV_U : (T == 2 ? 4 : 2));
+  uint32_t w[U][8];
+  uint32_t x[ACTS ? U : 1][ACTS ? T : 1][8];
+  float ws[U], xs[ACTS ? U : 1][ACTS ? T : 1];
+  int32_t wc[U];
+
+  // steps it0 .. it0 + U - 1 of this lane (its group 16 it + lane of each; a lane past the row's fours reads group
+  // 0 again, whose term it drops)
+  HQ_DEV void load(const char *wrow, const float *srow, const int32_t *crow, const ActSource<T, SRC> &A, int it0,
+                   int lane, int ng4) {
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int g = (it0 + u) * 16 + lane;
+      const int gl = g < ng4 ? g : 0;
+      load_group<PACK>(wrow, gl, w[u]);
+      ws[u] = srow[gl];
+      if (WC) wc[u] = crow[gl];
+      if (ACTS) {
+#pragma unroll
+        for (int t = 0; t < T; t++) {
+          A.get(t, gl, x[u][t]);
+          xs[u][t] = A.scale(t, gl);
+        }
+      }
+    }
+  }
+
+  // the chunk's terms, folded into the lanes' sums: lane k takes groups 16 it + k, + 4, + 8, + 12 in order
+  // (relaxed/int8.ts:26-39)
+  HQ_DEV void fold(float acc[T], const ActSource<T, SRC> &A, int it0, int lane, int ng4) const {
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int g = (it0 + u) * 16 + lane;
+      const bool valid = g < ng4;
+      const int gl = valid ? g : 0;
+      int32_t wsum = 0;
+      if (!WC) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) wsum = sdot4((int32_t)w[u][i], 0x01010101, wsum);
+      }
+#pragma unroll
+      for (int t = 0; t < T; t++) {
+        uint32_t xl[8];
+        float sx;
+        if (ACTS) {
+#pragma unroll
+          for (int i = 0; i < 8; i++) xl[i] = x[u][t][i];
+          sx = xs[u][t];
+        } else {
+          A.get(t, gl, xl);
+          sx = A.scale(t, gl);
+        }
+        int32_t d = WC ? wc[u] : -64 * wsum;
+#pragma unroll
+        for (int i = 0; i < 8; i++) d = sdot4((int32_t)w[u][i], (int32_t)xl[i], d);
+        const float p = fmul((float)d, fmul(ws[u], sx));
+        const float q = valid ? p : 0.0f;  // +0 leaves a lane as it is: a lane is never -0
+        float a = fadd(acc[t], q);
+        a = fadd(a, from_lane_plus<4>(q));
+        a = fadd(a, from_lane_plus<8>(q));
+        acc[t] = fadd(a, from_lane_plus<12>(q));
+      }
+    }
+  }
+};
+
+template <int PACK, int T, bool WC, int SRC>
 __global__ __launch_bounds__(256) void gemv_relaxed(GemvBatch batch) {
+  extern __shared__ __align__(16) char lds[];
   const int jb = job_of(batch, blockIdx.x);
   const Job &J = batch.job[jb];
   const int lane = threadIdx.x & 15;
@@ -99,34 +221,32 @@ __global__ __launch_bounds__(256) void gemv_relaxed(GemvBatch batch) {
   const char *wrow = J.wq + (int64_t)row * ng * GB;
   const float *srow = (const float *)J.ws + (int64_t)row * ng;
   const int32_t *crow = WC ? (const int32_t *)J.wc + (int64_t)row * ng : nullptr;
-  const char *xq[T];
-  const char *xs[T];
+  ActSource<T, SRC> A;
 #pragma unroll
   for (int t = 0; t < T; t++) {
-    xq[t] = J.xq + t * J.frame;
-    xs[t] = J.xs + t * J.sframe;
+    A.xq[t] = J.xq + t * J.frame;
+    A.xs[t] = J.xs + t * J.sframe;
   }
+  A.lq = lds;
+  A.ls = (const float *)(lds + T * J.n);
+  A.n = J.n;
+  A.ng = ng;
 
   float acc[T];
 #pragma unroll
   for (int t = 0; t < T; t++) acc[t] = 0.0f;
+  using Chunk = RelaxedChunk<PACK, T, WC, SRC>;
+  constexpr int U = Chunk::U;
   const int steps = (ng4 + 15) >> 4;
-  for (int it = 0; it < steps; ++it) {
-    const int g = it * 16 + lane;
-    const bool valid = g < ng4;
-    const int gl = valid ? g : 0;
-    uint32_t w[8];
-    load_group<PACK>(wrow, gl, w);
-    float p[T];
-    relaxed_terms<T, WC>(w, xq, xs, srow[gl], WC ? crow[gl] : 0, gl, p);
-#pragma unroll
-    for (int t = 0; t < T; t++) {
-      const float q = valid ? p[t] : 0.0f;  // +0 leaves a lane as it is: a lane is never -0
-      // lane k: groups 16 it + k, + 4, + 8, + 12 in order (relaxed/int8.ts:26-39)
-      float a = fadd(acc[t], q);
-      a = fadd(a, from_lane_plus<4>(q));
-      a = fadd(a, from_lane_plus<8>(q));
-      acc[t] = fadd(a, from_lane_plus<12>(q));
+  Chunk a, b;
+  if (steps > 0) a.load(wrow, srow, crow, A, 0, lane, ng4);  // the first weights in flight during the staging
+  if (SRC != GLOBAL) fill_acts<T, SRC>(batch, J, lds, (float *)(lds + T * J.n));
+  for (int it = 0; it < steps; it += 2 * U) {
+    if (it + U < steps) b.load(wrow, srow, crow, A, it + U, lane, ng4);
+    a.fold(acc, A, it, lane, ng4);
+    if (it + U < steps) {
+      if (it + 2 * U < steps) a.load(wrow, srow, crow, A, it + 2 * U, lane, ng4);
+      b.fold(acc, A, it + U, lane, ng4);
     }
   }
   // lane 0: ((l0 + l1) + l2) + l3 (math.ts:7-9), then the groups past the fours one at a time (int8.ts:40-47)
@@ -139,13 +259,23 @@ __global__ __launch_bounds__(256) void gemv_relaxed(GemvBatch batch) {
     const int g = ng4 + (lane < tail ? lane : 0);
     uint32_t w[8];
     load_group<PACK>(wrow, g, w);
-    float p[T];
-    relaxed_terms<T, WC>(w, xq, xs, srow[g], WC ? crow[g] : 0, g, p);
+    int32_t wsum = 0;
+    if (!WC) {
+#pragma unroll
+      for (int i = 0; i < 8; i++) wsum = sdot4((int32_t)w[i], 0x01010101, wsum);
+    }
+    const float ws = srow[g];
 #pragma unroll
     for (int t = 0; t < T; t++) {
-      sum[t] = fadd(sum[t], p[t]);
-      if (tail > 1) sum[t] = fadd(sum[t], from_lane_plus<1>(p[t]));
-      if (tail > 2) sum[t] = fadd(sum[t], from_lane_plus<2>(p[t]));
+      uint32_t x[8];
+      A.get(t, g, x);
+      int32_t d = WC ? crow[g] : -64 * wsum;
+#pragma unroll
+      for (int i = 0; i < 8; i++) d = sdot4((int32_t)w[i], (int32_t)x[i], d);
+      const float p = fmul((float)d, fmul(ws, A.scale(t, g)));
+      sum[t] = fadd(sum[t], p);
+      if (tail > 1) sum[t] = fadd(sum[t], from_lane_plus<1>(p));
+      if (tail > 2) sum[t] = fadd(sum[t], from_lane_plus<2>(p));
     }
   }
   if (live && lane == 0) {
@@ -334,18 +464,28 @@ __global__ __launch_bounds__(256) void gemv_ternary(GemvBatch batch) {
   }
 }
 
+template <int PACK, int T, int SRC>
+hipError_t launch_relaxed(const GemvBatch &b, int blocks, bool wc, size_t lds, hipStream_t s) {
+  dim3 grid(blocks), block(256);
+  if (wc) hipLaunchKernelGGL((gemv_relaxed<PACK, T, true, SRC>), grid, block, lds, s, b);
+  else hipLaunchKernelGGL((gemv_relaxed<PACK, T, false, SRC>), grid, block, lds, s, b);
+  return hipGetLastError();
+}
+
 template <int T>
-hipError_t launch_t(Kind kind, const GemvBatch &b, int blocks, bool wc, hipStream_t s) {
+hipError_t launch_t(Kind kind, const GemvBatch &b, int blocks, bool wc, int src, size_t lds, hipStream_t s) {
   dim3 grid(blocks), block(256);
   switch (kind) {
   case Q8R:
-    if (wc) hipLaunchKernelGGL((gemv_relaxed<8, T, true>), grid, block, 0, s, b);
-    else hipLaunchKernelGGL((gemv_relaxed<8, T, false>), grid, block, 0, s, b);
-    break;
   case Q6R:
-    if (wc) hipLaunchKernelGGL((gemv_relaxed<6, T, true>), grid, block, 0, s, b);
-    else hipLaunchKernelGGL((gemv_relaxed<6, T, false>), grid, block, 0, s, b);
-    break;
+    if (kind == Q8R) {
+      if (src == FUSED) return launch_relaxed<8, T, FUSED>(b, blocks, wc, lds, s);
+      if (src == STAGED) return launch_relaxed<8, T, STAGED>(b, blocks, wc, lds, s);
+      return launch_relaxed<8, T, GLOBAL>(b, blocks, wc, 0, s);
+    }
+    if (src == FUSED) return launch_relaxed<6, T, FUSED>(b, blocks, wc, lds, s);
+    if (src == STAGED) return launch_relaxed<6, T, STAGED>(b, blocks, wc, lds, s);
+    return launch_relaxed<6, T, GLOBAL>(b, blocks, wc, 0, s);
   case Q8: hipLaunchKernelGGL((gemv_plain<8, T>), grid, block, 0, s, b); break;
   case Q6: hipLaunchKernelGGL((gemv_plain<6, T>), grid, block, 0, s, b); break;
   case T2R:
@@ -357,27 +497,54 @@ hipError_t launch_t(Kind kind, const GemvBatch &b, int blocks, bool wc, hipStrea
 
 }  // namespace
 
-// jobs: one kind, one token count (1..4), one wc-ness (all with corrections or all without)
-hipError_t launch_gemv(Kind kind, const Job *jobs, int32_t njobs, hipStream_t s) {
+// the largest activations (bytes and scales of all tokens) a block copies into LDS (STAGED) rather than reading
+// them through the L1
+#ifndef HQ_GEMV_STAGE_MAX
+#define HQ_GEMV_STAGE_MAX 0
+#endif
+
+namespace {
+hipError_t launch_batch(Kind kind, const Job *jobs, int32_t njobs, const char *x, int64_t x_stride, int32_t bias,
+                        hipStream_t s) {
   if (njobs < 1 || njobs > kMaxJobs) return hipErrorInvalidValue;
   GemvBatch b{};
-  int blocks = 0;
+  int blocks = 0, nmax = 0;
   for (int j = 0; j < njobs; j++) {
     b.job[j] = jobs[j];
     b.block0[j] = blocks;
     blocks += (jobs[j].r1 - jobs[j].r0 + kRowsPerBlock - 1) / kRowsPerBlock;
+    nmax = jobs[j].n > nmax ? jobs[j].n : nmax;
   }
   b.block0[njobs] = blocks;
   b.njobs = njobs;
+  b.x = x;
+  b.x_stride = x_stride;
+  b.bias = bias;
   if (blocks == 0) return hipSuccess;
   const bool wc = jobs[0].wc != nullptr;
-  switch (jobs[0].count) {
-  case 1: return launch_t<1>(kind, b, blocks, wc, s);
-  case 2: return launch_t<2>(kind, b, blocks, wc, s);
-  case 3: return launch_t<3>(kind, b, blocks, wc, s);
-  case 4: return launch_t<4>(kind, b, blocks, wc, s);
+  const int T = jobs[0].count;
+  const size_t lds = (size_t)act_lds_bytes(T, nmax);
+  int src = x ? FUSED : (lds <= (size_t)HQ_GEMV_STAGE_MAX ? STAGED : GLOBAL);
+  switch (T) {
+  case 1: return launch_t<1>(kind, b, blocks, wc, src, lds, s);
+  case 2: return launch_t<2>(kind, b, blocks, wc, src, lds, s);
+  case 3: return launch_t<3>(kind, b, blocks, wc, src, lds, s);
+  case 4: return launch_t<4>(kind, b, blocks, wc, src, lds, s);
   default: return hipErrorInvalidValue;
   }
+}
+}  // namespace
+
+// jobs: one kind, one token count (1..4), one wc-ness (all with corrections or all without)
+hipError_t launch_gemv(Kind kind, const Job *jobs, int32_t njobs, hipStream_t s) {
+  return launch_batch(kind, jobs, njobs, nullptr, 0, 0, s);
+}
+
+// the same, the activations quantized by each block from token t's n float32 at x + t x_stride (relaxed kinds)
+hipError_t launch_gemv_fused(Kind kind, const Job *jobs, int32_t njobs, const char *x, int64_t x_stride,
+                             hipStream_t s) {
+  if (kind != Q8R && kind != Q6R) return hipErrorNotSupported;
+  return launch_batch(kind, jobs, njobs, x, x_stride, 64, s);
 }
 
 }  // namespace hq

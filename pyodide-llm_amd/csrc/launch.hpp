@@ -27,10 +27,19 @@ hipError_t launch_six_sums(int32_t *out, const char *w, int32_t groups, hipStrea
 // GEMV-shaped products (every job of one kind and one token count, 1..4; up to kMaxJobs jobs a launch)
 constexpr int kMaxJobs = 8;
 hipError_t launch_gemv(Kind kind, const Job *jobs, int32_t njobs, hipStream_t s);
+// the relaxed kinds with quantize_x fused: each block quantizes token t's n float32 activations at x + t x_stride
+// (bias 64) into LDS itself; the jobs' xq / xs are not read
+hipError_t launch_gemv_fused(Kind kind, const Job *jobs, int32_t njobs, const char *x, int64_t x_stride,
+                             hipStream_t s);
 
 // MFMA GEMM-shaped products (one job a launch; count > 4 tokens): the tiles of matmul_q8r_tile, matmul_q6r and
 // matmul_t2r_tile over a prompt.  Returns hipErrorNotSupported for a kind that has none.
 hipError_t launch_gemm(Kind kind, const Job &job, hipStream_t s);
+
+// the ceilings (ceilings.hip): every byte of [p, p + bytes) read once; `iterations` x 8 MFMAs a wave of `blocks`
+// blocks of 4 waves.  sink: 256 words that are almost never written
+hipError_t launch_ceiling_read(const char *p, int64_t bytes, uint32_t *sink, hipStream_t s);
+hipError_t launch_ceiling_mfma(int32_t blocks, int32_t iterations, int32_t *sink, hipStream_t s);
 
 // which path a job of `count` tokens takes
 constexpr int kGemvMaxTokens = 4;

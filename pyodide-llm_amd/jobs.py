@@ -83,10 +83,21 @@ def job(kind, out, a, b, a4, a5, a6, a7, a8=0, rows=0, count=1, os=0, as_=0, bs=
     return [number, out, a, b, a4, a5, a6, a7, a8, rows, count, os, as_, bs, 0, 0]
 
 
-def phase(lib, jobs, stream=None):
-    """Run a phase of jobs (lists of 14..16 numbers) in one call of hq_phase; returns its status."""
-    table = (ctypes.c_double * (JOB * max(1, len(jobs))))()
+def table(jobs):
+    """The reference's job table (JOB float64 numbers a job) of a list of jobs."""
+    out = (ctypes.c_double * (JOB * max(1, len(jobs))))()
     for i, entry in enumerate(jobs):
         for q, value in enumerate(entry[:JOB]):
-            table[i * JOB + q] = float(value)
-    return lib.hq_phase(table, len(jobs), JOB, getattr(stream, "cuda_stream", stream))
+            out[i * JOB + q] = float(value)
+    return out
+
+
+def phase(lib, jobs, stream=None):
+    """Run a phase of jobs (lists of 14..16 numbers) in one call of hq_phase; returns its status."""
+    return lib.hq_phase(table(jobs), len(jobs), JOB, getattr(stream, "cuda_stream", stream))
+
+
+def matmuls(lib, x, x_stride, jobs, stream=None):
+    """engine.ts:381-407 (matmulsAlike): the jobs of one float32 input (device address x, token stride in bytes)
+    readied and run in one call of hq_matmuls; returns its status."""
+    return lib.hq_matmuls(x, x_stride, table(jobs), len(jobs), JOB, getattr(stream, "cuda_stream", stream))

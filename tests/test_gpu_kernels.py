@@ -441,3 +441,71 @@ def test_phase_matches_single_calls(pkg, k, arena, oracle):
     assert jobs.phase(pkg.library(), table) == 0, pkg.library().hq_last_error_message()
     for addr, want in wants:
         assert same_bits(arena.get(addr, F, want.size), want)
+
+
+# ---- hq_matmuls: quantize_x in the products' launch (relaxed kinds), ready() + phase for the others ----------
+@pytest.mark.parametrize("tokens", [1, 2, 3, 4, 7])
+@pytest.mark.parametrize("n", [288, 4096, 17408])
+def test_matmuls_relaxed(pkg, arena, oracle, tokens, n):
+    from pyodide_llm_amd import jobs
+    rng = np.random.default_rng(n + tokens)
+    ng = n // 32
+    x = rng.standard_normal((tokens, n)).astype(F)
+    x[0, 32:64] = 0
+    ax = arena.put(x)
+    table, wants = [], []
+    for kind, rows in (("matmul_q8r", 70), ("matmul_q8r_derived", 33), ("matmul_q6r", 50)):
+        six = kind == "matmul_q6r"
+        if six:
+            v = (4 * rng.integers(-32, 32, rows * n)).astype(np.int8)
+            wbytes, wc = pack6(v), oracle.six_sums(pack6(v))
+        else:
+            wbytes = rng.integers(-128, 128, rows * n).astype(np.int8)
+            wc = oracle.int8_sums(wbytes)
+        ws = (np.abs(rng.standard_normal(rows * ng)) * 0.02 / 127).astype(F)
+        os_ = 4 * rows
+        out = arena.alloc(os_ * tokens, fill=np.full(rows * tokens, -7, F))
+        scratch = arena.alloc(tokens * 2 * n)  # where ready() would put xq / xs (unused when fused)
+        wca = 0 if kind == "matmul_q8r_derived" else arena.put(wc)
+        name = "matmul_q6r" if six else "matmul_q8r"
+        table.append(jobs.job(name, out, scratch, scratch + n, arena.put(wbytes), arena.put(ws), wca, n, rows=rows,
+                              count=tokens, os=os_, as_=2 * n, bs=2 * n))
+        for t in range(tokens):
+            q, s = oracle.quantize_x(x[t], 64)
+            full = (oracle.matmul_q6r if six else oracle.matmul_q8r)(q, s, wbytes, ws, wc, n)
+            wants.append((out + t * os_, full, f"{kind} token {t}"))
+    L = pkg.library()
+    assert jobs.matmuls(L, ax, 4 * n, table) == 0, L.hq_last_error_message()
+    for addr, want, what in wants:
+        got = arena.get(addr, F, want.size)
+        assert same_bits(got, want), f"{what}: {first_difference(got, want)}"
+
+
+@pytest.mark.parametrize("tokens", [1, 3, 5])
+def test_matmuls_plain_and_ternary(pkg, arena, oracle, tokens):
+    from pyodide_llm_amd import jobs
+    rng = np.random.default_rng(40 + tokens)
+    n, rows = 1024, 40
+    ng = n // 32
+    x = rng.standard_normal((tokens, n)).astype(F)
+    ax = arena.put(x)
+    w = rng.integers(-127, 128, rows * n).astype(np.int8)
+    ws = (np.abs(rng.standard_normal(rows * ng)) * 0.02 / 127).astype(F)
+    codes = rng.integers(0, 3, rows * n).astype(np.uint8)
+    halves = (np.abs(rng.standard_normal(rows * (n // 128))) * 0.01).astype(np.float16).view(np.uint16)
+    frame = 2 * n
+    sq, st = arena.alloc(tokens * frame), arena.alloc(tokens * frame)
+    oq, ot = arena.alloc(4 * rows * tokens), arena.alloc(4 * rows * tokens)
+    table = [jobs.job("matmul_q8", oq, sq, sq + n, arena.put(w), arena.put(ws), 0, n, rows=rows, count=tokens,
+                      os=4 * rows, as_=frame, bs=frame),
+             jobs.job("matmul_t2r", ot, st, st + n, arena.put(pack_ternary(codes)), arena.put(halves), 0, n, rows=rows,
+                      count=tokens, os=4 * rows, as_=frame, bs=frame)]
+    L = pkg.library()
+    assert jobs.matmuls(L, ax, 4 * n, table) == 0, L.hq_last_error_message()
+    for t in range(tokens):
+        q0, s0 = oracle.quantize_x(x[t], 0)
+        want = oracle.matmul_q8(q0.view(np.int8), s0, w, ws, n)
+        assert same_bits(arena.get(oq + 4 * rows * t, F, rows), want)
+        xi, area = oracle.interleave(q0.view(np.int8), s0)
+        want_t = oracle.matmul_t2r(xi, area, pack_ternary(codes), halves, n)
+        assert same_bits(arena.get(ot + 4 * rows * t, F, rows), want_t)
