@@ -15,9 +15,12 @@
 // the last four one at a time (relaxed/int8.ts:40-47).  Each term is f(f(C) * f(ws * xs)) (int8) or
 // f(f(C * xs) * d) (ternary), rounded as the reference rounds it (-ffp-contract=off).
 //
-// Roofline: per output element and group the epilogue is 4 VALU operations (convert, two multiplies, add) against
-// 32 MACs on the matrix core; CDNA4's VALU does 64 lanes a clock a CU against 4096 int8 MACs, so the epilogue, not
-// the MFMA, bounds this kernel (at best 32 / (4 x 4096 / 64) = 12.5 % of dense int8 peak).
+// The scales' product of int8 / int6, f(ws * xs) for every (row, token), is an outer product: a
+// v_mfma_f32_32x32x2_f32 with K = 2 and its second column zero gives it, each product rounded once as v_mul_f32
+// rounds it (subnormals included), on the matrix core.  Roofline: per output element and group the epilogue is then
+// 3 VALU operations (convert, multiply, add; ternary 4: f(f(C * xs) * d) has no such product) against 32 MACs on the
+// matrix core; CDNA4's VALU does 64 lanes a clock a CU against 4096 int8 MACs, so the epilogue, not the MFMA, bounds
+// this kernel (at best 32 / (3 x 4096 / 64) = 16.7 % of dense int8 peak, 12.5 % for ternary).
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -27,6 +30,7 @@ namespace {
 
 typedef int32_t v4i __attribute__((ext_vector_type(4)));
 typedef int32_t v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
 
 constexpr int BR = 64, BT = 64;     // block tile: rows x tokens
 constexpr int XPAD = 128 + 16;      // LDS row of a stage's 128 bytes, padded against bank conflicts
@@ -112,15 +116,15 @@ struct LoaderQ {
   }
 };
 
-// one group's term for the wave's 16 outputs: C (the MFMA result with the correction in it) times ws * xs
-HQ_DEV void q_terms(const v16i &C, const StageQ &S, int k, int rbase, float xs, float out[16]) {
+// f(ws * xs) for the wave's 32 rows x 32 tokens of group k: the outer product on the matrix core (A lane l < 32: the
+// scale of row l, B lane l < 32: the scale of token l, the K = 1 half zero), laid out as the int8 MFMA's result
+HQ_DEV v16f q_scales(const StageQ &S, int k, int wrow, int wtok, int lane) {
+  const float a = lane < 32 ? S.ws[k][wrow + lane] : 0.0f;
+  const float b = lane < 32 ? S.xs[wtok + lane][k] : 0.0f;
+  v16f z;
 #pragma unroll
-  for (int q = 0; q < 4; q++) {
-    const float4 w4 = *(const float4 *)&S.ws[k][rbase + 8 * q];
-    const float wv[4] = {w4.x, w4.y, w4.z, w4.w};
-#pragma unroll
-    for (int e = 0; e < 4; e++) out[4 * q + e] = fmul((float)C[4 * q + e], fmul(wv[e], xs));
-  }
+  for (int r = 0; r < 16; r++) z[r] = 0.0f;
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, z, 0, 0, 0);
 }
 
 HQ_DEV v16i q_mfma(const StageQ &S, int k, int wrow, int wtok, int lane) {
@@ -138,7 +142,7 @@ HQ_DEV v16i q_mfma(const StageQ &S, int k, int wrow, int wtok, int lane) {
 }
 
 template <int PACK, bool WC>
-__global__ __launch_bounds__(256) void gemm_relaxed(Job J) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gemm_relaxed(Job J) {
   __shared__ StageQ stage[2];
   const int M = J.count;
   const int ng = J.n >> 5, ng4 = ng & ~3;
@@ -146,7 +150,6 @@ __global__ __launch_bounds__(256) void gemm_relaxed(Job J) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wrow = 32 * (wave >> 1), wtok = 32 * (wave & 1);
   const int rbase = wrow + 4 * (lane >> 5);   // this lane's first row in the tile (then + 8 q + e)
-  const int tok = wtok + (lane & 31);         // this lane's token in the tile
 
   float acc[4][16];
 #pragma unroll
@@ -164,17 +167,12 @@ __global__ __launch_bounds__(256) void gemm_relaxed(Job J) {
   for (int j = 0; j < stages; ++j) {
     const StageQ &S = stage[j & 1];
     if (j + 1 < stages) L.load(J, row0, tok0, M, j + 1, ng);
-    const float4 x4 = *(const float4 *)S.xs[tok];
-    const float xsv[4] = {x4.x, x4.y, x4.z, x4.w};
-    v16i C[4];
 #pragma unroll
-    for (int k = 0; k < 4; k++) C[k] = q_mfma(S, k, wrow, wtok, lane);
+    for (int k = 0; k < 4; k++) {  // group 4 j + k: the reference's lane k (relaxed/int8.ts:26-39)
+      const v16i C = q_mfma(S, k, wrow, wtok, lane);
+      const v16f sc = q_scales(S, k, wrow, wtok, lane);
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-      float p[16];
-      q_terms(C[k], S, k, rbase, xsv[k], p);
-#pragma unroll
-      for (int r = 0; r < 16; r++) acc[k][r] = fadd(acc[k][r], p[r]);
+      for (int r = 0; r < 16; r++) acc[k][r] = fadd(acc[k][r], fmul((float)C[r], sc[r]));
     }
     if (j + 1 < stages) L.store(stage[(j + 1) & 1]);
     __syncthreads();
@@ -187,17 +185,14 @@ __global__ __launch_bounds__(256) void gemm_relaxed(Job J) {
     L.store(stage[stages & 1]);
     __syncthreads();
     const StageQ &S = stage[stages & 1];
-    const float4 x4 = *(const float4 *)S.xs[tok];
-    const float xsv[4] = {x4.x, x4.y, x4.z, x4.w};
     for (int k = 0; k < ng - ng4; k++) {
       const v16i C = q_mfma(S, k, wrow, wtok, lane);
-      float p[16];
-      q_terms(C, S, k, rbase, xsv[k], p);
+      const v16f sc = q_scales(S, k, wrow, wtok, lane);
 #pragma unroll
-      for (int r = 0; r < 16; r++) sum[r] = fadd(sum[r], p[r]);
+      for (int r = 0; r < 16; r++) sum[r] = fadd(sum[r], fmul((float)C[r], sc[r]));
     }
   }
-  const int t = tok0 + tok;
+  const int t = tok0 + wtok + (lane & 31);  // this lane's token
   if (t < M) {
     float *out = (float *)(J.out + t * J.os);
 #pragma unroll
@@ -303,7 +298,7 @@ HQ_DEV v16i t_mfma(const StageT &S, int k, int wrow, int wtok, int lane) {
   return __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, C, 0, 0, 0);
 }
 
-__global__ __launch_bounds__(256) void gemm_ternary(Job J) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gemm_ternary(Job J) {
   __shared__ StageT stage[2];
   const int M = J.count;
   const int groups = J.n >> 7;
@@ -327,18 +322,16 @@ __global__ __launch_bounds__(256) void gemm_ternary(Job J) {
     const StageT &S = stage[g & 1];
     if (g + 1 < groups) L.load(J, row0, tok0, M, g + 1);
     const float d = S.d[row];
-    v16i C[4];
 #pragma unroll
-    for (int k = 0; k < 4; k++) C[k] = t_mfma(S, k, wrow, wtok, lane);
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
+    for (int k = 0; k < 4; k++) {  // part k of the group: the reference's lane k (relaxed/signs.ts:198-207)
+      const v16i C = t_mfma(S, k, wrow, wtok, lane);
 #pragma unroll
       for (int q = 0; q < 4; q++) {
         const float4 x4 = *(const float4 *)&S.xs[k][tbase + 8 * q];
         const float xv[4] = {x4.x, x4.y, x4.z, x4.w};
 #pragma unroll
         for (int e = 0; e < 4; e++)
-          acc[k][4 * q + e] = fadd(acc[k][4 * q + e], fmul(fmul((float)C[k][4 * q + e], xv[e]), d));
+          acc[k][4 * q + e] = fadd(acc[k][4 * q + e], fmul(fmul((float)C[4 * q + e], xv[e]), d));
       }
     }
     if (g + 1 < groups) L.store(stage[(g + 1) & 1]);
