@@ -252,18 +252,23 @@ def test_q8r_tile(k, arena, oracle, count, ng):
     ws[::11] = F(2.0 ** -130)
     ws[5::13] = 0
     wc = oracle.int8_sums(w)
+    # a caller's own corrections: int8_sums' values with a few groups moved (the kernels add whatever wc holds)
+    moved = wc.copy()
+    moved[rng.integers(0, rows * ng, 3)] += np.array([1, -5000, 77], np.int32)
     q = tile_inputs(oracle, rng, n, count, frame, rows)
-    wq, wsa, wca, xq = arena.put(w), arena.put(ws), arena.put(wc), arena.put(q)
-    for derived in (False, True):
+    wq, wsa, xq = arena.put(w), arena.put(ws), arena.put(q)
+    for form, corrections in (("int8_sums", wc), ("derived", None), ("moved", moved)):
+        wca = 0 if corrections is None else arena.put(corrections)
         for r0, r1 in [(0, rows), (3, 64 + 3), (5, 6)]:
             out = arena.alloc(os_ * count, fill=np.full(os_ * count // 4, -7, F))
-            k.matmul_q8r_tile(out, xq, xq + n, wq, wsa, 0 if derived else wca, n, r0, r1, count, os_, frame)
+            k.matmul_q8r_tile(out, xq, xq + n, wq, wsa, wca, n, r0, r1, count, os_, frame)
             got = arena.get(out, F, os_ * count // 4).reshape(count, -1)
             for t in range(count):
-                full = oracle.matmul_q8r(q[t, :n], q[t, n:n + 4 * ng].view(F), w, ws, wc, n)
+                full = oracle.matmul_q8r(q[t, :n], q[t, n:n + 4 * ng].view(F), w, ws,
+                                         wc if corrections is None else corrections, n)
                 want = np.full(os_ // 4, F(-7), F)
                 want[r0:r1] = full[r0:r1]
-                assert same_bits(got[t], want), f"count {count} ng {ng} rows {r0}..{r1} token {t} derived {derived}: " \
+                assert same_bits(got[t], want), f"count {count} ng {ng} rows {r0}..{r1} token {t} wc {form}: " \
                                                 f"{first_difference(got[t], want)}"
 
 
@@ -278,17 +283,20 @@ def test_q6r_many_tokens(pkg, arena, oracle, count):
     v = (4 * rng.integers(-32, 32, rows * n)).astype(np.int8)
     packed = pack6(v)
     ws = (rng.random(rows * ng) * 1e-3).astype(F)
-    wc = oracle.six_sums(packed)
+    sums = oracle.six_sums(packed)
+    moved = sums.copy()
+    moved[[5, 600, rows * ng - 1]] += np.array([3, -64, 1 << 20], np.int32)
     q = tile_inputs(oracle, rng, n, count, frame, rows)
-    wq, wsa, wca, xq = arena.put(packed, align=256), arena.put(ws), arena.put(wc), arena.put(q)
-    out = arena.alloc(4 * rows * count, fill=np.full(rows * count, -7, F))
-    job = jobs.job("matmul_q6r", out, xq, xq + n, wq, wsa, wca, n, rows=rows, count=count, os=4 * rows, as_=frame,
-                   bs=frame)
-    assert jobs.phase(pkg.library(), [job]) == 0, pkg.library().hq_last_error_message()
-    got = arena.get(out, F, rows * count).reshape(count, rows)
-    for t in range(count):
-        want = oracle.matmul_q6r(q[t, :n], q[t, n:n + 4 * ng].view(F), packed, ws, wc, n)
-        assert same_bits(got[t], want), f"token {t}: {first_difference(got[t], want)}"
+    wq, wsa, xq = arena.put(packed, align=256), arena.put(ws), arena.put(q)
+    for form, wc in (("six_sums", sums), ("moved", moved)):
+        out = arena.alloc(4 * rows * count, fill=np.full(rows * count, -7, F))
+        job = jobs.job("matmul_q6r", out, xq, xq + n, wq, wsa, arena.put(wc), n, rows=rows, count=count, os=4 * rows,
+                       as_=frame, bs=frame)
+        assert jobs.phase(pkg.library(), [job]) == 0, pkg.library().hq_last_error_message()
+        got = arena.get(out, F, rows * count).reshape(count, rows)
+        for t in range(count):
+            want = oracle.matmul_q6r(q[t, :n], q[t, n:n + 4 * ng].view(F), packed, ws, wc, n)
+            assert same_bits(got[t], want), f"wc {form} token {t}: {first_difference(got[t], want)}"
 
 
 # ---- ternary -------------------------------------------------------------------------------------------------
