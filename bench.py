@@ -1,20 +1,24 @@
 """bench.py — the hot path's headline numbers on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-gemm]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-gemm] [--phases] [--mode phase|fused]
+    python bench.py --calibrate     (kernels of known traffic, for scaling rocprofv3's FETCH_SIZE / WRITE_SIZE)
 
 A step is one decode token of the Llama-3-8B-shaped Q8 path: per layer the reference's
 four phases (src/runtime/forward/attention.ts:173, ffn.ts:27-30): quantize_x of the input, then q / k / v
 (4096, 1024, 1024 rows x 4096) in one phase, o (4096 x 4096), gate and up (2 x 14336 x 4096) in one phase, down
 (4096 x 14336); 32 layers, then the classifier (128256 x 4096).  Every layer has its own weights (8.44 GB in all, far
 past the 256 MB Infinity Cache), int8 uniform in [-127, 127] with |N(0, 0.02)| / 127 scales, activations N(0, 1):
-synthetic, generated on the GPU from a seed.  The products are matmul_q8r's (relaxed form, quantize_x bias 64); each
-phase is one hq_matmuls() call (the reference's matmulsAlike: quantize_x inside the products' launch), the
+synthetic, generated on the GPU from a seed.  The products are matmul_q8r's (relaxed form, quantize_x bias 64): a phase
+is quantize_x of its input, then one hq_phase() call over the phase's jobs (the reference's ready() and phase()), the
 corrections derived in the kernel (wc = NULL: the same integers as int8_sums' wc, and 12.5 % fewer bytes).  Beside it:
-the same step as quantize_x then hq_phase(), without and with the caller's wc.
+the same step with the caller's wc, and with hq_matmuls() (quantize_x inside the products' launch, the reference's
+matmulsAlike; --mode fused makes it the headline).
 
 value: algorithmic bytes of a step (1.125 B a weight, the activations' bytes and scales, 4 B an output; jobs.ts:448-450)
 over the step's time, with all inputs resident in HBM.  The step runs as a HIP graph of its launches (captured once).
-roofline: the GEMV kernel alone, from HIP events around every phase launch of an eager pass of the same steps.
+roofline: the GEMV kernel alone: a graph of only a step's products launches, replayed between HIP events, gives its
+average launch duration; traffic: the HBM bytes a launch moves, from rocprofv3's counters
+(profiles/gemv_q8r_8b_decode_traffic.md).
 Also reported: the int8 prefill GEMM (config 3's M = 2048 over one layer's matrices) in TOPS against the dense int8
 MFMA peak, and the oracle (the C restatement, oracle/) on the host's cores as the CPU baseline.
 """
@@ -149,31 +153,46 @@ def measure_decode(torch, pkg, args, phases, fused, with_wc):
             g.replay()
         torch.cuda.synchronize()
         graph_s = (time.perf_counter() - t0) / args.steps
-        # the same K steps launched one by one, HIP events around every products launch: the GEMV kernel's times
-        events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in tables]
-        gemv_ms, launches = 0.0, 0
-        kinds = {}
-        t0 = time.perf_counter()
-        for step in range(args.steps):
-            run_step(lib, tables, handle, fused, events)
+        # the products alone: a graph of one step's products launches (no quantize_x; the activations are those the
+        # last step left), replayed K times between HIP events on this stream.  Its launches run back to back, so
+        # its time over its launches is the GEMV kernel's average duration (with the gaps between launches).
+        def products(subset):
+            gk = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gk, stream=stream):
+                for a, table, njobs, _ in subset:
+                    if fused:
+                        lib.hq_matmuls(a.x.data_ptr(), 4 * a.n, table, njobs, 16, handle)
+                    else:
+                        lib.hq_phase(table, njobs, 16, handle)
+            gk.replay()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(args.steps):
+                gk.replay()
+            e1.record(stream)
             torch.cuda.synchronize()
-            for i, ((e0, e1), t) in enumerate(zip(events, tables)):
-                ms = e0.elapsed_time(e1)
-                gemv_ms += ms
-                launches += 1
-                name = ["qkv", "o", "gate_up", "down"][i % 4] if i < 4 * LAYERS else "lm_head"
-                k = kinds.setdefault(name, [0.0, 0.0, 0])
-                k[0] += ms
-                k[1] += t[3]
-                k[2] += 1
+            return e0.elapsed_time(e1) * 1e-3 / args.steps
+
+        gemv_s = products(tables)
+        kinds = {}
+        if args.phases:  # each kind of phase on its own (a graph of at least 32 launches)
+            names = [["qkv", "o", "gate_up", "down"][i % 4] if i < 4 * LAYERS else "lm_head"
+                     for i in range(len(tables))]
+            for name in ("qkv", "o", "gate_up", "down", "lm_head"):
+                mine = [t for t, nm in zip(tables, names) if nm == name]
+                mine = mine * -(-32 // len(mine))
+                s = products(mine)
+                kinds[name] = {"us": round(1e6 * s / len(mine), 2),
+                               "GBps": round(sum(t[3] for t in mine) / s / 1e9, 1)}
+        pkg.check(lib.hq_last_error())
         pkg.check(lib.hq_set_stream(None))
     out["ms_per_step"] = 1e3 * graph_s
     out["GBps"] = step_bytes / graph_s / 1e9
-    out["gemv_avg_launch_us"] = 1e3 * gemv_ms / launches
+    out["gemv_avg_launch_us"] = 1e6 * gemv_s / len(tables)
     out["gemv_bytes_per_launch"] = step_bytes / len(tables)
-    out["gemv_GBps"] = step_bytes * args.steps / (gemv_ms * 1e-3) / 1e9
-    out["phases"] = {n: {"us": round(1e3 * v[0] / v[2], 2), "GBps": round(v[1] / (v[0] * 1e-3) / 1e9, 1)}
-                     for n, v in kinds.items()}
+    out["gemv_GBps"] = step_bytes / gemv_s / 1e9
+    if kinds:
+        out["phases"] = kinds
     return out
 
 
@@ -185,7 +204,9 @@ def measure_gemm(torch, pkg, args):
     M = 2048
     shapes = [(4096, HIDDEN), (1024, HIDDEN), (1024, HIDDEN), (HIDDEN, HIDDEN), (FFN, HIDDEN), (FFN, HIDDEN),
               (HIDDEN, FFN)]
-    mats = [Matrix(torch, gen, r, n) for r, n in shapes]
+    mats = [Matrix(torch, gen, r, n, wc=True) for r, n in shapes]
+    for m in mats:  # the caller's corrections, as the reference's loader makes them (tensors.ts:126-134)
+        pkg.check(lib.hq_int8_sums_ex(m.wc.data_ptr(), m.w.data_ptr(), m.rows * m.n // 32, None))
     acts = {}
     for n in (HIDDEN, FFN):
         x = torch.randn(M, n, device="cuda:0", generator=gen)
@@ -199,7 +220,7 @@ def measure_gemm(torch, pkg, args):
         for m, o in zip(mats, outs):
             buf, frame = acts[m.n]
             lib.hq_matmul_q8r_tile_ex(o.data_ptr(), buf.data_ptr(), buf.data_ptr() + m.n, m.w.data_ptr(),
-                                      m.ws.data_ptr(), None, m.n, 0, m.rows, M, 4 * m.rows, frame, None)
+                                      m.ws.data_ptr(), m.wc.data_ptr(), m.n, 0, m.rows, M, 4 * m.rows, frame, None)
 
     run()
     pkg.check(lib.hq_last_error())
@@ -216,9 +237,10 @@ def measure_gemm(torch, pkg, args):
     return {"M": M, "tops": ops / s / 1e12, "frac": ops / s / 1e12 / INT8_PEAK_TOPS, "ms_per_layer": s * 1e3}
 
 
-def cpu_baseline(args):
+def cpu_baseline(args, seconds=10.0):
     """The oracle's matmul_q8r (oracle/oracle.c: the reference arithmetic in C, scalar) on the host's cores, rows cut
-    as the reference's phase() cuts them, over one 8B layer's matrices (~245 MB, past the host's caches)."""
+    as the reference's phase() cuts them (4 chunks a thread, threads.ts:45), over one 8B layer's 7 matrices (~245 MB,
+    past the host's caches), pass after pass for about `seconds`: the bytes of all passes over their time."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
@@ -226,18 +248,50 @@ def cpu_baseline(args):
     rng = np.random.default_rng(9)
     shapes = [(4096, HIDDEN), (1024, HIDDEN), (1024, HIDDEN), (HIDDEN, HIDDEN), (FFN, HIDDEN), (FFN, HIDDEN),
               (HIDDEN, FFN)]
-    total_s, total_bytes = 0.0, 0.0
+    mats = []
     for rows, n in shapes:
         w = rng.integers(-127, 128, rows * n, dtype=np.int8)
         ws = (np.abs(rng.standard_normal(rows * n // 32)) * 0.02 / 127).astype(np.float32)
-        wc = oracle.int8_sums(w)
         xq, xs = oracle.quantize_x(rng.standard_normal(n).astype(np.float32), 64)
-        s = oracle.time_gemv("matmul_q8r", xq, xs, w, ws, wc, n, rows, threads, 3)
-        total_s += s
-        total_bytes += rows * n * 1.125 + n * 1.125 + 4 * rows
+        mats.append((rows, n, w, ws, oracle.int8_sums(w), xq, xs))
+    total_s, total_bytes, passes = 0.0, 0.0, 0
+    while total_s < seconds:
+        for rows, n, w, ws, wc, xq, xs in mats:
+            total_s += oracle.time_gemv("matmul_q8r", xq, xs, w, ws, wc, n, rows, threads, 1)
+            total_bytes += rows * n * 1.125 + n * 1.125 + 4 * rows
+        passes += 1
     return {"value": total_bytes / total_s / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": "oracle matmul_q8r (C restatement, scalar) over one Llama-3-8B layer's 7 matrices at M=1, "
-                      f"{threads} threads, fastest of 3 runs each"}
+            "sample": f"oracle matmul_q8r (C restatement, scalar) over one Llama-3-8B layer's 7 matrices at M=1 "
+                      f"(245 MB), {passes} passes in {total_s:.1f} s on {threads} threads"}
+
+
+def calibrate():
+    """Kernels of known traffic for the counters' scale: a device-to-device copy of 1 GiB (reads and writes 1 GiB)
+    and hq_ceiling_read over the same GiB (reads it), three times each."""
+    import torch
+    pkg = load_package()
+    lib = pkg.library()
+    size = 1 << 30
+    a = torch.empty(size, dtype=torch.uint8, device="cuda:0").fill_(1)
+    b = torch.empty_like(a)
+    sink = torch.zeros(256, dtype=torch.int32, device="cuda:0")
+    for _ in range(3):
+        b.copy_(a)
+        pkg.check(lib.hq_ceiling_read(a.data_ptr(), size, sink.data_ptr(), None))
+    torch.cuda.synchronize()
+    print(json.dumps({"calibrate": {"copy_bytes_read": size, "copy_bytes_written": size, "read_kernel_bytes": size}}))
+
+
+def traffic_per_launch():
+    """HBM bytes a launch of the headline GEMV kernel moves, as rocprofv3's FETCH_SIZE and WRITE_SIZE counted them
+    (scaled by the same counters over a copy of known size), from the summary in profiles/; None without one."""
+    path = os.path.join(ROOT, "profiles", "gemv_q8r_8b_decode_traffic.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
 
 
 def main():
@@ -250,7 +304,14 @@ def main():
     ap.add_argument("--mode", choices=("phase", "fused"), default="phase",
                     help="the headline's phases: quantize_x then hq_phase (the reference's ready() + phase()), or "
                          "hq_matmuls (quantize_x inside the products' launch)")
+    ap.add_argument("--phases", action="store_true",
+                    help="also time each kind of phase (q/k/v, o, gate/up, down, classifier) on its own")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="only run kernels of known traffic (for scaling rocprofv3's FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
+    if args.calibrate:
+        calibrate()
+        return
     if args.gpus != 1:
         print("bench.py measures one GPU: the path is built for one MI355X (rows would shard across GPUs with an "
               "all-gather of the outputs, which this build does not run); use --gpus 1", file=sys.stderr)
@@ -279,7 +340,7 @@ def main():
                                "configs[3])", "mode": args.mode,
                    "step_bytes": derived["step_bytes"], "parallelism": "1 GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_per_launch(),
                      "kernel": "gemv_relaxed<8,1,false,FUSED>" if args.mode == "fused" else "gemv_relaxed<8,1,false,GLOBAL>",
                      "avg_launch_us": round(derived["gemv_avg_launch_us"], 3),
                      "bytes_per_launch": round(derived["gemv_bytes_per_launch"])},
