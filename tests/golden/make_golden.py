@@ -1,0 +1,89 @@
+"""Writes tests/golden/golden.npz: small input / output vectors of every kernel on the path, computed by the oracle
+(oracle/, the C restatement of the reference arithmetic) from the reference tests' LCG streams (tests/int8-check.ts:116-117,
+seed 644; tests/ternary-check.ts:80-81, seed 231) and the stories15M shape of the first benchmark config (n = 288,
+24 of its 768 rows).  Arrays only (numpy.load with allow_pickle=False reads it).
+
+    python tests/golden/make_golden.py
+"""
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, os.path.join(ROOT, "oracle"))
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+import oracle  # noqa: E402
+from streams import LCG, pack6, pack_ternary, scale_rule  # noqa: E402
+
+F = np.float32
+ROWS, N, TOKENS = 24, 288, 6
+TN = 384  # ternary: 3 groups of 128
+
+
+def frames(qs, ss, n, area):
+    """tokens' bytes and their scale area in one buffer, a frame (16-byte multiple) a token"""
+    frame = (n + area + 15) // 16 * 16
+    buf = np.zeros((len(qs), frame), np.uint8)
+    for t, (q, s) in enumerate(zip(qs, ss)):
+        buf[t, :n] = np.asarray(q).view(np.uint8)
+        buf[t, n:n + s.nbytes] = s.view(np.uint8)
+    return buf, frame
+
+
+def make():
+    g = {}
+    rng = LCG(644)
+    x = np.array([((rng.next() % 20001) - 10000) * 3e-4 for _ in range(N)], F)
+    x[5], x[40] = F(0.0), F(-2.5)
+    g["x"] = x
+    for bias in (0, 64):
+        q, s = oracle.quantize_x(x, bias)
+        g[f"xq{bias}"], g[f"xs{bias}"] = q.view(np.uint8), s
+    w = np.array([(rng.next() & 255) - 128 for _ in range(ROWS * N)], np.int8)
+    w[:N] = -128
+    ws = np.array([scale_rule(rng, i) for i in range(ROWS * N // 32)], F)
+    g["w"], g["ws"] = w, ws
+    g["wc"] = oracle.int8_sums(w)
+    g["q8r"] = oracle.matmul_q8r(g["xq64"], g["xs64"], w, ws, g["wc"], N)
+    g["q8"] = oracle.matmul_q8(g["xq0"].view(np.int8), g["xs0"], w, ws, N)
+    # int6: 4 v, v in -32..31
+    v6 = np.array([4 * ((rng.next() & 63) - 32) for _ in range(ROWS * N)], np.int8)
+    p6 = pack6(v6)
+    g["w6"], g["wc6"] = p6, oracle.six_sums(p6)
+    g["q6r"] = oracle.matmul_q6r(g["xq64"], g["xs64"], p6, ws, g["wc6"], N)
+    g["q6"] = oracle.matmul_q6(g["xq0"].view(np.int8), g["xs0"], p6, ws, N)
+    # a prompt of TOKENS tokens for the tile: 7-bit bytes, scales by the rule
+    qs = [np.array([rng.next() & 127 for _ in range(N)], np.uint8) for _ in range(TOKENS)]
+    ss = [np.array([scale_rule(rng, j + t) for j in range(N // 32)], F) for t in range(TOKENS)]
+    buf, frame = frames(qs, ss, N, 4 * (N // 32))
+    g["tile_x"], g["tile_frame"] = buf, np.array([frame], np.int32)
+    g["tile_q8r"] = np.stack([oracle.matmul_q8r(q, s, w, ws, g["wc"], N) for q, s in zip(qs, ss)])
+    # ternary (seed 231): codes 0..2, float16 scales a group of 128, activations quantize_x(bias 0) + interleave
+    rt = LCG(231)
+    codes = np.array([rt.next() % 3 for _ in range(ROWS * TN)], np.uint8)
+    g["wt"] = pack_ternary(codes)
+    g["wst"] = np.array([(1e-3 * (1 + rt.next() % 1000)) for _ in range(ROWS * TN // 128)], np.float16).view(np.uint16)
+    xt = np.array([((rt.next() % 20001) - 10000) * 2e-4 for _ in range(TN)], F)
+    q, s = oracle.quantize_x(xt, 0)
+    tq, tarea = oracle.interleave(q.view(np.int8), s)
+    g["xt"], g["xtq"], g["xtarea"] = xt, tq.view(np.uint8), tarea
+    g["t2r"] = oracle.matmul_t2r(tq, tarea, g["wt"], g["wst"], TN)
+    tqs, tss = [], []
+    for t in range(TOKENS):
+        xx = np.array([((rt.next() % 20001) - 10000) * 2e-4 for _ in range(TN)], F)
+        q, s = oracle.quantize_x(xx, 0)
+        a, b = oracle.interleave(q.view(np.int8), s)
+        tqs.append(a)
+        tss.append(b)
+    tbuf, tframe = frames(tqs, tss, TN, 8 * (TN // 32))
+    g["ttile_x"], g["ttile_frame"] = tbuf, np.array([tframe], np.int32)
+    g["ttile_t2r"] = np.stack([oracle.matmul_t2r(a, b, g["wt"], g["wst"], TN) for a, b in zip(tqs, tss)])
+    return g
+
+
+if __name__ == "__main__":
+    g = make()
+    np.savez(os.path.join(HERE, "golden.npz"), **g)
+    print(f"wrote {len(g)} arrays, {sum(a.nbytes for a in g.values())} bytes")
