@@ -3,24 +3,20 @@
 //   a time: every (row, token) is matmul_q6r's number), matmul_t2r_tile (kernels/relaxed/signs.ts:232-297).
 //
 // The matrix core gives each group's exact integer: v_mfma_i32_32x32x32_i8 with K = 32 is one scale group of 32 (for
-// ternary, one part of 32 of a group of 128).
-//
-// Corrections (int8, int6).  The relaxed activations are 7-bit, 0..127 (the second factor of the reference's
-// relaxed_dot_i8x16_i7x16, kernels/relaxed/int8.ts:5-10, kernels/ceilings_relaxed.ts:6-8), biased by 64, and the
-// reference adds wc = int8_sums(w) = -64 sum(w) to each group's integer.  Staging subtracts the bias from the
-// activations (q - 64 lies in -64..63, an int8), so that dot(w, q - 64) is the corrected integer with the MFMA's
-// accumulator input 0.  A caller's wc may be anything, though: staging also keeps delta = wc + 64 sum(w) of every
-// (row, group), and a stage where any delta of the block is not 0 takes delta as the MFMA's accumulator input
-// (dot(w, q - 64) + delta = dot(w, q) + wc, wrapping in int32 as the reference's i32x4.add does).
-// Ternary: the accumulator input is interleave()'s sums of the part (one a token), as the reference adds them.
+// ternary, one part of 32 of a group of 128), and the correction rides in its accumulator input:
+//   int8 / int6 with the caller's wc: wc itself, so the integer is dot(w, q) + wc as the reference adds it
+//     (relaxed/int8.ts:37, wrapping in int32 like i32x4.add);
+//   int8 / int6 with wc == NULL: -64 sum(w), made by a second MFMA of the same weights against a constant -64
+//     (the value int8_sums would have given, exact for every byte);
+//   ternary: interleave()'s sums of the part (one a token), as the reference adds them.
 //
 // Float32 order: every (row, token) is the token kernel's number to the bit.  The reference's lane k adds groups
 // 4 j + k (int8, int6) or part k of every group (ternary), in order, and the four lanes are added
 // ((l0 + l1) + l2) + l3 at the end (math.ts:7-9), then (int8, int6) the groups past the last four one at a time
-// (relaxed/int8.ts:40-47).  Here a wave IS a lane k of the reference: the 4 waves of one 32 x 32 tile of (rows,
-// tokens) take chain k = 0..3 each, adding their groups / parts in order into 16 registers, and at the end add their
-// sums in LDS in that order.  Each term is f(f(C) * f(ws * xs)) (int8, int6) or f(f(f(C) * xs) * d) (ternary),
-// rounded as the reference rounds it (-ffp-contract=off).
+// (relaxed/int8.ts:40-47).  Here a wave IS a lane k of the reference: the 4 waves of one 32-row slice of the tile take
+// chain k = 0..3 each, adding their groups / parts in order into registers, and at the end add their sums through LDS
+// in that order.  Each term is f(f(C) * f(ws * xs)) (int8, int6) or f(f(f(C) * xs) * d) (ternary), rounded as the
+// reference rounds it (-ffp-contract=off).
 //
 // The scales' product of int8 / int6, f(ws * xs) for every (row, token), is an outer product: a
 // v_mfma_f32_32x32x2_f32 with K = 2 and its second column zero gives it, each product rounded once as v_mul_f32
@@ -29,10 +25,14 @@
 // matrix core; CDNA4's VALU does 64 lanes a clock a CU against 4096 int8 MACs, so the epilogue, not the MFMA, bounds
 // this kernel (at best 32 / (3 x 4096 / 64) = 16.7 % of dense int8 peak, 12.5 % for ternary).
 //
-// A block is 8 waves and a 64 x 32 tile of (rows, tokens): two 32 x 32 tiles x four chains.  A stage brings 8 groups
-// (int8, int6: two a chain) or 2 groups of 128 (ternary: part k of both for wave k) into LDS, double-buffered: the
-// next stage's global loads are in flight while the current one is computed, and a wave issues its second group's
-// MFMAs before its first group's epilogue.  Two blocks share a CU (64 KB of LDS each, at most 128 VGPRs a lane).
+// A block is 16 waves and a 128-row x 64-token tile: wave w takes rows 32 (w / 4) .. + 31 and chain w % 4, for both
+// 32-token halves (the weights' operand read once for two MFMAs).  The operands come into LDS by direct buffer-to-LDS
+// loads (no registers on the way), into a ring of 4 stage buffers: a stage is 4 groups (int8, int6) or 2 groups of
+// 128 (ternary), and the loads of stages s + 1 .. s + 3 are in flight while stage s is computed.  Every wave issues
+// exactly 3 loads a stage (some of them into a scratch area), so that one s_waitcnt vmcnt count means "my loads of
+// stage s have landed"; a bare s_barrier then makes them everyone's.  The 16-byte chunks of a row are stored XOR-
+// swizzled so that the MFMA operand reads (32 rows or tokens, one chunk each) spread over the LDS banks.  Blocks are
+// ordered so that the blocks one XCD runs at a time share their rows and tokens in that XCD's L2.
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -44,9 +44,11 @@ typedef int32_t v4i __attribute__((ext_vector_type(4)));
 typedef int32_t v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-constexpr int BR = 64, BT = 32;  // block tile: rows x tokens
-constexpr int NT = 512;          // threads a block: 2 tiles x 4 chains, a wave each
-
+constexpr int BR = 128, BT = 64;  // block tile: rows x tokens
+constexpr int NT = 1024;          // 16 waves: 4 slices of 32 rows x 4 chains
+constexpr int RING = 4;           // stage buffers
+constexpr int AHEAD = RING - 1;   // stages loaded beyond the one computed
+constexpr int LOADS = 3;          // loads a wave a stage
 
 HQ_DEV v16i zero16i() {
   v16i z;
@@ -61,218 +63,238 @@ HQ_DEV v16f zero16f() {
   return z;
 }
 
+// ---- loads -----------------------------------------------------------------------------------------------------
+// A block's rows, tokens and scales are each one buffer resource (base and size in scalar registers): a thread's
+// offsets are set once, a stage moves them by a scalar offset, and a load past the size reads nothing and returns
+// zeros (the tiles past the last row or token, the groups past the last one: their results are never stored).
+HQ_DEV __amdgpu_buffer_rsrc_t resource(const char *base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0,
+                                           (int)max((int64_t)0, min(bytes, (int64_t)0xFFFFFFFF)), 0x00020000);
+}
+// direct loads into LDS: lane l's `size` bytes land at dst + size * l (dst the same in the whole wave, in M0; 2-byte
+// loads land zero-extended in 4-byte slots).  Written as the instructions themselves: the compiler, which tracks
+// such loads only a few at a time, would otherwise wait for every one in flight before each LDS read; here the
+// waits are stage_ready's alone (which only these loads need: the loops issue no other vector memory operation).
+HQ_DEV uint32_t lds_address(void *p) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)p);
+}
+HQ_DEV void dma16(__amdgpu_buffer_rsrc_t r, void *dst, uint32_t vo, uint32_t so) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :: "s"(lds_address(dst)), "v"(vo), "s"(r), "s"(so) : "memory", "m0");
+}
+HQ_DEV void dma4(__amdgpu_buffer_rsrc_t r, void *dst, uint32_t vo, uint32_t so) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds"
+               :: "s"(lds_address(dst)), "v"(vo), "s"(r), "s"(so) : "memory", "m0");
+}
+HQ_DEV void dma2(__amdgpu_buffer_rsrc_t r, void *dst, uint32_t vo, uint32_t so) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_ushort %1, %2, %3 offen lds"
+               :: "s"(lds_address(dst)), "v"(vo), "s"(r), "s"(so) : "memory", "m0");
+}
+
+// the stage's loads have landed: wait until at most N of this wave's loads are outstanding (and its LDS reads are
+// done), then the block's barrier, which no memory operation is moved across
+template <int N>
+HQ_DEV void stage_ready() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt((N & 15) | 0x70 | ((N >> 4) << 14));  // vmcnt(N) expcnt(7) lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+// stage s of `total` loaded stages: the loads issued after its own are those of the next min(AHEAD - 1, ...) stages
+HQ_DEV void wait_for(int s, int total) {
+  const int later = min(AHEAD - 1, total - 1 - s);
+  if (later >= 2) stage_ready<2 * LOADS>();
+  else if (later == 1) stage_ready<LOADS>();
+  else stage_ready<0>();
+}
+
+// the 8 16-byte chunks of a row's 128 stage bytes: chunk c of row r is stored at c ^ swz(r), so that 8 (32 banks) or
+// 16 (64 banks) consecutive rows reading the same chunk hit different banks
+HQ_DEV int swz(int r) { return (r ^ (r >> 3)) & 7; }
+
 // Which tile a block computes.  Blocks are handed to the 8 XCDs in turn (block b to XCD b % 8), and each XCD has
 // its own L2: the blocks of one XCD take consecutive tiles, walked in strips of kStrip row tiles with the token tiles
 // inside a strip, so that the blocks running on one XCD at a time share their weights' rows and their tokens.
-constexpr int kXcds = 8, kStrip = 8;
+constexpr int kXcds = 8, kStrip = 4;
 
 HQ_DEV void tile_of(int b, int nb, int nrb, int &rb, int &tb) {
   const int q = nb / kXcds, r = nb % kXcds, x = b % kXcds;
   const int t = x * q + min(x, r) + b / kXcds;  // consecutive on one XCD
-  const int strip = t / (kStrip * (nb / nrb));
+  const int ntb = nb / nrb;
+  const int strip = t / (kStrip * ntb);
   const int first = strip * kStrip, width = min(kStrip, nrb - first);
-  const int in = t - first * (nb / nrb);
+  const int in = t - first * ntb;
   rb = first + in % width;
   tb = in / width;
 }
 
-// the 4 chains of a tile added in LDS, ((a0 + a1) + a2) + a3: wave k adds its sum to what waves 0..k-1 left (the
-// 16 values of a lane are the same (row, token)s in the four waves of a tile); the sum ends in chain 3's waves.
-// `part`: 2 x 64 x 16 floats that no wave reads or writes any more
-HQ_DEV void add_chains(float acc[16], float *part, int tile, int chain, int lane) {
-  float *p = part + (tile * 64 + lane) * 16;
+// the 4 chains of a slice added in LDS, ((a0 + a1) + a2) + a3, for both token halves: wave k adds its sums to what
+// waves 0..k-1 left (the 16 values of a lane are the same (row, token)s in the four waves of a slice); the sums end
+// in chain 3's waves.  p0, p1: 4 x 64 x 16 floats each that nothing else uses meanwhile
+HQ_DEV void add_chains(float acc0[16], float acc1[16], float *p0, float *p1, int slice, int chain, int lane) {
+  float *q0 = p0 + (slice * 64 + lane) * 16, *q1 = p1 + (slice * 64 + lane) * 16;
   for (int k = 0; k < 4; k++) {
     __syncthreads();
     if (chain == k) {
 #pragma unroll
       for (int r = 0; r < 16; r++) {
-        if (k > 0) acc[r] = fadd(p[r], acc[r]);
-        if (k < 3) p[r] = acc[r];
+        if (k > 0) {
+          acc0[r] = fadd(q0[r], acc0[r]);
+          acc1[r] = fadd(q1[r], acc1[r]);
+        }
+        if (k < 3) {
+          q0[r] = acc0[r];
+          q1[r] = acc1[r];
+        }
       }
     }
   }
 }
 
-// Buffer loads: a block's rows, tokens and scales are each one buffer resource (base and size in scalar registers),
-// so that a thread's offsets are set once and a stage moves them by a scalar offset alone; a load past the size
-// returns zeros and reads nothing (the tiles past the last row or token, groups past the last one: their results are
-// never stored).
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-
-HQ_DEV __amdgpu_buffer_rsrc_t resource(const char *base, int64_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)min(bytes, (int64_t)0xFFFFFFFF),
-                                           0x00020000);
-}
-HQ_DEV u32x4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
-  return __builtin_amdgcn_raw_buffer_load_b128(r, vo, so, 0);
-}
-HQ_DEV u32x2 bload8(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
-  return __builtin_amdgcn_raw_buffer_load_b64(r, vo, so, 0);
-}
-HQ_DEV uint32_t bload4(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
-  return __builtin_amdgcn_raw_buffer_load_b32(r, vo, so, 0);
-}
-HQ_DEV uint32_t bload2(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
-  return __builtin_amdgcn_raw_buffer_load_b16(r, vo, so, 0);
-}
-
 // ---------------------------------------------------------------------------------------------------------------
 // int8 / int6 weights, relaxed activations (matmul_q8r_tile, matmul_q6r)
-// MFMA A = weights (m = row), B = activations less their bias (n = token): lane l holds token l % 32 and rows
-// 8 (r / 4) + 4 (l / 32) + r % 4 of its tile's 32 (r = 0..15).
+// MFMA A = weights (m = row), B = activations (n = token): lane l holds token l % 32 of its half and rows
+// 8 (r / 4) + 4 (l / 32) + r % 4 of its slice (r = 0..15); K half l / 32 is bytes 16 (l / 32) .. + 15 of the group.
 // ---------------------------------------------------------------------------------------------------------------
-constexpr int QG = 8;               // groups a stage
-constexpr int QROW = QG * 32 + 16;  // an LDS row of a stage's bytes, padded against bank conflicts
+constexpr int QG = 4;  // groups a stage
 
 struct alignas(16) StageQ {
-  char w[BR][QROW];    // the stage's 8 groups of each row, widened to int8
-  char x[BT][QROW];    // and of each token, less the bias 64
+  char w[BR * 128];    // int8: 128 rows x 4 groups x 32 bytes, chunks swizzled; int6: 128 rows x 4 x 24 bytes
+  char x[BT * 128];    // 64 tokens x 4 groups x 32 bytes, chunks swizzled
   float ws[QG][BR];    // the rows' scales, group-major
-  int32_t dc[QG][BR];  // delta = wc + 64 sum(w) of each row and group (with the caller's wc only)
+  int32_t wc[QG][BR];  // the rows' corrections (with the caller's wc), group-major
   float xs[QG][BT];    // the tokens' scales, group-major
-  int32_t nz;          // the number of the last stage held here with a delta not 0 (-1: none)
 };
 
-// q - 64 of four 7-bit activations (0..127) in a word, byte by byte: q + 64 has no carry out of its byte, and
-// flipping its top bit takes 128 off again
-HQ_DEV uint32_t unbias(uint32_t q) { return (q + 0x40404040u) ^ 0x80808080u; }
+// K half kh (values 16 kh .. + 15) of an int6 group (24 bytes at p, kernels/six.ts:16-31): value j's low nibble is
+// in byte j % 16 (low half for j < 16, high half after), its top two bits at bits 2 (j / 8) of byte 16 + j % 8;
+// widened to the int8 4 v as six_widen does
+HQ_DEV v4i six_half(const char *p, int kh) {
+  const uint2 a = *(const uint2 *)p, b = *(const uint2 *)(p + 8), c = *(const uint2 *)(p + 16);
+  const uint32_t lo[4] = {a.x, a.y, b.x, b.y};
+  const uint32_t top[2] = {c.x, c.y};
+  const int sl = 4 * kh;
+  v4i v;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint32_t nib = ((lo[i] >> sl) & 0x0f0f0f0fu) << 2;
+    const uint32_t t = top[i & 1] << ((i < 2 ? 6 : 4) - sl);
+    v[i] = (int32_t)((t & 0xc0c0c0c0u) | nib);
+  }
+  return v;
+}
 
-// the block's view of a job: resources and each thread's offsets into them (thread i: weights of row i / 8, group
-// i % 8 of a stage; waves 0..3 also the activations of token i / 8, group i % 8, and their scale; waves 4..7 the
-// scales of row (i - 256) / 4, groups 2 ((i - 256) % 4) and + 1)
+// a block's loads of int8 / int6 stages: wave w's three loads a stage and their offsets
 template <int PACK, bool WC>
-struct LoaderQ {
+struct Relaxed {
   static constexpr int GB = PACK == 8 ? 32 : 24;  // bytes of a group of weights
-  __amdgpu_buffer_rsrc_t rw, rx, rxs, rws, rwc;
-  uint32_t ow, ox, oxs, ows, owc;
-  uint32_t v[8], x[8];
-  int32_t dc;
-  float f[2];
+  __amdgpu_buffer_rsrc_t rw, rx, rws, rwc, rxs;
+  uint32_t oa, ob, oc;
+  int wave;
+  char *junk;
 
-  HQ_DEV LoaderQ(const Job &J, int row0, int tok0, int M, int wave) {
-    const int i = threadIdx.x, ng = J.n >> 5;
+  HQ_DEV Relaxed(const Job &J, int row0, int tok0, int M, int w, char *junk_area) : wave(w), junk(junk_area) {
+    const int lane = threadIdx.x & 63, ng = J.n >> 5;
     const int64_t rb = (int64_t)ng * GB;
     rw = resource(J.wq + row0 * rb, (J.r1 - row0) * rb);
     rws = resource(J.ws + (int64_t)row0 * ng * 4, (int64_t)(J.r1 - row0) * ng * 4);
     rwc = resource(J.wc + (int64_t)row0 * ng * 4, WC ? (int64_t)(J.r1 - row0) * ng * 4 : 0);
     rx = resource(J.xq + tok0 * J.frame, (M - 1 - tok0) * J.frame + J.n);
     rxs = resource(J.xs + tok0 * J.sframe, (M - 1 - tok0) * J.sframe + 4 * ng);
-    ow = (uint32_t)((i >> 3) * rb + (i & 7) * GB);
-    owc = (uint32_t)(((i >> 3) * ng + (i & 7)) * 4);
-    ox = (uint32_t)((i >> 3) * J.frame + (i & 7) * 32);
-    oxs = (uint32_t)((i >> 3) * J.sframe + (i & 7) * 4);
-    ows = (uint32_t)((((i - 256) >> 2) * ng + 2 * ((i - 256) & 3)) * 4);
-    (void)wave;
-  }
-
-  HQ_DEV void load(int g0, int wave) {
+    // load a: the weights.  int8: wave w rows 8 w .. + 7, lane l row 8 w + l / 8, slot l % 8 holding chunk
+    // (l % 8) ^ swz(row); int6: 16-byte piece 64 w + l of the stage's 128 rows x 96 bytes (waves 0..11)
     if (PACK == 8) {
-      const u32x4 a = bload16(rw, ow, g0 * GB), b = bload16(rw, ow + 16, g0 * GB);
-      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+      const int row = 8 * w + (lane >> 3), c = (lane & 7) ^ swz(row);
+      oa = (uint32_t)(row * rb + (c >> 1) * 32 + (c & 1) * 16);
     } else {
-      const u32x2 a = bload8(rw, ow, g0 * GB), b = bload8(rw, ow + 8, g0 * GB), c = bload8(rw, ow + 16, g0 * GB);
-      const uint32_t d[6] = {a.x, a.y, b.x, b.y, c.x, c.y};
-      six_widen(d, v);
+      const int q = 64 * w + lane;
+      oa = (uint32_t)((q / 6) * rb + (q % 6) * 16);
     }
-    if (WC) dc = (int32_t)bload4(rwc, owc, g0 * 4);
-    if (wave < 4) {
-      const u32x4 a = bload16(rx, ox, g0 * 32), b = bload16(rx, ox + 16, g0 * 32);
-      x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
-      f[0] = __uint_as_float(bload4(rxs, oxs, g0 * 4));
+    // load b: waves 0..7 the activations (tokens 8 w .. + 7, as the weights); waves 8..15 the rows' scales
+    // (group (w - 8) / 2, rows 64 ((w - 8) % 2) + l)
+    if (w < 8) {
+      const int tok = 8 * w + (lane >> 3), c = (lane & 7) ^ swz(tok);
+      ob = (uint32_t)(tok * J.frame + (c >> 1) * 32 + (c & 1) * 16);
     } else {
-      f[0] = __uint_as_float(bload4(rws, ows, g0 * 4));
-      f[1] = __uint_as_float(bload4(rws, ows + 4, g0 * 4));
+      const int i = w - 8;
+      ob = (uint32_t)(((64 * (i & 1) + lane) * ng + (i >> 1)) * 4);
     }
+    // load c: waves 0..7 the corrections (as the scales), waves 8..11 the tokens' scales (group w - 8, token l)
+    if (w < 8) oc = (uint32_t)(((64 * (w & 1) + lane) * ng + (w >> 1)) * 4);
+    else oc = (uint32_t)(lane * J.sframe + (w - 8) * 4);
   }
 
-  // into S; `number`: the stage's number, kept in S.nz when a delta of it is not 0
-  HQ_DEV void store(StageQ &S, int wave, int number) {
-    const int i = threadIdx.x;
-    {
-      const int r = i >> 3, gi = i & 7;
-      uint4 *d = (uint4 *)(S.w[r] + 32 * gi);
-      d[0] = make_uint4(v[0], v[1], v[2], v[3]);
-      d[1] = make_uint4(v[4], v[5], v[6], v[7]);
-      if (WC) {
-        int32_t s = 0;
-#pragma unroll
-        for (int q = 0; q < 8; q++) s = sdot4((int32_t)v[q], 0x01010101, s);
-        const int32_t delta = (int32_t)((uint32_t)dc + 64u * (uint32_t)s);
-        S.dc[gi][r] = delta;
-        if (__builtin_amdgcn_ballot_w64(delta != 0) != 0 && (i & 63) == 0) S.nz = number;
-      }
-    }
-    if (wave < 4) {
-      const int t = i >> 3, gi = i & 7;
-      uint4 *d = (uint4 *)(S.x[t] + 32 * gi);
-      d[0] = make_uint4(unbias(x[0]), unbias(x[1]), unbias(x[2]), unbias(x[3]));
-      d[1] = make_uint4(unbias(x[4]), unbias(x[5]), unbias(x[6]), unbias(x[7]));
-      S.xs[gi][t] = f[0];
+  // the 3 loads of stage s (groups 4 s .. 4 s + 3) into S
+  HQ_DEV void load(StageQ &S, int s) {
+    const int w = wave;
+    if (PACK == 8 || w < 12) dma16(rw, S.w + w * 1024, oa, s * QG * GB);
+    else dma16(rxs, junk, 0, 0);
+    if (w < 8) dma16(rx, S.x + w * 1024, ob, s * QG * 32);
+    else dma4(rws, &S.ws[(w - 8) >> 1][64 * ((w - 8) & 1)], ob, s * QG * 4);
+    if (w < 8) {
+      if (WC) dma4(rwc, &S.wc[w >> 1][64 * (w & 1)], oc, s * QG * 4);
+      else dma4(rxs, junk, 0, 0);
+    } else if (w < 12) {
+      dma4(rxs, &S.xs[w - 8][0], oc, s * QG * 4);
     } else {
-      const int r = (i - 256) >> 2, gp = (i - 256) & 3;
-      S.ws[2 * gp][r] = f[0];
-      S.ws[2 * gp + 1][r] = f[1];
+      dma4(rxs, junk, 0, 0);
     }
   }
 };
 
-// group gi of the stage for the lane's tile: its exact integers C (MFMA) and the scales' products (the outer-product
-// MFMA: A lane l < 32 the scale of row l, B lane l < 32 the scale of token l, the K = 1 half zero)
-struct QTerm {
-  v16i c;
-  v16f s;
-};
-
-template <bool DELTA>
-HQ_DEV QTerm q_term(const StageQ &S, int gi, int trow, int lane) {
-  QTerm t;
-  const v4i A = *(const v4i *)(S.w[trow + (lane & 31)] + 32 * gi + 16 * (lane >> 5));
-  const v4i B = *(const v4i *)(S.x[lane & 31] + 32 * gi + 16 * (lane >> 5));
-  v16i c0;
-  if (DELTA) {
-    const int rbase = trow + 4 * (lane >> 5);
+// group gi of stage S for the lane's slice, both token halves: the exact integers (MFMA, from the corrections) and
+// the scales' products (the outer-product MFMA), each half added into its chain as soon as it is there
+template <int PACK, bool WC>
+HQ_DEV void q_group(float acc0[16], float acc1[16], const StageQ &S, int gi, int slice, int lane) {
+  const int kh = lane >> 5, row = 32 * slice + (lane & 31), tok = lane & 31;
+  v4i A;
+  if (PACK == 8) A = *(const v4i *)(S.w + row * 128 + ((2 * gi + kh) ^ swz(row)) * 16);
+  else A = six_half(S.w + row * 96 + gi * 24, kh);
+  v16i wc;
+  if (WC) {  // the caller's corrections of the lane's 16 rows
+    const int rbase = 32 * slice + 4 * kh;
 #pragma unroll
     for (int q = 0; q < 4; q++) {
-      const int4 c4 = *(const int4 *)&S.dc[gi][rbase + 8 * q];
-      c0[4 * q] = c4.x; c0[4 * q + 1] = c4.y; c0[4 * q + 2] = c4.z; c0[4 * q + 3] = c4.w;
+      const int4 c4 = *(const int4 *)&S.wc[gi][rbase + 8 * q];
+      wc[4 * q] = c4.x; wc[4 * q + 1] = c4.y; wc[4 * q + 2] = c4.z; wc[4 * q + 3] = c4.w;
     }
-  } else {
-    c0 = zero16i();
   }
-  t.c = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, c0, 0, 0, 0);
-  const float wsv = S.ws[gi][trow + (lane & 31)], xsv = S.xs[gi][lane & 31];
-  t.s = __builtin_amdgcn_mfma_f32_32x32x2f32(lane < 32 ? wsv : 0.0f, lane < 32 ? xsv : 0.0f, zero16f(), 0, 0, 0);
-  return t;
-}
-
-HQ_DEV void q_add(float acc[16], const QTerm &t) {
+  const float wsv = lane < 32 ? S.ws[gi][32 * slice + lane] : 0.0f;
 #pragma unroll
-  for (int r = 0; r < 16; r++) acc[r] = fadd(acc[r], fmul((float)t.c[r], t.s[r]));
+  for (int h = 0; h < 2; h++) {
+    const int t = tok + 32 * h;
+    const v4i B = *(const v4i *)(S.x + t * 128 + ((2 * gi + kh) ^ swz(t)) * 16);
+    v16i cin;
+    if (WC) {
+      cin = wc;
+    } else {  // -64 sum(w) of each row: the weights against 32 bytes of -64 (made again for each half: fewer registers)
+      const v4i m64 = {(int32_t)0xc0c0c0c0, (int32_t)0xc0c0c0c0, (int32_t)0xc0c0c0c0, (int32_t)0xc0c0c0c0};
+      cin = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, m64, zero16i(), 0, 0, 0);
+    }
+    const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, cin, 0, 0, 0);
+    const float xsv = lane < 32 ? S.xs[gi][32 * h + lane] : 0.0f;
+    const v16f sc = __builtin_amdgcn_mfma_f32_32x32x2f32(wsv, xsv, zero16f(), 0, 0, 0);
+    float *acc = h ? acc1 : acc0;
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[r] = fadd(acc[r], fmul((float)c[r], sc[r]));
+  }
 }
 
-// this wave's groups of a stage: gi = chain and chain + 4 (the second only in a full stage), in that order; with the
-// deltas (a caller's own corrections, never int8_sums') one group at a time, in fewer registers
-template <bool DELTA>
-HQ_DEV void q_stage(float acc[16], const StageQ &S, int chain, bool full, int trow, int lane) {
-  if (DELTA) {
-    q_add(acc, q_term<true>(S, chain, trow, lane));
-    if (full) q_add(acc, q_term<true>(S, chain + 4, trow, lane));
-    return;
-  }
-  const QTerm t0 = q_term<false>(S, chain, trow, lane);
-  if (full) {
-    const QTerm t1 = q_term<false>(S, chain + 4, trow, lane);
-    q_add(acc, t0);
-    q_add(acc, t1);
-  } else {
-    q_add(acc, t0);
-  }
+// stage s in `cur`, the loads of stage s + AHEAD into `next` (the buffer of stage s - 1)
+template <int PACK, bool WC>
+HQ_DEV void q_step(Relaxed<PACK, WC> &L, const StageQ &cur, StageQ &next, int s, int stages, int total,
+                   float acc0[16], float acc1[16], int slice, int chain, int lane) {
+  if (s >= stages) return;
+  wait_for(s, total);
+  if (s + AHEAD < total) L.load(next, s + AHEAD);
+  q_group<PACK, WC>(acc0, acc1, cur, chain, slice, lane);  // group 4 s + chain (relaxed/int8.ts:26-39)
 }
 
 template <int PACK, bool WC>
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void gemm_relaxed(Job J) {
-  __shared__ StageQ stage[2];
+__global__ __launch_bounds__(NT) void gemm_relaxed(Job J) {
+  __shared__ StageQ b0, b1, b2, b3;
+  __shared__ __attribute__((aligned(16))) char junk[1024];
   const int M = J.count;
   const int ng = J.n >> 5, ng4 = ng & ~3;
   int rb, tb;
@@ -280,134 +302,116 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void ge
   const int row0 = J.r0 + rb * BR, tok0 = tb * BT;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int tile = wave >> 2, chain = wave & 3;
-  const int trow = 32 * tile;
+  const int slice = wave >> 2, chain = wave & 3;
 
-  float acc[16];
+  float acc0[16], acc1[16];
 #pragma unroll
-  for (int r = 0; r < 16; r++) acc[r] = 0.0f;
+  for (int r = 0; r < 16; r++) acc0[r] = acc1[r] = 0.0f;
 
-  LoaderQ<PACK, WC> L(J, row0, tok0, M, wave);
-  if (WC) {
-    if (threadIdx.x == 0) stage[0].nz = stage[1].nz = -1;
-    __syncthreads();
+  Relaxed<PACK, WC> L(J, row0, tok0, M, wave, junk);
+  const int stages = ng4 / QG;
+  const int total = stages + (ng4 < ng ? 1 : 0);  // stages loaded: the tail's groups are one more
+  if (total > 0) L.load(b0, 0);
+  if (total > 1) L.load(b1, 1);
+  if (total > 2) L.load(b2, 2);
+  for (int s = 0; s < stages; s += RING) {
+    q_step<PACK, WC>(L, b0, b3, s, stages, total, acc0, acc1, slice, chain, lane);
+    q_step<PACK, WC>(L, b1, b0, s + 1, stages, total, acc0, acc1, slice, chain, lane);
+    q_step<PACK, WC>(L, b2, b1, s + 2, stages, total, acc0, acc1, slice, chain, lane);
+    q_step<PACK, WC>(L, b3, b2, s + 3, stages, total, acc0, acc1, slice, chain, lane);
   }
-  const int stages = (ng4 + QG - 1) / QG;  // the last one holds only 4 groups where ng4 % 8 == 4
-  if (stages > 0) {
-    L.load(0, wave);
-    L.store(stage[0], wave, 0);
-  }
-  __syncthreads();
-  for (int j = 0; j < stages; ++j) {
-    const StageQ &S = stage[j & 1];
-    if (j + 1 < stages) L.load((j + 1) * QG, wave);
-    // groups 8 j + chain and 8 j + 4 + chain (relaxed/int8.ts:26-39)
-    const bool full = QG * j + 4 < ng4;
-    if (WC && __builtin_amdgcn_readfirstlane(S.nz) == j) q_stage<true>(acc, S, chain, full, trow, lane);
-    else q_stage<false>(acc, S, chain, full, trow, lane);
-    if (j + 1 < stages) L.store(stage[(j + 1) & 1], wave, j + 1);
-    __syncthreads();
-  }
-  add_chains(acc, (float *)&stage[0], tile, chain, lane);
-  if (ng4 < ng) {  // the groups past the fours, one at a time, after the four chains' sum (relaxed/int8.ts:40-47)
-    L.load(ng4, wave);
-    L.store(stage[1], wave, stages);
-    __syncthreads();
-    if (chain == 3) {
-      const StageQ &S = stage[1];
-      const bool delta = WC && __builtin_amdgcn_readfirstlane(S.nz) == stages;
-      for (int gi = 0; gi < ng - ng4; gi++) {
-        if (delta) q_add(acc, q_term<true>(S, gi, trow, lane));
-        else q_add(acc, q_term<false>(S, gi, trow, lane));
-      }
-    }
-  }
+  stage_ready<0>();  // every load has landed (the tail's too) and every wave is done with the stages
+  auto ring = [&](int i) -> StageQ & { return i == 0 ? b0 : i == 1 ? b1 : i == 2 ? b2 : b3; };
+  add_chains(acc0, acc1, (float *)&ring((stages + 1) % RING), (float *)&ring((stages + 2) % RING), slice, chain,
+             lane);
   if (chain == 3) {
-    const int t = tok0 + (lane & 31);
-    if (t < M) {
-      float *out = (float *)(J.out + t * J.os);
-      const int rbase = row0 + trow + 4 * (lane >> 5);
+    // the groups past the fours, one at a time, after the four chains' sum (relaxed/int8.ts:40-47)
+    const StageQ &T = ring(stages % RING);
+    for (int gi = 0; gi < ng - ng4; gi++) q_group<PACK, WC>(acc0, acc1, T, gi, slice, lane);
+    const int rbase = row0 + 32 * slice + 4 * (lane >> 5);
 #pragma unroll
-      for (int q = 0; q < 4; q++)
+    for (int h = 0; h < 2; h++) {
+      const int t = tok0 + 32 * h + (lane & 31);
+      if (t < M) {
+        float *out = (float *)(J.out + t * J.os);
+        const float *acc = h ? acc1 : acc0;
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const int row = rbase + 8 * q + e;
-          if (row < J.r1) out[row] = acc[4 * q + e];
-        }
+        for (int q = 0; q < 4; q++)
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const int row = rbase + 8 * q + e;
+            if (row < J.r1) out[row] = acc[4 * q + e];
+          }
+      }
     }
   }
 }
 
 // ---------------------------------------------------------------------------------------------------------------
 // ternary (matmul_t2r_tile)
-// MFMA A = activations (m = token), B = codes (n = row): lane l holds row l % 32 and tokens 8 (r / 4) + 4 (l / 32)
-// + r % 4.  Part k of a group of 128 (block h = k / 2, bytes c = 8 (k % 2) .. + 7 of it) as 32 K values in the order
-// plane-major: K-half kh of a lane is planes 2 kh, 2 kh + 1, eight c's each, for the codes and for interleave()'s
-// activation bytes 64 h + 16 p + 8 (k % 2) .. + 7 alike.
+// MFMA A = activations (m = token), B = codes (n = row): lane l holds row l % 32 of its slice and tokens
+// 8 (r / 4) + 4 (l / 32) + r % 4 of its half.  Part k of a group of 128 (block h = k / 2, bytes c = 8 (k % 2) .. + 7
+// of it) as 32 K values in the order plane-major: K half kh of a lane is planes 2 kh, 2 kh + 1, eight c's each, for
+// the codes and for interleave()'s activation bytes 64 h + 16 p + 8 (k % 2) .. + 7 alike.
 // ---------------------------------------------------------------------------------------------------------------
-constexpr int TG = 2;                 // groups of 128 a stage
-constexpr int TWROW = TG * 32 + 16;   // an LDS row of a stage's code bytes
-constexpr int TXROW = TG * 128 + 16;  // and of a token's activation bytes
+constexpr int TG = 2;  // groups of 128 a stage
 
 struct alignas(16) StageT {
-  char w[BR][TWROW];         // the stage's groups' 32 bytes of each row
-  char x[BT][TXROW];         // the stage's groups' 128 interleaved activations of each token
+  char w[BR * 64];           // 128 rows x 2 groups x 32 code bytes; 16-byte chunk j of row r at j ^ tswz(r)
+  char x[BT * 256];          // 64 tokens x 2 groups x 128 activation bytes; chunk c of token t at c ^ (t & 15)
   float xs[TG * 4][BT];      // the tokens' scales of each (group, part)
   int32_t sums[TG * 4][BT];  // and their sums
-  float d[TG][BR];           // the rows' group scales, widened
+  uint32_t d[TG][BR];        // the rows' float16 group scales, one a word
 };
 
-// waves 0..3: 16 code bytes (row i / 4, group (i / 2) % 2, half i % 2) and 32 activation bytes (token i / 8, bytes
-// 32 (i % 8) of the stage's 256); waves 4..7: the scale and sum of (token (i - 256) / 8, group and part
-// (i - 256) % 8), and waves 4, 5 a row's group scale (row (i - 256) / 2, group i % 2)
-struct LoaderT {
-  __amdgpu_buffer_rsrc_t rw, rx, rxs, rws;
-  uint32_t ow, ox, oxs, osu, ows;
-  uint4 w, x[2];
-  float sc;
-  int32_t su;
-  uint32_t h;
+HQ_DEV int tswz(int r) { return (r >> 2) & 3; }
 
-  HQ_DEV LoaderT(const Job &J, int row0, int tok0, int M) {
-    const int i = threadIdx.x, groups = J.n >> 7;
+// a block's loads of ternary stages: wave w's three loads a stage and their offsets
+struct Ternary {
+  __amdgpu_buffer_rsrc_t rw, rx, rxs, rws;
+  uint32_t oa, ob, oc;
+  int wave;
+  char *junk;
+
+  HQ_DEV Ternary(const Job &J, int row0, int tok0, int M, int w, char *junk_area) : wave(w), junk(junk_area) {
+    const int lane = threadIdx.x & 63, groups = J.n >> 7;
+    const int nsc = 4 * (J.n >> 5);  // the bytes of a token's scales: its sums follow them
     rw = resource(J.wq + (int64_t)row0 * groups * 32, (int64_t)(J.r1 - row0) * groups * 32);
     rws = resource(J.ws + (int64_t)row0 * groups * 2, (int64_t)(J.r1 - row0) * groups * 2);
     rx = resource(J.xq + tok0 * J.frame, (M - 1 - tok0) * J.frame + J.n);
-    rxs = resource(J.xs + tok0 * J.sframe, (M - 1 - tok0) * J.sframe + 8 * (J.n >> 5));
-    ow = (uint32_t)((i >> 2) * groups * 32 + ((i >> 1) & 1) * 32 + (i & 1) * 16);
-    ox = (uint32_t)((i >> 3) * J.frame + ((i & 7) >> 2) * 128 + 32 * (i & 3));
-    const int q = i - 256;
-    oxs = (uint32_t)((q >> 3) * J.sframe + (q & 7) * 4);
-    osu = oxs + 4 * (J.n >> 5);
-    ows = (uint32_t)(((q >> 1) * groups + (q & 1)) * 2);
+    rxs = resource(J.xs + tok0 * J.sframe, (M - 1 - tok0) * J.sframe + 2 * nsc);
+    // load a: the activations, tokens 4 w .. + 3, lane l token 4 w + l / 16, slot l % 16 holding chunk
+    // (l % 16) ^ (token & 15) of the stage's 256 bytes
+    {
+      const int tok = 4 * w + (lane >> 4), c = (lane & 15) ^ (tok & 15);
+      oa = (uint32_t)(tok * J.frame + c * 16);
+    }
+    // load b: waves 0..7 the codes (rows 16 w .. + 15, lane l row 16 w + l / 4, slot l % 4 holding chunk
+    // (l % 4) ^ tswz(row) of the row's 64 bytes); waves 8..15 the tokens' scales of (group, part) w - 8
+    if (w < 8) {
+      const int row = 16 * w + (lane >> 2), j = (lane & 3) ^ tswz(row);
+      ob = (uint32_t)(row * groups * 32 + (j >> 1) * 32 + (j & 1) * 16);
+    } else {
+      ob = (uint32_t)(lane * J.sframe + (w - 8) * 4);
+    }
+    // load c: waves 0..7 the sums of (group, part) w; waves 8..11 the float16 scales (group (w - 8) / 2, rows
+    // 64 ((w - 8) % 2) + l)
+    if (w < 8) {
+      oc = (uint32_t)(lane * J.sframe + nsc + w * 4);
+    } else {
+      const int i = w - 8;
+      oc = (uint32_t)(((64 * (i & 1) + lane) * groups + (i >> 1)) * 2);
+    }
   }
 
-  HQ_DEV void load(int g0, int wave) {
-    if (wave < 4) {
-      const u32x4 c = bload16(rw, ow, g0 * 32);
-      w = make_uint4(c.x, c.y, c.z, c.w);
-      const u32x4 a = bload16(rx, ox, g0 * 128), b = bload16(rx, ox + 16, g0 * 128);
-      x[0] = make_uint4(a.x, a.y, a.z, a.w);
-      x[1] = make_uint4(b.x, b.y, b.z, b.w);
-    } else {
-      sc = __uint_as_float(bload4(rxs, oxs, g0 * 16));
-      su = (int32_t)bload4(rxs, osu, g0 * 16);
-      if (wave < 6) h = bload2(rws, ows, g0 * 2);
-    }
-  }
-  HQ_DEV void store(StageT &S, int wave) const {
-    const int i = threadIdx.x;
-    if (wave < 4) {
-      *(uint4 *)(S.w[i >> 2] + 32 * ((i >> 1) & 1) + 16 * (i & 1)) = w;
-      uint4 *d = (uint4 *)(S.x[i >> 3] + 32 * (i & 7));
-      d[0] = x[0];
-      d[1] = x[1];
-    } else {
-      const int q = i - 256;
-      S.xs[q & 7][q >> 3] = sc;
-      S.sums[q & 7][q >> 3] = su;
-      if (wave < 6) S.d[q & 1][q >> 1] = half_to_float(h);
-    }
+  HQ_DEV void load(StageT &S, int s) {
+    const int w = wave;
+    dma16(rx, S.x + w * 1024, oa, s * TG * 128);
+    if (w < 8) dma16(rw, S.w + w * 1024, ob, s * TG * 32);
+    else dma4(rxs, &S.xs[w - 8][0], ob, s * TG * 16);
+    if (w < 8) dma4(rxs, &S.sums[w][0], oc, s * TG * 16);
+    else if (w < 12) dma2(rws, &S.d[(w - 8) >> 1][64 * ((w - 8) & 1)], oc, s * TG * 2);
+    else dma4(rxs, junk, 0, 0);
   }
 };
 
@@ -421,41 +425,59 @@ HQ_DEV v4i plane_pair(uint32_t w0, uint32_t w1) {
   return b;
 }
 
-// part k of group gi of the stage for the lane's tile: its exact integers, starting at interleave()'s sums of the
-// lane's 16 tokens
-HQ_DEV v16i t_mfma(const StageT &S, int gi, int k, int trow, int lane) {
-  const int h = k >> 1, s = k & 1, kh = lane >> 5;
-  const char *xp = S.x[lane & 31] + 128 * gi + 64 * h + 8 * s + 32 * kh;
-  const uint2 a0 = *(const uint2 *)xp, a1 = *(const uint2 *)(xp + 16);
-  v4i A;
-  A[0] = (int32_t)a0.x; A[1] = (int32_t)a0.y; A[2] = (int32_t)a1.x; A[3] = (int32_t)a1.y;
-  const uint2 wv = *(const uint2 *)(S.w[trow + (lane & 31)] + 32 * gi + 16 * h + 8 * s);
+// 8 bytes at byte o (a multiple of 8) of a token's 256 stage bytes
+HQ_DEV uint2 t_acts8(const StageT &S, int tok, int o) {
+  return *(const uint2 *)(S.x + tok * 256 + (((o >> 4) ^ (tok & 15)) << 4) + (o & 8));
+}
+
+// part k of group gi of the stage for the lane's slice, both token halves: f(f(whole * xs) * d) into the part's
+// chain (relaxed/signs.ts:206)
+HQ_DEV void t_group(float acc0[16], float acc1[16], const StageT &S, int gi, int k, int slice, int lane) {
+  const int h = k >> 1, s = k & 1, kh = lane >> 5, row = 32 * slice + (lane & 31);
+  // B: the row's codes of planes 2 kh, 2 kh + 1, bytes c = 8 s .. + 7 of block h (chunk 2 gi + h, half s)
+  const int j = 2 * gi + h;
+  const uint2 wv = *(const uint2 *)(S.w + row * 64 + ((j ^ tswz(row)) << 4) + 8 * s);
   const v4i B = kh == 0 ? plane_pair<0>(wv.x, wv.y) : plane_pair<2>(wv.x, wv.y);
-  const int tbase = 4 * kh;
-  v16i C;
+  const float d = half_to_float(S.d[gi][row]);
+  const int o = 128 * gi + 64 * h + 8 * s + 32 * kh;
 #pragma unroll
-  for (int q = 0; q < 4; q++) {
-    const int4 c4 = *(const int4 *)&S.sums[4 * gi + k][tbase + 8 * q];
-    C[4 * q] = c4.x; C[4 * q + 1] = c4.y; C[4 * q + 2] = c4.z; C[4 * q + 3] = c4.w;
+  for (int half = 0; half < 2; half++) {
+    const int tok = 32 * half + (lane & 31);
+    const uint2 a0 = t_acts8(S, tok, o), a1 = t_acts8(S, tok, o + 16);
+    v4i A;
+    A[0] = (int32_t)a0.x; A[1] = (int32_t)a0.y; A[2] = (int32_t)a1.x; A[3] = (int32_t)a1.y;
+    const int tbase = 32 * half + 4 * kh;
+    v16i C;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int4 c4 = *(const int4 *)&S.sums[4 * gi + k][tbase + 8 * q];
+      C[4 * q] = c4.x; C[4 * q + 1] = c4.y; C[4 * q + 2] = c4.z; C[4 * q + 3] = c4.w;
+    }
+    C = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, C, 0, 0, 0);
+    float *acc = half ? acc1 : acc0;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const float4 x4 = *(const float4 *)&S.xs[4 * gi + k][tbase + 8 * q];
+      const float xv[4] = {x4.x, x4.y, x4.z, x4.w};
+#pragma unroll
+      for (int e = 0; e < 4; e++) acc[4 * q + e] = fadd(acc[4 * q + e], fmul(fmul((float)C[4 * q + e], xv[e]), d));
+    }
   }
-  return __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, C, 0, 0, 0);
 }
 
-// f(f(whole * xs) * d) into the part's chain (relaxed/signs.ts:206)
-HQ_DEV void t_add(float acc[16], const v16i &C, const StageT &S, int gi, int k, int trow, int lane) {
-  const float d = S.d[gi][trow + (lane & 31)];
-  const int tbase = 4 * (lane >> 5);
-#pragma unroll
-  for (int q = 0; q < 4; q++) {
-    const float4 x4 = *(const float4 *)&S.xs[4 * gi + k][tbase + 8 * q];
-    const float xv[4] = {x4.x, x4.y, x4.z, x4.w};
-#pragma unroll
-    for (int e = 0; e < 4; e++) acc[4 * q + e] = fadd(acc[4 * q + e], fmul(fmul((float)C[4 * q + e], xv[e]), d));
-  }
+HQ_DEV void t_step(Ternary &L, const StageT &cur, StageT &next, int s, int stages, int groups, float acc0[16],
+                   float acc1[16], int slice, int part, int lane) {
+  if (s >= stages) return;
+  wait_for(s, stages);
+  if (s + AHEAD < stages) L.load(next, s + AHEAD);
+  // part `part` of groups 2 s and 2 s + 1 (relaxed/signs.ts:198-207)
+  t_group(acc0, acc1, cur, 0, part, slice, lane);
+  if (TG * s + 1 < groups) t_group(acc0, acc1, cur, 1, part, slice, lane);
 }
 
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void gemm_ternary(Job J) {
-  __shared__ StageT stage[2];
+__global__ __launch_bounds__(NT) void gemm_ternary(Job J) {
+  __shared__ StageT b0, b1, b2, b3;
+  __shared__ __attribute__((aligned(16))) char junk[1024];
   const int M = J.count;
   const int groups = J.n >> 7;
   int rb, tb;
@@ -463,45 +485,40 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void ge
   const int row0 = J.r0 + rb * BR, tok0 = tb * BT;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int tile = wave >> 2, part = wave & 3;
-  const int trow = 32 * tile;
+  const int slice = wave >> 2, part = wave & 3;
 
-  float acc[16];
+  float acc0[16], acc1[16];
 #pragma unroll
-  for (int r = 0; r < 16; r++) acc[r] = 0.0f;
+  for (int r = 0; r < 16; r++) acc0[r] = acc1[r] = 0.0f;
 
-  LoaderT L(J, row0, tok0, M);
+  Ternary L(J, row0, tok0, M, wave, junk);
   const int stages = (groups + TG - 1) / TG;
-  L.load(0, wave);
-  L.store(stage[0], wave);
-  __syncthreads();
-  for (int j = 0; j < stages; ++j) {
-    const StageT &S = stage[j & 1];
-    if (j + 1 < stages) L.load((j + 1) * TG, wave);
-    // part `part` of groups 2 j and 2 j + 1 (relaxed/signs.ts:198-207)
-    const v16i c0 = t_mfma(S, 0, part, trow, lane);
-    if (TG * j + 1 < groups) {
-      const v16i c1 = t_mfma(S, 1, part, trow, lane);
-      t_add(acc, c0, S, 0, part, trow, lane);
-      t_add(acc, c1, S, 1, part, trow, lane);
-    } else {
-      t_add(acc, c0, S, 0, part, trow, lane);
-    }
-    if (j + 1 < stages) L.store(stage[(j + 1) & 1], wave);
-    __syncthreads();
+  if (stages > 0) L.load(b0, 0);
+  if (stages > 1) L.load(b1, 1);
+  if (stages > 2) L.load(b2, 2);
+  for (int s = 0; s < stages; s += RING) {
+    t_step(L, b0, b3, s, stages, groups, acc0, acc1, slice, part, lane);
+    t_step(L, b1, b0, s + 1, stages, groups, acc0, acc1, slice, part, lane);
+    t_step(L, b2, b1, s + 2, stages, groups, acc0, acc1, slice, part, lane);
+    t_step(L, b3, b2, s + 3, stages, groups, acc0, acc1, slice, part, lane);
   }
-  add_chains(acc, (float *)&stage[0], tile, part, lane);
+  stage_ready<0>();
+  add_chains(acc0, acc1, (float *)&b0, (float *)&b1, slice, part, lane);
   if (part == 3) {
-    const int rw = row0 + trow + (lane & 31);
+    const int rw = row0 + 32 * slice + (lane & 31);
     if (rw < J.r1) {
-      const int tbase = tok0 + 4 * (lane >> 5);
 #pragma unroll
-      for (int q = 0; q < 4; q++)
+      for (int h = 0; h < 2; h++) {
+        const int tbase = tok0 + 32 * h + 4 * (lane >> 5);
+        const float *acc = h ? acc1 : acc0;
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const int t = tbase + 8 * q + e;
-          if (t < M) ((float *)(J.out + t * J.os))[rw] = acc[4 * q + e];
-        }
+        for (int q = 0; q < 4; q++)
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const int t = tbase + 8 * q + e;
+            if (t < M) ((float *)(J.out + t * J.os))[rw] = acc[4 * q + e];
+          }
+      }
     }
   }
 }
