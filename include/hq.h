@@ -17,9 +17,9 @@
  *     activations 16-byte aligned, int6 weights 8-byte aligned, scales / corrections / outputs 4-byte aligned;
  *     frame a multiple of 16 and os a multiple of 4 where count > 1.
  *   - the relaxed int8 / int6 kernels' activation bytes are the 7-bit second factor of the reference's
- *     relaxed_dot_i8x16_i7x16 (kernels/ceilings_relaxed.ts:6-8): 0..127, as quantize_x(bias 64) writes them.  Like
- *     the reference, whose sums for other bytes depend on the machine, libhq defines its results for those bytes
- *     only: the one-token kernels take a byte as a signed int8, the prompt tiles (more than 4 tokens) do not.
+ *     relaxed_dot_i8x16_i7x16 (kernels/ceilings_relaxed.ts:6-8): 0..127, as quantize_x(bias 64) writes them.  For
+ *     other bytes the reference's sums depend on the machine; libhq takes every byte as a signed int8 (in the token
+ *     kernels and the prompt tiles alike).
  *   - matmul_q8r / matmul_q6r / matmul_q8r_tile accept wc == NULL (no counterpart in the reference): the group's
  *     integer is then dot(w, q - 64) computed directly, which is what the reference's integer is whenever wc is
  *     int8_sums' / six_sums' (relaxed/int8.ts:6-11), without reading wc (12.5 % fewer bytes for int8).

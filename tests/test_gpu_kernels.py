@@ -4,7 +4,7 @@ Integers and bytes exact, every float32 output to the bit (the kernels keep the 
 nothing written outside the rows / tokens of a call (outputs start at -7, as tests/int8-check.ts:176-181 checks).
 The cases are the reference tests' (tests/int8-check.ts, tests/ternary-check.ts: their group counts, row ranges,
 token counts, int8 ends, zero and subnormal scales, the largest sums), the order-revealing inputs of
-test_oracle.py, and the BASELINE.json shapes at full size.
+test_oracle.py; test_gpu_shapes.py holds the benchmark configs' shapes at full size.
 """
 import numpy as np
 import pytest
@@ -270,6 +270,31 @@ def test_q8r_tile(k, arena, oracle, count, ng):
                 want[r0:r1] = full[r0:r1]
                 assert same_bits(got[t], want), f"count {count} ng {ng} rows {r0}..{r1} token {t} wc {form}: " \
                                                 f"{first_difference(got[t], want)}"
+
+
+def test_relaxed_bytes_past_seven_bits(k, arena):
+    """Activation bytes 128..255 lie outside the reference's domain (its relaxed dot is machine-dependent there):
+    libhq takes every byte as a signed int8, so the token kernel and the prompt tile still agree to the bit."""
+    rng = np.random.default_rng(5)
+    rows, ng, count = 40, 9, 20
+    n = 32 * ng
+    frame = ((n + 4 * ng + 15) // 16) * 16
+    w = rng.integers(-128, 128, rows * n).astype(np.int8)
+    ws = (rng.random(rows * ng) * 1e-3).astype(F)
+    wc = rng.integers(-200000, 200000, rows * ng).astype(np.int32)
+    q = np.zeros((count, frame), np.uint8)
+    q[:, :n] = rng.integers(0, 256, (count, n))
+    q[:, n:n + 4 * ng] = (rng.random((count, ng)) * 1e-2).astype(F).view(np.uint8)
+    wq, wsa, xq = arena.put(w), arena.put(ws), arena.put(q)
+    for wca in (arena.put(wc), 0):
+        tile = arena.alloc(4 * rows * count)
+        k.matmul_q8r_tile(tile, xq, xq + n, wq, wsa, wca, n, 0, rows, count, 4 * rows, frame)
+        got = arena.get(tile, F, rows * count).reshape(count, rows)
+        for t in range(count):
+            one = arena.alloc(4 * rows)
+            k.matmul_q8r(one, xq + t * frame, xq + t * frame + n, wq, wsa, wca, n, 0, rows)
+            want = arena.get(one, F, rows)
+            assert same_bits(got[t], want), f"token {t} wc {bool(wca)}: {first_difference(got[t], want)}"
 
 
 @pytest.mark.parametrize("count", [2, 4, 5, 16, 40])
