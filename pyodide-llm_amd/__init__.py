@@ -81,11 +81,12 @@ _lib = None
 
 
 def library(path=None):
-    """libhq.so as a ctypes library with every export's signature set.  Raises when it is not built."""
+    """libhq.so (this package's, or the one HQ_LIBRARY names) as a ctypes library with every export's signature
+    set.  Raises when it is not built."""
     global _lib
     if _lib is not None and path is None:
         return _lib
-    where = path or LIBRARY
+    where = path or os.environ.get("HQ_LIBRARY") or LIBRARY
     if not os.path.exists(where):
         raise HQError(HQ_ERR_DEVICE, f"{where} is not built: run `python pyodide-llm_amd/build.py` "
                                      "(or __graft_entry__.build())")

@@ -67,6 +67,13 @@ HQ_DEV void fill_acts(const GemvBatch &b, const Job &J, char *lq, float *ls) {
 }
 
 constexpr int kRowsPerBlock = 16;
+// the relaxed kinds' blocks: kRelaxedRows rows of 16 lanes (fewer rows a block: more blocks, a finer balance of the
+// last ones over the CUs)
+#ifndef HQ_GEMV_ROWS
+#define HQ_GEMV_ROWS 8
+#endif
+constexpr int kRelaxedRows = HQ_GEMV_ROWS;
+HQ_HOST_DEV constexpr int rows_per_block(Kind kind) { return kind == Q8R || kind == Q6R ? kRelaxedRows : kRowsPerBlock; }
 
 HQ_DEV int job_of(const GemvBatch &b, int blk) {
   int j = 0;
@@ -208,12 +215,12 @@ struct RelaxedChunk {
 };
 
 template <int PACK, int T, bool WC, int SRC>
-__global__ __launch_bounds__(256) void gemv_relaxed(GemvBatch batch) {
+__global__ __launch_bounds__(16 * kRelaxedRows) void gemv_relaxed(GemvBatch batch) {
   extern __shared__ __align__(16) char lds[];
   const int jb = job_of(batch, blockIdx.x);
   const Job &J = batch.job[jb];
   const int lane = threadIdx.x & 15;
-  const int row_u = J.r0 + (blockIdx.x - batch.block0[jb]) * kRowsPerBlock + (threadIdx.x >> 4);
+  const int row_u = J.r0 + (blockIdx.x - batch.block0[jb]) * kRelaxedRows + (threadIdx.x >> 4);
   const bool live = row_u < J.r1;
   const int row = live ? row_u : J.r1 - 1;
   const int ng = J.n >> 5, ng4 = ng & ~3;
@@ -466,7 +473,7 @@ __global__ __launch_bounds__(256) void gemv_ternary(GemvBatch batch) {
 
 template <int PACK, int T, int SRC>
 hipError_t launch_relaxed(const GemvBatch &b, int blocks, bool wc, size_t lds, hipStream_t s) {
-  dim3 grid(blocks), block(256);
+  dim3 grid(blocks), block(16 * kRelaxedRows);
   if (wc) hipLaunchKernelGGL((gemv_relaxed<PACK, T, true, SRC>), grid, block, lds, s, b);
   else hipLaunchKernelGGL((gemv_relaxed<PACK, T, false, SRC>), grid, block, lds, s, b);
   return hipGetLastError();
@@ -512,7 +519,7 @@ hipError_t launch_batch(Kind kind, const Job *jobs, int32_t njobs, const char *x
   for (int j = 0; j < njobs; j++) {
     b.job[j] = jobs[j];
     b.block0[j] = blocks;
-    blocks += (jobs[j].r1 - jobs[j].r0 + kRowsPerBlock - 1) / kRowsPerBlock;
+    blocks += (jobs[j].r1 - jobs[j].r0 + rows_per_block(kind) - 1) / rows_per_block(kind);
     nmax = jobs[j].n > nmax ? jobs[j].n : nmax;
   }
   b.block0[njobs] = blocks;
