@@ -196,6 +196,141 @@ def measure_decode(torch, pkg, args, phases, fused, with_wc):
     return out
 
 
+def _graph_time(torch, launch, reps):
+    """seconds a replay of a graph of launch()'s launches takes, over `reps` replays between HIP events"""
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        launch(stream.cuda_stream)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            launch(stream.cuda_stream)
+        g.replay()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            g.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e-3 / reps
+
+
+def measure_configs(torch, pkg, args):
+    """The other configs' products on one GPU (BASELINE.json configs[0..2, 4]): GB/s of algorithmic bytes for the
+    token products (M = 1; copies of the weights past the Infinity Cache where the shapes allow), TOPS for the
+    prompts.  Products only (the activations prepared once), graphs of their launches timed with HIP events."""
+    from pyodide_llm_amd import jobs
+    lib = pkg.library()
+    gen = torch.Generator(device="cuda:0")
+    gen.manual_seed(11)
+    dev = "cuda:0"
+    reps = max(3, args.steps // 2)
+    out = {}
+
+    def acts(n, kind, count=1):
+        x = torch.randn(count, n, device=dev, generator=gen)
+        area = (8 if kind == "ternary" else 4) * (n // 32)
+        frame = (n + area + 15) // 16 * 16
+        buf = torch.empty(count * frame, dtype=torch.uint8, device=dev)
+        bias = 64 if kind in ("int8", "int6") else 0
+        pkg.check(lib.hq_quantize_x_batch(buf.data_ptr(), buf.data_ptr() + n, x.data_ptr(), n, bias, count, frame,
+                                          4 * n, None))
+        if kind == "ternary":
+            pkg.check(lib.hq_interleave_batch(buf.data_ptr(), buf.data_ptr() + n, n, count, frame, None))
+        return buf, frame
+
+    def weights(kind, rows, n):
+        if kind == "int8":
+            w = torch.randint(-127, 128, (rows, n), dtype=torch.int8, device=dev, generator=gen)
+            ws = (torch.randn(rows, n // 32, device=dev, generator=gen).abs_() * (0.02 / 127)).float()
+        elif kind == "int6":  # random bytes are valid packed int6 groups
+            w = torch.randint(0, 256, (rows, n // 32 * 24), dtype=torch.uint8, device=dev, generator=gen)
+            ws = (torch.randn(rows, n // 32, device=dev, generator=gen).abs_() * (0.02 / 124)).float()
+        else:  # ternary: codes 0..2 four to a byte, one float16 scale a row in every group of 128
+            codes = torch.randint(0, 3, (rows, n // 4, 4), dtype=torch.uint8, device=dev, generator=gen)
+            w = (codes[..., 0] | (codes[..., 1] << 2) | (codes[..., 2] << 4) | (codes[..., 3] << 6)).contiguous()
+            row = (torch.randn(rows, 1, device=dev, generator=gen).abs_() * 0.02 + 1e-3).half()
+            ws = row.expand(rows, n // 128).contiguous()
+        return w, ws
+
+    per_weight = {"int8": 1.125, "int6": 0.875, "ternary": 0.265625}
+    kind_name = {"int8": "matmul_q8r", "int6": "matmul_q6r", "ternary": "matmul_t2r"}
+
+    def decode(label, kind, phase_shapes, copies):
+        """phase_shapes: [[(rows, n), ...] a phase]; `copies` sets of distinct weights, every phase of each"""
+        a = {n: acts(n, kind) for ph in phase_shapes for _, n in ph}
+        tables, total = [], 0.0
+        keep = []
+        for _ in range(copies):
+            for ph in phase_shapes:
+                entries = []
+                for rows, n in ph:
+                    w, ws = weights(kind, rows, n)
+                    o = torch.empty(rows, device=dev)
+                    keep += [w, ws, o]
+                    buf, frame = a[n]
+                    # wc 0: the corrections derived in the kernel (int8, int6); ternary jobs have none
+                    entries.append(jobs.job(kind_name[kind], o.data_ptr(), buf.data_ptr(), buf.data_ptr() + n,
+                                            w.data_ptr(), ws.data_ptr(), 0, n, rows=rows))
+                    total += rows * n * per_weight[kind] + n * (1.25 if kind == "ternary" else 1.125) + 4 * rows
+                tables.append((jobs.table(entries), len(entries)))
+
+        def launch(h):
+            for t, nj in tables:
+                lib.hq_phase(t, nj, 16, h)
+        sec = _graph_time(torch, launch, reps)
+        pkg.check(lib.hq_last_error())
+        out[label] = {"GBps": round(total / sec / 1e9, 1), "us_per_launch": round(1e6 * sec / len(tables), 2),
+                      "launches": len(tables), "bytes": total}
+
+    def prefill(label, kind, shapes, count):
+        ops, calls, keep = 0.0, [], []
+        for rows, n in shapes:
+            w, ws = weights(kind, rows, n)
+            buf, frame = acts(n, kind, count)
+            o = torch.empty(count, rows, device=dev)
+            keep += [w, ws, buf, o]
+            ops += 2.0 * count * rows * n
+            if kind == "int8":
+                wc = torch.empty(rows, n // 32, dtype=torch.int32, device=dev)
+                pkg.check(lib.hq_int8_sums_ex(wc.data_ptr(), w.data_ptr(), rows * n // 32, None))
+                keep.append(wc)
+                calls.append(lambda h, w=w, ws=ws, wc=wc, buf=buf, frame=frame, o=o, rows=rows, n=n:
+                             lib.hq_matmul_q8r_tile_ex(o.data_ptr(), buf.data_ptr(), buf.data_ptr() + n, w.data_ptr(),
+                                                       ws.data_ptr(), wc.data_ptr(), n, 0, rows, count, 4 * rows,
+                                                       frame, h))
+            elif kind == "ternary":
+                calls.append(lambda h, w=w, ws=ws, buf=buf, frame=frame, o=o, rows=rows, n=n:
+                             lib.hq_matmul_t2r_tile_ex(o.data_ptr(), buf.data_ptr(), buf.data_ptr() + n, w.data_ptr(),
+                                                       ws.data_ptr(), n, 0, rows, count, 4 * rows, frame, 3, h))
+            else:
+                t = jobs.table([jobs.job("matmul_q6r", o.data_ptr(), buf.data_ptr(), buf.data_ptr() + n, w.data_ptr(),
+                                         ws.data_ptr(), 0, n, rows=rows, count=count, os=4 * rows, as_=frame,
+                                         bs=frame)])
+                keep.append(t)
+                calls.append(lambda h, t=t: lib.hq_phase(t, 1, 16, h))
+
+        def launch(h):
+            for c in calls:
+                c(h)
+        sec = _graph_time(torch, launch, reps)
+        pkg.check(lib.hq_last_error())
+        out[label] = {"TOPS": round(ops / sec / 1e12, 1), "frac": round(ops / sec / 1e12 / INT8_PEAK_TOPS, 4),
+                      "ms": round(1e3 * sec, 3)}
+
+    decode("c0 stories15M q8r M=1 (weights in cache: 221 KB x 64)", "int8", [[(768, 288)]], 64)
+    decode("c1 LFM2-350M q8r M=1, 16 layers + lm-head", "int8",
+           [[(1536, 1024)], [(1024, 1024)], [(9216, 1024)], [(1024, 4608)]] * 16 + [[(65536, 1024)]], 1)
+    prefill("c2 Llama-3.2-1B prefill M=512, one layer", "int8",
+            [(3072, 2048), (2048, 2048), (8192, 2048), (8192, 2048), (2048, 8192)], 512)
+    for kind in ("ternary", "int6"):
+        copies = 8 if kind == "ternary" else 3
+        decode(f"c4 27B {kind} M=1, gate+up x {copies}", kind, [[(17408, 5120), (17408, 5120)]], copies)
+        decode(f"c4 27B {kind} M=1, down x {copies}", kind, [[(5120, 17408)]], copies)
+        prefill(f"c4 27B {kind} prefill M=256", kind, [(17408, 5120), (17408, 5120), (5120, 17408)], 256)
+    return out
+
+
 def measure_gemm(torch, pkg, args):
     """config 3's prefill: M = 2048 tokens through one layer's matrices (q, k, v, o, gate, up, down)."""
     lib = pkg.library()
@@ -304,6 +439,8 @@ def main():
     ap.add_argument("--mode", choices=("phase", "fused"), default="phase",
                     help="the headline's phases: quantize_x then hq_phase (the reference's ready() + phase()), or "
                          "hq_matmuls (quantize_x inside the products' launch)")
+    ap.add_argument("--configs", action="store_true",
+                    help="also measure the other configs (stories15M, LFM2-350M, 1B prefill, 27B ternary / int6)")
     ap.add_argument("--phases", action="store_true",
                     help="also time each kind of phase (q/k/v, o, gate/up, down, classifier) on its own")
     ap.add_argument("--calibrate", action="store_true",
@@ -328,6 +465,7 @@ def main():
     del layers, head, phases
     torch.cuda.empty_cache()
     gemm = None if args.no_gemm else measure_gemm(torch, pkg, args)
+    configs = measure_configs(torch, pkg, args) if args.configs else None
     cpu = None if args.no_cpu else cpu_baseline(args)
     derived = fused if args.mode == "fused" else separate
     achieved = derived["gemv_GBps"]
@@ -346,7 +484,7 @@ def main():
                      "bytes_per_launch": round(derived["gemv_bytes_per_launch"])},
         "cpu_baseline": cpu,
         "detail": {"fused": fused, "quantize_then_phase": separate, "quantize_then_phase_with_wc": separate_wc,
-                   "prefill_gemm": gemm},
+                   "prefill_gemm": gemm, "configs": configs},
     }
     print(json.dumps(line))
 

@@ -398,8 +398,94 @@ __global__ __launch_bounds__(256) void gemv_plain(GemvBatch batch) {
 // (the reference's lane k: activations 32k..32k+31 of the group) is block h = k / 2, c in 8 (k % 2) .. + 7: weight
 // dwords 4h + 2(k%2) + {0,1} and, for every plane p, activation dwords 4p + 2(k%2) + {0,1} of the block.  Its
 // integer is sum(code * a) + (minus the sum of its 32 activations) = sum((code - 1) a) exactly (ternary.ts:37-43).
-template <int T>
+//
+// A lane reads 32 bytes of codes a group but 128 bytes of activations (and 32 of their scales and sums): the block
+// copies the activations of its T tokens into LDS once (STAGE; 1.25 n bytes a token), so that only the codes stream
+// from memory, U steps at a time with the next U steps' loads in flight.
+constexpr int kTernarySteps = 4;  // steps a chunk
+
+template <int T, bool STAGE>
+struct TernaryActs {
+  const char *xq[T], *xs[T];  // global (not STAGE)
+  const char *lds;            // STAGE: token t's bytes at lds + t * 1.25 n, its scales after its n bytes
+  int n;
+  HQ_DEV const char *bytes(int t) const { return STAGE ? lds + t * (n + n / 4) : xq[t]; }
+  HQ_DEV const char *area(int t) const { return STAGE ? lds + t * (n + n / 4) + n : xs[t]; }
+};
+
+template <int T, bool STAGE>
+HQ_DEV void ternary_step(const Fold<T> &cf, Fold<T> &f, const TernaryActs<T, STAGE> &A, const uint32_t w[8], float d,
+                         int g, bool valid, int buf, int slot, int lane, float acc[T]) {
+#pragma unroll
+  for (int t = 0; t < T; t++) {
+    const char *xb = A.bytes(t) + (int64_t)g * 128;
+    const float *xs = (const float *)A.area(t);
+    const float4 sc = *(const float4 *)(xs + 4 * g);
+    const int4 su = *(const int4 *)((const int32_t *)(xs + (A.n >> 5)) + 4 * g);
+    const float scale[4] = {sc.x, sc.y, sc.z, sc.w};
+    const int32_t sums[4] = {su.x, su.y, su.z, su.w};
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      uint32_t a[16];
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const uint4 v = ld16(xb + 64 * h + 16 * q);
+        a[4 * q] = v.x; a[4 * q + 1] = v.y; a[4 * q + 2] = v.z; a[4 * q + 3] = v.w;
+      }
+#pragma unroll
+      for (int s = 0; s < 2; s++) {
+        const uint32_t w0 = w[4 * h + 2 * s], w1 = w[4 * h + 2 * s + 1];
+        int32_t dot = sums[2 * h + s];
+        dot = sdot4((int32_t)codes<0>(w0), (int32_t)a[0 + 2 * s], dot);
+        dot = sdot4((int32_t)codes<0>(w1), (int32_t)a[1 + 2 * s], dot);
+        dot = sdot4((int32_t)codes<1>(w0), (int32_t)a[4 + 2 * s], dot);
+        dot = sdot4((int32_t)codes<1>(w1), (int32_t)a[5 + 2 * s], dot);
+        dot = sdot4((int32_t)codes<2>(w0), (int32_t)a[8 + 2 * s], dot);
+        dot = sdot4((int32_t)codes<2>(w1), (int32_t)a[9 + 2 * s], dot);
+        dot = sdot4((int32_t)codes<3>(w0), (int32_t)a[12 + 2 * s], dot);
+        dot = sdot4((int32_t)codes<3>(w1), (int32_t)a[13 + 2 * s], dot);
+        const int k = 2 * h + s;
+        // f(f(whole * xs) * d) (relaxed/signs.ts:206)
+        f.v[buf][slot][t][k][lane] = valid ? fmul(fmul((float)dot, scale[k]), d) : 0.0f;
+      }
+    }
+  }
+  fold_step<T>(cf, buf, slot, lane, acc);
+}
+
+// the codes and group scales of U steps of a lane (step it: group 16 it + lane; past the row's groups, group 0)
+struct TernaryChunk {
+  uint32_t w[kTernarySteps][8];
+  uint32_t h[kTernarySteps];
+  HQ_DEV void load(const char *wrow, const uint16_t *srow, int it0, int lane, int groups) {
+#pragma unroll
+    for (int u = 0; u < kTernarySteps; u++) {
+      const int g = (it0 + u) * 16 + lane;
+      const int gl = g < groups ? g : 0;
+      const uint4 a = ldw16(wrow + gl * 32), b = ldw16(wrow + gl * 32 + 16);
+      w[u][0] = a.x; w[u][1] = a.y; w[u][2] = a.z; w[u][3] = a.w;
+      w[u][4] = b.x; w[u][5] = b.y; w[u][6] = b.z; w[u][7] = b.w;
+      h[u] = srow[gl];
+    }
+  }
+  template <int T, bool STAGE>
+  HQ_DEV void run(Fold<T> &f, const TernaryActs<T, STAGE> &A, int it0, int steps, int groups, int slot, int lane,
+                  float acc[T]) const {
+#pragma unroll
+    for (int u = 0; u < kTernarySteps; u++) {
+      const int it = it0 + u;
+      if (it < steps) {  // uniform in the wave
+        const int g = it * 16 + lane;
+        const bool valid = g < groups;
+        ternary_step<T, STAGE>(f, f, A, w[u], half_to_float(h[u]), valid ? g : 0, valid, it & 1, slot, lane, acc);
+      }
+    }
+  }
+};
+
+template <int T, bool STAGE>
 __global__ __launch_bounds__(256) void gemv_ternary(GemvBatch batch) {
+  extern __shared__ __align__(16) char acts[];
   __shared__ Fold<T> fold[4];
   const int jb = job_of(batch, blockIdx.x);
   const Job &J = batch.job[jb];
@@ -412,54 +498,39 @@ __global__ __launch_bounds__(256) void gemv_ternary(GemvBatch batch) {
   const char *wrow = J.wq + (int64_t)row * groups * 32;
   const uint16_t *srow = (const uint16_t *)J.ws + (int64_t)row * groups;
   Fold<T> &f = fold[wave];
+  TernaryActs<T, STAGE> A;
+#pragma unroll
+  for (int t = 0; t < T; t++) {
+    A.xq[t] = J.xq + t * J.frame;
+    A.xs[t] = J.xs + t * J.sframe;
+  }
+  A.lds = acts;
+  A.n = J.n;
 
   float acc[T];
 #pragma unroll
   for (int t = 0; t < T; t++) acc[t] = 0.0f;
   const int steps = (groups + 15) >> 4;
-  for (int it = 0; it < steps; ++it) {
-    const int g = it * 16 + lane;
-    const bool valid = g < groups;
-    const int gl = valid ? g : 0;
-    const uint4 wa = ld16(wrow + gl * 32), wb = ld16(wrow + gl * 32 + 16);
-    const uint32_t w[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
-    const float d = half_to_float(srow[gl]);
-    const int buf = it & 1;
-#pragma unroll
-    for (int t = 0; t < T; t++) {
-      const char *xb = J.xq + t * J.frame + (int64_t)gl * 128;
-      const float *xs = (const float *)(J.xs + t * J.sframe);
-      const float4 sc = *(const float4 *)(xs + 4 * gl);
-      const int4 su = *(const int4 *)((const int32_t *)(xs + (J.n >> 5)) + 4 * gl);
-      const float scale[4] = {sc.x, sc.y, sc.z, sc.w};
-      const int32_t sums[4] = {su.x, su.y, su.z, su.w};
-#pragma unroll
-      for (int h = 0; h < 2; h++) {
-        uint32_t a[16];
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-          const uint4 v = ld16(xb + 64 * h + 16 * q);
-          a[4 * q] = v.x; a[4 * q + 1] = v.y; a[4 * q + 2] = v.z; a[4 * q + 3] = v.w;
-        }
-#pragma unroll
-        for (int s = 0; s < 2; s++) {
-          const uint32_t w0 = w[4 * h + 2 * s], w1 = w[4 * h + 2 * s + 1];
-          int32_t dot = sums[2 * h + s];
-          dot = sdot4((int32_t)codes<0>(w0), (int32_t)a[0 + 2 * s], dot);
-          dot = sdot4((int32_t)codes<0>(w1), (int32_t)a[1 + 2 * s], dot);
-          dot = sdot4((int32_t)codes<1>(w0), (int32_t)a[4 + 2 * s], dot);
-          dot = sdot4((int32_t)codes<1>(w1), (int32_t)a[5 + 2 * s], dot);
-          dot = sdot4((int32_t)codes<2>(w0), (int32_t)a[8 + 2 * s], dot);
-          dot = sdot4((int32_t)codes<2>(w1), (int32_t)a[9 + 2 * s], dot);
-          dot = sdot4((int32_t)codes<3>(w0), (int32_t)a[12 + 2 * s], dot);
-          dot = sdot4((int32_t)codes<3>(w1), (int32_t)a[13 + 2 * s], dot);
-          const int k = 2 * h + s;
-          // f(f(whole * xs) * d) (relaxed/signs.ts:206)
-          f.v[buf][slot][t][k][lane] = valid ? fmul(fmul((float)dot, scale[k]), d) : 0.0f;
-        }
+  TernaryChunk a, b;
+  if (steps > 0) a.load(wrow, srow, 0, lane, groups);  // the first codes in flight during the staging
+  if (STAGE) {
+    // every token's n bytes, then its n/32 scales and n/32 sums (1.25 n bytes), 16 bytes a thread at a time
+    const int per = J.n + J.n / 4, chunks = per / 16;
+    for (int t = 0; t < T; t++)
+      for (int c = threadIdx.x; c < chunks; c += blockDim.x) {
+        const int o = 16 * c;
+        const uint4 v = o < J.n ? ld16(J.xq + t * J.frame + o) : ld16(J.xs + t * J.sframe + (o - J.n));
+        *(uint4 *)(acts + t * per + o) = v;
       }
+    __syncthreads();
+  }
+  for (int it = 0; it < steps; it += 2 * kTernarySteps) {
+    if (it + kTernarySteps < steps) b.load(wrow, srow, it + kTernarySteps, lane, groups);
+    a.run<T, STAGE>(f, A, it, steps, groups, slot, lane, acc);
+    if (it + kTernarySteps < steps) {
+      if (it + 2 * kTernarySteps < steps) a.load(wrow, srow, it + 2 * kTernarySteps, lane, groups);
+      b.run<T, STAGE>(f, A, it + kTernarySteps, steps, groups, slot, lane, acc);
     }
-    fold_step<T>(f, buf, slot, lane, acc);
   }
   float sum[T];
 #pragma unroll
@@ -470,6 +541,10 @@ __global__ __launch_bounds__(256) void gemv_ternary(GemvBatch batch) {
     for (int t = 0; t < T; t++) ((float *)(J.out + t * J.os))[row] = sum[t];
   }
 }
+
+// the LDS a ternary block stages for T tokens of n activations (0: too large, read through the L1)
+constexpr size_t kTernaryStageMax = 64 * 1024;
+HQ_HOST_DEV constexpr size_t ternary_stage_bytes(int T, int n) { return (size_t)T * (n + n / 4); }
 
 template <int PACK, int T, int SRC>
 hipError_t launch_relaxed(const GemvBatch &b, int blocks, bool wc, size_t lds, hipStream_t s) {
@@ -496,7 +571,14 @@ hipError_t launch_t(Kind kind, const GemvBatch &b, int blocks, bool wc, int src,
   case Q8: hipLaunchKernelGGL((gemv_plain<8, T>), grid, block, 0, s, b); break;
   case Q6: hipLaunchKernelGGL((gemv_plain<6, T>), grid, block, 0, s, b); break;
   case T2R:
-  case T2: hipLaunchKernelGGL((gemv_ternary<T>), grid, block, 0, s, b); break;
+  case T2: {
+    int nmax = 0;
+    for (int j = 0; j < b.njobs; j++) nmax = b.job[j].n > nmax ? b.job[j].n : nmax;
+    const size_t bytes = ternary_stage_bytes(T, nmax);
+    if (bytes <= kTernaryStageMax) hipLaunchKernelGGL((gemv_ternary<T, true>), grid, block, bytes, s, b);
+    else hipLaunchKernelGGL((gemv_ternary<T, false>), grid, block, 0, s, b);
+    break;
+  }
   default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
