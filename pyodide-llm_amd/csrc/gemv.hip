@@ -400,17 +400,23 @@ __global__ __launch_bounds__(256) void gemv_plain(GemvBatch batch) {
 // integer is sum(code * a) + (minus the sum of its 32 activations) = sum((code - 1) a) exactly (ternary.ts:37-43).
 //
 // A lane reads 32 bytes of codes a group but 128 bytes of activations (and 32 of their scales and sums): the block
-// copies the activations of its T tokens into LDS once (STAGE; 1.25 n bytes a token), so that only the codes stream
-// from memory, U steps at a time with the next U steps' loads in flight.
+// copies the activations of its T tokens into LDS once (STAGE), so that only the codes stream from memory, U steps
+// at a time with the next U steps' loads in flight.  In LDS a group's 128 bytes take 144 (16 bytes of padding), so
+// that the 16 lanes of a row, which read the same 16 bytes of 16 consecutive groups, hit 16 different bank quads.
 constexpr int kTernarySteps = 4;  // steps a chunk
+constexpr int kTernaryPitch = 144;  // LDS bytes a group of 128 activations
+
+HQ_HOST_DEV constexpr int ternary_token_bytes(int n) { return (n >> 7) * kTernaryPitch + n / 4; }
 
 template <int T, bool STAGE>
 struct TernaryActs {
   const char *xq[T], *xs[T];  // global (not STAGE)
-  const char *lds;            // STAGE: token t's bytes at lds + t * 1.25 n, its scales after its n bytes
+  const char *lds;            // STAGE: token t's groups at lds + t * ternary_token_bytes(n), its scales after them
   int n;
-  HQ_DEV const char *bytes(int t) const { return STAGE ? lds + t * (n + n / 4) : xq[t]; }
-  HQ_DEV const char *area(int t) const { return STAGE ? lds + t * (n + n / 4) + n : xs[t]; }
+  HQ_DEV const char *group(int t, int g) const {
+    return STAGE ? lds + t * ternary_token_bytes(n) + g * kTernaryPitch : xq[t] + (int64_t)g * 128;
+  }
+  HQ_DEV const char *area(int t) const { return STAGE ? lds + t * ternary_token_bytes(n) + (n >> 7) * kTernaryPitch : xs[t]; }
 };
 
 template <int T, bool STAGE>
@@ -418,7 +424,7 @@ HQ_DEV void ternary_step(const Fold<T> &cf, Fold<T> &f, const TernaryActs<T, STA
                          int g, bool valid, int buf, int slot, int lane, float acc[T]) {
 #pragma unroll
   for (int t = 0; t < T; t++) {
-    const char *xb = A.bytes(t) + (int64_t)g * 128;
+    const char *xb = A.group(t, g);
     const float *xs = (const float *)A.area(t);
     const float4 sc = *(const float4 *)(xs + 4 * g);
     const int4 su = *(const int4 *)((const int32_t *)(xs + (A.n >> 5)) + 4 * g);
@@ -514,13 +520,13 @@ __global__ __launch_bounds__(256) void gemv_ternary(GemvBatch batch) {
   TernaryChunk a, b;
   if (steps > 0) a.load(wrow, srow, 0, lane, groups);  // the first codes in flight during the staging
   if (STAGE) {
-    // every token's n bytes, then its n/32 scales and n/32 sums (1.25 n bytes), 16 bytes a thread at a time
-    const int per = J.n + J.n / 4, chunks = per / 16;
+    // every token's n bytes (a group's 128 in 144), then its n/32 scales and n/32 sums, 16 bytes a thread at a time
+    const int per = ternary_token_bytes(J.n), chunks = (J.n + J.n / 4) / 16, gb = groups * kTernaryPitch;
     for (int t = 0; t < T; t++)
       for (int c = threadIdx.x; c < chunks; c += blockDim.x) {
         const int o = 16 * c;
-        const uint4 v = o < J.n ? ld16(J.xq + t * J.frame + o) : ld16(J.xs + t * J.sframe + (o - J.n));
-        *(uint4 *)(acts + t * per + o) = v;
+        if (o < J.n) *(uint4 *)(acts + t * per + (o >> 7) * kTernaryPitch + (o & 127)) = ld16(J.xq + t * J.frame + o);
+        else *(uint4 *)(acts + t * per + gb + (o - J.n)) = ld16(J.xs + t * J.sframe + (o - J.n));
       }
     __syncthreads();
   }
@@ -544,7 +550,7 @@ __global__ __launch_bounds__(256) void gemv_ternary(GemvBatch batch) {
 
 // the LDS a ternary block stages for T tokens of n activations (0: too large, read through the L1)
 constexpr size_t kTernaryStageMax = 64 * 1024;
-HQ_HOST_DEV constexpr size_t ternary_stage_bytes(int T, int n) { return (size_t)T * (n + n / 4); }
+HQ_HOST_DEV constexpr size_t ternary_stage_bytes(int T, int n) { return (size_t)T * ternary_token_bytes(n); }
 
 template <int PACK, int T, int SRC>
 hipError_t launch_relaxed(const GemvBatch &b, int blocks, bool wc, size_t lds, hipStream_t s) {
