@@ -320,6 +320,30 @@ HQ_DEV void fold_step(const Fold<T> &f, int buf, int slot, int lane, float acc[T
   }
 }
 
+// the same for rows of L lanes (64 / L rows a wave): lane k (k < 4) of each row adds part k of the L groups in order
+template <int T, int L>
+struct FoldL {
+  float v[2][64 / L][T][4][L];
+};
+template <int T, int L>
+HQ_DEV void fold_step_l(const FoldL<T, L> &f, int buf, int slot, int lane, float acc[T]) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const int k = lane & 3;
+#pragma unroll
+  for (int t = 0; t < T; t++) {
+    const float4 *src = (const float4 *)f.v[buf][slot][t][k];
+    float a = acc[t];
+#pragma unroll
+    for (int q = 0; q < L / 4; q++) {
+      const float4 v = src[q];
+      a = fadd(fadd(fadd(fadd(a, v.x), v.y), v.z), v.w);
+    }
+    acc[t] = a;
+  }
+}
+
 // ---------------------------------------------------------------------------------------------------------------
 // plain int8 / int6 (matmul_q8, matmul_q6)
 // ---------------------------------------------------------------------------------------------------------------
@@ -403,7 +427,10 @@ __global__ __launch_bounds__(256) void gemv_plain(GemvBatch batch) {
 // copies the activations of its T tokens into LDS once (STAGE), so that only the codes stream from memory, U steps
 // at a time with the next U steps' loads in flight.  In LDS a group's 128 bytes take 144 (16 bytes of padding), so
 // that the 16 lanes of a row, which read the same 16 bytes of 16 consecutive groups, hit 16 different bank quads.
-constexpr int kTernarySteps = 4;  // steps a chunk
+#ifndef HQ_TERNARY_STEPS
+#define HQ_TERNARY_STEPS 1
+#endif
+constexpr int kTernarySteps = HQ_TERNARY_STEPS;  // steps a chunk
 constexpr int kTernaryPitch = 144;  // LDS bytes a group of 128 activations
 
 HQ_HOST_DEV constexpr int ternary_token_bytes(int n) { return (n >> 7) * kTernaryPitch + n / 4; }
@@ -419,9 +446,9 @@ struct TernaryActs {
   HQ_DEV const char *area(int t) const { return STAGE ? lds + t * ternary_token_bytes(n) + (n >> 7) * kTernaryPitch : xs[t]; }
 };
 
-template <int T, bool STAGE>
-HQ_DEV void ternary_step(const Fold<T> &cf, Fold<T> &f, const TernaryActs<T, STAGE> &A, const uint32_t w[8], float d,
-                         int g, bool valid, int buf, int slot, int lane, float acc[T]) {
+template <int T, bool STAGE, int L>
+HQ_DEV void ternary_step(FoldL<T, L> &f, const TernaryActs<T, STAGE> &A, const uint32_t w[8], float d, int g,
+                         bool valid, int buf, int slot, int lane, float acc[T]) {
 #pragma unroll
   for (int t = 0; t < T; t++) {
     const char *xb = A.group(t, g);
@@ -456,17 +483,18 @@ HQ_DEV void ternary_step(const Fold<T> &cf, Fold<T> &f, const TernaryActs<T, STA
       }
     }
   }
-  fold_step<T>(cf, buf, slot, lane, acc);
+  fold_step_l<T, L>(f, buf, slot, lane, acc);
 }
 
-// the codes and group scales of U steps of a lane (step it: group 16 it + lane; past the row's groups, group 0)
+// the codes and group scales of U steps of a lane (step it: group L it + lane; past the row's groups, group 0)
+template <int L>
 struct TernaryChunk {
   uint32_t w[kTernarySteps][8];
   uint32_t h[kTernarySteps];
   HQ_DEV void load(const char *wrow, const uint16_t *srow, int it0, int lane, int groups) {
 #pragma unroll
     for (int u = 0; u < kTernarySteps; u++) {
-      const int g = (it0 + u) * 16 + lane;
+      const int g = (it0 + u) * L + lane;
       const int gl = g < groups ? g : 0;
       const uint4 a = ldw16(wrow + gl * 32), b = ldw16(wrow + gl * 32 + 16);
       w[u][0] = a.x; w[u][1] = a.y; w[u][2] = a.z; w[u][3] = a.w;
@@ -475,35 +503,36 @@ struct TernaryChunk {
     }
   }
   template <int T, bool STAGE>
-  HQ_DEV void run(Fold<T> &f, const TernaryActs<T, STAGE> &A, int it0, int steps, int groups, int slot, int lane,
+  HQ_DEV void run(FoldL<T, L> &f, const TernaryActs<T, STAGE> &A, int it0, int steps, int groups, int slot, int lane,
                   float acc[T]) const {
 #pragma unroll
     for (int u = 0; u < kTernarySteps; u++) {
       const int it = it0 + u;
       if (it < steps) {  // uniform in the wave
-        const int g = it * 16 + lane;
+        const int g = it * L + lane;
         const bool valid = g < groups;
-        ternary_step<T, STAGE>(f, f, A, w[u], half_to_float(h[u]), valid ? g : 0, valid, it & 1, slot, lane, acc);
+        ternary_step<T, STAGE, L>(f, A, w[u], half_to_float(h[u]), valid ? g : 0, valid, it & 1, slot, lane, acc);
       }
     }
   }
 };
 
-template <int T, bool STAGE>
+// rows of L lanes (16: 16 rows a block; 32 for long rows: twice the waves on the same rows)
+template <int T, bool STAGE, int L>
 __global__ __launch_bounds__(256) void gemv_ternary(GemvBatch batch) {
   extern __shared__ __align__(16) char acts[];
-  __shared__ Fold<T> fold[4];
+  __shared__ FoldL<T, L> fold[4];
   const int jb = job_of(batch, blockIdx.x);
   const Job &J = batch.job[jb];
-  const int lane = threadIdx.x & 15;
-  const int wave = threadIdx.x >> 6, slot = (threadIdx.x >> 4) & 3;
-  const int row_u = J.r0 + (blockIdx.x - batch.block0[jb]) * kRowsPerBlock + (threadIdx.x >> 4);
+  const int lane = threadIdx.x & (L - 1);
+  const int wave = threadIdx.x >> 6, slot = (threadIdx.x & 63) / L;
+  const int row_u = J.r0 + (blockIdx.x - batch.block0[jb]) * (256 / L) + threadIdx.x / L;
   const bool live = row_u < J.r1;
   const int row = live ? row_u : J.r1 - 1;
   const int groups = J.n >> 7;
   const char *wrow = J.wq + (int64_t)row * groups * 32;
   const uint16_t *srow = (const uint16_t *)J.ws + (int64_t)row * groups;
-  Fold<T> &f = fold[wave];
+  FoldL<T, L> &f = fold[wave];
   TernaryActs<T, STAGE> A;
 #pragma unroll
   for (int t = 0; t < T; t++) {
@@ -516,26 +545,38 @@ __global__ __launch_bounds__(256) void gemv_ternary(GemvBatch batch) {
   float acc[T];
 #pragma unroll
   for (int t = 0; t < T; t++) acc[t] = 0.0f;
-  const int steps = (groups + 15) >> 4;
-  TernaryChunk a, b;
+  const int steps = (groups + L - 1) / L;
+  TernaryChunk<L> a, b;
   if (steps > 0) a.load(wrow, srow, 0, lane, groups);  // the first codes in flight during the staging
   if (STAGE) {
-    // every token's n bytes (a group's 128 in 144), then its n/32 scales and n/32 sums, 16 bytes a thread at a time
+    // every token's n bytes (a group's 128 in 144), then its n/32 scales and n/32 sums: 16 bytes a thread at a time,
+    // eight loads of a thread in flight before their stores
     const int per = ternary_token_bytes(J.n), chunks = (J.n + J.n / 4) / 16, gb = groups * kTernaryPitch;
+    constexpr int K = 8;
     for (int t = 0; t < T; t++)
-      for (int c = threadIdx.x; c < chunks; c += blockDim.x) {
-        const int o = 16 * c;
-        if (o < J.n) *(uint4 *)(acts + t * per + (o >> 7) * kTernaryPitch + (o & 127)) = ld16(J.xq + t * J.frame + o);
-        else *(uint4 *)(acts + t * per + gb + (o - J.n)) = ld16(J.xs + t * J.sframe + (o - J.n));
+      for (int base = 0; base < chunks; base += K * 256) {
+        uint4 v[K];
+#pragma unroll
+        for (int u = 0; u < K; u++) {
+          const int o = 16 * (base + u * 256 + (int)threadIdx.x);
+          if (o < J.n) v[u] = ld16(J.xq + t * J.frame + o);
+          else if (o < J.n + J.n / 4) v[u] = ld16(J.xs + t * J.sframe + (o - J.n));
+        }
+#pragma unroll
+        for (int u = 0; u < K; u++) {
+          const int o = 16 * (base + u * 256 + (int)threadIdx.x);
+          if (o < J.n) *(uint4 *)(acts + t * per + (o >> 7) * kTernaryPitch + (o & 127)) = v[u];
+          else if (o < J.n + J.n / 4) *(uint4 *)(acts + t * per + gb + (o - J.n)) = v[u];
+        }
       }
     __syncthreads();
   }
   for (int it = 0; it < steps; it += 2 * kTernarySteps) {
     if (it + kTernarySteps < steps) b.load(wrow, srow, it + kTernarySteps, lane, groups);
-    a.run<T, STAGE>(f, A, it, steps, groups, slot, lane, acc);
+    a.template run<T, STAGE>(f, A, it, steps, groups, slot, lane, acc);
     if (it + kTernarySteps < steps) {
       if (it + 2 * kTernarySteps < steps) a.load(wrow, srow, it + 2 * kTernarySteps, lane, groups);
-      b.run<T, STAGE>(f, A, it + kTernarySteps, steps, groups, slot, lane, acc);
+      b.template run<T, STAGE>(f, A, it + kTernarySteps, steps, groups, slot, lane, acc);
     }
   }
   float sum[T];
@@ -548,8 +589,25 @@ __global__ __launch_bounds__(256) void gemv_ternary(GemvBatch batch) {
   }
 }
 
-// the LDS a ternary block stages for T tokens of n activations (0: too large, read through the L1)
-constexpr size_t kTernaryStageMax = 64 * 1024;
+// the LDS a ternary block stages for T tokens of n activations (beyond: read through the L1)
+#ifndef HQ_TERNARY_STAGE_MAX
+#define HQ_TERNARY_STAGE_MAX (64 * 1024)
+#endif
+constexpr size_t kTernaryStageMax = HQ_TERNARY_STAGE_MAX;
+// lanes a row of ternary weights: 32 for rows of at least kTernaryLongRow weights
+#ifndef HQ_TERNARY_LONG
+#define HQ_TERNARY_LONG 8192
+#endif
+#ifndef HQ_TERNARY_L8
+#define HQ_TERNARY_L8 1
+#endif
+#ifndef HQ_TERNARY_LONG64
+#define HQ_TERNARY_LONG64 1000000000
+#endif
+HQ_HOST_DEV constexpr int ternary_lanes(int n) {
+  return n >= HQ_TERNARY_LONG64 ? 64 : n >= HQ_TERNARY_LONG ? 32
+       : (HQ_TERNARY_L8 && (n >> 7) % 16 != 0 && (n >> 7) % 8 == 0) ? 8 : 16;
+}
 HQ_HOST_DEV constexpr size_t ternary_stage_bytes(int T, int n) { return (size_t)T * ternary_token_bytes(n); }
 
 template <int PACK, int T, int SRC>
@@ -581,8 +639,20 @@ hipError_t launch_t(Kind kind, const GemvBatch &b, int blocks, bool wc, int src,
     int nmax = 0;
     for (int j = 0; j < b.njobs; j++) nmax = b.job[j].n > nmax ? b.job[j].n : nmax;
     const size_t bytes = ternary_stage_bytes(T, nmax);
-    if (bytes <= kTernaryStageMax) hipLaunchKernelGGL((gemv_ternary<T, true>), grid, block, bytes, s, b);
-    else hipLaunchKernelGGL((gemv_ternary<T, false>), grid, block, 0, s, b);
+    const bool stage = bytes <= kTernaryStageMax;
+    if (ternary_lanes(nmax) == 32) {
+      if (stage) hipLaunchKernelGGL((gemv_ternary<T, true, 32>), grid, block, bytes, s, b);
+      else hipLaunchKernelGGL((gemv_ternary<T, false, 32>), grid, block, 0, s, b);
+    } else if (ternary_lanes(nmax) == 64) {
+      if (stage) hipLaunchKernelGGL((gemv_ternary<T, true, 64>), grid, block, bytes, s, b);
+      else hipLaunchKernelGGL((gemv_ternary<T, false, 64>), grid, block, 0, s, b);
+    } else if (ternary_lanes(nmax) == 8) {
+      if (stage) hipLaunchKernelGGL((gemv_ternary<T, true, 8>), grid, block, bytes, s, b);
+      else hipLaunchKernelGGL((gemv_ternary<T, false, 8>), grid, block, 0, s, b);
+    } else {
+      if (stage) hipLaunchKernelGGL((gemv_ternary<T, true, 16>), grid, block, bytes, s, b);
+      else hipLaunchKernelGGL((gemv_ternary<T, false, 16>), grid, block, 0, s, b);
+    }
     break;
   }
   default: return hipErrorInvalidValue;
@@ -604,11 +674,12 @@ hipError_t launch_batch(Kind kind, const Job *jobs, int32_t njobs, const char *x
   if (njobs < 1 || njobs > kMaxJobs) return hipErrorInvalidValue;
   GemvBatch b{};
   int blocks = 0, nmax = 0;
+  for (int j = 0; j < njobs; j++) nmax = jobs[j].n > nmax ? jobs[j].n : nmax;
+  const int rpb = (kind == T2R || kind == T2) ? 256 / ternary_lanes(nmax) : rows_per_block(kind);
   for (int j = 0; j < njobs; j++) {
     b.job[j] = jobs[j];
     b.block0[j] = blocks;
-    blocks += (jobs[j].r1 - jobs[j].r0 + rows_per_block(kind) - 1) / rows_per_block(kind);
-    nmax = jobs[j].n > nmax ? jobs[j].n : nmax;
+    blocks += (jobs[j].r1 - jobs[j].r0 + rpb - 1) / rpb;
   }
   b.block0[njobs] = blocks;
   b.njobs = njobs;

@@ -348,9 +348,11 @@ def ternary_acts(rng, oracle, n, pattern=None):
     return oracle.interleave(a, xs)
 
 
-@pytest.mark.parametrize("groups", [1, 2, 3, 4, 5, 7, 9, 40])
+@pytest.mark.parametrize("groups", [1, 2, 3, 4, 5, 7, 9, 24, 40, 72, 136])
 @pytest.mark.parametrize("name", ["matmul_t2r", "matmul_t2"])
 def test_ternary_token(k, arena, oracle, groups, name):
+    """Every row length class of the token kernel: rows of 8 lanes (groups a multiple of 8, not of 16), of 16, and of
+    32 (8192 weights and more); activations staged in LDS."""
     n, codes, halves, rng = ternary_case(groups)
     wq = arena.put(pack_ternary(codes))
     wsa = arena.put(halves)
@@ -394,9 +396,10 @@ def test_ternary_largest_sums(k, arena, oracle):
             assert same_bits(got, want), f"pattern {pi} token {t}: {first_difference(got, want)}"
 
 
-@pytest.mark.parametrize("count", [1, 2, 3, 4, 5, 7, 8, 9, 16, 17, 64, 65, 100])
-@pytest.mark.parametrize("groups", [1, 3, 9])
+@pytest.mark.parametrize("count,groups", [(c, g) for c in [1, 2, 3, 4, 5, 7, 8, 9, 16, 17, 64, 65, 100]
+                                          for g in [1, 3, 9]] + [(4, 136), (3, 136), (2, 40)])
 def test_t2r_tile(k, arena, oracle, count, groups):
+    """(4, 136): four tokens of 17408 activations are more than the token kernel stages in LDS (read through the L1)"""
     n, codes, halves, rng = ternary_case(groups, rows=70, seed=500 + count)
     rows = 70
     wbytes = pack_ternary(codes)
