@@ -25,14 +25,20 @@
 // matrix core; CDNA4's VALU does 64 lanes a clock a CU against 4096 int8 MACs, so the epilogue, not the MFMA, bounds
 // this kernel (at best 32 / (3 x 4096 / 64) = 16.7 % of dense int8 peak, 12.5 % for ternary).
 //
-// A block is 16 waves and a 128-row x 64-token tile: wave w takes rows 32 (w / 4) .. + 31 and chain w % 4, for both
-// 32-token halves (the weights' operand read once for two MFMAs).  The operands come into LDS by direct buffer-to-LDS
-// loads (no registers on the way), into a ring of 4 stage buffers: a stage is 4 groups (int8, int6) or 2 groups of
-// 128 (ternary), and the loads of stages s + 1 .. s + 3 are in flight while stage s is computed.  Every wave issues
-// exactly 3 loads a stage (some of them into a scratch area), so that one s_waitcnt vmcnt count means "my loads of
+// A block computes a 128-row x 64-token tile.  int8 / int6: 8 waves, two a SIMD; the waves of pair p (waves 4 p ..
+// 4 p + 3) take rows 64 p .. + 63 and chain w % 4, four 32 x 32 sub-tiles each (the weights' operand read once for
+// two MFMAs, the tokens' for two slices).  Ternary: 16 waves; wave w takes rows 32 (w / 4) .. + 31 and chain w % 4,
+// both 32-token halves.  The operands come into LDS by direct buffer-to-LDS loads (no registers on the way), into a
+// ring of 4 stage buffers: a stage is 4 groups (int8, int6) or 2 groups of 128 (ternary), and the loads of stages
+// s + 1 .. s + 3 are in flight while stage s is computed.  Every wave issues the same number of loads a stage (6 for
+// int8 / int6, 3 for ternary; some of them into a scratch area), so that one s_waitcnt vmcnt count means "my loads of
 // stage s have landed"; a bare s_barrier then makes them everyone's.  The 16-byte chunks of a row are stored XOR-
 // swizzled so that the MFMA operand reads (32 rows or tokens, one chunk each) spread over the LDS banks.  Blocks are
 // ordered so that the blocks one XCD runs at a time share their rows and tokens in that XCD's L2.
+//
+// Measured on MI355X (8B gate+up, 2048 tokens): the epilogue, the loads' issue and the f32 outer product add up
+// rather than overlap; one wave issues VALU at about half a SIMD's rate, and the VALU and the matrix core run side
+// by side only part of the time, so the kernel sits near 300 int8 TOP/s against the 16.7 % bound above.
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -45,10 +51,8 @@ typedef int32_t v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
 constexpr int BR = 128, BT = 64;  // block tile: rows x tokens
-constexpr int NT = 1024;          // 16 waves: 4 slices of 32 rows x 4 chains
 constexpr int RING = 4;           // stage buffers
 constexpr int AHEAD = RING - 1;   // stages loaded beyond the one computed
-constexpr int LOADS = 3;          // loads a wave a stage
 
 HQ_DEV v16i zero16i() {
   v16i z;
@@ -101,11 +105,13 @@ HQ_DEV void stage_ready() {
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 }
-// stage s of `total` loaded stages: the loads issued after its own are those of the next min(AHEAD - 1, ...) stages
+// stage s of `total` loaded stages, N loads a wave a stage: the loads issued after its own are those of the next
+// min(AHEAD - 1, ...) stages
+template <int N>
 HQ_DEV void wait_for(int s, int total) {
   const int later = min(AHEAD - 1, total - 1 - s);
-  if (later >= 2) stage_ready<2 * LOADS>();
-  else if (later == 1) stage_ready<LOADS>();
+  if (later >= 2) stage_ready<2 * N>();
+  else if (later == 1) stage_ready<N>();
   else stage_ready<0>();
 }
 
@@ -154,10 +160,15 @@ HQ_DEV void add_chains(float acc0[16], float acc1[16], float *p0, float *p1, int
 
 // ---------------------------------------------------------------------------------------------------------------
 // int8 / int6 weights, relaxed activations (matmul_q8r_tile, matmul_q6r)
+// A block is 8 waves, two waves a SIMD with up to 256 registers each: wave w takes chain w % 4 of rows
+// 64 (w / 4) .. + 63 (two 32-row slices) for both 32-token halves, four 32 x 32 sub-tiles, so that the MFMAs of one
+// sub-tile run while the epilogue of the one before it does.
 // MFMA A = weights (m = row), B = activations (n = token): lane l holds token l % 32 of its half and rows
 // 8 (r / 4) + 4 (l / 32) + r % 4 of its slice (r = 0..15); K half l / 32 is bytes 16 (l / 32) .. + 15 of the group.
 // ---------------------------------------------------------------------------------------------------------------
-constexpr int QG = 4;  // groups a stage
+constexpr int QG = 4;       // groups a stage
+constexpr int QNT = 512;    // threads a block
+constexpr int QLOADS = 6;   // loads a wave a stage
 
 struct alignas(16) StageQ {
   char w[BR * 128];    // int8: 128 rows x 4 groups x 32 bytes, chunks swizzled; int6: 128 rows x 4 x 24 bytes
@@ -185,12 +196,12 @@ HQ_DEV v4i six_half(const char *p, int kh) {
   return v;
 }
 
-// a block's loads of int8 / int6 stages: wave w's three loads a stage and their offsets
+// a block's loads of int8 / int6 stages: wave w's six loads a stage and their offsets
 template <int PACK, bool WC>
 struct Relaxed {
   static constexpr int GB = PACK == 8 ? 32 : 24;  // bytes of a group of weights
   __amdgpu_buffer_rsrc_t rw, rx, rws, rwc, rxs;
-  uint32_t oa, ob, oc;
+  uint32_t oa[2], ob, oc, oe;
   int wave;
   char *junk;
 
@@ -202,97 +213,123 @@ struct Relaxed {
     rwc = resource(J.wc + (int64_t)row0 * ng * 4, WC ? (int64_t)(J.r1 - row0) * ng * 4 : 0);
     rx = resource(J.xq + tok0 * J.frame, (M - 1 - tok0) * J.frame + J.n);
     rxs = resource(J.xs + tok0 * J.sframe, (M - 1 - tok0) * J.sframe + 4 * ng);
-    // load a: the weights.  int8: wave w rows 8 w .. + 7, lane l row 8 w + l / 8, slot l % 8 holding chunk
-    // (l % 8) ^ swz(row); int6: 16-byte piece 64 w + l of the stage's 128 rows x 96 bytes (waves 0..11)
-    if (PACK == 8) {
-      const int row = 8 * w + (lane >> 3), c = (lane & 7) ^ swz(row);
-      oa = (uint32_t)(row * rb + (c >> 1) * 32 + (c & 1) * 16);
-    } else {
-      const int q = 64 * w + lane;
-      oa = (uint32_t)((q / 6) * rb + (q % 6) * 16);
+    // loads a0, a1: 1 KB pieces 2 w and 2 w + 1 of the stage's weights.  int8: piece c is rows 8 c .. + 7, lane l
+    // row 8 c + l / 8, slot l % 8 holding chunk (l % 8) ^ swz(row); int6: 16-byte piece 64 c + l of 128 rows x 96
+    // bytes (pieces 0..11)
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const int c = 2 * w + i;
+      if (PACK == 8) {
+        const int row = 8 * c + (lane >> 3), ch = (lane & 7) ^ swz(row);
+        oa[i] = (uint32_t)(row * rb + (ch >> 1) * 32 + (ch & 1) * 16);
+      } else {
+        const int q = 64 * c + lane;
+        oa[i] = (uint32_t)((q / 6) * rb + (q % 6) * 16);
+      }
     }
-    // load b: waves 0..7 the activations (tokens 8 w .. + 7, as the weights); waves 8..15 the rows' scales
-    // (group (w - 8) / 2, rows 64 ((w - 8) % 2) + l)
-    if (w < 8) {
-      const int tok = 8 * w + (lane >> 3), c = (lane & 7) ^ swz(tok);
-      ob = (uint32_t)(tok * J.frame + (c >> 1) * 32 + (c & 1) * 16);
-    } else {
-      const int i = w - 8;
-      ob = (uint32_t)(((64 * (i & 1) + lane) * ng + (i >> 1)) * 4);
+    // load b: the activations of tokens 8 w .. + 7, as the weights
+    {
+      const int tok = 8 * w + (lane >> 3), ch = (lane & 7) ^ swz(tok);
+      ob = (uint32_t)(tok * J.frame + (ch >> 1) * 32 + (ch & 1) * 16);
     }
-    // load c: waves 0..7 the corrections (as the scales), waves 8..11 the tokens' scales (group w - 8, token l)
-    if (w < 8) oc = (uint32_t)(((64 * (w & 1) + lane) * ng + (w >> 1)) * 4);
-    else oc = (uint32_t)(lane * J.sframe + (w - 8) * 4);
+    // loads c, d: the rows' scales and corrections of group w / 2, rows 64 (w % 2) + l
+    oc = (uint32_t)(((64 * (w & 1) + lane) * ng + (w >> 1)) * 4);
+    // load e: waves 0..3 the tokens' scales of group w, token l
+    oe = (uint32_t)(lane * J.sframe + (w & 3) * 4);
   }
 
-  // the 3 loads of stage s (groups 4 s .. 4 s + 3) into S
+  // the 6 loads of stage s (groups 4 s .. 4 s + 3) into S
   HQ_DEV void load(StageQ &S, int s) {
     const int w = wave;
-    if (PACK == 8 || w < 12) dma16(rw, S.w + w * 1024, oa, s * QG * GB);
-    else dma16(rxs, junk, 0, 0);
-    if (w < 8) dma16(rx, S.x + w * 1024, ob, s * QG * 32);
-    else dma4(rws, &S.ws[(w - 8) >> 1][64 * ((w - 8) & 1)], ob, s * QG * 4);
-    if (w < 8) {
-      if (WC) dma4(rwc, &S.wc[w >> 1][64 * (w & 1)], oc, s * QG * 4);
-      else dma4(rxs, junk, 0, 0);
-    } else if (w < 12) {
-      dma4(rxs, &S.xs[w - 8][0], oc, s * QG * 4);
-    } else {
-      dma4(rxs, junk, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      if (PACK == 8 || 2 * w + i < 12) dma16(rw, S.w + (2 * w + i) * 1024, oa[i], s * QG * GB);
+      else dma16(rxs, junk, 0, 0);
     }
+    dma16(rx, S.x + w * 1024, ob, s * QG * 32);
+    dma4(rws, &S.ws[w >> 1][64 * (w & 1)], oc, s * QG * 4);
+    if (WC) dma4(rwc, &S.wc[w >> 1][64 * (w & 1)], oc, s * QG * 4);
+    else dma4(rxs, junk, 0, 0);
+    if (w < 4) dma4(rxs, &S.xs[w][0], oe, s * QG * 4);
+    else dma4(rxs, junk, 0, 0);
   }
 };
 
-// group gi of stage S for the lane's slice, both token halves: the exact integers (MFMA, from the corrections) and
-// the scales' products (the outer-product MFMA), each half added into its chain as soon as it is there
+// group gi of stage S into the chain of the lane's four sub-tiles (slices 2 pair, 2 pair + 1 x both token halves,
+// acc[2 slice + half]): the exact integers (MFMA, from the corrections) and the scales' products (the outer-product
+// MFMA), each term f(f(C) * f(ws * xs)) (relaxed/int8.ts:26-39)
 template <int PACK, bool WC>
-HQ_DEV void q_group(float acc0[16], float acc1[16], const StageQ &S, int gi, int slice, int lane) {
-  const int kh = lane >> 5, row = 32 * slice + (lane & 31), tok = lane & 31;
-  v4i A;
-  if (PACK == 8) A = *(const v4i *)(S.w + row * 128 + ((2 * gi + kh) ^ swz(row)) * 16);
-  else A = six_half(S.w + row * 96 + gi * 24, kh);
-  v16i wc;
-  if (WC) {  // the caller's corrections of the lane's 16 rows
-    const int rbase = 32 * slice + 4 * kh;
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-      const int4 c4 = *(const int4 *)&S.wc[gi][rbase + 8 * q];
-      wc[4 * q] = c4.x; wc[4 * q + 1] = c4.y; wc[4 * q + 2] = c4.z; wc[4 * q + 3] = c4.w;
-    }
-  }
-  const float wsv = lane < 32 ? S.ws[gi][32 * slice + lane] : 0.0f;
+HQ_DEV void q_group(float acc[4][16], const StageQ &S, int gi, int pair, int lane) {
+  const int kh = lane >> 5, tok = lane & 31;
+  v4i B[2];
 #pragma unroll
   for (int h = 0; h < 2; h++) {
     const int t = tok + 32 * h;
-    const v4i B = *(const v4i *)(S.x + t * 128 + ((2 * gi + kh) ^ swz(t)) * 16);
+    B[h] = *(const v4i *)(S.x + t * 128 + ((2 * gi + kh) ^ swz(t)) * 16);
+  }
+  const float x0 = lane < 32 ? S.xs[gi][lane] : 0.0f, x1 = lane < 32 ? S.xs[gi][32 + lane] : 0.0f;
+#pragma unroll
+  for (int sp = 0; sp < 2; sp++) {
+    const int base = 64 * pair + 32 * sp;
+    const int row = base + (lane & 31);
+    v4i A;
+    if (PACK == 8) A = *(const v4i *)(S.w + row * 128 + ((2 * gi + kh) ^ swz(row)) * 16);
+    else A = six_half(S.w + row * 96 + gi * 24, kh);
     v16i cin;
-    if (WC) {
-      cin = wc;
-    } else {  // -64 sum(w) of each row: the weights against 32 bytes of -64 (made again for each half: fewer registers)
+    if (WC) {  // the caller's corrections of the lane's 16 rows
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const int4 c4 = *(const int4 *)&S.wc[gi][base + 4 * kh + 8 * q];
+        cin[4 * q] = c4.x; cin[4 * q + 1] = c4.y; cin[4 * q + 2] = c4.z; cin[4 * q + 3] = c4.w;
+      }
+    } else {  // -64 sum(w) of each row: the weights against 32 bytes of -64
       const v4i m64 = {(int32_t)0xc0c0c0c0, (int32_t)0xc0c0c0c0, (int32_t)0xc0c0c0c0, (int32_t)0xc0c0c0c0};
       cin = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, m64, zero16i(), 0, 0, 0);
     }
-    const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, cin, 0, 0, 0);
-    const float xsv = lane < 32 ? S.xs[gi][32 * h + lane] : 0.0f;
-    const v16f sc = __builtin_amdgcn_mfma_f32_32x32x2f32(wsv, xsv, zero16f(), 0, 0, 0);
-    float *acc = h ? acc1 : acc0;
+    const float wsv = lane < 32 ? S.ws[gi][base + lane] : 0.0f;
 #pragma unroll
-    for (int r = 0; r < 16; r++) acc[r] = fadd(acc[r], fmul((float)c[r], sc[r]));
+    for (int h = 0; h < 2; h++) {
+      const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B[h], cin, 0, 0, 0);
+      const v16f sc = __builtin_amdgcn_mfma_f32_32x32x2f32(wsv, h ? x1 : x0, zero16f(), 0, 0, 0);
+      float *a = acc[2 * sp + h];
+#pragma unroll
+      for (int r = 0; r < 16; r++) a[r] = fadd(a[r], fmul((float)c[r], sc[r]));
+    }
   }
 }
 
 // stage s in `cur`, the loads of stage s + AHEAD into `next` (the buffer of stage s - 1)
 template <int PACK, bool WC>
 HQ_DEV void q_step(Relaxed<PACK, WC> &L, const StageQ &cur, StageQ &next, int s, int stages, int total,
-                   float acc0[16], float acc1[16], int slice, int chain, int lane) {
+                   float acc[4][16], int pair, int chain, int lane) {
   if (s >= stages) return;
-  wait_for(s, total);
+  wait_for<QLOADS>(s, total);
   if (s + AHEAD < total) L.load(next, s + AHEAD);
-  q_group<PACK, WC>(acc0, acc1, cur, chain, slice, lane);  // group 4 s + chain (relaxed/int8.ts:26-39)
+  q_group<PACK, WC>(acc, cur, chain, pair, lane);  // group 4 s + chain
+}
+
+// the 4 chains of a pair of slices added in LDS, ((a0 + a1) + a2) + a3, for its four sub-tiles: wave k adds its sums
+// to what waves 0..k-1 left (the values of a lane are the same (row, token)s in the four waves of a pair); the sums
+// end in chain 3's waves.  p0 (sub-tiles 0, 1) and p1 (2, 3): 2 x 64 x 32 floats each that nothing else uses
+HQ_DEV void add_chains4(float acc[4][16], float *p0, float *p1, int pair, int chain, int lane) {
+  float *q[2] = {p0 + (pair * 64 + lane) * 32, p1 + (pair * 64 + lane) * 32};
+  for (int k = 0; k < 4; k++) {
+    __syncthreads();
+    if (chain == k) {
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          float *m = q[i >> 1] + 16 * (i & 1) + r;
+          if (k > 0) acc[i][r] = fadd(*m, acc[i][r]);
+          if (k < 3) *m = acc[i][r];
+        }
+    }
+  }
 }
 
 template <int PACK, bool WC>
-__global__ __launch_bounds__(NT) void gemm_relaxed(Job J) {
+__global__ __launch_bounds__(QNT) void gemm_relaxed(Job J) {
   __shared__ StageQ b0, b1, b2, b3;
   __shared__ __attribute__((aligned(16))) char junk[1024];
   const int M = J.count;
@@ -302,11 +339,13 @@ __global__ __launch_bounds__(NT) void gemm_relaxed(Job J) {
   const int row0 = J.r0 + rb * BR, tok0 = tb * BT;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int slice = wave >> 2, chain = wave & 3;
+  const int pair = wave >> 2, chain = wave & 3;
 
-  float acc0[16], acc1[16];
+  float acc[4][16];
 #pragma unroll
-  for (int r = 0; r < 16; r++) acc0[r] = acc1[r] = 0.0f;
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[i][r] = 0.0f;
 
   Relaxed<PACK, WC> L(J, row0, tok0, M, wave, junk);
   const int stages = ng4 / QG;
@@ -315,32 +354,30 @@ __global__ __launch_bounds__(NT) void gemm_relaxed(Job J) {
   if (total > 1) L.load(b1, 1);
   if (total > 2) L.load(b2, 2);
   for (int s = 0; s < stages; s += RING) {
-    q_step<PACK, WC>(L, b0, b3, s, stages, total, acc0, acc1, slice, chain, lane);
-    q_step<PACK, WC>(L, b1, b0, s + 1, stages, total, acc0, acc1, slice, chain, lane);
-    q_step<PACK, WC>(L, b2, b1, s + 2, stages, total, acc0, acc1, slice, chain, lane);
-    q_step<PACK, WC>(L, b3, b2, s + 3, stages, total, acc0, acc1, slice, chain, lane);
+    q_step<PACK, WC>(L, b0, b3, s, stages, total, acc, pair, chain, lane);
+    q_step<PACK, WC>(L, b1, b0, s + 1, stages, total, acc, pair, chain, lane);
+    q_step<PACK, WC>(L, b2, b1, s + 2, stages, total, acc, pair, chain, lane);
+    q_step<PACK, WC>(L, b3, b2, s + 3, stages, total, acc, pair, chain, lane);
   }
   stage_ready<0>();  // every load has landed (the tail's too) and every wave is done with the stages
   auto ring = [&](int i) -> StageQ & { return i == 0 ? b0 : i == 1 ? b1 : i == 2 ? b2 : b3; };
-  add_chains(acc0, acc1, (float *)&ring((stages + 1) % RING), (float *)&ring((stages + 2) % RING), slice, chain,
-             lane);
+  add_chains4(acc, (float *)&ring((stages + 1) % RING), (float *)&ring((stages + 2) % RING), pair, chain, lane);
   if (chain == 3) {
     // the groups past the fours, one at a time, after the four chains' sum (relaxed/int8.ts:40-47)
     const StageQ &T = ring(stages % RING);
-    for (int gi = 0; gi < ng - ng4; gi++) q_group<PACK, WC>(acc0, acc1, T, gi, slice, lane);
-    const int rbase = row0 + 32 * slice + 4 * (lane >> 5);
+    for (int gi = 0; gi < ng - ng4; gi++) q_group<PACK, WC>(acc, T, gi, pair, lane);
 #pragma unroll
-    for (int h = 0; h < 2; h++) {
-      const int t = tok0 + 32 * h + (lane & 31);
+    for (int i = 0; i < 4; i++) {
+      const int t = tok0 + 32 * (i & 1) + (lane & 31);
       if (t < M) {
         float *out = (float *)(J.out + t * J.os);
-        const float *acc = h ? acc1 : acc0;
+        const int rbase = row0 + 64 * pair + 32 * (i >> 1) + 4 * (lane >> 5);
 #pragma unroll
         for (int q = 0; q < 4; q++)
 #pragma unroll
           for (int e = 0; e < 4; e++) {
             const int row = rbase + 8 * q + e;
-            if (row < J.r1) out[row] = acc[4 * q + e];
+            if (row < J.r1) out[row] = acc[i][4 * q + e];
           }
       }
     }
@@ -354,7 +391,9 @@ __global__ __launch_bounds__(NT) void gemm_relaxed(Job J) {
 // of it) as 32 K values in the order plane-major: K half kh of a lane is planes 2 kh, 2 kh + 1, eight c's each, for
 // the codes and for interleave()'s activation bytes 64 h + 16 p + 8 (k % 2) .. + 7 alike.
 // ---------------------------------------------------------------------------------------------------------------
-constexpr int TG = 2;  // groups of 128 a stage
+constexpr int TG = 2;       // groups of 128 a stage
+constexpr int NT = 1024;    // threads a block: 16 waves, 4 slices of 32 rows x 4 parts
+constexpr int TLOADS = 3;   // loads a wave a stage
 
 struct alignas(16) StageT {
   char w[BR * 64];           // 128 rows x 2 groups x 32 code bytes; 16-byte chunk j of row r at j ^ tswz(r)
@@ -468,7 +507,7 @@ HQ_DEV void t_group(float acc0[16], float acc1[16], const StageT &S, int gi, int
 HQ_DEV void t_step(Ternary &L, const StageT &cur, StageT &next, int s, int stages, int groups, float acc0[16],
                    float acc1[16], int slice, int part, int lane) {
   if (s >= stages) return;
-  wait_for(s, stages);
+  wait_for<TLOADS>(s, stages);
   if (s + AHEAD < stages) L.load(next, s + AHEAD);
   // part `part` of groups 2 s and 2 s + 1 (relaxed/signs.ts:198-207)
   t_group(acc0, acc1, cur, 0, part, slice, lane);
@@ -530,7 +569,7 @@ bool gemm_supported(Kind kind) { return kind == Q8R || kind == Q6R || kind == T2
 hipError_t launch_gemm(Kind kind, const Job &job, hipStream_t s) {
   const int rows = job.r1 - job.r0;
   if (rows <= 0 || job.count <= 0) return hipSuccess;
-  dim3 grid(((rows + BR - 1) / BR) * ((job.count + BT - 1) / BT)), block(NT);
+  dim3 grid(((rows + BR - 1) / BR) * ((job.count + BT - 1) / BT)), block(kind == T2R || kind == T2 ? NT : QNT);
   const bool wc = job.wc != nullptr;
   switch (kind) {
   case Q8R:
