@@ -4,9 +4,10 @@
 //   matmul_q8 / matmul_q6     (kernels/kernel/matmul.ts:77-104, 227-244)
 //   matmul_t2r / matmul_t2    (kernels/relaxed/signs.ts:203-230, kernel/matmul.ts:196-220; the same numbers)
 //
-// Layout (all kinds): a block is 4 waves, a wave 4 rows, a row 16 lanes.  Lane l of a row takes the groups
-// 16 i + l (i = 0, 1, ...): a group's bytes (32 int8, 24 int6 or 32 ternary) are one lane's, so its integer sum is
-// exact in that lane (v_dot4_i32_i8) and the row's 16 lanes read 512 (384) contiguous bytes a step.
+// Layout: a row is 16 lanes (ternary: 8, 16 or 32 by the row's length), a wave 4 rows; a block is 2 waves (8 rows)
+// for the relaxed kinds, 4 waves for the others.  Lane l of a row of L lanes takes the groups L i + l (i = 0, 1,
+// ...): a group's bytes (32 int8, 24 int6 or 32 ternary) are one lane's, so its integer sum is exact in that lane
+// (v_dot4_i32_i8) and the row's 16 lanes read 512 (384) contiguous bytes a step.
 //
 // The float32 order is the reference's, so every output is its number to the bit:
 //   relaxed int8 / int6: lane k (k = 0..3) of the reference's accumulator adds the groups 4 j + k in order.  Those
