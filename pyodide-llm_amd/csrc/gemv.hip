@@ -145,18 +145,41 @@ struct ActSource {
 
 template <int PACK, int T, bool WC, int SRC>
 struct RelaxedChunk {
-  static constexpr bool ACTS = SRC == GLOBAL;  // activations prefetched with the weights (else read from LDS)
 #ifndef HQ_GEMV_U
 #define HQ_GEMV_U 4
 #endif
-  static constexpr int U = ACTS ? (T == 1 ? HQ_GEMV_U : (T == 2 ? 2 : 1)) : (T == 1 ? 2 * HQ_GEMV_U : (T == 2 ? 4 : 2));
+  static constexpr int U = T == 1 ? HQ_GEMV_U : (T == 2 ? 2 : 1);
   uint32_t w[U][8];
-  uint32_t x[ACTS ? U : 1][ACTS ? T : 1][8];
-  float ws[U], xs[ACTS ? U : 1][ACTS ? T : 1];
+  uint32_t x[U][T][8];
+  float ws[U], xs[U][T];
   int32_t wc[U];
 
   // steps it0 .. it0 + U - 1 of this lane (its group 16 it + lane of each; a lane past the row's fours reads group
-  // 0 again, whose term it drops)
+  // 0 again, whose term it drops): the weights, their scales and corrections
+  HQ_DEV void load_w(const char *wrow, const float *srow, const int32_t *crow, int it0, int lane, int ng4) {
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int g = (it0 + u) * 16 + lane;
+      const int gl = g < ng4 ? g : 0;
+      load_group<PACK>(wrow, gl, w[u]);
+      ws[u] = srow[gl];
+      if (WC) wc[u] = crow[gl];
+    }
+  }
+  // ... and the activations of the same groups (from global memory or the block's LDS)
+  HQ_DEV void load_x(const ActSource<T, SRC> &A, int it0, int lane, int ng4) {
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int g = (it0 + u) * 16 + lane;
+      const int gl = g < ng4 ? g : 0;
+#pragma unroll
+      for (int t = 0; t < T; t++) {
+        A.get(t, gl, x[u][t]);
+        xs[u][t] = A.scale(t, gl);
+      }
+    }
+  }
+  // both, a group at a time
   HQ_DEV void load(const char *wrow, const float *srow, const int32_t *crow, const ActSource<T, SRC> &A, int it0,
                    int lane, int ng4) {
 #pragma unroll
@@ -166,24 +189,21 @@ struct RelaxedChunk {
       load_group<PACK>(wrow, gl, w[u]);
       ws[u] = srow[gl];
       if (WC) wc[u] = crow[gl];
-      if (ACTS) {
 #pragma unroll
-        for (int t = 0; t < T; t++) {
-          A.get(t, gl, x[u][t]);
-          xs[u][t] = A.scale(t, gl);
-        }
+      for (int t = 0; t < T; t++) {
+        A.get(t, gl, x[u][t]);
+        xs[u][t] = A.scale(t, gl);
       }
     }
   }
 
   // the chunk's terms, folded into the lanes' sums: lane k takes groups 16 it + k, + 4, + 8, + 12 in order
   // (relaxed/int8.ts:26-39)
-  HQ_DEV void fold(float acc[T], const ActSource<T, SRC> &A, int it0, int lane, int ng4) const {
+  HQ_DEV void fold(float acc[T], int it0, int lane, int ng4) const {
 #pragma unroll
     for (int u = 0; u < U; u++) {
       const int g = (it0 + u) * 16 + lane;
       const bool valid = g < ng4;
-      const int gl = valid ? g : 0;
       int32_t wsum = 0;
       if (!WC) {
 #pragma unroll
@@ -191,20 +211,10 @@ struct RelaxedChunk {
       }
 #pragma unroll
       for (int t = 0; t < T; t++) {
-        uint32_t xl[8];
-        float sx;
-        if (ACTS) {
-#pragma unroll
-          for (int i = 0; i < 8; i++) xl[i] = x[u][t][i];
-          sx = xs[u][t];
-        } else {
-          A.get(t, gl, xl);
-          sx = A.scale(t, gl);
-        }
         int32_t d = WC ? wc[u] : -64 * wsum;
 #pragma unroll
-        for (int i = 0; i < 8; i++) d = sdot4((int32_t)w[u][i], (int32_t)xl[i], d);
-        const float p = fmul((float)d, fmul(ws[u], sx));
+        for (int i = 0; i < 8; i++) d = sdot4((int32_t)w[u][i], (int32_t)x[u][t][i], d);
+        const float p = fmul((float)d, fmul(ws[u], xs[u][t]));
         const float q = valid ? p : 0.0f;  // +0 leaves a lane as it is: a lane is never -0
         float a = fadd(acc[t], q);
         a = fadd(a, from_lane_plus<4>(q));
@@ -215,13 +225,14 @@ struct RelaxedChunk {
   }
 };
 
+// the kRelaxedRows rows of tile `tile` (the batch's jobs' row ranges cut into tiles in order).  fill: first make the
+// block's LDS copy of the activations (STAGED, FUSED), while the first weights are in flight
 template <int PACK, int T, bool WC, int SRC>
-__global__ __launch_bounds__(16 * kRelaxedRows) void gemv_relaxed(GemvBatch batch) {
-  extern __shared__ __align__(16) char lds[];
-  const int jb = job_of(batch, blockIdx.x);
+HQ_DEV void relaxed_tile(const GemvBatch &batch, int tile, char *lds, bool fill) {
+  const int jb = job_of(batch, tile);
   const Job &J = batch.job[jb];
   const int lane = threadIdx.x & 15;
-  const int row_u = J.r0 + (blockIdx.x - batch.block0[jb]) * kRelaxedRows + (threadIdx.x >> 4);
+  const int row_u = J.r0 + (tile - batch.block0[jb]) * kRelaxedRows + (threadIdx.x >> 4);
   const bool live = row_u < J.r1;
   const int row = live ? row_u : J.r1 - 1;
   const int ng = J.n >> 5, ng4 = ng & ~3;
@@ -247,14 +258,19 @@ __global__ __launch_bounds__(16 * kRelaxedRows) void gemv_relaxed(GemvBatch batc
   constexpr int U = Chunk::U;
   const int steps = (ng4 + 15) >> 4;
   Chunk a, b;
-  if (steps > 0) a.load(wrow, srow, crow, A, 0, lane, ng4);  // the first weights in flight during the staging
-  if (SRC != GLOBAL) fill_acts<T, SRC>(batch, J, lds, (float *)(lds + T * J.n));
+  if (fill) {
+    if (steps > 0) a.load_w(wrow, srow, crow, 0, lane, ng4);  // the first weights in flight during the staging
+    fill_acts<T, SRC>(batch, J, lds, (float *)(lds + T * J.n));
+    if (steps > 0) a.load_x(A, 0, lane, ng4);
+  } else if (steps > 0) {
+    a.load(wrow, srow, crow, A, 0, lane, ng4);
+  }
   for (int it = 0; it < steps; it += 2 * U) {
     if (it + U < steps) b.load(wrow, srow, crow, A, it + U, lane, ng4);
-    a.fold(acc, A, it, lane, ng4);
+    a.fold(acc, it, lane, ng4);
     if (it + U < steps) {
       if (it + 2 * U < steps) a.load(wrow, srow, crow, A, it + 2 * U, lane, ng4);
-      b.fold(acc, A, it + U, lane, ng4);
+      b.fold(acc, it + U, lane, ng4);
     }
   }
   // lane 0: ((l0 + l1) + l2) + l3 (math.ts:7-9), then the groups past the fours one at a time (int8.ts:40-47)
@@ -289,6 +305,21 @@ __global__ __launch_bounds__(16 * kRelaxedRows) void gemv_relaxed(GemvBatch batc
   if (live && lane == 0) {
 #pragma unroll
     for (int t = 0; t < T; t++) ((float *)(J.out + t * J.os))[row] = sum[t];
+  }
+}
+
+// GLOBAL / STAGED: a tile a block.  FUSED: the block quantizes the activations once (they are every job's) and then
+// takes tiles blockIdx.x, + gridDim.x, ... (the grid is a few blocks a CU): one quantize_x a block, not a tile
+template <int PACK, int T, bool WC, int SRC>
+__global__ __launch_bounds__(16 * kRelaxedRows) void gemv_relaxed(GemvBatch batch) {
+  extern __shared__ __align__(16) char lds[];
+  if (SRC == FUSED) {
+    const int tiles = batch.block0[batch.njobs];
+    relaxed_tile<PACK, T, WC, SRC>(batch, blockIdx.x, lds, true);
+    for (int tile = blockIdx.x + gridDim.x; tile < tiles; tile += gridDim.x)
+      relaxed_tile<PACK, T, WC, SRC>(batch, tile, lds, false);
+  } else {
+    relaxed_tile<PACK, T, WC, SRC>(batch, blockIdx.x, lds, SRC == STAGED);
   }
 }
 
@@ -611,9 +642,26 @@ HQ_HOST_DEV constexpr int ternary_lanes(int n) {
 }
 HQ_HOST_DEV constexpr size_t ternary_stage_bytes(int T, int n) { return (size_t)T * ternary_token_bytes(n); }
 
+// FUSED: blocks a CU (each quantizes the activations once and takes tiles in turn)
+#ifndef HQ_FUSED_BLOCKS_PER_CU
+#define HQ_FUSED_BLOCKS_PER_CU 6
+#endif
+int cu_count() {
+  static int cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int cus = 0;
+    cache[dev] = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0
+                     ? cus : 256;
+  }
+  return cache[dev];
+}
+
 template <int PACK, int T, int SRC>
-hipError_t launch_relaxed(const GemvBatch &b, int blocks, bool wc, size_t lds, hipStream_t s) {
-  dim3 grid(blocks), block(16 * kRelaxedRows);
+hipError_t launch_relaxed(const GemvBatch &b, int tiles, bool wc, size_t lds, hipStream_t s) {
+  const int cap = HQ_FUSED_BLOCKS_PER_CU * cu_count();
+  dim3 grid(SRC == FUSED && tiles > cap ? cap : tiles), block(16 * kRelaxedRows);
   if (wc) hipLaunchKernelGGL((gemv_relaxed<PACK, T, true, SRC>), grid, block, lds, s, b);
   else hipLaunchKernelGGL((gemv_relaxed<PACK, T, false, SRC>), grid, block, lds, s, b);
   return hipGetLastError();

@@ -517,6 +517,44 @@ def test_matmuls_relaxed(pkg, arena, oracle, tokens, n):
         assert same_bits(got, want), f"{what}: {first_difference(got, want)}"
 
 
+@pytest.mark.parametrize("tokens", [1, 3])
+def test_matmuls_relaxed_many_tiles(pkg, arena, oracle, tokens):
+    """more 8-row tiles than the fused launch has blocks (a few a CU): every block quantizes once and then takes
+    several tiles, across the boundary of two jobs, with the groups past the fours (n = 320: 10 groups)"""
+    from pyodide_llm_amd import jobs
+    rng = np.random.default_rng(900 + tokens)
+    n = 320
+    ng = n // 32
+    x = rng.standard_normal((tokens, n)).astype(F)
+    ax = arena.put(x)
+    table, wants = [], []
+    for name, rows, derived in (("matmul_q8r", 30011, False), ("matmul_q8r", 9000, False),
+                                ("matmul_q8r", 25003, True), ("matmul_q6r", 14000, False)):
+        six = name == "matmul_q6r"
+        if six:
+            v = (4 * rng.integers(-32, 32, rows * n)).astype(np.int8)
+            wbytes, wc = pack6(v), oracle.six_sums(pack6(v))
+        else:
+            wbytes = rng.integers(-128, 128, rows * n).astype(np.int8)
+            wc = oracle.int8_sums(wbytes)
+        ws = (np.abs(rng.standard_normal(rows * ng)) * 0.02 / 127).astype(F)
+        os_ = 4 * rows
+        out = arena.alloc(os_ * tokens, fill=np.full(rows * tokens, -7, F))
+        scratch = arena.alloc(tokens * 2 * n)
+        table.append(jobs.job(name, out, scratch, scratch + n, arena.put(wbytes), arena.put(ws),
+                              0 if derived else arena.put(wc), n, rows=rows, count=tokens, os=os_, as_=2 * n,
+                              bs=2 * n))
+        for t in range(tokens):
+            q, sc = oracle.quantize_x(x[t], 64)
+            full = (oracle.matmul_q6r if six else oracle.matmul_q8r)(q, sc, wbytes, ws, wc, n)
+            wants.append((out + t * os_, full, f"{name} {rows} rows token {t}"))
+    L = pkg.library()
+    assert jobs.matmuls(L, ax, 4 * n, table) == 0, L.hq_last_error_message()
+    for addr, want, what in wants:
+        got = arena.get(addr, F, want.size)
+        assert same_bits(got, want), f"{what}: {first_difference(got, want)}"
+
+
 @pytest.mark.parametrize("tokens", [1, 3, 5])
 def test_matmuls_plain_and_ternary(pkg, arena, oracle, tokens):
     from pyodide_llm_amd import jobs
