@@ -18,11 +18,11 @@
 // in that order.  Each term is f(f(C) * f(ws * xs)) (int8, int6) or f(f(f(C) * xs) * d) (ternary), rounded as the
 // reference rounds it (-ffp-contract=off).
 //
-// The scales' product of int8 / int6, f(ws * xs) for every (row, token), is an outer product: a
-// v_mfma_f32_32x32x2_f32 with K = 2 and its second column zero gives it, each product rounded once as v_mul_f32
-// rounds it (subnormals included), on the matrix core.  Roofline: per output element and group the epilogue is then
-// 3 VALU operations (convert, multiply, add; ternary 4: f(f(C * xs) * d) has no such product) against 32 MACs on the
-// matrix core; CDNA4's VALU does 64 lanes a clock a CU against 4096 int8 MACs, so the epilogue, not the MFMA, bounds
+// The scales' product of int8 / int6, f(ws * xs) for every (row, token), is an outer product: four
+// v_mfma_f32_4x4x1_16b_f32 (sixteen 4 x 4 outer products each, K = 1) give a 32 x 32 sub-tile's, each product rounded
+// once as v_mul_f32 rounds it (subnormals included), on the matrix core.  Roofline: per output element and group the
+// epilogue is then 3 VALU operations (convert, multiply, add; ternary 4: f(f(C * xs) * d) has no such product)
+// against 32 MACs on the matrix core; CDNA4's VALU does 64 lanes a clock a CU against 4096 int8 MACs, so the epilogue, not the MFMA, bounds
 // this kernel (at best 32 / (3 x 4096 / 64) = 16.7 % of dense int8 peak, 12.5 % for ternary).
 //
 // A block computes a 128-row x 64-token tile.  int8 / int6: 8 waves, two a SIMD; the waves of pair p (waves 4 p ..
@@ -49,6 +49,7 @@ namespace {
 typedef int32_t v4i __attribute__((ext_vector_type(4)));
 typedef int32_t v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 constexpr int BR = 128, BT = 64;  // block tile: rows x tokens
 constexpr int RING = 4;           // stage buffers
@@ -60,12 +61,7 @@ HQ_DEV v16i zero16i() {
   for (int r = 0; r < 16; r++) z[r] = 0;
   return z;
 }
-HQ_DEV v16f zero16f() {
-  v16f z;
-#pragma unroll
-  for (int r = 0; r < 16; r++) z[r] = 0.0f;
-  return z;
-}
+HQ_DEV v4f zero4f() { return (v4f){0.0f, 0.0f, 0.0f, 0.0f}; }
 
 // ---- loads -----------------------------------------------------------------------------------------------------
 // A block's rows, tokens and scales are each one buffer resource (base and size in scalar registers): a thread's
@@ -173,7 +169,7 @@ constexpr int QLOADS = 6;   // loads a wave a stage
 struct alignas(16) StageQ {
   char w[BR * 128];    // int8: 128 rows x 4 groups x 32 bytes, chunks swizzled; int6: 128 rows x 4 x 24 bytes
   char x[BT * 128];    // 64 tokens x 4 groups x 32 bytes, chunks swizzled
-  float ws[QG][BR];    // the rows' scales, group-major
+  float ws[QG][BR];    // the rows' scales, group-major; in each 32-row slice row 8 m + 4 h + i at 16 h + 4 i + m
   int32_t wc[QG][BR];  // the rows' corrections (with the caller's wc), group-major
   float xs[QG][BT];    // the tokens' scales, group-major
 };
@@ -201,7 +197,7 @@ template <int PACK, bool WC>
 struct Relaxed {
   static constexpr int GB = PACK == 8 ? 32 : 24;  // bytes of a group of weights
   __amdgpu_buffer_rsrc_t rw, rx, rws, rwc, rxs;
-  uint32_t oa[2], ob, oc, oe;
+  uint32_t oa[2], ob, oc, ow, oe;
   int wave;
   char *junk;
 
@@ -232,8 +228,15 @@ struct Relaxed {
       const int tok = 8 * w + (lane >> 3), ch = (lane & 7) ^ swz(tok);
       ob = (uint32_t)(tok * J.frame + (ch >> 1) * 32 + (ch & 1) * 16);
     }
-    // loads c, d: the rows' scales and corrections of group w / 2, rows 64 (w % 2) + l
+    // loads c, d: the rows' scales and corrections of group w / 2, rows 64 (w % 2) + l; the scales with the rows of
+    // each 32-row slice reordered (entry 16 h + 4 i + m is row 8 m + 4 h + i), so that one 16-byte read gives a lane
+    // the four rows of its 4 x 4 outer products
     oc = (uint32_t)(((64 * (w & 1) + lane) * ng + (w >> 1)) * 4);
+    {
+      const int q = lane & 31;
+      const int row = 64 * (w & 1) + 32 * (lane >> 5) + 8 * (q & 3) + 4 * (q >> 4) + ((q >> 2) & 3);
+      ow = (uint32_t)((row * ng + (w >> 1)) * 4);
+    }
     // load e: waves 0..3 the tokens' scales of group w, token l
     oe = (uint32_t)(lane * J.sframe + (w & 3) * 4);
   }
@@ -247,7 +250,7 @@ struct Relaxed {
       else dma16(rxs, junk, 0, 0);
     }
     dma16(rx, S.x + w * 1024, ob, s * QG * 32);
-    dma4(rws, &S.ws[w >> 1][64 * (w & 1)], oc, s * QG * 4);
+    dma4(rws, &S.ws[w >> 1][64 * (w & 1)], ow, s * QG * 4);
     if (WC) dma4(rwc, &S.wc[w >> 1][64 * (w & 1)], oc, s * QG * 4);
     else dma4(rxs, junk, 0, 0);
     if (w < 4) dma4(rxs, &S.xs[w][0], oe, s * QG * 4);
@@ -267,7 +270,7 @@ HQ_DEV void q_group(float acc[4][16], const StageQ &S, int gi, int pair, int lan
     const int t = tok + 32 * h;
     B[h] = *(const v4i *)(S.x + t * 128 + ((2 * gi + kh) ^ swz(t)) * 16);
   }
-  const float x0 = lane < 32 ? S.xs[gi][lane] : 0.0f, x1 = lane < 32 ? S.xs[gi][32 + lane] : 0.0f;
+  const float xv[2] = {S.xs[gi][tok], S.xs[gi][32 + tok]};
 #pragma unroll
   for (int sp = 0; sp < 2; sp++) {
     const int base = 64 * pair + 32 * sp;
@@ -286,11 +289,21 @@ HQ_DEV void q_group(float acc[4][16], const StageQ &S, int gi, int pair, int lan
       const v4i m64 = {(int32_t)0xc0c0c0c0, (int32_t)0xc0c0c0c0, (int32_t)0xc0c0c0c0, (int32_t)0xc0c0c0c0};
       cin = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, m64, zero16i(), 0, 0, 0);
     }
-    const float wsv = lane < 32 ? S.ws[gi][base + lane] : 0.0f;
+    // the scales of rows 8 m + 4 kh + lane % 4 (m = 0..3) of the slice
+    const float4 wv = *(const float4 *)&S.ws[gi][base + 16 * kh + 4 * (lane & 3)];
+    const float w4[4] = {wv.x, wv.y, wv.z, wv.w};
 #pragma unroll
     for (int h = 0; h < 2; h++) {
       const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B[h], cin, 0, 0, 0);
-      const v16f sc = __builtin_amdgcn_mfma_f32_32x32x2f32(wsv, h ? x1 : x0, zero16f(), 0, 0, 0);
+      // f(ws * xs) of the sub-tile: v_mfma_f32_4x4x1_16b_f32 gives lane l, register i the product of lane
+      // 4 (l / 4) + i's A and lane l's B, so A = the scale of row 8 m + 4 kh + lane % 4 and B = the token's scale
+      // give registers 4 m .. 4 m + 3 the rows 8 m + 4 kh + i of the i8 MFMA's layout, one product each
+      v16f sc;
+#pragma unroll
+      for (int m = 0; m < 4; m++) {
+        const v4f d = __builtin_amdgcn_mfma_f32_4x4x1f32(w4[m], xv[h], zero4f(), 0, 0, 0);
+        sc[4 * m] = d[0]; sc[4 * m + 1] = d[1]; sc[4 * m + 2] = d[2]; sc[4 * m + 3] = d[3];
+      }
       float *a = acc[2 * sp + h];
 #pragma unroll
       for (int r = 0; r < 16; r++) a[r] = fadd(a[r], fmul((float)c[r], sc[r]));
