@@ -171,9 +171,9 @@ constexpr int QLOADS = 6;   // loads a wave a stage
 struct alignas(16) StageQ {
   char w[BR * 128];    // int8: 128 rows x 4 groups x 32 bytes, chunks swizzled; int6: 128 rows x 4 x 24 bytes
   char x[BT * 128];    // 64 tokens x 4 groups x 32 bytes, chunks swizzled
-  float ws[QG][BR];    // the rows' scales, group-major; in each 32-row slice row 8 m + 4 h + i at 16 h + 4 i + m
+  float ws[QG][BR];    // the rows' scales, group-major
   int32_t wc[QG][BR];  // the rows' corrections (with the caller's wc), group-major
-  float xs[QG][BT];    // the tokens' scales, group-major
+  float xs[QG][BT];    // the tokens' scales, group-major; in each 32-token half token 8 m + 4 h + i at 16 h + 4 i + m
 };
 
 // K half kh (values 16 kh .. + 15) of an int6 group (24 bytes at p, kernels/six.ts:16-31): value j's low nibble is
@@ -199,7 +199,7 @@ template <int PACK, bool WC>
 struct Relaxed {
   static constexpr int GB = PACK == 8 ? 32 : 24;  // bytes of a group of weights
   __amdgpu_buffer_rsrc_t rw, rx, rws, rwc, rxs;
-  uint32_t oa[2], ob, oc, ow, oe;
+  uint32_t oa[2], ob, oc, oe;
   int wave;
   char *junk;
 
@@ -230,17 +230,15 @@ struct Relaxed {
       const int tok = 8 * w + (lane >> 3), ch = (lane & 7) ^ swz(tok);
       ob = (uint32_t)(tok * J.frame + (ch >> 1) * 32 + (ch & 1) * 16);
     }
-    // loads c, d: the rows' scales and corrections of group w / 2, rows 64 (w % 2) + l; the scales with the rows of
-    // each 32-row slice reordered (entry 16 h + 4 i + m is row 8 m + 4 h + i), so that one 16-byte read gives a lane
-    // the four rows of its 4 x 4 outer products
+    // loads c, d: the rows' scales and corrections of group w / 2, rows 64 (w % 2) + l
     oc = (uint32_t)(((64 * (w & 1) + lane) * ng + (w >> 1)) * 4);
+    // load e: waves 0..3 the tokens' scales of group w, the tokens of each 32-token half reordered (entry 16 h + 4 i
+    // + m is token 8 m + 4 h + i), so that one 16-byte read gives a lane the four tokens of its 4 x 4 outer products
     {
       const int q = lane & 31;
-      const int row = 64 * (w & 1) + 32 * (lane >> 5) + 8 * (q & 3) + 4 * (q >> 4) + ((q >> 2) & 3);
-      ow = (uint32_t)((row * ng + (w >> 1)) * 4);
+      const int tok = 32 * (lane >> 5) + 8 * (q & 3) + 4 * (q >> 4) + ((q >> 2) & 3);
+      oe = (uint32_t)(tok * J.sframe + (w & 3) * 4);
     }
-    // load e: waves 0..3 the tokens' scales of group w, token l
-    oe = (uint32_t)(lane * J.sframe + (w & 3) * 4);
   }
 
   // the 6 loads of stage s (groups 4 s .. 4 s + 3) into S
@@ -252,7 +250,7 @@ struct Relaxed {
       else dma16(rxs, junk, 0, 0);
     }
     dma16(rx, S.x + w * 1024, ob, s * QG * 32);
-    dma4(rws, &S.ws[w >> 1][64 * (w & 1)], ow, s * QG * 4);
+    dma4(rws, &S.ws[w >> 1][64 * (w & 1)], oc, s * QG * 4);
     if (WC) dma4(rwc, &S.wc[w >> 1][64 * (w & 1)], oc, s * QG * 4);
     else dma4(rxs, junk, 0, 0);
     if (w < 4) dma4(rxs, &S.xs[w][0], oe, s * QG * 4);
@@ -261,49 +259,49 @@ struct Relaxed {
 };
 
 // group gi of stage S into the chain of the lane's four sub-tiles (slices 2 pair, 2 pair + 1 x both token halves,
-// acc[2 slice + half]): the exact integers (MFMA, from the corrections) and the scales' products (the outer-product
-// MFMA), each term f(f(C) * f(ws * xs)) (relaxed/int8.ts:26-39)
+// acc[2 slice + half]): the exact integers (MFMA, from the corrections) and the scales' products (outer-product
+// MFMAs), each term f(f(C) * f(ws * xs)) (relaxed/int8.ts:26-39).  MFMA A = activations (m = token), B = weights
+// (n = row): lane l holds row l % 32 of its slice and tokens 8 (r / 4) + 4 (l / 32) + r % 4 of its half, so a lane's
+// correction and row scale are one value each.
 template <int PACK, bool WC>
 HQ_DEV void q_group(float acc[4][16], const StageQ &S, int gi, int pair, int lane) {
-  const int kh = lane >> 5, tok = lane & 31;
-  v4i B[2];
+  const int kh = lane >> 5, l32 = lane & 31;
+  v4i X[2];
+  float xv[2][4];
 #pragma unroll
   for (int h = 0; h < 2; h++) {
-    const int t = tok + 32 * h;
-    B[h] = *(const v4i *)(S.x + t * 128 + ((2 * gi + kh) ^ swz(t)) * 16);
+    const int t = l32 + 32 * h;
+    X[h] = *(const v4i *)(S.x + t * 128 + ((2 * gi + kh) ^ swz(t)) * 16);
+    // the scales of tokens 8 m + 4 kh + lane % 4 (m = 0..3) of the half
+    const float4 v = *(const float4 *)&S.xs[gi][32 * h + 16 * kh + 4 * (lane & 3)];
+    xv[h][0] = v.x; xv[h][1] = v.y; xv[h][2] = v.z; xv[h][3] = v.w;
   }
-  const float xv[2] = {S.xs[gi][tok], S.xs[gi][32 + tok]};
 #pragma unroll
   for (int sp = 0; sp < 2; sp++) {
-    const int base = 64 * pair + 32 * sp;
-    const int row = base + (lane & 31);
-    v4i A;
-    if (PACK == 8) A = *(const v4i *)(S.w + row * 128 + ((2 * gi + kh) ^ swz(row)) * 16);
-    else A = six_half(S.w + row * 96 + gi * 24, kh);
+    const int row = 64 * pair + 32 * sp + l32;
+    v4i W;
+    if (PACK == 8) W = *(const v4i *)(S.w + row * 128 + ((2 * gi + kh) ^ swz(row)) * 16);
+    else W = six_half(S.w + row * 96 + gi * 24, kh);
     v16i cin;
-    if (WC) {  // the caller's corrections of the lane's 16 rows
+    if (WC) {  // the caller's correction of the lane's row
+      const int32_t c = S.wc[gi][row];
 #pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const int4 c4 = *(const int4 *)&S.wc[gi][base + 4 * kh + 8 * q];
-        cin[4 * q] = c4.x; cin[4 * q + 1] = c4.y; cin[4 * q + 2] = c4.z; cin[4 * q + 3] = c4.w;
-      }
-    } else {  // -64 sum(w) of each row: the weights against 32 bytes of -64
+      for (int r = 0; r < 16; r++) cin[r] = c;
+    } else {  // -64 sum(w) of the row: 32 bytes of -64 against the weights
       const v4i m64 = {(int32_t)0xc0c0c0c0, (int32_t)0xc0c0c0c0, (int32_t)0xc0c0c0c0, (int32_t)0xc0c0c0c0};
-      cin = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, m64, zero16i(), 0, 0, 0);
+      cin = __builtin_amdgcn_mfma_i32_32x32x32_i8(m64, W, zero16i(), 0, 0, 0);
     }
-    // the scales of rows 8 m + 4 kh + lane % 4 (m = 0..3) of the slice
-    const float4 wv = *(const float4 *)&S.ws[gi][base + 16 * kh + 4 * (lane & 3)];
-    const float w4[4] = {wv.x, wv.y, wv.z, wv.w};
+    const float wsv = S.ws[gi][row];
 #pragma unroll
     for (int h = 0; h < 2; h++) {
-      const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B[h], cin, 0, 0, 0);
-      // f(ws * xs) of the sub-tile: v_mfma_f32_4x4x1_16b_f32 gives lane l, register i the product of lane
-      // 4 (l / 4) + i's A and lane l's B, so A = the scale of row 8 m + 4 kh + lane % 4 and B = the token's scale
-      // give registers 4 m .. 4 m + 3 the rows 8 m + 4 kh + i of the i8 MFMA's layout, one product each
+      const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(X[h], W, cin, 0, 0, 0);
+      // f(xs * ws) of the sub-tile: v_mfma_f32_4x4x1_16b_f32 gives lane l, register i the product of lane
+      // 4 (l / 4) + i's A and lane l's B, so A = the scale of token 8 m + 4 kh + lane % 4 and B = the row's scale
+      // give registers 4 m .. 4 m + 3 the tokens 8 m + 4 kh + i of the i8 MFMA's layout, one product each
       v16f sc;
 #pragma unroll
       for (int m = 0; m < 4; m++) {
-        const v4f d = __builtin_amdgcn_mfma_f32_4x4x1f32(w4[m], xv[h], zero4f(), 0, 0, 0);
+        const v4f d = __builtin_amdgcn_mfma_f32_4x4x1f32(xv[h][m], wsv, zero4f(), 0, 0, 0);
         sc[4 * m] = d[0]; sc[4 * m + 1] = d[1]; sc[4 * m + 2] = d[2]; sc[4 * m + 3] = d[3];
       }
       float *a = acc[2 * sp + h];
@@ -383,16 +381,15 @@ __global__ __launch_bounds__(QNT) void gemm_relaxed(Job J) {
     for (int gi = 0; gi < ng - ng4; gi++) q_group<PACK, WC>(acc, T, gi, pair, lane);
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      const int t = tok0 + 32 * (i & 1) + (lane & 31);
-      if (t < M) {
-        float *out = (float *)(J.out + t * J.os);
-        const int rbase = row0 + 64 * pair + 32 * (i >> 1) + 4 * (lane >> 5);
+      const int row = row0 + 64 * pair + 32 * (i >> 1) + (lane & 31);
+      if (row < J.r1) {
+        const int tbase = tok0 + 32 * (i & 1) + 4 * (lane >> 5);
 #pragma unroll
         for (int q = 0; q < 4; q++)
 #pragma unroll
           for (int e = 0; e < 4; e++) {
-            const int row = rbase + 8 * q + e;
-            if (row < J.r1) out[row] = acc[i][4 * q + e];
+            const int t = tbase + 8 * q + e;
+            if (t < M) ((float *)(J.out + t * J.os))[row] = acc[i][4 * q + e];
           }
       }
     }
