@@ -20,7 +20,8 @@ roofline: the GEMV kernel alone: a graph of only a step's products launches, rep
 average launch duration; traffic: the HBM bytes a launch moves, from rocprofv3's counters
 (profiles/gemv_q8r_8b_decode_traffic.md).
 Also reported: the int8 prefill GEMM (config 3's M = 2048 over one layer's matrices) in TOPS against the dense int8
-MFMA peak, and the oracle (the C restatement, oracle/) on the host's cores as the CPU baseline.
+MFMA peak, the measured ceilings (hq_ceiling_read past the caches, hq_ceiling_mfma on registers), and the oracle (the
+C restatement, oracle/) on the host's cores as the CPU baseline.
 """
 import argparse
 import ctypes
@@ -400,6 +401,31 @@ def cpu_baseline(args, seconds=10.0):
                       f"(245 MB), {passes} passes in {total_s:.1f} s on {threads} threads"}
 
 
+def measure_ceilings(torch, pkg):
+    """The measured ceilings beside the nominal peaks: hq_ceiling_read over 512 MB buffers taken in turn (2 GB in
+    all, past the 256 MB Infinity Cache; a graph of 16 launches), and hq_ceiling_mfma (registers only, 8 blocks a CU)."""
+    lib = pkg.library()
+    sink = torch.zeros(256, dtype=torch.int32, device="cuda:0")
+    size = 512 << 20
+    bufs = [torch.ones(size, dtype=torch.uint8, device="cuda:0") for _ in range(4)]
+
+    def reads(h):
+        for i in range(16):
+            pkg.check(lib.hq_ceiling_read(bufs[i % 4].data_ptr(), size, sink.data_ptr(), h))
+    read_s = _graph_time(torch, reads, 3) / 16
+    del bufs
+    torch.cuda.empty_cache()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    blocks, iters = 8 * cus, 2000
+
+    def mfmas(h):
+        pkg.check(lib.hq_ceiling_mfma(blocks, iters, sink.data_ptr(), h))
+    mfma_s = _graph_time(torch, mfmas, 3)
+    ops = blocks * 4 * iters * 8 * 32768 * 2
+    return {"read_GBps": round(size / read_s / 1e9, 1), "read_bytes": size,
+            "mfma_int8_TOPS": round(ops / mfma_s / 1e12, 1)}
+
+
 def calibrate():
     """Kernels of known traffic for the counters' scale: a device-to-device copy of 1 GiB (reads and writes 1 GiB)
     and hq_ceiling_read over the same GiB (reads it), three times each."""
@@ -465,6 +491,7 @@ def main():
     del layers, head, phases
     torch.cuda.empty_cache()
     gemm = None if args.no_gemm else measure_gemm(torch, pkg, args)
+    ceilings = measure_ceilings(torch, pkg)
     configs = measure_configs(torch, pkg, args) if args.configs else None
     cpu = None if args.no_cpu else cpu_baseline(args)
     derived = fused if args.mode == "fused" else separate
@@ -484,7 +511,7 @@ def main():
                      "bytes_per_launch": round(derived["gemv_bytes_per_launch"])},
         "cpu_baseline": cpu,
         "detail": {"fused": fused, "quantize_then_phase": separate, "quantize_then_phase_with_wc": separate_wc,
-                   "prefill_gemm": gemm, "configs": configs},
+                   "prefill_gemm": gemm, "ceilings": ceilings, "configs": configs},
     }
     print(json.dumps(line))
 

@@ -583,3 +583,31 @@ def test_matmuls_plain_and_ternary(pkg, arena, oracle, tokens):
         xi, area = oracle.interleave(q0.view(np.int8), s0)
         want_t = oracle.matmul_t2r(xi, area, pack_ternary(codes), halves, n)
         assert same_bits(arena.get(ot + 4 * rows * t, F, rows), want_t)
+
+
+# ---- the ceilings -------------------------------------------------------------------------------------------------
+def test_ceiling_read_reads_every_byte(pkg, arena):
+    """hq_ceiling_read stores a lane's fold only when it equals 0x9e3779b9: a buffer whose only nonzero word is that
+    value, in the partial last block (16 KB + 48 bytes: three 16-byte pieces past the first block), makes lane 0 of
+    that block store it; an all-zero buffer stores nothing"""
+    L = pkg.library()
+    size = 16384 + 48
+    for where in (None, 16384, 16384 + 32):
+        words = np.zeros(size // 4, np.uint32)
+        if where is not None:
+            words[where // 4] = 0x9E3779B9
+        buf = arena.put(words)
+        sink = arena.alloc(1024, fill=np.zeros(256, np.uint32))
+        assert L.hq_ceiling_read(buf, size, sink, None) == 0, L.hq_last_error_message()
+        got = arena.get(sink, np.uint32, 256)
+        want = np.zeros(256, np.uint32)
+        if where is not None:  # uint4 1024 + 2 q is lane 2 q of the last block's first wave
+            want[(where - 16384) // 16] = 0x9E3779B9
+        assert np.array_equal(got, want), (where, np.nonzero(got))
+
+
+def test_ceiling_mfma_runs(pkg, arena):
+    L = pkg.library()
+    sink = arena.alloc(1024, fill=np.zeros(256, np.int32))
+    assert L.hq_ceiling_mfma(4, 3, sink, None) == 0, L.hq_last_error_message()
+    assert not arena.get(sink, np.int32, 256).any()
