@@ -65,20 +65,20 @@ void matmul_q8(void *xout, const void *xq, const void *xs, const void *wq, const
  * and xs + t frame (bytes), its outputs at xout + t os (bytes); every (row, token) is matmul_q8r's number */
 void matmul_q8r_tile(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, const void *wc,
                      int32_t n, int32_t r0, int32_t r1, int32_t count, int32_t os, int32_t frame);
-/* kernels/relaxed/six.ts:152-175: int6 weights (24 bytes a group of 32, kernels/six.ts), as matmul_q8r */
+/* kernels/relaxed/six.ts:16-39: int6 weights (24 bytes a group of 32, kernels/six.ts), as matmul_q8r */
 void matmul_q6r(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, const void *wc,
                 int32_t n, int32_t r0, int32_t r1);
 /* kernels/kernel/matmul.ts:227-244: int6 weights, as matmul_q8 */
 void matmul_q6(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, int32_t n, int32_t r0,
                int32_t r1);
-/* kernels/relaxed/signs.ts:292-294: ternary weights (32 bytes a group of 128, kernels/ternary.ts; ws: float16
+/* kernels/relaxed/signs.ts:117-119: ternary weights (32 bytes a group of 128, kernels/ternary.ts; ws: float16
  * scales, one a group) times the activations interleave() left (xs: scales, then the sums) */
 void matmul_t2r(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, int32_t n, int32_t r0,
                 int32_t r1, int32_t three);
 /* kernels/kernel/matmul.ts:218-220: the same numbers (tests/ternary-check.ts:7-10) */
 void matmul_t2(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, int32_t n, int32_t r0,
                int32_t r1, int32_t three);
-/* kernels/relaxed/signs.ts:295-297: matmul_t2r for `count` tokens, strides as matmul_q8r_tile's */
+/* kernels/relaxed/signs.ts:120-122: matmul_t2r for `count` tokens, strides as matmul_q8r_tile's */
 void matmul_t2r_tile(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, int32_t n,
                      int32_t r0, int32_t r1, int32_t count, int32_t os, int32_t frame, int32_t three);
 

@@ -35,7 +35,7 @@ static int32_t trunc_sat(float v) {
 
 static int32_t wrap16(int32_t v) { return (int32_t)(int16_t)(uint16_t)(uint32_t)v; }
 
-/* kernels/kernel/halves.ts:317-326: ((h sign-extended) << 13 & 0x8fffffff) as float, times 2^112 */
+/* kernels/kernel/halves.ts:6-23: ((h sign-extended) << 13 & 0x8fffffff) as float, times 2^112 */
 float o_half(uint16_t h) {
   int32_t bits = ((int32_t)(int16_t)h * 8192) & (int32_t)0x8fffffff;
   float f;
@@ -204,7 +204,7 @@ void o_matmul_q8r_tile(void *xout, const void *xq, const void *xs, const int8_t 
                  (const float *)((const char *)xs + (int64_t)t * frame), wq, ws, wc, n, r0, r1);
 }
 
-/* ---- int6 products: relaxed/six.ts:146-175, kernel/matmul.ts:227-244 ---------------------------------------- */
+/* ---- int6 products: relaxed/six.ts:10-39, kernel/matmul.ts:227-244 ---------------------------------------- */
 void o_matmul_q6r(float *xout, const uint8_t *xq, const float *xs, const uint8_t *wq, const float *ws,
                   const int32_t *wc, int32_t n, int32_t r0, int32_t r1) {
   const int32_t ng = n / GS;
@@ -235,9 +235,9 @@ void o_matmul_q6(float *xout, const int8_t *xq, const float *xs, const uint8_t *
   }
 }
 
-/* ---- ternary products: kernels/ternary.ts:54-65, relaxed/signs.ts:185-230 ------------------------------------- */
+/* ---- ternary products: kernels/ternary.ts:23-34, relaxed/signs.ts:17-55 ------------------------------------- */
 
-/* codes(v, p, three) (ternary.ts:56-58): i16x8.shr_u by 2p, then the mask; byte c of a 16-byte vector */
+/* codes(v, p, three) (ternary.ts:25-27): i16x8.shr_u by 2p, then the mask; byte c of a 16-byte vector */
 static int32_t code_of(const uint8_t *v16, int c, int p, int32_t three) {
   if (p == 0) return v16[c] & three;
   const int lo = c & ~1;

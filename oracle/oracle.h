@@ -26,7 +26,7 @@ void o_six_sums(int32_t *out, const uint8_t *w, int32_t groups);
 void o_six_unpack(int8_t *out32, const uint8_t *group24);
 /* kernels/kernel/matmul.ts:134-146 */
 void o_interleave(int8_t *xq, float *xs, int32_t n);
-/* kernels/kernel/halves.ts:320-326 (half) */
+/* kernels/kernel/halves.ts:21-23 (half) */
 float o_half(uint16_t h);
 
 /* kernels/relaxed/int8.ts:17-50 */
@@ -39,17 +39,17 @@ void o_matmul_q8(float *xout, const int8_t *xq, const float *xs, const int8_t *w
 void o_matmul_q8r_tile(void *xout, const void *xq, const void *xs, const int8_t *wq, const float *ws,
                        const int32_t *wc, int32_t n, int32_t r0, int32_t r1, int32_t count, int32_t os,
                        int32_t frame);
-/* kernels/relaxed/six.ts:152-175 */
+/* kernels/relaxed/six.ts:16-39 */
 void o_matmul_q6r(float *xout, const uint8_t *xq, const float *xs, const uint8_t *wq, const float *ws,
                   const int32_t *wc, int32_t n, int32_t r0, int32_t r1);
 /* kernels/kernel/matmul.ts:227-244 */
 void o_matmul_q6(float *xout, const int8_t *xq, const float *xs, const uint8_t *wq, const float *ws, int32_t n,
                  int32_t r0, int32_t r1);
-/* kernels/relaxed/signs.ts:203-230, 292-294 (matmul_t2r) and kernels/kernel/matmul.ts:196-220 (matmul_t2): the
+/* kernels/relaxed/signs.ts:28-55, 117-119 (matmul_t2r) and kernels/kernel/matmul.ts:196-220 (matmul_t2): the
  * same numbers to the bit (tests/ternary-check.ts:7-10) */
 void o_matmul_t2r(float *xout, const int8_t *xq, const float *xs, const uint8_t *wq, const uint16_t *ws,
                   int32_t n, int32_t r0, int32_t r1, int32_t three);
-/* kernels/relaxed/signs.ts:252-289, 295-297 */
+/* kernels/relaxed/signs.ts:77-114, 120-122 */
 void o_matmul_t2r_tile(void *xout, const void *xq, const void *xs, const uint8_t *wq, const uint16_t *ws,
                        int32_t n, int32_t r0, int32_t r1, int32_t count, int32_t os, int32_t frame,
                        int32_t three);

@@ -45,7 +45,7 @@ HQ_DEV float quad_lane(float v) {
 // f32x4.max lane semantics: NaN if either is NaN (kernels/kernel/quantize.ts:10-19); the inputs are |x| >= +0
 HQ_DEV float wasm_max_abs(float a, float b) { return (a != a || b != b) ? __int_as_float(0x7fc00000) : fmaxf(a, b); }
 
-// kernels/kernel/halves.ts:317-326: a half's bits sign-extended, << 13, & 0x8fffffff, as float, times 2^112:
+// kernels/kernel/halves.ts:6-23: a half's bits sign-extended, << 13, & 0x8fffffff, as float, times 2^112:
 // exact for every finite half, an infinity reads as 65536
 HQ_DEV float half_to_float(uint32_t h16) {
   const int32_t bits = ((int32_t)(int16_t)(uint16_t)h16 * 8192) & (int32_t)0x8fffffff;
@@ -101,7 +101,7 @@ HQ_DEV void quantize_group(const float *p, int32_t bias, uint32_t q[8], float &s
 // v_perm_b32: byte i of the result is byte sel.i of {hi:lo} (0..3 from lo, 4..7 from hi)
 HQ_DEV uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) { return __builtin_amdgcn_perm(hi, lo, sel); }
 
-// the ternary codes of plane p of four bytes: (v >> 2p) & 3 a byte (kernels/ternary.ts:54-58).  The reference
+// the ternary codes of plane p of four bytes: (v >> 2p) & 3 a byte (kernels/ternary.ts:23-27).  The reference
 // shifts 16-bit lanes; with the mask 3 a 32-bit shift leaves the same bits (what a byte takes from its neighbour
 // lands at bit 8 - 2p >= 2 and is masked away).
 template <int P>

@@ -1,6 +1,6 @@
 // gemm.hip — the prompt kernels on the matrix cores (a prompt's many tokens):
 //   matmul_q8r_tile (kernels/relaxed/int8.ts:52-166), matmul_q6r for many tokens (jobs.ts:243-248 runs it a token at
-//   a time: every (row, token) is matmul_q6r's number), matmul_t2r_tile (kernels/relaxed/signs.ts:232-297).
+//   a time: every (row, token) is matmul_q6r's number), matmul_t2r_tile (kernels/relaxed/signs.ts:77-114, 120-122).
 //
 // The matrix core gives each group's exact integer: v_mfma_i32_32x32x32_i8 with K = 32 is one scale group of 32 (for
 // ternary, one part of 32 of a group of 128), and the correction rides in its accumulator input:
@@ -482,7 +482,7 @@ HQ_DEV uint2 t_acts8(const StageT &S, int tok, int o) {
 }
 
 // part k of group gi of the stage for the lane's slice, both token halves: f(f(whole * xs) * d) into the part's
-// chain (relaxed/signs.ts:206)
+// chain (relaxed/signs.ts:31)
 HQ_DEV void t_group(float acc0[16], float acc1[16], const StageT &S, int gi, int k, int slice, int lane) {
   const int h = k >> 1, s = k & 1, kh = lane >> 5, row = 32 * slice + (lane & 31);
   // B: the row's codes of planes 2 kh, 2 kh + 1, bytes c = 8 s .. + 7 of block h (chunk 2 gi + h, half s)
@@ -521,7 +521,7 @@ HQ_DEV void t_step(Ternary &L, const StageT &cur, StageT &next, int s, int stage
   if (s >= stages) return;
   wait_for<TLOADS>(s, stages);
   if (s + AHEAD < stages) L.load(next, s + AHEAD);
-  // part `part` of groups 2 s and 2 s + 1 (relaxed/signs.ts:198-207)
+  // part `part` of groups 2 s and 2 s + 1 (relaxed/signs.ts:28-31)
   t_group(acc0, acc1, cur, 0, part, slice, lane);
   if (TG * s + 1 < groups) t_group(acc0, acc1, cur, 1, part, slice, lane);
 }

@@ -1,8 +1,8 @@
 // gemv.hip — the token kernels (decode, 1..4 tokens a launch, the weights read once for all of them):
-//   matmul_q8r / matmul_q6r   (kernels/relaxed/int8.ts:17-50, relaxed/six.ts:152-175; the tile's numbers for
+//   matmul_q8r / matmul_q6r   (kernels/relaxed/int8.ts:17-50, relaxed/six.ts:16-39; the tile's numbers for
 //                              2..4 tokens, relaxed/int8.ts:52-166)
 //   matmul_q8 / matmul_q6     (kernels/kernel/matmul.ts:77-104, 227-244)
-//   matmul_t2r / matmul_t2    (kernels/relaxed/signs.ts:203-230, kernel/matmul.ts:196-220; the same numbers)
+//   matmul_t2r / matmul_t2    (kernels/relaxed/signs.ts:35-55, 117-119, kernel/matmul.ts:196-220; the same numbers)
 //
 // Layout: a row is 16 lanes (ternary: 8, 16 or 32 by the row's length), a wave 4 rows; a block is 2 waves (8 rows)
 // for the relaxed kinds, 4 waves for the others.  Lane l of a row of L lanes takes the groups L i + l (i = 0, 1,
@@ -510,7 +510,7 @@ HQ_DEV void ternary_step(FoldL<T, L> &f, const TernaryActs<T, STAGE> &A, const u
         dot = sdot4((int32_t)codes<3>(w0), (int32_t)a[12 + 2 * s], dot);
         dot = sdot4((int32_t)codes<3>(w1), (int32_t)a[13 + 2 * s], dot);
         const int k = 2 * h + s;
-        // f(f(whole * xs) * d) (relaxed/signs.ts:206)
+        // f(f(whole * xs) * d) (relaxed/signs.ts:31)
         f.v[buf][slot][t][k][lane] = valid ? fmul(fmul((float)dot, scale[k]), d) : 0.0f;
       }
     }

@@ -7,7 +7,7 @@ Each check is one the reference's arithmetic fixes independently of how the orac
   * round trips: pack6 -> six unpack (tests/test_int6.py), hand-derived bytes of the int6 layout;
   * hand-derived float32 answers of order-revealing inputs: big/small products that tell the reference's lane
     chains, the order of the horizontal sum, the place of the tail groups and the separate (unfused) roundings apart
-    from every plausible alternative (relaxed/int8.ts:26-47, kernel/matmul.ts:60-97, relaxed/signs.ts:198-228);
+    from every plausible alternative (relaxed/int8.ts:26-47, kernel/matmul.ts:60-97, relaxed/signs.ts:28-55);
   * the lane membership of matmul_q8's integer partial sums, found position by position;
   * exact float64 sums of the same integers within a bound, and power-of-two scales where every order is exact;
   * the reference tests' own models (int8-check.ts:65-90, ternary-check.ts:129-139) on their LCG streams, bit for bit.
@@ -309,7 +309,7 @@ def t2_run(oracle, a, xs, wq, ws, n):
 
 
 def test_t2r_lane_is_subgroup(oracle):
-    """relaxed/signs.ts:198-228: lane k adds sub-group k (activations 32k..32k+31) of every group in order.
+    """relaxed/signs.ts:28-55: lane k adds sub-group k (activations 32k..32k+31) of every group in order.
     2^24 (g0 k0), 1 (g0 k1), -2^24 (g1 k0): lane 0 cancels, lane 1 keeps 1."""
     a, xs, wq, ws, n = t2_crafted({(0, 0): (1, BIG), (0, 1): (1, 0), (1, 0): (-1, BIG)}, 2)
     assert t2_run(oracle, a, xs, wq, ws, n) == F(1.0)
@@ -342,7 +342,7 @@ def test_t2r_scales_twice_rounded(oracle):
 
 
 def test_t2r_fourth_code(oracle):
-    """ternary.ts:54-58 / ternary-check.ts:7-10: code 3 (PQ2_0's fourth, weight 2) passes the mask."""
+    """ternary.ts:23-27 / ternary-check.ts:7-10: code 3 (PQ2_0's fourth, weight 2) passes the mask."""
     n = 128
     codes = np.ones(n, np.uint8)
     a = np.zeros(n, np.int8)
@@ -387,7 +387,7 @@ def test_q8r_float64_bound(oracle):
 
 
 def test_q6_is_q8_on_widened_weights(oracle):
-    """relaxed/six.ts:142-175, kernel/matmul.ts:226-244: the int6 products are the int8 ones on the widened
+    """relaxed/six.ts:10-39, kernel/matmul.ts:226-244: the int6 products are the int8 ones on the widened
     groups (six.ts:1-11), scale and order alike."""
     rng = np.random.default_rng(8)
     rows, ng = 9, 11
