@@ -81,6 +81,22 @@ void matmul_t2(void *xout, const void *xq, const void *xs, const void *wq, const
 /* kernels/relaxed/signs.ts:120-122: matmul_t2r for `count` tokens, strides as matmul_q8r_tile's */
 void matmul_t2r_tile(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, int32_t n,
                      int32_t r0, int32_t r1, int32_t count, int32_t os, int32_t frame, int32_t three);
+/* kernels/relaxed/signs.ts:123-125: binary weights (16 bytes a group of 128, kernels/binary.ts: weight 64h + 4c + p
+ * at bit 4h + p of byte c, set for +1; ws: float16 scales, one a group) times the activations interleave() left;
+ * every number is matmul_t2r's for the same signs (tests/ternary-check.ts:286-341).  two must be 2 (jobs.ts:52) */
+void matmul_b1r(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, int32_t n, int32_t r0,
+                int32_t r1, int32_t two);
+/* kernels/kernel/matmul.ts:222-224: the same numbers */
+void matmul_b1(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, int32_t n, int32_t r0,
+               int32_t r1, int32_t two);
+/* kernels/relaxed/signs.ts:126-128: matmul_b1r for `count` tokens, strides as matmul_q8r_tile's */
+void matmul_b1r_tile(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, int32_t n,
+                     int32_t r0, int32_t r1, int32_t count, int32_t os, int32_t frame, int32_t two);
+/* kernels/kernel/quantize.ts:232-247: n float32 values at x (device; groups of 128) -> out (n/8 bytes: bit 4h + p of
+ * byte c of a group set where value 64h + 4c + p is not below 0) and xs (the largest |value| of every group, float32);
+ * returns 1 where a value is not plus or minus its group's largest (or the call failed: hq_last_error), else 0.
+ * It waits for the library's stream to know. */
+int32_t binary_x(void *out, void *xs, const void *x, int32_t n);
 
 /* ---- the library's own ----------------------------------------------------------------------------------------- */
 
@@ -129,6 +145,14 @@ int32_t hq_matmul_t2r_ex(void *xout, const void *xq, const void *xs, const void 
 int32_t hq_matmul_t2r_tile_ex(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, int32_t n,
                               int32_t r0, int32_t r1, int32_t count, int32_t os, int32_t frame, int32_t three,
                               void *stream);
+int32_t hq_matmul_b1r_ex(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, int32_t n,
+                         int32_t r0, int32_t r1, int32_t two, void *stream);
+int32_t hq_matmul_b1r_tile_ex(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, int32_t n,
+                              int32_t r0, int32_t r1, int32_t count, int32_t os, int32_t frame, int32_t two,
+                              void *stream);
+/* binary_x on a stream, without waiting: `bad` (device, 4-byte aligned; may be NULL) is set to 1 where a value is
+ * refused and left as it was otherwise, so the caller clears it first */
+int32_t hq_binary_x_ex(void *out, void *xs, const void *x, int32_t n, void *bad, void *stream);
 
 /* The activations of `count` tokens prepared in one launch (src/runtime/forward/engine.ts:405 calls ready() once a
  * token): token t's float32 values at x + t x_stride (bytes) -> xq + t frame and xs + t frame, as quantize_x; and,
@@ -141,7 +165,7 @@ int32_t hq_interleave_batch(void *xq, void *xs, int32_t n, int32_t count, int32_
  * of `stride` float64 each (the reference's table has JOB = 16: the first 14 are used), each
  *   [kind, out, a, b, a4, a5, a6, a7, a8, rows, count, os, as, bs]
  * with kind the place of its line in jobs.ts's WORK (0 matmul_q8r, 1 matmul_q8, 5 matmul_q6r, 6 matmul_q6,
- * 8 matmul_t2r, 9 matmul_t2), the eight arguments as WORK's `one` reads them, and every row [0, rows) of every one
+ * 8 matmul_t2r, 9 matmul_t2, 13 matmul_b1r, 14 matmul_b1), the eight arguments as WORK's `one` reads them, and every row [0, rows) of every one
  * of `count` tokens run (a job's out / a / b advance by os / as / bs bytes a token).  The addresses are device
  * addresses held exactly in the doubles (below 2^53).  Jobs of one kind and token count share a launch. */
 int32_t hq_phase(const double *jobs, int32_t count, int32_t stride, void *stream);
@@ -150,8 +174,8 @@ int32_t hq_phase(const double *jobs, int32_t count, int32_t stride, void *stream
  * activations: every job takes the same n and token count, token t's n values at x + t x_stride (bytes; x and
  * x_stride 16-byte aligned).  The relaxed int8 / int6 jobs of up to 4 tokens run with quantize_x in the products'
  * own launch (each block quantizes the input into its LDS: one launch a phase, the jobs' a / b not written); the
- * others are readied into their a / b (quantize_x at their bias, and interleave for ternary; jobs.ts:376-379,
- * 421-424) and then run as hq_phase runs them.  Every output is the number quantize_x + the kernel give. */
+ * others are readied into their a / b (quantize_x at their bias, and interleave for ternary and binary;
+ * jobs.ts:376-379, 421-424, 435-438) and then run as hq_phase runs them.  Every output is the number quantize_x + the kernel give. */
 int32_t hq_matmuls(const void *x, int32_t x_stride, const double *jobs, int32_t count, int32_t stride, void *stream);
 
 /* The ceilings the kernels are measured against (no counterpart on this path: the reference's CPU ceiling loops,

@@ -235,7 +235,7 @@ void o_matmul_q6(float *xout, const int8_t *xq, const float *xs, const uint8_t *
   }
 }
 
-/* ---- ternary products: kernels/ternary.ts:23-34, relaxed/signs.ts:17-55 ------------------------------------- */
+/* ---- ternary and binary products: kernels/ternary.ts:23-34, binary.ts:19-22, relaxed/signs.ts:17-55 -------------- */
 
 /* codes(v, p, three) (ternary.ts:25-27): i16x8.shr_u by 2p, then the mask; byte c of a 16-byte vector */
 static int32_t code_of(const uint8_t *v16, int c, int p, int32_t three) {
@@ -247,20 +247,44 @@ static int32_t code_of(const uint8_t *v16, int c, int p, int32_t three) {
   return (int32_t)(int8_t)(uint8_t)(byte & (uint32_t)three);
 }
 
-/* one row of matmul_t2r / matmul_t2: lane k adds sub-group k (activations 32k..32k+31) of every group of 128, in
- * order: f(f(whole * xs) * d) (tests/ternary-check.ts:129-139) */
-static float t2_row(const uint8_t *row, const uint16_t *srow, const int8_t *xq, const float *xs,
-                    const int32_t *sums, int32_t groups, int32_t three) {
+/* bitCodes(v, k, two) (binary.ts:19-22): byte c of (k == 0 ? v + v (i8x16.add) : k == 1 ? v : v >> (k - 1) in 16-bit
+ * lanes), masked with two: twice the bit k of byte c */
+static int32_t bit_code_of(const uint8_t *v16, int c, int k, int32_t two) {
+  uint32_t byte;
+  if (k == 0) {
+    byte = (uint8_t)(v16[c] + v16[c]);
+  } else if (k == 1) {
+    byte = v16[c];
+  } else {
+    const int lo = c & ~1;
+    const uint32_t lane = (uint32_t)v16[lo] | ((uint32_t)v16[lo + 1] << 8);
+    const uint32_t shifted = (lane >> (k - 1)) & 0xffff;
+    byte = (c & 1) ? (shifted >> 8) : (shifted & 0xff);
+  }
+  return (int32_t)(int8_t)(uint8_t)(byte & (uint32_t)two);
+}
+
+/* one row of signsRows<P> (relaxed/signs.ts:28-55; kernel/matmul.ts:196-224 gives the same numbers): lane k adds
+ * sub-group k (activations 32k..32k+31) of every group of 128, in order, f(f(whole * xs) * d)
+ * (tests/ternary-check.ts:129-139).  Ternary (binary == 0): block h of a group is its bytes 16h..16h+15, plane p
+ * codes(v, p) (ternary.ts:25-27); binary: both blocks are the group's 16 bytes, plane p of block h
+ * bitCodes(v, 4h + p) (signs.ts:33-37) */
+static float signs_row(const uint8_t *row, const uint16_t *srow, const int8_t *xq, const float *xs,
+                       const int32_t *sums, int32_t groups, int32_t code, int binary) {
   float lane[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int32_t bytes = binary ? 16 : 32;
   for (int32_t g = 0; g < groups; g++) {
     const float d = o_half(srow[g]);
     for (int k = 0; k < 4; k++) {
       const int h = k >> 1, s = k & 1;
-      const uint8_t *v = row + (int64_t)g * 32 + 16 * h;
+      const uint8_t *v = row + (int64_t)g * bytes + (binary ? 0 : 16 * h);
       const int8_t *x = xq + (int64_t)g * 128 + 64 * h;
       int32_t dot = 0;
       for (int p = 0; p < 4; p++)
-        for (int c = 8 * s; c < 8 * s + 8; c++) dot += code_of(v, c, p, three) * (int32_t)x[16 * p + c];
+        for (int c = 8 * s; c < 8 * s + 8; c++) {
+          const int32_t cd = binary ? bit_code_of(v, c, 4 * h + p, code) : code_of(v, c, p, code);
+          dot += cd * (int32_t)x[16 * p + c];
+        }
       const int32_t whole = dot + sums[4 * g + k];
       const float a = (float)whole * xs[4 * g + k];
       const float b = a * d;
@@ -270,20 +294,70 @@ static float t2_row(const uint8_t *row, const uint16_t *srow, const int8_t *xq, 
   return ((lane[0] + lane[1]) + lane[2]) + lane[3];
 }
 
-void o_matmul_t2r(float *xout, const int8_t *xq, const float *xs, const uint8_t *wq, const uint16_t *ws,
-                  int32_t n, int32_t r0, int32_t r1, int32_t three) {
+static void signs_rows(float *xout, const int8_t *xq, const float *xs, const uint8_t *wq, const uint16_t *ws,
+                       int32_t n, int32_t r0, int32_t r1, int32_t code, int binary) {
   const int32_t groups = n >> 7;
   const int32_t *sums = (const int32_t *)(xs + (n >> 5));
+  const int64_t row_bytes = binary ? (n >> 3) : (n >> 2);
   for (int32_t i = r0; i < r1; i++)
-    xout[i] = t2_row(wq + (int64_t)i * (n >> 2), ws + (int64_t)i * groups, xq, xs, sums, groups, three);
+    xout[i] = signs_row(wq + (int64_t)i * row_bytes, ws + (int64_t)i * groups, xq, xs, sums, groups, code, binary);
+}
+
+void o_matmul_t2r(float *xout, const int8_t *xq, const float *xs, const uint8_t *wq, const uint16_t *ws,
+                  int32_t n, int32_t r0, int32_t r1, int32_t three) {
+  signs_rows(xout, xq, xs, wq, ws, n, r0, r1, three, 0);
+}
+
+void o_matmul_b1r(float *xout, const int8_t *xq, const float *xs, const uint8_t *wq, const uint16_t *ws,
+                  int32_t n, int32_t r0, int32_t r1, int32_t two) {
+  signs_rows(xout, xq, xs, wq, ws, n, r0, r1, two, 1);
+}
+
+/* signsTile<P> (relaxed/signs.ts:77-114): every (row, token) is the token kernel's number */
+static void signs_tile(void *xout, const void *xq, const void *xs, const uint8_t *wq, const uint16_t *ws,
+                       int32_t n, int32_t r0, int32_t r1, int32_t count, int32_t os, int32_t frame, int32_t code,
+                       int binary) {
+  for (int32_t t = 0; t < count; t++)
+    signs_rows((float *)((char *)xout + (int64_t)t * os), (const int8_t *)((const char *)xq + (int64_t)t * frame),
+               (const float *)((const char *)xs + (int64_t)t * frame), wq, ws, n, r0, r1, code, binary);
 }
 
 void o_matmul_t2r_tile(void *xout, const void *xq, const void *xs, const uint8_t *wq, const uint16_t *ws,
                        int32_t n, int32_t r0, int32_t r1, int32_t count, int32_t os, int32_t frame,
                        int32_t three) {
-  for (int32_t t = 0; t < count; t++)
-    o_matmul_t2r((float *)((char *)xout + (int64_t)t * os), (const int8_t *)((const char *)xq + (int64_t)t * frame),
-                 (const float *)((const char *)xs + (int64_t)t * frame), wq, ws, n, r0, r1, three);
+  signs_tile(xout, xq, xs, wq, ws, n, r0, r1, count, os, frame, three, 0);
+}
+
+void o_matmul_b1r_tile(void *xout, const void *xq, const void *xs, const uint8_t *wq, const uint16_t *ws,
+                       int32_t n, int32_t r0, int32_t r1, int32_t count, int32_t os, int32_t frame,
+                       int32_t two) {
+  signs_tile(xout, xq, xs, wq, ws, n, r0, r1, count, os, frame, two, 1);
+}
+
+/* ---- binary_x: kernels/kernel/quantize.ts:184-247 ------------------------------------------------------------ */
+int32_t o_binary_x(uint8_t *out, float *xs, const float *x, int32_t n) {
+  int32_t bad = 0;
+  for (int32_t g = 0; g < n; g += 128) {
+    const float *p = x + g;
+    /* groupLargest (quantize.ts:186-191): lane j's f32x4.max of |values 4i + j|, then max(max(l0, l1), max(l2, l3)) */
+    float lane[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = 0; i < 32; i++)
+      for (int j = 0; j < 4; j++) lane[j] = wasm_max(lane[j], fabsf(p[4 * i + j]));
+    const float scale = wasm_max(wasm_max(lane[0], lane[1]), wasm_max(lane[2], lane[3]));
+    xs[g >> 7] = scale;
+    uint8_t *to = out + (g >> 3);
+    for (int c = 0; c < 16; c++) {
+      uint32_t byte = 0;
+      for (int j = 0; j < 4; j++) {
+        const float v0 = p[4 * c + j], v1 = p[64 + 4 * c + j];
+        byte |= (uint32_t)(!(v0 < 0.0f)) << j;
+        byte |= (uint32_t)(!(v1 < 0.0f)) << (4 + j);
+        if (!(fabsf(v0) == scale && fabsf(v1) == scale)) bad = 1;
+      }
+      to[c] = (uint8_t)byte;
+    }
+  }
+  return bad;
 }
 
 /* ---- CPU baseline: phase()-style row chunks over host threads ------------------------------------------------ */

@@ -53,6 +53,19 @@ void o_matmul_t2r(float *xout, const int8_t *xq, const float *xs, const uint8_t 
 void o_matmul_t2r_tile(void *xout, const void *xq, const void *xs, const uint8_t *wq, const uint16_t *ws,
                        int32_t n, int32_t r0, int32_t r1, int32_t count, int32_t os, int32_t frame,
                        int32_t three);
+/* kernels/relaxed/signs.ts:123-125 (matmul_b1r) and kernels/kernel/matmul.ts:222-224 (matmul_b1): binary weights
+ * (kernels/binary.ts: 16 bytes a group of 128, weight 64h + 4c + p at bit 4h + p of byte c), ternary's kernels with
+ * bitCodes for the codes (signs.ts:33-37); ternary's numbers for the same signs (tests/ternary-check.ts:286-341) */
+void o_matmul_b1r(float *xout, const int8_t *xq, const float *xs, const uint8_t *wq, const uint16_t *ws,
+                  int32_t n, int32_t r0, int32_t r1, int32_t two);
+/* kernels/relaxed/signs.ts:77-114, 126-128 */
+void o_matmul_b1r_tile(void *xout, const void *xq, const void *xs, const uint8_t *wq, const uint16_t *ws,
+                       int32_t n, int32_t r0, int32_t r1, int32_t count, int32_t os, int32_t frame,
+                       int32_t two);
+/* kernels/kernel/quantize.ts:184-247: n float32 (groups of 128) -> 16 bytes a group (bit 4h + p of byte c set
+ * where value 64h + 4c + p is not below 0) and the largest |value| of every group; 1 where a value is not plus or
+ * minus its group's largest, else 0 */
+int32_t o_binary_x(uint8_t *out, float *xs, const float *x, int32_t n);
 
 /* CPU baseline: the GEMV above over rows [0, rows) on `threads` host threads, rows handed out in chunks as the
  * reference's phase() does (src/runtime/forward/threads.ts:45, 90-137: 4 chunks a thread, a shared counter).

@@ -45,11 +45,14 @@ def lib():
             "o_matmul_q6": [p, p, p, p, p, i32, i32, i32],
             "o_matmul_t2r": [p, p, p, p, p, i32, i32, i32, i32],
             "o_matmul_t2r_tile": [p, p, p, p, p, i32, i32, i32, i32, i32, i32, i32],
+            "o_matmul_b1r": [p, p, p, p, p, i32, i32, i32, i32],
+            "o_matmul_b1r_tile": [p, p, p, p, p, i32, i32, i32, i32, i32, i32, i32],
         }
         for name, argtypes in sigs.items():
             fn = getattr(L, name)
             fn.argtypes, fn.restype = argtypes, None
         L.o_half.argtypes, L.o_half.restype = [ctypes.c_uint16], ctypes.c_float
+        L.o_binary_x.argtypes, L.o_binary_x.restype = [p, p, p, i32], i32
         L.o_time_gemv.argtypes = [i32, p, p, p, p, p, p, i32, i32, i32, i32]
         L.o_time_gemv.restype = ctypes.c_double
         _lib = L
@@ -155,6 +158,26 @@ def matmul_t2r(xq, area, wq, ws_bits, n, r0=0, r1=None, three=3):
     lib().o_matmul_t2r(_p(out), _p(_c(xq, np.int8)), _p(_c(area, np.float32)), _p(_c(wq, np.uint8)),
                        _p(_c(ws_bits, np.uint16)), n, r0, r1, three)
     return out
+
+
+def matmul_b1r(xq, area, wq, ws_bits, n, r0=0, r1=None, two=2):
+    """binary weights (16 bytes a group of 128); xq, area as matmul_t2r's."""
+    rows = wq.size // (n // 8)
+    r1 = rows if r1 is None else r1
+    out = np.zeros(rows, np.float32)
+    lib().o_matmul_b1r(_p(out), _p(_c(xq, np.int8)), _p(_c(area, np.float32)), _p(_c(wq, np.uint8)),
+                       _p(_c(ws_bits, np.uint16)), n, r0, r1, two)
+    return out
+
+
+def binary_x(x):
+    """kernels/kernel/quantize.ts:232-247: float32 x (groups of 128) -> (uint8 bits (n/8), float32 scales (n/128),
+    the refusal flag)."""
+    x = _c(x, np.float32)
+    n = x.size
+    out, xs = np.zeros(n // 8, np.uint8), np.zeros(n // 128, np.float32)
+    bad = lib().o_binary_x(_p(out), _p(xs), _p(x), n)
+    return out, xs, bad
 
 
 def matmul_q8r_tokens(xq, xs, wq, ws, wc, n):

@@ -46,7 +46,13 @@ REFERENCE_SIGNATURES = {
     "matmul_t2r": [p, p, p, p, p, i32, i32, i32, i32],
     "matmul_t2": [p, p, p, p, p, i32, i32, i32, i32],
     "matmul_t2r_tile": [p, p, p, p, p, i32, i32, i32, i32, i32, i32, i32],
+    "matmul_b1r": [p, p, p, p, p, i32, i32, i32, i32],
+    "matmul_b1": [p, p, p, p, p, i32, i32, i32, i32],
+    "matmul_b1r_tile": [p, p, p, p, p, i32, i32, i32, i32, i32, i32, i32],
+    "binary_x": [p, p, p, i32],
 }
+# the reference kernels that return a value (the others return nothing)
+REFERENCE_RESTYPES = {"binary_x": i32}
 
 # the library's own (include/hq.h, second block): name -> (argtypes, restype)
 OWN_SIGNATURES = {
@@ -69,6 +75,9 @@ OWN_SIGNATURES = {
     "hq_matmul_q6_ex": ([p, p, p, p, p, i32, i32, i32, p], i32),
     "hq_matmul_t2r_ex": ([p, p, p, p, p, i32, i32, i32, i32, p], i32),
     "hq_matmul_t2r_tile_ex": ([p, p, p, p, p, i32, i32, i32, i32, i32, i32, i32, p], i32),
+    "hq_matmul_b1r_ex": ([p, p, p, p, p, i32, i32, i32, i32, p], i32),
+    "hq_matmul_b1r_tile_ex": ([p, p, p, p, p, i32, i32, i32, i32, i32, i32, i32, p], i32),
+    "hq_binary_x_ex": ([p, p, p, i32, p, p], i32),
     "hq_quantize_x_batch": ([p, p, p, i32, i32, i32, i32, i32, p], i32),
     "hq_interleave_batch": ([p, p, i32, i32, i32, p], i32),
     "hq_phase": ([ctypes.POINTER(ctypes.c_double), i32, i32, p], i32),
@@ -93,7 +102,7 @@ def library(path=None):
     lib = ctypes.CDLL(where)
     for name, argtypes in REFERENCE_SIGNATURES.items():
         fn = getattr(lib, name)
-        fn.argtypes, fn.restype = argtypes, None
+        fn.argtypes, fn.restype = argtypes, REFERENCE_RESTYPES.get(name)
     for name, (argtypes, restype) in OWN_SIGNATURES.items():
         fn = getattr(lib, name)
         fn.argtypes, fn.restype = argtypes, restype
@@ -132,12 +141,13 @@ class Kernels:
 
         def call(*args):
             lib.hq_clear_error()
-            fn(*args)
+            result = fn(*args)
             code = lib.hq_last_error()
             if code:
                 message = (lib.hq_last_error_message() or b"").decode()
                 lib.hq_clear_error()
                 raise HQError(code, message)
+            return result
 
         call.__name__ = name
         return call

@@ -64,6 +64,8 @@ bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0;
 
 hipStream_t stream_of(void *s) { return (hipStream_t)s; }
 
+constexpr int kKinds = 15;  // kinds are numbered by their place in WORK: the last one run here is matmul_b1 (14)
+
 const char *kind_name(hq::Kind k) {
   switch (k) {
   case hq::Q8R: return "matmul_q8r";
@@ -72,11 +74,14 @@ const char *kind_name(hq::Kind k) {
   case hq::Q6: return "matmul_q6";
   case hq::T2R: return "matmul_t2r";
   case hq::T2: return "matmul_t2";
+  case hq::B1R: return "matmul_b1r";
+  case hq::B1: return "matmul_b1";
   }
   return "?";
 }
 
-bool ternary(hq::Kind k) { return k == hq::T2R || k == hq::T2; }
+// ternary and binary: whole groups of 128, interleave()'s activations, float16 scales
+bool ternary(hq::Kind k) { return hq::signs_kind(k); }
 bool relaxed(hq::Kind k) { return k == hq::Q8R || k == hq::Q6R; }
 bool six(hq::Kind k) { return k == hq::Q6R || k == hq::Q6; }
 
@@ -87,7 +92,9 @@ int32_t check_job(hq::Kind kind, const hq::Job &j, int32_t three) {
   if (j.n <= 0 || j.n % unit) return fail(HQ_ERR_ARGUMENT, "%s: n = %d is not a positive multiple of %d", name, j.n, unit);
   if (j.r0 < 0 || j.r1 < j.r0) return fail(HQ_ERR_ARGUMENT, "%s: rows %d..%d", name, j.r0, j.r1);
   if (j.count < 0) return fail(HQ_ERR_ARGUMENT, "%s: count = %d", name, j.count);
-  if (ternary(kind) && three != 3) return fail(HQ_ERR_ARGUMENT, "%s: three = %d, not 3", name, three);
+  if (ternary(kind) && three != (hq::binary_kind(kind) ? 2 : 3))
+    return fail(HQ_ERR_ARGUMENT, "%s: %s = %d, not %d", name, hq::binary_kind(kind) ? "two" : "three", three,
+                hq::binary_kind(kind) ? 2 : 3);
   if (j.r1 == j.r0 || j.count == 0) return HQ_OK;
   if (!j.out || !j.xq || !j.xs || !j.wq || !j.ws) return fail(HQ_ERR_NULL, "%s: a NULL pointer", name);
   const uintptr_t wa = six(kind) ? 8 : 16;
@@ -267,6 +274,29 @@ int32_t hq_matmul_t2r_tile_ex(void *xout, const void *xq, const void *xs, const 
                               void *stream) {
   return matmul(hq::T2R, xout, xq, xs, wq, ws, nullptr, n, r0, r1, count, os, frame, three, stream);
 }
+int32_t hq_matmul_b1r_ex(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, int32_t n,
+                         int32_t r0, int32_t r1, int32_t two, void *stream) {
+  return matmul(hq::B1R, xout, xq, xs, wq, ws, nullptr, n, r0, r1, 1, 0, 0, two, stream);
+}
+int32_t hq_matmul_b1r_tile_ex(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, int32_t n,
+                              int32_t r0, int32_t r1, int32_t count, int32_t os, int32_t frame, int32_t two,
+                              void *stream) {
+  return matmul(hq::B1R, xout, xq, xs, wq, ws, nullptr, n, r0, r1, count, os, frame, two, stream);
+}
+
+// ---- binary weights from float32 (kernels/kernel/quantize.ts:232-247) -------------------------------------------
+int32_t hq_binary_x_ex(void *out, void *xs, const void *x, int32_t n, void *bad, void *stream) {
+  g_error = HQ_OK;
+  if (n < 0 || n % 128) return fail(HQ_ERR_ARGUMENT, "binary_x: n = %d is not a multiple of 128", n);
+  if (n == 0) return HQ_OK;
+  if (!out || !xs || !x) return fail(HQ_ERR_NULL, "binary_x: a NULL pointer");
+  if (!aligned(x, 16) || !aligned(xs, 4) || (bad && !aligned(bad, 4)))
+    return fail(HQ_ERR_ALIGNMENT, "binary_x: x not 16-, xs or bad not 4-byte aligned");
+  if (int32_t st = ensure_device()) return st;
+  return hip_status(hq::launch_binary_x((uint8_t *)out, (float *)xs, (const float *)x, n / 128, (int32_t *)bad,
+                                        stream_of(stream)),
+                    "binary_x");
+}
 
 // ---- a phase of jobs in the reference's table form ------------------------------------------------------------
 }  // extern "C"
@@ -274,7 +304,7 @@ int32_t hq_matmul_t2r_tile_ex(void *xout, const void *xq, const void *xs, const 
 namespace {
 
 // [kind, out, a, b, a4, a5, a6, a7, a8, rows, count, os, as, bs] (src/runtime/jobs.ts:46, 207-333) -> a Job
-int32_t parse_jobs(const double *jobs, int32_t count, int32_t stride, std::vector<hq::Job> by_kind[10],
+int32_t parse_jobs(const double *jobs, int32_t count, int32_t stride, std::vector<hq::Job> by_kind[kKinds],
                    const char *who) {
   if (count < 0 || (count > 0 && (!jobs || stride < 14)))
     return fail(HQ_ERR_ARGUMENT, "%s: count %d, stride %d (a job has 14 numbers at least)", who, count, stride);
@@ -296,9 +326,11 @@ int32_t parse_jobs(const double *jobs, int32_t count, int32_t stride, std::vecto
     case hq::Q6: k = hq::Q6; break;
     case hq::T2R: k = hq::T2R; j.sframe = j.count > 1 ? j.frame : j.sframe; break;  // its tile
     case hq::T2: k = hq::T2; break;
+    case hq::B1R: k = hq::B1R; j.sframe = j.count > 1 ? j.frame : j.sframe; break;  // its tile
+    case hq::B1: k = hq::B1; break;
     default: return fail(HQ_ERR_KIND, "%s: job %d is of kind %d, which this library does not run", who, i, kind);
     }
-    if (int32_t st = check_job(k, j, 3)) return st;
+    if (int32_t st = check_job(k, j, hq::binary_kind(k) ? 2 : 3)) return st;
     by_kind[kind].push_back(j);
   }
   return HQ_OK;
@@ -310,12 +342,12 @@ extern "C" {
 
 int32_t hq_phase(const double *jobs, int32_t count, int32_t stride, void *stream) {
   g_error = HQ_OK;
-  std::vector<hq::Job> by_kind[10];
+  std::vector<hq::Job> by_kind[kKinds];
   if (int32_t st = parse_jobs(jobs, count, stride, by_kind, "hq_phase")) return st;
   if (count > 0) {
     if (int32_t st = ensure_device()) return st;
   }
-  for (int kind = 0; kind < 10; kind++) {
+  for (int kind = 0; kind < kKinds; kind++) {
     if (by_kind[kind].empty()) continue;
     if (int32_t st = run_jobs((hq::Kind)kind, by_kind[kind], stream_of(stream))) return st;
   }
@@ -324,7 +356,7 @@ int32_t hq_phase(const double *jobs, int32_t count, int32_t stride, void *stream
 
 int32_t hq_matmuls(const void *x, int32_t x_stride, const double *jobs, int32_t count, int32_t stride, void *stream) {
   g_error = HQ_OK;
-  std::vector<hq::Job> by_kind[10];
+  std::vector<hq::Job> by_kind[kKinds];
   if (int32_t st = parse_jobs(jobs, count, stride, by_kind, "hq_matmuls")) return st;
   if (count == 0) return HQ_OK;
   // one input: every job of one n and one token count
@@ -342,7 +374,7 @@ int32_t hq_matmuls(const void *x, int32_t x_stride, const double *jobs, int32_t 
     return fail(HQ_ERR_ALIGNMENT, "hq_matmuls: x or x_stride not 16-byte aligned");
   if (int32_t st = ensure_device()) return st;
   const hipStream_t s = stream_of(stream);
-  for (int kind = 0; kind < 10; kind++) {
+  for (int kind = 0; kind < kKinds; kind++) {
     auto &list = by_kind[kind];
     if (list.empty()) continue;
     const hq::Kind k = (hq::Kind)kind;
@@ -442,6 +474,38 @@ void matmul_t2(void *xout, const void *xq, const void *xs, const void *wq, const
 void matmul_t2r_tile(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, int32_t n,
                      int32_t r0, int32_t r1, int32_t count, int32_t os, int32_t frame, int32_t three) {
   hq_matmul_t2r_tile_ex(xout, xq, xs, wq, ws, n, r0, r1, count, os, frame, three, g_stream.load());
+}
+void matmul_b1r(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, int32_t n, int32_t r0,
+                int32_t r1, int32_t two) {
+  hq_matmul_b1r_ex(xout, xq, xs, wq, ws, n, r0, r1, two, g_stream.load());
+}
+void matmul_b1(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, int32_t n, int32_t r0,
+               int32_t r1, int32_t two) {
+  matmul(hq::B1, xout, xq, xs, wq, ws, nullptr, n, r0, r1, 1, 0, 0, two, g_stream.load());
+}
+void matmul_b1r_tile(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, int32_t n,
+                     int32_t r0, int32_t r1, int32_t count, int32_t os, int32_t frame, int32_t two) {
+  hq_matmul_b1r_tile_ex(xout, xq, xs, wq, ws, n, r0, r1, count, os, frame, two, g_stream.load());
+}
+// the reference's binary_x returns its refusal: this one waits for the library's stream to give it (a word of
+// device memory the library keeps for it, one a device); 1 also when the call fails (hq_last_error says why)
+int32_t binary_x(void *out, void *xs, const void *x, int32_t n) {
+  static std::mutex lock;
+  static int32_t *word[64];
+  std::lock_guard<std::mutex> hold(lock);
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    fail(HQ_ERR_DEVICE, "binary_x: no device");
+    return 1;
+  }
+  if (!word[dev] && hip_status(hipMalloc((void **)&word[dev], 4), "hipMalloc")) return 1;
+  const hipStream_t s = stream_of(g_stream.load());
+  if (hip_status(hipMemsetAsync(word[dev], 0, 4, s), "hipMemsetAsync")) return 1;
+  if (hq_binary_x_ex(out, xs, x, n, word[dev], s)) return 1;
+  int32_t bad = 1;
+  if (hip_status(hipMemcpyAsync(&bad, word[dev], 4, hipMemcpyDeviceToHost, s), "hipMemcpyAsync")) return 1;
+  if (hip_status(hipStreamSynchronize(s), "hipStreamSynchronize")) return 1;
+  return bad;
 }
 
 }  // extern "C"

@@ -416,8 +416,11 @@ struct alignas(16) StageT {
 };
 
 HQ_DEV int tswz(int r) { return (r >> 2) & 3; }
+// binary: a row's two 16-byte groups of a stage, swapped on every other 8 rows
+HQ_DEV int bswz(int r) { return (r >> 3) & 1; }
 
-// a block's loads of ternary stages: wave w's three loads a stage and their offsets
+// a block's loads of ternary (binary: BIN) stages: wave w's three loads a stage and their offsets
+template <bool BIN>
 struct Ternary {
   __amdgpu_buffer_rsrc_t rw, rx, rxs, rws;
   uint32_t oa, ob, oc;
@@ -427,7 +430,8 @@ struct Ternary {
   HQ_DEV Ternary(const Job &J, int row0, int tok0, int M, int w, char *junk_area) : wave(w), junk(junk_area) {
     const int lane = threadIdx.x & 63, groups = J.n >> 7;
     const int nsc = 4 * (J.n >> 5);  // the bytes of a token's scales: its sums follow them
-    rw = resource(J.wq + (int64_t)row0 * groups * 32, (int64_t)(J.r1 - row0) * groups * 32);
+    constexpr int GB = BIN ? 16 : 32;  // bytes of a group's codes
+    rw = resource(J.wq + (int64_t)row0 * groups * GB, (int64_t)(J.r1 - row0) * groups * GB);
     rws = resource(J.ws + (int64_t)row0 * groups * 2, (int64_t)(J.r1 - row0) * groups * 2);
     rx = resource(J.xq + tok0 * J.frame, (M - 1 - tok0) * J.frame + J.n);
     rxs = resource(J.xs + tok0 * J.sframe, (M - 1 - tok0) * J.sframe + 2 * nsc);
@@ -438,8 +442,13 @@ struct Ternary {
       oa = (uint32_t)(tok * J.frame + c * 16);
     }
     // load b: waves 0..7 the codes (rows 16 w .. + 15, lane l row 16 w + l / 4, slot l % 4 holding chunk
-    // (l % 4) ^ tswz(row) of the row's 64 bytes); waves 8..15 the tokens' scales of (group, part) w - 8
-    if (w < 8) {
+    // (l % 4) ^ tswz(row) of the row's 64 bytes; binary: waves 0..3, rows 32 w .. + 31, lane l row 32 w + l / 2,
+    // slot l % 2 holding group (l % 2) ^ bswz(row) of the row's 32 bytes, waves 4..7 into the scratch area); waves
+    // 8..15 the tokens' scales of (group, part) w - 8
+    if (w < 8 && BIN) {
+      const int row = 32 * (w & 3) + (lane >> 1), j = (lane & 1) ^ bswz(row);
+      ob = (uint32_t)(row * groups * 16 + j * 16);
+    } else if (w < 8) {
       const int row = 16 * w + (lane >> 2), j = (lane & 3) ^ tswz(row);
       ob = (uint32_t)(row * groups * 32 + (j >> 1) * 32 + (j & 1) * 16);
     } else {
@@ -458,7 +467,8 @@ struct Ternary {
   HQ_DEV void load(StageT &S, int s) {
     const int w = wave;
     dma16(rx, S.x + w * 1024, oa, s * TG * 128);
-    if (w < 8) dma16(rw, S.w + w * 1024, ob, s * TG * 32);
+    if (w < 8 && (!BIN || w < 4)) dma16(rw, S.w + w * 1024, ob, s * TG * (BIN ? 16 : 32));
+    else if (w < 8) dma16(rxs, junk, 0, 0);
     else dma4(rxs, &S.xs[w - 8][0], ob, s * TG * 16);
     if (w < 8) dma4(rxs, &S.sums[w][0], oc, s * TG * 16);
     else if (w < 12) dma2(rws, &S.d[(w - 8) >> 1][64 * ((w - 8) & 1)], oc, s * TG * 2);
@@ -481,14 +491,32 @@ HQ_DEV uint2 t_acts8(const StageT &S, int tok, int o) {
   return *(const uint2 *)(S.x + tok * 256 + (((o >> 4) ^ (tok & 15)) << 4) + (o & 8));
 }
 
+// binary's planes 2 kh, 2 kh + 1 of block h (bits 4 h + 2 kh and + 1 of every byte, doubled: kernels/binary.ts:19-22)
+HQ_DEV v4i bit_pair(uint32_t w0, uint32_t w1, int b) {
+  v4i r;
+  r[0] = (int32_t)(((w0 >> b) & 0x01010101u) << 1);
+  r[1] = (int32_t)(((w1 >> b) & 0x01010101u) << 1);
+  r[2] = (int32_t)(((w0 >> (b + 1)) & 0x01010101u) << 1);
+  r[3] = (int32_t)(((w1 >> (b + 1)) & 0x01010101u) << 1);
+  return r;
+}
+
 // part k of group gi of the stage for the lane's slice, both token halves: f(f(whole * xs) * d) into the part's
 // chain (relaxed/signs.ts:31)
+template <bool BIN>
 HQ_DEV void t_group(float acc0[16], float acc1[16], const StageT &S, int gi, int k, int slice, int lane) {
   const int h = k >> 1, s = k & 1, kh = lane >> 5, row = 32 * slice + (lane & 31);
-  // B: the row's codes of planes 2 kh, 2 kh + 1, bytes c = 8 s .. + 7 of block h (chunk 2 gi + h, half s)
-  const int j = 2 * gi + h;
-  const uint2 wv = *(const uint2 *)(S.w + row * 64 + ((j ^ tswz(row)) << 4) + 8 * s);
-  const v4i B = kh == 0 ? plane_pair<0>(wv.x, wv.y) : plane_pair<2>(wv.x, wv.y);
+  // B: the row's codes of planes 2 kh, 2 kh + 1, bytes c = 8 s .. + 7 of block h (ternary: chunk 2 gi + h, half s;
+  // binary: group gi's 16 bytes, half s, bits 4 h + 2 kh ..)
+  v4i B;
+  if (BIN) {
+    const uint2 wv = *(const uint2 *)(S.w + row * 32 + ((gi ^ bswz(row)) << 4) + 8 * s);
+    B = bit_pair(wv.x, wv.y, 4 * h + 2 * kh);
+  } else {
+    const int j = 2 * gi + h;
+    const uint2 wv = *(const uint2 *)(S.w + row * 64 + ((j ^ tswz(row)) << 4) + 8 * s);
+    B = kh == 0 ? plane_pair<0>(wv.x, wv.y) : plane_pair<2>(wv.x, wv.y);
+  }
   const float d = half_to_float(S.d[gi][row]);
   const int o = 128 * gi + 64 * h + 8 * s + 32 * kh;
 #pragma unroll
@@ -516,16 +544,18 @@ HQ_DEV void t_group(float acc0[16], float acc1[16], const StageT &S, int gi, int
   }
 }
 
-HQ_DEV void t_step(Ternary &L, const StageT &cur, StageT &next, int s, int stages, int groups, float acc0[16],
+template <bool BIN>
+HQ_DEV void t_step(Ternary<BIN> &L, const StageT &cur, StageT &next, int s, int stages, int groups, float acc0[16],
                    float acc1[16], int slice, int part, int lane) {
   if (s >= stages) return;
   wait_for<TLOADS>(s, stages);
   if (s + AHEAD < stages) L.load(next, s + AHEAD);
   // part `part` of groups 2 s and 2 s + 1 (relaxed/signs.ts:28-31)
-  t_group(acc0, acc1, cur, 0, part, slice, lane);
-  if (TG * s + 1 < groups) t_group(acc0, acc1, cur, 1, part, slice, lane);
+  t_group<BIN>(acc0, acc1, cur, 0, part, slice, lane);
+  if (TG * s + 1 < groups) t_group<BIN>(acc0, acc1, cur, 1, part, slice, lane);
 }
 
+template <bool BIN>
 __global__ __launch_bounds__(NT) void gemm_ternary(Job J) {
   __shared__ StageT b0, b1, b2, b3;
   __shared__ __attribute__((aligned(16))) char junk[1024];
@@ -542,16 +572,16 @@ __global__ __launch_bounds__(NT) void gemm_ternary(Job J) {
 #pragma unroll
   for (int r = 0; r < 16; r++) acc0[r] = acc1[r] = 0.0f;
 
-  Ternary L(J, row0, tok0, M, wave, junk);
+  Ternary<BIN> L(J, row0, tok0, M, wave, junk);
   const int stages = (groups + TG - 1) / TG;
   if (stages > 0) L.load(b0, 0);
   if (stages > 1) L.load(b1, 1);
   if (stages > 2) L.load(b2, 2);
   for (int s = 0; s < stages; s += RING) {
-    t_step(L, b0, b3, s, stages, groups, acc0, acc1, slice, part, lane);
-    t_step(L, b1, b0, s + 1, stages, groups, acc0, acc1, slice, part, lane);
-    t_step(L, b2, b1, s + 2, stages, groups, acc0, acc1, slice, part, lane);
-    t_step(L, b3, b2, s + 3, stages, groups, acc0, acc1, slice, part, lane);
+    t_step<BIN>(L, b0, b3, s, stages, groups, acc0, acc1, slice, part, lane);
+    t_step<BIN>(L, b1, b0, s + 1, stages, groups, acc0, acc1, slice, part, lane);
+    t_step<BIN>(L, b2, b1, s + 2, stages, groups, acc0, acc1, slice, part, lane);
+    t_step<BIN>(L, b3, b2, s + 3, stages, groups, acc0, acc1, slice, part, lane);
   }
   stage_ready<0>();
   add_chains(acc0, acc1, (float *)&b0, (float *)&b1, slice, part, lane);
@@ -576,12 +606,12 @@ __global__ __launch_bounds__(NT) void gemm_ternary(Job J) {
 
 }  // namespace
 
-bool gemm_supported(Kind kind) { return kind == Q8R || kind == Q6R || kind == T2R || kind == T2; }
+bool gemm_supported(Kind kind) { return kind == Q8R || kind == Q6R || signs_kind(kind); }
 
 hipError_t launch_gemm(Kind kind, const Job &job, hipStream_t s) {
   const int rows = job.r1 - job.r0;
   if (rows <= 0 || job.count <= 0) return hipSuccess;
-  dim3 grid(((rows + BR - 1) / BR) * ((job.count + BT - 1) / BT)), block(kind == T2R || kind == T2 ? NT : QNT);
+  dim3 grid(((rows + BR - 1) / BR) * ((job.count + BT - 1) / BT)), block(signs_kind(kind) ? NT : QNT);
   const bool wc = job.wc != nullptr;
   switch (kind) {
   case Q8R:
@@ -593,7 +623,9 @@ hipError_t launch_gemm(Kind kind, const Job &job, hipStream_t s) {
     else hipLaunchKernelGGL((gemm_relaxed<6, false>), grid, block, 0, s, job);
     break;
   case T2R:
-  case T2: hipLaunchKernelGGL(gemm_ternary, grid, block, 0, s, job); break;
+  case T2: hipLaunchKernelGGL(gemm_ternary<false>, grid, block, 0, s, job); break;
+  case B1R:
+  case B1: hipLaunchKernelGGL(gemm_ternary<true>, grid, block, 0, s, job); break;
   default: return hipErrorNotSupported;
   }
   return hipGetLastError();

@@ -3,6 +3,8 @@
 //                              2..4 tokens, relaxed/int8.ts:52-166)
 //   matmul_q8 / matmul_q6     (kernels/kernel/matmul.ts:77-104, 227-244)
 //   matmul_t2r / matmul_t2    (kernels/relaxed/signs.ts:35-55, 117-119, kernel/matmul.ts:196-220; the same numbers)
+//   matmul_b1r / matmul_b1    (relaxed/signs.ts:123-125, kernel/matmul.ts:222-224: the ternary kernels on binary
+//                              weights, kernels/binary.ts; ternary's numbers for the same signs)
 //
 // Layout: a row is 16 lanes (ternary: 8, 16 or 32 by the row's length), a wave 4 rows; a block is 2 waves (8 rows)
 // for the relaxed kinds, 4 waves for the others.  Lane l of a row of L lanes takes the groups L i + l (i = 0, 1,
@@ -447,13 +449,16 @@ __global__ __launch_bounds__(256) void gemv_plain(GemvBatch batch) {
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// ternary (matmul_t2r == matmul_t2)
+// ternary (matmul_t2r == matmul_t2) and binary (matmul_b1r == matmul_b1)
 // ---------------------------------------------------------------------------------------------------------------
 // A group of 128 weights is 32 bytes: block h (bytes 16h..16h+15) holds the codes of weights 64h + 4c + p in byte c,
 // bits 2p.  The activations are interleave()'s: byte 16p + c of block (2g + h) is activation 4c + p of it.  Part k
 // (the reference's lane k: activations 32k..32k+31 of the group) is block h = k / 2, c in 8 (k % 2) .. + 7: weight
 // dwords 4h + 2(k%2) + {0,1} and, for every plane p, activation dwords 4p + 2(k%2) + {0,1} of the block.  Its
-// integer is sum(code * a) + (minus the sum of its 32 activations) = sum((code - 1) a) exactly (ternary.ts:37-43).
+// integer is sum(code * a) + (minus the sum of its 32 activations) = sum((code - 1) a) exactly (ternary.ts:6-12).
+// Binary (BIN, kernels/binary.ts): a group is 16 bytes, weight 64h + 4c + p at bit 4h + p of byte c, its code twice
+// the bit (0 or 2: the weight + 1 again), so part k takes dwords 2(k%2) + {0,1} for both blocks and plane p of block
+// h is ((dword >> (4h + p)) & 0x01010101) << 1 (binary.ts:19-22); everything after the codes is ternary's.
 //
 // A lane reads 32 bytes of codes a group but 128 bytes of activations (and 32 of their scales and sums): the block
 // copies the activations of its T tokens into LDS once (STAGE), so that only the codes stream from memory, U steps
@@ -478,7 +483,14 @@ struct TernaryActs {
   HQ_DEV const char *area(int t) const { return STAGE ? lds + t * ternary_token_bytes(n) + (n >> 7) * kTernaryPitch : xs[t]; }
 };
 
-template <int T, bool STAGE, int L>
+// plane p of block h of a group's dword of codes: ternary's 2-bit codes, or binary's bit 4h + p doubled
+template <bool BIN, int H, int P>
+HQ_DEV uint32_t plane_codes(uint32_t w) {
+  if (BIN) return ((w >> (4 * H + P)) & 0x01010101u) << 1;
+  return codes<P>(w);
+}
+
+template <int T, bool STAGE, int L, bool BIN>
 HQ_DEV void ternary_step(FoldL<T, L> &f, const TernaryActs<T, STAGE> &A, const uint32_t w[8], float d, int g,
                          bool valid, int buf, int slot, int lane, float acc[T]) {
 #pragma unroll
@@ -499,16 +511,28 @@ HQ_DEV void ternary_step(FoldL<T, L> &f, const TernaryActs<T, STAGE> &A, const u
       }
 #pragma unroll
       for (int s = 0; s < 2; s++) {
-        const uint32_t w0 = w[4 * h + 2 * s], w1 = w[4 * h + 2 * s + 1];
+        const int wi = BIN ? 2 * s : 4 * h + 2 * s;
+        const uint32_t w0 = w[wi], w1 = w[wi + 1];
         int32_t dot = sums[2 * h + s];
-        dot = sdot4((int32_t)codes<0>(w0), (int32_t)a[0 + 2 * s], dot);
-        dot = sdot4((int32_t)codes<0>(w1), (int32_t)a[1 + 2 * s], dot);
-        dot = sdot4((int32_t)codes<1>(w0), (int32_t)a[4 + 2 * s], dot);
-        dot = sdot4((int32_t)codes<1>(w1), (int32_t)a[5 + 2 * s], dot);
-        dot = sdot4((int32_t)codes<2>(w0), (int32_t)a[8 + 2 * s], dot);
-        dot = sdot4((int32_t)codes<2>(w1), (int32_t)a[9 + 2 * s], dot);
-        dot = sdot4((int32_t)codes<3>(w0), (int32_t)a[12 + 2 * s], dot);
-        dot = sdot4((int32_t)codes<3>(w1), (int32_t)a[13 + 2 * s], dot);
+        if (h == 0) {
+          dot = sdot4((int32_t)plane_codes<BIN, 0, 0>(w0), (int32_t)a[0 + 2 * s], dot);
+          dot = sdot4((int32_t)plane_codes<BIN, 0, 0>(w1), (int32_t)a[1 + 2 * s], dot);
+          dot = sdot4((int32_t)plane_codes<BIN, 0, 1>(w0), (int32_t)a[4 + 2 * s], dot);
+          dot = sdot4((int32_t)plane_codes<BIN, 0, 1>(w1), (int32_t)a[5 + 2 * s], dot);
+          dot = sdot4((int32_t)plane_codes<BIN, 0, 2>(w0), (int32_t)a[8 + 2 * s], dot);
+          dot = sdot4((int32_t)plane_codes<BIN, 0, 2>(w1), (int32_t)a[9 + 2 * s], dot);
+          dot = sdot4((int32_t)plane_codes<BIN, 0, 3>(w0), (int32_t)a[12 + 2 * s], dot);
+          dot = sdot4((int32_t)plane_codes<BIN, 0, 3>(w1), (int32_t)a[13 + 2 * s], dot);
+        } else {
+          dot = sdot4((int32_t)plane_codes<BIN, 1, 0>(w0), (int32_t)a[0 + 2 * s], dot);
+          dot = sdot4((int32_t)plane_codes<BIN, 1, 0>(w1), (int32_t)a[1 + 2 * s], dot);
+          dot = sdot4((int32_t)plane_codes<BIN, 1, 1>(w0), (int32_t)a[4 + 2 * s], dot);
+          dot = sdot4((int32_t)plane_codes<BIN, 1, 1>(w1), (int32_t)a[5 + 2 * s], dot);
+          dot = sdot4((int32_t)plane_codes<BIN, 1, 2>(w0), (int32_t)a[8 + 2 * s], dot);
+          dot = sdot4((int32_t)plane_codes<BIN, 1, 2>(w1), (int32_t)a[9 + 2 * s], dot);
+          dot = sdot4((int32_t)plane_codes<BIN, 1, 3>(w0), (int32_t)a[12 + 2 * s], dot);
+          dot = sdot4((int32_t)plane_codes<BIN, 1, 3>(w1), (int32_t)a[13 + 2 * s], dot);
+        }
         const int k = 2 * h + s;
         // f(f(whole * xs) * d) (relaxed/signs.ts:31)
         f.v[buf][slot][t][k][lane] = valid ? fmul(fmul((float)dot, scale[k]), d) : 0.0f;
@@ -518,8 +542,9 @@ HQ_DEV void ternary_step(FoldL<T, L> &f, const TernaryActs<T, STAGE> &A, const u
   fold_step_l<T, L>(f, buf, slot, lane, acc);
 }
 
-// the codes and group scales of U steps of a lane (step it: group L it + lane; past the row's groups, group 0)
-template <int L>
+// the codes and group scales of U steps of a lane (step it: group L it + lane; past the row's groups, group 0):
+// 32 bytes a group (ternary) or 16 (binary, in w[u][0..3])
+template <int L, bool BIN>
 struct TernaryChunk {
   uint32_t w[kTernarySteps][8];
   uint32_t h[kTernarySteps];
@@ -528,9 +553,14 @@ struct TernaryChunk {
     for (int u = 0; u < kTernarySteps; u++) {
       const int g = (it0 + u) * L + lane;
       const int gl = g < groups ? g : 0;
-      const uint4 a = ldw16(wrow + gl * 32), b = ldw16(wrow + gl * 32 + 16);
-      w[u][0] = a.x; w[u][1] = a.y; w[u][2] = a.z; w[u][3] = a.w;
-      w[u][4] = b.x; w[u][5] = b.y; w[u][6] = b.z; w[u][7] = b.w;
+      if (BIN) {
+        const uint4 a = ldw16(wrow + gl * 16);
+        w[u][0] = a.x; w[u][1] = a.y; w[u][2] = a.z; w[u][3] = a.w;
+      } else {
+        const uint4 a = ldw16(wrow + gl * 32), b = ldw16(wrow + gl * 32 + 16);
+        w[u][0] = a.x; w[u][1] = a.y; w[u][2] = a.z; w[u][3] = a.w;
+        w[u][4] = b.x; w[u][5] = b.y; w[u][6] = b.z; w[u][7] = b.w;
+      }
       h[u] = srow[gl];
     }
   }
@@ -543,14 +573,14 @@ struct TernaryChunk {
       if (it < steps) {  // uniform in the wave
         const int g = it * L + lane;
         const bool valid = g < groups;
-        ternary_step<T, STAGE, L>(f, A, w[u], half_to_float(h[u]), valid ? g : 0, valid, it & 1, slot, lane, acc);
+        ternary_step<T, STAGE, L, BIN>(f, A, w[u], half_to_float(h[u]), valid ? g : 0, valid, it & 1, slot, lane, acc);
       }
     }
   }
 };
 
 // rows of L lanes (16: 16 rows a block; 32 for long rows: twice the waves on the same rows)
-template <int T, bool STAGE, int L>
+template <int T, bool STAGE, int L, bool BIN>
 __global__ __launch_bounds__(256) void gemv_ternary(GemvBatch batch) {
   extern __shared__ __align__(16) char acts[];
   __shared__ FoldL<T, L> fold[4];
@@ -562,7 +592,7 @@ __global__ __launch_bounds__(256) void gemv_ternary(GemvBatch batch) {
   const bool live = row_u < J.r1;
   const int row = live ? row_u : J.r1 - 1;
   const int groups = J.n >> 7;
-  const char *wrow = J.wq + (int64_t)row * groups * 32;
+  const char *wrow = J.wq + (int64_t)row * groups * (BIN ? 16 : 32);
   const uint16_t *srow = (const uint16_t *)J.ws + (int64_t)row * groups;
   FoldL<T, L> &f = fold[wave];
   TernaryActs<T, STAGE> A;
@@ -578,7 +608,7 @@ __global__ __launch_bounds__(256) void gemv_ternary(GemvBatch batch) {
 #pragma unroll
   for (int t = 0; t < T; t++) acc[t] = 0.0f;
   const int steps = (groups + L - 1) / L;
-  TernaryChunk<L> a, b;
+  TernaryChunk<L, BIN> a, b;
   if (steps > 0) a.load(wrow, srow, 0, lane, groups);  // the first codes in flight during the staging
   if (STAGE) {
     // every token's n bytes (a group's 128 in 144), then its n/32 scales and n/32 sums: 16 bytes a thread at a time,
@@ -633,11 +663,8 @@ constexpr size_t kTernaryStageMax = HQ_TERNARY_STAGE_MAX;
 #ifndef HQ_TERNARY_L8
 #define HQ_TERNARY_L8 1
 #endif
-#ifndef HQ_TERNARY_LONG64
-#define HQ_TERNARY_LONG64 1000000000
-#endif
 HQ_HOST_DEV constexpr int ternary_lanes(int n) {
-  return n >= HQ_TERNARY_LONG64 ? 64 : n >= HQ_TERNARY_LONG ? 32
+  return n >= HQ_TERNARY_LONG ? 32
        : (HQ_TERNARY_L8 && (n >> 7) % 16 != 0 && (n >> 7) % 8 == 0) ? 8 : 16;
 }
 HQ_HOST_DEV constexpr size_t ternary_stage_bytes(int T, int n) { return (size_t)T * ternary_token_bytes(n); }
@@ -667,6 +694,30 @@ hipError_t launch_relaxed(const GemvBatch &b, int tiles, bool wc, size_t lds, hi
   return hipGetLastError();
 }
 
+// ternary / binary: rows of ternary_lanes(n) lanes, the activations staged in LDS when they fit
+template <int T, bool BIN>
+hipError_t launch_signs(const GemvBatch &b, int blocks, hipStream_t s) {
+  int nmax = 0;
+  for (int j = 0; j < b.njobs; j++) nmax = b.job[j].n > nmax ? b.job[j].n : nmax;
+  const size_t bytes = ternary_stage_bytes(T, nmax);
+  const bool stage = bytes <= kTernaryStageMax;
+  dim3 grid(blocks), block(256);
+  switch (ternary_lanes(nmax)) {
+  case 32:
+    if (stage) hipLaunchKernelGGL((gemv_ternary<T, true, 32, BIN>), grid, block, bytes, s, b);
+    else hipLaunchKernelGGL((gemv_ternary<T, false, 32, BIN>), grid, block, 0, s, b);
+    break;
+  case 8:
+    if (stage) hipLaunchKernelGGL((gemv_ternary<T, true, 8, BIN>), grid, block, bytes, s, b);
+    else hipLaunchKernelGGL((gemv_ternary<T, false, 8, BIN>), grid, block, 0, s, b);
+    break;
+  default:
+    if (stage) hipLaunchKernelGGL((gemv_ternary<T, true, 16, BIN>), grid, block, bytes, s, b);
+    else hipLaunchKernelGGL((gemv_ternary<T, false, 16, BIN>), grid, block, 0, s, b);
+  }
+  return hipGetLastError();
+}
+
 template <int T>
 hipError_t launch_t(Kind kind, const GemvBatch &b, int blocks, bool wc, int src, size_t lds, hipStream_t s) {
   dim3 grid(blocks), block(256);
@@ -684,26 +735,9 @@ hipError_t launch_t(Kind kind, const GemvBatch &b, int blocks, bool wc, int src,
   case Q8: hipLaunchKernelGGL((gemv_plain<8, T>), grid, block, 0, s, b); break;
   case Q6: hipLaunchKernelGGL((gemv_plain<6, T>), grid, block, 0, s, b); break;
   case T2R:
-  case T2: {
-    int nmax = 0;
-    for (int j = 0; j < b.njobs; j++) nmax = b.job[j].n > nmax ? b.job[j].n : nmax;
-    const size_t bytes = ternary_stage_bytes(T, nmax);
-    const bool stage = bytes <= kTernaryStageMax;
-    if (ternary_lanes(nmax) == 32) {
-      if (stage) hipLaunchKernelGGL((gemv_ternary<T, true, 32>), grid, block, bytes, s, b);
-      else hipLaunchKernelGGL((gemv_ternary<T, false, 32>), grid, block, 0, s, b);
-    } else if (ternary_lanes(nmax) == 64) {
-      if (stage) hipLaunchKernelGGL((gemv_ternary<T, true, 64>), grid, block, bytes, s, b);
-      else hipLaunchKernelGGL((gemv_ternary<T, false, 64>), grid, block, 0, s, b);
-    } else if (ternary_lanes(nmax) == 8) {
-      if (stage) hipLaunchKernelGGL((gemv_ternary<T, true, 8>), grid, block, bytes, s, b);
-      else hipLaunchKernelGGL((gemv_ternary<T, false, 8>), grid, block, 0, s, b);
-    } else {
-      if (stage) hipLaunchKernelGGL((gemv_ternary<T, true, 16>), grid, block, bytes, s, b);
-      else hipLaunchKernelGGL((gemv_ternary<T, false, 16>), grid, block, 0, s, b);
-    }
-    break;
-  }
+  case T2: return launch_signs<T, false>(b, blocks, s);
+  case B1R:
+  case B1: return launch_signs<T, true>(b, blocks, s);
   default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -724,7 +758,7 @@ hipError_t launch_batch(Kind kind, const Job *jobs, int32_t njobs, const char *x
   GemvBatch b{};
   int blocks = 0, nmax = 0;
   for (int j = 0; j < njobs; j++) nmax = jobs[j].n > nmax ? jobs[j].n : nmax;
-  const int rpb = (kind == T2R || kind == T2) ? 256 / ternary_lanes(nmax) : rows_per_block(kind);
+  const int rpb = signs_kind(kind) ? 256 / ternary_lanes(nmax) : rows_per_block(kind);
   for (int j = 0; j < njobs; j++) {
     b.job[j] = jobs[j];
     b.block0[j] = blocks;

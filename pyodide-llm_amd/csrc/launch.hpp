@@ -15,7 +15,11 @@ struct Job {
   int64_t os, frame, sframe;
 };
 
-enum Kind : int32_t { Q8R = 0, Q8 = 1, Q6R = 5, Q6 = 6, T2R = 8, T2 = 9 };
+// a kind's number is its place in the reference's WORK (src/runtime/jobs.ts:207-336)
+enum Kind : int32_t { Q8R = 0, Q8 = 1, Q6R = 5, Q6 = 6, T2R = 8, T2 = 9, B1R = 13, B1 = 14 };
+// the kinds whose weights are signs and a float16 scale a group of 128 (ternary, binary): interleave()'s activations
+constexpr bool signs_kind(Kind k) { return k == T2R || k == T2 || k == B1R || k == B1; }
+constexpr bool binary_kind(Kind k) { return k == B1R || k == B1; }
 
 // activations: count tokens of n values (x + t x_stride) -> xq + t frame, xs + t frame
 hipError_t launch_quantize_x(char *xq, char *xs, const char *x, int32_t n, int32_t bias, int32_t count,
@@ -23,6 +27,9 @@ hipError_t launch_quantize_x(char *xq, char *xs, const char *x, int32_t n, int32
 hipError_t launch_interleave(char *xq, char *xs, int32_t n, int32_t count, int64_t frame, hipStream_t s);
 hipError_t launch_int8_sums(int32_t *out, const char *w, int32_t groups, hipStream_t s);
 hipError_t launch_six_sums(int32_t *out, const char *w, int32_t groups, hipStream_t s);
+// binary weights from float32: groups of 128 -> 16 bytes and the largest |value| each; *bad = 1 (bad: NULL or a word
+// the caller cleared) where a value is not plus or minus its group's largest
+hipError_t launch_binary_x(uint8_t *out, float *xs, const float *x, int32_t groups, int32_t *bad, hipStream_t s);
 
 // GEMV-shaped products (every job of one kind and one token count, 1..4; up to kMaxJobs jobs a launch)
 constexpr int kMaxJobs = 8;

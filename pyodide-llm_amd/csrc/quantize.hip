@@ -1,6 +1,6 @@
 // quantize.hip — the activations' preparation and the weights' corrections:
 //   quantize_x (kernels/kernel/quantize.ts:124-151), interleave (kernels/kernel/matmul.ts:107-146),
-//   int8_sums (matmul.ts:50-58), six_sums (matmul.ts:38-46).
+//   int8_sums (matmul.ts:50-58), six_sums (matmul.ts:38-46), binary_x (quantize.ts:184-247: a converter's, at load).
 // Byte-for-byte the reference's outputs; small, latency-bound kernels (a token's activations are a few KB).
 #include "common.hpp"
 #include "launch.hpp"
@@ -128,6 +128,45 @@ __global__ __launch_bounds__(256) void six_sums_kernel(int32_t *out, const char 
 #pragma unroll
   for (int i = 0; i < 8; i++) s = sdot4((int32_t)v[i], 0x01010101, s);
   out[g] = -64 * s;
+}
+
+// binary_x: a group of 128 values a 16-lane row, lane c its byte c: values 4c..4c+3 (bits 0..3) and 64+4c.. (bits
+// 4..7), a bit set where the value is not below 0 (v128.not of f32x4.lt: -0 and NaN too).  The scale is groupLargest's
+// (quantize.ts:186-191): the largest |value|, NaN where there is one (a non-negative float's bits order as the float
+// does and every NaN's are above +inf's, so the largest bits are the result; which NaN is the engine's choice in
+// WebAssembly too).  A value that is not plus or minus it (a NaN never is) makes *bad 1.
+__global__ __launch_bounds__(256) void binary_x_kernel(uint8_t *out, float *xs, const float *x, int32_t groups,
+                                                       int32_t *bad) {
+  const int64_t g = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int c = threadIdx.x & 15;
+  const bool live = g < groups;
+  const int64_t gg = live ? g : 0;
+  const float4 lo = ((const float4 *)(x + gg * 128))[c], hi = ((const float4 *)(x + gg * 128 + 64))[c];
+  const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+  uint32_t m = 0;
+#pragma unroll
+  for (int i = 0; i < 8; i++) m = max(m, __float_as_uint(v[i]) & 0x7fffffffu);
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, o, 16));
+  const float scale = __uint_as_float(m);
+  uint32_t byte = 0;
+  bool refused = false;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    byte |= (uint32_t)(!(v[i] < 0.0f)) << i;
+    refused |= !(fabsf(v[i]) == scale);
+  }
+  if (live) {
+    out[gg * 16 + c] = (uint8_t)byte;
+    if (c == 0) xs[gg] = scale;
+    if (refused && bad) *bad = 1;
+  }
+}
+
+hipError_t launch_binary_x(uint8_t *out, float *xs, const float *x, int32_t groups, int32_t *bad, hipStream_t s) {
+  if (groups <= 0) return hipSuccess;
+  hipLaunchKernelGGL(binary_x_kernel, dim3((groups + 15) / 16), dim3(256), 0, s, out, xs, x, groups, bad);
+  return hipGetLastError();
 }
 
 hipError_t launch_int8_sums(int32_t *out, const char *w, int32_t groups, hipStream_t s) {

@@ -25,10 +25,13 @@ RUN = {
     "matmul_q6": dict(relaxed=False, tile=False, row_bytes=lambda n: n * 3 // 4),
     "matmul_t2r": dict(relaxed=True, tile=True, row_bytes=lambda n: n // 4),
     "matmul_t2": dict(relaxed=False, tile=False, row_bytes=lambda n: n // 4),
+    "matmul_b1r": dict(relaxed=True, tile=True, row_bytes=lambda n: n // 8),
+    "matmul_b1": dict(relaxed=False, tile=False, row_bytes=lambda n: n // 8),
 }
 JOB = 16            # numbers a job in the reference's table (jobs.ts:21)
 ROWS, COUNT = 9, 10  # jobs.ts:46
 THREE = 3           # jobs.ts:50
+TWO = 2             # jobs.ts:52
 
 
 @dataclass(frozen=True)
@@ -59,6 +62,7 @@ PACKED = {
     "int8": Packing("int8", 32, 4, "matmul_q8r", "matmul_q8", "int8_sums", "biased", 4),
     "int6": Packing("int6", 32, 4, "matmul_q6r", "matmul_q6", "six_sums", "biased", 4),
     "ternary": Packing("ternary", 128, 2, "matmul_t2r", "matmul_t2", "", "interleaved", 8),
+    "binary": Packing("binary", 128, 2, "matmul_b1r", "matmul_b1", "", "interleaved", 8),
 }
 
 

@@ -49,3 +49,17 @@ def uninterleave_index(n):
     (at & ~63) + 4 (at & 15) + ((at >> 4) & 3)."""
     at = np.arange(n)
     return (at & ~63) + 4 * (at & 15) + ((at >> 4) & 3)
+
+
+def pack_binary(bits, n):
+    """kernels/binary.ts:1-4 (the layout of packing.py's pack_binary), as tests/ternary-check.ts:303-305 writes it:
+    bit i of a row (1 for +1) at byte (group) 16 + ((i >> 2) & 15), bit ((i >> 6) & 1) * 4 + (i & 3)."""
+    b = np.asarray(bits, np.uint8).reshape(-1, n)
+    rows = b.shape[0]
+    out = np.zeros((rows, n // 8), np.uint8)
+    i = np.arange(n)
+    at = ((i >> 7) << 4) + ((i >> 2) & 15)
+    shift = (((i >> 6) & 1) << 2) | (i & 3)
+    for r in range(rows):
+        np.bitwise_or.at(out[r], at, (b[r] << shift).astype(np.uint8))
+    return out.reshape(-1)

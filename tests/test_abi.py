@@ -35,7 +35,7 @@ def test_reference_names_and_arities(pkg):
     names = declared()
     reference = {"quantize_x": 5, "int8_sums": 3, "six_sums": 3, "interleave": 3, "matmul_q8r": 9, "matmul_q8": 8,
                  "matmul_q8r_tile": 12, "matmul_q6r": 9, "matmul_q6": 8, "matmul_t2r": 9, "matmul_t2": 9,
-                 "matmul_t2r_tile": 12}
+                 "matmul_t2r_tile": 12, "matmul_b1r": 9, "matmul_b1": 9, "matmul_b1r_tile": 12, "binary_x": 4}
     for name, arity in reference.items():
         assert names[name] == arity, name
         assert len(pkg.REFERENCE_SIGNATURES[name]) == arity, name
@@ -53,6 +53,11 @@ def test_version(pkg):
     (lambda L: L.hq_matmul_q8r_ex(None, None, None, None, None, None, 64, 0, 2, None), 3, "NULL"),
     (lambda L: L.hq_matmul_t2r_ex(16, 16, 16, 16, 16, 128, 0, 1, 2, None), 1, "three"),
     (lambda L: L.hq_matmul_t2r_ex(16, 16, 16, 16, 16, 96, 0, 1, 3, None), 1, "multiple of 128"),
+    (lambda L: L.hq_matmul_b1r_ex(16, 16, 16, 16, 16, 128, 0, 1, 3, None), 1, "two = 3, not 2"),
+    (lambda L: L.hq_matmul_b1r_ex(16, 16, 16, 16, 16, 192, 0, 1, 2, None), 1, "multiple of 128"),
+    (lambda L: L.hq_matmul_b1r_tile_ex(16, 16, 16, 16, 16, 128, 0, 1, 2, 4, 8, 2, None), 2, "frame"),
+    (lambda L: L.hq_binary_x_ex(16, 16, 16, 100, None, None), 1, "multiple of 128"),
+    (lambda L: L.hq_binary_x_ex(16, 16, 8, 128, None, None), 2, "aligned"),
     (lambda L: L.hq_matmul_q8_ex(16, 17, 16, 16, 16, 64, 0, 1, None), 2, "xq"),
     (lambda L: L.hq_matmul_q6_ex(16, 16, 16, 12, 16, 64, 0, 1, None), 2, "wq"),
     (lambda L: L.hq_matmul_q8r_tile_ex(16, 16, 16, 16, 16, 16, 64, 0, 1, 3, 4, 8, None), 2, "frame"),
@@ -98,14 +103,17 @@ def test_phase_refuses_other_kinds_and_bad_numbers(pkg):
     assert jobs.phase(L, [bad]) == pkg.HQ_ERR_ARGUMENT
     odd = jobs.job("matmul_t2r", 16, 16, 16, 16, 16, 0, 100, rows=4)
     assert jobs.phase(L, [odd]) == pkg.HQ_ERR_ARGUMENT
+    odd = jobs.job("matmul_b1", 16, 16, 16, 16, 16, 0, 64, rows=4)
+    assert jobs.phase(L, [odd]) == pkg.HQ_ERR_ARGUMENT
     assert jobs.phase(L, []) == 0
 
 
 def test_work_numbers_match_the_reference():
-    """KIND is each kind's place in jobs.ts's WORK (jobs.ts:207-336); hq.h names 0, 1, 5, 6, 8, 9."""
+    """KIND is each kind's place in jobs.ts's WORK (jobs.ts:207-336); hq.h names 0, 1, 5, 6, 8, 9, 13, 14."""
     from pyodide_llm_amd import jobs
-    assert [jobs.KIND[k] for k in ("matmul_q8r", "matmul_q8", "matmul_q6r", "matmul_q6", "matmul_t2r", "matmul_t2")] \
-        == [0, 1, 5, 6, 8, 9]
+    assert [jobs.KIND[k] for k in ("matmul_q8r", "matmul_q8", "matmul_q6r", "matmul_q6", "matmul_t2r", "matmul_t2",
+                                   "matmul_b1r", "matmul_b1")] == [0, 1, 5, 6, 8, 9, 13, 14]
     assert jobs.PACKED["int8"].weight_bytes() == 1.125
     assert jobs.PACKED["int6"].weight_bytes() == 0.875
     assert jobs.PACKED["ternary"].weight_bytes() == 0.265625
+    assert jobs.PACKED["binary"].weight_bytes() == 0.140625  # (16 + 2) / 128

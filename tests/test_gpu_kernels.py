@@ -12,7 +12,7 @@ import pytest
 import models
 from gpu_util import Arena, first_difference, same_bits
 from models import F
-from streams import LCG, pack6, pack_ternary, scale_rule
+from streams import LCG, pack6, pack_binary, pack_ternary, scale_rule
 from test_oracle import quantize_cases
 
 pytestmark = pytest.mark.gpu
@@ -424,6 +424,123 @@ def test_t2r_tile(k, arena, oracle, count, groups):
             want[r0:r1] = full[r0:r1]
             assert same_bits(got[t], want), f"count {count} groups {groups} rows {r0}..{r1} token {t}: " \
                                             f"{first_difference(got[t], want)}"
+
+
+# ---- binary: the ternary kernels on one bit a weight ----------------------------------------------------------
+def binary_case(groups, rows=ROWS, seed=634):
+    """tests/ternary-check.ts:292-305: signs (row 0 all +1, row 1 all -1), written both ways, the scales of
+    ternary_case"""
+    n, _, halves, rng = ternary_case(groups, rows, seed)
+    bits = np.array([rng.next() & 1 for _ in range(rows * n)], np.uint8)
+    bits[:n], bits[n:2 * n] = 1, 0
+    return n, bits, pack_binary(bits, n), halves, rng
+
+
+@pytest.mark.parametrize("groups", [1, 2, 3, 4, 5, 7, 9, 24, 40, 72, 136])
+@pytest.mark.parametrize("name", ["matmul_b1r", "matmul_b1"])
+def test_binary_token(k, arena, oracle, groups, name):
+    """Every row length class of the token kernel (rows of 8, 16 and 32 lanes), bit for bit the oracle's binary kernel
+    and the ternary kernel's on the same signs"""
+    n, bits, bw, halves, rng = binary_case(groups)
+    wq, wsa = arena.put(bw), arena.put(halves)
+    for t in range(3):
+        pat = np.where(np.arange(n) & 1, 127, -128).astype(np.int8) if t == 0 else (
+            np.full(n, -128, np.int8) if t == 1 else None)
+        xq_b, area = ternary_acts(rng, oracle, n, pat)
+        xq, xs = arena.put(xq_b), arena.put(area)
+        full = oracle.matmul_b1r(xq_b, area, bw, halves, n)
+        assert same_bits(full, oracle.matmul_t2r(xq_b, area, pack_ternary(2 * bits), halves, n))
+        for r0, r1 in [(0, ROWS), (0, 1), (ROWS - 1, ROWS), (3, 8), (5, 5)]:
+            out = arena.alloc(4 * (ROWS + 1), fill=np.full(ROWS + 1, -7, F))
+            getattr(k, name)(out, xq, xs, wq, wsa, n, r0, r1, 2)
+            got = arena.get(out, F, ROWS + 1)
+            want = expect_range(full, r0, r1)
+            assert same_bits(got, want), f"{name} groups {groups} token {t} rows {r0}..{r1}: {first_difference(got, want)}"
+
+
+@pytest.mark.parametrize("count,groups", [(c, g) for c in [1, 2, 3, 4, 5, 7, 8, 9, 16, 17, 64, 65, 100]
+                                          for g in [1, 3, 9]] + [(4, 136), (3, 136), (2, 40), (33, 136)])
+def test_b1r_tile(k, arena, oracle, count, groups):
+    """every count of tokens (the token kernel up to 4 at a time, the MFMA tiles from 16), rows cut anywhere"""
+    rows = 70
+    n, bits, bw, halves, rng = binary_case(groups, rows=rows, seed=700 + count)
+    wq, wsa = arena.put(bw), arena.put(halves)
+    frame = ((n + 8 * (n // 32) + 15) // 16) * 16
+    buf = np.zeros((count, frame), np.uint8)
+    acts = []
+    for t in range(count):
+        xq_b, area = ternary_acts(rng, oracle, n)
+        buf[t, :n] = xq_b.view(np.uint8)
+        buf[t, n:n + area.nbytes] = area.view(np.uint8)
+        acts.append((xq_b, area))
+    xq = arena.put(buf)
+    os_ = 4 * (rows + 5)
+    for r0, r1 in [(0, rows), (2, 9), (rows - 1, rows), (3, 67)]:
+        out = arena.alloc(os_ * count, fill=np.full(os_ * count // 4, -7, F))
+        k.matmul_b1r_tile(out, xq, xq + n, wq, wsa, n, r0, r1, count, os_, frame, 2)
+        got = arena.get(out, F, os_ * count // 4).reshape(count, -1)
+        for t in range(count):
+            full = oracle.matmul_b1r(acts[t][0], acts[t][1], bw, halves, n)
+            want = np.full(os_ // 4, F(-7), F)
+            want[r0:r1] = full[r0:r1]
+            assert same_bits(got[t], want), f"count {count} groups {groups} rows {r0}..{r1} token {t}: " \
+                                            f"{first_difference(got[t], want)}"
+
+
+def test_binary_phase_and_matmuls(pkg, arena, oracle):
+    """binary jobs (kinds 13 and 14) in hq_phase beside ternary ones, and through hq_matmuls (quantize_x at bias 0 and
+    interleave, then the phase)"""
+    from pyodide_llm_amd import jobs
+    rng = np.random.default_rng(13)
+    groups, rows, tokens = 5, 45, 3
+    n = 128 * groups
+    bits = rng.integers(0, 2, rows * n).astype(np.uint8)
+    bw, tw = pack_binary(bits, n), pack_ternary(2 * bits)
+    halves = (rng.random(rows * groups) * 0.01).astype(np.float16).view(np.uint16)
+    x = rng.standard_normal((tokens, n)).astype(F)
+    frame = 2 * n
+    sq = arena.alloc(tokens * frame)
+    outs = {name: arena.alloc(4 * rows * tokens, fill=np.full(rows * tokens, -7, F))
+            for name in ("matmul_b1r", "matmul_b1", "matmul_t2r")}
+    wqs = {"matmul_b1r": arena.put(bw), "matmul_b1": arena.put(bw), "matmul_t2r": arena.put(tw)}
+    wsa = arena.put(halves)
+    table = [jobs.job(name, outs[name], sq, sq + n, wqs[name], wsa, 0, n, rows=rows, count=tokens, os=4 * rows,
+                      as_=frame, bs=frame) for name in outs]
+    L = pkg.library()
+    assert jobs.matmuls(L, arena.put(x), 4 * n, table) == 0, L.hq_last_error_message()
+    for t in range(tokens):
+        q, s = oracle.quantize_x(x[t], 0)
+        xi, area = oracle.interleave(q.view(np.int8), s)
+        want = oracle.matmul_b1r(xi, area, bw, halves, n)
+        for name in outs:
+            got = arena.get(outs[name] + 4 * rows * t, F, rows)
+            assert same_bits(got, want), f"{name} token {t}: {first_difference(got, want)}"
+
+
+def test_binary_x(pkg, k, arena, oracle):
+    """kernels/kernel/quantize.ts:232-247 on the GPU: the oracle's bytes and scales, and the refusal (the drop-in's
+    return value, and the _ex form's device word)"""
+    import test_oracle
+    rng = np.random.default_rng(6340)
+    L = pkg.library()
+    for case in range(4):
+        x = test_oracle.binary_x_case(rng, groups=40 + 200 * case)
+        if case == 2:
+            x[128 * 7 + 5] = F(-0.999999 * abs(float(x[128 * 7])))
+        if case == 3:
+            x[128 * 39 + 127] = np.nan
+        want_out, want_xs, want_bad = oracle.binary_x(x)
+        xa = arena.put(x)
+        out = arena.alloc(x.size // 8, fill=np.full(x.size // 8, 0xAA, np.uint8))
+        xs = arena.alloc(4 * (x.size // 128), fill=np.full(x.size // 128, -7, F))
+        assert k.binary_x(out, xs, xa, x.size) == want_bad
+        assert np.array_equal(arena.get(out, np.uint8, x.size // 8), want_out), case
+        got_xs = arena.get(xs, F, x.size // 128)
+        assert np.array_equal(np.isnan(got_xs), np.isnan(want_xs))
+        assert same_bits(np.nan_to_num(got_xs), np.nan_to_num(want_xs)), case
+        word = arena.alloc(4, fill=np.zeros(1, np.int32))
+        assert L.hq_binary_x_ex(out, xs, xa, x.size, word, None) == 0
+        assert arena.get(word, np.int32, 1)[0] == want_bad, case
 
 
 # ---- the order-revealing inputs of test_oracle.py, on the GPU ------------------------------------------------

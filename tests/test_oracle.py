@@ -17,7 +17,7 @@ import pytest
 
 import models
 from models import F
-from streams import LCG, pack6, pack_ternary, scale_rule, uninterleave_index
+from streams import LCG, pack6, pack_binary, pack_ternary, scale_rule, uninterleave_index
 
 
 # ---- quantize_x ---------------------------------------------------------------------------------------------
@@ -504,3 +504,106 @@ def test_t2r_reference_model(oracle, groups):
     for i in range(rows):
         want = models.t2_model(codes[i * n:(i + 1) * n], a, xs, hs[i * groups:(i + 1) * groups].astype(F), groups)
         assert got[i].view(np.uint32) == want.view(np.uint32), (groups, i)
+
+
+# ---- binary weights: kernels/binary.ts, relaxed/signs.ts:123-128, kernel/matmul.ts:222-224 -------------------------
+@pytest.mark.parametrize("groups", [1, 2, 3, 4, 5, 7, 9])
+def test_b1r_is_ternary_for_the_same_signs(oracle, groups):
+    """tests/ternary-check.ts:286-341: the binary kernel's numbers are the ternary kernel's to the bit for the same
+    signs (ternary code 2 b = the weight + 1), scales and activations.  Rows of all +1 and all -1, activations at
+    int8's ends and random, scales with subnormal and zero groups; row ranges anywhere.  The two packings are written
+    independently (pack_binary: bit 4 h + p of byte c; pack_ternary: 2 bits a weight), so a wrong bit or byte in
+    either kernel's unpacking gives a different integer."""
+    rows, n = 11, groups * 128
+    rng = np.random.default_rng(634 + groups)
+    bits = rng.integers(0, 2, rows * n).astype(np.uint8)
+    bits[:n], bits[n:2 * n] = 1, 0
+    bw = pack_binary(bits, n)
+    tw = pack_ternary(2 * bits)
+    halves = np.where(np.arange(rows * groups) % 11 == 7, 2.0 ** -20 * (1 + rng.integers(0, 1000, rows * groups)),
+                      np.where(np.arange(rows * groups) % 13 == 5, 0.0, 1e-3 * (1 + rng.integers(0, 1000, rows * groups))))
+    ws = halves.astype(np.float16).view(np.uint16)
+    for t in range(3):
+        a = np.where(np.arange(n) & 1, 127, -128) if t == 0 else (np.full(n, -128) if t == 1 else
+                                                                  rng.integers(-128, 128, n))
+        q = a.astype(np.int8)
+        s = (1e-2 * (1 + rng.integers(0, 1000, n // 32))).astype(F)
+        xi, area = oracle.interleave(q, s)
+        for r0, r1 in [(0, rows), (0, 1), (rows - 1, rows), (3, 8), (5, 5)]:
+            got = oracle.matmul_b1r(xi, area, bw, ws, n, r0, r1)
+            want = oracle.matmul_t2r(xi, area, tw, ws, n, r0, r1)
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (t, r0, r1)
+    # and a float64 bound against the signs themselves (no shared arithmetic with either kernel)
+    q = rng.integers(-128, 128, n).astype(np.int8)
+    s = (1e-2 * (1 + rng.integers(0, 1000, n // 32))).astype(F)
+    xi, area = oracle.interleave(q, s)
+    got = oracle.matmul_b1r(xi, area, bw, ws, n).astype(np.float64)
+    w = (2.0 * bits.reshape(rows, n) - 1.0)
+    d = np.array([oracle.half(h) for h in ws], np.float64).reshape(rows, groups)
+    exact = np.zeros(rows)
+    for g in range(groups):
+        for k in range(4):
+            lo = 128 * g + 32 * k
+            exact += (w[:, lo:lo + 32] @ q[lo:lo + 32].astype(np.float64)) * float(s[4 * g + k]) * d[:, g]
+    scale = np.abs(w).sum(1) * 128 * float(s.max()) * d.max(1) + 1e-30
+    assert np.all(np.abs(got - exact) <= 1e-5 * scale)
+
+
+def test_b1r_tile_is_the_token_kernel(oracle):
+    groups, rows, count = 3, 7, 5
+    n = 128 * groups
+    rng = np.random.default_rng(11)
+    bw = pack_binary(rng.integers(0, 2, rows * n), n)
+    ws = (rng.random(rows * groups) * 0.01).astype(np.float16).view(np.uint16)
+    frame, os_ = 2 * n, 4 * (rows + 1)
+    buf = np.zeros(count * frame, np.uint8)
+    toks = []
+    for t in range(count):
+        q = rng.integers(-128, 128, n).astype(np.int8)
+        s = (rng.random(n // 32) * 0.01).astype(F)
+        xi, area = oracle.interleave(q, s)
+        buf[t * frame:t * frame + n] = xi.view(np.uint8)
+        buf[t * frame + n:t * frame + n + area.nbytes] = area.view(np.uint8)
+        toks.append((xi, area))
+    out = np.full(count * os_ // 4, -7, F)
+    lib = oracle.lib()
+    lib.o_matmul_b1r_tile(out.ctypes.data, buf.ctypes.data, buf[n:].ctypes.data, bw.ctypes.data, ws.ctypes.data, n,
+                          1, rows, count, os_, frame, 2)
+    got = out.reshape(count, -1)
+    for t, (xi, area) in enumerate(toks):
+        want = oracle.matmul_b1r(xi, area, bw, ws, n)
+        assert np.array_equal(got[t, 1:rows].view(np.uint32), want[1:rows].view(np.uint32))
+        assert got[t, 0] == -7 and got[t, rows] == -7
+
+
+def binary_x_case(rng, groups=40):
+    """tests/ternary-check.ts:343-352: groups of +-d, d of every size (1e-30 to 65504), a group of zeros, one of -0"""
+    x = np.zeros(groups * 128, F)
+    for g in range(groups):
+        d = 0.0 if g == 3 else float(F([1, 0.0078125, 3.0000002, 1e-30, 65504, 1.5e-5][g % 6] * (1 + rng.integers(0, 7))))
+        x[g * 128:(g + 1) * 128] = -0.0 if g == 5 else np.where(rng.integers(0, 2, 128) == 1, d, -d)
+    return x
+
+
+def test_binary_x_bytes_scales_and_refusals(oracle):
+    """tests/ternary-check.ts:343-376: pack_binary's bytes (bit 4 h + p of byte c set where value 64 h + 4 c + p is not
+    below 0: -0 counts as 0), the largest |value| a group, and 1 for a value that is not plus or minus it"""
+    rng = np.random.default_rng(634)
+    x = binary_x_case(rng)
+    out, xs, bad = oracle.binary_x(x)
+    assert bad == 0
+    groups = x.size // 128
+    assert np.array_equal(xs, np.abs(x.reshape(groups, 128)).max(1))
+    assert np.array_equal(out, pack_binary((~(x < 0)).astype(np.uint8), x.size))
+    for at, spoil in [(0, 0.5), (127, 1.0000001), (128 + 63, 2), (128 * 39 + 127, np.nan), (128 * 7 + 5, -0.999999),
+                      (128 * 9 + 64 + 3, 0), (128 * 9 + 32 + 1, 0.5), (128 * 9 + 64 + 6, 0.5), (128 * 9 + 96 + 11, 0.5),
+                      (128 * 9 + 14, 0.5), (128 * 39 + 127, 0.5)]:
+        y = binary_x_case(rng)
+        g = at >> 7
+        y[g * 128:(g + 1) * 128] = np.where(np.arange(128) % 2 == 1, 3.0, -3.0)
+        y[at] = F(spoil * 3)
+        assert oracle.binary_x(y)[2] == 1, (at, spoil)
+    # a NaN makes its group's scale NaN (f32x4.max keeps it)
+    y = binary_x_case(rng)
+    y[130] = np.nan
+    assert np.isnan(oracle.binary_x(y)[1][1])
