@@ -217,7 +217,8 @@ def _graph_time(torch, launch, reps):
 
 
 def measure_configs(torch, pkg, args):
-    """The other configs' products on one GPU (BASELINE.json configs[0..2, 4]): GB/s of algorithmic bytes for the
+    """The other configs' products on one GPU (BASELINE.json configs[0..2, 4], and config 4's shapes with binary
+    weights, the packing the reference ranks next): GB/s of algorithmic bytes for the
     token products (M = 1; copies of the weights past the Infinity Cache where the shapes allow), TOPS for the
     prompts.  Products only (the activations prepared once), graphs of their launches timed with HIP events."""
     from pyodide_llm_amd import jobs
@@ -230,13 +231,13 @@ def measure_configs(torch, pkg, args):
 
     def acts(n, kind, count=1):
         x = torch.randn(count, n, device=dev, generator=gen)
-        area = (8 if kind == "ternary" else 4) * (n // 32)
+        area = (8 if kind in ("ternary", "binary") else 4) * (n // 32)
         frame = (n + area + 15) // 16 * 16
         buf = torch.empty(count * frame, dtype=torch.uint8, device=dev)
         bias = 64 if kind in ("int8", "int6") else 0
         pkg.check(lib.hq_quantize_x_batch(buf.data_ptr(), buf.data_ptr() + n, x.data_ptr(), n, bias, count, frame,
                                           4 * n, None))
-        if kind == "ternary":
+        if kind in ("ternary", "binary"):
             pkg.check(lib.hq_interleave_batch(buf.data_ptr(), buf.data_ptr() + n, n, count, frame, None))
         return buf, frame
 
@@ -247,15 +248,18 @@ def measure_configs(torch, pkg, args):
         elif kind == "int6":  # random bytes are valid packed int6 groups
             w = torch.randint(0, 256, (rows, n // 32 * 24), dtype=torch.uint8, device=dev, generator=gen)
             ws = (torch.randn(rows, n // 32, device=dev, generator=gen).abs_() * (0.02 / 124)).float()
-        else:  # ternary: codes 0..2 four to a byte, one float16 scale a row in every group of 128
-            codes = torch.randint(0, 3, (rows, n // 4, 4), dtype=torch.uint8, device=dev, generator=gen)
-            w = (codes[..., 0] | (codes[..., 1] << 2) | (codes[..., 2] << 4) | (codes[..., 3] << 6)).contiguous()
+        else:  # ternary: codes 0..2 four to a byte; binary: random bytes (a bit a sign); a float16 scale a row
+            if kind == "ternary":
+                codes = torch.randint(0, 3, (rows, n // 4, 4), dtype=torch.uint8, device=dev, generator=gen)
+                w = (codes[..., 0] | (codes[..., 1] << 2) | (codes[..., 2] << 4) | (codes[..., 3] << 6)).contiguous()
+            else:
+                w = torch.randint(0, 256, (rows, n // 8), dtype=torch.uint8, device=dev, generator=gen)
             row = (torch.randn(rows, 1, device=dev, generator=gen).abs_() * 0.02 + 1e-3).half()
             ws = row.expand(rows, n // 128).contiguous()
         return w, ws
 
-    per_weight = {"int8": 1.125, "int6": 0.875, "ternary": 0.265625}
-    kind_name = {"int8": "matmul_q8r", "int6": "matmul_q6r", "ternary": "matmul_t2r"}
+    per_weight = {"int8": 1.125, "int6": 0.875, "ternary": 0.265625, "binary": 0.140625}
+    kind_name = {"int8": "matmul_q8r", "int6": "matmul_q6r", "ternary": "matmul_t2r", "binary": "matmul_b1r"}
 
     def decode(label, kind, phase_shapes, copies):
         """phase_shapes: [[(rows, n), ...] a phase]; `copies` sets of distinct weights, every phase of each"""
@@ -273,7 +277,7 @@ def measure_configs(torch, pkg, args):
                     # wc 0: the corrections derived in the kernel (int8, int6); ternary jobs have none
                     entries.append(jobs.job(kind_name[kind], o.data_ptr(), buf.data_ptr(), buf.data_ptr() + n,
                                             w.data_ptr(), ws.data_ptr(), 0, n, rows=rows))
-                    total += rows * n * per_weight[kind] + n * (1.25 if kind == "ternary" else 1.125) + 4 * rows
+                    total += rows * n * per_weight[kind] + n * (1.25 if kind in ("ternary", "binary") else 1.125) + 4 * rows
                 tables.append((jobs.table(entries), len(entries)))
 
         def launch(h):
@@ -304,6 +308,10 @@ def measure_configs(torch, pkg, args):
                 calls.append(lambda h, w=w, ws=ws, buf=buf, frame=frame, o=o, rows=rows, n=n:
                              lib.hq_matmul_t2r_tile_ex(o.data_ptr(), buf.data_ptr(), buf.data_ptr() + n, w.data_ptr(),
                                                        ws.data_ptr(), n, 0, rows, count, 4 * rows, frame, 3, h))
+            elif kind == "binary":
+                calls.append(lambda h, w=w, ws=ws, buf=buf, frame=frame, o=o, rows=rows, n=n:
+                             lib.hq_matmul_b1r_tile_ex(o.data_ptr(), buf.data_ptr(), buf.data_ptr() + n, w.data_ptr(),
+                                                       ws.data_ptr(), n, 0, rows, count, 4 * rows, frame, 2, h))
             else:
                 t = jobs.table([jobs.job("matmul_q6r", o.data_ptr(), buf.data_ptr(), buf.data_ptr() + n, w.data_ptr(),
                                          ws.data_ptr(), 0, n, rows=rows, count=count, os=4 * rows, as_=frame,
@@ -324,11 +332,12 @@ def measure_configs(torch, pkg, args):
            [[(1536, 1024)], [(1024, 1024)], [(9216, 1024)], [(1024, 4608)]] * 16 + [[(65536, 1024)]], 1)
     prefill("c2 Llama-3.2-1B prefill M=512, one layer", "int8",
             [(3072, 2048), (2048, 2048), (8192, 2048), (8192, 2048), (2048, 8192)], 512)
-    for kind in ("ternary", "int6"):
-        copies = 8 if kind == "ternary" else 3
-        decode(f"c4 27B {kind} M=1, gate+up x {copies}", kind, [[(17408, 5120), (17408, 5120)]], copies)
-        decode(f"c4 27B {kind} M=1, down x {copies}", kind, [[(5120, 17408)]], copies)
-        prefill(f"c4 27B {kind} prefill M=256", kind, [(17408, 5120), (17408, 5120), (5120, 17408)], 256)
+    for kind in ("ternary", "int6", "binary"):
+        copies = {"ternary": 8, "int6": 3, "binary": 12}[kind]
+        tag = "c4 27B" if kind != "binary" else "27B shapes"
+        decode(f"{tag} {kind} M=1, gate+up x {copies}", kind, [[(17408, 5120), (17408, 5120)]], copies)
+        decode(f"{tag} {kind} M=1, down x {copies}", kind, [[(5120, 17408)]], copies)
+        prefill(f"{tag} {kind} prefill M=256", kind, [(17408, 5120), (17408, 5120), (5120, 17408)], 256)
     return out
 
 

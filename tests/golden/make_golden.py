@@ -1,5 +1,5 @@
 """Writes tests/golden/golden.npz: small input / output vectors of every kernel on the path, computed by the oracle
-(oracle/, the C restatement of the reference arithmetic) from the reference tests' LCG streams (tests/int8-check.ts:116-117,
+(oracle/, the C restatement of the reference arithmetic; binary included) from the reference tests' LCG streams (tests/int8-check.ts:116-117,
 seed 644; tests/ternary-check.ts:80-81, seed 231) and the stories15M shape of the first benchmark config (n = 288,
 24 of its 768 rows).  Arrays only (numpy.load with allow_pickle=False reads it).
 
@@ -15,7 +15,7 @@ ROOT = os.path.dirname(os.path.dirname(HERE))
 sys.path.insert(0, os.path.join(ROOT, "oracle"))
 sys.path.insert(0, os.path.join(ROOT, "tests"))
 import oracle  # noqa: E402
-from streams import LCG, pack6, pack_ternary, scale_rule  # noqa: E402
+from streams import LCG, pack6, pack_binary, pack_ternary, scale_rule  # noqa: E402
 
 F = np.float32
 ROWS, N, TOKENS = 24, 288, 6
@@ -80,6 +80,16 @@ def make():
     tbuf, tframe = frames(tqs, tss, TN, 8 * (TN // 32))
     g["ttile_x"], g["ttile_frame"] = tbuf, np.array([tframe], np.int32)
     g["ttile_t2r"] = np.stack([oracle.matmul_t2r(a, b, g["wt"], g["wst"], TN) for a, b in zip(tqs, tss)])
+    # binary (the same stream on): signs a bit (1 for +1), the ternary scales and activations; binary_x of +-d groups
+    signs = np.array([rt.next() & 1 for _ in range(ROWS * TN)], np.uint8)
+    g["wb"] = pack_binary(signs, TN)
+    g["b1r"] = oracle.matmul_b1r(tq, tarea, g["wb"], g["wst"], TN)
+    g["btile_b1r"] = np.stack([oracle.matmul_b1r(a, b, g["wb"], g["wst"], TN) for a, b in zip(tqs, tss)])
+    xb = np.array([(1 if rt.next() & 1 else -1) * 0.02 * (1 + (j >> 7)) for j in range(TN)], F)
+    xb[3] = F(0.5 * xb[3])  # a value that is not its group's +-largest: binary_x refuses it
+    g["xb"] = xb
+    g["xb_bits"], g["xb_scales"], bad = oracle.binary_x(xb)
+    g["xb_bad"] = np.array([bad], np.int32)
     return g
 
 

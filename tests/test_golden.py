@@ -36,6 +36,9 @@ def test_oracle_reproduces_golden(oracle, golden):
     tq, area = oracle.interleave(q.view(np.int8), s)
     assert same(tq.view(np.uint8), g["xtq"]) and same(area, g["xtarea"])
     assert same(oracle.matmul_t2r(g["xtq"].view(np.int8), g["xtarea"], g["wt"], g["wst"], TN), g["t2r"])
+    assert same(oracle.matmul_b1r(g["xtq"].view(np.int8), g["xtarea"], g["wb"], g["wst"], TN), g["b1r"])
+    bits, scales, bad = oracle.binary_x(g["xb"])
+    assert same(bits, g["xb_bits"]) and same(scales, g["xb_scales"]) and bad == g["xb_bad"][0] == 1
     frame = int(g["tile_frame"][0])
     for t in range(g["tile_x"].shape[0]):
         row = g["tile_x"][t]
@@ -110,3 +113,15 @@ def test_kernels_reproduce_golden(pkg, golden):
         o = out(ROWS * count)
         k.matmul_t2r_tile(o, tbuf, tbuf + TN, awt, awst, TN, 0, ROWS, count, 4 * ROWS, tframe, 3)
         assert same(arena.get(o, F, ROWS * count).reshape(count, ROWS), np.tile(g["ttile_t2r"], (reps, 1))), count
+        awb = arena.put(g["wb"])
+        o = out(ROWS * count)
+        k.matmul_b1r_tile(o, tbuf, tbuf + TN, awb, awst, TN, 0, ROWS, count, 4 * ROWS, tframe, 2)
+        assert same(arena.get(o, F, ROWS * count).reshape(count, ROWS), np.tile(g["btile_b1r"], (reps, 1))), count
+    # binary: the token kernel, and binary_x
+    o = out(ROWS)
+    k.matmul_b1r(o, txq, txs, arena.put(g["wb"]), awst, TN, 0, ROWS, 2)
+    assert same(arena.get(o, F, ROWS), g["b1r"])
+    bits, scales = arena.alloc(TN // 8), arena.alloc(4 * (TN // 128))
+    assert k.binary_x(bits, scales, arena.put(g["xb"]), TN) == g["xb_bad"][0]
+    assert same(arena.get(bits, np.uint8, TN // 8), g["xb_bits"])
+    assert same(arena.get(scales, F, TN // 128), g["xb_scales"])
