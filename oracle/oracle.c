@@ -419,3 +419,300 @@ double o_time_gemv(int32_t kind, float *xout, const void *xq, const void *xs, co
   }
   return best;
 }
+
+/* ---- llama.cpp's blocks of 256 weights: kernels/blocks/types.ts, token.ts, row.ts ----------------------------------
+ * A weight is F S W - Fm M (types.ts:32-47): W a small integer of its own (decoded here as the kernels hold it,
+ * magnitudes / minuses / weights, types.ts:194-270), S the integer of its unit of 16 or 32 (scaleOf, 273-292), for
+ * the K types M the minimum of its unit (minimumOf, 294-300), F and Fm the block's (blockScale, blockMinimum,
+ * 302-319).  The tables are sb_tables's (types.ts:323-348). */
+enum { SB_Q2_K = 10, SB_Q4_K = 12, SB_IQ2_XXS = 16, SB_IQ2_XS = 17, SB_IQ3_XXS = 18, SB_IQ1_S = 19, SB_IQ3_S = 21,
+       SB_IQ2_S = 22, SB_IQ4_XS = 23, SB_IQ1_M = 29 };
+enum { T_IQ2XS = 2048, T_IQ2S = 6144, T_IQ3XXS = 14336, T_IQ3S = 15360, T_IQ1S = 17408, T_SIGNS = 33792,
+       T_IQ4 = 34816, T_VECTORS = 34864, SB_GRIDS = 33792, SB_TABLES = 34992 };
+
+int32_t o_sb_bytes(int32_t type) {
+  switch (type) {
+  case SB_IQ2_XXS: return 66;
+  case SB_IQ3_S: return 110;
+  case SB_IQ2_XS: return 74;
+  case SB_IQ2_S: return 82;
+  case SB_IQ3_XXS: return 98;
+  case SB_IQ1_M: return 56;
+  case SB_IQ1_S: return 50;
+  case SB_Q2_K: return 84;
+  case SB_IQ4_XS: return 136;
+  case SB_Q4_K: return 144;
+  }
+  return 0;
+}
+
+static uint32_t u16_at(const uint8_t *p) { return (uint32_t)p[0] | ((uint32_t)p[1] << 8); }
+static uint32_t u32_at(const uint8_t *p) { return u16_at(p) | (u16_at(p + 2) << 16); }
+
+/* sb_tables (types.ts:323-348): the grids as the codebooks row has them (IQ1_S's plus one: codes 0, 1, 2), the
+ * signs of 8 weights by a 7-bit index (the eighth makes the number of minus signs even), IQ4_XS's values, their
+ * magnitudes and their signs, then the constant vectors */
+int32_t o_sb_tables(uint8_t *area, const uint8_t *codebooks) {
+  for (int i = 0; i < SB_GRIDS; i++) area[i] = (uint8_t)(codebooks[i] + (i >= T_IQ1S ? 1 : 0));
+  for (int i = 0; i < 128; i++) {
+    int ones = 0;
+    for (int j = 0; j < 7; j++) ones += (i >> j) & 1;
+    const int held = i | ((ones & 1) << 7);
+    for (int j = 0; j < 8; j++) area[T_SIGNS + 8 * i + j] = ((held >> j) & 1) ? 255 : 0;
+  }
+  for (int i = 0; i < 16; i++) {
+    const int8_t v = (int8_t)codebooks[SB_GRIDS + i];
+    area[T_IQ4 + i] = (uint8_t)v;
+    area[T_IQ4 + 16 + i] = (uint8_t)(int8_t)(v < 0 ? -v : v);
+    area[T_IQ4 + 32 + i] = v < 0 ? 255 : 0;
+  }
+  uint8_t *v = area + T_VECTORS;
+  for (int j = 0; j < 16; j++) {
+    v[0 + j] = (uint8_t)(1u << (j & 7));
+    v[16 + j] = (uint8_t)(j >> 3);
+    v[32 + j] = 3;
+    v[48 + j] = 15;
+    v[80 + j] = 7;
+    v[96 + j] = 1;
+  }
+  for (int j = 0; j < 4; j++) {
+    const int32_t p3 = 512 >> (3 * j), p4 = 4096 >> (4 * j);
+    memcpy(v + 64 + 4 * j, &p3, 4);
+    memcpy(v + 112 + 4 * j, &p4, 4);
+  }
+  return SB_TABLES;
+}
+
+/* sums_x (token.ts:149-165): after the n/32 scales at xs, n/16 int16 sums of each 16 activations, then n/8 of each 8 */
+void o_sums_x(void *xs, const int8_t *xq, int32_t n) {
+  int16_t *s16 = (int16_t *)((char *)xs + 4 * (n >> 5)), *s8 = s16 + (n >> 4);
+  for (int32_t i = 0; i < n / 8; i++) {
+    int32_t s = 0;
+    for (int j = 0; j < 8; j++) s += xq[8 * i + j];
+    s8[i] = (int16_t)s;
+  }
+  for (int32_t i = 0; i < n / 16; i++) s16[i] = (int16_t)(s8[2 * i] + s8[2 * i + 1]);
+}
+
+/* halfOf (halves.ts:26-28): a half's 16 bits in the low bits of an int */
+static float half_of(uint32_t bits) { return o_half((uint16_t)bits); }
+
+/* one block at p: W[256], S[16] and M[16] (a unit's integer for each 16 weights), F, Fm; and, for sb_row, the block's
+ * d (the float16 before the type's power of two), and IQ1's grid codes and shifts */
+typedef struct {
+  int32_t W[256], S[16], M[16];
+  int32_t code[256], down[256];
+  float F, Fm, d;
+} sb_block;
+
+static void sb_decode(const uint8_t *p, const uint8_t *tab, int32_t type, sb_block *B) {
+  int32_t *S = B->S, *M = B->M;
+  for (int h = 0; h < 16; h++) {
+    const int g = h >> 1;
+    int32_t *w = B->W + 16 * h;
+    int mag[16], neg[16] = {0}, down[16] = {0};
+    switch (type) {
+    case SB_IQ2_XXS: {  /* types.ts:197-200, 227-230, 277 */
+      const uint8_t *q = p + 2 + 8 * (h >> 1) + 2 * (h & 1);
+      const uint32_t aux = u32_at(p + 6 + 8 * (h >> 1)) >> (14 * (h & 1));
+      for (int j = 0; j < 16; j++) {
+        mag[j] = tab[8 * q[j >> 3] + (j & 7)];
+        neg[j] = tab[T_SIGNS + 8 * ((aux >> (7 * (j >> 3))) & 127) + (j & 7)] != 0;
+      }
+      S[h] = (int32_t)((u32_at(p + 6 + 8 * g) >> 27) | 1);
+      break;
+    }
+    case SB_IQ2_XS: {  /* types.ts:201-204, 232-235, 279 */
+      const uint8_t *q = p + 2 + 4 * h;
+      for (int j = 0; j < 16; j++) {
+        const uint32_t word = u16_at(q + 2 * (j >> 3));
+        mag[j] = tab[T_IQ2XS + 8 * (word & 511) + (j & 7)];
+        neg[j] = tab[T_SIGNS + 8 * (word >> 9) + (j & 7)] != 0;
+      }
+      S[h] = (int32_t)((((p[66 + g] >> (4 * (h & 1))) & 15) << 1) | 1);
+      break;
+    }
+    case SB_IQ2_S: {  /* types.ts:205-208, 237, 280 */
+      const uint8_t *q = p + 2 + 2 * h;
+      const uint32_t high = p[66 + (h >> 1)] >> (4 * (h & 1)), bits = u16_at(p + 34 + 2 * h);
+      const uint32_t idx[2] = {q[0] | ((high & 3) << 8), q[1] | ((high & 12) << 6)};
+      for (int j = 0; j < 16; j++) {
+        mag[j] = tab[T_IQ2S + 8 * idx[j >> 3] + (j & 7)];
+        neg[j] = (bits >> j) & 1;
+      }
+      S[h] = (int32_t)((((p[74 + g] >> (4 * (h & 1))) & 15) << 1) | 1);
+      break;
+    }
+    case SB_IQ3_XXS: {  /* types.ts:209-212, 227-230, 278 */
+      const uint8_t *q = p + 2 + 4 * h;
+      const uint32_t aux = u32_at(p + 66 + 4 * (h >> 1)) >> (14 * (h & 1));
+      for (int j = 0; j < 16; j++) {
+        mag[j] = tab[T_IQ3XXS + 4 * q[j >> 2] + (j & 3)];
+        neg[j] = tab[T_SIGNS + 8 * ((aux >> (7 * (j >> 3))) & 127) + (j & 7)] != 0;
+      }
+      S[h] = (int32_t)((u32_at(p + 66 + 4 * g) >> 27) | 1);
+      break;
+    }
+    case SB_IQ3_S: {  /* types.ts:213-217, 238, 281 */
+      const uint8_t *q = p + 2 + 4 * h;
+      const uint32_t high = p[66 + (h >> 1)] >> (4 * (h & 1)), bits = u16_at(p + 74 + 2 * h);
+      for (int j = 0; j < 16; j++) {
+        const int t = j >> 2;
+        mag[j] = tab[T_IQ3S + 4 * (q[t] | (((high >> t) & 1) << 8)) + (j & 3)];
+        neg[j] = (bits >> j) & 1;
+      }
+      S[h] = (int32_t)((((p[106 + (g >> 1)] >> (4 * ((h >> 1) & 1))) & 15) << 1) | 1);
+      break;
+    }
+    case SB_IQ1_S: {  /* types.ts:218-221, 247-249, 260-261, 282 */
+      const uint8_t *q = p + 2 + 2 * h;
+      const uint32_t word = u16_at(p + 34 + 2 * (h >> 1)), high = word >> (6 * (h & 1));
+      const uint32_t idx[2] = {q[0] | ((high & 7) << 8), q[1] | ((high & 56) << 5)};
+      for (int j = 0; j < 16; j++) {
+        mag[j] = tab[T_IQ1S + 8 * idx[j >> 3] + (j & 7)];
+        down[j] = (int)(word >> 15);
+      }
+      S[h] = (int32_t)((((word >> 12) & 7) << 1) | 1);
+      break;
+    }
+    case SB_IQ1_M: {  /* types.ts:222-225, 247-249, 262-264, 283 */
+      const uint8_t *q = p + 2 * h;
+      const uint32_t high = p[32 + h];
+      const uint32_t idx[2] = {q[0] | ((high & 7) << 8), q[1] | ((high & 0x70) << 4)};
+      for (int j = 0; j < 16; j++) {
+        mag[j] = tab[T_IQ1S + 8 * idx[j >> 3] + (j & 7)];
+        down[j] = (int)(j < 8 ? (high >> 3) & 1 : high >> 7);
+      }
+      S[h] = (int32_t)((((u16_at(p + 48 + 2 * (h >> 2)) >> (3 * (h & 3))) & 7) << 1) | 1);
+      break;
+    }
+    case SB_Q2_K: {  /* types.ts:226-229 (bits 2 s, 2 s + 1 of byte b of a half's 32 are weight 32 s + b), 284, 297 */
+      const uint8_t *v = p + 16 + 32 * (h >> 3) + 16 * (h & 1);
+      const int s = (h & 7) >> 1;
+      for (int j = 0; j < 16; j++) mag[j] = (v[j] >> (2 * s)) & 3;
+      S[h] = p[h] & 15;
+      M[h] = p[h] >> 4;
+      break;
+    }
+    case SB_Q4_K: {  /* types.ts:230-232, 285-287, 298-300 */
+      const uint8_t *v = p + 16 + 32 * (h >> 2) + 16 * (h & 1);
+      const int hi = (h >> 1) & 1;
+      for (int j = 0; j < 16; j++) mag[j] = (v[j] >> (4 * hi)) & 15;
+      S[h] = h < 8 ? (p[4 + g] & 63) : ((p[8 + g] & 15) | ((p[g] >> 6) << 4));
+      M[h] = h < 8 ? (p[8 + g] & 63) : ((p[8 + g] >> 4) | ((p[4 + g] >> 6) << 4));
+      break;
+    }
+    case SB_IQ4_XS: {  /* types.ts:233-234, 288-290 */
+      const uint8_t *v = p + 8 + 16 * (h >> 1);
+      for (int j = 0; j < 16; j++) mag[j] = (int8_t)tab[T_IQ4 + ((v[j] >> (4 * (h & 1))) & 15)];
+      S[h] = (int32_t)((((p[4 + (g >> 1)] >> (4 * ((h >> 1) & 1))) & 15) | (((u16_at(p + 2) >> (2 * (h >> 1))) & 3) << 4)) - 32);
+      break;
+    }
+    }
+    for (int j = 0; j < 16; j++) {
+      if (type == SB_IQ1_S || type == SB_IQ1_M) w[j] = 8 * mag[j] - 7 - 2 * down[j];  /* 8 code - 7, 2 less when down */
+      else w[j] = neg[j] ? -mag[j] : mag[j];
+      B->code[16 * h + j] = mag[j];
+      B->down[16 * h + j] = down[j];
+    }
+    if (type != SB_Q2_K && type != SB_Q4_K) M[h] = 0;
+  }
+  if (type == SB_IQ1_M) {  /* wholeScale (types.ts:312-316): the top four bits of the four words, the first's lowest */
+    const uint32_t w0 = u16_at(p + 48), w1 = u16_at(p + 50), w2 = u16_at(p + 52), w3 = u16_at(p + 54);
+    B->d = half_of((w0 >> 12) | ((w1 >> 8) & 0xf0) | ((w2 >> 4) & 0xf00) | (w3 & 0xf000));
+  } else {
+    B->d = o_half((uint16_t)u16_at(p + (type == SB_Q2_K ? 80 : 0)));
+  }
+  switch (type) {  /* blockScale (types.ts:302-310) */
+  case SB_IQ2_XXS: case SB_IQ2_XS: case SB_IQ2_S: case SB_IQ1_S: case SB_IQ1_M: B->F = B->d * 0.125f; break;
+  case SB_IQ3_XXS: B->F = B->d * 0.25f; break;
+  default: B->F = B->d; break;
+  }
+  /* blockMinimum (types.ts:318-320) */
+  B->Fm = type == SB_Q2_K ? o_half((uint16_t)u16_at(p + 82)) : type == SB_Q4_K ? o_half((uint16_t)u16_at(p + 2)) : 0.0f;
+}
+
+/* one row of matmul_sbr / matmul_sb (token.ts:111-134, types.ts:48-57): per block, G[k] = sum over group k of
+ * S W a (exact), M[k] = sum over group k of M a (K types); lane k += f(f(f(G[k] xs[k]) + f(G[k+4] xs[k+4])) F), less
+ * f(f(f(M[k] xs[k]) + f(M[k+4] xs[k+4])) Fm) for the K types; ((l0 + l1) + l2) + l3 at the end */
+static float sb_row_dot(const uint8_t *row, const uint8_t *tab, const int8_t *xq, const float *xs, int32_t n,
+                        int32_t type) {
+  const int32_t size = o_sb_bytes(type);
+  const int minimums = type == SB_Q2_K || type == SB_Q4_K;
+  float lane[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  sb_block B;
+  const int32_t *W = B.W, *S = B.S, *M = B.M;
+  for (int32_t b = 0; b < (n >> 8); b++) {
+    sb_decode(row + (int64_t)b * size, tab, type, &B);
+    const float F = B.F, Fm = B.Fm;
+    const int8_t *a = xq + 256 * b;
+    const float *s = xs + 8 * b;
+    int32_t G[8] = {0}, Mi[8] = {0};
+    for (int i = 0; i < 256; i++) {
+      G[i >> 5] += S[i >> 4] * W[i] * (int32_t)a[i];
+      Mi[i >> 5] += M[i >> 4] * (int32_t)a[i];
+    }
+    for (int k = 0; k < 4; k++) {
+      const float lo = (float)G[k] * s[k], hi = (float)G[k + 4] * s[k + 4];
+      const float sum = lo + hi;
+      float part = sum * F;
+      if (minimums) {
+        const float mlo = (float)Mi[k] * s[k], mhi = (float)Mi[k + 4] * s[k + 4];
+        const float msum = mlo + mhi;
+        part = part - msum * Fm;
+      }
+      lane[k] = lane[k] + part;
+    }
+  }
+  return ((lane[0] + lane[1]) + lane[2]) + lane[3];
+}
+
+void o_matmul_sbr(float *xout, const int8_t *xq, const void *xs, const uint8_t *w, const uint8_t *tab, int32_t n,
+                  int32_t r0, int32_t r1, int32_t type) {
+  const int32_t size = o_sb_bytes(type);
+  if (!size) return;  /* an unknown type writes nothing (token.ts:136-149) */
+  for (int32_t i = r0; i < r1; i++)
+    xout[i] = sb_row_dot(w + (int64_t)i * (n >> 8) * size, tab, xq, (const float *)xs, n, type);
+}
+
+void o_matmul_sbr_tile(void *xout, const void *xq, const void *xs, const uint8_t *w, const uint8_t *tab, int32_t n,
+                       int32_t r0, int32_t r1, int32_t count, int32_t os, int32_t frame, int32_t type) {
+  for (int32_t t = 0; t < count; t++)
+    o_matmul_sbr((float *)((char *)xout + (int64_t)t * os), (const int8_t *)((const char *)xq + (int64_t)t * frame),
+                 (const char *)xs + (int64_t)t * frame, w, tab, n, r0, r1, type);
+}
+
+/* sb_row (row.ts:7-58): the row's n weights as float32, each f(f(scale) W) (less f(Fm M) for the K types), scale the
+ * reader's product of the block's and the unit's floats; IQ1: f(scale (g + or - 1/8)), g the grid's -1, 0, 1 */
+void o_sb_row(float *out, const uint8_t *w, const uint8_t *tab, int32_t n, int32_t type) {
+  const int32_t size = o_sb_bytes(type);
+  if (!size) return;
+  sb_block B;
+  for (int32_t b = 0; b < (n >> 8); b++) {
+    const uint8_t *p = w + (int64_t)b * size;
+    sb_decode(p, tab, type, &B);
+    for (int h = 0; h < 16; h++) {
+      float scale;
+      const float s = (float)(B.S[h] >> 1);
+      switch (type) {  /* row.ts:9-17 (floatScale) */
+      case SB_IQ2_XXS: case SB_IQ2_XS: case SB_IQ2_S: scale = B.d * (0.5f + s) * 0.25f; break;
+      case SB_IQ3_XXS: scale = B.d * (0.5f + s) * 0.5f; break;
+      default: scale = B.d * (float)B.S[h]; break;
+      }
+      for (int j = 0; j < 16; j++) {
+        const int i = 16 * h + j;
+        float v;
+        if (type == SB_IQ1_S || type == SB_IQ1_M)  /* the grid's -1, 0, 1 and an eighth more or less (row.ts:22-31) */
+          v = (float)(B.code[i] - 1) + (B.down[i] ? -0.125f : 0.125f);
+        else
+          v = (float)B.W[i];
+        float x = scale * v;
+        if (type == SB_Q2_K || type == SB_Q4_K) {
+          const float least = B.Fm * (float)B.M[h];
+          x = x - least;
+        }
+        out[256 * b + i] = x;
+      }
+    }
+  }
+}

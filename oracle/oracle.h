@@ -67,6 +67,24 @@ void o_matmul_b1r_tile(void *xout, const void *xq, const void *xs, const uint8_t
  * minus its group's largest, else 0 */
 int32_t o_binary_x(uint8_t *out, float *xs, const float *x, int32_t n);
 
+/* llama.cpp's blocks of 256 weights (kernels/blocks/types.ts: Q2_K 10, Q4_K 12, IQ2_XXS 16, IQ2_XS 17, IQ3_XXS 18,
+ * IQ1_S 19, IQ3_S 21, IQ2_S 22, IQ4_XS 23, IQ1_M 29): the bytes of a block of `type` (types.ts:103-106), 0 for
+ * another */
+int32_t o_sb_bytes(int32_t type);
+/* kernels/blocks/types.ts:323-348: the 34992 bytes of tables from the codebooks row (33808 bytes) */
+int32_t o_sb_tables(uint8_t *area, const uint8_t *codebooks);
+/* kernels/blocks/token.ts:149-165: after quantize_x(.., 0)'s n/32 scales at xs, the int16 sums of each 16 and 8 */
+void o_sums_x(void *xs, const int8_t *xq, int32_t n);
+/* kernels/blocks/token.ts:111-147 (matmul_sbr; matmul_sb the same numbers): rows r0..r1 of w (n weights a row in
+ * blocks of `type`), tab: o_sb_tables's area, xq / xs: quantize_x(.., 0) + sums_x */
+void o_matmul_sbr(float *xout, const int8_t *xq, const void *xs, const uint8_t *w, const uint8_t *tab, int32_t n,
+                  int32_t r0, int32_t r1, int32_t type);
+/* kernels/blocks/tile.ts (matmul_sbr_tile, matmul_sbw_tile): every (row, token) matmul_sbr's number */
+void o_matmul_sbr_tile(void *xout, const void *xq, const void *xs, const uint8_t *w, const uint8_t *tab, int32_t n,
+                       int32_t r0, int32_t r1, int32_t count, int32_t os, int32_t frame, int32_t type);
+/* kernels/blocks/row.ts:7-72 (sb_row): a row's n weights as float32 */
+void o_sb_row(float *out, const uint8_t *w, const uint8_t *tab, int32_t n, int32_t type);
+
 /* CPU baseline: the GEMV above over rows [0, rows) on `threads` host threads, rows handed out in chunks as the
  * reference's phase() does (src/runtime/forward/threads.ts:45, 90-137: 4 chunks a thread, a shared counter).
  * kind: 0 matmul_q8r, 1 matmul_q8, 2 matmul_q6r, 3 matmul_q6, 4 matmul_t2r.  Runs `reps` times, returns seconds

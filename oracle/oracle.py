@@ -47,12 +47,18 @@ def lib():
             "o_matmul_t2r_tile": [p, p, p, p, p, i32, i32, i32, i32, i32, i32, i32],
             "o_matmul_b1r": [p, p, p, p, p, i32, i32, i32, i32],
             "o_matmul_b1r_tile": [p, p, p, p, p, i32, i32, i32, i32, i32, i32, i32],
+            "o_sums_x": [p, p, i32],
+            "o_matmul_sbr": [p, p, p, p, p, i32, i32, i32, i32],
+            "o_matmul_sbr_tile": [p, p, p, p, p, i32, i32, i32, i32, i32, i32, i32],
+            "o_sb_row": [p, p, p, i32, i32],
         }
         for name, argtypes in sigs.items():
             fn = getattr(L, name)
             fn.argtypes, fn.restype = argtypes, None
         L.o_half.argtypes, L.o_half.restype = [ctypes.c_uint16], ctypes.c_float
         L.o_binary_x.argtypes, L.o_binary_x.restype = [p, p, p, i32], i32
+        L.o_sb_bytes.argtypes, L.o_sb_bytes.restype = [i32], i32
+        L.o_sb_tables.argtypes, L.o_sb_tables.restype = [p, p], i32
         L.o_time_gemv.argtypes = [i32, p, p, p, p, p, p, i32, i32, i32, i32]
         L.o_time_gemv.restype = ctypes.c_double
         _lib = L
@@ -178,6 +184,48 @@ def binary_x(x):
     out, xs = np.zeros(n // 8, np.uint8), np.zeros(n // 128, np.float32)
     bad = lib().o_binary_x(_p(out), _p(xs), _p(x), n)
     return out, xs, bad
+
+
+SB_TYPES = {"Q2_K": 10, "Q4_K": 12, "IQ2_XXS": 16, "IQ2_XS": 17, "IQ3_XXS": 18, "IQ1_S": 19, "IQ3_S": 21,
+            "IQ2_S": 22, "IQ4_XS": 23, "IQ1_M": 29}
+SB_TABLES = 34992
+
+
+def sb_bytes(type_):
+    return lib().o_sb_bytes(type_)
+
+
+def sb_tables(codebooks):
+    """kernels/blocks/types.ts:323-348: the tables (uint8, 34992) from the codebooks row (uint8, 33808)."""
+    area = np.zeros(SB_TABLES, np.uint8)
+    lib().o_sb_tables(_p(area), _p(_c(codebooks, np.uint8)))
+    return area
+
+
+def sums_x(xq, xs):
+    """quantize_x(.., 0)'s int8 xq (n) and scales xs (n/32) -> the area kernels/blocks/token.ts reads: the scales,
+    then n/16 and n/8 int16 sums, as one uint8 array"""
+    xq = _c(xq, np.int8)
+    n = xq.size
+    area = np.zeros(4 * (n // 32) + 2 * (n // 16) + 2 * (n // 8), np.uint8)
+    area[:4 * (n // 32)] = _c(xs, np.float32).view(np.uint8)
+    lib().o_sums_x(_p(area), _p(xq), n)
+    return area
+
+
+def matmul_sbr(xq, area, w, tab, n, type_, r0=0, r1=None):
+    rows = w.size // ((n // 256) * sb_bytes(type_))
+    r1 = rows if r1 is None else r1
+    out = np.zeros(rows, np.float32)
+    lib().o_matmul_sbr(_p(out), _p(_c(xq, np.int8)), _p(_c(area, np.uint8)), _p(_c(w, np.uint8)),
+                       _p(_c(tab, np.uint8)), n, r0, r1, type_)
+    return out
+
+
+def sb_row(w, tab, n, type_):
+    out = np.zeros(n, np.float32)
+    lib().o_sb_row(_p(out), _p(_c(w, np.uint8)), _p(_c(tab, np.uint8)), n, type_)
+    return out
 
 
 def matmul_q8r_tokens(xq, xs, wq, ws, wc, n):

@@ -607,3 +607,102 @@ def test_binary_x_bytes_scales_and_refusals(oracle):
     y = binary_x_case(rng)
     y[130] = np.nan
     assert np.isnan(oracle.binary_x(y)[1][1])
+
+
+# ---- llama.cpp's blocks: kernels/blocks/types.ts, token.ts, row.ts ------------------------------------------------
+import blocks_model as bm  # noqa: E402
+
+
+@pytest.fixture(scope="module")
+def sb_setup(oracle):
+    rng = np.random.default_rng(363)
+    row = bm.codebooks(rng)
+    return row, bm.grids(row), oracle.sb_tables(row)
+
+
+def test_sb_tables(oracle, sb_setup):
+    """types.ts:323-348: the grids as given (IQ1_S's plus one), the signs of a 7-bit index with an even count of
+    minus signs, IQ4_XS's values / magnitudes / signs, the vectors"""
+    row, _, tab = sb_setup
+    assert np.array_equal(tab[:17408], row[:17408])
+    assert np.array_equal(tab[17408:33792], (row[17408:33792].astype(np.int32) + 1).astype(np.uint8))
+    signs = tab[33792:34816].reshape(128, 8)
+    assert set(np.unique(signs)) <= {0, 255}
+    assert np.all((signs == 255).sum(1) % 2 == 0)
+    assert np.array_equal(signs[:, :7] == 255, bm.bits_of(np.arange(128))[:, :7] == 1)
+    v = row[33792:].view(np.int8)
+    assert np.array_equal(tab[34816:34832].view(np.int8), v)
+    assert np.array_equal(tab[34832:34848], np.abs(v.astype(np.int32)).astype(np.uint8))
+    assert np.array_equal(tab[34848:34864], np.where(v < 0, 255, 0).astype(np.uint8))
+
+
+def test_sums_x_closed_form(oracle):
+    rng = np.random.default_rng(5)
+    n = 512
+    q = rng.integers(-127, 128, n).astype(np.int8)
+    s = rng.random(n // 32).astype(F)
+    area = oracle.sums_x(q, s)
+    assert np.array_equal(area[:4 * (n // 32)].view(F), s)
+    s16 = area[4 * (n // 32):4 * (n // 32) + 2 * (n // 16)].view(np.int16)
+    s8 = area[4 * (n // 32) + 2 * (n // 16):].view(np.int16)
+    assert np.array_equal(s16, q.astype(np.int32).reshape(-1, 16).sum(1))
+    assert np.array_equal(s8, q.astype(np.int32).reshape(-1, 8).sum(1))
+
+
+@pytest.mark.parametrize("name", sorted(bm.TYPES))
+def test_sb_row_is_the_reader(oracle, sb_setup, name):
+    """row.ts: a row as float32 is the converter's reader's (superblocks.py), to the bit: here against a model
+    written from the blocks' forms, for random blocks with ordinary and with subnormal scales"""
+    _, g, tab = sb_setup
+    t = bm.TYPES[name]
+    rng = np.random.default_rng(t)
+    for tiny in (False, True):
+        blocks = bm.random_blocks(rng, t, 12, tiny)
+        got = oracle.sb_row(blocks.reshape(-1), tab, 256 * len(blocks), t)
+        want = bm.read_floats(t, blocks, g).reshape(-1)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (name, tiny, np.nonzero(got != want)[0][:5])
+
+
+@pytest.mark.parametrize("name", sorted(bm.TYPES))
+def test_matmul_sbr_order_and_integers(oracle, sb_setup, name):
+    """token.ts / types.ts:48-57: the exact integers of every group and the kernels' float32 order, to the bit against
+    the model; rows cut anywhere; the tile is the token kernel's; and a float64 bound from the reader's weights"""
+    _, g, tab = sb_setup
+    t = bm.TYPES[name]
+    rng = np.random.default_rng(100 + t)
+    rows, nb = 7, 3
+    n = 256 * nb
+    blocks = bm.random_blocks(rng, t, rows * nb)
+    w = blocks.reshape(-1)
+    for trial in range(3):
+        x = rng.standard_normal(n).astype(F) * (1 + 3 * trial)
+        q, s = oracle.quantize_x(x, 0)
+        q = q.view(np.int8)
+        area = oracle.sums_x(q, s)
+        got = oracle.matmul_sbr(q, area, w, tab, n, t)
+        for r in range(rows):
+            want = bm.matmul(t, blocks[r * nb:(r + 1) * nb], q, s, g)
+            assert got[r].view(np.uint32) == np.float32(want).view(np.uint32), (name, trial, r, got[r], want)
+        part = oracle.matmul_sbr(q, area, w, tab, n, t, 2, 5)
+        assert np.array_equal(part[2:5].view(np.uint32), got[2:5].view(np.uint32))
+        assert not part[:2].any() and not part[5:].any()
+        weights = bm.read_floats(t, blocks, g).reshape(rows, n).astype(np.float64)
+        exact = weights @ (q.astype(np.float64) * np.repeat(s.astype(np.float64), 32))
+        bound = np.abs(weights) @ (np.abs(q.astype(np.float64)) * np.repeat(s.astype(np.float64), 32))
+        assert np.all(np.abs(got - exact) <= 1e-5 * bound + 1e-30), name
+    # the tile: three tokens a frame apart
+    count, frame = 3, 2 * n + 64
+    buf = np.zeros(count * frame, np.uint8)
+    toks = []
+    for tk in range(count):
+        q, s = oracle.quantize_x(rng.standard_normal(n).astype(F), 0)
+        area = oracle.sums_x(q.view(np.int8), s)
+        buf[tk * frame:tk * frame + n] = q
+        buf[tk * frame + n:tk * frame + n + area.size] = area
+        toks.append((q.view(np.int8), area))
+    out = np.full(count * (rows + 1), -7, F)
+    oracle.lib().o_matmul_sbr_tile(out.ctypes.data, buf.ctypes.data, buf[n:].ctypes.data, w.ctypes.data, tab.ctypes.data,
+                                   n, 0, rows, count, 4 * (rows + 1), frame, t)
+    for tk, (q, area) in enumerate(toks):
+        want = oracle.matmul_sbr(q, area, w, tab, n, t)
+        assert np.array_equal(out[tk * (rows + 1):tk * (rows + 1) + rows].view(np.uint32), want.view(np.uint32))
