@@ -98,6 +98,35 @@ void matmul_b1r_tile(void *xout, const void *xq, const void *xs, const void *wq,
  * It waits for the library's stream to know. */
 int32_t binary_x(void *out, void *xs, const void *x, int32_t n);
 
+/* llama.cpp's blocks of 256 weights (kernels/blocks/: Q2_K 10, Q4_K 12, IQ2_XXS 16, IQ2_XS 17, IQ3_XXS 18, IQ1_S 19,
+ * IQ3_S 21, IQ2_S 22, IQ4_XS 23, IQ1_M 29; a row is whole blocks, n a multiple of 256; w 2-byte aligned).
+ * kernels/blocks/types.ts:323-348: the 34992 bytes of tables at area (16-byte aligned) from the checkpoint's row of
+ * codebooks (33808 bytes: the six grids a value a byte, then IQ4_XS's 16 values); returns 34992 */
+int32_t sb_tables(void *area, const void *codebooks);
+/* kernels/blocks/token.ts:149-165: after quantize_x(xq, xs, x, n, 0)'s n/32 scales at xs, the int16 sums of each
+ * 16 of the n activations (n/16), then of each 8 (n/8) */
+void sums_x(void *xs, const void *xq, int32_t n);
+/* kernels/blocks/token.ts:140-142 (matmul_sbr): rows r0..r1 of w (blocks of `type`) times the activations of
+ * quantize_x(.., 0) + sums_x (xq, xs 16-byte aligned); tab: sb_tables's area */
+void matmul_sbr(void *xout, const void *xq, const void *xs, const void *w, const void *tab, int32_t n, int32_t r0,
+                int32_t r1, int32_t type);
+/* kernels/blocks/token.ts:137-139 (matmul_sb): the same numbers */
+void matmul_sb(void *xout, const void *xq, const void *xs, const void *w, const void *tab, int32_t n, int32_t r0,
+               int32_t r1, int32_t type);
+/* kernels/blocks/tile.ts:144-147: matmul_sbr for `count` tokens, strides as matmul_q8r_tile's (multiples of 16) */
+void matmul_sbr_tile(void *xout, const void *xq, const void *xs, const void *w, const void *tab, int32_t n, int32_t r0,
+                     int32_t r1, int32_t count, int32_t os, int32_t frame, int32_t type);
+/* kernels/blocks/tile.ts:231-253: the same numbers (the reference's form for engines whose dot product multiplies
+ * signed by signed, with a scratch area of the caller's; this library needs none and does not touch it) */
+void matmul_sbw_tile(void *xout, const void *xq, const void *xs, const void *w, const void *tab, int32_t n, int32_t r0,
+                     int32_t r1, int32_t count, int32_t os, int32_t frame, int32_t type, void *scratch);
+/* kernels/blocks/tile.ts:158-162: out[k] (int32) = the sum of the 4 products a[4k + j] b[4k + j] of the 16 signed
+ * bytes at a and b (device): on this device every product is exact, signed by signed */
+void signed_dots(void *out, const void *a, const void *b);
+/* kernels/blocks/row.ts: the n weights of the row at w as float32 (out 16-byte aligned), each as the converter's
+ * reader (src/python/convert/superblocks.py) gives it */
+void sb_row(void *out, const void *w, const void *tab, int32_t n, int32_t type);
+
 /* ---- the library's own ----------------------------------------------------------------------------------------- */
 
 enum {
@@ -153,6 +182,13 @@ int32_t hq_matmul_b1r_tile_ex(void *xout, const void *xq, const void *xs, const 
 /* binary_x on a stream, without waiting: `bad` (device, 4-byte aligned; may be NULL) is set to 1 where a value is
  * refused and left as it was otherwise, so the caller clears it first */
 int32_t hq_binary_x_ex(void *out, void *xs, const void *x, int32_t n, void *bad, void *stream);
+int32_t hq_sb_tables_ex(void *area, const void *codebooks, void *stream);
+int32_t hq_matmul_sbr_ex(void *xout, const void *xq, const void *xs, const void *w, const void *tab, int32_t n,
+                         int32_t r0, int32_t r1, int32_t type, void *stream);
+int32_t hq_matmul_sbr_tile_ex(void *xout, const void *xq, const void *xs, const void *w, const void *tab, int32_t n,
+                              int32_t r0, int32_t r1, int32_t count, int32_t os, int32_t frame, int32_t type,
+                              void *stream);
+int32_t hq_sb_row_ex(void *out, const void *w, const void *tab, int32_t n, int32_t type, void *stream);
 
 /* The activations of `count` tokens prepared in one launch (src/runtime/forward/engine.ts:405 calls ready() once a
  * token): token t's float32 values at x + t x_stride (bytes) -> xq + t frame and xs + t frame, as quantize_x; and,
@@ -160,12 +196,14 @@ int32_t hq_binary_x_ex(void *out, void *xs, const void *x, int32_t n, void *bad,
 int32_t hq_quantize_x_batch(void *xq, void *xs, const void *x, int32_t n, int32_t bias, int32_t count, int32_t frame,
                             int32_t x_stride, void *stream);
 int32_t hq_interleave_batch(void *xq, void *xs, int32_t n, int32_t count, int32_t frame, void *stream);
+/* sums_x of `count` tokens (token t's xq and xs at + t frame) */
+int32_t hq_sums_x_batch(void *xs, const void *xq, int32_t n, int32_t count, int32_t frame, void *stream);
 
 /* One phase of jobs (src/runtime/forward/threads.ts:90-137, src/runtime/jobs.ts:36-46): `jobs` holds `count` jobs
  * of `stride` float64 each (the reference's table has JOB = 16: the first 14 are used), each
  *   [kind, out, a, b, a4, a5, a6, a7, a8, rows, count, os, as, bs]
  * with kind the place of its line in jobs.ts's WORK (0 matmul_q8r, 1 matmul_q8, 5 matmul_q6r, 6 matmul_q6,
- * 8 matmul_t2r, 9 matmul_t2, 13 matmul_b1r, 14 matmul_b1), the eight arguments as WORK's `one` reads them, and every row [0, rows) of every one
+ * 8 matmul_t2r, 9 matmul_t2, 10 matmul_sbr, 11 matmul_sb, 12 matmul_sbw, 13 matmul_b1r, 14 matmul_b1), the eight arguments as WORK's `one` reads them, and every row [0, rows) of every one
  * of `count` tokens run (a job's out / a / b advance by os / as / bs bytes a token).  The addresses are device
  * addresses held exactly in the doubles (below 2^53).  Jobs of one kind and token count share a launch. */
 int32_t hq_phase(const double *jobs, int32_t count, int32_t stride, void *stream);
@@ -174,8 +212,8 @@ int32_t hq_phase(const double *jobs, int32_t count, int32_t stride, void *stream
  * activations: every job takes the same n and token count, token t's n values at x + t x_stride (bytes; x and
  * x_stride 16-byte aligned).  The relaxed int8 / int6 jobs of up to 4 tokens run with quantize_x in the products'
  * own launch (each block quantizes the input into its LDS: one launch a phase, the jobs' a / b not written); the
- * others are readied into their a / b (quantize_x at their bias, and interleave for ternary and binary;
- * jobs.ts:376-379, 421-424, 435-438) and then run as hq_phase runs them.  Every output is the number quantize_x + the kernel give. */
+ * others are readied into their a / b (quantize_x at their bias, and interleave for ternary and binary, sums_x
+ * for llama.cpp's blocks; jobs.ts:376-379, 385-395, 421-424, 435-438) and then run as hq_phase runs them.  Every output is the number quantize_x + the kernel give. */
 int32_t hq_matmuls(const void *x, int32_t x_stride, const double *jobs, int32_t count, int32_t stride, void *stream);
 
 /* The ceilings the kernels are measured against (no counterpart on this path: the reference's CPU ceiling loops,

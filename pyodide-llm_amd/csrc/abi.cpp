@@ -76,6 +76,9 @@ const char *kind_name(hq::Kind k) {
   case hq::T2: return "matmul_t2";
   case hq::B1R: return "matmul_b1r";
   case hq::B1: return "matmul_b1";
+  case hq::SBR: return "matmul_sbr";
+  case hq::SB: return "matmul_sb";
+  case hq::SBW: return "matmul_sbw";
   }
   return "?";
 }
@@ -85,8 +88,30 @@ bool ternary(hq::Kind k) { return hq::signs_kind(k); }
 bool relaxed(hq::Kind k) { return k == hq::Q8R || k == hq::Q6R; }
 bool six(hq::Kind k) { return k == hq::Q6R || k == hq::Q6; }
 
+// the preconditions of a job of llama.cpp's blocks
+int32_t check_blocks_job(hq::Kind kind, const hq::Job &j) {
+  const char *name = kind_name(kind);
+  if (!hq::sb_block_bytes(j.type)) return fail(HQ_ERR_ARGUMENT, "%s: type %d is not one of the ten block types", name, j.type);
+  if (j.n <= 0 || j.n % 256) return fail(HQ_ERR_ARGUMENT, "%s: n = %d is not a positive multiple of 256", name, j.n);
+  if (j.r0 < 0 || j.r1 < j.r0) return fail(HQ_ERR_ARGUMENT, "%s: rows %d..%d", name, j.r0, j.r1);
+  if (j.count < 0) return fail(HQ_ERR_ARGUMENT, "%s: count = %d", name, j.count);
+  if (j.r1 == j.r0 || j.count == 0) return HQ_OK;
+  if (!j.out || !j.xq || !j.xs || !j.wq || !j.ws) return fail(HQ_ERR_NULL, "%s: a NULL pointer", name);
+  if (!aligned(j.wq, 2)) return fail(HQ_ERR_ALIGNMENT, "%s: w not 2-byte aligned", name);
+  if (!aligned(j.ws, 16)) return fail(HQ_ERR_ALIGNMENT, "%s: the tables not 16-byte aligned", name);
+  if (!aligned(j.xq, 16) || !aligned(j.xs, 16)) return fail(HQ_ERR_ALIGNMENT, "%s: xq or xs not 16-byte aligned", name);
+  if (!aligned(j.out, 4)) return fail(HQ_ERR_ALIGNMENT, "%s: xout not 4-byte aligned", name);
+  if (j.count > 1) {
+    if (j.os < 0 || j.os % 4) return fail(HQ_ERR_ALIGNMENT, "%s: os = %lld is not a multiple of 4", name, (long long)j.os);
+    if (j.frame < 0 || j.frame % 16 || j.sframe < 0 || j.sframe % 16)
+      return fail(HQ_ERR_ALIGNMENT, "%s: a token stride is not a multiple of 16", name);
+  }
+  return HQ_OK;
+}
+
 // the preconditions of a matrix job (include/hq.h's list)
 int32_t check_job(hq::Kind kind, const hq::Job &j, int32_t three) {
+  if (hq::blocks_kind(kind)) return check_blocks_job(kind, j);
   const char *name = kind_name(kind);
   const int32_t unit = ternary(kind) ? 128 : 32;
   if (j.n <= 0 || j.n % unit) return fail(HQ_ERR_ARGUMENT, "%s: n = %d is not a positive multiple of %d", name, j.n, unit);
@@ -115,7 +140,38 @@ int32_t check_job(hq::Kind kind, const hq::Job &j, int32_t three) {
 
 // runs jobs of one kind: GEMV jobs (up to 4 tokens; more in slices of 4) batched in launches of up to kMaxJobs,
 // GEMM jobs one a launch
+int32_t run_blocks(hq::Kind kind, const std::vector<hq::Job> &jobs, hipStream_t s) {
+  // up to 4 tokens a launch (a prompt in slices of 4: every (row, token) the token kernel's number), jobs of one
+  // block type and one token count together
+  std::vector<hq::Job> parts;
+  for (const hq::Job &j : jobs) {
+    if (j.r1 == j.r0 || j.count == 0) continue;
+    for (int32_t t0 = 0; t0 < j.count; t0 += hq::kGemvMaxTokens) {
+      hq::Job part = j;
+      part.count = j.count - t0 < hq::kGemvMaxTokens ? j.count - t0 : hq::kGemvMaxTokens;
+      part.out = j.out + t0 * j.os;
+      part.xq = j.xq + t0 * j.frame;
+      part.xs = j.xs + t0 * j.sframe;
+      parts.push_back(part);
+    }
+  }
+  std::vector<bool> done(parts.size(), false);
+  for (size_t i = 0; i < parts.size(); i++) {
+    if (done[i]) continue;
+    std::vector<hq::Job> same;
+    for (size_t k = i; k < parts.size() && same.size() < (size_t)hq::kMaxJobs; k++)
+      if (!done[k] && parts[k].type == parts[i].type && parts[k].count == parts[i].count) {
+        same.push_back(parts[k]);
+        done[k] = true;
+      }
+    const int32_t st = hip_status(hq::launch_sb(same.data(), (int32_t)same.size(), s), kind_name(kind));
+    if (st) return st;
+  }
+  return HQ_OK;
+}
+
 int32_t run_jobs(hq::Kind kind, const std::vector<hq::Job> &jobs, hipStream_t s) {
+  if (hq::blocks_kind(kind)) return run_blocks(kind, jobs, s);
   std::vector<hq::Job> gemv[hq::kGemvMaxTokens + 1][2];  // by token count, by wc-ness
   for (const hq::Job &j : jobs) {
     if (j.r1 == j.r0 || j.count == 0) continue;
@@ -152,6 +208,18 @@ int32_t matmul(hq::Kind kind, void *xout, const void *xq, const void *xs, const 
   hq::Job j{(char *)xout, (const char *)xq, (const char *)xs, (const char *)wq, (const char *)ws,
             relaxed(kind) ? (const char *)wc : nullptr, n, r0, r1, count, os, frame, frame};
   if (int32_t st = check_job(kind, j, three)) return st;
+  if (j.r1 == j.r0 || j.count == 0) return HQ_OK;
+  if (int32_t st = ensure_device()) return st;
+  return run_jobs(kind, {j}, stream_of(stream));
+}
+
+int32_t matmul_blocks(hq::Kind kind, void *xout, const void *xq, const void *xs, const void *w, const void *tab,
+                      int32_t n, int32_t r0, int32_t r1, int32_t count, int32_t os, int32_t frame, int32_t type,
+                      void *stream) {
+  g_error = HQ_OK;
+  hq::Job j{(char *)xout, (const char *)xq, (const char *)xs, (const char *)w, (const char *)tab, nullptr, n, r0, r1,
+            count, os, frame, frame, type};
+  if (int32_t st = check_job(kind, j, 0)) return st;
   if (j.r1 == j.r0 || j.count == 0) return HQ_OK;
   if (int32_t st = ensure_device()) return st;
   return run_jobs(kind, {j}, stream_of(stream));
@@ -284,6 +352,50 @@ int32_t hq_matmul_b1r_tile_ex(void *xout, const void *xq, const void *xs, const 
   return matmul(hq::B1R, xout, xq, xs, wq, ws, nullptr, n, r0, r1, count, os, frame, two, stream);
 }
 
+// ---- llama.cpp's blocks (kernels/blocks/) -----------------------------------------------------------------------
+int32_t hq_sb_tables_ex(void *area, const void *codebooks, void *stream) {
+  g_error = HQ_OK;
+  if (!area || !codebooks) return fail(HQ_ERR_NULL, "sb_tables: a NULL pointer");
+  if (!aligned(area, 16)) return fail(HQ_ERR_ALIGNMENT, "sb_tables: the area not 16-byte aligned");
+  if (int32_t st = ensure_device()) return st;
+  return hip_status(hq::launch_sb_tables((uint8_t *)area, (const uint8_t *)codebooks, stream_of(stream)), "sb_tables");
+}
+
+int32_t hq_sums_x_batch(void *xs, const void *xq, int32_t n, int32_t count, int32_t frame, void *stream) {
+  g_error = HQ_OK;
+  if (n <= 0 || n % 32) return fail(HQ_ERR_ARGUMENT, "sums_x: n = %d is not a positive multiple of 32", n);
+  if (count < 0) return fail(HQ_ERR_ARGUMENT, "sums_x: count = %d", count);
+  if (count == 0) return HQ_OK;
+  if (!xs || !xq) return fail(HQ_ERR_NULL, "sums_x: a NULL pointer");
+  if (!aligned(xs, 4)) return fail(HQ_ERR_ALIGNMENT, "sums_x: xs not 4-byte aligned");
+  if (count > 1 && (frame < 0 || frame % 4)) return fail(HQ_ERR_ALIGNMENT, "sums_x: frame not a multiple of 4");
+  if (int32_t st = ensure_device()) return st;
+  return hip_status(hq::launch_sums_x((char *)xs, (const char *)xq, n, count, frame, stream_of(stream)), "sums_x");
+}
+
+int32_t hq_matmul_sbr_ex(void *xout, const void *xq, const void *xs, const void *w, const void *tab, int32_t n,
+                         int32_t r0, int32_t r1, int32_t type, void *stream) {
+  return matmul_blocks(hq::SBR, xout, xq, xs, w, tab, n, r0, r1, 1, 0, 0, type, stream);
+}
+int32_t hq_matmul_sbr_tile_ex(void *xout, const void *xq, const void *xs, const void *w, const void *tab, int32_t n,
+                              int32_t r0, int32_t r1, int32_t count, int32_t os, int32_t frame, int32_t type,
+                              void *stream) {
+  return matmul_blocks(hq::SBR, xout, xq, xs, w, tab, n, r0, r1, count, os, frame, type, stream);
+}
+
+int32_t hq_sb_row_ex(void *out, const void *w, const void *tab, int32_t n, int32_t type, void *stream) {
+  g_error = HQ_OK;
+  if (!hq::sb_block_bytes(type)) return fail(HQ_ERR_ARGUMENT, "sb_row: type %d is not one of the ten block types", type);
+  if (n < 0 || n % 256) return fail(HQ_ERR_ARGUMENT, "sb_row: n = %d is not a multiple of 256", n);
+  if (n == 0) return HQ_OK;
+  if (!out || !w || !tab) return fail(HQ_ERR_NULL, "sb_row: a NULL pointer");
+  if (!aligned(out, 16) || !aligned(w, 2) || !aligned(tab, 16))
+    return fail(HQ_ERR_ALIGNMENT, "sb_row: out or the tables not 16-, or w not 2-byte aligned");
+  if (int32_t st = ensure_device()) return st;
+  return hip_status(hq::launch_sb_row((float *)out, (const char *)w, (const uint8_t *)tab, n, type, stream_of(stream)),
+                    "sb_row");
+}
+
 // ---- binary weights from float32 (kernels/kernel/quantize.ts:232-247) -------------------------------------------
 int32_t hq_binary_x_ex(void *out, void *xs, const void *x, int32_t n, void *bad, void *stream) {
   g_error = HQ_OK;
@@ -328,6 +440,13 @@ int32_t parse_jobs(const double *jobs, int32_t count, int32_t stride, std::vecto
     case hq::T2: k = hq::T2; break;
     case hq::B1R: k = hq::B1R; j.sframe = j.count > 1 ? j.frame : j.sframe; break;  // its tile
     case hq::B1: k = hq::B1; break;
+    case hq::SBR:
+    case hq::SBW:  // their tiles take a prompt's tokens a frame apart (jobs.ts:206, 297-301)
+      k = (hq::Kind)kind;
+      j.type = (int32_t)e[6];
+      j.sframe = j.count > 1 ? j.frame : j.sframe;
+      break;
+    case hq::SB: k = hq::SB; j.type = (int32_t)e[6]; break;
     default: return fail(HQ_ERR_KIND, "%s: job %d is of kind %d, which this library does not run", who, i, kind);
     }
     if (int32_t st = check_job(k, j, hq::binary_kind(k) ? 2 : 3)) return st;
@@ -412,6 +531,10 @@ int32_t hq_matmuls(const void *x, int32_t x_stride, const double *jobs, int32_t 
         if (int32_t st = hip_status(hq::launch_interleave((char *)j.xq, (char *)j.xs, n, tokens, j.frame, s), "interleave"))
           return st;
       }
+      if (hq::blocks_kind(k)) {  // and the sums of each 16 and 8 (jobs.ts:385-395)
+        if (int32_t st = hip_status(hq::launch_sums_x((char *)j.xs, (const char *)j.xq, n, tokens, j.frame, s), "sums_x"))
+          return st;
+      }
     }
     if (int32_t st = run_jobs(k, list, s)) return st;
   }
@@ -486,6 +609,47 @@ void matmul_b1(void *xout, const void *xq, const void *xs, const void *wq, const
 void matmul_b1r_tile(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, int32_t n,
                      int32_t r0, int32_t r1, int32_t count, int32_t os, int32_t frame, int32_t two) {
   hq_matmul_b1r_tile_ex(xout, xq, xs, wq, ws, n, r0, r1, count, os, frame, two, g_stream.load());
+}
+int32_t sb_tables(void *area, const void *codebooks) {
+  hq_sb_tables_ex(area, codebooks, g_stream.load());
+  return hq::kSbTables;
+}
+void sums_x(void *xs, const void *xq, int32_t n) { hq_sums_x_batch(xs, xq, n, 1, 0, g_stream.load()); }
+void matmul_sbr(void *xout, const void *xq, const void *xs, const void *w, const void *tab, int32_t n, int32_t r0,
+                int32_t r1, int32_t type) {
+  hq_matmul_sbr_ex(xout, xq, xs, w, tab, n, r0, r1, type, g_stream.load());
+}
+void matmul_sb(void *xout, const void *xq, const void *xs, const void *w, const void *tab, int32_t n, int32_t r0,
+               int32_t r1, int32_t type) {
+  matmul_blocks(hq::SB, xout, xq, xs, w, tab, n, r0, r1, 1, 0, 0, type, g_stream.load());
+}
+void matmul_sbr_tile(void *xout, const void *xq, const void *xs, const void *w, const void *tab, int32_t n, int32_t r0,
+                     int32_t r1, int32_t count, int32_t os, int32_t frame, int32_t type) {
+  hq_matmul_sbr_tile_ex(xout, xq, xs, w, tab, n, r0, r1, count, os, frame, type, g_stream.load());
+}
+// the reference's tile for engines whose dot product multiplies signed by signed, with a scratch area of the
+// caller's for a row spread once: the same numbers, and this library needs no scratch
+void matmul_sbw_tile(void *xout, const void *xq, const void *xs, const void *w, const void *tab, int32_t n, int32_t r0,
+                     int32_t r1, int32_t count, int32_t os, int32_t frame, int32_t type, void *scratch) {
+  (void)scratch;
+  matmul_blocks(hq::SBW, xout, xq, xs, w, tab, n, r0, r1, count, os, frame, type, g_stream.load());
+}
+void signed_dots(void *out, const void *a, const void *b) {
+  g_error = HQ_OK;
+  if (!out || !a || !b) {
+    fail(HQ_ERR_NULL, "signed_dots: a NULL pointer");
+    return;
+  }
+  if (!aligned(out, 4)) {
+    fail(HQ_ERR_ALIGNMENT, "signed_dots: out not 4-byte aligned");
+    return;
+  }
+  if (ensure_device()) return;
+  hip_status(hq::launch_signed_dots((int32_t *)out, (const int8_t *)a, (const int8_t *)b, stream_of(g_stream.load())),
+             "signed_dots");
+}
+void sb_row(void *out, const void *w, const void *tab, int32_t n, int32_t type) {
+  hq_sb_row_ex(out, w, tab, n, type, g_stream.load());
 }
 // the reference's binary_x returns its refusal: this one waits for the library's stream to give it (a word of
 // device memory the library keeps for it, one a device); 1 also when the call fails (hq_last_error says why)

@@ -1,0 +1,494 @@
+// blocks.hip — llama.cpp's blocks of 256 weights (kernels/blocks/: types.ts, token.ts, row.ts, tile.ts), the ten
+// types Q2_K, Q4_K, IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M, IQ4_XS:
+//   sb_tables (types.ts:323-348), sums_x (token.ts:149-165), matmul_sbr / matmul_sb (token.ts:111-147: the same
+//   numbers), their tile for a prompt (tile.ts:144-147; matmul_sbw_tile's numbers too), sb_row (row.ts), signed_dots
+//   (tile.ts:158-162).
+//
+// A weight is F S W - Fm M (types.ts:32-47).  Every block is decoded 16 weights at a time (a "chunk" h = 0..15) into
+// four dwords of W's bytes and its unit's integers, in registers, as the reference reads it (the grids, the sign
+// table and IQ4_XS's values from sb_tables's area, read through the caches).  A chunk's integer is exact in int32:
+//   signed grids:  dot(|W|, a) - 2 dot(|W| of the negative weights, a)  (the sign on the weight, not on a byte add)
+//   IQ4_XS, K:     dot(W, a)  (IQ4_XS's W signed, the K types' 0..3 / 0..15)
+//   IQ1:           8 dot(code, a) - (7 or 9) (the sum of each 8 activations), by the shift of the 8 (token.ts:93-110)
+// then G[k] += S (chunk), M[k] += M (sum of the chunk's 16 activations) for the K types, k = h / 2 the group of 32.
+// Float32 (types.ts:48-57, token.ts:100-110): lane k of the reference adds, for every block in order,
+//   f(f(f(G[k] xs[k]) + f(G[k+4] xs[k+4])) F), less f(f(f(M[k] xs[k]) + f(M[k+4] xs[k+4])) Fm) for the K types,
+// and the four lanes are added in order at the end: a lane of a row here takes a block a step, and the parts go
+// through fold.hpp's LDS fold, lane k adding part k of the step's blocks in order, as the ternary kernels do.
+// A prompt's tokens go 4 at a time through the same kernel (every (row, token) the token kernel's number).
+#include "common.hpp"
+#include "launch.hpp"
+#include "fold.hpp"
+
+namespace hq {
+
+namespace {
+
+// sb_tables's area (types.ts:88-92)
+constexpr int T_IQ2XS = 2048, T_IQ2S = 6144, T_IQ3XXS = 14336, T_IQ3S = 15360, T_IQ1S = 17408, T_SIGNS = 33792,
+              T_IQ4 = 34816, T_VECTORS = 34864, GRIDS = 33792;
+constexpr int Q2_K = 10, Q4_K = 12, IQ2_XXS = 16, IQ2_XS = 17, IQ3_XXS = 18, IQ1_S = 19, IQ3_S = 21, IQ2_S = 22,
+              IQ4_XS = 23, IQ1_M = 29;
+
+template <int TY> constexpr bool has_signs() {
+  return TY == IQ2_XXS || TY == IQ2_XS || TY == IQ2_S || TY == IQ3_XXS || TY == IQ3_S;
+}
+template <int TY> constexpr bool has_minimums() { return TY == Q2_K || TY == Q4_K; }
+template <int TY> constexpr bool is_iq1() { return TY == IQ1_S || TY == IQ1_M; }
+
+// a block's bytes (its start 2-byte aligned: every type's size is even) as dwords from its first byte.  The aligned
+// dwords read are only those holding a byte of the block, so no read leaves the block's own 4-byte words.
+template <int BYTES>
+struct BlockBytes {
+  static constexpr int N = (BYTES + 3) / 4;
+  static constexpr int M = (BYTES + 2 + 3) / 4;  // the aligned dwords of a block that starts 2 bytes into one
+  uint32_t d[N];
+  HQ_DEV void load(const char *p) {
+    const uintptr_t a = (uintptr_t)p;
+    const uint32_t *q = (const uint32_t *)(a & ~(uintptr_t)3);
+    const bool odd = (a & 2) != 0;
+    uint32_t r[M];
+#pragma unroll
+    for (int i = 0; i < M; i++) r[i] = (i < N || odd) ? q[i] : 0u;
+#pragma unroll
+    for (int i = 0; i < N; i++) d[i] = odd ? __builtin_amdgcn_alignbit(i + 1 < M ? r[i + 1] : 0u, r[i], 16) : r[i];
+  }
+  HQ_DEV uint32_t u8(int x) const { return (d[x >> 2] >> (8 * (x & 3))) & 0xffu; }
+  HQ_DEV uint32_t u16(int x) const { return (d[x >> 2] >> (8 * (x & 3))) & 0xffffu; }  // x even
+  HQ_DEV uint32_t u32(int x) const {                                                  // x even
+    return (x & 3) == 0 ? d[x >> 2] : __builtin_amdgcn_alignbit(d[(x >> 2) + 1], d[x >> 2], 16);
+  }
+};
+
+// 16 bits -> 16 bytes of 0xff where a bit is set, the lowest first (bytesOfBits, types.ts:181-184): dword j of them
+HQ_DEV uint32_t bit_bytes(uint32_t bits, int j) {
+  uint32_t x = (bits >> (4 * j)) & 15u;
+  x = (x | (x << 7) | (x << 14) | (x << 21)) & 0x01010101u;
+  return x * 0xffu;
+}
+
+HQ_DEV uint2 entry8(const uint8_t *tab, int at) { return *(const uint2 *)(tab + at); }
+HQ_DEV uint32_t entry4(const uint8_t *tab, int at) { return *(const uint32_t *)(tab + at); }
+
+// chunk h of a block: W's bytes (magnitudes where the sign is apart, IQ1's codes), 0xff where a weight is negative,
+// the unit's S (and M), IQ1's shifts of the two 8s (1: down)
+struct Chunk {
+  uint32_t mag[4], neg[4];
+  int32_t S, M;
+  uint32_t down0, down1;
+};
+
+template <int TY, int BYTES>
+HQ_DEV void chunk(const BlockBytes<BYTES> &B, int h, const uint8_t *tab, const uint32_t iq4[4], Chunk &c) {
+  const int g = h >> 1;
+  c.M = 0;
+  c.down0 = c.down1 = 0;
+#pragma unroll
+  for (int j = 0; j < 4; j++) c.neg[j] = 0;
+  if (TY == IQ2_XXS) {  // types.ts:197-200, 227-230, 277
+    const int at = 2 + 8 * (h >> 1) + 2 * (h & 1);
+    const uint2 e0 = entry8(tab, 8 * (int)B.u8(at)), e1 = entry8(tab, 8 * (int)B.u8(at + 1));
+    c.mag[0] = e0.x; c.mag[1] = e0.y; c.mag[2] = e1.x; c.mag[3] = e1.y;
+    const uint32_t word = B.u32(6 + 8 * (h >> 1)), aux = word >> (14 * (h & 1));
+    const uint2 s0 = entry8(tab, T_SIGNS + 8 * (int)(aux & 127)), s1 = entry8(tab, T_SIGNS + 8 * (int)((aux >> 7) & 127));
+    c.neg[0] = s0.x; c.neg[1] = s0.y; c.neg[2] = s1.x; c.neg[3] = s1.y;
+    c.S = (int32_t)((word >> 27) | 1);
+  } else if (TY == IQ2_XS) {  // types.ts:201-204, 232-235, 279
+    const uint32_t w0 = B.u16(2 + 4 * h), w1 = B.u16(4 + 4 * h);
+    const uint2 e0 = entry8(tab, T_IQ2XS + 8 * (int)(w0 & 511)), e1 = entry8(tab, T_IQ2XS + 8 * (int)(w1 & 511));
+    c.mag[0] = e0.x; c.mag[1] = e0.y; c.mag[2] = e1.x; c.mag[3] = e1.y;
+    const uint2 s0 = entry8(tab, T_SIGNS + 8 * (int)(w0 >> 9)), s1 = entry8(tab, T_SIGNS + 8 * (int)(w1 >> 9));
+    c.neg[0] = s0.x; c.neg[1] = s0.y; c.neg[2] = s1.x; c.neg[3] = s1.y;
+    c.S = (int32_t)((((B.u8(66 + g) >> (4 * (h & 1))) & 15) << 1) | 1);
+  } else if (TY == IQ2_S) {  // types.ts:205-208, 237, 280
+    const uint32_t high = B.u8(66 + (h >> 1)) >> (4 * (h & 1));
+    const uint32_t i0 = B.u8(2 + 2 * h) | ((high & 3) << 8), i1 = B.u8(3 + 2 * h) | ((high & 12) << 6);
+    const uint2 e0 = entry8(tab, T_IQ2S + 8 * (int)i0), e1 = entry8(tab, T_IQ2S + 8 * (int)i1);
+    c.mag[0] = e0.x; c.mag[1] = e0.y; c.mag[2] = e1.x; c.mag[3] = e1.y;
+    const uint32_t bits = B.u16(34 + 2 * h);
+#pragma unroll
+    for (int j = 0; j < 4; j++) c.neg[j] = bit_bytes(bits, j);
+    c.S = (int32_t)((((B.u8(74 + g) >> (4 * (h & 1))) & 15) << 1) | 1);
+  } else if (TY == IQ3_XXS) {  // types.ts:209-212, 227-230, 278
+#pragma unroll
+    for (int j = 0; j < 4; j++) c.mag[j] = entry4(tab, T_IQ3XXS + 4 * (int)B.u8(2 + 4 * h + j));
+    const uint32_t word = B.u32(66 + 4 * (h >> 1)), aux = word >> (14 * (h & 1));
+    const uint2 s0 = entry8(tab, T_SIGNS + 8 * (int)(aux & 127)), s1 = entry8(tab, T_SIGNS + 8 * (int)((aux >> 7) & 127));
+    c.neg[0] = s0.x; c.neg[1] = s0.y; c.neg[2] = s1.x; c.neg[3] = s1.y;
+    c.S = (int32_t)((word >> 27) | 1);
+  } else if (TY == IQ3_S) {  // types.ts:213-217, 238, 281
+    const uint32_t high = B.u8(66 + (h >> 1)) >> (4 * (h & 1));
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      c.mag[j] = entry4(tab, T_IQ3S + 4 * (int)(B.u8(2 + 4 * h + j) | (((high >> j) & 1) << 8)));
+    const uint32_t bits = B.u16(74 + 2 * h);
+#pragma unroll
+    for (int j = 0; j < 4; j++) c.neg[j] = bit_bytes(bits, j);
+    c.S = (int32_t)((((B.u8(106 + (h >> 2)) >> (4 * ((h >> 1) & 1))) & 15) << 1) | 1);
+  } else if (TY == IQ1_S) {  // types.ts:218-221, 260-261, 282
+    const uint32_t word = B.u16(34 + 2 * (h >> 1)), high = word >> (6 * (h & 1));
+    const uint32_t i0 = B.u8(2 + 2 * h) | ((high & 7) << 8), i1 = B.u8(3 + 2 * h) | ((high & 56) << 5);
+    const uint2 e0 = entry8(tab, T_IQ1S + 8 * (int)i0), e1 = entry8(tab, T_IQ1S + 8 * (int)i1);
+    c.mag[0] = e0.x; c.mag[1] = e0.y; c.mag[2] = e1.x; c.mag[3] = e1.y;
+    c.down0 = c.down1 = word >> 15;
+    c.S = (int32_t)((((word >> 12) & 7) << 1) | 1);
+  } else if (TY == IQ1_M) {  // types.ts:222-225, 262-264, 283
+    const uint32_t high = B.u8(32 + h);
+    const uint32_t i0 = B.u8(2 * h) | ((high & 7) << 8), i1 = B.u8(2 * h + 1) | ((high & 0x70) << 4);
+    const uint2 e0 = entry8(tab, T_IQ1S + 8 * (int)i0), e1 = entry8(tab, T_IQ1S + 8 * (int)i1);
+    c.mag[0] = e0.x; c.mag[1] = e0.y; c.mag[2] = e1.x; c.mag[3] = e1.y;
+    c.down0 = (high >> 3) & 1;
+    c.down1 = high >> 7;
+    c.S = (int32_t)((((B.u16(48 + 2 * (h >> 2)) >> (3 * (h & 3))) & 7) << 1) | 1);
+  } else if (TY == Q2_K) {  // bits 2 s, 2 s + 1 of byte c of a half's 32 are weight 32 s + c (types.ts:226-229)
+    const int at = 16 + 32 * (h >> 3) + 16 * (h & 1), s = (h & 7) >> 1;
+#pragma unroll
+    for (int j = 0; j < 4; j++) c.mag[j] = (B.u32(at + 4 * j) >> (2 * s)) & 0x03030303u;
+    c.S = (int32_t)(B.u8(h) & 15);
+    c.M = (int32_t)(B.u8(h) >> 4);
+  } else if (TY == Q4_K) {  // of every 32 bytes the low halves are 32 weights, the high halves the next (230-232)
+    const int at = 16 + 32 * (h >> 2) + 16 * (h & 1), hi = (h >> 1) & 1;
+#pragma unroll
+    for (int j = 0; j < 4; j++) c.mag[j] = (B.u32(at + 4 * j) >> (4 * hi)) & 0x0f0f0f0fu;
+    c.S = (int32_t)(h < 8 ? (B.u8(4 + g) & 63) : ((B.u8(8 + g) & 15) | ((B.u8(g) >> 6) << 4)));
+    c.M = (int32_t)(h < 8 ? (B.u8(8 + g) & 63) : ((B.u8(8 + g) >> 4) | ((B.u8(4 + g) >> 6) << 4)));
+  } else {  // IQ4_XS: a group's 16 bytes, low halves its first 16 weights, as IQ4_XS's values (types.ts:233-234)
+    const int at = 8 + 16 * (h >> 1), hi = h & 1;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const uint32_t nb = (B.u32(at + 4 * j) >> (4 * hi)) & 0x0f0f0f0fu;
+      const uint32_t sel = nb & 0x07070707u, upper = ((nb >> 3) & 0x01010101u) * 0xffu;
+      const uint32_t low = __builtin_amdgcn_perm(iq4[1], iq4[0], sel), high = __builtin_amdgcn_perm(iq4[3], iq4[2], sel);
+      c.mag[j] = (low & ~upper) | (high & upper);
+    }
+    c.S = (int32_t)((((B.u8(4 + (h >> 2)) >> (4 * ((h >> 1) & 1))) & 15) | (((B.u16(2) >> (2 * (h >> 1))) & 3) << 4)) - 32);
+  }
+}
+
+// the block's F (blockScale, types.ts:302-310) and Fm (blockMinimum, 318-320); d: the block's own float16 (IQ1_M's
+// put together from its four words' tops, wholeScale 312-316)
+template <int TY, int BYTES>
+HQ_DEV float block_d(const BlockBytes<BYTES> &B) {
+  if (TY == IQ1_M)
+    return half_to_float((B.u16(48) >> 12) | ((B.u16(50) >> 8) & 0xf0u) | ((B.u16(52) >> 4) & 0xf00u) | (B.u16(54) & 0xf000u));
+  return half_to_float(B.u16(TY == Q2_K ? 80 : 0));
+}
+template <int TY, int BYTES>
+HQ_DEV float block_f(const BlockBytes<BYTES> &B) {
+  const float d = block_d<TY>(B);
+  if (TY == IQ2_XXS || TY == IQ2_XS || TY == IQ2_S || TY == IQ1_S || TY == IQ1_M) return fmul(d, 0.125f);
+  if (TY == IQ3_XXS) return fmul(d, 0.25f);
+  return d;
+}
+template <int TY, int BYTES>
+HQ_DEV float block_fm(const BlockBytes<BYTES> &B) {
+  return has_minimums<TY>() ? half_to_float(B.u16(TY == Q2_K ? 82 : 2)) : 0.0f;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// the products (matmul_sbr == matmul_sb): rows of 16 lanes, 16 rows a block, a block of 256 weights a lane a step
+// ---------------------------------------------------------------------------------------------------------------
+struct SbBatch {
+  Job job[kMaxJobs];
+  int32_t block0[kMaxJobs + 1];
+  int32_t njobs;
+};
+
+HQ_DEV int sb_job_of(const SbBatch &b, int blk) {
+  int j = 0;
+  while (j + 1 < b.njobs && blk >= b.block0[j + 1]) ++j;
+  return j;
+}
+
+constexpr int kSbLanes = 16;
+
+template <int TY, int T>
+__global__ __launch_bounds__(256) void gemv_sb(SbBatch batch) {
+  constexpr int L = kSbLanes;
+  constexpr int BYTES = sb_block_bytes(TY);
+  __shared__ FoldL<T, L> fold[4];
+  const int jb = sb_job_of(batch, blockIdx.x);
+  const Job &J = batch.job[jb];
+  const int lane = threadIdx.x & (L - 1);
+  const int wave = threadIdx.x >> 6, slot = (threadIdx.x & 63) / L;
+  const int row_u = J.r0 + (blockIdx.x - batch.block0[jb]) * (256 / L) + threadIdx.x / L;
+  const bool live = row_u < J.r1;
+  const int row = live ? row_u : J.r1 - 1;
+  const int blocks = J.n >> 8;
+  const char *wrow = J.wq + (int64_t)row * blocks * BYTES;
+  const uint8_t *tab = (const uint8_t *)J.ws;
+  uint32_t iq4[4] = {0u, 0u, 0u, 0u};
+  if (TY == IQ4_XS) {
+    const uint4 v = *(const uint4 *)(tab + T_IQ4);
+    iq4[0] = v.x; iq4[1] = v.y; iq4[2] = v.z; iq4[3] = v.w;
+  }
+  // token t's activations (n int8), its scales (n / 32 float32), its sums of 16 and of 8 (int16)
+  const int8_t *xq[T];
+  const float *xs[T];
+  const int16_t *s16[T], *s8[T];
+#pragma unroll
+  for (int t = 0; t < T; t++) {
+    xq[t] = (const int8_t *)(J.xq + t * J.frame);
+    xs[t] = (const float *)(J.xs + t * J.sframe);
+    s16[t] = (const int16_t *)(xs[t] + (J.n >> 5));
+    s8[t] = s16[t] + (J.n >> 4);
+  }
+  FoldL<T, L> &f = fold[wave];
+  float acc[T];
+#pragma unroll
+  for (int t = 0; t < T; t++) acc[t] = 0.0f;
+  const int steps = (blocks + L - 1) / L;
+  for (int it = 0; it < steps; it++) {
+    const int b = it * L + lane;
+    const bool valid = b < blocks;
+    const int bl = valid ? b : 0;
+    BlockBytes<BYTES> B;
+    B.load(wrow + (int64_t)bl * BYTES);
+    int32_t G[T][8], Mi[T][8];
+#pragma unroll
+    for (int t = 0; t < T; t++)
+#pragma unroll
+      for (int k = 0; k < 8; k++) G[t][k] = Mi[t][k] = 0;
+#pragma unroll
+    for (int h = 0; h < 16; h++) {
+      Chunk c;
+      chunk<TY>(B, h, tab, iq4, c);
+      uint32_t signed_part[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) signed_part[j] = c.mag[j] & c.neg[j];
+#pragma unroll
+      for (int t = 0; t < T; t++) {
+        const uint4 av = *(const uint4 *)(xq[t] + 256 * bl + 16 * h);
+        const int32_t a[4] = {(int32_t)av.x, (int32_t)av.y, (int32_t)av.z, (int32_t)av.w};
+        int32_t d = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) d = sdot4((int32_t)c.mag[j], a[j], d);
+        if (has_signs<TY>()) {
+          int32_t e = 0;
+#pragma unroll
+          for (int j = 0; j < 4; j++) e = sdot4((int32_t)signed_part[j], a[j], e);
+          d -= 2 * e;
+        }
+        if (is_iq1<TY>()) {  // 8 dot(code, a) - (7 + 2 down) sum of each 8 (token.ts:93-99, 117-127)
+          const int32_t e0 = s8[t][32 * bl + 2 * h], e1 = s8[t][32 * bl + 2 * h + 1];
+          d = 8 * d - (7 + 2 * (int32_t)c.down0) * e0 - (7 + 2 * (int32_t)c.down1) * e1;
+        }
+        G[t][h >> 1] += c.S * d;
+        if (has_minimums<TY>()) Mi[t][h >> 1] += c.M * (int32_t)s16[t][16 * bl + h];
+      }
+    }
+    const float F = block_f<TY>(B), Fm = block_fm<TY>(B);
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+      const float4 x0 = *(const float4 *)(xs[t] + 8 * bl), x1 = *(const float4 *)(xs[t] + 8 * bl + 4);
+      const float sl[4] = {x0.x, x0.y, x0.z, x0.w}, sh[4] = {x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        float part = fmul(fadd(fmul((float)G[t][k], sl[k]), fmul((float)G[t][k + 4], sh[k])), F);
+        if (has_minimums<TY>())
+          part = fsub(part, fmul(fadd(fmul((float)Mi[t][k], sl[k]), fmul((float)Mi[t][k + 4], sh[k])), Fm));
+        f.v[it & 1][slot][t][k][lane] = valid ? part : 0.0f;  // +0 leaves a lane as it is: a lane is never -0
+      }
+    }
+    fold_step_l<T, L>(f, it & 1, slot, lane, acc);
+  }
+  // lanes 0..3 hold the four lanes' sums: ((l0 + l1) + l2) + l3 in lane 0 (math.ts:7-9)
+  float sum[T];
+#pragma unroll
+  for (int t = 0; t < T; t++)
+    sum[t] = fadd(fadd(fadd(acc[t], from_lane_plus<1>(acc[t])), from_lane_plus<2>(acc[t])), from_lane_plus<3>(acc[t]));
+  if (live && lane == 0) {
+#pragma unroll
+    for (int t = 0; t < T; t++) ((float *)(J.out + t * J.os))[row] = sum[t];
+  }
+}
+
+template <int TY>
+hipError_t launch_type(const SbBatch &b, int blocks, int T, hipStream_t s) {
+  dim3 grid(blocks), block(256);
+  switch (T) {
+  case 1: hipLaunchKernelGGL((gemv_sb<TY, 1>), grid, block, 0, s, b); break;
+  case 2: hipLaunchKernelGGL((gemv_sb<TY, 2>), grid, block, 0, s, b); break;
+  case 3: hipLaunchKernelGGL((gemv_sb<TY, 3>), grid, block, 0, s, b); break;
+  case 4: hipLaunchKernelGGL((gemv_sb<TY, 4>), grid, block, 0, s, b); break;
+  default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// sb_row: a row as float32 (row.ts), a chunk of 16 weights a thread
+// ---------------------------------------------------------------------------------------------------------------
+template <int TY>
+__global__ __launch_bounds__(256) void sb_row_kernel(float *out, const char *w, const uint8_t *tab, int32_t n) {
+  constexpr int BYTES = sb_block_bytes(TY);
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // chunk: block i / 16, h = i % 16
+  if (i >= (int64_t)(n >> 4)) return;
+  const int b = (int)(i >> 4), h = (int)(i & 15);
+  BlockBytes<BYTES> B;
+  B.load(w + (int64_t)b * BYTES);
+  uint32_t iq4[4] = {0u, 0u, 0u, 0u};
+  if (TY == IQ4_XS) {
+    const uint4 v = *(const uint4 *)(tab + T_IQ4);
+    iq4[0] = v.x; iq4[1] = v.y; iq4[2] = v.z; iq4[3] = v.w;
+  }
+  Chunk c;
+  // h is not a constant here: the chunk is decoded for each h and the one of this thread kept
+#pragma unroll
+  for (int hh = 0; hh < 16; hh++)
+    if (hh == h) chunk<TY>(B, hh, tab, iq4, c);
+  const float d = block_d<TY>(B), fm = block_fm<TY>(B);
+  // floatScale (row.ts:9-17): d (s + 1/2) / 4 (IQ2), d (s + 1/2) / 2 (IQ3_XXS), d S otherwise
+  const float s = (float)(c.S >> 1);
+  const float scale = (TY == IQ2_XXS || TY == IQ2_XS || TY == IQ2_S) ? fmul(fmul(d, fadd(0.5f, s)), 0.25f)
+                    : TY == IQ3_XXS ? fmul(fmul(d, fadd(0.5f, s)), 0.5f) : fmul(d, (float)c.S);
+  const float least = has_minimums<TY>() ? fmul(fm, (float)c.M) : 0.0f;
+  float *to = out + 16 * i;
+#pragma unroll
+  for (int j = 0; j < 16; j++) {
+    const int32_t byte = (int32_t)(int8_t)((c.mag[j >> 2] >> (8 * (j & 3))) & 0xff);
+    float v;
+    if (is_iq1<TY>()) {  // the grid's -1, 0, 1 and an eighth more or less (row.ts:22-31)
+      const uint32_t down = j < 8 ? c.down0 : c.down1;
+      v = fadd((float)(byte - 1), down ? -0.125f : 0.125f);
+    } else if (has_signs<TY>()) {
+      const bool negative = ((c.neg[j >> 2] >> (8 * (j & 3))) & 0xff) != 0;
+      v = (float)(negative ? -byte : byte);
+    } else {
+      v = (float)byte;
+    }
+    float x = fmul(scale, v);
+    if (has_minimums<TY>()) x = fsub(x, least);
+    to[j] = x;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// sb_tables, sums_x, signed_dots
+// ---------------------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void sb_tables_kernel(uint8_t *area, const uint8_t *codebooks) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < GRIDS) area[i] = (uint8_t)(codebooks[i] + (i >= T_IQ1S ? 1 : 0));
+  if (i < 128 * 8) {  // the signs of 8 weights by a 7-bit index; the eighth makes the count of minus signs even
+    const int idx = i >> 3, j = i & 7;
+    const int held = idx | ((__builtin_popcount(idx) & 1) << 7);
+    area[T_SIGNS + i] = ((held >> j) & 1) ? 255 : 0;
+  }
+  if (i < 16) {
+    const int8_t v = (int8_t)codebooks[GRIDS + i];
+    area[T_IQ4 + i] = (uint8_t)v;
+    area[T_IQ4 + 16 + i] = (uint8_t)(int8_t)(v < 0 ? -v : v);
+    area[T_IQ4 + 32 + i] = v < 0 ? 255 : 0;
+    uint8_t *vec = area + T_VECTORS;
+    vec[0 + i] = (uint8_t)(1u << (i & 7));
+    vec[16 + i] = (uint8_t)(i >> 3);
+    vec[32 + i] = 3;
+    vec[48 + i] = 15;
+    vec[80 + i] = 7;
+    vec[96 + i] = 1;
+  }
+  if (i < 4) {
+    ((int32_t *)(area + T_VECTORS + 64))[i] = 512 >> (3 * i);
+    ((int32_t *)(area + T_VECTORS + 112))[i] = 4096 >> (4 * i);
+  }
+}
+
+// a thread per 16 activations of a token: its two sums of 8 and its sum of 16 (int16)
+__global__ __launch_bounds__(256) void sums_x_kernel(char *xs, const char *xq, int32_t n, int64_t total, int64_t frame) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  const int32_t per = n >> 4;
+  const int64_t t = i / per;
+  const int32_t u = (int32_t)(i - t * per);
+  const int8_t *a = (const int8_t *)(xq + t * frame) + 16 * u;
+  int32_t s0 = 0, s1 = 0;
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    s0 += a[j];
+    s1 += a[8 + j];
+  }
+  int16_t *s16 = (int16_t *)(xs + t * frame + 4 * (n >> 5)), *s8 = s16 + (n >> 4);
+  s16[u] = (int16_t)(s0 + s1);
+  s8[2 * u] = (int16_t)s0;
+  s8[2 * u + 1] = (int16_t)s1;
+}
+
+__global__ void signed_dots_kernel(int32_t *out, const int8_t *a, const int8_t *b) {
+  const int k = threadIdx.x;
+  if (k < 4) {
+    int32_t s = 0;
+    for (int j = 0; j < 4; j++) s += (int32_t)a[4 * k + j] * (int32_t)b[4 * k + j];
+    out[k] = s;
+  }
+}
+
+}  // namespace
+
+hipError_t launch_sb_tables(uint8_t *area, const uint8_t *codebooks, hipStream_t s) {
+  hipLaunchKernelGGL(sb_tables_kernel, dim3((GRIDS + 255) / 256), dim3(256), 0, s, area, codebooks);
+  return hipGetLastError();
+}
+
+hipError_t launch_sums_x(char *xs, const char *xq, int32_t n, int32_t count, int64_t frame, hipStream_t s) {
+  const int64_t total = (int64_t)count * (n >> 4);
+  if (total <= 0) return hipSuccess;
+  hipLaunchKernelGGL(sums_x_kernel, dim3((uint32_t)((total + 255) / 256)), dim3(256), 0, s, xs, xq, n, total, frame);
+  return hipGetLastError();
+}
+
+hipError_t launch_signed_dots(int32_t *out, const int8_t *a, const int8_t *b, hipStream_t s) {
+  hipLaunchKernelGGL(signed_dots_kernel, dim3(1), dim3(64), 0, s, out, a, b);
+  return hipGetLastError();
+}
+
+hipError_t launch_sb_row(float *out, const char *w, const uint8_t *tab, int32_t n, int32_t type, hipStream_t s) {
+  const int64_t chunks = n >> 4;
+  if (chunks <= 0) return hipSuccess;
+  const dim3 grid((uint32_t)((chunks + 255) / 256)), block(256);
+  switch (type) {
+  case Q2_K: hipLaunchKernelGGL(sb_row_kernel<Q2_K>, grid, block, 0, s, out, w, tab, n); break;
+  case Q4_K: hipLaunchKernelGGL(sb_row_kernel<Q4_K>, grid, block, 0, s, out, w, tab, n); break;
+  case IQ2_XXS: hipLaunchKernelGGL(sb_row_kernel<IQ2_XXS>, grid, block, 0, s, out, w, tab, n); break;
+  case IQ2_XS: hipLaunchKernelGGL(sb_row_kernel<IQ2_XS>, grid, block, 0, s, out, w, tab, n); break;
+  case IQ2_S: hipLaunchKernelGGL(sb_row_kernel<IQ2_S>, grid, block, 0, s, out, w, tab, n); break;
+  case IQ3_XXS: hipLaunchKernelGGL(sb_row_kernel<IQ3_XXS>, grid, block, 0, s, out, w, tab, n); break;
+  case IQ3_S: hipLaunchKernelGGL(sb_row_kernel<IQ3_S>, grid, block, 0, s, out, w, tab, n); break;
+  case IQ1_S: hipLaunchKernelGGL(sb_row_kernel<IQ1_S>, grid, block, 0, s, out, w, tab, n); break;
+  case IQ1_M: hipLaunchKernelGGL(sb_row_kernel<IQ1_M>, grid, block, 0, s, out, w, tab, n); break;
+  case IQ4_XS: hipLaunchKernelGGL(sb_row_kernel<IQ4_XS>, grid, block, 0, s, out, w, tab, n); break;
+  default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+// jobs: one block type, one token count (1..4)
+hipError_t launch_sb(const Job *jobs, int32_t njobs, hipStream_t s) {
+  if (njobs < 1 || njobs > kMaxJobs) return hipErrorInvalidValue;
+  SbBatch b{};
+  int blocks = 0;
+  constexpr int rpb = 256 / kSbLanes;
+  for (int j = 0; j < njobs; j++) {
+    b.job[j] = jobs[j];
+    b.block0[j] = blocks;
+    blocks += (jobs[j].r1 - jobs[j].r0 + rpb - 1) / rpb;
+  }
+  b.block0[njobs] = blocks;
+  b.njobs = njobs;
+  if (blocks == 0) return hipSuccess;
+  const int T = jobs[0].count;
+  switch (jobs[0].type) {
+  case Q2_K: return launch_type<Q2_K>(b, blocks, T, s);
+  case Q4_K: return launch_type<Q4_K>(b, blocks, T, s);
+  case IQ2_XXS: return launch_type<IQ2_XXS>(b, blocks, T, s);
+  case IQ2_XS: return launch_type<IQ2_XS>(b, blocks, T, s);
+  case IQ2_S: return launch_type<IQ2_S>(b, blocks, T, s);
+  case IQ3_XXS: return launch_type<IQ3_XXS>(b, blocks, T, s);
+  case IQ3_S: return launch_type<IQ3_S>(b, blocks, T, s);
+  case IQ1_S: return launch_type<IQ1_S>(b, blocks, T, s);
+  case IQ1_M: return launch_type<IQ1_M>(b, blocks, T, s);
+  case IQ4_XS: return launch_type<IQ4_XS>(b, blocks, T, s);
+  default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace hq

@@ -15,6 +15,7 @@ constexpr int GS = 32;  // int8 quantization group (kernels/kernel/math.ts:4)
 HQ_DEV float fmul(float a, float b) { return __fmul_rn(a, b); }
 HQ_DEV float fadd(float a, float b) { return __fadd_rn(a, b); }
 HQ_DEV float fdiv(float a, float b) { return __fdiv_rn(a, b); }
+HQ_DEV float fsub(float a, float b) { return __fsub_rn(a, b); }
 
 // v_dot4_i32_i8: c + the four products of signed bytes (exact in int32 for every byte)
 HQ_DEV int32_t sdot4(int32_t a, int32_t b, int32_t c) { return __builtin_amdgcn_sdot4(a, b, c, false); }

@@ -21,6 +21,7 @@
 // Rows past r1 in a block compute on a clamped row and store nothing (DPP needs the whole row of lanes live).
 #include "common.hpp"
 #include "launch.hpp"
+#include "fold.hpp"
 
 #define HQ_HOST_DEV __host__ __device__
 
@@ -347,30 +348,6 @@ HQ_DEV void fold_step(const Fold<T> &f, int buf, int slot, int lane, float acc[T
     float a = acc[t];
 #pragma unroll
     for (int q = 0; q < 4; q++) {
-      const float4 v = src[q];
-      a = fadd(fadd(fadd(fadd(a, v.x), v.y), v.z), v.w);
-    }
-    acc[t] = a;
-  }
-}
-
-// the same for rows of L lanes (64 / L rows a wave): lane k (k < 4) of each row adds part k of the L groups in order
-template <int T, int L>
-struct FoldL {
-  float v[2][64 / L][T][4][L];
-};
-template <int T, int L>
-HQ_DEV void fold_step_l(const FoldL<T, L> &f, int buf, int slot, int lane, float acc[T]) {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  const int k = lane & 3;
-#pragma unroll
-  for (int t = 0; t < T; t++) {
-    const float4 *src = (const float4 *)f.v[buf][slot][t][k];
-    float a = acc[t];
-#pragma unroll
-    for (int q = 0; q < L / 4; q++) {
       const float4 v = src[q];
       a = fadd(fadd(fadd(fadd(a, v.x), v.y), v.z), v.w);
     }

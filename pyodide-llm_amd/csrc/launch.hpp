@@ -8,18 +8,30 @@ namespace hq {
 
 // one matrix-times-activations job: rows [r0, r1) of the weights at wq (scales ws, corrections wc or NULL) for
 // `count` tokens (activations at xq + t frame, their scales at xs + t sframe; outputs at out + t os, row i at + 4 i)
+// llama.cpp's blocks (the sb kinds): ws is the tables (sb_tables's area) and type the block type
 struct Job {
   char *out;
   const char *xq, *xs, *wq, *ws, *wc;
   int32_t n, r0, r1, count;
   int64_t os, frame, sframe;
+  int32_t type;
 };
 
 // a kind's number is its place in the reference's WORK (src/runtime/jobs.ts:207-336)
-enum Kind : int32_t { Q8R = 0, Q8 = 1, Q6R = 5, Q6 = 6, T2R = 8, T2 = 9, B1R = 13, B1 = 14 };
+enum Kind : int32_t { Q8R = 0, Q8 = 1, Q6R = 5, Q6 = 6, T2R = 8, T2 = 9, SBR = 10, SB = 11, SBW = 12, B1R = 13, B1 = 14 };
 // the kinds whose weights are signs and a float16 scale a group of 128 (ternary, binary): interleave()'s activations
 constexpr bool signs_kind(Kind k) { return k == T2R || k == T2 || k == B1R || k == B1; }
 constexpr bool binary_kind(Kind k) { return k == B1R || k == B1; }
+// llama.cpp's blocks of 256 weights (kernels/blocks/): matmul_sbr, matmul_sb (and matmul_sbw's numbers, the same)
+constexpr bool blocks_kind(Kind k) { return k == SBR || k == SB || k == SBW; }
+// the bytes of a block of a GGUF type (Q2_K 10, Q4_K 12, IQ2_XXS 16, IQ2_XS 17, IQ3_XXS 18, IQ1_S 19, IQ3_S 21,
+// IQ2_S 22, IQ4_XS 23, IQ1_M 29), 0 for another (kernels/blocks/types.ts:103-106)
+constexpr int32_t sb_block_bytes(int32_t type) {
+  return type == 16 ? 66 : type == 21 ? 110 : type == 17 ? 74 : type == 22 ? 82 : type == 18 ? 98 : type == 29 ? 56
+       : type == 19 ? 50 : type == 10 ? 84 : type == 23 ? 136 : type == 12 ? 144 : 0;
+}
+constexpr int32_t kSbTables = 34992;  // the bytes of sb_tables's area
+constexpr int32_t kSbCodebooks = 33808;  // the bytes of the codebooks row it is made of
 
 // activations: count tokens of n values (x + t x_stride) -> xq + t frame, xs + t frame
 hipError_t launch_quantize_x(char *xq, char *xs, const char *x, int32_t n, int32_t bias, int32_t count,
@@ -38,6 +50,15 @@ hipError_t launch_gemv(Kind kind, const Job *jobs, int32_t njobs, hipStream_t s)
 // (bias 64) into LDS itself; the jobs' xq / xs are not read
 hipError_t launch_gemv_fused(Kind kind, const Job *jobs, int32_t njobs, const char *x, int64_t x_stride,
                              hipStream_t s);
+
+// llama.cpp's blocks: the tables from the codebooks row; a token's sums of 16 and 8 after its scales (count tokens,
+// frame apart); a row as float32; the products (jobs of the sb kinds, 1..4 tokens, up to kMaxJobs a launch); the
+// four lanes of the signed dot product of 16 bytes by 16
+hipError_t launch_sb_tables(uint8_t *area, const uint8_t *codebooks, hipStream_t s);
+hipError_t launch_sums_x(char *xs, const char *xq, int32_t n, int32_t count, int64_t frame, hipStream_t s);
+hipError_t launch_sb_row(float *out, const char *w, const uint8_t *tab, int32_t n, int32_t type, hipStream_t s);
+hipError_t launch_sb(const Job *jobs, int32_t njobs, hipStream_t s);
+hipError_t launch_signed_dots(int32_t *out, const int8_t *a, const int8_t *b, hipStream_t s);
 
 // MFMA GEMM-shaped products (one job a launch; count > 4 tokens): the tiles of matmul_q8r_tile, matmul_q6r and
 // matmul_t2r_tile over a prompt.  Returns hipErrorNotSupported for a kind that has none.

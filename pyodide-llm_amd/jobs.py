@@ -4,7 +4,7 @@ WORK's kinds keep their numbers (a kind's number is its place in jobs.ts's WORK,
 reference's forward pass writes (jobs.ts:36-46: [kind, out, a, b, a4, a5, a6, a7, a8, rows, count, os, as, bs, SIZE,
 FIRST]) is the one hq_phase() takes.  PACKED gives each weight packing's bytes, the kinds of its jobs, its corrections
 kernel and its activations' preparation (jobs.ts:396-444).  Kinds this library does not run (attention, the delta
-rule, float32 rows, llama.cpp's blocks) keep their numbers and are refused by hq_phase.
+rule, float32 rows) keep their numbers and are refused by hq_phase.
 """
 import ctypes
 from dataclasses import dataclass
@@ -27,7 +27,14 @@ RUN = {
     "matmul_t2": dict(relaxed=False, tile=False, row_bytes=lambda n: n // 4),
     "matmul_b1r": dict(relaxed=True, tile=True, row_bytes=lambda n: n // 8),
     "matmul_b1": dict(relaxed=False, tile=False, row_bytes=lambda n: n // 8),
+    # llama.cpp's blocks: the bytes of a row depend on the block type (BLOCK_TYPES), a job's a6
+    "matmul_sbr": dict(relaxed=True, tile=True, row_bytes=None),
+    "matmul_sb": dict(relaxed=False, tile=False, row_bytes=None),
+    "matmul_sbw": dict(relaxed=True, tile=True, row_bytes=None),
 }
+# jobs.ts:380-395 and kernels/blocks/types.ts:60-63: a block type's GGUF number and the bytes of its 256 weights
+BLOCK_TYPES = {"Q2_K": (10, 84), "Q4_K": (12, 144), "IQ2_XXS": (16, 66), "IQ2_XS": (17, 74), "IQ3_XXS": (18, 98),
+               "IQ1_S": (19, 50), "IQ3_S": (21, 110), "IQ2_S": (22, 82), "IQ4_XS": (23, 136), "IQ1_M": (29, 56)}
 JOB = 16            # numbers a job in the reference's table (jobs.ts:21)
 ROWS, COUNT = 9, 10  # jobs.ts:46
 THREE = 3           # jobs.ts:50

@@ -35,7 +35,9 @@ def test_reference_names_and_arities(pkg):
     names = declared()
     reference = {"quantize_x": 5, "int8_sums": 3, "six_sums": 3, "interleave": 3, "matmul_q8r": 9, "matmul_q8": 8,
                  "matmul_q8r_tile": 12, "matmul_q6r": 9, "matmul_q6": 8, "matmul_t2r": 9, "matmul_t2": 9,
-                 "matmul_t2r_tile": 12, "matmul_b1r": 9, "matmul_b1": 9, "matmul_b1r_tile": 12, "binary_x": 4}
+                 "matmul_t2r_tile": 12, "matmul_b1r": 9, "matmul_b1": 9, "matmul_b1r_tile": 12, "binary_x": 4,
+                 "sb_tables": 2, "sums_x": 3, "matmul_sbr": 9, "matmul_sb": 9, "matmul_sbr_tile": 12,
+                 "matmul_sbw_tile": 13, "signed_dots": 3, "sb_row": 5}
     for name, arity in reference.items():
         assert names[name] == arity, name
         assert len(pkg.REFERENCE_SIGNATURES[name]) == arity, name
@@ -58,6 +60,14 @@ def test_version(pkg):
     (lambda L: L.hq_matmul_b1r_tile_ex(16, 16, 16, 16, 16, 128, 0, 1, 2, 4, 8, 2, None), 2, "frame"),
     (lambda L: L.hq_binary_x_ex(16, 16, 16, 100, None, None), 1, "multiple of 128"),
     (lambda L: L.hq_binary_x_ex(16, 16, 8, 128, None, None), 2, "aligned"),
+    (lambda L: L.hq_matmul_sbr_ex(16, 16, 16, 16, 16, 256, 0, 1, 11, None), 1, "type 11"),
+    (lambda L: L.hq_matmul_sbr_ex(16, 16, 16, 16, 16, 384, 0, 1, 12, None), 1, "multiple of 256"),
+    (lambda L: L.hq_matmul_sbr_ex(16, 16, 16, 17, 16, 256, 0, 1, 12, None), 2, "w not 2-byte"),
+    (lambda L: L.hq_matmul_sbr_ex(16, 16, 16, 16, 8, 256, 0, 1, 12, None), 2, "tables"),
+    (lambda L: L.hq_matmul_sbr_ex(16, 16, 8, 16, 16, 256, 0, 1, 12, None), 2, "xq or xs"),
+    (lambda L: L.hq_matmul_sbr_tile_ex(16, 16, 16, 16, 16, 256, 0, 1, 2, 4, 8, 12, None), 2, "token stride"),
+    (lambda L: L.hq_sb_row_ex(16, 16, 16, 100, 16, None), 1, "multiple of 256"),
+    (lambda L: L.hq_sums_x_batch(16, 16, 100, 1, 0, None), 1, "multiple of"),
     (lambda L: L.hq_matmul_q8_ex(16, 17, 16, 16, 16, 64, 0, 1, None), 2, "xq"),
     (lambda L: L.hq_matmul_q6_ex(16, 16, 16, 12, 16, 64, 0, 1, None), 2, "wq"),
     (lambda L: L.hq_matmul_q8r_tile_ex(16, 16, 16, 16, 16, 16, 64, 0, 1, 3, 4, 8, None), 2, "frame"),
@@ -105,14 +115,21 @@ def test_phase_refuses_other_kinds_and_bad_numbers(pkg):
     assert jobs.phase(L, [odd]) == pkg.HQ_ERR_ARGUMENT
     odd = jobs.job("matmul_b1", 16, 16, 16, 16, 16, 0, 64, rows=4)
     assert jobs.phase(L, [odd]) == pkg.HQ_ERR_ARGUMENT
+    untyped = jobs.job("matmul_sbr", 16, 16, 16, 16, 16, 11, 256, rows=4)
+    assert jobs.phase(L, [untyped]) == pkg.HQ_ERR_ARGUMENT
+    assert "type 11" in L.hq_last_error_message().decode()
     assert jobs.phase(L, []) == 0
 
 
 def test_work_numbers_match_the_reference():
-    """KIND is each kind's place in jobs.ts's WORK (jobs.ts:207-336); hq.h names 0, 1, 5, 6, 8, 9, 13, 14."""
+    """KIND is each kind's place in jobs.ts's WORK (jobs.ts:207-336); hq.h names 0, 1, 5, 6, 8..14."""
     from pyodide_llm_amd import jobs
     assert [jobs.KIND[k] for k in ("matmul_q8r", "matmul_q8", "matmul_q6r", "matmul_q6", "matmul_t2r", "matmul_t2",
-                                   "matmul_b1r", "matmul_b1")] == [0, 1, 5, 6, 8, 9, 13, 14]
+                                   "matmul_sbr", "matmul_sb", "matmul_sbw", "matmul_b1r", "matmul_b1")] == \
+        [0, 1, 5, 6, 8, 9, 10, 11, 12, 13, 14]
+    assert {name: jobs.BLOCK_TYPES[name][0] for name in jobs.BLOCK_TYPES} == \
+        {"Q2_K": 10, "Q4_K": 12, "IQ2_XXS": 16, "IQ2_XS": 17, "IQ3_XXS": 18, "IQ1_S": 19, "IQ3_S": 21, "IQ2_S": 22,
+         "IQ4_XS": 23, "IQ1_M": 29}
     assert jobs.PACKED["int8"].weight_bytes() == 1.125
     assert jobs.PACKED["int6"].weight_bytes() == 0.875
     assert jobs.PACKED["ternary"].weight_bytes() == 0.265625
