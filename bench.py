@@ -338,6 +338,96 @@ def measure_configs(torch, pkg, args):
         decode(f"{tag} {kind} M=1, gate+up x {copies}", kind, [[(17408, 5120), (17408, 5120)]], copies)
         decode(f"{tag} {kind} M=1, down x {copies}", kind, [[(5120, 17408)]], copies)
         prefill(f"{tag} {kind} prefill M=256", kind, [(17408, 5120), (17408, 5120), (5120, 17408)], 256)
+    out.update(measure_blocks(torch, pkg, args, gen))
+    return out
+
+
+# where each block type keeps its float16 scales (kernels/blocks/types.ts:60-79): set to 2^-7 in the synthetic
+# blocks so that every product is finite; IQ1_M's is spread over the top nibbles of the words at 48..55
+BLOCK_SCALES = {10: (80, 82), 12: (0, 2), 16: (0,), 17: (0,), 18: (0,), 19: (0,), 21: (0,), 22: (0,), 23: (0,)}
+
+
+def measure_blocks(torch, pkg, args, gen):
+    """llama.cpp's blocks (job kinds 10-12) at Llama-3-8B's MLP shapes: the token product (M = 1; copies of the
+    weights past the Infinity Cache) in GB/s of algorithmic bytes (the blocks, the activations and the sums of 16
+    or 8 the type reads, the outputs) and a prompt of 64 tokens in TOPS.  Random blocks (random bytes, sane
+    scales), random codebooks."""
+    from pyodide_llm_amd import jobs
+    lib = pkg.library()
+    dev = "cuda:0"
+    reps = max(3, args.steps // 2)
+    out = {}
+    tab = torch.empty(34992, dtype=torch.uint8, device=dev)
+    books = torch.randint(0, 256, (33808,), dtype=torch.uint8, device=dev, generator=gen)
+    pkg.check(lib.hq_sb_tables_ex(tab.data_ptr(), books.data_ptr(), None))
+
+    def acts(n, count=1):
+        x = torch.randn(count, n, device=dev, generator=gen)
+        frame = (n + n // 2 + 15) // 16 * 16
+        buf = torch.empty(count * frame, dtype=torch.uint8, device=dev)
+        pkg.check(lib.hq_quantize_x_batch(buf.data_ptr(), buf.data_ptr() + n, x.data_ptr(), n, 0, count, frame,
+                                          4 * n, None))
+        pkg.check(lib.hq_sums_x_batch(buf.data_ptr() + n, buf.data_ptr(), n, count, frame, None))
+        return buf, frame
+
+    def weights(t, size, rows, n):
+        w = torch.randint(0, 256, (rows * (n // 256), size), dtype=torch.uint8, device=dev, generator=gen)
+        for at in BLOCK_SCALES.get(t, ()):
+            w[:, at], w[:, at + 1] = 0x00, 0x20
+        if t == 29:  # 0x2000: the nibbles 0, 0, 0, 2 at the tops of the four words
+            for k, nib in enumerate((0, 0, 0, 2)):
+                w[:, 49 + 2 * k] = (w[:, 49 + 2 * k] & 0x0F) | (nib << 4)
+        return w
+
+    def act_bytes(t, n):
+        """per token: xq, the scales, and the sums of 16 (the K types) or of 8 (IQ1)"""
+        return n + n // 8 + (n // 8 if t in (10, 12) else n // 4 if t in (19, 29) else 0)
+
+    shapes = [(14336, 4096), (14336, 4096), (4096, 14336)]
+    for name, (t, size) in jobs.BLOCK_TYPES.items():
+        per_layer = sum(rows * (n // 256) * size for rows, n in shapes)
+        copies = max(2, -(-1_200_000_000 // per_layer))
+        a = {n: acts(n) for _, n in shapes}
+        tables, total, keep = [], 0.0, []
+        for _ in range(copies):
+            entries = []
+            for rows, n in shapes:
+                w = weights(t, size, rows, n)
+                o = torch.empty(rows, device=dev)
+                keep += [w, o]
+                buf, _ = a[n]
+                entries.append(jobs.job("matmul_sbr", o.data_ptr(), buf.data_ptr(), buf.data_ptr() + n, w.data_ptr(),
+                                        tab.data_ptr(), t, n, rows=rows))
+                total += rows * (n // 256) * size + act_bytes(t, n) + 4 * rows
+            # gate and up in one phase, down in the next (their launches as the forward pass makes them)
+            tables.append((jobs.table(entries[:2]), 2))
+            tables.append((jobs.table(entries[2:]), 1))
+
+        def launch(h):
+            for tb, nj in tables:
+                lib.hq_phase(tb, nj, 16, h)
+        sec = _graph_time(torch, launch, reps)
+        pkg.check(lib.hq_last_error())
+        out[f"8B MLP {name} M=1 x {copies}"] = {"GBps": round(total / sec / 1e9, 1),
+                                                  "us_per_layer": round(1e6 * sec / copies, 2), "bytes": total}
+        del keep, tables
+        # a prompt of 64 tokens through one layer's MLP (the tile: 4 tokens a launch)
+        count = 64
+        entries, keep = [], []
+        for rows, n in shapes:
+            w = weights(t, size, rows, n)
+            buf, frame = acts(n, count)
+            o = torch.empty(count, rows, device=dev)
+            keep += [w, buf, o]
+            entries.append(jobs.job("matmul_sbr", o.data_ptr(), buf.data_ptr(), buf.data_ptr() + n, w.data_ptr(),
+                                    tab.data_ptr(), t, n, rows=rows, count=count, os=4 * rows, as_=frame, bs=frame))
+        tb = jobs.table(entries)
+        ops = sum(2.0 * count * rows * n for rows, n in shapes)
+        sec = _graph_time(torch, lambda h: lib.hq_phase(tb, len(entries), 16, h), reps)
+        pkg.check(lib.hq_last_error())
+        out[f"8B MLP {name} prompt M={count}"] = {"TOPS": round(ops / sec / 1e12, 2), "ms": round(1e3 * sec, 3)}
+        del keep
+        torch.cuda.empty_cache()
     return out
 
 

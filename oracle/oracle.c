@@ -505,6 +505,9 @@ typedef struct {
   float F, Fm, d;
 } sb_block;
 
+/* The grids' bytes are signed: the reference's plain dot product multiplies them with extmul_*_i8x16_s
+ * (types.ts:171-173). The converter's grids hold magnitudes of 0 to 127 (IQ1: codes 0, 1, 2), where the relaxed dot
+ * (types.ts:170) agrees; other bytes give the plain kernel's numbers. */
 static void sb_decode(const uint8_t *p, const uint8_t *tab, int32_t type, sb_block *B) {
   int32_t *S = B->S, *M = B->M;
   for (int h = 0; h < 16; h++) {
@@ -516,7 +519,7 @@ static void sb_decode(const uint8_t *p, const uint8_t *tab, int32_t type, sb_blo
       const uint8_t *q = p + 2 + 8 * (h >> 1) + 2 * (h & 1);
       const uint32_t aux = u32_at(p + 6 + 8 * (h >> 1)) >> (14 * (h & 1));
       for (int j = 0; j < 16; j++) {
-        mag[j] = tab[8 * q[j >> 3] + (j & 7)];
+        mag[j] = (int8_t)tab[8 * q[j >> 3] + (j & 7)];
         neg[j] = tab[T_SIGNS + 8 * ((aux >> (7 * (j >> 3))) & 127) + (j & 7)] != 0;
       }
       S[h] = (int32_t)((u32_at(p + 6 + 8 * g) >> 27) | 1);
@@ -526,7 +529,7 @@ static void sb_decode(const uint8_t *p, const uint8_t *tab, int32_t type, sb_blo
       const uint8_t *q = p + 2 + 4 * h;
       for (int j = 0; j < 16; j++) {
         const uint32_t word = u16_at(q + 2 * (j >> 3));
-        mag[j] = tab[T_IQ2XS + 8 * (word & 511) + (j & 7)];
+        mag[j] = (int8_t)tab[T_IQ2XS + 8 * (word & 511) + (j & 7)];
         neg[j] = tab[T_SIGNS + 8 * (word >> 9) + (j & 7)] != 0;
       }
       S[h] = (int32_t)((((p[66 + g] >> (4 * (h & 1))) & 15) << 1) | 1);
@@ -537,7 +540,7 @@ static void sb_decode(const uint8_t *p, const uint8_t *tab, int32_t type, sb_blo
       const uint32_t high = p[66 + (h >> 1)] >> (4 * (h & 1)), bits = u16_at(p + 34 + 2 * h);
       const uint32_t idx[2] = {q[0] | ((high & 3) << 8), q[1] | ((high & 12) << 6)};
       for (int j = 0; j < 16; j++) {
-        mag[j] = tab[T_IQ2S + 8 * idx[j >> 3] + (j & 7)];
+        mag[j] = (int8_t)tab[T_IQ2S + 8 * idx[j >> 3] + (j & 7)];
         neg[j] = (bits >> j) & 1;
       }
       S[h] = (int32_t)((((p[74 + g] >> (4 * (h & 1))) & 15) << 1) | 1);
@@ -547,7 +550,7 @@ static void sb_decode(const uint8_t *p, const uint8_t *tab, int32_t type, sb_blo
       const uint8_t *q = p + 2 + 4 * h;
       const uint32_t aux = u32_at(p + 66 + 4 * (h >> 1)) >> (14 * (h & 1));
       for (int j = 0; j < 16; j++) {
-        mag[j] = tab[T_IQ3XXS + 4 * q[j >> 2] + (j & 3)];
+        mag[j] = (int8_t)tab[T_IQ3XXS + 4 * q[j >> 2] + (j & 3)];
         neg[j] = tab[T_SIGNS + 8 * ((aux >> (7 * (j >> 3))) & 127) + (j & 7)] != 0;
       }
       S[h] = (int32_t)((u32_at(p + 66 + 4 * g) >> 27) | 1);
@@ -558,7 +561,7 @@ static void sb_decode(const uint8_t *p, const uint8_t *tab, int32_t type, sb_blo
       const uint32_t high = p[66 + (h >> 1)] >> (4 * (h & 1)), bits = u16_at(p + 74 + 2 * h);
       for (int j = 0; j < 16; j++) {
         const int t = j >> 2;
-        mag[j] = tab[T_IQ3S + 4 * (q[t] | (((high >> t) & 1) << 8)) + (j & 3)];
+        mag[j] = (int8_t)tab[T_IQ3S + 4 * (q[t] | (((high >> t) & 1) << 8)) + (j & 3)];
         neg[j] = (bits >> j) & 1;
       }
       S[h] = (int32_t)((((p[106 + (g >> 1)] >> (4 * ((h >> 1) & 1))) & 15) << 1) | 1);
@@ -569,7 +572,7 @@ static void sb_decode(const uint8_t *p, const uint8_t *tab, int32_t type, sb_blo
       const uint32_t word = u16_at(p + 34 + 2 * (h >> 1)), high = word >> (6 * (h & 1));
       const uint32_t idx[2] = {q[0] | ((high & 7) << 8), q[1] | ((high & 56) << 5)};
       for (int j = 0; j < 16; j++) {
-        mag[j] = tab[T_IQ1S + 8 * idx[j >> 3] + (j & 7)];
+        mag[j] = (int8_t)tab[T_IQ1S + 8 * idx[j >> 3] + (j & 7)];
         down[j] = (int)(word >> 15);
       }
       S[h] = (int32_t)((((word >> 12) & 7) << 1) | 1);
@@ -580,7 +583,7 @@ static void sb_decode(const uint8_t *p, const uint8_t *tab, int32_t type, sb_blo
       const uint32_t high = p[32 + h];
       const uint32_t idx[2] = {q[0] | ((high & 7) << 8), q[1] | ((high & 0x70) << 4)};
       for (int j = 0; j < 16; j++) {
-        mag[j] = tab[T_IQ1S + 8 * idx[j >> 3] + (j & 7)];
+        mag[j] = (int8_t)tab[T_IQ1S + 8 * idx[j >> 3] + (j & 7)];
         down[j] = (int)(j < 8 ? (high >> 3) & 1 : high >> 7);
       }
       S[h] = (int32_t)((((u16_at(p + 48 + 2 * (h >> 2)) >> (3 * (h & 3))) & 7) << 1) | 1);
@@ -702,10 +705,12 @@ void o_sb_row(float *out, const uint8_t *w, const uint8_t *tab, int32_t n, int32
       for (int j = 0; j < 16; j++) {
         const int i = 16 * h + j;
         float v;
+        /* W as an int8 (row.ts:32-37: the signs put on the magnitudes with i8x16.sub, IQ1's code less 1 with
+         * i8x16.sub (row.ts:24), both wrapping: only a grid byte of -128 shows it) */
         if (type == SB_IQ1_S || type == SB_IQ1_M)  /* the grid's -1, 0, 1 and an eighth more or less (row.ts:22-31) */
-          v = (float)(B.code[i] - 1) + (B.down[i] ? -0.125f : 0.125f);
+          v = (float)(int8_t)(B.code[i] - 1) + (B.down[i] ? -0.125f : 0.125f);
         else
-          v = (float)B.W[i];
+          v = (float)(int8_t)B.W[i];
         float x = scale * v;
         if (type == SB_Q2_K || type == SB_Q4_K) {
           const float least = B.Fm * (float)B.M[h];

@@ -189,6 +189,7 @@ def binary_x(x):
 SB_TYPES = {"Q2_K": 10, "Q4_K": 12, "IQ2_XXS": 16, "IQ2_XS": 17, "IQ3_XXS": 18, "IQ1_S": 19, "IQ3_S": 21,
             "IQ2_S": 22, "IQ4_XS": 23, "IQ1_M": 29}
 SB_TABLES = 34992
+SB_CODEBOOKS = 33808  # the codebooks row (src/python/engine/dtypes.py CODEBOOKS)
 
 
 def sb_bytes(type_):

@@ -142,7 +142,7 @@ int32_t check_job(hq::Kind kind, const hq::Job &j, int32_t three) {
 // GEMM jobs one a launch
 int32_t run_blocks(hq::Kind kind, const std::vector<hq::Job> &jobs, hipStream_t s) {
   // up to 4 tokens a launch (a prompt in slices of 4: every (row, token) the token kernel's number), jobs of one
-  // block type and one token count together
+  // block type, one token count and one tables' area together
   std::vector<hq::Job> parts;
   for (const hq::Job &j : jobs) {
     if (j.r1 == j.r0 || j.count == 0) continue;
@@ -160,7 +160,7 @@ int32_t run_blocks(hq::Kind kind, const std::vector<hq::Job> &jobs, hipStream_t 
     if (done[i]) continue;
     std::vector<hq::Job> same;
     for (size_t k = i; k < parts.size() && same.size() < (size_t)hq::kMaxJobs; k++)
-      if (!done[k] && parts[k].type == parts[i].type && parts[k].count == parts[i].count) {
+      if (!done[k] && parts[k].type == parts[i].type && parts[k].count == parts[i].count && parts[k].ws == parts[i].ws) {
         same.push_back(parts[k]);
         done[k] = true;
       }

@@ -5,8 +5,9 @@
 //   (tile.ts:158-162).
 //
 // A weight is F S W - Fm M (types.ts:32-47).  Every block is decoded 16 weights at a time (a "chunk" h = 0..15) into
-// four dwords of W's bytes and its unit's integers, in registers, as the reference reads it (the grids, the sign
-// table and IQ4_XS's values from sb_tables's area, read through the caches).  A chunk's integer is exact in int32:
+// four dwords of W's bytes and its unit's integers, in registers, as the reference reads it (the type's grid and
+// the sign table from sb_tables's area, copied into LDS; IQ4_XS's 16 values in registers).  A chunk's integer is
+// exact in int32:
 //   signed grids:  dot(|W|, a) - 2 dot(|W| of the negative weights, a)  (the sign on the weight, not on a byte add)
 //   IQ4_XS, K:     dot(W, a)  (IQ4_XS's W signed, the K types' 0..3 / 0..15)
 //   IQ1:           8 dot(code, a) - (7 or 9) (the sum of each 8 activations), by the shift of the 8 (token.ts:93-110)
@@ -78,8 +79,21 @@ struct Chunk {
   uint32_t down0, down1;
 };
 
+// the grid a type reads (its offset in sb_tables's area and its bytes) and whether it reads the sign table
+template <int TY> constexpr int grid_at() {
+  return TY == IQ2_XXS ? 0 : TY == IQ2_XS ? T_IQ2XS : TY == IQ2_S ? T_IQ2S : TY == IQ3_XXS ? T_IQ3XXS
+       : TY == IQ3_S ? T_IQ3S : is_iq1<TY>() ? T_IQ1S : 0;
+}
+template <int TY> constexpr int grid_bytes() {
+  return TY == IQ2_XXS ? 2048 : TY == IQ2_XS ? 4096 : TY == IQ2_S ? 8192 : TY == IQ3_XXS ? 1024 : TY == IQ3_S ? 2048
+       : is_iq1<TY>() ? 16384 : 0;
+}
+template <int TY> constexpr bool reads_signs() { return TY == IQ2_XXS || TY == IQ2_XS || TY == IQ3_XXS; }
+
+// grid: the type's grid (grid_at's bytes of the area, in LDS or in global memory); signs: the sign table (T_SIGNS)
 template <int TY, int BYTES>
-HQ_DEV void chunk(const BlockBytes<BYTES> &B, int h, const uint8_t *tab, const uint32_t iq4[4], Chunk &c) {
+HQ_DEV void chunk(const BlockBytes<BYTES> &B, int h, const uint8_t *grid, const uint8_t *signs, const uint32_t iq4[4],
+                  Chunk &c) {
   const int g = h >> 1;
   c.M = 0;
   c.down0 = c.down1 = 0;
@@ -87,23 +101,23 @@ HQ_DEV void chunk(const BlockBytes<BYTES> &B, int h, const uint8_t *tab, const u
   for (int j = 0; j < 4; j++) c.neg[j] = 0;
   if (TY == IQ2_XXS) {  // types.ts:197-200, 227-230, 277
     const int at = 2 + 8 * (h >> 1) + 2 * (h & 1);
-    const uint2 e0 = entry8(tab, 8 * (int)B.u8(at)), e1 = entry8(tab, 8 * (int)B.u8(at + 1));
+    const uint2 e0 = entry8(grid, 8 * (int)B.u8(at)), e1 = entry8(grid, 8 * (int)B.u8(at + 1));
     c.mag[0] = e0.x; c.mag[1] = e0.y; c.mag[2] = e1.x; c.mag[3] = e1.y;
     const uint32_t word = B.u32(6 + 8 * (h >> 1)), aux = word >> (14 * (h & 1));
-    const uint2 s0 = entry8(tab, T_SIGNS + 8 * (int)(aux & 127)), s1 = entry8(tab, T_SIGNS + 8 * (int)((aux >> 7) & 127));
+    const uint2 s0 = entry8(signs, 8 * (int)(aux & 127)), s1 = entry8(signs, 8 * (int)((aux >> 7) & 127));
     c.neg[0] = s0.x; c.neg[1] = s0.y; c.neg[2] = s1.x; c.neg[3] = s1.y;
     c.S = (int32_t)((word >> 27) | 1);
   } else if (TY == IQ2_XS) {  // types.ts:201-204, 232-235, 279
     const uint32_t w0 = B.u16(2 + 4 * h), w1 = B.u16(4 + 4 * h);
-    const uint2 e0 = entry8(tab, T_IQ2XS + 8 * (int)(w0 & 511)), e1 = entry8(tab, T_IQ2XS + 8 * (int)(w1 & 511));
+    const uint2 e0 = entry8(grid, 8 * (int)(w0 & 511)), e1 = entry8(grid, 8 * (int)(w1 & 511));
     c.mag[0] = e0.x; c.mag[1] = e0.y; c.mag[2] = e1.x; c.mag[3] = e1.y;
-    const uint2 s0 = entry8(tab, T_SIGNS + 8 * (int)(w0 >> 9)), s1 = entry8(tab, T_SIGNS + 8 * (int)(w1 >> 9));
+    const uint2 s0 = entry8(signs, 8 * (int)(w0 >> 9)), s1 = entry8(signs, 8 * (int)(w1 >> 9));
     c.neg[0] = s0.x; c.neg[1] = s0.y; c.neg[2] = s1.x; c.neg[3] = s1.y;
     c.S = (int32_t)((((B.u8(66 + g) >> (4 * (h & 1))) & 15) << 1) | 1);
   } else if (TY == IQ2_S) {  // types.ts:205-208, 237, 280
     const uint32_t high = B.u8(66 + (h >> 1)) >> (4 * (h & 1));
     const uint32_t i0 = B.u8(2 + 2 * h) | ((high & 3) << 8), i1 = B.u8(3 + 2 * h) | ((high & 12) << 6);
-    const uint2 e0 = entry8(tab, T_IQ2S + 8 * (int)i0), e1 = entry8(tab, T_IQ2S + 8 * (int)i1);
+    const uint2 e0 = entry8(grid, 8 * (int)i0), e1 = entry8(grid, 8 * (int)i1);
     c.mag[0] = e0.x; c.mag[1] = e0.y; c.mag[2] = e1.x; c.mag[3] = e1.y;
     const uint32_t bits = B.u16(34 + 2 * h);
 #pragma unroll
@@ -111,16 +125,16 @@ HQ_DEV void chunk(const BlockBytes<BYTES> &B, int h, const uint8_t *tab, const u
     c.S = (int32_t)((((B.u8(74 + g) >> (4 * (h & 1))) & 15) << 1) | 1);
   } else if (TY == IQ3_XXS) {  // types.ts:209-212, 227-230, 278
 #pragma unroll
-    for (int j = 0; j < 4; j++) c.mag[j] = entry4(tab, T_IQ3XXS + 4 * (int)B.u8(2 + 4 * h + j));
+    for (int j = 0; j < 4; j++) c.mag[j] = entry4(grid, 4 * (int)B.u8(2 + 4 * h + j));
     const uint32_t word = B.u32(66 + 4 * (h >> 1)), aux = word >> (14 * (h & 1));
-    const uint2 s0 = entry8(tab, T_SIGNS + 8 * (int)(aux & 127)), s1 = entry8(tab, T_SIGNS + 8 * (int)((aux >> 7) & 127));
+    const uint2 s0 = entry8(signs, 8 * (int)(aux & 127)), s1 = entry8(signs, 8 * (int)((aux >> 7) & 127));
     c.neg[0] = s0.x; c.neg[1] = s0.y; c.neg[2] = s1.x; c.neg[3] = s1.y;
     c.S = (int32_t)((word >> 27) | 1);
   } else if (TY == IQ3_S) {  // types.ts:213-217, 238, 281
     const uint32_t high = B.u8(66 + (h >> 1)) >> (4 * (h & 1));
 #pragma unroll
     for (int j = 0; j < 4; j++)
-      c.mag[j] = entry4(tab, T_IQ3S + 4 * (int)(B.u8(2 + 4 * h + j) | (((high >> j) & 1) << 8)));
+      c.mag[j] = entry4(grid, 4 * (int)(B.u8(2 + 4 * h + j) | (((high >> j) & 1) << 8)));
     const uint32_t bits = B.u16(74 + 2 * h);
 #pragma unroll
     for (int j = 0; j < 4; j++) c.neg[j] = bit_bytes(bits, j);
@@ -128,14 +142,14 @@ HQ_DEV void chunk(const BlockBytes<BYTES> &B, int h, const uint8_t *tab, const u
   } else if (TY == IQ1_S) {  // types.ts:218-221, 260-261, 282
     const uint32_t word = B.u16(34 + 2 * (h >> 1)), high = word >> (6 * (h & 1));
     const uint32_t i0 = B.u8(2 + 2 * h) | ((high & 7) << 8), i1 = B.u8(3 + 2 * h) | ((high & 56) << 5);
-    const uint2 e0 = entry8(tab, T_IQ1S + 8 * (int)i0), e1 = entry8(tab, T_IQ1S + 8 * (int)i1);
+    const uint2 e0 = entry8(grid, 8 * (int)i0), e1 = entry8(grid, 8 * (int)i1);
     c.mag[0] = e0.x; c.mag[1] = e0.y; c.mag[2] = e1.x; c.mag[3] = e1.y;
     c.down0 = c.down1 = word >> 15;
     c.S = (int32_t)((((word >> 12) & 7) << 1) | 1);
   } else if (TY == IQ1_M) {  // types.ts:222-225, 262-264, 283
     const uint32_t high = B.u8(32 + h);
     const uint32_t i0 = B.u8(2 * h) | ((high & 7) << 8), i1 = B.u8(2 * h + 1) | ((high & 0x70) << 4);
-    const uint2 e0 = entry8(tab, T_IQ1S + 8 * (int)i0), e1 = entry8(tab, T_IQ1S + 8 * (int)i1);
+    const uint2 e0 = entry8(grid, 8 * (int)i0), e1 = entry8(grid, 8 * (int)i1);
     c.mag[0] = e0.x; c.mag[1] = e0.y; c.mag[2] = e1.x; c.mag[3] = e1.y;
     c.down0 = (high >> 3) & 1;
     c.down1 = high >> 7;
@@ -186,134 +200,168 @@ HQ_DEV float block_fm(const BlockBytes<BYTES> &B) {
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// the products (matmul_sbr == matmul_sb): rows of 16 lanes, 16 rows a block, a block of 256 weights a lane a step
+// the products (matmul_sbr == matmul_sb): rows of 16 lanes, 4 rows a wave, a block of 256 weights a lane a step.
+// The blocks of a launch are persistent: each copies its type's grid and sign table (at most 17 KB) into LDS once,
+// and its waves take groups of 4 rows in turn.
 // ---------------------------------------------------------------------------------------------------------------
 struct SbBatch {
   Job job[kMaxJobs];
-  int32_t block0[kMaxJobs + 1];
+  int32_t unit0[kMaxJobs + 1];  // the first group of 4 rows of each job; unit0[njobs]: the groups of the launch
   int32_t njobs;
 };
 
-HQ_DEV int sb_job_of(const SbBatch &b, int blk) {
+HQ_DEV int sb_job_of(const SbBatch &b, int unit) {
   int j = 0;
-  while (j + 1 < b.njobs && blk >= b.block0[j + 1]) ++j;
+  while (j + 1 < b.njobs && unit >= b.unit0[j + 1]) ++j;
   return j;
 }
 
 constexpr int kSbLanes = 16;
+constexpr int kSbRowsPerWave = 64 / kSbLanes;
+
+template <int TY> constexpr int lds_table_bytes() {
+  return grid_bytes<TY>() + (reads_signs<TY>() ? 1024 : 0) > 0 ? grid_bytes<TY>() + (reads_signs<TY>() ? 1024 : 0)
+                                                                : 16;
+}
 
 template <int TY, int T>
 __global__ __launch_bounds__(256) void gemv_sb(SbBatch batch) {
   constexpr int L = kSbLanes;
   constexpr int BYTES = sb_block_bytes(TY);
+  constexpr int GRID = grid_bytes<TY>();
   __shared__ FoldL<T, L> fold[4];
-  const int jb = sb_job_of(batch, blockIdx.x);
-  const Job &J = batch.job[jb];
-  const int lane = threadIdx.x & (L - 1);
-  const int wave = threadIdx.x >> 6, slot = (threadIdx.x & 63) / L;
-  const int row_u = J.r0 + (blockIdx.x - batch.block0[jb]) * (256 / L) + threadIdx.x / L;
-  const bool live = row_u < J.r1;
-  const int row = live ? row_u : J.r1 - 1;
-  const int blocks = J.n >> 8;
-  const char *wrow = J.wq + (int64_t)row * blocks * BYTES;
-  const uint8_t *tab = (const uint8_t *)J.ws;
+  __shared__ __align__(16) uint8_t table[lds_table_bytes<TY>()];
+  const uint8_t *tab = (const uint8_t *)batch.job[0].ws;  // every job of a launch has the same tables' area
+  {
+    const uint4 *from = (const uint4 *)(tab + grid_at<TY>());
+    for (int i = threadIdx.x; i < GRID / 16; i += 256) ((uint4 *)table)[i] = from[i];
+    if (reads_signs<TY>())
+      for (int i = threadIdx.x; i < 1024 / 16; i += 256) ((uint4 *)(table + GRID))[i] = ((const uint4 *)(tab + T_SIGNS))[i];
+  }
   uint32_t iq4[4] = {0u, 0u, 0u, 0u};
   if (TY == IQ4_XS) {
     const uint4 v = *(const uint4 *)(tab + T_IQ4);
     iq4[0] = v.x; iq4[1] = v.y; iq4[2] = v.z; iq4[3] = v.w;
   }
-  // token t's activations (n int8), its scales (n / 32 float32), its sums of 16 and of 8 (int16)
-  const int8_t *xq[T];
-  const float *xs[T];
-  const int16_t *s16[T], *s8[T];
-#pragma unroll
-  for (int t = 0; t < T; t++) {
-    xq[t] = (const int8_t *)(J.xq + t * J.frame);
-    xs[t] = (const float *)(J.xs + t * J.sframe);
-    s16[t] = (const int16_t *)(xs[t] + (J.n >> 5));
-    s8[t] = s16[t] + (J.n >> 4);
-  }
+  __syncthreads();
+  const int lane = threadIdx.x & (L - 1);
+  const int wave = threadIdx.x >> 6, slot = (threadIdx.x & 63) / L;
   FoldL<T, L> &f = fold[wave];
-  float acc[T];
-#pragma unroll
-  for (int t = 0; t < T; t++) acc[t] = 0.0f;
-  const int steps = (blocks + L - 1) / L;
-  for (int it = 0; it < steps; it++) {
-    const int b = it * L + lane;
-    const bool valid = b < blocks;
-    const int bl = valid ? b : 0;
-    BlockBytes<BYTES> B;
-    B.load(wrow + (int64_t)bl * BYTES);
-    int32_t G[T][8], Mi[T][8];
-#pragma unroll
-    for (int t = 0; t < T; t++)
-#pragma unroll
-      for (int k = 0; k < 8; k++) G[t][k] = Mi[t][k] = 0;
-#pragma unroll
-    for (int h = 0; h < 16; h++) {
-      Chunk c;
-      chunk<TY>(B, h, tab, iq4, c);
-      uint32_t signed_part[4];
-#pragma unroll
-      for (int j = 0; j < 4; j++) signed_part[j] = c.mag[j] & c.neg[j];
-#pragma unroll
-      for (int t = 0; t < T; t++) {
-        const uint4 av = *(const uint4 *)(xq[t] + 256 * bl + 16 * h);
-        const int32_t a[4] = {(int32_t)av.x, (int32_t)av.y, (int32_t)av.z, (int32_t)av.w};
-        int32_t d = 0;
-#pragma unroll
-        for (int j = 0; j < 4; j++) d = sdot4((int32_t)c.mag[j], a[j], d);
-        if (has_signs<TY>()) {
-          int32_t e = 0;
-#pragma unroll
-          for (int j = 0; j < 4; j++) e = sdot4((int32_t)signed_part[j], a[j], e);
-          d -= 2 * e;
-        }
-        if (is_iq1<TY>()) {  // 8 dot(code, a) - (7 + 2 down) sum of each 8 (token.ts:93-99, 117-127)
-          const int32_t e0 = s8[t][32 * bl + 2 * h], e1 = s8[t][32 * bl + 2 * h + 1];
-          d = 8 * d - (7 + 2 * (int32_t)c.down0) * e0 - (7 + 2 * (int32_t)c.down1) * e1;
-        }
-        G[t][h >> 1] += c.S * d;
-        if (has_minimums<TY>()) Mi[t][h >> 1] += c.M * (int32_t)s16[t][16 * bl + h];
-      }
-    }
-    const float F = block_f<TY>(B), Fm = block_fm<TY>(B);
+  const int units = batch.unit0[batch.njobs];
+  for (int unit = blockIdx.x * 4 + wave; unit < units; unit += gridDim.x * 4) {
+    const int jb = sb_job_of(batch, unit);
+    const Job &J = batch.job[jb];
+    const int row_u = J.r0 + (unit - batch.unit0[jb]) * kSbRowsPerWave + slot;
+    const bool live = row_u < J.r1;
+    const int row = live ? row_u : J.r1 - 1;
+    const int blocks = J.n >> 8;
+    const char *wrow = J.wq + (int64_t)row * blocks * BYTES;
+    // token t's activations (n int8), its scales (n / 32 float32), its sums of 16 and of 8 (int16)
+    const int8_t *xq[T];
+    const float *xs[T];
+    const int16_t *s16[T], *s8[T];
 #pragma unroll
     for (int t = 0; t < T; t++) {
-      const float4 x0 = *(const float4 *)(xs[t] + 8 * bl), x1 = *(const float4 *)(xs[t] + 8 * bl + 4);
-      const float sl[4] = {x0.x, x0.y, x0.z, x0.w}, sh[4] = {x1.x, x1.y, x1.z, x1.w};
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        float part = fmul(fadd(fmul((float)G[t][k], sl[k]), fmul((float)G[t][k + 4], sh[k])), F);
-        if (has_minimums<TY>())
-          part = fsub(part, fmul(fadd(fmul((float)Mi[t][k], sl[k]), fmul((float)Mi[t][k + 4], sh[k])), Fm));
-        f.v[it & 1][slot][t][k][lane] = valid ? part : 0.0f;  // +0 leaves a lane as it is: a lane is never -0
-      }
+      xq[t] = (const int8_t *)(J.xq + t * J.frame);
+      xs[t] = (const float *)(J.xs + t * J.sframe);
+      s16[t] = (const int16_t *)(xs[t] + (J.n >> 5));
+      s8[t] = s16[t] + (J.n >> 4);
     }
-    fold_step_l<T, L>(f, it & 1, slot, lane, acc);
-  }
-  // lanes 0..3 hold the four lanes' sums: ((l0 + l1) + l2) + l3 in lane 0 (math.ts:7-9)
-  float sum[T];
+    float acc[T];
 #pragma unroll
-  for (int t = 0; t < T; t++)
-    sum[t] = fadd(fadd(fadd(acc[t], from_lane_plus<1>(acc[t])), from_lane_plus<2>(acc[t])), from_lane_plus<3>(acc[t]));
-  if (live && lane == 0) {
+    for (int t = 0; t < T; t++) acc[t] = 0.0f;
+    const int steps = (blocks + L - 1) / L;
+    for (int it = 0; it < steps; it++) {
+      const int b = it * L + lane;
+      const bool valid = b < blocks;
+      const int bl = valid ? b : 0;
+      BlockBytes<BYTES> B;
+      B.load(wrow + (int64_t)bl * BYTES);
+      int32_t G[T][8], Mi[T][8];
 #pragma unroll
-    for (int t = 0; t < T; t++) ((float *)(J.out + t * J.os))[row] = sum[t];
+      for (int t = 0; t < T; t++)
+#pragma unroll
+        for (int k = 0; k < 8; k++) G[t][k] = Mi[t][k] = 0;
+#pragma unroll
+      for (int h = 0; h < 16; h++) {
+        Chunk c;
+        chunk<TY>(B, h, table, table + GRID, iq4, c);
+        uint32_t signed_part[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) signed_part[j] = c.mag[j] & c.neg[j];
+#pragma unroll
+        for (int t = 0; t < T; t++) {
+          const uint4 av = *(const uint4 *)(xq[t] + 256 * bl + 16 * h);
+          const int32_t a[4] = {(int32_t)av.x, (int32_t)av.y, (int32_t)av.z, (int32_t)av.w};
+          int32_t d = 0;
+#pragma unroll
+          for (int j = 0; j < 4; j++) d = sdot4((int32_t)c.mag[j], a[j], d);
+          if (has_signs<TY>()) {
+            int32_t e = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) e = sdot4((int32_t)signed_part[j], a[j], e);
+            d -= 2 * e;
+          }
+          if (is_iq1<TY>()) {  // 8 dot(code, a) - (7 + 2 down) sum of each 8 (token.ts:93-99, 117-127)
+            const int32_t e0 = s8[t][32 * bl + 2 * h], e1 = s8[t][32 * bl + 2 * h + 1];
+            d = 8 * d - (7 + 2 * (int32_t)c.down0) * e0 - (7 + 2 * (int32_t)c.down1) * e1;
+          }
+          G[t][h >> 1] += c.S * d;
+          if (has_minimums<TY>()) Mi[t][h >> 1] += c.M * (int32_t)s16[t][16 * bl + h];
+        }
+      }
+      const float F = block_f<TY>(B), Fm = block_fm<TY>(B);
+#pragma unroll
+      for (int t = 0; t < T; t++) {
+        const float4 x0 = *(const float4 *)(xs[t] + 8 * bl), x1 = *(const float4 *)(xs[t] + 8 * bl + 4);
+        const float sl[4] = {x0.x, x0.y, x0.z, x0.w}, sh[4] = {x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          float part = fmul(fadd(fmul((float)G[t][k], sl[k]), fmul((float)G[t][k + 4], sh[k])), F);
+          if (has_minimums<TY>())
+            part = fsub(part, fmul(fadd(fmul((float)Mi[t][k], sl[k]), fmul((float)Mi[t][k + 4], sh[k])), Fm));
+          f.v[it & 1][slot][t][k][lane] = valid ? part : 0.0f;  // +0 leaves a lane as it is: a lane is never -0
+        }
+      }
+      fold_step_l<T, L>(f, it & 1, slot, lane, acc);
+    }
+    // lanes 0..3 hold the four lanes' sums: ((l0 + l1) + l2) + l3 in lane 0 (math.ts:7-9)
+    float sum[T];
+#pragma unroll
+    for (int t = 0; t < T; t++)
+      sum[t] = fadd(fadd(fadd(acc[t], from_lane_plus<1>(acc[t])), from_lane_plus<2>(acc[t])), from_lane_plus<3>(acc[t]));
+    if (live && lane == 0) {
+#pragma unroll
+      for (int t = 0; t < T; t++) ((float *)(J.out + t * J.os))[row] = sum[t];
+    }
   }
 }
 
+// a launch's blocks: as many as stay resident together (at most the groups of 4 rows over 4)
+template <int TY, int T>
+hipError_t launch_tt(const SbBatch &b, hipStream_t s) {
+  static int per_cu[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (per_cu[dev] == 0) {
+    int k = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&k, gemv_sb<TY, T>, 256, 0) != hipSuccess || k < 1) k = 1;
+    per_cu[dev] = k;
+  }
+  const int want = (b.unit0[b.njobs] + 3) / 4, cap = per_cu[dev] * cu_count();
+  hipLaunchKernelGGL((gemv_sb<TY, T>), dim3(want < cap ? want : cap), dim3(256), 0, s, b);
+  return hipGetLastError();
+}
+
 template <int TY>
-hipError_t launch_type(const SbBatch &b, int blocks, int T, hipStream_t s) {
-  dim3 grid(blocks), block(256);
+hipError_t launch_type(const SbBatch &b, int T, hipStream_t s) {
   switch (T) {
-  case 1: hipLaunchKernelGGL((gemv_sb<TY, 1>), grid, block, 0, s, b); break;
-  case 2: hipLaunchKernelGGL((gemv_sb<TY, 2>), grid, block, 0, s, b); break;
-  case 3: hipLaunchKernelGGL((gemv_sb<TY, 3>), grid, block, 0, s, b); break;
-  case 4: hipLaunchKernelGGL((gemv_sb<TY, 4>), grid, block, 0, s, b); break;
+  case 1: return launch_tt<TY, 1>(b, s);
+  case 2: return launch_tt<TY, 2>(b, s);
+  case 3: return launch_tt<TY, 3>(b, s);
+  case 4: return launch_tt<TY, 4>(b, s);
   default: return hipErrorInvalidValue;
   }
-  return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -336,7 +384,7 @@ __global__ __launch_bounds__(256) void sb_row_kernel(float *out, const char *w, 
   // h is not a constant here: the chunk is decoded for each h and the one of this thread kept
 #pragma unroll
   for (int hh = 0; hh < 16; hh++)
-    if (hh == h) chunk<TY>(B, hh, tab, iq4, c);
+    if (hh == h) chunk<TY>(B, hh, tab + grid_at<TY>(), tab + T_SIGNS, iq4, c);
   const float d = block_d<TY>(B), fm = block_fm<TY>(B);
   // floatScale (row.ts:9-17): d (s + 1/2) / 4 (IQ2), d (s + 1/2) / 2 (IQ3_XXS), d S otherwise
   const float s = (float)(c.S >> 1);
@@ -347,13 +395,15 @@ __global__ __launch_bounds__(256) void sb_row_kernel(float *out, const char *w, 
 #pragma unroll
   for (int j = 0; j < 16; j++) {
     const int32_t byte = (int32_t)(int8_t)((c.mag[j >> 2] >> (8 * (j & 3))) & 0xff);
+    // W as an int8: the reference puts the signs on the magnitudes and takes IQ1's 1 off with byte subtractions that
+    // wrap (row.ts:24, 32-37); only a grid byte of -128 (outside the converter's grids) shows it
     float v;
     if (is_iq1<TY>()) {  // the grid's -1, 0, 1 and an eighth more or less (row.ts:22-31)
       const uint32_t down = j < 8 ? c.down0 : c.down1;
-      v = fadd((float)(byte - 1), down ? -0.125f : 0.125f);
+      v = fadd((float)(int8_t)(byte - 1), down ? -0.125f : 0.125f);
     } else if (has_signs<TY>()) {
       const bool negative = ((c.neg[j >> 2] >> (8 * (j & 3))) & 0xff) != 0;
-      v = (float)(negative ? -byte : byte);
+      v = (float)(int8_t)(negative ? -byte : byte);
     } else {
       v = (float)byte;
     }
@@ -461,32 +511,33 @@ hipError_t launch_sb_row(float *out, const char *w, const uint8_t *tab, int32_t 
   return hipGetLastError();
 }
 
-// jobs: one block type, one token count (1..4)
+// jobs: one block type, one token count (1..4), one tables' area
 hipError_t launch_sb(const Job *jobs, int32_t njobs, hipStream_t s) {
   if (njobs < 1 || njobs > kMaxJobs) return hipErrorInvalidValue;
   SbBatch b{};
-  int blocks = 0;
-  constexpr int rpb = 256 / kSbLanes;
+  int units = 0;
   for (int j = 0; j < njobs; j++) {
+    if (jobs[j].type != jobs[0].type || jobs[j].count != jobs[0].count || jobs[j].ws != jobs[0].ws)
+      return hipErrorInvalidValue;
     b.job[j] = jobs[j];
-    b.block0[j] = blocks;
-    blocks += (jobs[j].r1 - jobs[j].r0 + rpb - 1) / rpb;
+    b.unit0[j] = units;
+    units += (jobs[j].r1 - jobs[j].r0 + kSbRowsPerWave - 1) / kSbRowsPerWave;
   }
-  b.block0[njobs] = blocks;
+  b.unit0[njobs] = units;
   b.njobs = njobs;
-  if (blocks == 0) return hipSuccess;
+  if (units == 0) return hipSuccess;
   const int T = jobs[0].count;
   switch (jobs[0].type) {
-  case Q2_K: return launch_type<Q2_K>(b, blocks, T, s);
-  case Q4_K: return launch_type<Q4_K>(b, blocks, T, s);
-  case IQ2_XXS: return launch_type<IQ2_XXS>(b, blocks, T, s);
-  case IQ2_XS: return launch_type<IQ2_XS>(b, blocks, T, s);
-  case IQ2_S: return launch_type<IQ2_S>(b, blocks, T, s);
-  case IQ3_XXS: return launch_type<IQ3_XXS>(b, blocks, T, s);
-  case IQ3_S: return launch_type<IQ3_S>(b, blocks, T, s);
-  case IQ1_S: return launch_type<IQ1_S>(b, blocks, T, s);
-  case IQ1_M: return launch_type<IQ1_M>(b, blocks, T, s);
-  case IQ4_XS: return launch_type<IQ4_XS>(b, blocks, T, s);
+  case Q2_K: return launch_type<Q2_K>(b, T, s);
+  case Q4_K: return launch_type<Q4_K>(b, T, s);
+  case IQ2_XXS: return launch_type<IQ2_XXS>(b, T, s);
+  case IQ2_XS: return launch_type<IQ2_XS>(b, T, s);
+  case IQ2_S: return launch_type<IQ2_S>(b, T, s);
+  case IQ3_XXS: return launch_type<IQ3_XXS>(b, T, s);
+  case IQ3_S: return launch_type<IQ3_S>(b, T, s);
+  case IQ1_S: return launch_type<IQ1_S>(b, T, s);
+  case IQ1_M: return launch_type<IQ1_M>(b, T, s);
+  case IQ4_XS: return launch_type<IQ4_XS>(b, T, s);
   default: return hipErrorInvalidValue;
   }
 }

@@ -650,18 +650,6 @@ HQ_HOST_DEV constexpr size_t ternary_stage_bytes(int T, int n) { return (size_t)
 #ifndef HQ_FUSED_BLOCKS_PER_CU
 #define HQ_FUSED_BLOCKS_PER_CU 6
 #endif
-int cu_count() {
-  static int cache[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cache[dev] == 0) {
-    int cus = 0;
-    cache[dev] = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0
-                     ? cus : 256;
-  }
-  return cache[dev];
-}
-
 template <int PACK, int T, int SRC>
 hipError_t launch_relaxed(const GemvBatch &b, int tiles, bool wc, size_t lds, hipStream_t s) {
   const int cap = HQ_FUSED_BLOCKS_PER_CU * cu_count();

@@ -43,6 +43,20 @@ hipError_t launch_six_sums(int32_t *out, const char *w, int32_t groups, hipStrea
 // the caller cleared) where a value is not plus or minus its group's largest
 hipError_t launch_binary_x(uint8_t *out, float *xs, const float *x, int32_t groups, int32_t *bad, hipStream_t s);
 
+// the current device's compute units (256 on an MI355X; 256 when the query fails), for grids of blocks that take
+// work in turn
+inline int cu_count() {
+  static int cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int cus = 0;
+    cache[dev] = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0
+                     ? cus : 256;
+  }
+  return cache[dev];
+}
+
 // GEMV-shaped products (every job of one kind and one token count, 1..4; up to kMaxJobs jobs a launch)
 constexpr int kMaxJobs = 8;
 hipError_t launch_gemv(Kind kind, const Job *jobs, int32_t njobs, hipStream_t s);

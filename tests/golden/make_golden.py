@@ -1,6 +1,7 @@
 """Writes tests/golden/golden.npz: small input / output vectors of every kernel on the path, computed by the oracle
-(oracle/, the C restatement of the reference arithmetic; binary included) from the reference tests' LCG streams (tests/int8-check.ts:116-117,
-seed 644; tests/ternary-check.ts:80-81, seed 231) and the stories15M shape of the first benchmark config (n = 288,
+(oracle/, the C restatement of the reference arithmetic; binary and llama.cpp's blocks included) from the reference
+tests' LCG streams (tests/int8-check.ts:116-117, seed 644; tests/ternary-check.ts:80-81, seed 231; the blocks' stream
+seed 363) and the stories15M shape of the first benchmark config (n = 288,
 24 of its 768 rows).  Arrays only (numpy.load with allow_pickle=False reads it).
 
     python tests/golden/make_golden.py
@@ -20,6 +21,10 @@ from streams import LCG, pack6, pack_binary, pack_ternary, scale_rule  # noqa: E
 F = np.float32
 ROWS, N, TOKENS = 24, 288, 6
 TN = 384  # ternary: 3 groups of 128
+SB_ROWS, SB_N = 3, 512  # llama.cpp's blocks: 3 rows of 2 blocks
+# where each block type keeps a float16 scale (kernels/blocks/types.ts:60-79; IQ1_M's is spread over four words and
+# stays the stream's bytes)
+SB_SCALES = {10: (80, 82), 12: (0, 2), 16: (0,), 17: (0,), 18: (0,), 19: (0,), 21: (0,), 22: (0,), 23: (0,)}
 
 
 def frames(qs, ss, n, area):
@@ -90,6 +95,23 @@ def make():
     g["xb"] = xb
     g["xb_bits"], g["xb_scales"], bad = oracle.binary_x(xb)
     g["xb_bad"] = np.array([bad], np.int32)
+    # llama.cpp's blocks (seed 363): codebooks of stream bytes, and for each type SB_ROWS rows of SB_N weights of stream
+    # bytes with float16 scales of 1e-5 .. 1e-2 where the type keeps them, one token (quantize_x at bias 0, sums_x)
+    rb = LCG(363)
+    books = np.array([rb.next() & 255 for _ in range(oracle.SB_CODEBOOKS)], np.uint8)
+    g["sb_books"], g["sb_tables"] = books, oracle.sb_tables(books)
+    xs_ = np.array([((rb.next() % 20001) - 10000) * 3e-4 for _ in range(SB_N)], F)
+    q, s = oracle.quantize_x(xs_, 0)
+    g["sb_x"], g["sb_xq"], g["sb_area"] = xs_, q, oracle.sums_x(q.view(np.int8), s)
+    for name, t in oracle.SB_TYPES.items():
+        size = oracle.sb_bytes(t)
+        b = np.array([rb.next() & 255 for _ in range(SB_ROWS * (SB_N // 256) * size)], np.uint8).reshape(-1, size)
+        for blk in b:
+            for at in SB_SCALES.get(t, ()):
+                blk[at:at + 2] = np.array([(1 + rb.next() % 1000) * 1e-5], np.float16).view(np.uint8)
+        g[f"sb_w_{name}"] = b.reshape(-1)
+        g[f"sb_out_{name}"] = oracle.matmul_sbr(q.view(np.int8), g["sb_area"], b.reshape(-1), g["sb_tables"], SB_N, t)
+        g[f"sb_row_{name}"] = oracle.sb_row(b.reshape(-1)[:(SB_N // 256) * size], g["sb_tables"], SB_N, t)
     return g
 
 

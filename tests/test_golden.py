@@ -8,6 +8,9 @@ import pytest
 HERE = os.path.dirname(os.path.abspath(__file__))
 F = np.float32
 ROWS, N, TN = 24, 288, 384
+SB_ROWS, SB_N = 3, 512
+SB_NAMES = ("Q2_K", "Q4_K", "IQ2_XXS", "IQ2_XS", "IQ3_XXS", "IQ1_S", "IQ3_S", "IQ2_S", "IQ4_XS", "IQ1_M")
+SB_NUMBERS = (10, 12, 16, 17, 18, 19, 21, 22, 23, 29)
 
 
 @pytest.fixture(scope="module")
@@ -39,6 +42,15 @@ def test_oracle_reproduces_golden(oracle, golden):
     assert same(oracle.matmul_b1r(g["xtq"].view(np.int8), g["xtarea"], g["wb"], g["wst"], TN), g["b1r"])
     bits, scales, bad = oracle.binary_x(g["xb"])
     assert same(bits, g["xb_bits"]) and same(scales, g["xb_scales"]) and bad == g["xb_bad"][0] == 1
+    assert same(oracle.sb_tables(g["sb_books"]), g["sb_tables"])
+    q, s = oracle.quantize_x(g["sb_x"], 0)
+    assert same(q, g["sb_xq"]) and same(oracle.sums_x(q.view(np.int8), s), g["sb_area"])
+    for name, t in oracle.SB_TYPES.items():
+        w = g[f"sb_w_{name}"]
+        assert same(oracle.matmul_sbr(g["sb_xq"].view(np.int8), g["sb_area"], w, g["sb_tables"], SB_N, t),
+                    g[f"sb_out_{name}"]), name
+        assert same(oracle.sb_row(w[:w.size // SB_ROWS], g["sb_tables"], SB_N, t), g[f"sb_row_{name}"]), name
+        assert np.all(np.isfinite(g[f"sb_out_{name}"])), name
     frame = int(g["tile_frame"][0])
     for t in range(g["tile_x"].shape[0]):
         row = g["tile_x"][t]
@@ -125,3 +137,20 @@ def test_kernels_reproduce_golden(pkg, golden):
     assert k.binary_x(bits, scales, arena.put(g["xb"]), TN) == g["xb_bad"][0]
     assert same(arena.get(bits, np.uint8, TN // 8), g["xb_bits"])
     assert same(arena.get(scales, F, TN // 128), g["xb_scales"])
+    # llama.cpp's blocks: the tables, the sums of 16 and 8, the token product and the rows
+    tab = arena.alloc(g["sb_tables"].size)
+    assert k.sb_tables(tab, arena.put(g["sb_books"])) == g["sb_tables"].size
+    assert same(arena.get(tab, np.uint8, g["sb_tables"].size), g["sb_tables"])
+    xq, area = arena.put(g["sb_xq"]), arena.alloc(g["sb_area"].size)
+    arena.write(area, g["sb_area"][:4 * (SB_N // 32)])
+    k.sums_x(area, xq, SB_N)
+    assert same(arena.get(area, np.uint8, g["sb_area"].size), g["sb_area"])
+    for name, t in {n: int(n2) for n, n2 in zip(SB_NAMES, SB_NUMBERS)}.items():
+        w = g[f"sb_w_{name}"]
+        aw = arena.put(w)
+        o = out(SB_ROWS)
+        k.matmul_sbr(o, xq, area, aw, tab, SB_N, 0, SB_ROWS, t)
+        assert same(arena.get(o, F, SB_ROWS), g[f"sb_out_{name}"]), name
+        r = arena.alloc(4 * SB_N)
+        k.sb_row(r, aw, tab, SB_N, t)
+        assert same(arena.get(r, F, SB_N), g[f"sb_row_{name}"]), name

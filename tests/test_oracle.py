@@ -663,6 +663,39 @@ def test_sb_row_is_the_reader(oracle, sb_setup, name):
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (name, tiny, np.nonzero(got != want)[0][:5])
 
 
+@pytest.mark.parametrize("name", ["IQ2_XXS", "IQ2_XS", "IQ2_S", "IQ3_XXS", "IQ3_S"])
+def test_grid_bytes_are_signed(oracle, name):
+    """Outside the converter's grids (magnitudes 0..127): the plain kernel multiplies a grid's bytes as int8
+    (types.ts:171-173, extmul_*_i8x16_s), so a byte of 128..255 is a negative magnitude, and sb_row puts the signs on
+    with a wrapping byte subtraction (row.ts:32-37, types.ts:163-165: -(-128) is -128)"""
+    rng = np.random.default_rng(77)
+    row = bm.codebooks(rng)
+    row[:17408] = rng.integers(0, 256, 17408, dtype=np.uint8)
+    tab = oracle.sb_tables(row)
+    g = bm.grids(row)
+    for key, (at, count, k) in bm.GRIDS.items():
+        if key != "IQ1S":
+            g[key] = row[at:at + count * k].view(np.int8).reshape(count, k).astype(np.int32)
+    t = bm.TYPES[name]
+    nb, rows = 3, 4
+    n = 256 * nb
+    blocks = bm.random_blocks(rng, t, rows * nb)
+    q, s = oracle.quantize_x(rng.standard_normal(n).astype(F), 0)
+    q = q.view(np.int8)
+    got = oracle.matmul_sbr(q, oracle.sums_x(q, s), blocks.reshape(-1), tab, n, t)
+    for r in range(rows):
+        want = bm.matmul(t, blocks[r * nb:(r + 1) * nb], q, s, g)
+        assert got[r].view(np.uint32) == np.float32(want).view(np.uint32), (name, r)
+    # every magnitude -128: with its sign a weight is -(-128) = -128 too, so every weight of the row is -128 S d
+    row[:17408] = 0x80
+    tab = oracle.sb_tables(row)
+    g = {key: np.full((count, k), -128, np.int32) for key, (at, count, k) in bm.GRIDS.items() if key != "IQ1S"}
+    g.update({key: value for key, value in bm.grids(row).items() if key not in g})
+    got = oracle.sb_row(blocks[:nb].reshape(-1), tab, n, t)
+    model = bm.read_floats(t, blocks[:nb], g).reshape(-1)
+    assert np.array_equal(got, -np.abs(model)) and np.any(model > 0), name
+
+
 @pytest.mark.parametrize("name", sorted(bm.TYPES))
 def test_matmul_sbr_order_and_integers(oracle, sb_setup, name):
     """token.ts / types.ts:48-57: the exact integers of every group and the kernels' float32 order, to the bit against
