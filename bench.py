@@ -339,6 +339,58 @@ def measure_configs(torch, pkg, args):
         decode(f"{tag} {kind} M=1, down x {copies}", kind, [[(5120, 17408)]], copies)
         prefill(f"{tag} {kind} prefill M=256", kind, [(17408, 5120), (17408, 5120), (5120, 17408)], 256)
     out.update(measure_blocks(torch, pkg, args, gen))
+    out.update(measure_outliers(torch, pkg, args, gen))
+    return out
+
+
+def measure_outliers(torch, pkg, args, gen):
+    """The classifier's outlier channels (engine.ts:459-466): add_columns alone (8 columns of GPT-2's 50257 and
+    Llama-3's 128256 words: GB/s of its 4 vocab (count + 2) bytes), and Llama-3-8B's classifier of one token
+    ([128256, 4096] int8) with the 8 channels taken apart, the product and add_columns, against the product alone."""
+    import ctypes
+    from pyodide_llm_amd import jobs
+    lib = pkg.library()
+    dev = "cuda:0"
+    reps = max(3, args.steps // 2)
+    out = {}
+    count = 8
+    channels = (ctypes.c_int32 * count)(*[1, 50, 300, 777, 1024, 2000, 3000, 4095])
+    for vocab in (50257, 128256):
+        y = torch.randn(vocab, device=dev, generator=gen)
+        rows = torch.randn(count, vocab, device=dev, generator=gen)
+        a = torch.randn(count, device=dev, generator=gen)
+        def launches(h, y=y, rows=rows, a=a, vocab=vocab):  # 50 back to back: a graph's own cost is not the kernel's
+            for _ in range(50):
+                lib.hq_add_columns_ex(y.data_ptr(), rows.data_ptr(), a.data_ptr(), count, vocab, h)
+        sec = _graph_time(torch, launches, reps) / 50
+        pkg.check(lib.hq_last_error())
+        out[f"add_columns {count} x {vocab}"] = {"GBps": round(4 * vocab * (count + 2) / sec / 1e9, 1),
+                                                 "us": round(1e6 * sec, 2)}
+    vocab, dim = 128256, 4096
+    w = torch.randint(-127, 128, (vocab, dim), dtype=torch.int8, device=dev, generator=gen)
+    ws = (torch.rand(vocab, dim // 32, device=dev, generator=gen) * 0.001).float()
+    x = torch.randn(dim, device=dev, generator=gen)
+    logits = torch.empty(vocab, device=dev)
+    xq = torch.empty(2 * dim, dtype=torch.uint8, device=dev)
+    columns = torch.empty(count, vocab, device=dev)
+    picked = torch.empty(count, device=dev)
+    pkg.check(lib.hq_outlier_columns_ex(columns.data_ptr(), w.data_ptr(), ws.data_ptr(), 0, channels, count, vocab,
+                                        dim, None))
+    table = jobs.table([jobs.job("matmul_q8r", logits.data_ptr(), xq.data_ptr(), xq.data_ptr() + dim, w.data_ptr(),
+                                 ws.data_ptr(), 0, dim, rows=vocab)])
+
+    def product(h):
+        lib.hq_matmuls(x.data_ptr(), 4 * dim, table, 1, 16, h)
+
+    def classify(h):
+        lib.hq_take_channels_ex(picked.data_ptr(), x.data_ptr(), channels, count, h)
+        product(h)
+        lib.hq_add_columns_ex(logits.data_ptr(), columns.data_ptr(), picked.data_ptr(), count, vocab, h)
+    alone = _graph_time(torch, product, reps)
+    apart = _graph_time(torch, classify, reps)
+    pkg.check(lib.hq_last_error())
+    out["8B classifier, 8 outlier channels apart"] = {"us": round(1e6 * apart, 2), "us_product_alone":
+                                                      round(1e6 * alone, 2)}
     return out
 
 

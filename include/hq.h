@@ -127,6 +127,11 @@ void signed_dots(void *out, const void *a, const void *b);
  * reader (src/python/convert/superblocks.py) gives it */
 void sb_row(void *out, const void *w, const void *tab, int32_t n, int32_t type);
 
+/* kernels/kernel/matmul.ts:246-266 (add_columns, jobs.ts:108): y[j] += the sum over c < count of a[c] rows[c][j],
+ * for j < n, added to y[j] one product at a time in the order of c (each product a float32); rows is (count, n)
+ * row-major; y, rows, a 4-byte aligned (device) */
+void add_columns(void *y, const void *rows, const void *a, int32_t count, int32_t n);
+
 /* ---- the library's own ----------------------------------------------------------------------------------------- */
 
 enum {
@@ -189,6 +194,20 @@ int32_t hq_matmul_sbr_tile_ex(void *xout, const void *xq, const void *xs, const 
                               int32_t r0, int32_t r1, int32_t count, int32_t os, int32_t frame, int32_t type,
                               void *stream);
 int32_t hq_sb_row_ex(void *out, const void *w, const void *tab, int32_t n, int32_t type, void *stream);
+
+/* The classifier's outlier channels (src/runtime/forward/tensors.ts:170-187, engine.ts:459-466): the columns of the
+ * packed classifier for these channels (a host array of count <= 64 channel numbers below dim), widened to float32
+ * as columns[i][w] = value(w dim + c_i) x its group's scale, for the vocab words w; values and scales as the loader
+ * keeps them (packing: HQ_PACK_INT8, whose group is the largest power of two up to 32 that divides dim, float32
+ * scales; HQ_PACK_INT6, groups of 32, float32 scales; HQ_PACK_TERNARY / HQ_PACK_BINARY, groups of 128, float16
+ * scales). columns 4-byte aligned. */
+enum { HQ_PACK_INT8 = 0, HQ_PACK_INT6 = 1, HQ_PACK_TERNARY = 2, HQ_PACK_BINARY = 3 };
+int32_t hq_outlier_columns_ex(void *columns, const void *values, const void *scales, int32_t packing,
+                              const int32_t *channels, int32_t count, int32_t vocab, int32_t dim, void *stream);
+/* engine.ts:461-464: picked[i] = x[c_i], then x[c_i] = 0, channel by channel (x the classifier's input before
+ * quantize_x; channels a host array as above); add_columns then adds their products to the logits */
+int32_t hq_take_channels_ex(void *picked, void *x, const int32_t *channels, int32_t count, void *stream);
+int32_t hq_add_columns_ex(void *y, const void *rows, const void *a, int32_t count, int32_t n, void *stream);
 
 /* The activations of `count` tokens prepared in one launch (src/runtime/forward/engine.ts:405 calls ready() once a
  * token): token t's float32 values at x + t x_stride (bytes) -> xq + t frame and xs + t frame, as quantize_x; and,

@@ -721,3 +721,16 @@ void o_sb_row(float *out, const uint8_t *w, const uint8_t *tab, int32_t n, int32
     }
   }
 }
+
+/* matmul.ts:248-266: for each j the reference starts from y[j] and adds f(a[c] rows[c][j]) for c in order; its
+ * four-wide loop (v128 lanes j .. j+3) and its scalar tail (j from n & ~3) do the same for every j */
+void o_add_columns(float *y, const float *rows, const float *a, int32_t count, int32_t n) {
+  for (int32_t j = 0; j < n; j++) {
+    float acc = y[j];
+    for (int32_t c = 0; c < count; c++) {
+      const float product = a[c] * rows[(int64_t)c * n + j];
+      acc = acc + product;
+    }
+    y[j] = acc;
+  }
+}

@@ -85,6 +85,10 @@ void o_matmul_sbr_tile(void *xout, const void *xq, const void *xs, const uint8_t
 /* kernels/blocks/row.ts:7-72 (sb_row): a row's n weights as float32 */
 void o_sb_row(float *out, const uint8_t *w, const uint8_t *tab, int32_t n, int32_t type);
 
+/* kernels/kernel/matmul.ts:246-266 (add_columns): y[j] += a[c] rows[c][j] for c = 0 .. count-1 in order, each
+ * product and each sum a float32 (the four-wide loop and the scalar tail add in this one order) */
+void o_add_columns(float *y, const float *rows, const float *a, int32_t count, int32_t n);
+
 /* CPU baseline: the GEMV above over rows [0, rows) on `threads` host threads, rows handed out in chunks as the
  * reference's phase() does (src/runtime/forward/threads.ts:45, 90-137: 4 chunks a thread, a shared counter).
  * kind: 0 matmul_q8r, 1 matmul_q8, 2 matmul_q6r, 3 matmul_q6, 4 matmul_t2r.  Runs `reps` times, returns seconds

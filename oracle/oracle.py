@@ -51,6 +51,7 @@ def lib():
             "o_matmul_sbr": [p, p, p, p, p, i32, i32, i32, i32],
             "o_matmul_sbr_tile": [p, p, p, p, p, i32, i32, i32, i32, i32, i32, i32],
             "o_sb_row": [p, p, p, i32, i32],
+            "o_add_columns": [p, p, p, i32, i32],
         }
         for name, argtypes in sigs.items():
             fn = getattr(L, name)
@@ -245,3 +246,59 @@ def time_gemv(kind, xq, xs, wq, ws, wc, n, rows, threads, reps):
     """The oracle's GEMV over all rows on `threads` host threads (phase()-style chunks); fastest of reps, seconds."""
     out = np.zeros(rows, np.float32)
     return lib().o_time_gemv(KINDS[kind], _p(out), _p(xq), _p(xs), _p(wq), _p(ws), _p(wc), n, rows, threads, reps)
+
+
+def add_columns(y, rows, a):
+    """kernels/kernel/matmul.ts:248-266: y (n) plus the products of a (count) and rows (count, n), in order"""
+    y = np.array(y, np.float32)
+    rows = _c(rows, np.float32).reshape(-1, y.size)
+    a = _c(a, np.float32)
+    lib().o_add_columns(_p(y), _p(rows), _p(a), a.size, y.size)
+    return y
+
+
+def packed_values(packing, raw, count):
+    """jobs.ts:398-433 (each packing's value()): the first `count` weights of a packed tensor as int32 —
+    int8 the bytes; int6 (six.ts:1-11) 4 v from its 24 bytes a group of 32; ternary (ternary.ts:25-34) code - 1;
+    binary (binary.ts:1-4) +1 where bit 4 h + p of byte c of a group is set for weight 64 h + 4 c + p, else -1"""
+    u = np.ascontiguousarray(raw, np.uint8).reshape(-1)
+    i = np.arange(count, dtype=np.int64)
+    if packing == "int8":
+        return u[:count].view(np.int8).astype(np.int32)
+    if packing == "int6":
+        g, j = (i >> 5) * 24, i & 31
+        low = np.where(j < 16, u[g + np.minimum(j, 15)] & 15, u[g + np.maximum(j - 16, 0)] >> 4).astype(np.int32)
+        top = (u[g + 16 + (j & 7)].astype(np.int32) >> (2 * (j >> 3))) & 3
+        return ((low | (top << 4)) << 2).astype(np.uint8).view(np.int8).astype(np.int32)
+    if packing == "ternary":
+        return ((u[i >> 2].astype(np.int32) >> (2 * (i & 3))) & 3) - 1
+    if packing == "binary":
+        byte = u[((i >> 7) << 4) + ((i >> 2) & 15)].astype(np.int32)
+        return (((byte >> ((((i >> 6) & 1) << 2) | (i & 3))) & 1) << 1) - 1
+    raise ValueError(packing)
+
+
+def outlier_columns(packing, values, scales, channels, vocab, dim, group):
+    """src/runtime/forward/tensors.ts:175-186: columns[i][w] = f(value(w dim + c_i) scale(w groups + c_i / group))
+    (float32 scales, or float16 ones for ternary and binary, widened exactly), as (len(channels), vocab) float32"""
+    v = packed_values(packing, values, vocab * dim).reshape(vocab, dim)
+    if packing in ("ternary", "binary"):
+        s = np.ascontiguousarray(scales).reshape(-1).view(np.uint16)[:vocab * (dim // group)]
+        s = np.array([half(h) for h in s], np.float32)
+    else:
+        s = np.ascontiguousarray(scales).reshape(-1).view(np.float32)[:vocab * (dim // group)]
+    s = s.reshape(vocab, dim // group)
+    out = np.zeros((len(channels), vocab), np.float32)
+    for i, c in enumerate(channels):
+        out[i] = v[:, c].astype(np.float32) * s[:, c // group]
+    return out
+
+
+def take_channels(x, channels):
+    """src/runtime/forward/engine.ts:461-464: (picked, x with those channels set to 0), channel by channel"""
+    x = np.array(x, np.float32)
+    picked = np.zeros(len(channels), np.float32)
+    for i, c in enumerate(channels):
+        picked[i] = x[c]
+        x[c] = 0.0
+    return picked, x

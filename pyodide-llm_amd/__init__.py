@@ -22,6 +22,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIBRARY = os.path.join(HERE, "libhq.so")
 
 HQ_OK, HQ_ERR_ARGUMENT, HQ_ERR_ALIGNMENT, HQ_ERR_NULL, HQ_ERR_HIP, HQ_ERR_KIND, HQ_ERR_DEVICE = range(7)
+# the packings of hq_outlier_columns_ex (include/hq.h)
+HQ_PACK = {"int8": 0, "int6": 1, "ternary": 2, "binary": 3}
 
 
 class HQError(RuntimeError):
@@ -58,6 +60,7 @@ REFERENCE_SIGNATURES = {
     "matmul_sbw_tile": [p, p, p, p, p, i32, i32, i32, i32, i32, i32, i32, p],
     "signed_dots": [p, p, p],
     "sb_row": [p, p, p, i32, i32],
+    "add_columns": [p, p, p, i32, i32],
 }
 # the reference kernels that return a value (the others return nothing)
 REFERENCE_RESTYPES = {"binary_x": i32, "sb_tables": i32}
@@ -91,6 +94,9 @@ OWN_SIGNATURES = {
     "hq_matmul_sbr_tile_ex": ([p, p, p, p, p, i32, i32, i32, i32, i32, i32, i32, p], i32),
     "hq_sb_row_ex": ([p, p, p, i32, i32, p], i32),
     "hq_sums_x_batch": ([p, p, i32, i32, i32, p], i32),
+    "hq_add_columns_ex": ([p, p, p, i32, i32, p], i32),
+    "hq_outlier_columns_ex": ([p, p, p, i32, ctypes.POINTER(i32), i32, i32, i32, p], i32),
+    "hq_take_channels_ex": ([p, p, ctypes.POINTER(i32), i32, p], i32),
     "hq_quantize_x_batch": ([p, p, p, i32, i32, i32, i32, i32, p], i32),
     "hq_interleave_batch": ([p, p, i32, i32, i32, p], i32),
     "hq_phase": ([ctypes.POINTER(ctypes.c_double), i32, i32, p], i32),

@@ -18,7 +18,7 @@ CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 OBJ = os.path.join(HERE, "_build")
 LIBRARY = os.path.join(HERE, "libhq.so")
-SOURCES = ["quantize.hip", "gemv.hip", "gemm.hip", "blocks.hip", "ceilings.hip", "abi.cpp"]
+SOURCES = ["quantize.hip", "gemv.hip", "gemm.hip", "blocks.hip", "columns.hip", "ceilings.hip", "abi.cpp"]
 # gemm.hip issues its direct-to-LDS loads as the instructions themselves, which set M0 (a register the compiler
 # reserves and does not use in those kernels): its warning about that clobber is expected
 EXTRA = {"gemm.hip": ["-Wno-inline-asm"]}

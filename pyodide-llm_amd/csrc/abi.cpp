@@ -225,6 +225,27 @@ int32_t matmul_blocks(hq::Kind kind, void *xout, const void *xq, const void *xs,
   return run_jobs(kind, {j}, stream_of(stream));
 }
 
+// a host list of channel numbers (each below dim) as the kernels take it
+int32_t channels_of(const char *who, const int32_t *channels, int32_t count, int32_t dim, hq::Channels &ch) {
+  if (count < 0 || count > hq::kMaxChannels)
+    return fail(HQ_ERR_ARGUMENT, "%s: %d channels (at most %d)", who, count, hq::kMaxChannels);
+  if (count && !channels) return fail(HQ_ERR_NULL, "%s: channels NULL", who);
+  ch.count = count;
+  for (int32_t i = 0; i < count; i++) {
+    if (channels[i] < 0 || channels[i] >= dim)
+      return fail(HQ_ERR_ARGUMENT, "%s: channel %d is not below %d", who, channels[i], dim);
+    ch.c[i] = channels[i];
+  }
+  return HQ_OK;
+}
+// the weights a scale is of (dtypes.py: int8's group32, int6's 32, ternary's and binary's 128)
+int32_t group_of(int32_t packing, int32_t dim) {
+  if (packing == hq::kPackTernary || packing == hq::kPackBinary) return 128;
+  if (packing == hq::kPackInt6) return 32;
+  int32_t size = 32;
+  while (size > 1 && dim % size) size >>= 1;
+  return size;
+}
 }  // namespace
 
 extern "C" {
@@ -394,6 +415,52 @@ int32_t hq_sb_row_ex(void *out, const void *w, const void *tab, int32_t n, int32
   if (int32_t st = ensure_device()) return st;
   return hip_status(hq::launch_sb_row((float *)out, (const char *)w, (const uint8_t *)tab, n, type, stream_of(stream)),
                     "sb_row");
+}
+
+// ---- the classifier's outlier channels (tensors.ts:170-187, engine.ts:459-466, matmul.ts:246-266) --------------
+int32_t hq_add_columns_ex(void *y, const void *rows, const void *a, int32_t count, int32_t n, void *stream) {
+  g_error = HQ_OK;
+  if (n < 0 || count < 0) return fail(HQ_ERR_ARGUMENT, "add_columns: count = %d, n = %d", count, n);
+  if (n == 0 || count == 0) return HQ_OK;
+  if (!y || !rows || !a) return fail(HQ_ERR_NULL, "add_columns: a NULL pointer");
+  if (!aligned(y, 4) || !aligned(rows, 4) || !aligned(a, 4))
+    return fail(HQ_ERR_ALIGNMENT, "add_columns: y, rows or a not 4-byte aligned");
+  if (int32_t st = ensure_device()) return st;
+  return hip_status(hq::launch_add_columns((float *)y, (const float *)rows, (const float *)a, count, n,
+                                           stream_of(stream)),
+                    "add_columns");
+}
+
+int32_t hq_outlier_columns_ex(void *columns, const void *values, const void *scales, int32_t packing,
+                              const int32_t *channels, int32_t count, int32_t vocab, int32_t dim, void *stream) {
+  g_error = HQ_OK;
+  if (packing < hq::kPackInt8 || packing > hq::kPackBinary)
+    return fail(HQ_ERR_ARGUMENT, "outlier_columns: packing %d is none of int8, int6, ternary, binary", packing);
+  if (vocab < 0 || dim <= 0) return fail(HQ_ERR_ARGUMENT, "outlier_columns: vocab = %d, dim = %d", vocab, dim);
+  const int32_t group = group_of(packing, dim);
+  if (dim % group) return fail(HQ_ERR_ARGUMENT, "outlier_columns: dim = %d is not whole groups of %d", dim, group);
+  hq::Channels ch{};
+  if (int32_t st = channels_of("outlier_columns", channels, count, dim, ch)) return st;
+  if (count == 0 || vocab == 0) return HQ_OK;
+  if (!columns || !values || !scales) return fail(HQ_ERR_NULL, "outlier_columns: a NULL pointer");
+  const uintptr_t sa = (packing == hq::kPackTernary || packing == hq::kPackBinary) ? 2 : 4;
+  if (!aligned(columns, 4) || !aligned(scales, sa))
+    return fail(HQ_ERR_ALIGNMENT, "outlier_columns: columns not 4-, or scales not %d-byte aligned", (int)sa);
+  if (int32_t st = ensure_device()) return st;
+  return hip_status(hq::launch_outlier_columns((float *)columns, (const uint8_t *)values, (const uint8_t *)scales,
+                                               packing, ch, vocab, dim, group, stream_of(stream)),
+                    "outlier_columns");
+}
+
+int32_t hq_take_channels_ex(void *picked, void *x, const int32_t *channels, int32_t count, void *stream) {
+  g_error = HQ_OK;
+  hq::Channels ch{};
+  if (int32_t st = channels_of("take_channels", channels, count, INT32_MAX, ch)) return st;
+  if (count == 0) return HQ_OK;
+  if (!picked || !x) return fail(HQ_ERR_NULL, "take_channels: a NULL pointer");
+  if (!aligned(picked, 4) || !aligned(x, 4)) return fail(HQ_ERR_ALIGNMENT, "take_channels: picked or x not 4-byte aligned");
+  if (int32_t st = ensure_device()) return st;
+  return hip_status(hq::launch_take_channels((float *)picked, (float *)x, ch, stream_of(stream)), "take_channels");
 }
 
 // ---- binary weights from float32 (kernels/kernel/quantize.ts:232-247) -------------------------------------------
@@ -650,6 +717,9 @@ void signed_dots(void *out, const void *a, const void *b) {
 }
 void sb_row(void *out, const void *w, const void *tab, int32_t n, int32_t type) {
   hq_sb_row_ex(out, w, tab, n, type, g_stream.load());
+}
+void add_columns(void *y, const void *rows, const void *a, int32_t count, int32_t n) {
+  hq_add_columns_ex(y, rows, a, count, n, g_stream.load());
 }
 // the reference's binary_x returns its refusal: this one waits for the library's stream to give it (a word of
 // device memory the library keeps for it, one a device); 1 also when the call fails (hq_last_error says why)

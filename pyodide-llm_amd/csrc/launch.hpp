@@ -74,6 +74,19 @@ hipError_t launch_sb_row(float *out, const char *w, const uint8_t *tab, int32_t 
 hipError_t launch_sb(const Job *jobs, int32_t njobs, hipStream_t s);
 hipError_t launch_signed_dots(int32_t *out, const int8_t *a, const int8_t *b, hipStream_t s);
 
+// the classifier's outlier channels: add_columns (y += the columns' products, in order); the columns of a packed
+// classifier widened to float32 (packing: kPack*; group: the weights a scale is of); the channels taken apart
+constexpr int kPackInt8 = 0, kPackInt6 = 1, kPackTernary = 2, kPackBinary = 3;
+constexpr int kMaxChannels = 64;
+struct Channels {
+  int32_t c[kMaxChannels];
+  int32_t count;
+};
+hipError_t launch_add_columns(float *y, const float *rows, const float *a, int32_t count, int32_t n, hipStream_t s);
+hipError_t launch_outlier_columns(float *columns, const uint8_t *values, const uint8_t *scales, int32_t packing,
+                                  const Channels &ch, int32_t vocab, int32_t dim, int32_t group, hipStream_t s);
+hipError_t launch_take_channels(float *picked, float *x, const Channels &ch, hipStream_t s);
+
 // MFMA GEMM-shaped products (one job a launch; count > 4 tokens): the tiles of matmul_q8r_tile, matmul_q6r and
 // matmul_t2r_tile over a prompt.  Returns hipErrorNotSupported for a kind that has none.
 hipError_t launch_gemm(Kind kind, const Job &job, hipStream_t s);

@@ -37,7 +37,7 @@ def test_reference_names_and_arities(pkg):
                  "matmul_q8r_tile": 12, "matmul_q6r": 9, "matmul_q6": 8, "matmul_t2r": 9, "matmul_t2": 9,
                  "matmul_t2r_tile": 12, "matmul_b1r": 9, "matmul_b1": 9, "matmul_b1r_tile": 12, "binary_x": 4,
                  "sb_tables": 2, "sums_x": 3, "matmul_sbr": 9, "matmul_sb": 9, "matmul_sbr_tile": 12,
-                 "matmul_sbw_tile": 13, "signed_dots": 3, "sb_row": 5}
+                 "matmul_sbw_tile": 13, "signed_dots": 3, "sb_row": 5, "add_columns": 5}
     for name, arity in reference.items():
         assert names[name] == arity, name
         assert len(pkg.REFERENCE_SIGNATURES[name]) == arity, name
@@ -68,6 +68,13 @@ def test_version(pkg):
     (lambda L: L.hq_matmul_sbr_tile_ex(16, 16, 16, 16, 16, 256, 0, 1, 2, 4, 8, 12, None), 2, "token stride"),
     (lambda L: L.hq_sb_row_ex(16, 16, 16, 100, 16, None), 1, "multiple of 256"),
     (lambda L: L.hq_sums_x_batch(16, 16, 100, 1, 0, None), 1, "multiple of"),
+    (lambda L: L.hq_add_columns_ex(16, 16, 16, -1, 8, None), 1, "count = -1"),
+    (lambda L: L.hq_add_columns_ex(16, 18, 16, 1, 8, None), 2, "4-byte"),
+    (lambda L: L.hq_outlier_columns_ex(16, 16, 16, 4, None, 0, 8, 32, None), 1, "packing 4"),
+    (lambda L: L.hq_outlier_columns_ex(16, 16, 16, 2, None, 0, 8, 64, None), 1, "whole groups of 128"),
+    (lambda L: L.hq_outlier_columns_ex(16, 16, 16, 0, (ctypes.c_int32 * 1)(32), 1, 8, 32, None), 1, "not below 32"),
+    (lambda L: L.hq_outlier_columns_ex(16, 16, 16, 0, (ctypes.c_int32 * 65)(), 65, 8, 32, None), 1, "at most 64"),
+    (lambda L: L.hq_take_channels_ex(16, 16, None, 2, None), 3, "channels NULL"),
     (lambda L: L.hq_matmul_q8_ex(16, 17, 16, 16, 16, 64, 0, 1, None), 2, "xq"),
     (lambda L: L.hq_matmul_q6_ex(16, 16, 16, 12, 16, 64, 0, 1, None), 2, "wq"),
     (lambda L: L.hq_matmul_q8r_tile_ex(16, 16, 16, 16, 16, 16, 64, 0, 1, 3, 4, 8, None), 2, "frame"),
