@@ -544,14 +544,14 @@ struct TernaryChunk {
   template <int T, bool STAGE>
   HQ_DEV void run(FoldL<T, L> &f, const TernaryActs<T, STAGE> &A, int it0, int steps, int groups, int slot, int lane,
                   float acc[T]) const {
+    // every step of the chunk, also those past the row (their lanes' parts are +0, which leaves an accumulator as it
+    // is: one is never -0): no branch between a chunk's loads and their use
 #pragma unroll
     for (int u = 0; u < kTernarySteps; u++) {
       const int it = it0 + u;
-      if (it < steps) {  // uniform in the wave
-        const int g = it * L + lane;
-        const bool valid = g < groups;
-        ternary_step<T, STAGE, L, BIN>(f, A, w[u], half_to_float(h[u]), valid ? g : 0, valid, it & 1, slot, lane, acc);
-      }
+      const int g = it * L + lane;
+      const bool valid = g < groups;
+      ternary_step<T, STAGE, L, BIN>(f, A, w[u], half_to_float(h[u]), valid ? g : 0, valid, it & 1, slot, lane, acc);
     }
   }
 };
@@ -586,7 +586,6 @@ __global__ __launch_bounds__(256) void gemv_ternary(GemvBatch batch) {
   for (int t = 0; t < T; t++) acc[t] = 0.0f;
   const int steps = (groups + L - 1) / L;
   TernaryChunk<L, BIN> a, b;
-  if (steps > 0) a.load(wrow, srow, 0, lane, groups);  // the first codes in flight during the staging
   if (STAGE) {
     // every token's n bytes (a group's 128 in 144), then its n/32 scales and n/32 sums: 16 bytes a thread at a time,
     // eight loads of a thread in flight before their stores
@@ -608,15 +607,20 @@ __global__ __launch_bounds__(256) void gemv_ternary(GemvBatch batch) {
           else if (o < J.n + J.n / 4) *(uint4 *)(acts + t * per + gb + (o - J.n)) = v[u];
         }
       }
-    __syncthreads();
   }
+  // the first codes in flight during the barrier (issued after the staging's loads: the memory counter is in order,
+  // so a store of staged bytes waits for no code)
+  a.load(wrow, srow, 0, lane, groups);
+  if (STAGE) __syncthreads();
+  // the next step's codes are loaded whether or not the row has that step (past its groups a lane loads its group 0
+  // again): the same loads outstanding on every path, so using a step's codes waits for them alone and not for the
+  // ones just issued
   for (int it = 0; it < steps; it += 2 * kTernarySteps) {
-    if (it + kTernarySteps < steps) b.load(wrow, srow, it + kTernarySteps, lane, groups);
+    b.load(wrow, srow, it + kTernarySteps, lane, groups);
     a.template run<T, STAGE>(f, A, it, steps, groups, slot, lane, acc);
-    if (it + kTernarySteps < steps) {
-      if (it + 2 * kTernarySteps < steps) a.load(wrow, srow, it + 2 * kTernarySteps, lane, groups);
-      b.template run<T, STAGE>(f, A, it + kTernarySteps, steps, groups, slot, lane, acc);
-    }
+    if (it + kTernarySteps >= steps) break;  // uniform
+    a.load(wrow, srow, it + 2 * kTernarySteps, lane, groups);
+    b.template run<T, STAGE>(f, A, it + kTernarySteps, steps, groups, slot, lane, acc);
   }
   float sum[T];
 #pragma unroll
