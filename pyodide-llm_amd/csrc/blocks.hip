@@ -200,7 +200,8 @@ HQ_DEV float block_fm(const BlockBytes<BYTES> &B) {
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// the products (matmul_sbr == matmul_sb): rows of 16 lanes, 4 rows a wave, a block of 256 weights a lane a step.
+// the products (matmul_sbr == matmul_sb): rows of L lanes (16, 4 rows a wave; 64 for rows of 32 blocks or more,
+// a row a wave), a block of 256 weights a lane a step.
 // The blocks of a launch are persistent: each copies its type's grid and sign table (at most 17 KB) into LDS once,
 // and its waves take groups of 4 rows in turn.
 // ---------------------------------------------------------------------------------------------------------------
@@ -216,17 +217,19 @@ HQ_DEV int sb_job_of(const SbBatch &b, int unit) {
   return j;
 }
 
-constexpr int kSbLanes = 16;
-constexpr int kSbRowsPerWave = 64 / kSbLanes;
+// the lanes of a row: 16, or 64 for rows of kSbLongRow blocks or more (the down projections: four times the waves,
+// a step a row)
+constexpr int kSbLongRow = 32;
+constexpr int sb_lanes(int blocks) { return blocks >= kSbLongRow ? 64 : 16; }
 
 template <int TY> constexpr int lds_table_bytes() {
   return grid_bytes<TY>() + (reads_signs<TY>() ? 1024 : 0) > 0 ? grid_bytes<TY>() + (reads_signs<TY>() ? 1024 : 0)
                                                                 : 16;
 }
 
-template <int TY, int T>
+template <int TY, int T, int L>
 __global__ __launch_bounds__(256) void gemv_sb(SbBatch batch) {
-  constexpr int L = kSbLanes;
+  constexpr int R = 64 / L;  // rows a wave
   constexpr int BYTES = sb_block_bytes(TY);
   constexpr int GRID = grid_bytes<TY>();
   __shared__ FoldL<T, L> fold[4];
@@ -251,7 +254,7 @@ __global__ __launch_bounds__(256) void gemv_sb(SbBatch batch) {
   for (int unit = blockIdx.x * 4 + wave; unit < units; unit += gridDim.x * 4) {
     const int jb = sb_job_of(batch, unit);
     const Job &J = batch.job[jb];
-    const int row_u = J.r0 + (unit - batch.unit0[jb]) * kSbRowsPerWave + slot;
+    const int row_u = J.r0 + (unit - batch.unit0[jb]) * R + slot;
     const bool live = row_u < J.r1;
     const int row = live ? row_u : J.r1 - 1;
     const int blocks = J.n >> 8;
@@ -337,31 +340,35 @@ __global__ __launch_bounds__(256) void gemv_sb(SbBatch batch) {
   }
 }
 
-// a launch's blocks: as many as stay resident together (at most the groups of 4 rows over 4)
-template <int TY, int T>
+// a launch's blocks: as many as stay resident together (at most the waves' groups of rows over 4)
+template <int TY, int T, int L>
 hipError_t launch_tt(const SbBatch &b, hipStream_t s) {
   static int per_cu[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
   if (per_cu[dev] == 0) {
     int k = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&k, gemv_sb<TY, T>, 256, 0) != hipSuccess || k < 1) k = 1;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&k, gemv_sb<TY, T, L>, 256, 0) != hipSuccess || k < 1) k = 1;
     per_cu[dev] = k;
   }
   const int want = (b.unit0[b.njobs] + 3) / 4, cap = per_cu[dev] * cu_count();
-  hipLaunchKernelGGL((gemv_sb<TY, T>), dim3(want < cap ? want : cap), dim3(256), 0, s, b);
+  hipLaunchKernelGGL((gemv_sb<TY, T, L>), dim3(want < cap ? want : cap), dim3(256), 0, s, b);
   return hipGetLastError();
 }
 
-template <int TY>
-hipError_t launch_type(const SbBatch &b, int T, hipStream_t s) {
+template <int TY, int L>
+hipError_t launch_tl(const SbBatch &b, int T, hipStream_t s) {
   switch (T) {
-  case 1: return launch_tt<TY, 1>(b, s);
-  case 2: return launch_tt<TY, 2>(b, s);
-  case 3: return launch_tt<TY, 3>(b, s);
-  case 4: return launch_tt<TY, 4>(b, s);
+  case 1: return launch_tt<TY, 1, L>(b, s);
+  case 2: return launch_tt<TY, 2, L>(b, s);
+  case 3: return launch_tt<TY, 3, L>(b, s);
+  case 4: return launch_tt<TY, 4, L>(b, s);
   default: return hipErrorInvalidValue;
   }
+}
+template <int TY>
+hipError_t launch_type(const SbBatch &b, int T, int L, hipStream_t s) {
+  return L == 64 ? launch_tl<TY, 64>(b, T, s) : launch_tl<TY, 16>(b, T, s);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -515,29 +522,33 @@ hipError_t launch_sb_row(float *out, const char *w, const uint8_t *tab, int32_t 
 hipError_t launch_sb(const Job *jobs, int32_t njobs, hipStream_t s) {
   if (njobs < 1 || njobs > kMaxJobs) return hipErrorInvalidValue;
   SbBatch b{};
+  int longest = 0;
+  for (int j = 0; j < njobs; j++) longest = (jobs[j].n >> 8) > longest ? (jobs[j].n >> 8) : longest;
+  // (a prompt's slices of 2..4 tokens keep 16 lanes: their steps are long enough)
+  const int L = jobs[0].count == 1 ? sb_lanes(longest) : 16, R = 64 / L;
   int units = 0;
   for (int j = 0; j < njobs; j++) {
     if (jobs[j].type != jobs[0].type || jobs[j].count != jobs[0].count || jobs[j].ws != jobs[0].ws)
       return hipErrorInvalidValue;
     b.job[j] = jobs[j];
     b.unit0[j] = units;
-    units += (jobs[j].r1 - jobs[j].r0 + kSbRowsPerWave - 1) / kSbRowsPerWave;
+    units += (jobs[j].r1 - jobs[j].r0 + R - 1) / R;
   }
   b.unit0[njobs] = units;
   b.njobs = njobs;
   if (units == 0) return hipSuccess;
   const int T = jobs[0].count;
   switch (jobs[0].type) {
-  case Q2_K: return launch_type<Q2_K>(b, T, s);
-  case Q4_K: return launch_type<Q4_K>(b, T, s);
-  case IQ2_XXS: return launch_type<IQ2_XXS>(b, T, s);
-  case IQ2_XS: return launch_type<IQ2_XS>(b, T, s);
-  case IQ2_S: return launch_type<IQ2_S>(b, T, s);
-  case IQ3_XXS: return launch_type<IQ3_XXS>(b, T, s);
-  case IQ3_S: return launch_type<IQ3_S>(b, T, s);
-  case IQ1_S: return launch_type<IQ1_S>(b, T, s);
-  case IQ1_M: return launch_type<IQ1_M>(b, T, s);
-  case IQ4_XS: return launch_type<IQ4_XS>(b, T, s);
+  case Q2_K: return launch_type<Q2_K>(b, T, L, s);
+  case Q4_K: return launch_type<Q4_K>(b, T, L, s);
+  case IQ2_XXS: return launch_type<IQ2_XXS>(b, T, L, s);
+  case IQ2_XS: return launch_type<IQ2_XS>(b, T, L, s);
+  case IQ2_S: return launch_type<IQ2_S>(b, T, L, s);
+  case IQ3_XXS: return launch_type<IQ3_XXS>(b, T, L, s);
+  case IQ3_S: return launch_type<IQ3_S>(b, T, L, s);
+  case IQ1_S: return launch_type<IQ1_S>(b, T, L, s);
+  case IQ1_M: return launch_type<IQ1_M>(b, T, L, s);
+  case IQ4_XS: return launch_type<IQ4_XS>(b, T, L, s);
   default: return hipErrorInvalidValue;
   }
 }
