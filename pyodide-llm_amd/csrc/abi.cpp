@@ -98,6 +98,8 @@ int32_t check_blocks_job(hq::Kind kind, const hq::Job &j) {
   if (j.r1 == j.r0 || j.count == 0) return HQ_OK;
   if (!j.out || !j.xq || !j.xs || !j.wq || !j.ws) return fail(HQ_ERR_NULL, "%s: a NULL pointer", name);
   if (!aligned(j.wq, 2)) return fail(HQ_ERR_ALIGNMENT, "%s: w not 2-byte aligned", name);
+  if ((int64_t)j.r1 * (j.n >> 8) * hq::sb_block_bytes(j.type) > 0xFFFFFFF0LL)
+    return fail(HQ_ERR_ARGUMENT, "%s: rows 0..%d of w take 4 GiB or more", name, j.r1);
   if (!aligned(j.ws, 16)) return fail(HQ_ERR_ALIGNMENT, "%s: the tables not 16-byte aligned", name);
   if (!aligned(j.xq, 16) || !aligned(j.xs, 16)) return fail(HQ_ERR_ALIGNMENT, "%s: xq or xs not 16-byte aligned", name);
   if (!aligned(j.out, 4)) return fail(HQ_ERR_ALIGNMENT, "%s: xout not 4-byte aligned", name);

@@ -54,6 +54,16 @@ struct BlockBytes {
 #pragma unroll
     for (int i = 0; i < N; i++) d[i] = odd ? __builtin_amdgcn_alignbit(i + 1 < M ? r[i + 1] : 0u, r[i], 16) : r[i];
   }
+  // the same from a buffer whose byte `start` (even) is the block's first: M dwords always loaded (past the buffer's
+  // end they read 0), the funnel shift 0 or 16 bits: no branch
+  HQ_DEV void load(__amdgpu_buffer_rsrc_t r, uint32_t start) {
+    const uint32_t a = start & ~3u, shift = (start & 2u) * 8u;
+    uint32_t q[M];
+#pragma unroll
+    for (int i = 0; i < M; i++) q[i] = __builtin_amdgcn_raw_buffer_load_b32(r, (int)(a + 4u * i), 0, 0);
+#pragma unroll
+    for (int i = 0; i < N; i++) d[i] = __builtin_amdgcn_alignbit(i + 1 < M ? q[i + 1] : 0u, q[i], shift);
+  }
   HQ_DEV uint32_t u8(int x) const { return (d[x >> 2] >> (8 * (x & 3))) & 0xffu; }
   HQ_DEV uint32_t u16(int x) const { return (d[x >> 2] >> (8 * (x & 3))) & 0xffffu; }  // x even
   HQ_DEV uint32_t u32(int x) const {                                                  // x even
@@ -211,15 +221,42 @@ struct SbBatch {
   int32_t njobs;
 };
 
+// the job of a unit (the units of the jobs one after the other): counted, not searched, so that no branch comes
+// between a wave's loads and their use
 HQ_DEV int sb_job_of(const SbBatch &b, int unit) {
   int j = 0;
-  while (j + 1 < b.njobs && unit >= b.unit0[j + 1]) ++j;
+#pragma unroll
+  for (int i = 1; i < kMaxJobs; i++) j += (i < b.njobs && unit >= b.unit0[i]) ? 1 : 0;
   return j;
 }
 
 // the lanes of a row: 16, or 64 for rows of kSbLongRow blocks or more (the down projections: four times the waves,
 // a step a row)
+// lane `lane`'s block of step `it` of unit `unit` (a unit: the R = 64 / L rows of a wave; past the row's blocks,
+// its block 0; past the job's rows, its last row), row slot `slot`, loaded through a buffer over the job's rows: its
+// base the 4-byte word the weights start in, its size the whole words they take (a word holding a byte of them lies
+// in their allocation's pages), so that a load of a word past them reads zeros (the host refuses a matrix of 4 GiB
+// or more)
+template <int BYTES, int L>
+HQ_DEV void sb_load_block(BlockBytes<BYTES> &B, const SbBatch &b, int unit, int it, int slot, int lane) {
+  const int jb = sb_job_of(b, unit);
+  const Job &J = b.job[jb];
+  const int row_u = J.r0 + (unit - b.unit0[jb]) * (64 / L) + slot;
+  const int row = row_u < J.r1 ? row_u : J.r1 - 1;
+  const int blocks = J.n >> 8, blk = it * L + lane;
+  const uintptr_t at = (uintptr_t)J.wq;
+  const uint32_t delta = (uint32_t)(at & 3u);
+  const int64_t end = delta + (int64_t)J.r1 * blocks * BYTES;
+  B.load(resource((const char *)(at - delta), (end + 3) & ~(int64_t)3),
+         delta + (uint32_t)(((int64_t)row * blocks + (blk < blocks ? blk : 0)) * BYTES));
+}
+
 constexpr int kSbLongRow = 32;
+// the most a launch stages of a token's activations (n + n/2 bytes: n up to 32768)
+#ifndef HQ_SB_STAGE_MAX
+#define HQ_SB_STAGE_MAX (48 * 1024)
+#endif
+constexpr size_t kSbStageMax = HQ_SB_STAGE_MAX;
 constexpr int sb_lanes(int blocks) { return blocks >= kSbLongRow ? 64 : 16; }
 
 template <int TY> constexpr int lds_table_bytes() {
@@ -227,19 +264,32 @@ template <int TY> constexpr int lds_table_bytes() {
                                                                 : 16;
 }
 
-template <int TY, int T, int L>
+// STAGE (one token, and every job of the launch the same activations): the block copies the token's n bytes and
+// its n/2 bytes of scales and sums into LDS first, so a step's activations are LDS reads, which the next step's block
+// loads in flight do not hold up (a vector memory load waits for every one issued before it)
+template <int TY, int T, int L, bool STAGE>
 __global__ __launch_bounds__(256) void gemv_sb(SbBatch batch) {
   constexpr int R = 64 / L;  // rows a wave
   constexpr int BYTES = sb_block_bytes(TY);
   constexpr int GRID = grid_bytes<TY>();
   __shared__ FoldL<T, L> fold[4];
   __shared__ __align__(16) uint8_t table[lds_table_bytes<TY>()];
+  extern __shared__ __align__(16) char staged[];
   const uint8_t *tab = (const uint8_t *)batch.job[0].ws;  // every job of a launch has the same tables' area
   {
     const uint4 *from = (const uint4 *)(tab + grid_at<TY>());
     for (int i = threadIdx.x; i < GRID / 16; i += 256) ((uint4 *)table)[i] = from[i];
     if (reads_signs<TY>())
       for (int i = threadIdx.x; i < 1024 / 16; i += 256) ((uint4 *)(table + GRID))[i] = ((const uint4 *)(tab + T_SIGNS))[i];
+  }
+  if (STAGE) {
+    const Job &J0 = batch.job[0];
+    const int per = J0.n + J0.n / 2;
+    for (int i = threadIdx.x; i < per / 16; i += 256) {
+      const int o = 16 * i;
+      const char *from = o < J0.n ? J0.xq + o : J0.xs + (o - J0.n);
+      *(uint4 *)(staged + o) = *(const uint4 *)from;
+    }
   }
   uint32_t iq4[4] = {0u, 0u, 0u, 0u};
   if (TY == IQ4_XS) {
@@ -248,127 +298,146 @@ __global__ __launch_bounds__(256) void gemv_sb(SbBatch batch) {
   }
   __syncthreads();
   const int lane = threadIdx.x & (L - 1);
-  const int wave = threadIdx.x >> 6, slot = (threadIdx.x & 63) / L;
+  // the wave's number as a scalar: its units, jobs and buffers are then the wave's own (scalar registers)
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), slot = (threadIdx.x & 63) / L;
   FoldL<T, L> &f = fold[wave];
-  const int units = batch.unit0[batch.njobs];
-  for (int unit = blockIdx.x * 4 + wave; unit < units; unit += gridDim.x * 4) {
+  const int units = batch.unit0[batch.njobs], stride = gridDim.x * 4;
+  int unit = blockIdx.x * 4 + wave, it = 0, count = 0;
+  if (unit >= units) return;  // (no barrier follows)
+  // a wave's steps one after the other (a step: a unit's rows, a block a lane), the next step's blocks loaded before
+  // this one is decoded; past the wave's last step it loads this step's blocks again, so every step issues the same
+  // loads and a step's decode waits only for its own
+  BlockBytes<BYTES> B;
+  sb_load_block<BYTES, L>(B, batch, unit, it, slot, lane);
+  float acc[T];
+#pragma unroll
+  for (int t = 0; t < T; t++) acc[t] = 0.0f;
+  for (;;) {
     const int jb = sb_job_of(batch, unit);
     const Job &J = batch.job[jb];
     const int row_u = J.r0 + (unit - batch.unit0[jb]) * R + slot;
     const bool live = row_u < J.r1;
     const int row = live ? row_u : J.r1 - 1;
-    const int blocks = J.n >> 8;
-    const char *wrow = J.wq + (int64_t)row * blocks * BYTES;
+    const int blocks = J.n >> 8, steps = (blocks + L - 1) / L;
+    const bool last = it + 1 >= steps;
+    const int next_unit = last ? unit + stride : unit, next_it = last ? 0 : it + 1;
+    const bool more = next_unit < units;
+    BlockBytes<BYTES> Bn;
+    sb_load_block<BYTES, L>(Bn, batch, more ? next_unit : unit, more ? next_it : it, slot, lane);
     // token t's activations (n int8), its scales (n / 32 float32), its sums of 16 and of 8 (int16)
     const int8_t *xq[T];
     const float *xs[T];
     const int16_t *s16[T], *s8[T];
 #pragma unroll
     for (int t = 0; t < T; t++) {
-      xq[t] = (const int8_t *)(J.xq + t * J.frame);
-      xs[t] = (const float *)(J.xs + t * J.sframe);
+      xq[t] = STAGE ? (const int8_t *)staged : (const int8_t *)(J.xq + t * J.frame);
+      xs[t] = STAGE ? (const float *)(staged + J.n) : (const float *)(J.xs + t * J.sframe);
       s16[t] = (const int16_t *)(xs[t] + (J.n >> 5));
       s8[t] = s16[t] + (J.n >> 4);
     }
-    float acc[T];
-#pragma unroll
-    for (int t = 0; t < T; t++) acc[t] = 0.0f;
-    const int steps = (blocks + L - 1) / L;
-    for (int it = 0; it < steps; it++) {
-      const int b = it * L + lane;
-      const bool valid = b < blocks;
-      const int bl = valid ? b : 0;
-      BlockBytes<BYTES> B;
-      B.load(wrow + (int64_t)bl * BYTES);
-      int32_t G[T][8], Mi[T][8];
-#pragma unroll
-      for (int t = 0; t < T; t++)
-#pragma unroll
-        for (int k = 0; k < 8; k++) G[t][k] = Mi[t][k] = 0;
-#pragma unroll
-      for (int h = 0; h < 16; h++) {
-        Chunk c;
-        chunk<TY>(B, h, table, table + GRID, iq4, c);
-        uint32_t signed_part[4];
-#pragma unroll
-        for (int j = 0; j < 4; j++) signed_part[j] = c.mag[j] & c.neg[j];
-#pragma unroll
-        for (int t = 0; t < T; t++) {
-          const uint4 av = *(const uint4 *)(xq[t] + 256 * bl + 16 * h);
-          const int32_t a[4] = {(int32_t)av.x, (int32_t)av.y, (int32_t)av.z, (int32_t)av.w};
-          int32_t d = 0;
-#pragma unroll
-          for (int j = 0; j < 4; j++) d = sdot4((int32_t)c.mag[j], a[j], d);
-          if (has_signs<TY>()) {
-            int32_t e = 0;
-#pragma unroll
-            for (int j = 0; j < 4; j++) e = sdot4((int32_t)signed_part[j], a[j], e);
-            d -= 2 * e;
-          }
-          if (is_iq1<TY>()) {  // 8 dot(code, a) - (7 + 2 down) sum of each 8 (token.ts:93-99, 117-127)
-            const int32_t e0 = s8[t][32 * bl + 2 * h], e1 = s8[t][32 * bl + 2 * h + 1];
-            d = 8 * d - (7 + 2 * (int32_t)c.down0) * e0 - (7 + 2 * (int32_t)c.down1) * e1;
-          }
-          G[t][h >> 1] += c.S * d;
-          if (has_minimums<TY>()) Mi[t][h >> 1] += c.M * (int32_t)s16[t][16 * bl + h];
-        }
-      }
-      const float F = block_f<TY>(B), Fm = block_fm<TY>(B);
-#pragma unroll
-      for (int t = 0; t < T; t++) {
-        const float4 x0 = *(const float4 *)(xs[t] + 8 * bl), x1 = *(const float4 *)(xs[t] + 8 * bl + 4);
-        const float sl[4] = {x0.x, x0.y, x0.z, x0.w}, sh[4] = {x1.x, x1.y, x1.z, x1.w};
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-          float part = fmul(fadd(fmul((float)G[t][k], sl[k]), fmul((float)G[t][k + 4], sh[k])), F);
-          if (has_minimums<TY>())
-            part = fsub(part, fmul(fadd(fmul((float)Mi[t][k], sl[k]), fmul((float)Mi[t][k + 4], sh[k])), Fm));
-          f.v[it & 1][slot][t][k][lane] = valid ? part : 0.0f;  // +0 leaves a lane as it is: a lane is never -0
-        }
-      }
-      fold_step_l<T, L>(f, it & 1, slot, lane, acc);
-    }
-    // lanes 0..3 hold the four lanes' sums: ((l0 + l1) + l2) + l3 in lane 0 (math.ts:7-9)
-    float sum[T];
+    const int b = it * L + lane;
+    const bool valid = b < blocks;
+    const int bl = valid ? b : 0;
+    int32_t G[T][8], Mi[T][8];
 #pragma unroll
     for (int t = 0; t < T; t++)
-      sum[t] = fadd(fadd(fadd(acc[t], from_lane_plus<1>(acc[t])), from_lane_plus<2>(acc[t])), from_lane_plus<3>(acc[t]));
-    if (live && lane == 0) {
 #pragma unroll
-      for (int t = 0; t < T; t++) ((float *)(J.out + t * J.os))[row] = sum[t];
+      for (int k = 0; k < 8; k++) G[t][k] = Mi[t][k] = 0;
+#pragma unroll
+    for (int h = 0; h < 16; h++) {
+      Chunk c;
+      chunk<TY>(B, h, table, table + GRID, iq4, c);
+      uint32_t signed_part[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) signed_part[j] = c.mag[j] & c.neg[j];
+#pragma unroll
+      for (int t = 0; t < T; t++) {
+        const uint4 av = *(const uint4 *)(xq[t] + 256 * bl + 16 * h);
+        const int32_t a[4] = {(int32_t)av.x, (int32_t)av.y, (int32_t)av.z, (int32_t)av.w};
+        int32_t d = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) d = sdot4((int32_t)c.mag[j], a[j], d);
+        if (has_signs<TY>()) {
+          int32_t e = 0;
+#pragma unroll
+          for (int j = 0; j < 4; j++) e = sdot4((int32_t)signed_part[j], a[j], e);
+          d -= 2 * e;
+        }
+        if (is_iq1<TY>()) {  // 8 dot(code, a) - (7 + 2 down) sum of each 8 (token.ts:93-99, 117-127)
+          const int32_t e0 = s8[t][32 * bl + 2 * h], e1 = s8[t][32 * bl + 2 * h + 1];
+          d = 8 * d - (7 + 2 * (int32_t)c.down0) * e0 - (7 + 2 * (int32_t)c.down1) * e1;
+        }
+        G[t][h >> 1] += c.S * d;
+        if (has_minimums<TY>()) Mi[t][h >> 1] += c.M * (int32_t)s16[t][16 * bl + h];
+      }
     }
+    const float F = block_f<TY>(B), Fm = block_fm<TY>(B);
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+      const float4 x0 = *(const float4 *)(xs[t] + 8 * bl), x1 = *(const float4 *)(xs[t] + 8 * bl + 4);
+      const float sl[4] = {x0.x, x0.y, x0.z, x0.w}, sh[4] = {x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        float part = fmul(fadd(fmul((float)G[t][k], sl[k]), fmul((float)G[t][k + 4], sh[k])), F);
+        if (has_minimums<TY>())
+          part = fsub(part, fmul(fadd(fmul((float)Mi[t][k], sl[k]), fmul((float)Mi[t][k + 4], sh[k])), Fm));
+        f.v[count & 1][slot][t][k][lane] = valid ? part : 0.0f;  // +0 leaves a lane as it is: a lane is never -0
+      }
+    }
+    fold_step_l<T, L>(f, count & 1, slot, lane, acc);
+    ++count;
+    if (last) {
+      // lanes 0..3 hold the four lanes' sums: ((l0 + l1) + l2) + l3 in lane 0 (math.ts:7-9)
+      float sum[T];
+#pragma unroll
+      for (int t = 0; t < T; t++)
+        sum[t] = fadd(fadd(fadd(acc[t], from_lane_plus<1>(acc[t])), from_lane_plus<2>(acc[t])),
+                      from_lane_plus<3>(acc[t]));
+      if (live && lane == 0) {
+#pragma unroll
+        for (int t = 0; t < T; t++) ((float *)(J.out + t * J.os))[row] = sum[t];
+      }
+#pragma unroll
+      for (int t = 0; t < T; t++) acc[t] = 0.0f;
+    }
+    if (!more) break;
+    unit = next_unit;
+    it = next_it;
+    B = Bn;
   }
 }
 
-// a launch's blocks: as many as stay resident together (at most the waves' groups of rows over 4)
-template <int TY, int T, int L>
-hipError_t launch_tt(const SbBatch &b, hipStream_t s) {
-  static int per_cu[64];
+// a launch's blocks: as many as stay resident together (at most the waves' groups of rows over 4); lds: the staged
+// activations' bytes (0: none)
+template <int TY, int T, int L, bool STAGE>
+hipError_t launch_tt(const SbBatch &b, size_t lds, hipStream_t s) {
+  static int per_cu[64][16];  // by device and 4 KB of staged bytes
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  if (per_cu[dev] == 0) {
+  const int slot = (int)(lds / 4096) < 16 ? (int)(lds / 4096) : 15;
+  if (per_cu[dev][slot] == 0) {
     int k = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&k, gemv_sb<TY, T, L>, 256, 0) != hipSuccess || k < 1) k = 1;
-    per_cu[dev] = k;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&k, gemv_sb<TY, T, L, STAGE>, 256, 4096 * (slot + 1)) !=
+            hipSuccess || k < 1)
+      k = 1;
+    per_cu[dev][slot] = k;
   }
-  const int want = (b.unit0[b.njobs] + 3) / 4, cap = per_cu[dev] * cu_count();
-  hipLaunchKernelGGL((gemv_sb<TY, T, L>), dim3(want < cap ? want : cap), dim3(256), 0, s, b);
+  const int want = (b.unit0[b.njobs] + 3) / 4, cap = per_cu[dev][slot] * cu_count();
+  hipLaunchKernelGGL((gemv_sb<TY, T, L, STAGE>), dim3(want < cap ? want : cap), dim3(256), lds, s, b);
   return hipGetLastError();
 }
 
-template <int TY, int L>
-hipError_t launch_tl(const SbBatch &b, int T, hipStream_t s) {
+template <int TY>
+hipError_t launch_type(const SbBatch &b, int T, int L, size_t lds, hipStream_t s) {
   switch (T) {
-  case 1: return launch_tt<TY, 1, L>(b, s);
-  case 2: return launch_tt<TY, 2, L>(b, s);
-  case 3: return launch_tt<TY, 3, L>(b, s);
-  case 4: return launch_tt<TY, 4, L>(b, s);
+  case 1:
+    if (lds) return L == 64 ? launch_tt<TY, 1, 64, true>(b, lds, s) : launch_tt<TY, 1, 16, true>(b, lds, s);
+    return L == 64 ? launch_tt<TY, 1, 64, false>(b, 0, s) : launch_tt<TY, 1, 16, false>(b, 0, s);
+  case 2: return launch_tt<TY, 2, 16, false>(b, 0, s);
+  case 3: return launch_tt<TY, 3, 16, false>(b, 0, s);
+  case 4: return launch_tt<TY, 4, 16, false>(b, 0, s);
   default: return hipErrorInvalidValue;
   }
-}
-template <int TY>
-hipError_t launch_type(const SbBatch &b, int T, int L, hipStream_t s) {
-  return L == 64 ? launch_tl<TY, 64>(b, T, s) : launch_tl<TY, 16>(b, T, s);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -538,17 +607,26 @@ hipError_t launch_sb(const Job *jobs, int32_t njobs, hipStream_t s) {
   b.njobs = njobs;
   if (units == 0) return hipSuccess;
   const int T = jobs[0].count;
+  // one token's activations, the same for every job: staged in LDS (n + n/2 bytes) when they fit, for the types
+  // that read no grid (Q2_K, Q4_K, IQ4_XS: measured faster; the grids' gathers and the activations' reads would
+  // share the LDS)
+  const int ty = jobs[0].type;
+  bool same = T == 1 && (ty == Q2_K || ty == Q4_K || ty == IQ4_XS);
+  for (int j = 1; j < njobs; j++)
+    same = same && jobs[j].xq == jobs[0].xq && jobs[j].xs == jobs[0].xs && jobs[j].n == jobs[0].n;
+  const size_t stage_bytes = (size_t)jobs[0].n + jobs[0].n / 2;
+  const size_t lds = same && stage_bytes <= kSbStageMax ? stage_bytes : 0;
   switch (jobs[0].type) {
-  case Q2_K: return launch_type<Q2_K>(b, T, L, s);
-  case Q4_K: return launch_type<Q4_K>(b, T, L, s);
-  case IQ2_XXS: return launch_type<IQ2_XXS>(b, T, L, s);
-  case IQ2_XS: return launch_type<IQ2_XS>(b, T, L, s);
-  case IQ2_S: return launch_type<IQ2_S>(b, T, L, s);
-  case IQ3_XXS: return launch_type<IQ3_XXS>(b, T, L, s);
-  case IQ3_S: return launch_type<IQ3_S>(b, T, L, s);
-  case IQ1_S: return launch_type<IQ1_S>(b, T, L, s);
-  case IQ1_M: return launch_type<IQ1_M>(b, T, L, s);
-  case IQ4_XS: return launch_type<IQ4_XS>(b, T, L, s);
+  case Q2_K: return launch_type<Q2_K>(b, T, L, lds, s);
+  case Q4_K: return launch_type<Q4_K>(b, T, L, lds, s);
+  case IQ2_XXS: return launch_type<IQ2_XXS>(b, T, L, lds, s);
+  case IQ2_XS: return launch_type<IQ2_XS>(b, T, L, lds, s);
+  case IQ2_S: return launch_type<IQ2_S>(b, T, L, lds, s);
+  case IQ3_XXS: return launch_type<IQ3_XXS>(b, T, L, lds, s);
+  case IQ3_S: return launch_type<IQ3_S>(b, T, L, lds, s);
+  case IQ1_S: return launch_type<IQ1_S>(b, T, L, lds, s);
+  case IQ1_M: return launch_type<IQ1_M>(b, T, L, lds, s);
+  case IQ4_XS: return launch_type<IQ4_XS>(b, T, L, lds, s);
   default: return hipErrorInvalidValue;
   }
 }

@@ -20,6 +20,13 @@ HQ_DEV float fsub(float a, float b) { return __fsub_rn(a, b); }
 // v_dot4_i32_i8: c + the four products of signed bytes (exact in int32 for every byte)
 HQ_DEV int32_t sdot4(int32_t a, int32_t b, int32_t c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
+// a raw buffer over [base, base + bytes) (bytes clamped to 32 bits): a load past its end reads nothing and returns
+// zeros
+HQ_DEV __amdgpu_buffer_rsrc_t resource(const char *base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0,
+                                           (int)max((int64_t)0, min(bytes, (int64_t)0xFFFFFFFF)), 0x00020000);
+}
+
 // DPP moves within a row of 16 lanes (row_ror:n gives lane l the value of lane (l - n) mod 16 of its row)
 template <int CTRL>
 HQ_DEV int32_t dpp(int32_t v) {

@@ -66,13 +66,10 @@ HQ_DEV v16i zero16i() {
 HQ_DEV v4f zero4f() { return (v4f){0.0f, 0.0f, 0.0f, 0.0f}; }
 
 // ---- loads -----------------------------------------------------------------------------------------------------
-// A block's rows, tokens and scales are each one buffer resource (base and size in scalar registers): a thread's
-// offsets are set once, a stage moves them by a scalar offset, and a load past the size reads nothing and returns
-// zeros (the tiles past the last row or token, the groups past the last one: their results are never stored).
-HQ_DEV __amdgpu_buffer_rsrc_t resource(const char *base, int64_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0,
-                                           (int)max((int64_t)0, min(bytes, (int64_t)0xFFFFFFFF)), 0x00020000);
-}
+// A block's rows, tokens and scales are each one buffer resource (common.hpp's resource(): base and size in scalar
+// registers): a thread's offsets are set once, a stage moves them by a scalar offset, and a load past the size reads
+// nothing and returns zeros (the tiles past the last row or token, the groups past the last one: their results are
+// never stored).
 // direct loads into LDS: lane l's `size` bytes land at dst + size * l (dst the same in the whole wave, in M0; 2-byte
 // loads land zero-extended in 4-byte slots).  Written as the instructions themselves: the compiler, which tracks
 // such loads only a few at a time, would otherwise wait for every one in flight before each LDS read; here the

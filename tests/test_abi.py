@@ -66,6 +66,7 @@ def test_version(pkg):
     (lambda L: L.hq_matmul_sbr_ex(16, 16, 16, 16, 8, 256, 0, 1, 12, None), 2, "tables"),
     (lambda L: L.hq_matmul_sbr_ex(16, 16, 8, 16, 16, 256, 0, 1, 12, None), 2, "xq or xs"),
     (lambda L: L.hq_matmul_sbr_tile_ex(16, 16, 16, 16, 16, 256, 0, 1, 2, 4, 8, 12, None), 2, "token stride"),
+    (lambda L: L.hq_matmul_sbr_ex(16, 16, 16, 16, 16, 256, 0, 30000000, 12, None), 1, "4 GiB"),
     (lambda L: L.hq_sb_row_ex(16, 16, 16, 100, 16, None), 1, "multiple of 256"),
     (lambda L: L.hq_sums_x_batch(16, 16, 100, 1, 0, None), 1, "multiple of"),
     (lambda L: L.hq_add_columns_ex(16, 16, 16, -1, 8, None), 1, "count = -1"),
