@@ -197,6 +197,45 @@ def measure_decode(torch, pkg, args, phases, fused, with_wc):
     return out
 
 
+def measure_decode_m4(torch, pkg, args, phases):
+    """config 3's decode at M = 4: the same step for four tokens at once (each phase quantize_x of its input for the
+    four tokens in one launch, then one hq_phase whose jobs take the four: every weight read once for four tokens).
+    GB/s of the step's algorithmic bytes: the weights, four tokens' activations, four outputs a row."""
+    from pyodide_llm_amd import jobs
+    lib = pkg.library()
+    dev = "cuda:0"
+    T = 4
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(4)
+    acts = {}
+    for a, _ in phases:
+        if a.n not in acts:
+            frame = (a.n + a.n // 8 + 15) // 16 * 16
+            acts[a.n] = (torch.randn(T, a.n, device=dev, generator=gen),
+                         torch.empty(T * frame, dtype=torch.uint8, device=dev), frame)
+    outs = {}
+    tables, step_bytes = [], 0.0
+    for a, mats in phases:
+        x, buf, frame = acts[a.n]
+        entries = []
+        for m, out in mats:
+            o = outs.setdefault((m.rows, id(out)), torch.empty(T, m.rows, device=dev))
+            entries.append(jobs.job("matmul_q8r", o.data_ptr(), buf.data_ptr(), buf.data_ptr() + a.n, m.w.data_ptr(),
+                                    m.ws.data_ptr(), 0, m.n, rows=m.rows, count=T, os=4 * m.rows, as_=frame,
+                                    bs=frame))
+            step_bytes += m.bytes() + T * (a.bytes() + 4 * m.rows)
+        tables.append((a.n, x, buf, frame, jobs.table(entries), len(entries)))
+
+    def step(h):
+        for n, x, buf, frame, table, njobs in tables:
+            lib.hq_quantize_x_batch(buf.data_ptr(), buf.data_ptr() + n, x.data_ptr(), n, 64, T, frame, 4 * n, h)
+            lib.hq_phase(table, njobs, 16, h)
+    sec = _graph_time(torch, step, max(3, args.steps // 2))
+    pkg.check(lib.hq_last_error())
+    return {"M": T, "ms_per_step": round(1e3 * sec, 4), "GBps": round(step_bytes / sec / 1e9, 1),
+            "tokens_per_s": round(T / sec, 1), "step_bytes": step_bytes}
+
+
 def _graph_time(torch, launch, reps):
     """seconds a replay of a graph of launch()'s launches takes, over `reps` replays between HIP events"""
     stream = torch.cuda.Stream()
@@ -639,6 +678,7 @@ def main():
     fused = measure_decode(torch, pkg, args, phases, fused=True, with_wc=False)
     separate = measure_decode(torch, pkg, args, phases, fused=False, with_wc=False)
     separate_wc = measure_decode(torch, pkg, args, phases, fused=False, with_wc=True)
+    decode_m4 = measure_decode_m4(torch, pkg, args, phases)
     del layers, head, phases
     torch.cuda.empty_cache()
     gemm = None if args.no_gemm else measure_gemm(torch, pkg, args)
@@ -662,6 +702,7 @@ def main():
                      "bytes_per_launch": round(derived["gemv_bytes_per_launch"])},
         "cpu_baseline": cpu,
         "detail": {"fused": fused, "quantize_then_phase": separate, "quantize_then_phase_with_wc": separate_wc,
+                   "decode_m4": decode_m4,
                    "prefill_gemm": gemm, "ceilings": ceilings, "configs": configs},
     }
     print(json.dumps(line))
