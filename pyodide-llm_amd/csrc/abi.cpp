@@ -148,6 +148,11 @@ int32_t run_blocks(hq::Kind kind, const std::vector<hq::Job> &jobs, hipStream_t 
   std::vector<hq::Job> parts;
   for (const hq::Job &j : jobs) {
     if (j.r1 == j.r0 || j.count == 0) continue;
+    if (j.count >= hq::kSbTileMin && j.frame > 0 && j.sframe > 0) {  // a prompt: the matrix-core tile
+      const int32_t st = hip_status(hq::launch_sb_tile(j, s), kind_name(kind));
+      if (st) return st;
+      continue;
+    }
     for (int32_t t0 = 0; t0 < j.count; t0 += hq::kGemvMaxTokens) {
       hq::Job part = j;
       part.count = j.count - t0 < hq::kGemvMaxTokens ? j.count - t0 : hq::kGemvMaxTokens;

@@ -100,10 +100,18 @@ template <int TY> constexpr int grid_bytes() {
 }
 template <int TY> constexpr bool reads_signs() { return TY == IQ2_XXS || TY == IQ2_XS || TY == IQ3_XXS; }
 
-// grid: the type's grid (grid_at's bytes of the area, in LDS or in global memory); signs: the sign table (T_SIGNS)
-template <int TY, int BYTES>
-HQ_DEV void chunk(const BlockBytes<BYTES> &B, int h, const uint8_t *grid, const uint8_t *signs, const uint32_t iq4[4],
-                  Chunk &c) {
+// a block's bytes in LDS (its first byte p even: the 2-byte loads are aligned): the same reads as BlockBytes's
+struct LdsBytes {
+  const uint8_t *p;
+  HQ_DEV uint32_t u8(int x) const { return p[x]; }
+  HQ_DEV uint32_t u16(int x) const { return *(const uint16_t *)(p + x); }  // x even
+  HQ_DEV uint32_t u32(int x) const { return u16(x) | (u16(x + 2) << 16); }   // x even
+};
+
+// grid: the type's grid (grid_at's bytes of the area, in LDS or in global memory); signs: the sign table (T_SIGNS);
+// B: the block's bytes (BlockBytes in registers, or LdsBytes)
+template <int TY, class BB>
+HQ_DEV void chunk(const BB &B, int h, const uint8_t *grid, const uint8_t *signs, const uint32_t iq4[4], Chunk &c) {
   const int g = h >> 1;
   c.M = 0;
   c.down0 = c.down1 = 0;
@@ -191,21 +199,21 @@ HQ_DEV void chunk(const BlockBytes<BYTES> &B, int h, const uint8_t *grid, const 
 
 // the block's F (blockScale, types.ts:302-310) and Fm (blockMinimum, 318-320); d: the block's own float16 (IQ1_M's
 // put together from its four words' tops, wholeScale 312-316)
-template <int TY, int BYTES>
-HQ_DEV float block_d(const BlockBytes<BYTES> &B) {
+template <int TY, class BB>
+HQ_DEV float block_d(const BB &B) {
   if (TY == IQ1_M)
     return half_to_float((B.u16(48) >> 12) | ((B.u16(50) >> 8) & 0xf0u) | ((B.u16(52) >> 4) & 0xf00u) | (B.u16(54) & 0xf000u));
   return half_to_float(B.u16(TY == Q2_K ? 80 : 0));
 }
-template <int TY, int BYTES>
-HQ_DEV float block_f(const BlockBytes<BYTES> &B) {
+template <int TY, class BB>
+HQ_DEV float block_f(const BB &B) {
   const float d = block_d<TY>(B);
   if (TY == IQ2_XXS || TY == IQ2_XS || TY == IQ2_S || TY == IQ1_S || TY == IQ1_M) return fmul(d, 0.125f);
   if (TY == IQ3_XXS) return fmul(d, 0.25f);
   return d;
 }
-template <int TY, int BYTES>
-HQ_DEV float block_fm(const BlockBytes<BYTES> &B) {
+template <int TY, class BB>
+HQ_DEV float block_fm(const BB &B) {
   return has_minimums<TY>() ? half_to_float(B.u16(TY == Q2_K ? 82 : 2)) : 0.0f;
 }
 
@@ -441,6 +449,298 @@ hipError_t launch_type(const SbBatch &b, int T, int L, size_t lds, hipStream_t s
 }
 
 // ---------------------------------------------------------------------------------------------------------------
+// the prompt tile (matmul_sbr_tile / matmul_sbw_tile for kSbTileMin tokens or more): a block takes 64 rows x 64
+// tokens, four waves of 32 x 32.  For each block of 256 weights it stages the tokens' activations (with their
+// scales and sums) and the rows' raw blocks into LDS, decodes the 64 blocks once (four chunks of 16 a thread, the
+// token kernel's decoder reading the LDS copy) into int8 tiles, and multiplies them on the matrix cores:
+// v_mfma_i32_32x32x32_i8, A = 32 tokens, B = 32 rows, K = 32 = a group, so a lane holds one row (l % 32) and 16
+// tokens (8 (r / 4) + 4 (l / 32) + r % 4).  The integers are exactly the token kernel's:
+//   signed grids: |W| and |W| of the negative weights in two tiles, d = C(|W|) - 2 C(|W| neg);
+//   a scale S for each 16 (IQ2_XS, IQ2_S, IQ1_M): two products a group, B zero in one half of the lanes (K 0..15
+//   is lanes 0..31's, K 16..31 lanes 32..63's), G = S_lo d_lo + S_hi d_hi; Q2_K's S W (at most 45) is its tile;
+//   IQ1: C of the codes, d = 8 C - (7 + 2 down) (sum of each 8); the K types' M against the sums of 16;
+// then each (row, token) adds f(f(f(G_k xs_k) + f(G_{k+4} xs_{k+4})) F) (less the minimums') to its lane k in block
+// order, and ((l0 + l1) + l2) + l3 at the end (types.ts:48-57): every (row, token) the token kernel's number.
+// ---------------------------------------------------------------------------------------------------------------
+typedef int32_t v4i_t __attribute__((ext_vector_type(4)));
+typedef int32_t v16i_t __attribute__((ext_vector_type(16)));
+
+constexpr int SBT_R = 64, SBT_T = 64;  // a block's rows and tokens
+constexpr int SBT_PITCH = 256 + 16;    // an LDS row of a block's 256 bytes (16 more: 16-byte reads of rows apart)
+
+template <int TY> constexpr bool tile_signed() { return has_signs<TY>(); }
+template <int TY> constexpr bool tile_split() { return TY == IQ2_XS || TY == IQ2_S || TY == IQ1_M; }
+
+template <int TY>
+struct SbTileLayout {
+  static constexpr int BYTES = sb_block_bytes(TY);
+  static constexpr int WORDS = (BYTES + 2 + 3) / 4;  // the aligned words that hold a block
+  static constexpr int RAWP = 4 * WORDS;
+  static constexpr int X = 0;                                      // int8 [SBT_T][SBT_PITCH]
+  static constexpr int XS = X + SBT_T * SBT_PITCH;                 // float [8][SBT_T]
+  static constexpr int S16 = XS + 8 * SBT_T * 4;                   // int32 [16][SBT_T]
+  static constexpr int S8 = S16 + 16 * SBT_T * 4;                  // int32 [32][SBT_T] (IQ1_M)
+  static constexpr int RAW = S8 + (TY == IQ1_M ? 32 * SBT_T * 4 : 0);  // bytes [SBT_R][RAWP]
+  static constexpr int WM = RAW + SBT_R * RAWP;                    // int8 [SBT_R][SBT_PITCH]
+  static constexpr int WN = WM + SBT_R * SBT_PITCH;                // int8 [SBT_R][SBT_PITCH] (signed grids)
+  static constexpr int RS = WN + (tile_signed<TY>() ? SBT_R * SBT_PITCH : 0);  // int8 [SBT_R][16] S
+  static constexpr int RM = RS + SBT_R * 16;                       // int8 [SBT_R][16] M
+  static constexpr int RD = RM + SBT_R * 16;                       // uint8 [SBT_R][16] IQ1's shifts
+  static constexpr int FF = RD + SBT_R * 16;                       // float [SBT_R] F, then [SBT_R] Fm
+  static constexpr int GRIDS = FF + 2 * SBT_R * 4;                 // the type's grid and sign table
+  static constexpr int SIZE = GRIDS + lds_table_bytes<TY>();
+};
+
+HQ_DEV int32_t sbyte(uint32_t w, int i) { return (int32_t)(int8_t)(uint8_t)(w >> (8 * i)); }
+
+template <int TY>
+__global__ __launch_bounds__(256) void gemm_sb(Job J) {
+  using Lay = SbTileLayout<TY>;
+  constexpr int BYTES = Lay::BYTES, WORDS = Lay::WORDS, GRID = grid_bytes<TY>();
+  extern __shared__ __align__(16) char lds[];
+  int8_t *x = (int8_t *)(lds + Lay::X);
+  float *xsT = (float *)(lds + Lay::XS);
+  int32_t *s16T = (int32_t *)(lds + Lay::S16), *s8T = (int32_t *)(lds + Lay::S8);
+  uint8_t *raw = (uint8_t *)(lds + Lay::RAW);
+  int8_t *wm = (int8_t *)(lds + Lay::WM), *wn = (int8_t *)(lds + Lay::WN);
+  int8_t *rs = (int8_t *)(lds + Lay::RS), *rm = (int8_t *)(lds + Lay::RM);
+  uint8_t *rd = (uint8_t *)(lds + Lay::RD);
+  float *ff = (float *)(lds + Lay::FF);
+  uint8_t *table = (uint8_t *)(lds + Lay::GRIDS);
+
+  const int tid = threadIdx.x;
+  const int nrt = (J.r1 - J.r0 + SBT_R - 1) / SBT_R;
+  const int rt = blockIdx.x % nrt, tt = blockIdx.x / nrt;
+  const int r0 = J.r0 + SBT_R * rt, t0 = SBT_T * tt;
+  const int blocks = J.n >> 8;
+  const int64_t frame = J.frame;
+  // the type's grid and sign table, and IQ4_XS's values
+  const uint8_t *tab = (const uint8_t *)J.ws;
+  for (int i = tid; i < GRID / 16; i += 256) ((uint4 *)table)[i] = ((const uint4 *)(tab + grid_at<TY>()))[i];
+  if (reads_signs<TY>())
+    for (int i = tid; i < 1024 / 16; i += 256) ((uint4 *)(table + GRID))[i] = ((const uint4 *)(tab + T_SIGNS))[i];
+  uint32_t iq4[4] = {0u, 0u, 0u, 0u};
+  if (TY == IQ4_XS) {
+    const uint4 v = *(const uint4 *)(tab + T_IQ4);
+    iq4[0] = v.x; iq4[1] = v.y; iq4[2] = v.z; iq4[3] = v.w;
+  }
+  // buffers: the tile's tokens (a token past the prompt reads zeros) and the weights (the aligned words of rows
+  // 0 .. r1 - 1)
+  const int64_t tokens_left = (int64_t)J.count - t0;
+  const __amdgpu_buffer_rsrc_t rq = resource(J.xq + t0 * frame, tokens_left * frame);
+  const int64_t sframe = J.sframe;
+  const __amdgpu_buffer_rsrc_t ra = resource(J.xs + t0 * sframe, tokens_left * sframe);
+  const uintptr_t wat = (uintptr_t)J.wq;
+  const uint32_t wdelta = (uint32_t)(wat & 3u);
+  const int64_t wend = wdelta + (int64_t)J.r1 * blocks * BYTES;
+  const __amdgpu_buffer_rsrc_t rw = resource((const char *)(wat - wdelta), (wend + 3) & ~(int64_t)3);
+  // this thread's row for the decode: tile row tid / 4 (past the job's rows: its last), chunks 4 (tid % 4) ..
+  const int dr = tid >> 2, dq = tid & 3;
+  const int drow = r0 + dr < J.r1 ? r0 + dr : J.r1 - 1;
+  // the wave's 32 x 32: tokens 32 th .., rows 32 rh ..; the lane's row, and its 16 tokens' first of each four
+  const int wave = tid >> 6, lane = tid & 63, kh = lane >> 5, l32 = lane & 31;
+  const int th = wave & 1, rh = wave >> 1;
+  const int mrow = 32 * rh + l32, mtok = 32 * th + l32;
+  float acc[4][16];
+#pragma unroll
+  for (int k = 0; k < 4; k++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[k][r] = 0.0f;
+
+  for (int b = 0; b < blocks; b++) {
+    __syncthreads();  // (the last block's tiles read)
+    // ---- staging: the tokens' 256 bytes of the block, their 8 scales and their sums; the rows' raw blocks
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int idx = tid + 256 * u, tok = idx >> 4, q = idx & 15;
+      const v4i_t v = __builtin_amdgcn_raw_buffer_load_b128(rq, (int)(tok * frame + 256 * b + 16 * q), 0, 0);
+      *(v4i_t *)(x + tok * SBT_PITCH + 16 * q) = v;
+    }
+    if (tid < 128) {
+      const int tok = tid >> 1, half = tid & 1;
+      const v4i_t v = __builtin_amdgcn_raw_buffer_load_b128(ra, (int)(tok * sframe + 32 * b + 16 * half), 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; i++) xsT[(4 * half + i) * SBT_T + tok] = __int_as_float(v[i]);
+    } else if (has_minimums<TY>() || is_iq1<TY>()) {
+      const int tok = (tid - 128) >> 1, half = tid & 1;
+      const v4i_t v = __builtin_amdgcn_raw_buffer_load_b128(ra, (int)(tok * sframe + 4 * (J.n >> 5) + 32 * b + 16 * half), 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        s16T[(8 * half + 2 * i) * SBT_T + tok] = (int32_t)(int16_t)(v[i] & 0xffff);
+        s16T[(8 * half + 2 * i + 1) * SBT_T + tok] = (int32_t)(int16_t)((uint32_t)v[i] >> 16);
+      }
+    }
+    if (TY == IQ1_M) {
+      const int tok = tid >> 2, qq = tid & 3;
+      const v4i_t v = __builtin_amdgcn_raw_buffer_load_b128(
+          ra, (int)(tok * sframe + 4 * (J.n >> 5) + 2 * (J.n >> 4) + 64 * b + 16 * qq), 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        s8T[(8 * qq + 2 * i) * SBT_T + tok] = (int32_t)(int16_t)(v[i] & 0xffff);
+        s8T[(8 * qq + 2 * i + 1) * SBT_T + tok] = (int32_t)(int16_t)((uint32_t)v[i] >> 16);
+      }
+    }
+    for (int idx = tid; idx < SBT_R * WORDS; idx += 256) {
+      const int r = idx / WORDS, w = idx - r * WORDS;
+      const int row = r0 + r < J.r1 ? r0 + r : J.r1 - 1;
+      const uint32_t start = wdelta + (uint32_t)(((int64_t)row * blocks + b) * BYTES);
+      *(uint32_t *)(raw + r * Lay::RAWP + 4 * w) =
+          __builtin_amdgcn_raw_buffer_load_b32(rw, (int)((start & ~3u) + 4u * w), 0, 0);
+    }
+    __syncthreads();
+    // ---- decode: this thread's four chunks of its row's block into the tiles
+    {
+      const uint32_t start = wdelta + (uint32_t)(((int64_t)drow * blocks + b) * BYTES);
+      const LdsBytes B{raw + dr * Lay::RAWP + (start & 2u)};
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const int h = 4 * dq + u;
+        Chunk c;
+        chunk<TY>(B, h, table, table + GRID, iq4, c);
+        uint32_t m4[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) m4[j] = TY == Q2_K ? c.mag[j] * (uint32_t)c.S : c.mag[j];  // (S W <= 45)
+        *(uint4 *)(wm + dr * SBT_PITCH + 16 * h) = make_uint4(m4[0], m4[1], m4[2], m4[3]);
+        if (tile_signed<TY>())
+          *(uint4 *)(wn + dr * SBT_PITCH + 16 * h) =
+              make_uint4(c.mag[0] & c.neg[0], c.mag[1] & c.neg[1], c.mag[2] & c.neg[2], c.mag[3] & c.neg[3]);
+        rs[dr * 16 + h] = (int8_t)c.S;
+        rm[dr * 16 + h] = (int8_t)c.M;
+        rd[dr * 16 + h] = (uint8_t)(c.down0 | (c.down1 << 1));
+      }
+      if (dq == 0) {
+        ff[dr] = block_f<TY>(B);
+        ff[SBT_R + dr] = block_fm<TY>(B);
+      }
+    }
+    __syncthreads();
+    // ---- the products: the wave's 32 x 32, group pairs (k, k + 4)
+    const float F = ff[mrow], Fm = ff[SBT_R + mrow];
+    const uint4 S4 = *(const uint4 *)(rs + mrow * 16), M4 = *(const uint4 *)(rm + mrow * 16),
+                D4 = *(const uint4 *)(rd + mrow * 16);
+    const uint32_t Sw[4] = {S4.x, S4.y, S4.z, S4.w}, Mw[4] = {M4.x, M4.y, M4.z, M4.w}, Dw[4] = {D4.x, D4.y, D4.z, D4.w};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      int32_t G[2][16], Mi[2][16];
+#pragma unroll
+      for (int e = 0; e < 2; e++) {
+        const int gg = k + 4 * e, c0 = 2 * gg, c1 = 2 * gg + 1;
+        const v4i_t A = *(const v4i_t *)(x + mtok * SBT_PITCH + 32 * gg + 16 * kh);
+        const v4i_t Bm = *(const v4i_t *)(wm + mrow * SBT_PITCH + 32 * gg + 16 * kh);
+        const v16i_t zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+        const int32_t S0 = sbyte(Sw[c0 >> 2], c0 & 3), S1 = sbyte(Sw[c1 >> 2], c1 & 3);
+        if (tile_split<TY>()) {
+          const v4i_t z4 = {0, 0, 0, 0};
+          v16i_t lo = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, kh == 0 ? Bm : z4, zero, 0, 0, 0);
+          v16i_t hi = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, kh == 1 ? Bm : z4, zero, 0, 0, 0);
+          if (tile_signed<TY>()) {
+            const v4i_t Bn = *(const v4i_t *)(wn + mrow * SBT_PITCH + 32 * gg + 16 * kh);
+            const v16i_t nlo = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, kh == 0 ? Bn : z4, zero, 0, 0, 0);
+            const v16i_t nhi = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, kh == 1 ? Bn : z4, zero, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+              lo[r] -= 2 * nlo[r];
+              hi[r] -= 2 * nhi[r];
+            }
+          }
+          if (is_iq1<TY>()) {  // 8 dot(code, a) - (7 + 2 down) (sum of each 8), for each of the two 16s
+            const uint32_t d0 = (Dw[c0 >> 2] >> (8 * (c0 & 3))) & 3u, d1 = (Dw[c1 >> 2] >> (8 * (c1 & 3))) & 3u;
+            const int32_t a0 = 7 + 2 * (int32_t)(d0 & 1u), b0 = 7 + 2 * (int32_t)(d0 >> 1);
+            const int32_t a1 = 7 + 2 * (int32_t)(d1 & 1u), b1 = 7 + 2 * (int32_t)(d1 >> 1);
+#pragma unroll
+            for (int m = 0; m < 4; m++) {
+              const int tk = 32 * th + 8 * m + 4 * kh;
+              const int4 e00 = *(const int4 *)(s8T + (2 * c0) * SBT_T + tk), e01 = *(const int4 *)(s8T + (2 * c0 + 1) * SBT_T + tk);
+              const int4 e10 = *(const int4 *)(s8T + (2 * c1) * SBT_T + tk), e11 = *(const int4 *)(s8T + (2 * c1 + 1) * SBT_T + tk);
+              const int32_t v00[4] = {e00.x, e00.y, e00.z, e00.w}, v01[4] = {e01.x, e01.y, e01.z, e01.w};
+              const int32_t v10[4] = {e10.x, e10.y, e10.z, e10.w}, v11[4] = {e11.x, e11.y, e11.z, e11.w};
+#pragma unroll
+              for (int i = 0; i < 4; i++) {
+                lo[4 * m + i] = 8 * lo[4 * m + i] - a0 * v00[i] - b0 * v01[i];
+                hi[4 * m + i] = 8 * hi[4 * m + i] - a1 * v10[i] - b1 * v11[i];
+              }
+            }
+          }
+#pragma unroll
+          for (int r = 0; r < 16; r++) G[e][r] = S0 * lo[r] + S1 * hi[r];
+        } else {
+          v16i_t C = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, Bm, zero, 0, 0, 0);
+          if (tile_signed<TY>()) {
+            const v4i_t Bn = *(const v4i_t *)(wn + mrow * SBT_PITCH + 32 * gg + 16 * kh);
+            const v16i_t Cn = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, Bn, zero, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 16; r++) C[r] -= 2 * Cn[r];
+          }
+          if (is_iq1<TY>()) {  // IQ1_S: one shift for the 32, against the sum of the 32
+            const int32_t a = 7 + 2 * (int32_t)((Dw[c0 >> 2] >> (8 * (c0 & 3))) & 1u);
+#pragma unroll
+            for (int m = 0; m < 4; m++) {
+              const int tk = 32 * th + 8 * m + 4 * kh;
+              const int4 e0 = *(const int4 *)(s16T + c0 * SBT_T + tk), e1 = *(const int4 *)(s16T + c1 * SBT_T + tk);
+              const int32_t v0[4] = {e0.x, e0.y, e0.z, e0.w}, v1[4] = {e1.x, e1.y, e1.z, e1.w};
+#pragma unroll
+              for (int i = 0; i < 4; i++) C[4 * m + i] = 8 * C[4 * m + i] - a * (v0[i] + v1[i]);
+            }
+          }
+#pragma unroll
+          for (int r = 0; r < 16; r++) G[e][r] = TY == Q2_K ? C[r] : S0 * C[r];
+        }
+        if (has_minimums<TY>()) {
+          const int32_t M0 = sbyte(Mw[c0 >> 2], c0 & 3), M1 = sbyte(Mw[c1 >> 2], c1 & 3);
+#pragma unroll
+          for (int m = 0; m < 4; m++) {
+            const int tk = 32 * th + 8 * m + 4 * kh;
+            const int4 e0 = *(const int4 *)(s16T + c0 * SBT_T + tk), e1 = *(const int4 *)(s16T + c1 * SBT_T + tk);
+            const int32_t v0[4] = {e0.x, e0.y, e0.z, e0.w}, v1[4] = {e1.x, e1.y, e1.z, e1.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) Mi[e][4 * m + i] = M0 * v0[i] + M1 * v1[i];
+          }
+        }
+      }
+#pragma unroll
+      for (int m = 0; m < 4; m++) {
+        const int tk = 32 * th + 8 * m + 4 * kh;
+        const float4 l4 = *(const float4 *)(xsT + k * SBT_T + tk), h4 = *(const float4 *)(xsT + (k + 4) * SBT_T + tk);
+        const float sl[4] = {l4.x, l4.y, l4.z, l4.w}, sh[4] = {h4.x, h4.y, h4.z, h4.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int r = 4 * m + i;
+          float part = fmul(fadd(fmul((float)G[0][r], sl[i]), fmul((float)G[1][r], sh[i])), F);
+          if (has_minimums<TY>())
+            part = fsub(part, fmul(fadd(fmul((float)Mi[0][r], sl[i]), fmul((float)Mi[1][r], sh[i])), Fm));
+          acc[k][r] = fadd(acc[k][r], part);
+        }
+      }
+    }
+  }
+  // ((l0 + l1) + l2) + l3 (math.ts:7-9): the lane's row, its 16 tokens
+  const int row = r0 + mrow;
+  if (row < J.r1) {
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int t = t0 + 32 * th + 8 * (r >> 2) + 4 * kh + (r & 3);
+      if (t < J.count) ((float *)(J.out + t * J.os))[row] = fadd(fadd(fadd(acc[0][r], acc[1][r]), acc[2][r]), acc[3][r]);
+    }
+  }
+}
+
+template <int TY>
+hipError_t launch_tile_type(const Job &j, hipStream_t s) {
+  static bool sized[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (!sized[dev]) {  // (more than 64 KB of LDS a block)
+    const hipError_t e = hipFuncSetAttribute((const void *)gemm_sb<TY>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             SbTileLayout<TY>::SIZE);
+    if (e != hipSuccess) return e;
+    sized[dev] = true;
+  }
+  const int nrt = (j.r1 - j.r0 + SBT_R - 1) / SBT_R, ntt = (j.count + SBT_T - 1) / SBT_T;
+  hipLaunchKernelGGL(gemm_sb<TY>, dim3(nrt * ntt), dim3(256), SbTileLayout<TY>::SIZE, s, j);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------------------------
 // sb_row: a row as float32 (row.ts), a chunk of 16 weights a thread
 // ---------------------------------------------------------------------------------------------------------------
 template <int TY>
@@ -585,6 +885,24 @@ hipError_t launch_sb_row(float *out, const char *w, const uint8_t *tab, int32_t 
   default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+// a prompt (kSbTileMin tokens or more) of one job through the tile
+hipError_t launch_sb_tile(const Job &j, hipStream_t s) {
+  if (j.r1 <= j.r0 || j.count <= 0) return hipSuccess;
+  switch (j.type) {
+  case Q2_K: return launch_tile_type<Q2_K>(j, s);
+  case Q4_K: return launch_tile_type<Q4_K>(j, s);
+  case IQ2_XXS: return launch_tile_type<IQ2_XXS>(j, s);
+  case IQ2_XS: return launch_tile_type<IQ2_XS>(j, s);
+  case IQ2_S: return launch_tile_type<IQ2_S>(j, s);
+  case IQ3_XXS: return launch_tile_type<IQ3_XXS>(j, s);
+  case IQ3_S: return launch_tile_type<IQ3_S>(j, s);
+  case IQ1_S: return launch_tile_type<IQ1_S>(j, s);
+  case IQ1_M: return launch_tile_type<IQ1_M>(j, s);
+  case IQ4_XS: return launch_tile_type<IQ4_XS>(j, s);
+  default: return hipErrorInvalidValue;
+  }
 }
 
 // jobs: one block type, one token count (1..4), one tables' area

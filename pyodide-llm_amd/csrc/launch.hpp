@@ -72,6 +72,10 @@ hipError_t launch_sb_tables(uint8_t *area, const uint8_t *codebooks, hipStream_t
 hipError_t launch_sums_x(char *xs, const char *xq, int32_t n, int32_t count, int64_t frame, hipStream_t s);
 hipError_t launch_sb_row(float *out, const char *w, const uint8_t *tab, int32_t n, int32_t type, hipStream_t s);
 hipError_t launch_sb(const Job *jobs, int32_t njobs, hipStream_t s);
+// a prompt of kSbTileMin tokens or more of one job (the sb kinds), on the matrix cores: every (row, token)
+// launch_sb's number
+constexpr int kSbTileMin = 16;
+hipError_t launch_sb_tile(const Job &job, hipStream_t s);
 hipError_t launch_signed_dots(int32_t *out, const int8_t *a, const int8_t *b, hipStream_t s);
 
 // the classifier's outlier channels: add_columns (y += the columns' products, in order); the columns of a packed

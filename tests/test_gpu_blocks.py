@@ -120,7 +120,8 @@ def test_matmul_sbr(k, arena, oracle, setup, name, t, nb):
 
 @pytest.mark.parametrize("name,t", TYPES)
 def test_matmul_sbr_tile(k, arena, oracle, setup, name, t):
-    """1..17 tokens (4 a launch), rows cut anywhere; matmul_sbw_tile the same numbers"""
+    """1..100 tokens (4 a launch below 16, the matrix-core tile from 16: one, two and partial tiles of 64),
+    rows cut anywhere; matmul_sbw_tile the same numbers"""
     row, tab = setup
     area = put_tables(k, arena, row)
     rng = np.random.default_rng(77 + t)
@@ -130,7 +131,7 @@ def test_matmul_sbr_tile(k, arena, oracle, setup, name, t):
     wbytes = blocks.reshape(-1)
     w = arena.put(wbytes)
     frame = ((n + n // 2 + 15) // 16) * 16
-    tokens = 17
+    tokens = 100
     buf = np.zeros(tokens * frame, np.uint8)
     fulls = []
     for tk in range(tokens):
@@ -140,7 +141,7 @@ def test_matmul_sbr_tile(k, arena, oracle, setup, name, t):
         fulls.append(oracle.matmul_sbr(q, act, wbytes, tab, n, t))
     xq = arena.put(buf)
     os_ = 4 * (rows + 3)
-    for count in (1, 2, 3, 4, 5, 8, 9, 17):
+    for count in (1, 2, 3, 4, 5, 8, 9, 16, 17, 64, 65, 100):
         for r0, r1 in [(0, rows), (2, 9), (rows - 1, rows)]:
             for form in ("matmul_sbr_tile", "matmul_sbw_tile"):
                 out = arena.alloc(os_ * count, fill=np.full(os_ * count // 4, -7, F))
