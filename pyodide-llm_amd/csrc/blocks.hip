@@ -449,11 +449,11 @@ hipError_t launch_type(const SbBatch &b, int T, int L, size_t lds, hipStream_t s
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// the prompt tile (matmul_sbr_tile / matmul_sbw_tile for kSbTileMin tokens or more): a block takes 64 rows x 64
-// tokens, four waves of 32 x 32.  For each block of 256 weights it stages the tokens' activations (with their
-// scales and sums) and the rows' raw blocks into LDS, decodes the 64 blocks once (four chunks of 16 a thread, the
-// token kernel's decoder reading the LDS copy) into int8 tiles, and multiplies them on the matrix cores:
-// v_mfma_i32_32x32x32_i8, A = 32 tokens, B = 32 rows, K = 32 = a group, so a lane holds one row (l % 32) and 16
+// the prompt tile (matmul_sbr_tile / matmul_sbw_tile for kSbTileMin tokens or more): a block takes 32 rows x NT
+// tokens (NT 32 or 64).  For each block of 256 weights it stages the tokens' activations (with their scales and
+// sums) and the rows' raw blocks into LDS, decodes the 32 blocks once (two chunks of 16 a thread, the token kernel's
+// decoder reading the LDS copy) into int8 tiles, and multiplies them on the matrix cores:
+// v_mfma_i32_32x32x32_i8, A = 32 tokens, B = the 32 rows, K = 32 = a group, so a lane holds one row (l % 32) and 16
 // tokens (8 (r / 4) + 4 (l / 32) + r % 4).  The integers are exactly the token kernel's:
 //   signed grids: |W| and |W| of the negative weights in two tiles, d = C(|W|) - 2 C(|W| neg);
 //   a scale S for each 16 (IQ2_XS, IQ2_S, IQ1_M): two products a group, B zero in one half of the lanes (K 0..15
@@ -461,47 +461,150 @@ hipError_t launch_type(const SbBatch &b, int T, int L, size_t lds, hipStream_t s
 //   IQ1: C of the codes, d = 8 C - (7 + 2 down) (sum of each 8); the K types' M against the sums of 16;
 // then each (row, token) adds f(f(f(G_k xs_k) + f(G_{k+4} xs_{k+4})) F) (less the minimums') to its lane k in block
 // order, and ((l0 + l1) + l2) + l3 at the end (types.ts:48-57): every (row, token) the token kernel's number.
+// The four waves split the tokens and the lanes k: NT = 64, two token halves x two pairs of lanes; NT = 32, a lane
+// k a wave; the lanes meet in LDS at the end in that order.  The next block's bytes are loaded into registers while
+// this one is decoded and multiplied, and stored into LDS after.
 // ---------------------------------------------------------------------------------------------------------------
 typedef int32_t v4i_t __attribute__((ext_vector_type(4)));
 typedef int32_t v16i_t __attribute__((ext_vector_type(16)));
 
-constexpr int SBT_R = 64, SBT_T = 64;  // a block's rows and tokens
-constexpr int SBT_PITCH = 256 + 16;    // an LDS row of a block's 256 bytes (16 more: 16-byte reads of rows apart)
+constexpr int SBT_R = 32;            // a block's rows
+constexpr int SBT_PITCH = 256 + 16;  // an LDS row of a block's 256 bytes (16 more: 16-byte reads of rows apart)
+#ifndef HQ_SB_TILE_NT
+#define HQ_SB_TILE_NT 0  // 0: 64 tokens a block where that gives enough blocks, else 32
+#endif
 
 template <int TY> constexpr bool tile_signed() { return has_signs<TY>(); }
 template <int TY> constexpr bool tile_split() { return TY == IQ2_XS || TY == IQ2_S || TY == IQ1_M; }
+template <int TY> constexpr bool tile_sums16() { return has_minimums<TY>() || is_iq1<TY>(); }
 
-template <int TY>
+template <int TY, int NT>
 struct SbTileLayout {
   static constexpr int BYTES = sb_block_bytes(TY);
   static constexpr int WORDS = (BYTES + 2 + 3) / 4;  // the aligned words that hold a block
   static constexpr int RAWP = 4 * WORDS;
-  static constexpr int X = 0;                                      // int8 [SBT_T][SBT_PITCH]
-  static constexpr int XS = X + SBT_T * SBT_PITCH;                 // float [8][SBT_T]
-  static constexpr int S16 = XS + 8 * SBT_T * 4;                   // int32 [16][SBT_T]
-  static constexpr int S8 = S16 + 16 * SBT_T * 4;                  // int32 [32][SBT_T] (IQ1_M)
-  static constexpr int RAW = S8 + (TY == IQ1_M ? 32 * SBT_T * 4 : 0);  // bytes [SBT_R][RAWP]
-  static constexpr int WM = RAW + SBT_R * RAWP;                    // int8 [SBT_R][SBT_PITCH]
-  static constexpr int WN = WM + SBT_R * SBT_PITCH;                // int8 [SBT_R][SBT_PITCH] (signed grids)
+  static constexpr int X = 0;                                              // int8 [NT][SBT_PITCH]
+  static constexpr int XS = X + NT * SBT_PITCH;                            // float [8][NT]
+  static constexpr int S16 = XS + 8 * NT * 4;                              // int32 [16][NT] (K, IQ1)
+  static constexpr int S8 = S16 + (tile_sums16<TY>() ? 16 * NT * 4 : 0);   // int32 [32][NT] (IQ1_M)
+  static constexpr int RAW = S8 + (TY == IQ1_M ? 32 * NT * 4 : 0);         // bytes [SBT_R][RAWP]
+  static constexpr int WM = RAW + SBT_R * RAWP;                            // int8 [SBT_R][SBT_PITCH]
+  static constexpr int WN = WM + SBT_R * SBT_PITCH;                        // int8 [SBT_R][SBT_PITCH] (signed grids)
   static constexpr int RS = WN + (tile_signed<TY>() ? SBT_R * SBT_PITCH : 0);  // int8 [SBT_R][16] S
-  static constexpr int RM = RS + SBT_R * 16;                       // int8 [SBT_R][16] M
-  static constexpr int RD = RM + SBT_R * 16;                       // uint8 [SBT_R][16] IQ1's shifts
-  static constexpr int FF = RD + SBT_R * 16;                       // float [SBT_R] F, then [SBT_R] Fm
-  static constexpr int GRIDS = FF + 2 * SBT_R * 4;                 // the type's grid and sign table
+  static constexpr int RM = RS + SBT_R * 16;                               // int8 [SBT_R][16] M
+  static constexpr int RD = RM + SBT_R * 16;                               // uint8 [SBT_R][16] IQ1's shifts
+  static constexpr int FF = RD + SBT_R * 16;                               // float [SBT_R] F, then [SBT_R] Fm
+  static constexpr int GRIDS = FF + 2 * SBT_R * 4;                         // the type's grid and sign table
   static constexpr int SIZE = GRIDS + lds_table_bytes<TY>();
+  // the lanes' sums at the end, over X .. : NT = 64, l0 + l1 [SBT_R][NT]; NT = 32, l0, l1, l2 [3][SBT_R][NT]
+  static constexpr int LANES = (NT == 64 ? 1 : 3) * SBT_R * NT * 4;
+  static_assert(LANES <= GRIDS, "the lanes' sums fit below the grids");
+  // the loads of a block a thread: the tokens' bytes (16 a load), their scales and sums (16 bytes a load), the raw
+  // blocks' words
+  static constexpr int XU = NT * 16 / 256;
+  static constexpr int AUX = NT * (2 + (tile_sums16<TY>() ? 2 : 0) + (TY == IQ1_M ? 4 : 0));
+  static constexpr int AU = (AUX + 255) / 256;
+  static constexpr int RU = (SBT_R * WORDS + 255) / 256;
 };
 
 HQ_DEV int32_t sbyte(uint32_t w, int i) { return (int32_t)(int8_t)(uint8_t)(w >> (8 * i)); }
 
-template <int TY>
-__global__ __launch_bounds__(256) void gemm_sb(Job J) {
-  using Lay = SbTileLayout<TY>;
-  constexpr int BYTES = Lay::BYTES, WORDS = Lay::WORDS, GRID = grid_bytes<TY>();
-  extern __shared__ __align__(16) char lds[];
+// a block's loads in flight: block b's bytes of the tile's tokens and rows, in registers
+template <int TY, int NT>
+struct TileLoads {
+  using Lay = SbTileLayout<TY, NT>;
+  v4i_t x[Lay::XU], aux[Lay::AU];
+  uint32_t raw[Lay::RU];
+};
+
+template <int TY, int NT>
+HQ_DEV void tile_load(TileLoads<TY, NT> &L, int tid, int b, __amdgpu_buffer_rsrc_t rq, __amdgpu_buffer_rsrc_t ra,
+                      __amdgpu_buffer_rsrc_t rw, int64_t frame, int64_t sframe, int n, int blocks, int r0, int r1,
+                      uint32_t wdelta) {
+  using Lay = SbTileLayout<TY, NT>;
+  constexpr int BYTES = Lay::BYTES, WORDS = Lay::WORDS;
+#pragma unroll
+  for (int u = 0; u < Lay::XU; u++) {
+    const int idx = tid + 256 * u, tok = idx >> 4, q = idx & 15;
+    L.x[u] = __builtin_amdgcn_raw_buffer_load_b128(rq, (int)(tok * frame + 256 * b + 16 * q), 0, 0);
+  }
+#pragma unroll
+  for (int u = 0; u < Lay::AU; u++) {
+    // a < 2 NT: the scales (token a / 2, half a % 2); < 4 NT: the sums of 16; then IQ1_M's sums of 8 (a quarter)
+    const int a0 = tid + 256 * u, a = a0 < Lay::AUX ? a0 : Lay::AUX - 1;
+    int off;
+    if (a < 2 * NT) off = (a >> 1) * (int)sframe + 32 * b + 16 * (a & 1);
+    else if (a < 4 * NT && tile_sums16<TY>()) off = ((a - 2 * NT) >> 1) * (int)sframe + 4 * (n >> 5) + 32 * b + 16 * (a & 1);
+    else off = ((a - 4 * NT) >> 2) * (int)sframe + 4 * (n >> 5) + 2 * (n >> 4) + 64 * b + 16 * (a & 3);
+    L.aux[u] = __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0);
+  }
+#pragma unroll
+  for (int u = 0; u < Lay::RU; u++) {
+    const int i0 = tid + 256 * u, idx = i0 < SBT_R * WORDS ? i0 : SBT_R * WORDS - 1;
+    const int r = idx / WORDS, w = idx - r * WORDS;
+    const int row = r0 + r < r1 ? r0 + r : r1 - 1;
+    const uint32_t start = wdelta + (uint32_t)(((int64_t)row * blocks + b) * BYTES);
+    L.raw[u] = __builtin_amdgcn_raw_buffer_load_b32(rw, (int)((start & ~3u) + 4u * w), 0, 0);
+  }
+}
+
+template <int TY, int NT>
+HQ_DEV void tile_store(const TileLoads<TY, NT> &L, int tid, char *lds) {
+  using Lay = SbTileLayout<TY, NT>;
+  constexpr int WORDS = Lay::WORDS;
   int8_t *x = (int8_t *)(lds + Lay::X);
   float *xsT = (float *)(lds + Lay::XS);
   int32_t *s16T = (int32_t *)(lds + Lay::S16), *s8T = (int32_t *)(lds + Lay::S8);
+#pragma unroll
+  for (int u = 0; u < Lay::XU; u++) {
+    const int idx = tid + 256 * u, tok = idx >> 4, q = idx & 15;
+    *(v4i_t *)(x + tok * SBT_PITCH + 16 * q) = L.x[u];
+  }
+#pragma unroll
+  for (int u = 0; u < Lay::AU; u++) {
+    const int a = tid + 256 * u;  // (the kinds change at multiples of 64: a wave takes one)
+    const v4i_t v = L.aux[u];
+    if (a < 2 * NT) {
+      const int tok = a >> 1, half = a & 1;
+#pragma unroll
+      for (int i = 0; i < 4; i++) xsT[(4 * half + i) * NT + tok] = __int_as_float(v[i]);
+    } else if (a < 4 * NT && tile_sums16<TY>()) {
+      const int tok = (a - 2 * NT) >> 1, half = a & 1;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        s16T[(8 * half + 2 * i) * NT + tok] = (int32_t)(int16_t)(v[i] & 0xffff);
+        s16T[(8 * half + 2 * i + 1) * NT + tok] = (int32_t)(int16_t)((uint32_t)v[i] >> 16);
+      }
+    } else if (a < Lay::AUX) {
+      const int tok = (a - 4 * NT) >> 2, qq = a & 3;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        s8T[(8 * qq + 2 * i) * NT + tok] = (int32_t)(int16_t)(v[i] & 0xffff);
+        s8T[(8 * qq + 2 * i + 1) * NT + tok] = (int32_t)(int16_t)((uint32_t)v[i] >> 16);
+      }
+    }
+  }
   uint8_t *raw = (uint8_t *)(lds + Lay::RAW);
+#pragma unroll
+  for (int u = 0; u < Lay::RU; u++) {
+    const int idx = tid + 256 * u;
+    if (idx < SBT_R * WORDS) {
+      const int r = idx / WORDS, w = idx - r * WORDS;
+      *(uint32_t *)(raw + r * Lay::RAWP + 4 * w) = L.raw[u];
+    }
+  }
+}
+
+template <int TY, int NT>
+__global__ __launch_bounds__(256) void gemm_sb(Job J) {
+  using Lay = SbTileLayout<TY, NT>;
+  constexpr int BYTES = Lay::BYTES, GRID = grid_bytes<TY>();
+  constexpr int TH = NT / 32;  // token halves; also the lanes k a wave
+  extern __shared__ __align__(16) char lds[];
+  const int8_t *x = (const int8_t *)(lds + Lay::X);
+  const float *xsT = (const float *)(lds + Lay::XS);
+  const int32_t *s16T = (const int32_t *)(lds + Lay::S16), *s8T = (const int32_t *)(lds + Lay::S8);
+  const uint8_t *raw = (const uint8_t *)(lds + Lay::RAW);
   int8_t *wm = (int8_t *)(lds + Lay::WM), *wn = (int8_t *)(lds + Lay::WN);
   int8_t *rs = (int8_t *)(lds + Lay::RS), *rm = (int8_t *)(lds + Lay::RM);
   uint8_t *rd = (uint8_t *)(lds + Lay::RD);
@@ -511,9 +614,8 @@ __global__ __launch_bounds__(256) void gemm_sb(Job J) {
   const int tid = threadIdx.x;
   const int nrt = (J.r1 - J.r0 + SBT_R - 1) / SBT_R;
   const int rt = blockIdx.x % nrt, tt = blockIdx.x / nrt;
-  const int r0 = J.r0 + SBT_R * rt, t0 = SBT_T * tt;
+  const int r0 = J.r0 + SBT_R * rt, t0 = NT * tt;
   const int blocks = J.n >> 8;
-  const int64_t frame = J.frame;
   // the type's grid and sign table, and IQ4_XS's values
   const uint8_t *tab = (const uint8_t *)J.ws;
   for (int i = tid; i < GRID / 16; i += 256) ((uint4 *)table)[i] = ((const uint4 *)(tab + grid_at<TY>()))[i];
@@ -527,74 +629,41 @@ __global__ __launch_bounds__(256) void gemm_sb(Job J) {
   // buffers: the tile's tokens (a token past the prompt reads zeros) and the weights (the aligned words of rows
   // 0 .. r1 - 1)
   const int64_t tokens_left = (int64_t)J.count - t0;
-  const __amdgpu_buffer_rsrc_t rq = resource(J.xq + t0 * frame, tokens_left * frame);
-  const int64_t sframe = J.sframe;
-  const __amdgpu_buffer_rsrc_t ra = resource(J.xs + t0 * sframe, tokens_left * sframe);
+  const __amdgpu_buffer_rsrc_t rq = resource(J.xq + t0 * J.frame, tokens_left * J.frame);
+  const __amdgpu_buffer_rsrc_t ra = resource(J.xs + t0 * J.sframe, tokens_left * J.sframe);
   const uintptr_t wat = (uintptr_t)J.wq;
   const uint32_t wdelta = (uint32_t)(wat & 3u);
   const int64_t wend = wdelta + (int64_t)J.r1 * blocks * BYTES;
   const __amdgpu_buffer_rsrc_t rw = resource((const char *)(wat - wdelta), (wend + 3) & ~(int64_t)3);
-  // this thread's row for the decode: tile row tid / 4 (past the job's rows: its last), chunks 4 (tid % 4) ..
-  const int dr = tid >> 2, dq = tid & 3;
+  // this thread's row for the decode: tile row tid / 8 (past the job's rows: its last), chunks 2 (tid % 8), + 1
+  const int dr = tid >> 3, dq = tid & 7;
   const int drow = r0 + dr < J.r1 ? r0 + dr : J.r1 - 1;
-  // the wave's 32 x 32: tokens 32 th .., rows 32 rh ..; the lane's row, and its 16 tokens' first of each four
-  const int wave = tid >> 6, lane = tid & 63, kh = lane >> 5, l32 = lane & 31;
-  const int th = wave & 1, rh = wave >> 1;
-  const int mrow = 32 * rh + l32, mtok = 32 * th + l32;
-  float acc[4][16];
+  // the wave's tokens 32 th .. and lanes k0 .. k0 + TH - 1; the lane's row, and its 16 tokens' first of each four
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, kh = lane >> 5, l32 = lane & 31;
+  const int th = wave % TH, k0 = (wave / TH) * TH;
+  const int mrow = l32, mtok = 32 * th + l32;
+  float acc[TH][16];
 #pragma unroll
-  for (int k = 0; k < 4; k++)
+  for (int kk = 0; kk < TH; kk++)
 #pragma unroll
-    for (int r = 0; r < 16; r++) acc[k][r] = 0.0f;
+    for (int r = 0; r < 16; r++) acc[kk][r] = 0.0f;
 
+  TileLoads<TY, NT> loads;
+  tile_load<TY, NT>(loads, tid, 0, rq, ra, rw, J.frame, J.sframe, J.n, blocks, r0, J.r1, wdelta);
   for (int b = 0; b < blocks; b++) {
     __syncthreads();  // (the last block's tiles read)
-    // ---- staging: the tokens' 256 bytes of the block, their 8 scales and their sums; the rows' raw blocks
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-      const int idx = tid + 256 * u, tok = idx >> 4, q = idx & 15;
-      const v4i_t v = __builtin_amdgcn_raw_buffer_load_b128(rq, (int)(tok * frame + 256 * b + 16 * q), 0, 0);
-      *(v4i_t *)(x + tok * SBT_PITCH + 16 * q) = v;
-    }
-    if (tid < 128) {
-      const int tok = tid >> 1, half = tid & 1;
-      const v4i_t v = __builtin_amdgcn_raw_buffer_load_b128(ra, (int)(tok * sframe + 32 * b + 16 * half), 0, 0);
-#pragma unroll
-      for (int i = 0; i < 4; i++) xsT[(4 * half + i) * SBT_T + tok] = __int_as_float(v[i]);
-    } else if (has_minimums<TY>() || is_iq1<TY>()) {
-      const int tok = (tid - 128) >> 1, half = tid & 1;
-      const v4i_t v = __builtin_amdgcn_raw_buffer_load_b128(ra, (int)(tok * sframe + 4 * (J.n >> 5) + 32 * b + 16 * half), 0, 0);
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        s16T[(8 * half + 2 * i) * SBT_T + tok] = (int32_t)(int16_t)(v[i] & 0xffff);
-        s16T[(8 * half + 2 * i + 1) * SBT_T + tok] = (int32_t)(int16_t)((uint32_t)v[i] >> 16);
-      }
-    }
-    if (TY == IQ1_M) {
-      const int tok = tid >> 2, qq = tid & 3;
-      const v4i_t v = __builtin_amdgcn_raw_buffer_load_b128(
-          ra, (int)(tok * sframe + 4 * (J.n >> 5) + 2 * (J.n >> 4) + 64 * b + 16 * qq), 0, 0);
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        s8T[(8 * qq + 2 * i) * SBT_T + tok] = (int32_t)(int16_t)(v[i] & 0xffff);
-        s8T[(8 * qq + 2 * i + 1) * SBT_T + tok] = (int32_t)(int16_t)((uint32_t)v[i] >> 16);
-      }
-    }
-    for (int idx = tid; idx < SBT_R * WORDS; idx += 256) {
-      const int r = idx / WORDS, w = idx - r * WORDS;
-      const int row = r0 + r < J.r1 ? r0 + r : J.r1 - 1;
-      const uint32_t start = wdelta + (uint32_t)(((int64_t)row * blocks + b) * BYTES);
-      *(uint32_t *)(raw + r * Lay::RAWP + 4 * w) =
-          __builtin_amdgcn_raw_buffer_load_b32(rw, (int)((start & ~3u) + 4u * w), 0, 0);
-    }
+    tile_store<TY, NT>(loads, tid, lds);
+    // the next block's loads (the last block's again at the end: not used)
+    tile_load<TY, NT>(loads, tid, b + 1 < blocks ? b + 1 : b, rq, ra, rw, J.frame, J.sframe, J.n, blocks, r0, J.r1,
+                      wdelta);
     __syncthreads();
-    // ---- decode: this thread's four chunks of its row's block into the tiles
+    // ---- decode: this thread's two chunks of its row's block into the tiles
     {
       const uint32_t start = wdelta + (uint32_t)(((int64_t)drow * blocks + b) * BYTES);
       const LdsBytes B{raw + dr * Lay::RAWP + (start & 2u)};
 #pragma unroll
-      for (int u = 0; u < 4; u++) {
-        const int h = 4 * dq + u;
+      for (int u = 0; u < 2; u++) {
+        const int h = 2 * dq + u;
         Chunk c;
         chunk<TY>(B, h, table, table + GRID, iq4, c);
         uint32_t m4[4];
@@ -614,14 +683,15 @@ __global__ __launch_bounds__(256) void gemm_sb(Job J) {
       }
     }
     __syncthreads();
-    // ---- the products: the wave's 32 x 32, group pairs (k, k + 4)
+    // ---- the products: the wave's 32 x 32 for its lanes k, group pairs (k, k + 4)
     const float F = ff[mrow], Fm = ff[SBT_R + mrow];
     const uint4 S4 = *(const uint4 *)(rs + mrow * 16), M4 = *(const uint4 *)(rm + mrow * 16),
                 D4 = *(const uint4 *)(rd + mrow * 16);
     const uint32_t Sw[4] = {S4.x, S4.y, S4.z, S4.w}, Mw[4] = {M4.x, M4.y, M4.z, M4.w}, Dw[4] = {D4.x, D4.y, D4.z, D4.w};
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-      int32_t G[2][16], Mi[2][16];
+    for (int kk = 0; kk < TH; kk++) {
+      const int k = k0 + kk;
+      float q0[16], qm0[16];  // group k's f(G xs) and f(M xs)
 #pragma unroll
       for (int e = 0; e < 2; e++) {
         const int gg = k + 4 * e, c0 = 2 * gg, c1 = 2 * gg + 1;
@@ -629,6 +699,7 @@ __global__ __launch_bounds__(256) void gemm_sb(Job J) {
         const v4i_t Bm = *(const v4i_t *)(wm + mrow * SBT_PITCH + 32 * gg + 16 * kh);
         const v16i_t zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
         const int32_t S0 = sbyte(Sw[c0 >> 2], c0 & 3), S1 = sbyte(Sw[c1 >> 2], c1 & 3);
+        int32_t G[16], Mi[16];
         if (tile_split<TY>()) {
           const v4i_t z4 = {0, 0, 0, 0};
           v16i_t lo = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, kh == 0 ? Bm : z4, zero, 0, 0, 0);
@@ -650,8 +721,8 @@ __global__ __launch_bounds__(256) void gemm_sb(Job J) {
 #pragma unroll
             for (int m = 0; m < 4; m++) {
               const int tk = 32 * th + 8 * m + 4 * kh;
-              const int4 e00 = *(const int4 *)(s8T + (2 * c0) * SBT_T + tk), e01 = *(const int4 *)(s8T + (2 * c0 + 1) * SBT_T + tk);
-              const int4 e10 = *(const int4 *)(s8T + (2 * c1) * SBT_T + tk), e11 = *(const int4 *)(s8T + (2 * c1 + 1) * SBT_T + tk);
+              const int4 e00 = *(const int4 *)(s8T + (2 * c0) * NT + tk), e01 = *(const int4 *)(s8T + (2 * c0 + 1) * NT + tk);
+              const int4 e10 = *(const int4 *)(s8T + (2 * c1) * NT + tk), e11 = *(const int4 *)(s8T + (2 * c1 + 1) * NT + tk);
               const int32_t v00[4] = {e00.x, e00.y, e00.z, e00.w}, v01[4] = {e01.x, e01.y, e01.z, e01.w};
               const int32_t v10[4] = {e10.x, e10.y, e10.z, e10.w}, v11[4] = {e11.x, e11.y, e11.z, e11.w};
 #pragma unroll
@@ -662,7 +733,7 @@ __global__ __launch_bounds__(256) void gemm_sb(Job J) {
             }
           }
 #pragma unroll
-          for (int r = 0; r < 16; r++) G[e][r] = S0 * lo[r] + S1 * hi[r];
+          for (int r = 0; r < 16; r++) G[r] = S0 * lo[r] + S1 * hi[r];
         } else {
           v16i_t C = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, Bm, zero, 0, 0, 0);
           if (tile_signed<TY>()) {
@@ -676,68 +747,117 @@ __global__ __launch_bounds__(256) void gemm_sb(Job J) {
 #pragma unroll
             for (int m = 0; m < 4; m++) {
               const int tk = 32 * th + 8 * m + 4 * kh;
-              const int4 e0 = *(const int4 *)(s16T + c0 * SBT_T + tk), e1 = *(const int4 *)(s16T + c1 * SBT_T + tk);
+              const int4 e0 = *(const int4 *)(s16T + c0 * NT + tk), e1 = *(const int4 *)(s16T + c1 * NT + tk);
               const int32_t v0[4] = {e0.x, e0.y, e0.z, e0.w}, v1[4] = {e1.x, e1.y, e1.z, e1.w};
 #pragma unroll
               for (int i = 0; i < 4; i++) C[4 * m + i] = 8 * C[4 * m + i] - a * (v0[i] + v1[i]);
             }
           }
 #pragma unroll
-          for (int r = 0; r < 16; r++) G[e][r] = TY == Q2_K ? C[r] : S0 * C[r];
+          for (int r = 0; r < 16; r++) G[r] = TY == Q2_K ? C[r] : S0 * C[r];
         }
         if (has_minimums<TY>()) {
           const int32_t M0 = sbyte(Mw[c0 >> 2], c0 & 3), M1 = sbyte(Mw[c1 >> 2], c1 & 3);
 #pragma unroll
           for (int m = 0; m < 4; m++) {
             const int tk = 32 * th + 8 * m + 4 * kh;
-            const int4 e0 = *(const int4 *)(s16T + c0 * SBT_T + tk), e1 = *(const int4 *)(s16T + c1 * SBT_T + tk);
+            const int4 e0 = *(const int4 *)(s16T + c0 * NT + tk), e1 = *(const int4 *)(s16T + c1 * NT + tk);
             const int32_t v0[4] = {e0.x, e0.y, e0.z, e0.w}, v1[4] = {e1.x, e1.y, e1.z, e1.w};
 #pragma unroll
-            for (int i = 0; i < 4; i++) Mi[e][4 * m + i] = M0 * v0[i] + M1 * v1[i];
+            for (int i = 0; i < 4; i++) Mi[4 * m + i] = M0 * v0[i] + M1 * v1[i];
           }
         }
-      }
+        // group gg's scales: f(G xs) (and f(M xs)); the second group of the pair completes the part
 #pragma unroll
-      for (int m = 0; m < 4; m++) {
-        const int tk = 32 * th + 8 * m + 4 * kh;
-        const float4 l4 = *(const float4 *)(xsT + k * SBT_T + tk), h4 = *(const float4 *)(xsT + (k + 4) * SBT_T + tk);
-        const float sl[4] = {l4.x, l4.y, l4.z, l4.w}, sh[4] = {h4.x, h4.y, h4.z, h4.w};
+        for (int m = 0; m < 4; m++) {
+          const int tk = 32 * th + 8 * m + 4 * kh;
+          const float4 s4 = *(const float4 *)(xsT + gg * NT + tk);
+          const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const int r = 4 * m + i;
-          float part = fmul(fadd(fmul((float)G[0][r], sl[i]), fmul((float)G[1][r], sh[i])), F);
-          if (has_minimums<TY>())
-            part = fsub(part, fmul(fadd(fmul((float)Mi[0][r], sl[i]), fmul((float)Mi[1][r], sh[i])), Fm));
-          acc[k][r] = fadd(acc[k][r], part);
+          for (int i = 0; i < 4; i++) {
+            const int r = 4 * m + i;
+            if (e == 0) {
+              q0[r] = fmul((float)G[r], sv[i]);
+              if (has_minimums<TY>()) qm0[r] = fmul((float)Mi[r], sv[i]);
+            } else {
+              float part = fmul(fadd(q0[r], fmul((float)G[r], sv[i])), F);
+              if (has_minimums<TY>()) part = fsub(part, fmul(fadd(qm0[r], fmul((float)Mi[r], sv[i])), Fm));
+              acc[kk][r] = fadd(acc[kk][r], part);
+            }
+          }
         }
       }
     }
   }
-  // ((l0 + l1) + l2) + l3 (math.ts:7-9): the lane's row, its 16 tokens
+  // ((l0 + l1) + l2) + l3 (math.ts:7-9) through LDS (the tiles are free): the lane's row, its 16 tokens
+  __syncthreads();
+  float *lanes = (float *)(lds + Lay::X);
   const int row = r0 + mrow;
-  if (row < J.r1) {
+  if (NT == 64) {  // waves 0, 1 (lanes 0, 1) leave l0 + l1; waves 2, 3 add l2, then l3
+    if (k0 == 0) {
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int t = t0 + 32 * th + 8 * (r >> 2) + 4 * kh + (r & 3);
-      if (t < J.count) ((float *)(J.out + t * J.os))[row] = fadd(fadd(fadd(acc[0][r], acc[1][r]), acc[2][r]), acc[3][r]);
+      for (int r = 0; r < 16; r++) {
+        const int t = 32 * th + 8 * (r >> 2) + 4 * kh + (r & 3);
+        lanes[t * SBT_R + mrow] = fadd(acc[0][r], acc[TH - 1][r]);
+      }
+    }
+    __syncthreads();
+    if (k0 != 0 && row < J.r1) {
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int t = 32 * th + 8 * (r >> 2) + 4 * kh + (r & 3);
+        if (t0 + t < J.count)
+          ((float *)(J.out + (t0 + t) * J.os))[row] = fadd(fadd(lanes[t * SBT_R + mrow], acc[0][r]), acc[TH - 1][r]);
+      }
+    }
+  } else {  // a lane a wave: waves 0..2 leave l0, l1, l2; wave 3 adds them in order, then l3
+    if (k0 < 3) {
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int t = 8 * (r >> 2) + 4 * kh + (r & 3);
+        lanes[(k0 * NT + t) * SBT_R + mrow] = acc[0][r];
+      }
+    }
+    __syncthreads();
+    if (k0 == 3 && row < J.r1) {
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int t = 8 * (r >> 2) + 4 * kh + (r & 3);
+        if (t0 + t < J.count) {
+          const float l0 = lanes[t * SBT_R + mrow], l1 = lanes[(NT + t) * SBT_R + mrow],
+                      l2 = lanes[(2 * NT + t) * SBT_R + mrow];
+          ((float *)(J.out + (t0 + t) * J.os))[row] = fadd(fadd(fadd(l0, l1), l2), acc[0][r]);
+        }
+      }
     }
   }
 }
 
-template <int TY>
-hipError_t launch_tile_type(const Job &j, hipStream_t s) {
+template <int TY, int NT>
+hipError_t launch_tile_nt(const Job &j, int nrt, hipStream_t s) {
   static bool sized[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
   if (!sized[dev]) {  // (more than 64 KB of LDS a block)
-    const hipError_t e = hipFuncSetAttribute((const void *)gemm_sb<TY>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                             SbTileLayout<TY>::SIZE);
+    const hipError_t e = hipFuncSetAttribute((const void *)gemm_sb<TY, NT>,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, SbTileLayout<TY, NT>::SIZE);
     if (e != hipSuccess) return e;
     sized[dev] = true;
   }
-  const int nrt = (j.r1 - j.r0 + SBT_R - 1) / SBT_R, ntt = (j.count + SBT_T - 1) / SBT_T;
-  hipLaunchKernelGGL(gemm_sb<TY>, dim3(nrt * ntt), dim3(256), SbTileLayout<TY>::SIZE, s, j);
+  const int ntt = (j.count + NT - 1) / NT;
+  constexpr int lds = SbTileLayout<TY, NT>::SIZE;
+  hipLaunchKernelGGL((gemm_sb<TY, NT>), dim3(nrt * ntt), dim3(256), lds, s, j);
   return hipGetLastError();
+}
+
+// 64 tokens a block when that makes at least two blocks a compute unit, else 32 (twice the decoding, twice the
+// blocks)
+template <int TY>
+hipError_t launch_tile_type(const Job &j, hipStream_t s) {
+  const int nrt = (j.r1 - j.r0 + SBT_R - 1) / SBT_R;
+  const bool wide = HQ_SB_TILE_NT == 64 ||
+                    (HQ_SB_TILE_NT == 0 && (int64_t)nrt * ((j.count + 63) / 64) >= 2 * (int64_t)cu_count());
+  return wide ? launch_tile_nt<TY, 64>(j, nrt, s) : launch_tile_nt<TY, 32>(j, nrt, s);
 }
 
 // ---------------------------------------------------------------------------------------------------------------

@@ -157,6 +157,37 @@ def test_matmul_sbr_tile(k, arena, oracle, setup, name, t):
                         f"{form} {name} count {count} rows {r0}..{r1} token {tk}: {first_difference(got[tk], want)}"
 
 
+@pytest.mark.parametrize("name,t", TYPES)
+def test_matmul_sbr_tile_rows(k, arena, oracle, setup, name, t):
+    """the matrix-core tile over several tiles of rows and two of tokens, row ranges that start and end inside a
+    tile, the weights 2 bytes into a word"""
+    row, tab = setup
+    area = put_tables(k, arena, row)
+    rng = np.random.default_rng(500 + t)
+    rows, nb, tokens = 150, 3, 80
+    n = 256 * nb
+    wbytes = bm.random_blocks(rng, t, rows * nb).reshape(-1)
+    w = arena.put(np.concatenate([np.zeros(2, np.uint8), wbytes])) + 2
+    frame = ((n + n // 2 + 15) // 16) * 16
+    buf = np.zeros(tokens * frame, np.uint8)
+    fulls = []
+    for tk in range(tokens):
+        q, act = token_area(oracle, rng, n, scale=1.0 + tk % 7)
+        buf[tk * frame:tk * frame + n] = q.view(np.uint8)
+        buf[tk * frame + n:tk * frame + n + act.size] = act
+        fulls.append(oracle.matmul_sbr(q, act, wbytes, tab, n, t))
+    xq = arena.put(buf)
+    os_ = 4 * (rows + 1)
+    for r0, r1 in [(0, rows), (5, rows), (64, 129)]:
+        out = arena.alloc(os_ * tokens, fill=np.full(os_ * tokens // 4, -7, F))
+        k.matmul_sbr_tile(out, xq, xq + n, w, area, n, r0, r1, tokens, os_, frame, t)
+        got = arena.get(out, F, os_ * tokens // 4).reshape(tokens, -1)
+        for tk in range(tokens):
+            want = np.full(os_ // 4, F(-7), F)
+            want[r0:r1] = fulls[tk][r0:r1]
+            assert same_bits(got[tk], want), f"{name} rows {r0}..{r1} token {tk}: {first_difference(got[tk], want)}"
+
+
 def test_phase_and_matmuls_of_blocks(pkg, k, arena, oracle, setup):
     """jobs of kinds 10, 11, 12 of several types in one hq_phase, and hq_matmuls (quantize_x at bias 0 and sums_x,
     then the phase) for three tokens"""
