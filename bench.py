@@ -441,7 +441,7 @@ BLOCK_SCALES = {10: (80, 82), 12: (0, 2), 16: (0,), 17: (0,), 18: (0,), 19: (0,)
 def measure_blocks(torch, pkg, args, gen):
     """llama.cpp's blocks (job kinds 10-12) at Llama-3-8B's MLP shapes: the token product (M = 1; copies of the
     weights past the Infinity Cache) in GB/s of algorithmic bytes (the blocks, the activations and the sums of 16
-    or 8 the type reads, the outputs) and a prompt of 64 tokens in TOPS.  Random blocks (random bytes, sane
+    or 8 the type reads, the outputs) and prompts of 64 and 512 tokens in TOPS.  Random blocks (random bytes, sane
     scales), random codebooks."""
     from pyodide_llm_amd import jobs
     lib = pkg.library()
@@ -502,23 +502,24 @@ def measure_blocks(torch, pkg, args, gen):
         out[f"8B MLP {name} M=1 x {copies}"] = {"GBps": round(total / sec / 1e9, 1),
                                                   "us_per_layer": round(1e6 * sec / copies, 2), "bytes": total}
         del keep, tables
-        # a prompt of 64 tokens through one layer's MLP (the tile: 4 tokens a launch)
-        count = 64
-        entries, keep = [], []
-        for rows, n in shapes:
-            w = weights(t, size, rows, n)
-            buf, frame = acts(n, count)
-            o = torch.empty(count, rows, device=dev)
-            keep += [w, buf, o]
-            entries.append(jobs.job("matmul_sbr", o.data_ptr(), buf.data_ptr(), buf.data_ptr() + n, w.data_ptr(),
-                                    tab.data_ptr(), t, n, rows=rows, count=count, os=4 * rows, as_=frame, bs=frame))
-        tb = jobs.table(entries)
-        ops = sum(2.0 * count * rows * n for rows, n in shapes)
-        sec = _graph_time(torch, lambda h: lib.hq_phase(tb, len(entries), 16, h), reps)
-        pkg.check(lib.hq_last_error())
-        out[f"8B MLP {name} prompt M={count}"] = {"TOPS": round(ops / sec / 1e12, 2), "ms": round(1e3 * sec, 3)}
-        del keep
-        torch.cuda.empty_cache()
+        # prompts of 64 and 512 tokens through one layer's MLP (the matrix-core tile)
+        for count in getattr(args, "block_prompts", (64, 512)):
+            entries, keep = [], []
+            for rows, n in shapes:
+                w = weights(t, size, rows, n)
+                buf, frame = acts(n, count)
+                o = torch.empty(count, rows, device=dev)
+                keep += [w, buf, o]
+                entries.append(jobs.job("matmul_sbr", o.data_ptr(), buf.data_ptr(), buf.data_ptr() + n,
+                                        w.data_ptr(), tab.data_ptr(), t, n, rows=rows, count=count, os=4 * rows,
+                                        as_=frame, bs=frame))
+            tb = jobs.table(entries)
+            ops = sum(2.0 * count * rows * n for rows, n in shapes)
+            sec = _graph_time(torch, lambda h: lib.hq_phase(tb, len(entries), 16, h), reps)
+            pkg.check(lib.hq_last_error())
+            out[f"8B MLP {name} prompt M={count}"] = {"TOPS": round(ops / sec / 1e12, 2), "ms": round(1e3 * sec, 3)}
+            del keep
+            torch.cuda.empty_cache()
     return out
 
 

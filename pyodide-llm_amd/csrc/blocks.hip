@@ -455,7 +455,8 @@ hipError_t launch_type(const SbBatch &b, int T, int L, size_t lds, hipStream_t s
 // decoder reading the LDS copy) into int8 tiles, and multiplies them on the matrix cores:
 // v_mfma_i32_32x32x32_i8, A = 32 tokens, B = the 32 rows, K = 32 = a group, so a lane holds one row (l % 32) and 16
 // tokens (8 (r / 4) + 4 (l / 32) + r % 4).  The integers are exactly the token kernel's:
-//   signed grids: |W| and |W| of the negative weights in two tiles, d = C(|W|) - 2 C(|W| neg);
+//   signed grids: W ^ neg (W where the sign is plus, ~W = -W - 1 where it is minus: always an int8) and neg's 0 / 1
+//   in two tiles, d = C(W ^ neg) + C(neg & 1), the second product added in the first's accumulator;
 //   a scale S for each 16 (IQ2_XS, IQ2_S, IQ1_M): two products a group, B zero in one half of the lanes (K 0..15
 //   is lanes 0..31's, K 16..31 lanes 32..63's), G = S_lo d_lo + S_hi d_hi; Q2_K's S W (at most 45) is its tile;
 //   IQ1: C of the codes, d = 8 C - (7 + 2 down) (sum of each 8); the K types' M against the sums of 16;
@@ -669,10 +670,14 @@ __global__ __launch_bounds__(256) void gemm_sb(Job J) {
         uint32_t m4[4];
 #pragma unroll
         for (int j = 0; j < 4; j++) m4[j] = TY == Q2_K ? c.mag[j] * (uint32_t)c.S : c.mag[j];  // (S W <= 45)
-        *(uint4 *)(wm + dr * SBT_PITCH + 16 * h) = make_uint4(m4[0], m4[1], m4[2], m4[3]);
-        if (tile_signed<TY>())
-          *(uint4 *)(wn + dr * SBT_PITCH + 16 * h) =
-              make_uint4(c.mag[0] & c.neg[0], c.mag[1] & c.neg[1], c.mag[2] & c.neg[2], c.mag[3] & c.neg[3]);
+        if (tile_signed<TY>()) {
+          *(uint4 *)(wm + dr * SBT_PITCH + 16 * h) =
+              make_uint4(c.mag[0] ^ c.neg[0], c.mag[1] ^ c.neg[1], c.mag[2] ^ c.neg[2], c.mag[3] ^ c.neg[3]);
+          *(uint4 *)(wn + dr * SBT_PITCH + 16 * h) = make_uint4(c.neg[0] & 0x01010101u, c.neg[1] & 0x01010101u,
+                                                                c.neg[2] & 0x01010101u, c.neg[3] & 0x01010101u);
+        } else {
+          *(uint4 *)(wm + dr * SBT_PITCH + 16 * h) = make_uint4(m4[0], m4[1], m4[2], m4[3]);
+        }
         rs[dr * 16 + h] = (int8_t)c.S;
         rm[dr * 16 + h] = (int8_t)c.M;
         rd[dr * 16 + h] = (uint8_t)(c.down0 | (c.down1 << 1));
@@ -706,13 +711,8 @@ __global__ __launch_bounds__(256) void gemm_sb(Job J) {
           v16i_t hi = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, kh == 1 ? Bm : z4, zero, 0, 0, 0);
           if (tile_signed<TY>()) {
             const v4i_t Bn = *(const v4i_t *)(wn + mrow * SBT_PITCH + 32 * gg + 16 * kh);
-            const v16i_t nlo = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, kh == 0 ? Bn : z4, zero, 0, 0, 0);
-            const v16i_t nhi = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, kh == 1 ? Bn : z4, zero, 0, 0, 0);
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-              lo[r] -= 2 * nlo[r];
-              hi[r] -= 2 * nhi[r];
-            }
+            lo = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, kh == 0 ? Bn : z4, lo, 0, 0, 0);
+            hi = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, kh == 1 ? Bn : z4, hi, 0, 0, 0);
           }
           if (is_iq1<TY>()) {  // 8 dot(code, a) - (7 + 2 down) (sum of each 8), for each of the two 16s
             const uint32_t d0 = (Dw[c0 >> 2] >> (8 * (c0 & 3))) & 3u, d1 = (Dw[c1 >> 2] >> (8 * (c1 & 3))) & 3u;
@@ -727,20 +727,18 @@ __global__ __launch_bounds__(256) void gemm_sb(Job J) {
               const int32_t v10[4] = {e10.x, e10.y, e10.z, e10.w}, v11[4] = {e11.x, e11.y, e11.z, e11.w};
 #pragma unroll
               for (int i = 0; i < 4; i++) {
-                lo[4 * m + i] = 8 * lo[4 * m + i] - a0 * v00[i] - b0 * v01[i];
-                hi[4 * m + i] = 8 * hi[4 * m + i] - a1 * v10[i] - b1 * v11[i];
+                lo[4 * m + i] = 8 * lo[4 * m + i] - __mul24(a0, v00[i]) - __mul24(b0, v01[i]);
+                hi[4 * m + i] = 8 * hi[4 * m + i] - __mul24(a1, v10[i]) - __mul24(b1, v11[i]);
               }
             }
           }
 #pragma unroll
-          for (int r = 0; r < 16; r++) G[r] = S0 * lo[r] + S1 * hi[r];
+          for (int r = 0; r < 16; r++) G[r] = __mul24(S0, lo[r]) + __mul24(S1, hi[r]);  // (|lo|, |hi| < 2^23)
         } else {
           v16i_t C = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, Bm, zero, 0, 0, 0);
           if (tile_signed<TY>()) {
             const v4i_t Bn = *(const v4i_t *)(wn + mrow * SBT_PITCH + 32 * gg + 16 * kh);
-            const v16i_t Cn = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, Bn, zero, 0, 0, 0);
-#pragma unroll
-            for (int r = 0; r < 16; r++) C[r] -= 2 * Cn[r];
+            C = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, Bn, C, 0, 0, 0);
           }
           if (is_iq1<TY>()) {  // IQ1_S: one shift for the 32, against the sum of the 32
             const int32_t a = 7 + 2 * (int32_t)((Dw[c0 >> 2] >> (8 * (c0 & 3))) & 1u);
@@ -750,11 +748,11 @@ __global__ __launch_bounds__(256) void gemm_sb(Job J) {
               const int4 e0 = *(const int4 *)(s16T + c0 * NT + tk), e1 = *(const int4 *)(s16T + c1 * NT + tk);
               const int32_t v0[4] = {e0.x, e0.y, e0.z, e0.w}, v1[4] = {e1.x, e1.y, e1.z, e1.w};
 #pragma unroll
-              for (int i = 0; i < 4; i++) C[4 * m + i] = 8 * C[4 * m + i] - a * (v0[i] + v1[i]);
+              for (int i = 0; i < 4; i++) C[4 * m + i] = 8 * C[4 * m + i] - __mul24(a, v0[i] + v1[i]);
             }
           }
 #pragma unroll
-          for (int r = 0; r < 16; r++) G[r] = TY == Q2_K ? C[r] : S0 * C[r];
+          for (int r = 0; r < 16; r++) G[r] = TY == Q2_K ? C[r] : __mul24(S0, C[r]);
         }
         if (has_minimums<TY>()) {
           const int32_t M0 = sbyte(Mw[c0 >> 2], c0 & 3), M1 = sbyte(Mw[c1 >> 2], c1 & 3);
@@ -764,7 +762,7 @@ __global__ __launch_bounds__(256) void gemm_sb(Job J) {
             const int4 e0 = *(const int4 *)(s16T + c0 * NT + tk), e1 = *(const int4 *)(s16T + c1 * NT + tk);
             const int32_t v0[4] = {e0.x, e0.y, e0.z, e0.w}, v1[4] = {e1.x, e1.y, e1.z, e1.w};
 #pragma unroll
-            for (int i = 0; i < 4; i++) Mi[4 * m + i] = M0 * v0[i] + M1 * v1[i];
+            for (int i = 0; i < 4; i++) Mi[4 * m + i] = __mul24(M0, v0[i]) + __mul24(M1, v1[i]);
           }
         }
         // group gg's scales: f(G xs) (and f(M xs)); the second group of the pair completes the part
