@@ -16,7 +16,8 @@
 //   f(f(f(G[k] xs[k]) + f(G[k+4] xs[k+4])) F), less f(f(f(M[k] xs[k]) + f(M[k+4] xs[k+4])) Fm) for the K types,
 // and the four lanes are added in order at the end: a lane of a row here takes a block a step, and the parts go
 // through fold.hpp's LDS fold, lane k adding part k of the step's blocks in order, as the ternary kernels do.
-// A prompt's tokens go 4 at a time through the same kernel (every (row, token) the token kernel's number).
+// A prompt of fewer than kSbTileMin tokens goes 4 tokens at a time through the same kernel; a longer one through
+// the matrix-core tile below (gemm_sb): every (row, token) the token kernel's number either way.
 #include "common.hpp"
 #include "launch.hpp"
 #include "fold.hpp"
