@@ -22,9 +22,9 @@
 // v_mfma_f32_4x4x1_16b_f32 (sixteen 4 x 4 outer products each, K = 1) give a 32 x 32 sub-tile's, each product rounded
 // once as v_mul_f32 rounds it (subnormals included), on the matrix core.  Roofline: per output element and group the
 // epilogue is then 3 VALU operations (convert, multiply, add; ternary 4: f(f(C * xs) * d) has no such product)
-// against 32 MACs on the matrix core; MI355X's VALU does 128 float32 lanes a clock a CU against 4096 int8 MACs, so
-// the epilogue, not the MFMA, bounds this kernel: at best 32 / (3 x 4096 / 128) = 33 % of dense int8 peak (25 % for
-// ternary).
+// against 32 MACs on the matrix core.  Without packed float32 instructions (this build turns them off) MI355X's VALU
+// does 64 float32 lanes a clock a CU (4 SIMDs x 16) against 4096 int8 MACs, so the epilogue, not the MFMA, bounds
+// this kernel: at best 32 / (3 x 4096 / 64) = 16.7 % of dense int8 peak, 833 TOP/s (12.5 % for ternary).
 //
 // A block computes a 128-row x 64-token tile.  int8 / int6: 8 waves, two a SIMD; the waves of pair p (waves 4 p ..
 // 4 p + 3) take rows 64 p .. + 63 and chain w % 4, four 32 x 32 sub-tiles each (the weights' operand read once for
