@@ -451,7 +451,7 @@ hipError_t launch_type(const SbBatch &b, int T, int L, size_t lds, hipStream_t s
 
 // ---------------------------------------------------------------------------------------------------------------
 // the prompt tile (matmul_sbr_tile / matmul_sbw_tile for kSbTileMin tokens or more): a block takes 32 rows x NT
-// tokens (NT 32 or 64).  For each block of 256 weights it stages the tokens' activations (with their scales and
+// tokens (NT 32, 64 or 128).  For each block of 256 weights it stages the tokens' activations (with their scales and
 // sums) and the rows' raw blocks into LDS, decodes the 32 blocks once (two chunks of 16 a thread, the token kernel's
 // decoder reading the LDS copy) into int8 tiles, and multiplies them on the matrix cores:
 // v_mfma_i32_32x32x32_i8, A = 32 tokens, B = the 32 rows, K = 32 = a group, so a lane holds one row (l % 32) and 16
@@ -463,8 +463,8 @@ hipError_t launch_type(const SbBatch &b, int T, int L, size_t lds, hipStream_t s
 //   IQ1: C of the codes, d = 8 C - (7 + 2 down) (sum of each 8); the K types' M against the sums of 16;
 // then each (row, token) adds f(f(f(G_k xs_k) + f(G_{k+4} xs_{k+4})) F) (less the minimums') to its lane k in block
 // order, and ((l0 + l1) + l2) + l3 at the end (types.ts:48-57): every (row, token) the token kernel's number.
-// The four waves split the tokens and the lanes k: NT = 64, two token halves x two pairs of lanes; NT = 32, a lane
-// k a wave; the lanes meet in LDS at the end in that order.  The next block's bytes are loaded into registers while
+// The four waves split the tokens and the lanes k: NT = 128, 32 tokens and all four lanes a wave; NT = 64, two token
+// halves x two pairs of lanes; NT = 32, a lane k a wave; the lanes meet in LDS at the end in that order.  The next block's bytes are loaded into registers while
 // this one is decoded and multiplied, and stored into LDS after.
 // ---------------------------------------------------------------------------------------------------------------
 typedef int32_t v4i_t __attribute__((ext_vector_type(4)));
@@ -473,12 +473,15 @@ typedef int32_t v16i_t __attribute__((ext_vector_type(16)));
 constexpr int SBT_R = 32;            // a block's rows
 constexpr int SBT_PITCH = 256 + 16;  // an LDS row of a block's 256 bytes (16 more: 16-byte reads of rows apart)
 #ifndef HQ_SB_TILE_NT
-#define HQ_SB_TILE_NT 0  // 0: 64 tokens a block where that gives enough blocks, else 32
+#define HQ_SB_TILE_NT 0  // 0: the widest of 128, 64, 32 tokens a block that gives enough blocks
 #endif
 
 template <int TY> constexpr bool tile_signed() { return has_signs<TY>(); }
 template <int TY> constexpr bool tile_split() { return TY == IQ2_XS || TY == IQ2_S || TY == IQ1_M; }
 template <int TY> constexpr bool tile_sums16() { return has_minimums<TY>() || is_iq1<TY>(); }
+// the types with a 128-token tile (one scale a group, no sums: two waves a SIMD still fit; the others measured
+// slower at 128 than at 64)
+template <int TY> constexpr bool tile_wide() { return !tile_sums16<TY>() && !tile_split<TY>(); }
 
 template <int TY, int NT>
 struct SbTileLayout {
@@ -499,7 +502,7 @@ struct SbTileLayout {
   static constexpr int GRIDS = FF + 2 * SBT_R * 4;                         // the type's grid and sign table
   static constexpr int SIZE = GRIDS + lds_table_bytes<TY>();
   // the lanes' sums at the end, over X .. : NT = 64, l0 + l1 [SBT_R][NT]; NT = 32, l0, l1, l2 [3][SBT_R][NT]
-  static constexpr int LANES = (NT == 64 ? 1 : 3) * SBT_R * NT * 4;
+  static constexpr int LANES = (NT == 128 ? 0 : NT == 64 ? 1 : 3) * SBT_R * NT * 4;
   static_assert(LANES <= GRIDS, "the lanes' sums fit below the grids");
   // the loads of a block a thread: the tokens' bytes (16 a load), their scales and sums (16 bytes a load), the raw
   // blocks' words
@@ -601,7 +604,7 @@ template <int TY, int NT>
 __global__ __launch_bounds__(256) void gemm_sb(Job J) {
   using Lay = SbTileLayout<TY, NT>;
   constexpr int BYTES = Lay::BYTES, GRID = grid_bytes<TY>();
-  constexpr int TH = NT / 32;  // token halves; also the lanes k a wave
+  constexpr int TH = NT / 32;  // the waves' token slices; also the lanes k a wave
   extern __shared__ __align__(16) char lds[];
   const int8_t *x = (const int8_t *)(lds + Lay::X);
   const float *xsT = (const float *)(lds + Lay::XS);
@@ -792,7 +795,17 @@ __global__ __launch_bounds__(256) void gemm_sb(Job J) {
   __syncthreads();
   float *lanes = (float *)(lds + Lay::X);
   const int row = r0 + mrow;
-  if (NT == 64) {  // waves 0, 1 (lanes 0, 1) leave l0 + l1; waves 2, 3 add l2, then l3
+  if (NT == 128) {  // a wave holds the four lanes
+    if (row < J.r1) {
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int t = 32 * th + 8 * (r >> 2) + 4 * kh + (r & 3);
+        if (t0 + t < J.count)
+          ((float *)(J.out + (t0 + t) * J.os))[row] =
+              fadd(fadd(fadd(acc[0][r], acc[1 % TH][r]), acc[2 % TH][r]), acc[3 % TH][r]);
+      }
+    }
+  } else if (NT == 64) {  // waves 0, 1 (lanes 0, 1) leave l0 + l1; waves 2, 3 add l2, then l3
     if (k0 == 0) {
 #pragma unroll
       for (int r = 0; r < 16; r++) {
@@ -849,14 +862,18 @@ hipError_t launch_tile_nt(const Job &j, int nrt, hipStream_t s) {
   return hipGetLastError();
 }
 
-// 64 tokens a block when that makes at least two blocks a compute unit, else 32 (twice the decoding, twice the
-// blocks)
+// the widest tile (128 for the tile_wide types, 64, 32 tokens) that still makes at least two blocks a compute unit:
+// a wider one decodes each block of weights for more tokens, a narrower one has more blocks to hide a block's waits
 template <int TY>
 hipError_t launch_tile_type(const Job &j, hipStream_t s) {
   const int nrt = (j.r1 - j.r0 + SBT_R - 1) / SBT_R;
-  const bool wide = HQ_SB_TILE_NT == 64 ||
-                    (HQ_SB_TILE_NT == 0 && (int64_t)nrt * ((j.count + 63) / 64) >= 2 * (int64_t)cu_count());
-  return wide ? launch_tile_nt<TY, 64>(j, nrt, s) : launch_tile_nt<TY, 32>(j, nrt, s);
+  const int64_t want = 2 * (int64_t)cu_count();
+  int nt = HQ_SB_TILE_NT;
+  if (nt == 0) nt = tile_wide<TY>() && (int64_t)nrt * ((j.count + 127) / 128) >= want ? 128
+                  : (int64_t)nrt * ((j.count + 63) / 64) >= want ? 64 : 32;
+  if constexpr (tile_wide<TY>())
+    if (nt == 128) return launch_tile_nt<TY, 128>(j, nrt, s);
+  return nt == 64 ? launch_tile_nt<TY, 64>(j, nrt, s) : launch_tile_nt<TY, 32>(j, nrt, s);
 }
 
 // ---------------------------------------------------------------------------------------------------------------

@@ -586,6 +586,9 @@ __global__ __launch_bounds__(256) void gemv_ternary(GemvBatch batch) {
   for (int t = 0; t < T; t++) acc[t] = 0.0f;
   const int steps = (groups + L - 1) / L;
   TernaryChunk<L, BIN> a, b;
+  // the first codes in flight during the staging: the staged bytes' stores then wait for them too (the memory
+  // counter is in order), but the two round trips overlap instead of following one another
+  a.load(wrow, srow, 0, lane, groups);
   if (STAGE) {
     // every token's n bytes (a group's 128 in 144), then its n/32 scales and n/32 sums: 16 bytes a thread at a time,
     // eight loads of a thread in flight before their stores
@@ -608,9 +611,6 @@ __global__ __launch_bounds__(256) void gemv_ternary(GemvBatch batch) {
         }
       }
   }
-  // the first codes in flight during the barrier (issued after the staging's loads: the memory counter is in order,
-  // so a store of staged bytes waits for no code)
-  a.load(wrow, srow, 0, lane, groups);
   if (STAGE) __syncthreads();
   // the next step's codes are loaded whether or not the row has that step (past its groups a lane loads its group 0
   // again): the same loads outstanding on every path, so using a step's codes waits for them alone and not for the

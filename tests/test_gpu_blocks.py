@@ -188,6 +188,39 @@ def test_matmul_sbr_tile_rows(k, arena, oracle, setup, name, t):
             assert same_bits(got[tk], want), f"{name} rows {r0}..{r1} token {tk}: {first_difference(got[tk], want)}"
 
 
+@pytest.mark.parametrize("name,t", TYPES)
+def test_matmul_sbr_tile_wide(k, arena, oracle, setup, name, t):
+    """enough rows that the launch takes the wide tiles (a block of 128 tokens for one-scale-a-group types without
+    sums, 64 for the others: at least two blocks a compute unit), 130 tokens (a partial second tile): every token of
+    the first and last 64 rows, and every row of seven tokens"""
+    row, tab = setup
+    area = put_tables(k, arena, row)
+    rng = np.random.default_rng(900 + t)
+    rows, n, tokens = 16400, 256, 130
+    wbytes = bm.random_blocks(rng, t, rows).reshape(-1)
+    w = arena.put(wbytes)
+    frame = ((n + n // 2 + 15) // 16) * 16
+    buf = np.zeros(tokens * frame, np.uint8)
+    acts = []
+    for tk in range(tokens):
+        q, act = token_area(oracle, rng, n, scale=1.0 + tk % 5)
+        buf[tk * frame:tk * frame + n] = q.view(np.uint8)
+        buf[tk * frame + n:tk * frame + n + act.size] = act
+        acts.append((q, act))
+    xq = arena.put(buf)
+    os_ = 4 * rows
+    out = arena.alloc(os_ * tokens, fill=np.full(rows * tokens, -7, F))
+    k.matmul_sbr_tile(out, xq, xq + n, w, area, n, 0, rows, tokens, os_, frame, t)
+    got = arena.get(out, F, rows * tokens).reshape(tokens, rows)
+    for tk, (q, act) in enumerate(acts):
+        for r0, r1 in ((0, 64), (rows - 64, rows)):
+            want = oracle.matmul_sbr(q, act, wbytes, tab, n, t, r0, r1)[r0:r1]
+            assert same_bits(got[tk, r0:r1], want), f"{name} token {tk} rows {r0}..{r1}: {first_difference(got[tk, r0:r1], want)}"
+    for tk in (0, 31, 64, 100, 127, 128, 129):
+        want = oracle.matmul_sbr(*acts[tk], wbytes, tab, n, t)
+        assert same_bits(got[tk], want), f"{name} token {tk}: {first_difference(got[tk], want)}"
+
+
 def test_phase_and_matmuls_of_blocks(pkg, k, arena, oracle, setup):
     """jobs of kinds 10, 11, 12 of several types in one hq_phase, and hq_matmuls (quantize_x at bias 0 and sums_x,
     then the phase) for three tokens"""
