@@ -460,7 +460,8 @@ hipError_t launch_type(const SbBatch &b, int T, int L, size_t lds, hipStream_t s
 //   in two tiles, d = C(W ^ neg) + C(neg & 1), the second product added in the first's accumulator;
 //   a scale S for each 16 (IQ2_XS, IQ2_S, IQ1_M): two products a group, B zero in one half of the lanes (K 0..15
 //   is lanes 0..31's, K 16..31 lanes 32..63's), G = S_lo d_lo + S_hi d_hi; Q2_K's S W (at most 45) is its tile;
-//   IQ1: C of the codes, d = 8 C - (7 + 2 down) (sum of each 8); the K types' M against the sums of 16;
+//   IQ1: C of the codes, d = 8 C - (7 + 2 down) (sum of each 8); the K types' M against the sums of 16 (an f32
+//   outer product on the matrix core, K = 2: the two chunks of the group);
 // then each (row, token) adds f(f(f(G_k xs_k) + f(G_{k+4} xs_{k+4})) F) (less the minimums') to its lane k in block
 // order, and ((l0 + l1) + l2) + l3 at the end (types.ts:48-57): every (row, token) the token kernel's number.
 // The four waves split the tokens and the lanes k: NT = 128, 32 tokens and all four lanes a wave; NT = 64, two token
@@ -469,6 +470,7 @@ hipError_t launch_type(const SbBatch &b, int T, int L, size_t lds, hipStream_t s
 // ---------------------------------------------------------------------------------------------------------------
 typedef int32_t v4i_t __attribute__((ext_vector_type(4)));
 typedef int32_t v16i_t __attribute__((ext_vector_type(16)));
+typedef float v16f_t __attribute__((ext_vector_type(16)));
 
 constexpr int SBT_R = 32;            // a block's rows
 constexpr int SBT_PITCH = 256 + 16;  // an LDS row of a block's 256 bytes (16 more: 16-byte reads of rows apart)
@@ -708,7 +710,7 @@ __global__ __launch_bounds__(256) void gemm_sb(Job J) {
         const v4i_t Bm = *(const v4i_t *)(wm + mrow * SBT_PITCH + 32 * gg + 16 * kh);
         const v16i_t zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
         const int32_t S0 = sbyte(Sw[c0 >> 2], c0 & 3), S1 = sbyte(Sw[c1 >> 2], c1 & 3);
-        int32_t G[16], Mi[16];
+        int32_t G[16];
         if (tile_split<TY>()) {
           const v4i_t z4 = {0, 0, 0, 0};
           v16i_t lo = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, kh == 0 ? Bm : z4, zero, 0, 0, 0);
@@ -758,16 +760,13 @@ __global__ __launch_bounds__(256) void gemm_sb(Job J) {
 #pragma unroll
           for (int r = 0; r < 16; r++) G[r] = TY == Q2_K ? C[r] : __mul24(S0, C[r]);
         }
-        if (has_minimums<TY>()) {
-          const int32_t M0 = sbyte(Mw[c0 >> 2], c0 & 3), M1 = sbyte(Mw[c1 >> 2], c1 & 3);
-#pragma unroll
-          for (int m = 0; m < 4; m++) {
-            const int tk = 32 * th + 8 * m + 4 * kh;
-            const int4 e0 = *(const int4 *)(s16T + c0 * NT + tk), e1 = *(const int4 *)(s16T + c1 * NT + tk);
-            const int32_t v0[4] = {e0.x, e0.y, e0.z, e0.w}, v1[4] = {e1.x, e1.y, e1.z, e1.w};
-#pragma unroll
-            for (int i = 0; i < 4; i++) Mi[4 * m + i] = __mul24(M0, v0[i]) + __mul24(M1, v1[i]);
-          }
+        v16f_t Mf;  // M0 v0 + M1 v1 (the K types' minimums against the sums of 16), exact in float32: |.| < 2^18
+        if (has_minimums<TY>()) {  // an outer product with K = 2: A the tokens' sums of chunks c0 (lanes 0..31) and
+                                   // c1 (32..63), B the row's M of the same chunks
+          const int c = kh ? c1 : c0;
+          const v16f_t z = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+          Mf = __builtin_amdgcn_mfma_f32_32x32x2f32((float)s16T[c * NT + mtok], (float)sbyte(Mw[c >> 2], c & 3), z, 0,
+                                                    0, 0);
         }
         // group gg's scales: f(G xs) (and f(M xs)); the second group of the pair completes the part
 #pragma unroll
@@ -780,10 +779,10 @@ __global__ __launch_bounds__(256) void gemm_sb(Job J) {
             const int r = 4 * m + i;
             if (e == 0) {
               q0[r] = fmul((float)G[r], sv[i]);
-              if (has_minimums<TY>()) qm0[r] = fmul((float)Mi[r], sv[i]);
+              if (has_minimums<TY>()) qm0[r] = fmul(Mf[r], sv[i]);
             } else {
               float part = fmul(fadd(q0[r], fmul((float)G[r], sv[i])), F);
-              if (has_minimums<TY>()) part = fsub(part, fmul(fadd(qm0[r], fmul((float)Mi[r], sv[i])), Fm));
+              if (has_minimums<TY>()) part = fsub(part, fmul(fadd(qm0[r], fmul(Mf[r], sv[i])), Fm));
               acc[kk][r] = fadd(acc[kk][r], part);
             }
           }
