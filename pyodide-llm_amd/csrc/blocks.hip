@@ -460,8 +460,9 @@ hipError_t launch_type(const SbBatch &b, int T, int L, size_t lds, hipStream_t s
 //   in two tiles, d = C(W ^ neg) + C(neg & 1), the second product added in the first's accumulator;
 //   a scale S for each 16 (IQ2_XS, IQ2_S, IQ1_M): two products a group, B zero in one half of the lanes (K 0..15
 //   is lanes 0..31's, K 16..31 lanes 32..63's), G = S_lo d_lo + S_hi d_hi; Q2_K's S W (at most 45) is its tile;
-//   IQ1: C of the codes, d = 8 C - (7 + 2 down) (sum of each 8); the K types' M against the sums of 16 (an f32
-//   outer product on the matrix core, K = 2: the two chunks of the group);
+//   IQ1: C of the codes and C of a second tile holding -(7 + 2 down) for each 8 weights, d = 8 C + C(corr) = 8
+//   dot(code, a) - (7 + 2 down) (sum of each 8); the K types' M against the sums of 16 (an f32 outer product on the
+//   matrix core, K = 2: the two chunks of the group);
 // then each (row, token) adds f(f(f(G_k xs_k) + f(G_{k+4} xs_{k+4})) F) (less the minimums') to its lane k in block
 // order, and ((l0 + l1) + l2) + l3 at the end (types.ts:48-57): every (row, token) the token kernel's number.
 // The four waves split the tokens and the lanes k: NT = 128, 32 tokens and all four lanes a wave; NT = 64, two token
@@ -480,10 +481,12 @@ constexpr int SBT_PITCH = 256 + 16;  // an LDS row of a block's 256 bytes (16 mo
 
 template <int TY> constexpr bool tile_signed() { return has_signs<TY>(); }
 template <int TY> constexpr bool tile_split() { return TY == IQ2_XS || TY == IQ2_S || TY == IQ1_M; }
-template <int TY> constexpr bool tile_sums16() { return has_minimums<TY>() || is_iq1<TY>(); }
+template <int TY> constexpr bool tile_sums16() { return has_minimums<TY>(); }
+// a second int8 tile: neg's 0 / 1 (signed grids) or IQ1's -(7 + 2 down) for each 8 weights
+template <int TY> constexpr bool tile_second() { return has_signs<TY>() || is_iq1<TY>(); }
 // the types with a 128-token tile (one scale a group, no sums: two waves a SIMD still fit; the others measured
 // slower at 128 than at 64)
-template <int TY> constexpr bool tile_wide() { return !tile_sums16<TY>() && !tile_split<TY>(); }
+template <int TY> constexpr bool tile_wide() { return !tile_sums16<TY>() && !tile_split<TY>() && !is_iq1<TY>(); }
 
 template <int TY, int NT>
 struct SbTileLayout {
@@ -492,15 +495,13 @@ struct SbTileLayout {
   static constexpr int RAWP = 4 * WORDS;
   static constexpr int X = 0;                                              // int8 [NT][SBT_PITCH]
   static constexpr int XS = X + NT * SBT_PITCH;                            // float [8][NT]
-  static constexpr int S16 = XS + 8 * NT * 4;                              // int32 [16][NT] (K, IQ1)
-  static constexpr int S8 = S16 + (tile_sums16<TY>() ? 16 * NT * 4 : 0);   // int32 [32][NT] (IQ1_M)
-  static constexpr int RAW = S8 + (TY == IQ1_M ? 32 * NT * 4 : 0);         // bytes [SBT_R][RAWP]
+  static constexpr int S16 = XS + 8 * NT * 4;                              // int32 [16][NT] (K)
+  static constexpr int RAW = S16 + (tile_sums16<TY>() ? 16 * NT * 4 : 0);  // bytes [SBT_R][RAWP]
   static constexpr int WM = RAW + SBT_R * RAWP;                            // int8 [SBT_R][SBT_PITCH]
-  static constexpr int WN = WM + SBT_R * SBT_PITCH;                        // int8 [SBT_R][SBT_PITCH] (signed grids)
-  static constexpr int RS = WN + (tile_signed<TY>() ? SBT_R * SBT_PITCH : 0);  // int8 [SBT_R][16] S
+  static constexpr int WN = WM + SBT_R * SBT_PITCH;                        // int8 [SBT_R][SBT_PITCH] (tile_second)
+  static constexpr int RS = WN + (tile_second<TY>() ? SBT_R * SBT_PITCH : 0);  // int8 [SBT_R][16] S
   static constexpr int RM = RS + SBT_R * 16;                               // int8 [SBT_R][16] M
-  static constexpr int RD = RM + SBT_R * 16;                               // uint8 [SBT_R][16] IQ1's shifts
-  static constexpr int FF = RD + SBT_R * 16;                               // float [SBT_R] F, then [SBT_R] Fm
+  static constexpr int FF = RM + SBT_R * 16;                               // float [SBT_R] F, then [SBT_R] Fm
   static constexpr int GRIDS = FF + 2 * SBT_R * 4;                         // the type's grid and sign table
   static constexpr int SIZE = GRIDS + lds_table_bytes<TY>();
   // the lanes' sums at the end, over X .. : NT = 64, l0 + l1 [SBT_R][NT]; NT = 32, l0, l1, l2 [3][SBT_R][NT]
@@ -509,7 +510,7 @@ struct SbTileLayout {
   // the loads of a block a thread: the tokens' bytes (16 a load), their scales and sums (16 bytes a load), the raw
   // blocks' words
   static constexpr int XU = NT * 16 / 256;
-  static constexpr int AUX = NT * (2 + (tile_sums16<TY>() ? 2 : 0) + (TY == IQ1_M ? 4 : 0));
+  static constexpr int AUX = NT * (2 + (tile_sums16<TY>() ? 2 : 0));
   static constexpr int AU = (AUX + 255) / 256;
   static constexpr int RU = (SBT_R * WORDS + 255) / 256;
 };
@@ -537,12 +538,10 @@ HQ_DEV void tile_load(TileLoads<TY, NT> &L, int tid, int b, __amdgpu_buffer_rsrc
   }
 #pragma unroll
   for (int u = 0; u < Lay::AU; u++) {
-    // a < 2 NT: the scales (token a / 2, half a % 2); < 4 NT: the sums of 16; then IQ1_M's sums of 8 (a quarter)
+    // a < 2 NT: the scales (token a / 2, half a % 2); then the K types' sums of 16
     const int a0 = tid + 256 * u, a = a0 < Lay::AUX ? a0 : Lay::AUX - 1;
-    int off;
-    if (a < 2 * NT) off = (a >> 1) * (int)sframe + 32 * b + 16 * (a & 1);
-    else if (a < 4 * NT && tile_sums16<TY>()) off = ((a - 2 * NT) >> 1) * (int)sframe + 4 * (n >> 5) + 32 * b + 16 * (a & 1);
-    else off = ((a - 4 * NT) >> 2) * (int)sframe + 4 * (n >> 5) + 2 * (n >> 4) + 64 * b + 16 * (a & 3);
+    const int off = a < 2 * NT ? (a >> 1) * (int)sframe + 32 * b + 16 * (a & 1)
+                               : ((a - 2 * NT) >> 1) * (int)sframe + 4 * (n >> 5) + 32 * b + 16 * (a & 1);
     L.aux[u] = __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0);
   }
 #pragma unroll
@@ -561,7 +560,7 @@ HQ_DEV void tile_store(const TileLoads<TY, NT> &L, int tid, char *lds) {
   constexpr int WORDS = Lay::WORDS;
   int8_t *x = (int8_t *)(lds + Lay::X);
   float *xsT = (float *)(lds + Lay::XS);
-  int32_t *s16T = (int32_t *)(lds + Lay::S16), *s8T = (int32_t *)(lds + Lay::S8);
+  int32_t *s16T = (int32_t *)(lds + Lay::S16);
 #pragma unroll
   for (int u = 0; u < Lay::XU; u++) {
     const int idx = tid + 256 * u, tok = idx >> 4, q = idx & 15;
@@ -575,19 +574,12 @@ HQ_DEV void tile_store(const TileLoads<TY, NT> &L, int tid, char *lds) {
       const int tok = a >> 1, half = a & 1;
 #pragma unroll
       for (int i = 0; i < 4; i++) xsT[(4 * half + i) * NT + tok] = __int_as_float(v[i]);
-    } else if (a < 4 * NT && tile_sums16<TY>()) {
+    } else if (a < Lay::AUX) {
       const int tok = (a - 2 * NT) >> 1, half = a & 1;
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         s16T[(8 * half + 2 * i) * NT + tok] = (int32_t)(int16_t)(v[i] & 0xffff);
         s16T[(8 * half + 2 * i + 1) * NT + tok] = (int32_t)(int16_t)((uint32_t)v[i] >> 16);
-      }
-    } else if (a < Lay::AUX) {
-      const int tok = (a - 4 * NT) >> 2, qq = a & 3;
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        s8T[(8 * qq + 2 * i) * NT + tok] = (int32_t)(int16_t)(v[i] & 0xffff);
-        s8T[(8 * qq + 2 * i + 1) * NT + tok] = (int32_t)(int16_t)((uint32_t)v[i] >> 16);
       }
     }
   }
@@ -610,11 +602,10 @@ __global__ __launch_bounds__(256) void gemm_sb(Job J) {
   extern __shared__ __align__(16) char lds[];
   const int8_t *x = (const int8_t *)(lds + Lay::X);
   const float *xsT = (const float *)(lds + Lay::XS);
-  const int32_t *s16T = (const int32_t *)(lds + Lay::S16), *s8T = (const int32_t *)(lds + Lay::S8);
+  const int32_t *s16T = (const int32_t *)(lds + Lay::S16);
   const uint8_t *raw = (const uint8_t *)(lds + Lay::RAW);
   int8_t *wm = (int8_t *)(lds + Lay::WM), *wn = (int8_t *)(lds + Lay::WN);
   int8_t *rs = (int8_t *)(lds + Lay::RS), *rm = (int8_t *)(lds + Lay::RM);
-  uint8_t *rd = (uint8_t *)(lds + Lay::RD);
   float *ff = (float *)(lds + Lay::FF);
   uint8_t *table = (uint8_t *)(lds + Lay::GRIDS);
 
@@ -684,9 +675,13 @@ __global__ __launch_bounds__(256) void gemm_sb(Job J) {
         } else {
           *(uint4 *)(wm + dr * SBT_PITCH + 16 * h) = make_uint4(m4[0], m4[1], m4[2], m4[3]);
         }
+        if (is_iq1<TY>()) {  // -(7 + 2 down) for each 8 weights of the chunk
+          const uint32_t e0 = (uint32_t)(uint8_t)(int8_t)(-7 - 2 * (int32_t)c.down0) * 0x01010101u;
+          const uint32_t e1 = (uint32_t)(uint8_t)(int8_t)(-7 - 2 * (int32_t)c.down1) * 0x01010101u;
+          *(uint4 *)(wn + dr * SBT_PITCH + 16 * h) = make_uint4(e0, e0, e1, e1);
+        }
         rs[dr * 16 + h] = (int8_t)c.S;
         rm[dr * 16 + h] = (int8_t)c.M;
-        rd[dr * 16 + h] = (uint8_t)(c.down0 | (c.down1 << 1));
       }
       if (dq == 0) {
         ff[dr] = block_f<TY>(B);
@@ -696,9 +691,8 @@ __global__ __launch_bounds__(256) void gemm_sb(Job J) {
     __syncthreads();
     // ---- the products: the wave's 32 x 32 for its lanes k, group pairs (k, k + 4)
     const float F = ff[mrow], Fm = ff[SBT_R + mrow];
-    const uint4 S4 = *(const uint4 *)(rs + mrow * 16), M4 = *(const uint4 *)(rm + mrow * 16),
-                D4 = *(const uint4 *)(rd + mrow * 16);
-    const uint32_t Sw[4] = {S4.x, S4.y, S4.z, S4.w}, Mw[4] = {M4.x, M4.y, M4.z, M4.w}, Dw[4] = {D4.x, D4.y, D4.z, D4.w};
+    const uint4 S4 = *(const uint4 *)(rs + mrow * 16), M4 = *(const uint4 *)(rm + mrow * 16);
+    const uint32_t Sw[4] = {S4.x, S4.y, S4.z, S4.w}, Mw[4] = {M4.x, M4.y, M4.z, M4.w};
 #pragma unroll
     for (int kk = 0; kk < TH; kk++) {
       const int k = k0 + kk;
@@ -721,21 +715,13 @@ __global__ __launch_bounds__(256) void gemm_sb(Job J) {
             hi = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, kh == 1 ? Bn : z4, hi, 0, 0, 0);
           }
           if (is_iq1<TY>()) {  // 8 dot(code, a) - (7 + 2 down) (sum of each 8), for each of the two 16s
-            const uint32_t d0 = (Dw[c0 >> 2] >> (8 * (c0 & 3))) & 3u, d1 = (Dw[c1 >> 2] >> (8 * (c1 & 3))) & 3u;
-            const int32_t a0 = 7 + 2 * (int32_t)(d0 & 1u), b0 = 7 + 2 * (int32_t)(d0 >> 1);
-            const int32_t a1 = 7 + 2 * (int32_t)(d1 & 1u), b1 = 7 + 2 * (int32_t)(d1 >> 1);
+            const v4i_t Bc = *(const v4i_t *)(wn + mrow * SBT_PITCH + 32 * gg + 16 * kh);
+            const v16i_t clo = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, kh == 0 ? Bc : z4, zero, 0, 0, 0);
+            const v16i_t chi = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, kh == 1 ? Bc : z4, zero, 0, 0, 0);
 #pragma unroll
-            for (int m = 0; m < 4; m++) {
-              const int tk = 32 * th + 8 * m + 4 * kh;
-              const int4 e00 = *(const int4 *)(s8T + (2 * c0) * NT + tk), e01 = *(const int4 *)(s8T + (2 * c0 + 1) * NT + tk);
-              const int4 e10 = *(const int4 *)(s8T + (2 * c1) * NT + tk), e11 = *(const int4 *)(s8T + (2 * c1 + 1) * NT + tk);
-              const int32_t v00[4] = {e00.x, e00.y, e00.z, e00.w}, v01[4] = {e01.x, e01.y, e01.z, e01.w};
-              const int32_t v10[4] = {e10.x, e10.y, e10.z, e10.w}, v11[4] = {e11.x, e11.y, e11.z, e11.w};
-#pragma unroll
-              for (int i = 0; i < 4; i++) {
-                lo[4 * m + i] = 8 * lo[4 * m + i] - __mul24(a0, v00[i]) - __mul24(b0, v01[i]);
-                hi[4 * m + i] = 8 * hi[4 * m + i] - __mul24(a1, v10[i]) - __mul24(b1, v11[i]);
-              }
+            for (int r = 0; r < 16; r++) {
+              lo[r] = 8 * lo[r] + clo[r];
+              hi[r] = 8 * hi[r] + chi[r];
             }
           }
 #pragma unroll
@@ -747,15 +733,10 @@ __global__ __launch_bounds__(256) void gemm_sb(Job J) {
             C = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, Bn, C, 0, 0, 0);
           }
           if (is_iq1<TY>()) {  // IQ1_S: one shift for the 32, against the sum of the 32
-            const int32_t a = 7 + 2 * (int32_t)((Dw[c0 >> 2] >> (8 * (c0 & 3))) & 1u);
+            const v4i_t Bc = *(const v4i_t *)(wn + mrow * SBT_PITCH + 32 * gg + 16 * kh);
+            const v16i_t Cc = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, Bc, zero, 0, 0, 0);
 #pragma unroll
-            for (int m = 0; m < 4; m++) {
-              const int tk = 32 * th + 8 * m + 4 * kh;
-              const int4 e0 = *(const int4 *)(s16T + c0 * NT + tk), e1 = *(const int4 *)(s16T + c1 * NT + tk);
-              const int32_t v0[4] = {e0.x, e0.y, e0.z, e0.w}, v1[4] = {e1.x, e1.y, e1.z, e1.w};
-#pragma unroll
-              for (int i = 0; i < 4; i++) C[4 * m + i] = 8 * C[4 * m + i] - __mul24(a, v0[i] + v1[i]);
-            }
+            for (int r = 0; r < 16; r++) C[r] = 8 * C[r] + Cc[r];
           }
 #pragma unroll
           for (int r = 0; r < 16; r++) G[r] = TY == Q2_K ? C[r] : __mul24(S0, C[r]);
