@@ -486,7 +486,7 @@ template <int TY> constexpr bool tile_sums16() { return has_minimums<TY>(); }
 template <int TY> constexpr bool tile_second() { return has_signs<TY>() || is_iq1<TY>(); }
 // the types with a 128-token tile (one scale a group, no sums: two waves a SIMD still fit; the others measured
 // slower at 128 than at 64)
-template <int TY> constexpr bool tile_wide() { return !tile_sums16<TY>() && !tile_split<TY>() && !is_iq1<TY>(); }
+template <int TY> constexpr bool tile_wide() { return !tile_sums16<TY>() && !tile_split<TY>(); }
 
 template <int TY, int NT>
 struct SbTileLayout {
