@@ -148,7 +148,9 @@ int32_t run_blocks(hq::Kind kind, const std::vector<hq::Job> &jobs, hipStream_t 
   std::vector<hq::Job> parts;
   for (const hq::Job &j : jobs) {
     if (j.r1 == j.r0 || j.count == 0) continue;
-    if (j.count >= hq::kSbTileMin && j.frame > 0 && j.sframe > 0) {  // a prompt: the matrix-core tile
+    // a prompt: the matrix-core tile (its offsets within a tile of tokens are 32-bit: frames under 16 MB)
+    if (j.count >= hq::kSbTileMin && j.frame > 0 && j.sframe > 0 && j.frame < hq::kSbTileFrameMax &&
+        j.sframe < hq::kSbTileFrameMax) {
       const int32_t st = hip_status(hq::launch_sb_tile(j, s), kind_name(kind));
       if (st) return st;
       continue;

@@ -75,6 +75,7 @@ hipError_t launch_sb(const Job *jobs, int32_t njobs, hipStream_t s);
 // a prompt of kSbTileMin tokens or more of one job (the sb kinds), on the matrix cores: every (row, token)
 // launch_sb's number
 constexpr int kSbTileMin = 16;
+constexpr int64_t kSbTileFrameMax = (int64_t)1 << 24;  // frame and sframe of a job the tile takes: 128 tokens' offsets fit in int32
 hipError_t launch_sb_tile(const Job &job, hipStream_t s);
 hipError_t launch_signed_dots(int32_t *out, const int8_t *a, const int8_t *b, hipStream_t s);
 
