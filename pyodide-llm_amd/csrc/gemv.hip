@@ -556,16 +556,20 @@ struct TernaryChunk {
   }
 };
 
+#ifndef HQ_TERN_THREADS
+#define HQ_TERN_THREADS 256
+#endif
+constexpr int kTernThreads = HQ_TERN_THREADS;  // a block's threads: kTernThreads / L rows
 // rows of L lanes (16: 16 rows a block; 32 for long rows: twice the waves on the same rows)
 template <int T, bool STAGE, int L, bool BIN>
-__global__ __launch_bounds__(256) void gemv_ternary(GemvBatch batch) {
+__global__ __launch_bounds__(kTernThreads) void gemv_ternary(GemvBatch batch) {
   extern __shared__ __align__(16) char acts[];
-  __shared__ FoldL<T, L> fold[4];
+  __shared__ FoldL<T, L> fold[kTernThreads / 64];
   const int jb = job_of(batch, blockIdx.x);
   const Job &J = batch.job[jb];
   const int lane = threadIdx.x & (L - 1);
   const int wave = threadIdx.x >> 6, slot = (threadIdx.x & 63) / L;
-  const int row_u = J.r0 + (blockIdx.x - batch.block0[jb]) * (256 / L) + threadIdx.x / L;
+  const int row_u = J.r0 + (blockIdx.x - batch.block0[jb]) * (kTernThreads / L) + threadIdx.x / L;
   const bool live = row_u < J.r1;
   const int row = live ? row_u : J.r1 - 1;
   const int groups = J.n >> 7;
@@ -595,17 +599,17 @@ __global__ __launch_bounds__(256) void gemv_ternary(GemvBatch batch) {
     const int per = ternary_token_bytes(J.n), chunks = (J.n + J.n / 4) / 16, gb = groups * kTernaryPitch;
     constexpr int K = 8;
     for (int t = 0; t < T; t++)
-      for (int base = 0; base < chunks; base += K * 256) {
+      for (int base = 0; base < chunks; base += K * kTernThreads) {
         uint4 v[K];
 #pragma unroll
         for (int u = 0; u < K; u++) {
-          const int o = 16 * (base + u * 256 + (int)threadIdx.x);
+          const int o = 16 * (base + u * kTernThreads + (int)threadIdx.x);
           if (o < J.n) v[u] = ld16(J.xq + t * J.frame + o);
           else if (o < J.n + J.n / 4) v[u] = ld16(J.xs + t * J.sframe + (o - J.n));
         }
 #pragma unroll
         for (int u = 0; u < K; u++) {
-          const int o = 16 * (base + u * 256 + (int)threadIdx.x);
+          const int o = 16 * (base + u * kTernThreads + (int)threadIdx.x);
           if (o < J.n) *(uint4 *)(acts + t * per + (o >> 7) * kTernaryPitch + (o & 127)) = v[u];
           else if (o < J.n + J.n / 4) *(uint4 *)(acts + t * per + gb + (o - J.n)) = v[u];
         }
@@ -670,7 +674,7 @@ hipError_t launch_signs(const GemvBatch &b, int blocks, hipStream_t s) {
   for (int j = 0; j < b.njobs; j++) nmax = b.job[j].n > nmax ? b.job[j].n : nmax;
   const size_t bytes = ternary_stage_bytes(T, nmax);
   const bool stage = bytes <= kTernaryStageMax;
-  dim3 grid(blocks), block(256);
+  dim3 grid(blocks), block(kTernThreads);
   switch (ternary_lanes(nmax)) {
   case 32:
     if (stage) hipLaunchKernelGGL((gemv_ternary<T, true, 32, BIN>), grid, block, bytes, s, b);
@@ -730,7 +734,7 @@ hipError_t launch_batch(Kind kind, const Job *jobs, int32_t njobs, const char *x
   GemvBatch b{};
   int blocks = 0, nmax = 0;
   for (int j = 0; j < njobs; j++) nmax = jobs[j].n > nmax ? jobs[j].n : nmax;
-  const int rpb = signs_kind(kind) ? 256 / ternary_lanes(nmax) : rows_per_block(kind);
+  const int rpb = signs_kind(kind) ? kTernThreads / ternary_lanes(nmax) : rows_per_block(kind);
   for (int j = 0; j < njobs; j++) {
     b.job[j] = jobs[j];
     b.block0[j] = blocks;
