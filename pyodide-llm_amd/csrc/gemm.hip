@@ -161,16 +161,19 @@ HQ_DEV void add_chains(float acc0[16], float acc1[16], float *p0, float *p1, int
 // MFMA A = weights (m = row), B = activations (n = token): lane l holds token l % 32 of its half and rows
 // 8 (r / 4) + 4 (l / 32) + r % 4 of its slice (r = 0..15); K half l / 32 is bytes 16 (l / 32) .. + 15 of the group.
 // ---------------------------------------------------------------------------------------------------------------
-constexpr int QG = 4;       // groups a stage
-constexpr int QNT = 512;    // threads a block
-constexpr int QLOADS = 6;   // loads a wave a stage
+constexpr int QG = 4;  // groups a stage
+// the rows of a block's tile (BRT 128: 8 waves; 64, for launches of few tiles: 4 waves, twice the blocks), its
+// threads and each wave's loads a stage
+template <int BRT> constexpr int q_threads() { return 4 * BRT; }
+template <int BRT> constexpr int q_loads() { return BRT == 128 ? 6 : 7; }
 
+template <int BRT>
 struct alignas(16) StageQ {
-  char w[BR * 128];    // int8: 128 rows x 4 groups x 32 bytes, chunks swizzled; int6: 128 rows x 4 x 24 bytes
-  char x[BT * 128];    // 64 tokens x 4 groups x 32 bytes, chunks swizzled
-  float ws[QG][BR];    // the rows' scales, group-major
-  int32_t wc[QG][BR];  // the rows' corrections (with the caller's wc), group-major
-  float xs[QG][BT];    // the tokens' scales, group-major; in each 32-token half token 8 m + 4 h + i at 16 h + 4 i + m
+  char w[BRT * 128];    // int8: BRT rows x 4 groups x 32 bytes, chunks swizzled; int6: BRT rows x 4 x 24 bytes
+  char x[BT * 128];     // 64 tokens x 4 groups x 32 bytes, chunks swizzled
+  float ws[QG][BRT];    // the rows' scales, group-major
+  int32_t wc[QG][BRT];  // the rows' corrections (with the caller's wc), group-major
+  float xs[QG][BT];     // the tokens' scales, group-major; in each 32-token half token 8 m + 4 h + i at 16 h + 4 i + m
 };
 
 // K half kh (values 16 kh .. + 15) of an int6 group (24 bytes at p, kernels/six.ts:16-31): value j's low nibble is
@@ -191,12 +194,15 @@ HQ_DEV v4i six_half(const char *p, int kh) {
   return v;
 }
 
-// a block's loads of int8 / int6 stages: wave w's six loads a stage and their offsets
-template <int PACK, bool WC>
+// a block's loads of int8 / int6 stages: wave w's q_loads a stage and their offsets
+template <int PACK, bool WC, int BRT>
 struct Relaxed {
   static constexpr int GB = PACK == 8 ? 32 : 24;  // bytes of a group of weights
+  static constexpr int NW = BRT / 16;             // waves
+  static constexpr int XPW = 8 / NW;              // 1 KB pieces of the activations a wave
+  static constexpr int SPG = BRT / 64;            // 64-row pieces of a group's scales
   __amdgpu_buffer_rsrc_t rw, rx, rws, rwc, rxs;
-  uint32_t oa[2], ob, oc, oe;
+  uint32_t oa[2], ob[XPW], oc, oe;
   int wave;
   char *junk;
 
@@ -222,13 +228,14 @@ struct Relaxed {
         oa[i] = (uint32_t)((q / 6) * rb + (q % 6) * 16);
       }
     }
-    // load b: the activations of tokens 8 w .. + 7, as the weights
-    {
-      const int tok = 8 * w + (lane >> 3), ch = (lane & 7) ^ swz(tok);
-      ob = (uint32_t)(tok * J.frame + (ch >> 1) * 32 + (ch & 1) * 16);
+    // load b: the activations of tokens 8 c .. + 7 (pieces c = XPW w ..), as the weights
+#pragma unroll
+    for (int i = 0; i < XPW; i++) {
+      const int tok = 8 * (XPW * w + i) + (lane >> 3), ch = (lane & 7) ^ swz(tok);
+      ob[i] = (uint32_t)(tok * J.frame + (ch >> 1) * 32 + (ch & 1) * 16);
     }
-    // loads c, d: the rows' scales and corrections of group w / 2, rows 64 (w % 2) + l
-    oc = (uint32_t)(((64 * (w & 1) + lane) * ng + (w >> 1)) * 4);
+    // loads c, d: the rows' scales and corrections of group w / SPG, rows 64 (w % SPG) + l
+    oc = (uint32_t)(((64 * (w % SPG) + lane) * ng + w / SPG) * 4);
     // load e: waves 0..3 the tokens' scales of group w, the tokens of each 32-token half reordered (entry 16 h + 4 i
     // + m is token 8 m + 4 h + i), so that one 16-byte read gives a lane the four tokens of its 4 x 4 outer products
     {
@@ -238,17 +245,18 @@ struct Relaxed {
     }
   }
 
-  // the 6 loads of stage s (groups 4 s .. 4 s + 3) into S
-  HQ_DEV void load(StageQ &S, int s) {
+  // the q_loads of stage s (groups 4 s .. 4 s + 3) into S
+  HQ_DEV void load(StageQ<BRT> &S, int s) {
     const int w = wave;
 #pragma unroll
     for (int i = 0; i < 2; i++) {
-      if (PACK == 8 || 2 * w + i < 12) dma16(rw, S.w + (2 * w + i) * 1024, oa[i], s * QG * GB);
+      if (PACK == 8 || 2 * w + i < 12 * BRT / 128) dma16(rw, S.w + (2 * w + i) * 1024, oa[i], s * QG * GB);
       else dma16(rxs, junk, 0, 0);
     }
-    dma16(rx, S.x + w * 1024, ob, s * QG * 32);
-    dma4(rws, &S.ws[w >> 1][64 * (w & 1)], oc, s * QG * 4);
-    if (WC) dma4(rwc, &S.wc[w >> 1][64 * (w & 1)], oc, s * QG * 4);
+#pragma unroll
+    for (int i = 0; i < XPW; i++) dma16(rx, S.x + (XPW * w + i) * 1024, ob[i], s * QG * 32);
+    dma4(rws, &S.ws[w / SPG][64 * (w % SPG)], oc, s * QG * 4);
+    if (WC) dma4(rwc, &S.wc[w / SPG][64 * (w % SPG)], oc, s * QG * 4);
     else dma4(rxs, junk, 0, 0);
     if (w < 4) dma4(rxs, &S.xs[w][0], oe, s * QG * 4);
     else dma4(rxs, junk, 0, 0);
@@ -260,8 +268,8 @@ struct Relaxed {
 // MFMAs), each term f(f(C) * f(ws * xs)) (relaxed/int8.ts:26-39).  MFMA A = activations (m = token), B = weights
 // (n = row): lane l holds row l % 32 of its slice and tokens 8 (r / 4) + 4 (l / 32) + r % 4 of its half, so a lane's
 // correction and row scale are one value each.
-template <int PACK, bool WC>
-HQ_DEV void q_group(float acc[4][16], const StageQ &S, int gi, int pair, int lane) {
+template <int PACK, bool WC, int BRT>
+HQ_DEV void q_group(float acc[4][16], const StageQ<BRT> &S, int gi, int pair, int lane) {
   const int kh = lane >> 5, l32 = lane & 31;
   v4i X[2];
   float xv[2][4];
@@ -309,13 +317,13 @@ HQ_DEV void q_group(float acc[4][16], const StageQ &S, int gi, int pair, int lan
 }
 
 // stage s in `cur`, the loads of stage s + AHEAD into `next` (the buffer of stage s - 1)
-template <int PACK, bool WC>
-HQ_DEV void q_step(Relaxed<PACK, WC> &L, const StageQ &cur, StageQ &next, int s, int stages, int total,
-                   float acc[4][16], int pair, int chain, int lane) {
+template <int PACK, bool WC, int BRT>
+HQ_DEV void q_step(Relaxed<PACK, WC, BRT> &L, const StageQ<BRT> &cur, StageQ<BRT> &next, int s, int stages,
+                   int total, float acc[4][16], int pair, int chain, int lane) {
   if (s >= stages) return;
-  wait_for<QLOADS>(s, total);
+  wait_for<q_loads<BRT>()>(s, total);
   if (s + AHEAD < total) L.load(next, s + AHEAD);
-  q_group<PACK, WC>(acc, cur, chain, pair, lane);  // group 4 s + chain
+  q_group<PACK, WC, BRT>(acc, cur, chain, pair, lane);  // group 4 s + chain
 }
 
 // the 4 chains of a pair of slices added in LDS, ((a0 + a1) + a2) + a3, for its four sub-tiles: wave k adds its sums
@@ -338,15 +346,15 @@ HQ_DEV void add_chains4(float acc[4][16], float *p0, float *p1, int pair, int ch
   }
 }
 
-template <int PACK, bool WC>
-__global__ __launch_bounds__(QNT) void gemm_relaxed(Job J) {
-  __shared__ StageQ b0, b1, b2, b3;
+template <int PACK, bool WC, int BRT>
+__global__ __launch_bounds__(q_threads<BRT>()) void gemm_relaxed(Job J) {
+  __shared__ StageQ<BRT> b0, b1, b2, b3;
   __shared__ __attribute__((aligned(16))) char junk[1024];
   const int M = J.count;
   const int ng = J.n >> 5, ng4 = ng & ~3;
   int rb, tb;
-  tile_of(blockIdx.x, gridDim.x, (J.r1 - J.r0 + BR - 1) / BR, rb, tb);
-  const int row0 = J.r0 + rb * BR, tok0 = tb * BT;
+  tile_of(blockIdx.x, gridDim.x, (J.r1 - J.r0 + BRT - 1) / BRT, rb, tb);
+  const int row0 = J.r0 + rb * BRT, tok0 = tb * BT;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int pair = wave >> 2, chain = wave & 3;
@@ -357,25 +365,25 @@ __global__ __launch_bounds__(QNT) void gemm_relaxed(Job J) {
 #pragma unroll
     for (int r = 0; r < 16; r++) acc[i][r] = 0.0f;
 
-  Relaxed<PACK, WC> L(J, row0, tok0, M, wave, junk);
+  Relaxed<PACK, WC, BRT> L(J, row0, tok0, M, wave, junk);
   const int stages = ng4 / QG;
   const int total = stages + (ng4 < ng ? 1 : 0);  // stages loaded: the tail's groups are one more
   if (total > 0) L.load(b0, 0);
   if (total > 1) L.load(b1, 1);
   if (total > 2) L.load(b2, 2);
   for (int s = 0; s < stages; s += RING) {
-    q_step<PACK, WC>(L, b0, b3, s, stages, total, acc, pair, chain, lane);
-    q_step<PACK, WC>(L, b1, b0, s + 1, stages, total, acc, pair, chain, lane);
-    q_step<PACK, WC>(L, b2, b1, s + 2, stages, total, acc, pair, chain, lane);
-    q_step<PACK, WC>(L, b3, b2, s + 3, stages, total, acc, pair, chain, lane);
+    q_step<PACK, WC, BRT>(L, b0, b3, s, stages, total, acc, pair, chain, lane);
+    q_step<PACK, WC, BRT>(L, b1, b0, s + 1, stages, total, acc, pair, chain, lane);
+    q_step<PACK, WC, BRT>(L, b2, b1, s + 2, stages, total, acc, pair, chain, lane);
+    q_step<PACK, WC, BRT>(L, b3, b2, s + 3, stages, total, acc, pair, chain, lane);
   }
   stage_ready<0>();  // every load has landed (the tail's too) and every wave is done with the stages
-  auto ring = [&](int i) -> StageQ & { return i == 0 ? b0 : i == 1 ? b1 : i == 2 ? b2 : b3; };
+  auto ring = [&](int i) -> StageQ<BRT> & { return i == 0 ? b0 : i == 1 ? b1 : i == 2 ? b2 : b3; };
   add_chains4(acc, (float *)&ring((stages + 1) % RING), (float *)&ring((stages + 2) % RING), pair, chain, lane);
   if (chain == 3) {
     // the groups past the fours, one at a time, after the four chains' sum (relaxed/int8.ts:40-47)
-    const StageQ &T = ring(stages % RING);
-    for (int gi = 0; gi < ng - ng4; gi++) q_group<PACK, WC>(acc, T, gi, pair, lane);
+    const StageQ<BRT> &T = ring(stages % RING);
+    for (int gi = 0; gi < ng - ng4; gi++) q_group<PACK, WC, BRT>(acc, T, gi, pair, lane);
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const int row = row0 + 64 * pair + 32 * (i >> 1) + (lane & 31);
@@ -608,16 +616,30 @@ bool gemm_supported(Kind kind) { return kind == Q8R || kind == Q6R || signs_kind
 hipError_t launch_gemm(Kind kind, const Job &job, hipStream_t s) {
   const int rows = job.r1 - job.r0;
   if (rows <= 0 || job.count <= 0) return hipSuccess;
-  dim3 grid(((rows + BR - 1) / BR) * ((job.count + BT - 1) / BT)), block(signs_kind(kind) ? NT : QNT);
+  const int token_tiles = (job.count + BT - 1) / BT;
+  dim3 grid(((rows + BR - 1) / BR) * token_tiles), block(NT);
   const bool wc = job.wc != nullptr;
+  // int8 / int6: 64-row tiles where 128-row ones would leave fewer than two blocks a compute unit
+  const bool narrow = (int64_t)((rows + BR - 1) / BR) * token_tiles < 2 * (int64_t)cu_count();
+  const dim3 grid64(((rows + 63) / 64) * token_tiles), block64(q_threads<64>()), block128(q_threads<128>());
   switch (kind) {
   case Q8R:
-    if (wc) hipLaunchKernelGGL((gemm_relaxed<8, true>), grid, block, 0, s, job);
-    else hipLaunchKernelGGL((gemm_relaxed<8, false>), grid, block, 0, s, job);
+    if (narrow) {
+      if (wc) hipLaunchKernelGGL((gemm_relaxed<8, true, 64>), grid64, block64, 0, s, job);
+      else hipLaunchKernelGGL((gemm_relaxed<8, false, 64>), grid64, block64, 0, s, job);
+    } else {
+      if (wc) hipLaunchKernelGGL((gemm_relaxed<8, true, 128>), grid, block128, 0, s, job);
+      else hipLaunchKernelGGL((gemm_relaxed<8, false, 128>), grid, block128, 0, s, job);
+    }
     break;
   case Q6R:
-    if (wc) hipLaunchKernelGGL((gemm_relaxed<6, true>), grid, block, 0, s, job);
-    else hipLaunchKernelGGL((gemm_relaxed<6, false>), grid, block, 0, s, job);
+    if (narrow) {
+      if (wc) hipLaunchKernelGGL((gemm_relaxed<6, true, 64>), grid64, block64, 0, s, job);
+      else hipLaunchKernelGGL((gemm_relaxed<6, false, 64>), grid64, block64, 0, s, job);
+    } else {
+      if (wc) hipLaunchKernelGGL((gemm_relaxed<6, true, 128>), grid, block128, 0, s, job);
+      else hipLaunchKernelGGL((gemm_relaxed<6, false, 128>), grid, block128, 0, s, job);
+    }
     break;
   case T2R:
   case T2: hipLaunchKernelGGL(gemm_ternary<false>, grid, block, 0, s, job); break;
