@@ -466,8 +466,8 @@ hipError_t launch_type(const SbBatch &b, int T, int L, size_t lds, hipStream_t s
 // then each (row, token) adds f(f(f(G_k xs_k) + f(G_{k+4} xs_{k+4})) F) (less the minimums') to its lane k in block
 // order, and ((l0 + l1) + l2) + l3 at the end (types.ts:48-57): every (row, token) the token kernel's number.
 // The four waves split the tokens and the lanes k: NT = 128, 32 tokens and all four lanes a wave; NT = 64, two token
-// halves x two pairs of lanes; NT = 32, a lane k a wave; the lanes meet in LDS at the end in that order.  The next block's bytes are loaded into registers while
-// this one is decoded and multiplied, and stored into LDS after.
+// halves x two pairs of lanes; NT = 32, a lane k a wave; the lanes meet in LDS at the end in that order.  The next
+// block's bytes are loaded into registers while this one is decoded and multiplied, and stored into LDS after.
 // ---------------------------------------------------------------------------------------------------------------
 typedef int32_t v4i_t __attribute__((ext_vector_type(4)));
 typedef int32_t v16i_t __attribute__((ext_vector_type(16)));

@@ -28,8 +28,8 @@
 //
 // A block computes a 128-row x 64-token tile.  int8 / int6: 8 waves, two a SIMD; the waves of pair p (waves 4 p ..
 // 4 p + 3) take rows 64 p .. + 63 and chain w % 4, four 32 x 32 sub-tiles each (the weights' operand read once for
-// two MFMAs, the tokens' for two slices); a launch of few tiles takes 64-row tiles of one pair (4 waves) instead.  Ternary: 16 waves; wave w takes rows 32 (w / 4) .. + 31 and chain w % 4,
-// both 32-token halves.  The operands come into LDS by direct buffer-to-LDS loads (no registers on the way), into a
+// two MFMAs, the tokens' for two slices); a launch of few tiles takes 64-row tiles of one pair (4 waves) instead.
+// Ternary: 16 waves; wave w takes rows 32 (w / 4) .. + 31 and chain w % 4, both 32-token halves.  The operands come into LDS by direct buffer-to-LDS loads (no registers on the way), into a
 // ring of 4 stage buffers: a stage is 4 groups (int8, int6) or 2 groups of 128 (ternary), and the loads of stages
 // s + 1 .. s + 3 are in flight while stage s is computed.  Every wave issues the same number of loads a stage (6 for
 // int8 / int6, 3 for ternary; some of them into a scratch area), so that one s_waitcnt vmcnt count means "my loads of
