@@ -19,8 +19,9 @@ over the step's time, with all inputs resident in HBM.  The step runs as a HIP g
 roofline: the GEMV kernel alone: a graph of only a step's products launches, replayed between HIP events, gives its
 average launch duration; traffic: the HBM bytes a launch moves, from rocprofv3's counters
 (profiles/gemv_q8r_8b_decode_traffic.md).
-Also reported: the int8 prefill GEMM (config 3's M = 2048 over one layer's matrices) in TOPS against the dense int8
-MFMA peak, the measured ceilings (hq_ceiling_read past the caches, hq_ceiling_mfma on registers), and the oracle (the
+Also reported: config 3's decode at M = 4 (four tokens a step), the int8 prefill GEMM (config 3's M = 2048 over one
+layer's matrices, corrections derived and the caller's) in TOPS against the dense int8 MFMA peak, the measured
+ceilings (hq_ceiling_read past the caches, hq_ceiling_mfma on registers), and the oracle (the
 C restatement, oracle/) on the host's cores as the CPU baseline.
 """
 import argparse
