@@ -235,6 +235,12 @@ int32_t hq_phase(const double *jobs, int32_t count, int32_t stride, void *stream
  * for llama.cpp's blocks; jobs.ts:376-379, 385-395, 421-424, 435-438) and then run as hq_phase runs them.  Every output is the number quantize_x + the kernel give. */
 int32_t hq_matmuls(const void *x, int32_t x_stride, const double *jobs, int32_t count, int32_t stride, void *stream);
 
+/* Which kernels take a job of `kind` (hq_phase's numbers), row length n and `count` tokens whose activations are
+ * frame bytes apart and their scales sframe: 1 the matrix-core tile (16 tokens or more, and every offset within a
+ * tile of 64 tokens, 128 for llama.cpp's blocks, and of 128 rows below 4 GiB), 0 the token kernel (4 tokens a
+ * launch: the same numbers), -1 a kind not run here.  Host-only: no device is touched. */
+int32_t hq_job_path(int32_t kind, int32_t n, int32_t count, int64_t frame, int64_t sframe);
+
 /* The ceilings the kernels are measured against (no counterpart on this path: the reference's CPU ceiling loops,
  * kernels/ceilings.ts:12-25 and ceilings_relaxed.ts:34-52, are its model).  hq_ceiling_read reads every byte of
  * [p, p + bytes) once (bytes a multiple of 16): time it for the achievable HBM read bandwidth of a buffer past the

@@ -23,6 +23,22 @@ std::atomic<void *> g_stream{nullptr};
 // more tokens than this take the matrix cores (fewer: the token kernel, the weights read once a 4 tokens)
 constexpr int32_t kGemmMinTokens = 16;
 
+// Which kernels take a job: 1 the matrix-core tile, 0 the token kernel (4 tokens a launch).  The tiles keep a lane's
+// offsets within a tile in 32 bits: 64 tokens of activations (frame and sframe bytes apart: 128 for the blocks' tile)
+// and 128 rows of weights, so a job whose tile would reach 4 GiB from its first byte takes the token kernel, whose
+// addresses are 64-bit.
+int32_t path_of(hq::Kind kind, const hq::Job &j) {
+  if (hq::blocks_kind(kind)) {
+    return j.count >= hq::kSbTileMin && j.frame > 0 && j.sframe > 0 && j.frame < hq::kSbTileFrameMax &&
+           j.sframe < hq::kSbTileFrameMax;
+  }
+  if (j.count < kGemmMinTokens || !hq::gemm_supported(kind)) return 0;
+  constexpr int64_t kLimit = (int64_t)1 << 32;
+  const int64_t row_bytes = hq::signs_kind(kind) ? (int64_t)(j.n >> 7) * 32 : (int64_t)(j.n >> 5) * 32;
+  const int64_t scales = hq::signs_kind(kind) ? 8 * (int64_t)(j.n >> 5) : 4 * (int64_t)(j.n >> 5);
+  return 64 * j.frame + j.n < kLimit && 64 * j.sframe + scales < kLimit && 128 * row_bytes < kLimit;
+}
+
 int32_t fail(int32_t code, const char *fmt, ...) {
   va_list ap;
   va_start(ap, fmt);
@@ -149,8 +165,7 @@ int32_t run_blocks(hq::Kind kind, const std::vector<hq::Job> &jobs, hipStream_t 
   for (const hq::Job &j : jobs) {
     if (j.r1 == j.r0 || j.count == 0) continue;
     // a prompt: the matrix-core tile (its offsets within a tile of tokens are 32-bit: frames under 16 MB)
-    if (j.count >= hq::kSbTileMin && j.frame > 0 && j.sframe > 0 && j.frame < hq::kSbTileFrameMax &&
-        j.sframe < hq::kSbTileFrameMax) {
+    if (path_of(kind, j)) {
       const int32_t st = hip_status(hq::launch_sb_tile(j, s), kind_name(kind));
       if (st) return st;
       continue;
@@ -184,7 +199,7 @@ int32_t run_jobs(hq::Kind kind, const std::vector<hq::Job> &jobs, hipStream_t s)
   std::vector<hq::Job> gemv[hq::kGemvMaxTokens + 1][2];  // by token count, by wc-ness
   for (const hq::Job &j : jobs) {
     if (j.r1 == j.r0 || j.count == 0) continue;
-    if (j.count >= kGemmMinTokens && hq::gemm_supported(kind)) {
+    if (path_of(kind, j)) {
       const int32_t st = hip_status(hq::launch_gemm(kind, j, s), kind_name(kind));
       if (st) return st;
       continue;
@@ -260,6 +275,15 @@ int32_t group_of(int32_t packing, int32_t dim) {
 extern "C" {
 
 const char *hq_version(void) { return "hq 1.0 gfx950"; }
+
+int32_t hq_job_path(int32_t kind, int32_t n, int32_t count, int64_t frame, int64_t sframe) {
+  g_error = HQ_OK;
+  if (kind < 0 || kind >= kKinds || kind_name((hq::Kind)kind)[0] == '?')
+    return fail(HQ_ERR_KIND, "hq_job_path: kind %d is not run here", kind), -1;
+  hq::Job j{};
+  j.n = n, j.count = count, j.frame = frame, j.sframe = sframe;
+  return path_of((hq::Kind)kind, j);
+}
 
 int32_t hq_init(void) {
   g_error = HQ_OK;

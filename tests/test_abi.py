@@ -142,3 +142,27 @@ def test_work_numbers_match_the_reference():
     assert jobs.PACKED["int6"].weight_bytes() == 0.875
     assert jobs.PACKED["ternary"].weight_bytes() == 0.265625
     assert jobs.PACKED["binary"].weight_bytes() == 0.140625  # (16 + 2) / 128
+
+
+def test_job_path_keeps_tile_offsets_in_32_bits(pkg):
+    """The matrix-core tiles keep a lane's offsets within a tile of 64 tokens (128 for llama.cpp's blocks) and 128
+    rows in 32 bits: a prompt whose activations are 64 MiB apart (or whose rows are 32 MiB long) takes the token
+    kernel, which gives the same numbers with 64-bit addresses."""
+    from pyodide_llm_amd import jobs
+    L = pkg.library()
+    q8r, t2r, q8, sbr = (jobs.KIND[k] for k in ("matmul_q8r", "matmul_t2r", "matmul_q8", "matmul_sbr"))
+    n = 4096
+    frame = n + n // 8
+    assert L.hq_job_path(q8r, n, 2048, frame, frame) == 1
+    assert L.hq_job_path(q8r, n, 15, frame, frame) == 0  # under 16 tokens: the token kernel
+    assert L.hq_job_path(q8, n, 2048, frame, frame) == 0  # no matrix-core tile for the plain form
+    big = 1 << 26  # 64 tokens x 64 MiB reach 4 GiB
+    assert L.hq_job_path(q8r, n, 2048, big - 4096, big - 4096) == 1
+    assert L.hq_job_path(q8r, n, 2048, big, frame) == 0
+    assert L.hq_job_path(q8r, n, 2048, frame, big) == 0
+    assert L.hq_job_path(t2r, n, 64, big, big) == 0
+    assert L.hq_job_path(t2r, n, 64, frame, frame) == 1
+    assert L.hq_job_path(q8r, 1 << 25, 64, 1 << 25, 1 << 25) == 0  # 128 rows of 32 MiB
+    assert L.hq_job_path(sbr, n, 64, 1 << 24, 4096) == 0  # the blocks' tile: frames under 16 MiB
+    assert L.hq_job_path(sbr, n, 64, (1 << 24) - 16, 4096) == 1
+    assert L.hq_job_path(3, n, 64, frame, frame) == -1  # attention is not a kind run here
