@@ -19,11 +19,9 @@ INCLUDE = os.path.join(ROOT, "include")
 OBJ = os.path.join(HERE, "_build")
 LIBRARY = os.path.join(HERE, "libhq.so")
 SOURCES = ["quantize.hip", "gemv.hip", "gemm.hip", "blocks.hip", "columns.hip", "ceilings.hip", "abi.cpp"]
-# gemm.hip issues its direct-to-LDS loads as the instructions themselves, which set M0 (a register the compiler
-# reserves and does not use in those kernels): its warning about that clobber is expected
 # blocks.hip's prompt tile keeps its matrix-core results in ordinary VGPRs (no copies out of AGPRs: it has registers
 # to spare and reads every result on the VALU)
-EXTRA = {"gemm.hip": ["-Wno-inline-asm"], "blocks.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+EXTRA = {"blocks.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 FLAGS = [

@@ -13,34 +13,41 @@
 // Float32 order: every (row, token) is the token kernel's number to the bit.  The reference's lane k adds groups
 // 4 j + k (int8, int6) or part k of every group (ternary), in order, and the four lanes are added
 // ((l0 + l1) + l2) + l3 at the end (math.ts:7-9), then (int8, int6) the groups past the last four one at a time
-// (relaxed/int8.ts:40-47).  Here a wave IS a lane k of the reference: the 4 waves of one 32-row slice of the tile take
+// (relaxed/int8.ts:40-47).  Here a wave IS a lane k of the reference: the 4 waves of one slice of the tile take
 // chain k = 0..3 each, adding their groups / parts in order into registers, and at the end add their sums through LDS
 // in that order.  Each term is f(f(C) * f(ws * xs)) (int8, int6) or f(f(f(C) * xs) * d) (ternary), rounded as the
 // reference rounds it (-ffp-contract=off).
 //
-// The scales' product of int8 / int6, f(ws * xs) for every (row, token), is an outer product: four
-// v_mfma_f32_4x4x1_16b_f32 (sixteen 4 x 4 outer products each, K = 1) give a 32 x 32 sub-tile's, each product rounded
-// once as v_mul_f32 rounds it (subnormals included), on the matrix core.  Roofline: per output element and group the
-// epilogue is then 3 VALU operations (convert, multiply, add; ternary 4: f(f(C * xs) * d) has no such product)
-// against 32 MACs on the matrix core.  Without packed float32 instructions (this build turns them off) MI355X's VALU
-// does 64 float32 lanes a clock a CU (4 SIMDs x 16) against 4096 int8 MACs, so the epilogue, not the MFMA, bounds
-// this kernel: at best 32 / (3 x 4096 / 64) = 16.7 % of dense int8 peak, 833 TOP/s (12.5 % for ternary).
+// The scales' product of int8 / int6, f(ws * xs) for every (row, token), is an outer product on the matrix core: one
+// v_mfma_f32_32x32x1_2b_f32 (two 32 x 32 blocks, K = 1) gives a 32-row slice's products with both 32-token halves,
+// each rounded once as v_mul_f32 rounds it (subnormals, zeros, infinities and NaN included), in the same lane layout
+// as the integer MFMA's result.
 //
-// A block computes a 128-row x 64-token tile.  int8 / int6: 8 waves, two a SIMD; the waves of pair p (waves 4 p ..
-// 4 p + 3) take rows 64 p .. + 63 and chain w % 4, four 32 x 32 sub-tiles each (the weights' operand read once for
-// two MFMAs, the tokens' for two slices); a launch of few tiles takes 64-row tiles of one pair (4 waves) instead.
-// Ternary: 16 waves; wave w takes rows 32 (w / 4) .. + 31 and chain w % 4, both 32-token halves.  The operands come into LDS by direct buffer-to-LDS loads (no registers on the way), into a
-// ring of 4 stage buffers: a stage is 4 groups (int8, int6) or 2 groups of 128 (ternary), and the loads of stages
-// s + 1 .. s + 3 are in flight while stage s is computed.  Every wave issues the same number of loads a stage (6 for
-// int8 / int6, 3 for ternary; some of them into a scratch area), so that one s_waitcnt vmcnt count means "my loads of
-// stage s have landed"; a bare s_barrier then makes them everyone's.  The 16-byte chunks of a row are stored XOR-
-// swizzled so that the MFMA operand reads (32 rows or tokens, one chunk each) spread over the LDS banks.  Blocks are
-// ordered so that the blocks one XCD runs at a time share their rows and tokens in that XCD's L2.
+// Roofline.  The dense int8 MFMA peak is 5.0 POPS (32 cycles a v_mfma_i32_32x32x32_i8, 32768 MACs, a SIMD), but the
+// bit-exact epilogue is 3 VALU operations per (row, token, group): convert, multiply, add (ternary 4), which this
+// build issues unpacked (packed float32 instructions are off).  Measured on MI355X: two or more waves a SIMD issue a
+// wave's VALU instruction every ~2.2 cycles (one wave alone every ~4.4), and a SIMD whose VALU is busy that way does
+// not run MFMAs beside it, so a 32 x 32 sub-tile's group costs ~48 x 2.2 cycles of VALU plus 32 (integer MFMA) + 32
+// (half a 32x32x1_2b) + 16 (half a correction MFMA) of the matrix core: ~185 cycles for 65536 operations, about a
+// third of the int8 peak (0.83 POPS at 2.3 GHz) — the bound this kernel is measured against.
 //
-// Measured on MI355X (8B gate+up, 2048 tokens): a stage takes about twice the sum of its MFMA, VALU and LDS time;
-// the rest is waiting for the stage's loads, and the parts add up rather than overlap (one wave issues VALU at about
-// half a SIMD's rate; the VALU and the matrix core run side by side only part of the time), so the kernel sits
-// near 320 int8 TOP/s, well under the bound above.
+// Tiles.  A block computes a 128-row x 64-token tile.  int8 / int6: 8 waves, two a SIMD; the waves of pair p (waves
+// 4 p .. 4 p + 3) take rows 64 p .. + 63 and chain w % 4, four 32 x 32 sub-tiles each (two row slices x two token
+// halves: the weights' operand read once for two MFMAs, the tokens' for two slices); a launch of few tiles takes
+// 64-row tiles of one pair (4 waves, two blocks a CU) instead.  Ternary: 16 waves; wave w takes rows 32 (w / 4) .. + 31
+// and chain w % 4, both 32-token halves.
+//
+// Pipeline (int8 / int6).  A wave issues each sub-tile's MFMAs one sub-tile ahead of its epilogue, so the matrix core
+// works on the next sub-tile while the VALU folds this one, and a stage's last epilogue runs beside the first MFMAs
+// of the next stage.  Its operands for stage s + 1 are read from LDS in the middle of stage s, right after the
+// block's barrier that makes stage s + 1's loads everyone's.  The operands go from HBM / L2 straight into LDS with
+// buffer-to-LDS loads into a ring of 4 stage buffers (a stage: 4 groups of int8 / int6, 2 groups of 128 of ternary):
+// at the barrier for stage s + 1 the loads of stage s + 4 go into the buffer stage s's operands were read from.  Every
+// wave issues the same number of loads a stage (some into a scratch area of LDS), so one s_waitcnt vmcnt count says
+// "my loads of stage s + 1 have landed".  A load past the tile's last row or token, or past the last group, reads
+// zeros (buffer bounds; such results are never stored).  The 16-byte chunks of a row are stored XOR-swizzled so that
+// the MFMA operand reads (32 rows or tokens, one chunk each) spread over the LDS banks, and tiles are ordered so that
+// the blocks one XCD runs at a time share rows and tokens in that XCD's L2.
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -51,6 +58,7 @@ namespace {
 typedef int32_t v4i __attribute__((ext_vector_type(4)));
 typedef int32_t v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v32f __attribute__((ext_vector_type(32)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 constexpr int BR = 128, BT = 64;  // block tile: rows x tokens
@@ -63,31 +71,31 @@ HQ_DEV v16i zero16i() {
   for (int r = 0; r < 16; r++) z[r] = 0;
   return z;
 }
-HQ_DEV v4f zero4f() { return (v4f){0.0f, 0.0f, 0.0f, 0.0f}; }
+HQ_DEV v32f zero32f() {
+  v32f z;
+#pragma unroll
+  for (int r = 0; r < 32; r++) z[r] = 0.0f;
+  return z;
+}
 
 // ---- loads -----------------------------------------------------------------------------------------------------
 // A block's rows, tokens and scales are each one buffer resource (common.hpp's resource(): base and size in scalar
 // registers): a thread's offsets are set once, a stage moves them by a scalar offset, and a load past the size reads
 // nothing and returns zeros (the tiles past the last row or token, the groups past the last one: their results are
 // never stored).
-// direct loads into LDS: lane l's `size` bytes land at dst + size * l (dst the same in the whole wave, in M0; 2-byte
-// loads land zero-extended in 4-byte slots).  Written as the instructions themselves: the compiler, which tracks
-// such loads only a few at a time, would otherwise wait for every one in flight before each LDS read; here the
-// waits are stage_ready's alone (which only these loads need: the loops issue no other vector memory operation).
-HQ_DEV uint32_t lds_address(void *p) {
-  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)p);
-}
+// Direct loads into LDS: lane l's `size` bytes land at dst + size * l (dst the same in the whole wave; 2-byte loads
+// land zero-extended in 4-byte slots).  The stage buffers are distinct __shared__ objects, so the compiler can tell
+// that a load into one buffer does not write the one being read, and waits for these loads only where the stage
+// barriers say so.
+#define HQ_LDS(p) ((__attribute__((address_space(3))) void *)(p))
 HQ_DEV void dma16(__amdgpu_buffer_rsrc_t r, void *dst, uint32_t vo, uint32_t so) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-               :: "s"(lds_address(dst)), "v"(vo), "s"(r), "s"(so) : "memory", "m0");
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, HQ_LDS(dst), 16, vo, so, 0, 0);
 }
 HQ_DEV void dma4(__amdgpu_buffer_rsrc_t r, void *dst, uint32_t vo, uint32_t so) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds"
-               :: "s"(lds_address(dst)), "v"(vo), "s"(r), "s"(so) : "memory", "m0");
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, HQ_LDS(dst), 4, vo, so, 0, 0);
 }
 HQ_DEV void dma2(__amdgpu_buffer_rsrc_t r, void *dst, uint32_t vo, uint32_t so) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_ushort %1, %2, %3 offen lds"
-               :: "s"(lds_address(dst)), "v"(vo), "s"(r), "s"(so) : "memory", "m0");
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, HQ_LDS(dst), 2, vo, so, 0, 0);
 }
 
 // the stage's loads have landed: wait until at most N of this wave's loads are outstanding (and its LDS reads are
@@ -100,11 +108,10 @@ HQ_DEV void stage_ready() {
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 }
-// stage s of `total` loaded stages, N loads a wave a stage: the loads issued after its own are those of the next
-// min(AHEAD - 1, ...) stages
+// stage s of `total` loaded stages is ready, N loads a wave a stage, the loads of stages up to s + `ahead` issued
 template <int N>
-HQ_DEV void wait_for(int s, int total) {
-  const int later = min(AHEAD - 1, total - 1 - s);
+HQ_DEV void wait_for(int s, int total, int ahead) {
+  const int later = min(ahead, total - 1 - s);
   if (later >= 2) stage_ready<2 * N>();
   else if (later == 1) stage_ready<N>();
   else stage_ready<0>();
@@ -132,21 +139,22 @@ HQ_DEV void tile_of(int b, int nb, int nrb, int &rb, int &tb) {
 
 // the 4 chains of a slice added in LDS, ((a0 + a1) + a2) + a3, for both token halves: wave k adds its sums to what
 // waves 0..k-1 left (the 16 values of a lane are the same (row, token)s in the four waves of a slice); the sums end
-// in chain 3's waves.  p0, p1: 4 x 64 x 16 floats each that nothing else uses meanwhile
+// in chain 3's waves.  p0, p1: 4 x 16 x 64 floats each that nothing else uses meanwhile, value r of a lane at
+// [r][lane] (consecutive lanes, consecutive banks)
 HQ_DEV void add_chains(float acc0[16], float acc1[16], float *p0, float *p1, int slice, int chain, int lane) {
-  float *q0 = p0 + (slice * 64 + lane) * 16, *q1 = p1 + (slice * 64 + lane) * 16;
+  float *q0 = p0 + slice * 16 * 64 + lane, *q1 = p1 + slice * 16 * 64 + lane;
   for (int k = 0; k < 4; k++) {
     __syncthreads();
     if (chain == k) {
 #pragma unroll
       for (int r = 0; r < 16; r++) {
         if (k > 0) {
-          acc0[r] = fadd(q0[r], acc0[r]);
-          acc1[r] = fadd(q1[r], acc1[r]);
+          acc0[r] = fadd(q0[r * 64], acc0[r]);
+          acc1[r] = fadd(q1[r * 64], acc1[r]);
         }
         if (k < 3) {
-          q0[r] = acc0[r];
-          q1[r] = acc1[r];
+          q0[r * 64] = acc0[r];
+          q1[r * 64] = acc1[r];
         }
       }
     }
@@ -155,26 +163,30 @@ HQ_DEV void add_chains(float acc0[16], float acc1[16], float *p0, float *p1, int
 
 // ---------------------------------------------------------------------------------------------------------------
 // int8 / int6 weights, relaxed activations (matmul_q8r_tile, matmul_q6r)
-// A block is 8 waves, two waves a SIMD with up to 256 registers each: wave w takes chain w % 4 of rows
-// 64 (w / 4) .. + 63 (two 32-row slices) for both 32-token halves, four 32 x 32 sub-tiles, so that the MFMAs of one
-// sub-tile run while the epilogue of the one before it does.
-// MFMA A = weights (m = row), B = activations (n = token): lane l holds token l % 32 of its half and rows
-// 8 (r / 4) + 4 (l / 32) + r % 4 of its slice (r = 0..15); K half l / 32 is bytes 16 (l / 32) .. + 15 of the group.
+// MFMA A = activations (m = token), B = weights (n = row): lane l holds row l % 32 of its slice and tokens
+// 8 (r / 4) + 4 (l / 32) + r % 4 of its half (register r = 0..15); K half l / 32 is bytes 16 (l / 32) .. + 15 of the
+// group.  The scales' outer product takes A = the scale of token l of the tile and B = the scale of row l % 32 of the
+// slice: its register r (r + 16) is the same (token, row) of the first (second) token half.
 // ---------------------------------------------------------------------------------------------------------------
-constexpr int QG = 4;  // groups a stage
-// the rows of a block's tile (BRT 128: 8 waves; 64, for launches of few tiles: 4 waves, twice the blocks), its
-// threads and each wave's loads a stage
-template <int BRT> constexpr int q_threads() { return 4 * BRT; }
-template <int BRT> constexpr int q_loads() { return BRT == 128 ? 6 : 7; }
+constexpr int QG = 4;   // groups a stage
+constexpr int QR = 64;  // rows of a block's tile: 4 waves, one chain each, two row slices x two token halves a wave
+constexpr int QT = 256; // threads a block
 
-template <int BRT>
 struct alignas(16) StageQ {
-  char w[BRT * 128];    // int8: BRT rows x 4 groups x 32 bytes, chunks swizzled; int6: BRT rows x 4 x 24 bytes
-  char x[BT * 128];     // 64 tokens x 4 groups x 32 bytes, chunks swizzled
-  float ws[QG][BRT];    // the rows' scales, group-major
-  int32_t wc[QG][BRT];  // the rows' corrections (with the caller's wc), group-major
-  float xs[QG][BT];     // the tokens' scales, group-major; in each 32-token half token 8 m + 4 h + i at 16 h + 4 i + m
+  char w[QR * 128];    // int8: 64 rows x 4 groups x 32 bytes, chunks swizzled; int6: 64 rows x 4 x 24 bytes
+  char x[BT * 128];    // 64 tokens x 4 groups x 32 bytes, chunks swizzled
+  float ws[QR][QG];    // the rows' scales of the stage's groups
+  int32_t wc[QR][QG];  // the rows' corrections (with the caller's wc)
+  float xs[BT][QG];    // the tokens' scales
 };
+
+// A stage's scales are 16 contiguous bytes of a row (or token).  Where every such run is 16-byte aligned (WIDE: the
+// group count a multiple of 4 and the bases and token stride 16-byte aligned) one lane loads a row's 16 bytes, 64
+// rows a load; otherwise four lanes load a row's four scales, 16 rows a load, group g of row r stored at
+// g ^ gswz(r) so that 32 rows 16 bytes apart reading one group hit 32 different banks.  Loads into LDS cost about
+// the same whatever their width, so the wide form's fewer loads are what count.
+HQ_DEV int gswz(int r) { return (r >> 3) & 3; }
+template <bool WIDE> HQ_DEV int sslot(int r, int g) { return WIDE ? g : g ^ gswz(r); }
 
 // K half kh (values 16 kh .. + 15) of an int6 group (24 bytes at p, kernels/six.ts:16-31): value j's low nibble is
 // in byte j % 16 (low half for j < 16, high half after), its top two bits at bits 2 (j / 8) of byte 16 + j % 8;
@@ -194,19 +206,24 @@ HQ_DEV v4i six_half(const char *p, int kh) {
   return v;
 }
 
-// a block's loads of int8 / int6 stages: wave w's q_loads a stage and their offsets
-template <int PACK, bool WC, int BRT>
+// A block's loads of a stage, as 1 KB pieces (256 B for the narrow scale loads) dealt to the four waves in turn:
+// the weights' pieces (8 of int8, 6 of int6), the activations' (8), then the scales' (wide: the rows', the
+// corrections' with wc, the tokens'; narrow: 4 of each).  Wave w issues pieces w, w + 4, ..., so its loads a stage
+// are count(w); no load is issued that is not needed.
+template <int PACK, bool WC, bool WIDE>
 struct Relaxed {
-  static constexpr int GB = PACK == 8 ? 32 : 24;  // bytes of a group of weights
-  static constexpr int NW = BRT / 16;             // waves
-  static constexpr int XPW = 8 / NW;              // 1 KB pieces of the activations a wave
-  static constexpr int SPG = BRT / 64;            // 64-row pieces of a group's scales
+  static constexpr int GB = PACK == 8 ? 32 : 24;    // bytes of a group of weights
+  static constexpr int NWP = PACK == 8 ? 8 : 6;     // the weights' pieces
+  static constexpr int NSK = WC ? 3 : 2;            // kinds of scale pieces: ws, (wc), xs
+  static constexpr int SPK = WIDE ? 1 : 4;          // pieces of each
+  static constexpr int P = NWP + 8 + NSK * SPK;     // pieces a stage
+  static constexpr int PW = (P + 3) / 4;            // the most pieces of a wave
+  static HQ_DEV int count(int w) { return P / 4 + (w < P % 4 ? 1 : 0); }
   __amdgpu_buffer_rsrc_t rw, rx, rws, rwc, rxs;
-  uint32_t oa[2], ob[XPW], oc, oe;
+  uint32_t off[PW];
   int wave;
-  char *junk;
 
-  HQ_DEV Relaxed(const Job &J, int row0, int tok0, int M, int w, char *junk_area) : wave(w), junk(junk_area) {
+  HQ_DEV Relaxed(const Job &J, int row0, int tok0, int M, int w) : wave(w) {
     const int lane = threadIdx.x & 63, ng = J.n >> 5;
     const int64_t rb = (int64_t)ng * GB;
     rw = resource(J.wq + row0 * rb, (J.r1 - row0) * rb);
@@ -214,123 +231,249 @@ struct Relaxed {
     rwc = resource(J.wc + (int64_t)row0 * ng * 4, WC ? (int64_t)(J.r1 - row0) * ng * 4 : 0);
     rx = resource(J.xq + tok0 * J.frame, (M - 1 - tok0) * J.frame + J.n);
     rxs = resource(J.xs + tok0 * J.sframe, (M - 1 - tok0) * J.sframe + 4 * ng);
-    // loads a0, a1: 1 KB pieces 2 w and 2 w + 1 of the stage's weights.  int8: piece c is rows 8 c .. + 7, lane l
-    // row 8 c + l / 8, slot l % 8 holding chunk (l % 8) ^ swz(row); int6: 16-byte piece 64 c + l of 128 rows x 96
-    // bytes (pieces 0..11)
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-      const int c = 2 * w + i;
-      if (PACK == 8) {
-        const int row = 8 * c + (lane >> 3), ch = (lane & 7) ^ swz(row);
-        oa[i] = (uint32_t)(row * rb + (ch >> 1) * 32 + (ch & 1) * 16);
-      } else {
-        const int q = 64 * c + lane;
-        oa[i] = (uint32_t)((q / 6) * rb + (q % 6) * 16);
+    for (int k = 0; k < PW; k++) {
+      const int p = w + 4 * k;
+      uint32_t o = 0;
+      if (p < NWP) {
+        // int8: rows 8 p .. + 7, lane l row 8 p + l / 8, slot l % 8 holding chunk (l % 8) ^ swz(row); int6: 16-byte
+        // piece 64 p + l of 64 rows x 96 bytes
+        if (PACK == 8) {
+          const int row = 8 * p + (lane >> 3), ch = (lane & 7) ^ swz(row);
+          o = (uint32_t)(row * rb + (ch >> 1) * 32 + (ch & 1) * 16);
+        } else {
+          const int q = 64 * p + lane;
+          o = (uint32_t)((q / 6) * rb + (q % 6) * 16);
+        }
+      } else if (p < NWP + 8) {
+        // the activations of tokens 8 c .. + 7, as the weights
+        const int c = p - NWP, tok = 8 * c + (lane >> 3), ch = (lane & 7) ^ swz(tok);
+        o = (uint32_t)(tok * J.frame + (ch >> 1) * 32 + (ch & 1) * 16);
+      } else if (p < P) {
+        const int q = p - NWP - 8, kind = q / SPK, i = q % SPK;  // kind 0 ws, 1 wc (or xs without wc), 2 xs
+        const bool tokens = kind == NSK - 1;
+        if (WIDE) {  // lane l: row (or token) l, its 16 bytes
+          o = tokens ? (uint32_t)(lane * J.sframe) : (uint32_t)(lane * ng * 4);
+        } else {     // lane l: row 16 i + l / 4, group (l % 4) ^ gswz(row)
+          const int r = 16 * i + (lane >> 2), g = (lane & 3) ^ gswz(r);
+          o = tokens ? (uint32_t)(r * J.sframe + g * 4) : (uint32_t)((r * ng + g) * 4);
+        }
       }
-    }
-    // load b: the activations of tokens 8 c .. + 7 (pieces c = XPW w ..), as the weights
-#pragma unroll
-    for (int i = 0; i < XPW; i++) {
-      const int tok = 8 * (XPW * w + i) + (lane >> 3), ch = (lane & 7) ^ swz(tok);
-      ob[i] = (uint32_t)(tok * J.frame + (ch >> 1) * 32 + (ch & 1) * 16);
-    }
-    // loads c, d: the rows' scales and corrections of group w / SPG, rows 64 (w % SPG) + l
-    oc = (uint32_t)(((64 * (w % SPG) + lane) * ng + w / SPG) * 4);
-    // load e: waves 0..3 the tokens' scales of group w, the tokens of each 32-token half reordered (entry 16 h + 4 i
-    // + m is token 8 m + 4 h + i), so that one 16-byte read gives a lane the four tokens of its 4 x 4 outer products
-    {
-      const int q = lane & 31;
-      const int tok = 32 * (lane >> 5) + 8 * (q & 3) + 4 * (q >> 4) + ((q >> 2) & 3);
-      oe = (uint32_t)(tok * J.sframe + (w & 3) * 4);
+      off[k] = o;
     }
   }
 
-  // the q_loads of stage s (groups 4 s .. 4 s + 3) into S
-  HQ_DEV void load(StageQ<BRT> &S, int s) {
-    const int w = wave;
+  // wave w's loads of stage s (groups 4 s .. 4 s + 3) into S
+  HQ_DEV void load(StageQ &S, int s) {
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-      if (PACK == 8 || 2 * w + i < 12 * BRT / 128) dma16(rw, S.w + (2 * w + i) * 1024, oa[i], s * QG * GB);
-      else dma16(rxs, junk, 0, 0);
+    for (int k = 0; k < PW; k++) {
+      const int p = wave + 4 * k;
+      if (p < NWP) {
+        dma16(rw, S.w + p * 1024, off[k], s * QG * GB);
+      } else if (p < NWP + 8) {
+        dma16(rx, S.x + (p - NWP) * 1024, off[k], s * QG * 32);
+      } else if (p < P) {
+        const int q = p - NWP - 8, kind = q / SPK, i = q % SPK;
+        const bool tokens = kind == NSK - 1;
+        char *dst = tokens ? (char *)&S.xs[16 * i][0] : (kind == 0 || !WC) ? (char *)&S.ws[16 * i][0]
+                                                                           : (char *)&S.wc[16 * i][0];
+        const __amdgpu_buffer_rsrc_t r = tokens ? rxs : (kind == 0 || !WC) ? rws : rwc;
+        if (WIDE) dma16(r, dst, off[k], s * QG * 4);
+        else dma4(r, dst, off[k], s * QG * 4);
+      }
     }
-#pragma unroll
-    for (int i = 0; i < XPW; i++) dma16(rx, S.x + (XPW * w + i) * 1024, ob[i], s * QG * 32);
-    dma4(rws, &S.ws[w / SPG][64 * (w % SPG)], oc, s * QG * 4);
-    if (WC) dma4(rwc, &S.wc[w / SPG][64 * (w % SPG)], oc, s * QG * 4);
-    else dma4(rxs, junk, 0, 0);
-    if (w < 4) dma4(rxs, &S.xs[w][0], oe, s * QG * 4);
-    else dma4(rxs, junk, 0, 0);
   }
 };
 
-// group gi of stage S into the chain of the lane's four sub-tiles (slices 2 pair, 2 pair + 1 x both token halves,
-// acc[2 slice + half]): the exact integers (MFMA, from the corrections) and the scales' products (outer-product
-// MFMAs), each term f(f(C) * f(ws * xs)) (relaxed/int8.ts:26-39).  MFMA A = activations (m = token), B = weights
-// (n = row): lane l holds row l % 32 of its slice and tokens 8 (r / 4) + 4 (l / 32) + r % 4 of its half, so a lane's
-// correction and row scale are one value each.
-template <int PACK, bool WC, int BRT>
-HQ_DEV void q_group(float acc[4][16], const StageQ<BRT> &S, int gi, int pair, int lane) {
+// stage s's loads have landed everywhere: this wave's own, with those of the two stages after it still in flight,
+// then the block's barrier
+template <int PACK, bool WC, bool WIDE>
+HQ_DEV void q_ready(int wave) {
+  using L = Relaxed<PACK, WC, WIDE>;
+  if (wave < L::P % 4) stage_ready<2 * (L::P / 4 + 1)>();
+  else stage_ready<2 * (L::P / 4)>();
+}
+
+// a wave's operands of one group gi of a stage: the activations of both token halves, the weights of both row slices
+// (int6 widened to int8), the scale of token `lane` and of the slices' rows, the slices' corrections (with wc)
+struct OpsQ {
+  v4i X[2], W[2];
+  float xs, ws[2];
+  int32_t wc[2];
+};
+
+// the LDS address of p (a __shared__ object's byte)
+HQ_DEV uint32_t lds_addr(const void *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)p;
+}
+
+// The main loop's reads of a stage's operands are one block of ds_read instructions and one wait for them.  Read as
+// C++ loads, the compiler would also wait for every buffer-to-LDS load still in flight before them (it cannot tell
+// that those write other stage buffers once more than a few are in flight), which would leave the loads no time to
+// land ahead of their stage; here the stage barrier alone says when a buffer is ready.
+template <int PACK, bool WC>
+HQ_DEV void ds_ops(OpsQ &o, uint2 six[2][3], const uint32_t ax[2], const uint32_t aw[2], uint32_t axs,
+                   const uint32_t aws[2], const uint32_t awc[2]) {
+  if (PACK == 8 && WC) {
+    asm volatile(
+        "ds_read_b128 %0, %9\n\tds_read_b128 %1, %10\n\tds_read_b128 %2, %11\n\tds_read_b128 %3, %12\n\t"
+        "ds_read_b32 %4, %13\n\tds_read_b32 %5, %14\n\tds_read_b32 %6, %15\n\tds_read_b32 %7, %16\n\t"
+        "ds_read_b32 %8, %17\n\ts_waitcnt lgkmcnt(0)"
+        : "=&v"(o.X[0]), "=&v"(o.X[1]), "=&v"(o.W[0]), "=&v"(o.W[1]), "=&v"(o.xs), "=&v"(o.ws[0]), "=&v"(o.ws[1]),
+          "=&v"(o.wc[0]), "=&v"(o.wc[1])
+        : "v"(ax[0]), "v"(ax[1]), "v"(aw[0]), "v"(aw[1]), "v"(axs), "v"(aws[0]), "v"(aws[1]), "v"(awc[0]),
+          "v"(awc[1])
+        : "memory");
+  } else if (PACK == 8) {
+    asm volatile(
+        "ds_read_b128 %0, %7\n\tds_read_b128 %1, %8\n\tds_read_b128 %2, %9\n\tds_read_b128 %3, %10\n\t"
+        "ds_read_b32 %4, %11\n\tds_read_b32 %5, %12\n\tds_read_b32 %6, %13\n\ts_waitcnt lgkmcnt(0)"
+        : "=&v"(o.X[0]), "=&v"(o.X[1]), "=&v"(o.W[0]), "=&v"(o.W[1]), "=&v"(o.xs), "=&v"(o.ws[0]), "=&v"(o.ws[1])
+        : "v"(ax[0]), "v"(ax[1]), "v"(aw[0]), "v"(aw[1]), "v"(axs), "v"(aws[0]), "v"(aws[1])
+        : "memory");
+    o.wc[0] = o.wc[1] = 0;
+  } else {
+    // int6: a slice's group is three 8-byte pieces (the low nibbles, then the top bits) at aw, + 8, + 16
+    asm volatile(
+        "ds_read_b128 %0, %11\n\tds_read_b128 %1, %12\n\t"
+        "ds_read_b64 %2, %13\n\tds_read_b64 %3, %13 offset:8\n\tds_read_b64 %4, %13 offset:16\n\t"
+        "ds_read_b64 %5, %14\n\tds_read_b64 %6, %14 offset:8\n\tds_read_b64 %7, %14 offset:16\n\t"
+        "ds_read_b32 %8, %15\n\tds_read_b32 %9, %16\n\tds_read_b32 %10, %17\n\ts_waitcnt lgkmcnt(0)"
+        : "=&v"(o.X[0]), "=&v"(o.X[1]), "=&v"(six[0][0]), "=&v"(six[0][1]), "=&v"(six[0][2]), "=&v"(six[1][0]),
+          "=&v"(six[1][1]), "=&v"(six[1][2]), "=&v"(o.xs), "=&v"(o.ws[0]), "=&v"(o.ws[1])
+        : "v"(ax[0]), "v"(ax[1]), "v"(aw[0]), "v"(aw[1]), "v"(axs), "v"(aws[0]), "v"(aws[1])
+        : "memory");
+    if (WC) {
+      asm volatile("ds_read_b32 %0, %2\n\tds_read_b32 %1, %3\n\ts_waitcnt lgkmcnt(0)"
+                   : "=&v"(o.wc[0]), "=&v"(o.wc[1]) : "v"(awc[0]), "v"(awc[1]) : "memory");
+    } else {
+      o.wc[0] = o.wc[1] = 0;
+    }
+  }
+}
+
+// K half kh of an int6 group from its three 8-byte pieces (six_half's arithmetic on registers)
+HQ_DEV v4i six_regs(const uint2 p[3], int kh) {
+  const uint32_t lo[4] = {p[0].x, p[0].y, p[1].x, p[1].y};
+  const uint32_t top[2] = {p[2].x, p[2].y};
+  const int sl = 4 * kh;
+  v4i v;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint32_t nib = ((lo[i] >> sl) & 0x0f0f0f0fu) << 2;
+    const uint32_t t = top[i & 1] << ((i < 2 ? 6 : 4) - sl);
+    v[i] = (int32_t)((t & 0xc0c0c0c0u) | nib);
+  }
+  return v;
+}
+
+// a wave's operands of group gi of stage S (ds_ops' reads)
+template <int PACK, bool WC, bool WIDE>
+HQ_DEV OpsQ read_ops(const StageQ &S, int gi, int lane) {
+  OpsQ o;
+  uint2 six[2][3];
   const int kh = lane >> 5, l32 = lane & 31;
-  v4i X[2];
-  float xv[2][4];
+  uint32_t ax[2], aw[2], aws[2], awc[2];
 #pragma unroll
   for (int h = 0; h < 2; h++) {
     const int t = l32 + 32 * h;
-    X[h] = *(const v4i *)(S.x + t * 128 + ((2 * gi + kh) ^ swz(t)) * 16);
-    // the scales of tokens 8 m + 4 kh + lane % 4 (m = 0..3) of the half
-    const float4 v = *(const float4 *)&S.xs[gi][32 * h + 16 * kh + 4 * (lane & 3)];
-    xv[h][0] = v.x; xv[h][1] = v.y; xv[h][2] = v.z; xv[h][3] = v.w;
+    ax[h] = lds_addr(S.x + t * 128 + ((2 * gi + kh) ^ swz(t)) * 16);
   }
 #pragma unroll
   for (int sp = 0; sp < 2; sp++) {
-    const int row = 64 * pair + 32 * sp + l32;
-    v4i W;
-    if (PACK == 8) W = *(const v4i *)(S.w + row * 128 + ((2 * gi + kh) ^ swz(row)) * 16);
-    else W = six_half(S.w + row * 96 + gi * 24, kh);
-    v16i cin;
-    if (WC) {  // the caller's correction of the lane's row
-      const int32_t c = S.wc[gi][row];
-#pragma unroll
-      for (int r = 0; r < 16; r++) cin[r] = c;
-    } else {  // -64 sum(w) of the row: 32 bytes of -64 against the weights
-      const v4i m64 = {(int32_t)0xc0c0c0c0, (int32_t)0xc0c0c0c0, (int32_t)0xc0c0c0c0, (int32_t)0xc0c0c0c0};
-      cin = __builtin_amdgcn_mfma_i32_32x32x32_i8(m64, W, zero16i(), 0, 0, 0);
-    }
-    const float wsv = S.ws[gi][row];
-#pragma unroll
-    for (int h = 0; h < 2; h++) {
-      const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(X[h], W, cin, 0, 0, 0);
-      // f(xs * ws) of the sub-tile: v_mfma_f32_4x4x1_16b_f32 gives lane l, register i the product of lane
-      // 4 (l / 4) + i's A and lane l's B, so A = the scale of token 8 m + 4 kh + lane % 4 and B = the row's scale
-      // give registers 4 m .. 4 m + 3 the tokens 8 m + 4 kh + i of the i8 MFMA's layout, one product each
-      v16f sc;
-#pragma unroll
-      for (int m = 0; m < 4; m++) {
-        const v4f d = __builtin_amdgcn_mfma_f32_4x4x1f32(xv[h][m], wsv, zero4f(), 0, 0, 0);
-        sc[4 * m] = d[0]; sc[4 * m + 1] = d[1]; sc[4 * m + 2] = d[2]; sc[4 * m + 3] = d[3];
-      }
-      float *a = acc[2 * sp + h];
-#pragma unroll
-      for (int r = 0; r < 16; r++) a[r] = fadd(a[r], fmul((float)c[r], sc[r]));
-    }
+    const int row = 32 * sp + l32;
+    aw[sp] = PACK == 8 ? lds_addr(S.w + row * 128 + ((2 * gi + kh) ^ swz(row)) * 16) : lds_addr(S.w + row * 96 + gi * 24);
+    aws[sp] = lds_addr(&S.ws[row][sslot<WIDE>(row, gi)]);
+    awc[sp] = lds_addr(&S.wc[row][sslot<WIDE>(row, gi)]);
   }
+  ds_ops<PACK, WC>(o, six, ax, aw, lds_addr(&S.xs[lane][sslot<WIDE>(lane, gi)]), aws, awc);
+  if (PACK == 6) {
+    o.W[0] = six_regs(six[0], kh);
+    o.W[1] = six_regs(six[1], kh);
+  }
+  return o;
 }
 
-// stage s in `cur`, the loads of stage s + AHEAD into `next` (the buffer of stage s - 1)
-template <int PACK, bool WC, int BRT>
-HQ_DEV void q_step(Relaxed<PACK, WC, BRT> &L, const StageQ<BRT> &cur, StageQ<BRT> &next, int s, int stages,
-                   int total, float acc[4][16], int pair, int chain, int lane) {
-  if (s >= stages) return;
-  wait_for<q_loads<BRT>()>(s, total);
-  if (s + AHEAD < total) L.load(next, s + AHEAD);
-  q_group<PACK, WC, BRT>(acc, cur, chain, pair, lane);  // group 4 s + chain
+// the same from C++ loads (outside the main loop, where no load into LDS is in flight)
+template <int PACK, bool WC, bool WIDE>
+HQ_DEV OpsQ read_ops_plain(const StageQ &S, int gi, int lane) {
+  OpsQ o;
+  const int kh = lane >> 5, l32 = lane & 31;
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    const int t = l32 + 32 * h;
+    o.X[h] = *(const v4i *)(S.x + t * 128 + ((2 * gi + kh) ^ swz(t)) * 16);
+  }
+#pragma unroll
+  for (int sp = 0; sp < 2; sp++) {
+    const int row = 32 * sp + l32;
+    if (PACK == 8) o.W[sp] = *(const v4i *)(S.w + row * 128 + ((2 * gi + kh) ^ swz(row)) * 16);
+    else o.W[sp] = six_half(S.w + row * 96 + gi * 24, kh);
+    o.ws[sp] = S.ws[row][sslot<WIDE>(row, gi)];
+    o.wc[sp] = WC ? S.wc[row][sslot<WIDE>(row, gi)] : 0;
+  }
+  o.xs = S.xs[lane][sslot<WIDE>(lane, gi)];
+  return o;
 }
 
-// the 4 chains of a pair of slices added in LDS, ((a0 + a1) + a2) + a3, for its four sub-tiles: wave k adds its sums
-// to what waves 0..k-1 left (the values of a lane are the same (row, token)s in the four waves of a pair); the sums
-// end in chain 3's waves.  p0 (sub-tiles 0, 1) and p1 (2, 3): 2 x 64 x 32 floats each that nothing else uses
-HQ_DEV void add_chains4(float acc[4][16], float *p0, float *p1, int pair, int chain, int lane) {
-  float *q[2] = {p0 + (pair * 64 + lane) * 32, p1 + (pair * 64 + lane) * 32};
+// the accumulator input of slice sp's integer MFMAs: the caller's correction of the lane's row (the same for every
+// token), or -64 sum(w) of the row (32 bytes of -64 against the weights)
+template <bool WC>
+HQ_DEV v16i corrections(const OpsQ &o, int sp) {
+  if (WC) {
+    v16i c;
+#pragma unroll
+    for (int r = 0; r < 16; r++) c[r] = o.wc[sp];
+    return c;
+  }
+  const v4i m64 = {(int32_t)0xc0c0c0c0, (int32_t)0xc0c0c0c0, (int32_t)0xc0c0c0c0, (int32_t)0xc0c0c0c0};
+  return __builtin_amdgcn_mfma_i32_32x32x32_i8(m64, o.W[sp], zero16i(), 0, 0, 0);
+}
+HQ_DEV v16i integers(const OpsQ &o, int sp, int h, const v16i &cin) {
+  return __builtin_amdgcn_mfma_i32_32x32x32_i8(o.X[h], o.W[sp], cin, 0, 0, 0);
+}
+// f(xs * ws) of slice sp with both token halves (registers 0..15: the first half, 16..31: the second)
+HQ_DEV v32f scales(const OpsQ &o, int sp) { return __builtin_amdgcn_mfma_f32_32x32x1f32(o.xs, o.ws[sp], zero32f(), 0, 0, 0); }
+
+// the chain's term of one sub-tile, f(f(C) * f(ws * xs)) added in order (relaxed/int8.ts:26-39)
+HQ_DEV void fold(float a[16], const v16i &c, const v32f &sc, int h) {
+#pragma unroll
+  for (int r = 0; r < 16; r++) a[r] = fadd(a[r], fmul((float)c[r], sc[16 * h + r]));
+}
+
+// Stage s of a wave's chain (group 4 s + chain): the stage's loads landed everywhere (the block's barrier), the
+// wave's operands read from `cur`, its loads of stage s + 3 issued into `dma` (the buffer stage s - 1's operands came
+// from, which every wave has read by this barrier), then the four sub-tiles (slice, half) = (0, 0), (0, 1), (1, 0),
+// (1, 1), each sub-tile's MFMAs issued before the previous one's fold so that the matrix core and the VALU take
+// turns without waiting for each other.  Every wave has issued its loads of stages up to s + 2 at the barrier (a
+// stage past the job's last group loads zeros, and its buffer is never read), so "stage s landed" is always "at most
+// two stages of this wave's loads in flight".
+template <int PACK, bool WC, bool WIDE>
+HQ_DEV void q_stage(Relaxed<PACK, WC, WIDE> &L, const StageQ &cur, StageQ &dma, int s, float acc[4][16], int chain,
+                    int lane) {
+  q_ready<PACK, WC, WIDE>(L.wave);
+  const OpsQ op = read_ops<PACK, WC, WIDE>(cur, chain, lane);
+  L.load(dma, s + AHEAD);
+  const v16i cin0 = corrections<WC>(op, 0);
+  const v32f S0 = scales(op, 0);
+  const v16i C0 = integers(op, 0, 0, cin0);
+  const v16i C1 = integers(op, 0, 1, cin0);
+  const v16i cin1 = corrections<WC>(op, 1);
+  fold(acc[0], C0, S0, 0);
+  const v32f S1 = scales(op, 1);
+  const v16i C2 = integers(op, 1, 0, cin1);
+  fold(acc[1], C1, S0, 1);
+  const v16i C3 = integers(op, 1, 1, cin1);
+  fold(acc[2], C2, S1, 0);
+  fold(acc[3], C3, S1, 1);
+}
+
+// the 4 chains of the tile added in LDS, ((a0 + a1) + a2) + a3, for its four sub-tiles: wave k adds its sums to
+// what waves 0..k-1 left (the values of a lane are the same (row, token)s in the four waves); the sums end in chain
+// 3's wave.  p0 (sub-tiles 0, 1) and p1 (2, 3): 32 x 64 floats each that nothing else uses, value v of a lane at
+// [v][lane] (consecutive lanes, consecutive banks)
+HQ_DEV void add_chains4(float acc[4][16], float *p0, float *p1, int chain, int lane) {
+  float *q[2] = {p0 + lane, p1 + lane};
   for (int k = 0; k < 4; k++) {
     __syncthreads();
     if (chain == k) {
@@ -338,7 +481,7 @@ HQ_DEV void add_chains4(float acc[4][16], float *p0, float *p1, int pair, int ch
       for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-          float *m = q[i >> 1] + 16 * (i & 1) + r;
+          float *m = q[i >> 1] + (16 * (i & 1) + r) * 64;
           if (k > 0) acc[i][r] = fadd(*m, acc[i][r]);
           if (k < 3) *m = acc[i][r];
         }
@@ -346,18 +489,16 @@ HQ_DEV void add_chains4(float acc[4][16], float *p0, float *p1, int pair, int ch
   }
 }
 
-template <int PACK, bool WC, int BRT>
-__global__ __launch_bounds__(q_threads<BRT>()) void gemm_relaxed(Job J) {
-  __shared__ StageQ<BRT> b0, b1, b2, b3;
-  __shared__ __attribute__((aligned(16))) char junk[1024];
+template <int PACK, bool WC, bool WIDE>
+__global__ __launch_bounds__(QT, 2) void gemm_relaxed(Job J) {
+  __shared__ StageQ b0, b1, b2, b3;
   const int M = J.count;
   const int ng = J.n >> 5, ng4 = ng & ~3;
   int rb, tb;
-  tile_of(blockIdx.x, gridDim.x, (J.r1 - J.r0 + BRT - 1) / BRT, rb, tb);
-  const int row0 = J.r0 + rb * BRT, tok0 = tb * BT;
+  tile_of(blockIdx.x, gridDim.x, (J.r1 - J.r0 + QR - 1) / QR, rb, tb);
+  const int row0 = J.r0 + rb * QR, tok0 = tb * BT;
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int pair = wave >> 2, chain = wave & 3;
+  const int chain = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 
   float acc[4][16];
 #pragma unroll
@@ -365,28 +506,41 @@ __global__ __launch_bounds__(q_threads<BRT>()) void gemm_relaxed(Job J) {
 #pragma unroll
     for (int r = 0; r < 16; r++) acc[i][r] = 0.0f;
 
-  Relaxed<PACK, WC, BRT> L(J, row0, tok0, M, wave, junk);
-  const int stages = ng4 / QG;
-  const int total = stages + (ng4 < ng ? 1 : 0);  // stages loaded: the tail's groups are one more
-  if (total > 0) L.load(b0, 0);
-  if (total > 1) L.load(b1, 1);
-  if (total > 2) L.load(b2, 2);
+  Relaxed<PACK, WC, WIDE> L(J, row0, tok0, M, chain);
+  const int stages = ng4 / QG;  // whole stages of the four chains; the groups past them (ng % 4) are one more stage
+  // stages 0..2 first (whatever the job has: a stage past its groups loads zeros); stage s's operands come from
+  // buffer s % 4 and its loads of stage s + 3 go into buffer (s - 1) % 4
+  L.load(b0, 0);
+  L.load(b1, 1);
+  L.load(b2, 2);
   for (int s = 0; s < stages; s += RING) {
-    q_step<PACK, WC, BRT>(L, b0, b3, s, stages, total, acc, pair, chain, lane);
-    q_step<PACK, WC, BRT>(L, b1, b0, s + 1, stages, total, acc, pair, chain, lane);
-    q_step<PACK, WC, BRT>(L, b2, b1, s + 2, stages, total, acc, pair, chain, lane);
-    q_step<PACK, WC, BRT>(L, b3, b2, s + 3, stages, total, acc, pair, chain, lane);
+    q_stage<PACK, WC, WIDE>(L, b0, b3, s, acc, chain, lane);
+    if (s + 1 >= stages) break;
+    q_stage<PACK, WC, WIDE>(L, b1, b0, s + 1, acc, chain, lane);
+    if (s + 2 >= stages) break;
+    q_stage<PACK, WC, WIDE>(L, b2, b1, s + 2, acc, chain, lane);
+    if (s + 3 >= stages) break;
+    q_stage<PACK, WC, WIDE>(L, b3, b2, s + 3, acc, chain, lane);
   }
   stage_ready<0>();  // every load has landed (the tail's too) and every wave is done with the stages
-  auto ring = [&](int i) -> StageQ<BRT> & { return i == 0 ? b0 : i == 1 ? b1 : i == 2 ? b2 : b3; };
-  add_chains4(acc, (float *)&ring((stages + 1) % RING), (float *)&ring((stages + 2) % RING), pair, chain, lane);
+  auto ring = [&](int i) -> StageQ & { return i == 0 ? b0 : i == 1 ? b1 : i == 2 ? b2 : b3; };
+  add_chains4(acc, (float *)&ring((stages + 1) % RING), (float *)&ring((stages + 2) % RING), chain, lane);
   if (chain == 3) {
     // the groups past the fours, one at a time, after the four chains' sum (relaxed/int8.ts:40-47)
-    const StageQ<BRT> &T = ring(stages % RING);
-    for (int gi = 0; gi < ng - ng4; gi++) q_group<PACK, WC, BRT>(acc, T, gi, pair, lane);
+    const StageQ &T = ring(stages % RING);
+    for (int gi = 0; gi < ng - ng4; gi++) {
+      const OpsQ o = read_ops_plain<PACK, WC, WIDE>(T, gi, lane);
+#pragma unroll
+      for (int sp = 0; sp < 2; sp++) {
+        const v16i cin = corrections<WC>(o, sp);
+        const v32f sc = scales(o, sp);
+#pragma unroll
+        for (int h = 0; h < 2; h++) fold(acc[2 * sp + h], integers(o, sp, h, cin), sc, h);
+      }
+    }
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      const int row = row0 + 64 * pair + 32 * (i >> 1) + (lane & 31);
+      const int row = row0 + 32 * (i >> 1) + (lane & 31);
       if (row < J.r1) {
         const int tbase = tok0 + 32 * (i & 1) + 4 * (lane >> 5);
 #pragma unroll
@@ -553,7 +707,7 @@ template <bool BIN>
 HQ_DEV void t_step(Ternary<BIN> &L, const StageT &cur, StageT &next, int s, int stages, int groups, float acc0[16],
                    float acc1[16], int slice, int part, int lane) {
   if (s >= stages) return;
-  wait_for<TLOADS>(s, stages);
+  wait_for<TLOADS>(s, stages, AHEAD - 1);
   if (s + AHEAD < stages) L.load(next, s + AHEAD);
   // part `part` of groups 2 s and 2 s + 1 (relaxed/signs.ts:28-31)
   t_group<BIN>(acc0, acc1, cur, 0, part, slice, lane);
@@ -609,6 +763,22 @@ __global__ __launch_bounds__(NT) void gemm_ternary(Job J) {
   }
 }
 
+// int8 / int6: the wide scale loads where a stage's four scales of every row and token are 16-byte aligned runs
+bool wide_scales(const Job &j) {
+  const auto a16 = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
+  return (j.n >> 5) % 4 == 0 && a16(j.ws) && (j.wc == nullptr || a16(j.wc)) && a16(j.xs) &&
+         (j.count <= 1 || j.sframe % 16 == 0);
+}
+
+template <int PACK>
+void launch_relaxed(const Job &job, dim3 grid, hipStream_t s) {
+  const bool wc = job.wc != nullptr, wide = wide_scales(job);
+  if (wc && wide) hipLaunchKernelGGL((gemm_relaxed<PACK, true, true>), grid, dim3(QT), 0, s, job);
+  else if (wc) hipLaunchKernelGGL((gemm_relaxed<PACK, true, false>), grid, dim3(QT), 0, s, job);
+  else if (wide) hipLaunchKernelGGL((gemm_relaxed<PACK, false, true>), grid, dim3(QT), 0, s, job);
+  else hipLaunchKernelGGL((gemm_relaxed<PACK, false, false>), grid, dim3(QT), 0, s, job);
+}
+
 }  // namespace
 
 bool gemm_supported(Kind kind) { return kind == Q8R || kind == Q6R || signs_kind(kind); }
@@ -617,34 +787,13 @@ hipError_t launch_gemm(Kind kind, const Job &job, hipStream_t s) {
   const int rows = job.r1 - job.r0;
   if (rows <= 0 || job.count <= 0) return hipSuccess;
   const int token_tiles = (job.count + BT - 1) / BT;
-  dim3 grid(((rows + BR - 1) / BR) * token_tiles), block(NT);
-  const bool wc = job.wc != nullptr;
-  // int8 / int6: 64-row tiles where 128-row ones would leave fewer than two blocks a compute unit
-  const bool narrow = (int64_t)((rows + BR - 1) / BR) * token_tiles < 2 * (int64_t)cu_count();
-  const dim3 grid64(((rows + 63) / 64) * token_tiles), block64(q_threads<64>()), block128(q_threads<128>());
   switch (kind) {
-  case Q8R:
-    if (narrow) {
-      if (wc) hipLaunchKernelGGL((gemm_relaxed<8, true, 64>), grid64, block64, 0, s, job);
-      else hipLaunchKernelGGL((gemm_relaxed<8, false, 64>), grid64, block64, 0, s, job);
-    } else {
-      if (wc) hipLaunchKernelGGL((gemm_relaxed<8, true, 128>), grid, block128, 0, s, job);
-      else hipLaunchKernelGGL((gemm_relaxed<8, false, 128>), grid, block128, 0, s, job);
-    }
-    break;
-  case Q6R:
-    if (narrow) {
-      if (wc) hipLaunchKernelGGL((gemm_relaxed<6, true, 64>), grid64, block64, 0, s, job);
-      else hipLaunchKernelGGL((gemm_relaxed<6, false, 64>), grid64, block64, 0, s, job);
-    } else {
-      if (wc) hipLaunchKernelGGL((gemm_relaxed<6, true, 128>), grid, block128, 0, s, job);
-      else hipLaunchKernelGGL((gemm_relaxed<6, false, 128>), grid, block128, 0, s, job);
-    }
-    break;
+  case Q8R: launch_relaxed<8>(job, dim3(((rows + QR - 1) / QR) * token_tiles), s); break;
+  case Q6R: launch_relaxed<6>(job, dim3(((rows + QR - 1) / QR) * token_tiles), s); break;
   case T2R:
-  case T2: hipLaunchKernelGGL(gemm_ternary<false>, grid, block, 0, s, job); break;
+  case T2: hipLaunchKernelGGL(gemm_ternary<false>, dim3(((rows + BR - 1) / BR) * token_tiles), dim3(NT), 0, s, job); break;
   case B1R:
-  case B1: hipLaunchKernelGGL(gemm_ternary<true>, grid, block, 0, s, job); break;
+  case B1: hipLaunchKernelGGL(gemm_ternary<true>, dim3(((rows + BR - 1) / BR) * token_tiles), dim3(NT), 0, s, job); break;
   default: return hipErrorNotSupported;
   }
   return hipGetLastError();

@@ -204,18 +204,19 @@ def run_token_kernel(k, arena, name, n, wq_addr, ws_addr, wc_addr, q, s, r0, r1)
 
 
 @pytest.mark.parametrize("ng", GROUPS)
-@pytest.mark.parametrize("form", ["matmul_q8r", "matmul_q8r_derived", "matmul_q6r", "matmul_q8", "matmul_q6"])
+@pytest.mark.parametrize("form", ["matmul_q8r", "matmul_q8r_derived", "matmul_q6r", "matmul_q6r_derived", "matmul_q8",
+                                  "matmul_q6"])
 def test_token_kernels(k, arena, oracle, ng, form):
     n, w8, v6, ws, xf, relaxed, plain = int8_case(ng)
-    six = form in ("matmul_q6r", "matmul_q6")
+    six = form in ("matmul_q6r", "matmul_q6r_derived", "matmul_q6")
     wbytes = pack6(v6) if six else w8
     wq = arena.put(wbytes)
     wsa = arena.put(ws)
-    is_relaxed = form.startswith("matmul_q8r") or form == "matmul_q6r"
+    is_relaxed = form.startswith("matmul_q8r") or form.startswith("matmul_q6r")
     toks = quantized_tokens(oracle, xf, relaxed if is_relaxed else plain, 64 if is_relaxed else 0)
     wc = (oracle.six_sums(wbytes) if six else oracle.int8_sums(w8)) if is_relaxed else None
-    wca = arena.put(wc) if form in ("matmul_q8r", "matmul_q6r") else 0
-    name = "matmul_q8r" if form == "matmul_q8r_derived" else form
+    wca = arena.put(wc) if form in ("matmul_q8r", "matmul_q6r") else 0  # the _derived forms pass wc = NULL
+    name = form[:-len("_derived")] if form.endswith("_derived") else form
     for t, (q, s) in enumerate(toks):
         if is_relaxed:
             full = (oracle.matmul_q6r if six else oracle.matmul_q8r)(q, s, wbytes, ws, wc, n)
@@ -296,7 +297,7 @@ def test_relaxed_tokens_long_rows(pkg, k, arena, oracle, count, packing):
     wq, wsa, xq = arena.put(wbytes, align=256), arena.put(ws), arena.put(q)
     kind = "matmul_q8r" if packing == "int8" else "matmul_q6r"
     product = oracle.matmul_q8r if packing == "int8" else oracle.matmul_q6r
-    forms = (("sums", sums), ("derived", None), ("moved", moved)) if packing == "int8" else (("sums", sums), ("moved", moved))
+    forms = (("sums", sums), ("derived", None), ("moved", moved))
     for form, corrections in forms:
         wca = 0 if corrections is None else arena.put(corrections)
         # int8 through the drop-in tile (rows cut at both ends), int6 through a phase (a job's rows start at 0)
@@ -344,11 +345,14 @@ def test_relaxed_bytes_past_seven_bits(k, arena):
 
 
 @pytest.mark.parametrize("count", [2, 4, 5, 16, 40])
-def test_q6r_many_tokens(pkg, arena, oracle, count):
-    """matmul_q6r over a prompt (no tile in the reference: a call a token, jobs.ts:471-475) through hq_phase."""
+@pytest.mark.parametrize("ng", [13, 16])
+def test_q6r_many_tokens(pkg, arena, oracle, count, ng):
+    """matmul_q6r over a prompt (no tile in the reference: a call a token, jobs.ts:471-475) through hq_phase, with
+    the corrections given, moved and derived (wc = NULL); 13 groups a row (the prompt tile loads a stage's scales four
+    bytes a lane) and 16 (sixteen bytes a lane)"""
     from pyodide_llm_amd import jobs
-    rng = np.random.default_rng(77 + count)
-    rows, ng = 90, 13
+    rng = np.random.default_rng(77 + count + 1000 * ng)
+    rows = 90
     n = 32 * ng
     frame = ((n + 4 * ng + 15) // 16) * 16
     v = (4 * rng.integers(-32, 32, rows * n)).astype(np.int8)
@@ -359,15 +363,59 @@ def test_q6r_many_tokens(pkg, arena, oracle, count):
     moved[[5, 600, rows * ng - 1]] += np.array([3, -64, 1 << 20], np.int32)
     q = tile_inputs(oracle, rng, n, count, frame, rows)
     wq, wsa, xq = arena.put(packed, align=256), arena.put(ws), arena.put(q)
-    for form, wc in (("six_sums", sums), ("moved", moved)):
+    for form, wc in (("six_sums", sums), ("moved", moved), ("derived", None)):
         out = arena.alloc(4 * rows * count, fill=np.full(rows * count, -7, F))
-        job = jobs.job("matmul_q6r", out, xq, xq + n, wq, wsa, arena.put(wc), n, rows=rows, count=count, os=4 * rows,
-                       as_=frame, bs=frame)
+        job = jobs.job("matmul_q6r", out, xq, xq + n, wq, wsa, 0 if wc is None else arena.put(wc), n, rows=rows,
+                       count=count, os=4 * rows, as_=frame, bs=frame)
         assert jobs.phase(pkg.library(), [job]) == 0, pkg.library().hq_last_error_message()
         got = arena.get(out, F, rows * count).reshape(count, rows)
         for t in range(count):
-            want = oracle.matmul_q6r(q[t, :n], q[t, n:n + 4 * ng].view(F), packed, ws, wc, n)
+            want = oracle.matmul_q6r(q[t, :n], q[t, n:n + 4 * ng].view(F), packed, ws, sums if wc is None else wc, n)
             assert same_bits(got[t], want), f"wc {form} token {t}: {first_difference(got[t], want)}"
+
+
+@pytest.mark.parametrize("packing", ["int8", "int6"])
+@pytest.mark.parametrize("ng", [13, 16])
+def test_relaxed_prompt_many_tiles(pkg, arena, oracle, packing, ng):
+    """A prompt over many of the matrix cores' 64-row x 64-token tiles: 301 rows cut at 5 and 299 (tiles starting
+    off a multiple of 64, a ragged last tile), 131 tokens (a ragged third token tile), the corrections given, moved
+    and derived, the scales loaded four bytes a lane (13 groups: also groups past the last four) and sixteen (16)."""
+    from pyodide_llm_amd import jobs
+    rng = np.random.default_rng(4242 + ng + (100 if packing == "int6" else 0))
+    rows, count, r0, r1 = 301, 131, 5, 299
+    n = 32 * ng
+    frame = ((n + 4 * ng + 15) // 16) * 16
+    if packing == "int8":
+        wbytes = rng.integers(-128, 128, rows * n).astype(np.int8)
+        sums = oracle.int8_sums(wbytes)
+        product, kind = oracle.matmul_q8r, "matmul_q8r"
+    else:
+        wbytes = pack6((4 * rng.integers(-32, 32, rows * n)).astype(np.int8))
+        sums = oracle.six_sums(wbytes)
+        product, kind = oracle.matmul_q6r, "matmul_q6r"
+    ws = (rng.random(rows * ng) * 1e-3).astype(F)
+    ws[7::17] = F(2.0 ** -140)
+    moved = sums.copy()
+    moved[rng.integers(0, rows * ng, 5)] += np.array([1, -5000, 77, 1 << 21, -3], np.int32)
+    q = tile_inputs(oracle, rng, n, count, frame, rows)
+    wq, wsa, xq = arena.put(wbytes, align=256), arena.put(ws), arena.put(q)
+    os_ = 4 * (rows + 5)
+    for form, wc in (("sums", sums), ("moved", moved), ("derived", None)):
+        out = arena.alloc(os_ * count, fill=np.full(os_ * count // 4, -7, F))
+        wca = 0 if wc is None else arena.put(wc)
+        # int8 through the drop-in tile (rows r0..r1), int6 through a phase (a job's rows start at 0)
+        if packing == "int8":
+            pkg.load_kernels().matmul_q8r_tile(out, xq, xq + n, wq, wsa, wca, n, r0, r1, count, os_, frame)
+        else:
+            job = jobs.job(kind, out, xq, xq + n, wq, wsa, wca, n, rows=r1, count=count, os=os_, as_=frame, bs=frame)
+            assert jobs.phase(pkg.library(), [job]) == 0, pkg.library().hq_last_error_message()
+        lo = r0 if packing == "int8" else 0
+        got = arena.get(out, F, os_ * count // 4).reshape(count, -1)
+        for t in range(count):
+            full = product(q[t, :n], q[t, n:n + 4 * ng].view(F), wbytes, ws, sums if wc is None else wc, n)
+            want = np.full(os_ // 4, F(-7), F)
+            want[lo:r1] = full[lo:r1]
+            assert same_bits(got[t], want), f"{packing} ng {ng} token {t} wc {form}: {first_difference(got[t], want)}"
 
 
 # ---- ternary -------------------------------------------------------------------------------------------------
