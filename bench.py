@@ -1,6 +1,8 @@
 """bench.py — the hot path's headline numbers on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-gemm] [--phases] [--mode phase|fused]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-gemm] [--no-configs] [--configs]
+                    [--mode phase|matmuls]
+    python bench.py --profile gemm|gemv|gemv_m4   (one workload's launches alone, for rocprofv3's counters)
     python bench.py --calibrate     (kernels of known traffic, for scaling rocprofv3's FETCH_SIZE / WRITE_SIZE)
 
 A step is one decode token of the Llama-3-8B-shaped Q8 path: per layer the reference's
@@ -10,19 +12,21 @@ four phases (src/runtime/forward/attention.ts:173, ffn.ts:27-30): quantize_x of 
 past the 256 MB Infinity Cache), int8 uniform in [-127, 127] with |N(0, 0.02)| / 127 scales, activations N(0, 1):
 synthetic, generated on the GPU from a seed.  The products are matmul_q8r's (relaxed form, quantize_x bias 64): a phase
 is quantize_x of its input, then one hq_phase() call over the phase's jobs (the reference's ready() and phase()), the
-corrections derived in the kernel (wc = NULL: the same integers as int8_sums' wc, and 12.5 % fewer bytes).  Beside it:
-the same step with the caller's wc, and with hq_matmuls() (quantize_x inside the products' launch, the reference's
-matmulsAlike; --mode fused makes it the headline).
+corrections derived in the kernel (wc = NULL: the same integers as int8_sums' wc, and 1/9 fewer bytes).  Beside it:
+the same step with the caller's wc (the reference's own call; its bytes counted), and through hq_matmuls() (the
+reference's matmulsAlike: quantize_x into the jobs' a / b and the phase in one call; --mode matmuls makes it the
+headline).
 
 value: algorithmic bytes of a step (1.125 B a weight, the activations' bytes and scales, 4 B an output; jobs.ts:448-450)
 over the step's time, with all inputs resident in HBM.  The step runs as a HIP graph of its launches (captured once).
 roofline: the GEMV kernel alone: a graph of only a step's products launches, replayed between HIP events, gives its
 average launch duration; traffic: the HBM bytes a launch moves, from rocprofv3's counters
-(profiles/gemv_q8r_8b_decode_traffic.md).
+(profiles/gemv_q8r_8b_decode_traffic.md).  Each kind of phase (q/k/v, o, gate/up, down, classifier) is also timed on
+its own.
 Also reported: config 3's decode at M = 4 (four tokens a step), the int8 prefill GEMM (config 3's M = 2048 over one
 layer's matrices, corrections derived and the caller's) in TOPS against the dense int8 MFMA peak, the measured
-ceilings (hq_ceiling_read past the caches, hq_ceiling_mfma on registers), and the oracle (the
-C restatement, oracle/) on the host's cores as the CPU baseline.
+ceilings (hq_ceiling_read past the caches, hq_ceiling_mfma on registers), configs 0, 1, 2 and 4, and
+the CPU baseline: oracle/fast.c (the reference arithmetic, AVX2) on the host's cores, decode and prefill.
 """
 import argparse
 import ctypes
@@ -110,14 +114,15 @@ def phase_tables(jobs, phases, with_wc):
                             m.ws.data_ptr(), m.wc.data_ptr() if with_wc else 0, m.n, rows=m.rows)
                    for m, out in mats]
         table = (ctypes.c_double * (16 * len(entries)))(*[float(v) for e in entries for v in e])
-        bytes_ = sum(m.bytes() + a.bytes() + 4 * m.rows for m, _ in mats)
+        # with the caller's wc the kernel also reads its int32 a group: 4 rows n / 32 bytes more
+        bytes_ = sum(m.bytes() + (m.rows * m.n / 8 if with_wc else 0) + a.bytes() + 4 * m.rows for m, _ in mats)
         tables.append((a, table, len(entries), bytes_))
     return tables
 
 
-def run_step(lib, tables, stream, fused, events=None):
+def run_step(lib, tables, stream, matmuls, events=None):
     for i, (a, table, njobs, _) in enumerate(tables):
-        if fused:  # engine.ts's matmulsAlike: quantize_x inside the products' launch
+        if matmuls:  # engine.ts's matmulsAlike in one call: quantize_x into the jobs' a / b, then the phase
             if events is not None:
                 events[i][0].record()
             lib.hq_matmuls(a.x.data_ptr(), 4 * a.n, table, njobs, 16, stream)
@@ -130,7 +135,10 @@ def run_step(lib, tables, stream, fused, events=None):
             events[i][1].record()
 
 
-def measure_decode(torch, pkg, args, phases, fused, with_wc):
+PHASE_NAMES = ("qkv", "o", "gate_up", "down", "lm_head")
+
+
+def measure_decode(torch, pkg, args, phases, matmuls, with_wc, by_phase=True):
     from pyodide_llm_amd import jobs
     lib = pkg.library()
     stream = torch.cuda.Stream()
@@ -141,13 +149,13 @@ def measure_decode(torch, pkg, args, phases, fused, with_wc):
         handle = stream.cuda_stream
         pkg.check(lib.hq_set_stream(handle))
         for _ in range(args.warmup):
-            run_step(lib, tables, handle, fused)
+            run_step(lib, tables, handle, matmuls)
         pkg.check(lib.hq_last_error())
         torch.cuda.synchronize()
         # the timed region: K steps as a HIP graph of one step's launches
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=stream):
-            run_step(lib, tables, handle, fused)
+            run_step(lib, tables, handle, matmuls)
         g.replay()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
@@ -162,7 +170,7 @@ def measure_decode(torch, pkg, args, phases, fused, with_wc):
             gk = torch.cuda.CUDAGraph()
             with torch.cuda.graph(gk, stream=stream):
                 for a, table, njobs, _ in subset:
-                    if fused:
+                    if matmuls:
                         lib.hq_matmuls(a.x.data_ptr(), 4 * a.n, table, njobs, 16, handle)
                     else:
                         lib.hq_phase(table, njobs, 16, handle)
@@ -177,10 +185,9 @@ def measure_decode(torch, pkg, args, phases, fused, with_wc):
 
         gemv_s = products(tables)
         kinds = {}
-        if args.phases:  # each kind of phase on its own (a graph of at least 32 launches)
-            names = [["qkv", "o", "gate_up", "down"][i % 4] if i < 4 * LAYERS else "lm_head"
-                     for i in range(len(tables))]
-            for name in ("qkv", "o", "gate_up", "down", "lm_head"):
+        if by_phase:  # each kind of phase on its own (a graph of at least 32 launches)
+            names = [PHASE_NAMES[i % 4] if i < 4 * LAYERS else "lm_head" for i in range(len(tables))]
+            for name in PHASE_NAMES:
                 mine = [t for t, nm in zip(tables, names) if nm == name]
                 mine = mine * -(-32 // len(mine))
                 s = products(mine)
@@ -198,10 +205,11 @@ def measure_decode(torch, pkg, args, phases, fused, with_wc):
     return out
 
 
-def measure_decode_m4(torch, pkg, args, phases):
+def build_decode_m4(torch, pkg, phases):
     """config 3's decode at M = 4: the same step for four tokens at once (each phase quantize_x of its input for the
     four tokens in one launch, then one hq_phase whose jobs take the four: every weight read once for four tokens).
-    GB/s of the step's algorithmic bytes: the weights, four tokens' activations, four outputs a row."""
+    Returns step(stream) (the whole step), products(stream) (its hq_phase calls alone) and the step's algorithmic
+    bytes: the weights, four tokens' activations, four outputs a row."""
     from pyodide_llm_amd import jobs
     lib = pkg.library()
     dev = "cuda:0"
@@ -231,10 +239,23 @@ def measure_decode_m4(torch, pkg, args, phases):
         for n, x, buf, frame, table, njobs in tables:
             lib.hq_quantize_x_batch(buf.data_ptr(), buf.data_ptr() + n, x.data_ptr(), n, 64, T, frame, 4 * n, h)
             lib.hq_phase(table, njobs, 16, h)
-    sec = _graph_time(torch, step, max(3, args.steps // 2))
+
+    def products(h):
+        for n, x, buf, frame, table, njobs in tables:
+            lib.hq_phase(table, njobs, 16, h)
+    return step, products, step_bytes, len(tables), outs
+
+
+def measure_decode_m4(torch, pkg, args, phases):
+    lib = pkg.library()
+    step, products, step_bytes, launches, keep = build_decode_m4(torch, pkg, phases)
+    reps = max(3, args.steps // 2)
+    sec = _graph_time(torch, step, reps)
+    gemv = _graph_time(torch, products, reps)
     pkg.check(lib.hq_last_error())
-    return {"M": T, "ms_per_step": round(1e3 * sec, 4), "GBps": round(step_bytes / sec / 1e9, 1),
-            "tokens_per_s": round(T / sec, 1), "step_bytes": step_bytes}
+    return {"M": 4, "ms_per_step": round(1e3 * sec, 4), "GBps": round(step_bytes / sec / 1e9, 1),
+            "tokens_per_s": round(4 / sec, 1), "step_bytes": step_bytes,
+            "gemv_avg_launch_us": round(1e6 * gemv / launches, 3), "gemv_GBps": round(step_bytes / gemv / 1e9, 1)}
 
 
 def _graph_time(torch, launch, reps):
@@ -256,11 +277,12 @@ def _graph_time(torch, launch, reps):
     return e0.elapsed_time(e1) * 1e-3 / reps
 
 
-def measure_configs(torch, pkg, args):
-    """The other configs' products on one GPU (BASELINE.json configs[0..2, 4], and config 4's shapes with binary
-    weights, the packing the reference ranks next): GB/s of algorithmic bytes for the
-    token products (M = 1; copies of the weights past the Infinity Cache where the shapes allow), TOPS for the
-    prompts.  Products only (the activations prepared once), graphs of their launches timed with HIP events."""
+def measure_configs(torch, pkg, args, extras):
+    """The other configs' products on one GPU (BASELINE.json configs[0..2, 4]; with `extras` also config 4's shapes
+    with binary weights, the packing the reference ranks next, llama.cpp's blocks and the classifier's outlier
+    channels): GB/s of algorithmic bytes for the token products (M = 1; copies of the weights past the Infinity Cache
+    where the shapes allow), TOPS for the prompts.  Products only (the activations prepared once), graphs of their
+    launches timed with HIP events."""
     from pyodide_llm_amd import jobs
     lib = pkg.library()
     gen = torch.Generator(device="cuda:0")
@@ -372,14 +394,15 @@ def measure_configs(torch, pkg, args):
            [[(1536, 1024)], [(1024, 1024)], [(9216, 1024)], [(1024, 4608)]] * 16 + [[(65536, 1024)]], 1)
     prefill("c2 Llama-3.2-1B prefill M=512, one layer", "int8",
             [(3072, 2048), (2048, 2048), (8192, 2048), (8192, 2048), (2048, 8192)], 512)
-    for kind in ("ternary", "int6", "binary"):
+    for kind in ("ternary", "int6", "binary") if extras else ("ternary", "int6"):
         copies = {"ternary": 8, "int6": 3, "binary": 12}[kind]
         tag = "c4 27B" if kind != "binary" else "27B shapes"
         decode(f"{tag} {kind} M=1, gate+up x {copies}", kind, [[(17408, 5120), (17408, 5120)]], copies)
         decode(f"{tag} {kind} M=1, down x {copies}", kind, [[(5120, 17408)]], copies)
         prefill(f"{tag} {kind} prefill M=256", kind, [(17408, 5120), (17408, 5120), (5120, 17408)], 256)
-    out.update(measure_blocks(torch, pkg, args, gen))
-    out.update(measure_outliers(torch, pkg, args, gen))
+    if extras:
+        out.update(measure_blocks(torch, pkg, args, gen))
+        out.update(measure_outliers(torch, pkg, args, gen))
     return out
 
 
@@ -524,10 +547,11 @@ def measure_blocks(torch, pkg, args, gen):
     return out
 
 
-def measure_gemm(torch, pkg, args):
-    """config 3's prefill: M = 2048 tokens through one layer's matrices (q, k, v, o, gate, up, down), with the
-    corrections derived in the kernel (wc = NULL, as the headline GEMV runs) and with the caller's (int8_sums', as
-    the reference's loader makes them, tensors.ts:126-134): the same numbers either way."""
+def gemm_workload(torch, pkg):
+    """config 3's prefill: M = 2048 tokens through one layer's matrices (q, k, v, o, gate, up, down), the activations
+    quantized once.  Returns run(with_wc) (the 7 products on the null stream: corrections derived in the kernel,
+    wc = NULL, as the headline GEMV runs, or the caller's, int8_sums' as the reference's loader makes them,
+    tensors.ts:126-134; the same numbers either way), the launches of a run, and its int8 operations."""
     lib = pkg.library()
     gen = torch.Generator(device="cuda:0")
     gen.manual_seed(5)
@@ -535,7 +559,7 @@ def measure_gemm(torch, pkg, args):
     shapes = [(4096, HIDDEN), (1024, HIDDEN), (1024, HIDDEN), (HIDDEN, HIDDEN), (FFN, HIDDEN), (FFN, HIDDEN),
               (HIDDEN, FFN)]
     mats = [Matrix(torch, gen, r, n, wc=True) for r, n in shapes]
-    for m in mats:  # the caller's corrections, as the reference's loader makes them (tensors.ts:126-134)
+    for m in mats:
         pkg.check(lib.hq_int8_sums_ex(m.wc.data_ptr(), m.w.data_ptr(), m.rows * m.n // 32, None))
     acts = {}
     for n in (HIDDEN, FFN):
@@ -552,22 +576,36 @@ def measure_gemm(torch, pkg, args):
             lib.hq_matmul_q8r_tile_ex(o.data_ptr(), buf.data_ptr(), buf.data_ptr() + m.n, m.w.data_ptr(),
                                       m.ws.data_ptr(), m.wc.data_ptr() if with_wc else None, m.n, 0, m.rows, M,
                                       4 * m.rows, frame, None)
+    run.keep = (mats, acts, outs)
+    return run, len(shapes), sum(2.0 * M * r * n for r, n in shapes)
 
-    ops = sum(2.0 * M * r * n for r, n in shapes)
-    out = {"M": M}
+
+def measure_gemm(torch, pkg, args):
+    """the prefill GEMM in TOPS: gemm_workload's layer, both forms taking turns (5 rounds of `steps` layers each, the
+    median round's rate: one round alone varies by several per cent)"""
+    lib = pkg.library()
+    run, _, ops = gemm_workload(torch, pkg)
+    times = {False: [], True: []}
     for with_wc in (False, True):
         run(with_wc)
-        pkg.check(lib.hq_last_error())
-        torch.cuda.synchronize()
-        reps = max(2, args.steps // 5)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(reps):
-            run(with_wc)
-        e1.record()
-        torch.cuda.synchronize()
-        s = e0.elapsed_time(e1) * 1e-3 / reps
-        r = {"tops": ops / s / 1e12, "frac": ops / s / 1e12 / INT8_PEAK_TOPS, "ms_per_layer": s * 1e3}
+    pkg.check(lib.hq_last_error())
+    torch.cuda.synchronize()
+    reps = max(5, args.steps)
+    for _ in range(5):
+        for with_wc in (False, True):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                run(with_wc)
+            e1.record()
+            torch.cuda.synchronize()
+            times[with_wc].append(e0.elapsed_time(e1) * 1e-3 / reps)
+    pkg.check(lib.hq_last_error())
+    out = {"M": 2048}
+    for with_wc in (False, True):
+        s = sorted(times[with_wc])[2]
+        r = {"tops": round(ops / s / 1e12, 1), "frac": round(ops / s / 1e12 / INT8_PEAK_TOPS, 4),
+             "ms_per_layer": round(s * 1e3, 4), "best_tops": round(ops / min(times[with_wc]) / 1e12, 1)}
         if with_wc:
             out["with_wc"] = r
         else:
@@ -575,32 +613,84 @@ def measure_gemm(torch, pkg, args):
     return out
 
 
-def cpu_baseline(args, seconds=10.0):
-    """The oracle's matmul_q8r (oracle/oracle.c: the reference arithmetic in C, scalar) on the host's cores, rows cut
-    as the reference's phase() cuts them (4 chunks a thread, threads.ts:45), over one 8B layer's 7 matrices (~245 MB,
-    past the host's caches), pass after pass for about `seconds`: the bytes of all passes over their time."""
+def cpu_description():
+    """the host's CPU model, its logical CPUs and the CPUs this process may run on"""
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return model, os.cpu_count() or 1, len(os.sched_getaffinity(0))
+
+
+# the reference's own CPU figures (one thread, WebAssembly relaxed SIMD on an Ampere A1 Neoverse-N1,
+# docs/notes/t158-cpu-audit-2026-09-27.md:5): :36 matmul_q8r out of the caches, :39 the prompt's blocks
+REFERENCE_CPU = {"matmul_q8r_GBps_per_thread": "11.4-11.5 (t158:36, 51-75 MB matrices)",
+                 "matmul_q8r_tile_GMACps_per_thread": "15.0-15.8 (t158:39, 16-token blocks)"}
+
+
+def cpu_baseline(args, gemv_seconds=8.0, tile_seconds=6.0):
+    """The CPU baseline: oracle/fast.c, the reference's relaxed int8 arithmetic vectorised for x86-64 (AVX2; every
+    output the oracle's, tests/test_oracle.py), on the host threads one GPU's share allows (at most 16), rows cut as
+    the reference's phase() cuts them (threads.ts:45, 109-110).
+      GEMV: matmul_q8r with the caller's wc (as the reference's loader passes it) over two Llama-3-8B layers' 7
+        matrices (490 MB, read in turn: past a socket's last-level cache as tests/tile-bench.ts:15-17 asks), pass
+        after pass for about gemv_seconds: GB/s of the bytes a pass reads (1.25 B a weight, activations, outputs).
+      prefill: matmul_q8r_tile of config 3's M = 2048 tokens over one layer's 7 matrices (4 rows x 4 tokens a
+        step), pass after pass for about tile_seconds: TOPS = 2 M N K / time."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
-    threads = min(16, os.cpu_count() or 1)
+    model, nproc, allowed = cpu_description()
+    threads = min(16, allowed)
     rng = np.random.default_rng(9)
     shapes = [(4096, HIDDEN), (1024, HIDDEN), (1024, HIDDEN), (HIDDEN, HIDDEN), (FFN, HIDDEN), (FFN, HIDDEN),
               (HIDDEN, FFN)]
     mats = []
-    for rows, n in shapes:
-        w = rng.integers(-127, 128, rows * n, dtype=np.int8)
-        ws = (np.abs(rng.standard_normal(rows * n // 32)) * 0.02 / 127).astype(np.float32)
-        xq, xs = oracle.quantize_x(rng.standard_normal(n).astype(np.float32), 64)
-        mats.append((rows, n, w, ws, oracle.int8_sums(w), xq, xs))
-    total_s, total_bytes, passes = 0.0, 0.0, 0
-    while total_s < seconds:
-        for rows, n, w, ws, wc, xq, xs in mats:
-            total_s += oracle.time_gemv("matmul_q8r", xq, xs, w, ws, wc, n, rows, threads, 1)
-            total_bytes += rows * n * 1.125 + n * 1.125 + 4 * rows
+    for _ in range(2):
+        for rows, n in shapes:
+            w = rng.integers(-127, 128, rows * n, dtype=np.int8)
+            ws = (np.abs(rng.standard_normal(rows * n // 32)) * 0.02 / 127).astype(np.float32)
+            mats.append((rows, n, w, ws, oracle.int8_sums(w)))
+    acts = {n: oracle.quantize_x(rng.standard_normal(n).astype(np.float32), 64) for n in (HIDDEN, FFN)}
+    gemv_s, gemv_bytes, passes = 0.0, 0.0, 0
+    while gemv_s < gemv_seconds:
+        for rows, n, w, ws, wc in mats:
+            xq, xs = acts[n]
+            gemv_s += oracle.time_fast_q8r(xq, xs, w, ws, wc, n, rows, threads)
+            gemv_bytes += rows * n * 1.25 + n * 1.125 + 4 * rows
         passes += 1
-    return {"value": total_bytes / total_s / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"oracle matmul_q8r (C restatement, scalar) over one Llama-3-8B layer's 7 matrices at M=1 "
-                      f"(245 MB), {passes} passes in {total_s:.1f} s on {threads} threads"}
+    M = 2048
+    frames = {}
+    for n in (HIDDEN, FFN):
+        frame = n + n // 8
+        buf = np.zeros((M, frame), np.uint8)
+        x = rng.standard_normal((M, n)).astype(np.float32)
+        for t in range(M):
+            q, sc = oracle.quantize_x(x[t], 64)
+            buf[t, :n], buf[t, n:] = q, sc.view(np.uint8)
+        frames[n] = (buf, frame)
+    tile_s, tile_ops, tile_passes = 0.0, 0.0, 0
+    while tile_s < tile_seconds:
+        for rows, n, w, ws, wc in mats[:7]:
+            buf, frame = frames[n]
+            tile_s += oracle.time_fast_q8r(buf, buf[:, n:], w, ws, wc, n, rows, threads, count=M, frame=frame)
+            tile_ops += 2.0 * M * rows * n
+        tile_passes += 1
+    gbps = gemv_bytes / gemv_s / 1e9
+    return {"value": round(gbps, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"oracle/fast.c matmul_q8r (AVX2, the oracle's numbers) with wc over two Llama-3-8B layers' 7 "
+                      f"matrices at M=1 (490 MB read in turn), {passes} passes in {gemv_s:.1f} s on {threads} "
+                      f"threads",
+            "per_thread_GBps": round(gbps / threads, 2),
+            "prefill": {"TOPS": round(tile_ops / tile_s / 1e12, 3), "M": M,
+                        "per_thread_GMACps": round(tile_ops / 2 / tile_s / 1e9 / threads, 1),
+                        "sample": f"matmul_q8r_tile over one layer's 7 matrices, {tile_passes} passes in "
+                                  f"{tile_s:.1f} s"},
+            "cpu_model": model, "nproc": nproc, "cpus_allowed": allowed, "reference": REFERENCE_CPU}
 
 
 def measure_ceilings(torch, pkg):
@@ -657,6 +747,40 @@ def traffic_per_launch():
     return None
 
 
+def profile(torch, pkg, args):
+    """--profile WHAT: WHAT's launches alone, issued directly (no graph) `steps` times after `warmup` untimed ones,
+    for rocprofv3's counters (a counter pass serialises the dispatches):
+      gemm     config 3's prefill, M = 2048 through one layer's 7 matrices, corrections derived (gemm_relaxed)
+      gemv     one decode step's products at M = 1 (129 hq_phase launches of gemv_relaxed<8,1,...>)
+      gemv_m4  the same at M = 4 (gemv_relaxed<8,4,...>)
+    Prints one JSON line naming what ran."""
+    from pyodide_llm_amd import jobs
+    lib = pkg.library()
+    if args.profile == "gemm":
+        run, launches, _ = gemm_workload(torch, pkg)
+        for _ in range(args.warmup + args.steps):
+            run(False)
+    else:
+        layers, head, phases = build_decode(torch, jobs, lib)
+        if args.profile == "gemv":
+            tables = phase_tables(jobs, phases, False)
+            for a, _ in phases:  # the activations the products read
+                pkg.check(lib.hq_quantize_x_ex(a.xq.data_ptr(), a.xs.data_ptr(), a.x.data_ptr(), a.n, 64, None))
+
+            def products(h):
+                for a, table, njobs, _ in tables:
+                    lib.hq_phase(table, njobs, 16, h)
+            launches = len(tables)
+        else:
+            step, products, _, launches, keep = build_decode_m4(torch, pkg, phases)
+            step(None)
+        for _ in range(args.warmup + args.steps):
+            products(None)
+    torch.cuda.synchronize()
+    pkg.check(lib.hq_last_error())
+    print(json.dumps({"profile": args.profile, "launches_per_step": launches, "steps": args.warmup + args.steps}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -664,13 +788,15 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemm", action="store_true")
-    ap.add_argument("--mode", choices=("phase", "fused"), default="phase",
+    ap.add_argument("--no-configs", action="store_true", help="skip configs 0, 1, 2 and 4")
+    ap.add_argument("--mode", choices=("phase", "matmuls"), default="phase",
                     help="the headline's phases: quantize_x then hq_phase (the reference's ready() + phase()), or "
-                         "hq_matmuls (quantize_x inside the products' launch)")
+                         "hq_matmuls (the same in one call, the reference's matmulsAlike)")
     ap.add_argument("--configs", action="store_true",
-                    help="also measure the other configs (stories15M, LFM2-350M, 1B prefill, 27B ternary / int6)")
-    ap.add_argument("--phases", action="store_true",
-                    help="also time each kind of phase (q/k/v, o, gate/up, down, classifier) on its own")
+                    help="also measure binary weights at config 4's shapes, llama.cpp's blocks and the outlier "
+                         "channels")
+    ap.add_argument("--profile", choices=("gemm", "gemv", "gemv_m4"),
+                    help="only run one workload's launches, for rocprofv3's counters")
     ap.add_argument("--calibrate", action="store_true",
                     help="only run kernels of known traffic (for scaling rocprofv3's FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
@@ -685,36 +811,39 @@ def main():
     pkg = load_package()
     torch.cuda.set_device(0)
     pkg.check(pkg.library().hq_init())
+    if args.profile:
+        profile(torch, pkg, args)
+        return
     from pyodide_llm_amd import jobs
     layers, head, phases = build_decode(torch, jobs, pkg.library())
-    fused = measure_decode(torch, pkg, args, phases, fused=True, with_wc=False)
-    separate = measure_decode(torch, pkg, args, phases, fused=False, with_wc=False)
-    separate_wc = measure_decode(torch, pkg, args, phases, fused=False, with_wc=True)
+    separate = measure_decode(torch, pkg, args, phases, matmuls=False, with_wc=False)
+    separate_wc = measure_decode(torch, pkg, args, phases, matmuls=False, with_wc=True)
+    one_call = measure_decode(torch, pkg, args, phases, matmuls=True, with_wc=False, by_phase=False)
     decode_m4 = measure_decode_m4(torch, pkg, args, phases)
     del layers, head, phases
     torch.cuda.empty_cache()
     gemm = None if args.no_gemm else measure_gemm(torch, pkg, args)
     ceilings = measure_ceilings(torch, pkg)
-    configs = measure_configs(torch, pkg, args) if args.configs else None
+    configs = None if args.no_configs else measure_configs(torch, pkg, args, extras=args.configs)
     cpu = None if args.no_cpu else cpu_baseline(args)
-    derived = fused if args.mode == "fused" else separate
-    achieved = derived["gemv_GBps"]
+    headline = one_call if args.mode == "matmuls" else separate
+    achieved = separate["gemv_GBps"]
     line = {
-        "metric": METRIC, "value": round(derived["GBps"], 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(derived["ms_per_step"], 4), "higher_is_better": True,
+        "metric": METRIC, "value": round(headline["GBps"], 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(headline["ms_per_step"], 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic (seeded, generated on the GPU)",
         "config": {"workload": "Llama-3-8B Q8 decode GEMV, M=1: 32 layers x (q/k/v, o, gate/up, down) + lm-head "
                                "[128256, 4096]; a phase is quantize_x + matmul_q8r of its matrices (BASELINE "
                                "configs[3])", "mode": args.mode,
-                   "step_bytes": derived["step_bytes"], "parallelism": "1 GPU"},
+                   "step_bytes": headline["step_bytes"], "parallelism": "1 GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_per_launch(),
-                     "kernel": "gemv_relaxed<8,1,false,FUSED>" if args.mode == "fused" else "gemv_relaxed<8,1,false,GLOBAL>",
-                     "avg_launch_us": round(derived["gemv_avg_launch_us"], 3),
-                     "bytes_per_launch": round(derived["gemv_bytes_per_launch"])},
+                     "kernel": "gemv_relaxed<8,1,false,0>",
+                     "avg_launch_us": round(separate["gemv_avg_launch_us"], 3),
+                     "bytes_per_launch": round(separate["gemv_bytes_per_launch"])},
         "cpu_baseline": cpu,
-        "detail": {"fused": fused, "quantize_then_phase": separate, "quantize_then_phase_with_wc": separate_wc,
-                   "decode_m4": decode_m4,
+        "detail": {"quantize_then_phase": separate, "quantize_then_phase_with_wc": separate_wc,
+                   "hq_matmuls": one_call, "decode_m4": decode_m4,
                    "prefill_gemm": gemm, "ceilings": ceilings, "configs": configs},
     }
     print(json.dumps(line))

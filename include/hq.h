@@ -229,10 +229,11 @@ int32_t hq_phase(const double *jobs, int32_t count, int32_t stride, void *stream
 
 /* src/runtime/forward/engine.ts:381-407 (matmulsAlike): the phase of jobs of one input, from its float32
  * activations: every job takes the same n and token count, token t's n values at x + t x_stride (bytes; x and
- * x_stride 16-byte aligned).  The relaxed int8 / int6 jobs of up to 4 tokens run with quantize_x in the products'
- * own launch (each block quantizes the input into its LDS: one launch a phase, the jobs' a / b not written); the
- * others are readied into their a / b (quantize_x at their bias, and interleave for ternary and binary, sums_x
- * for llama.cpp's blocks; jobs.ts:376-379, 385-395, 421-424, 435-438) and then run as hq_phase runs them.  Every output is the number quantize_x + the kernel give. */
+ * x_stride 16-byte aligned).  A kind at a time, the input is readied into its jobs' a / b as that kind takes it
+ * (quantize_x at its bias, and interleave for ternary and binary, sums_x for llama.cpp's blocks; jobs.ts:376-379,
+ * 385-395, 421-424: a pair of a / b several jobs share is readied once) and then those jobs run as hq_phase runs
+ * them; a job's a and b advance by one frame a token (as = bs).  Every output is the number quantize_x + the kernel
+ * give, and a / b hold the readied activations after the call. */
 int32_t hq_matmuls(const void *x, int32_t x_stride, const double *jobs, int32_t count, int32_t stride, void *stream);
 
 /* Which kernels take a job of `kind` (hq_phase's numbers), row length n and `count` tokens whose activations are

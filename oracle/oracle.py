@@ -62,6 +62,11 @@ def lib():
         L.o_sb_tables.argtypes, L.o_sb_tables.restype = [p, p], i32
         L.o_time_gemv.argtypes = [i32, p, p, p, p, p, p, i32, i32, i32, i32]
         L.o_time_gemv.restype = ctypes.c_double
+        L.f_matmul_q8r.argtypes, L.f_matmul_q8r.restype = [p, p, p, p, p, p, i32, i32, i32], None
+        L.f_matmul_q8r_tile.argtypes = [p, p, p, p, p, p, i32, i32, i32, i32, i32, i32]
+        L.f_matmul_q8r_tile.restype = None
+        L.f_time_q8r.argtypes = [p, p, p, p, p, p, i32, i32, i32, i32, i32, i32]
+        L.f_time_q8r.restype = ctypes.c_double
         _lib = L
     return _lib
 
@@ -246,6 +251,39 @@ def time_gemv(kind, xq, xs, wq, ws, wc, n, rows, threads, reps):
     """The oracle's GEMV over all rows on `threads` host threads (phase()-style chunks); fastest of reps, seconds."""
     out = np.zeros(rows, np.float32)
     return lib().o_time_gemv(KINDS[kind], _p(out), _p(xq), _p(xs), _p(wq), _p(ws), _p(wc), n, rows, threads, reps)
+
+
+def fast_matmul_q8r(xq, xs, wq, ws, wc, n, r0=0, r1=None):
+    """fast.c's vectorised matmul_q8r (the CPU baseline's kernel): the oracle's numbers to the bit."""
+    wq = _c(wq, np.int8).reshape(-1)
+    r1 = wq.size // n if r1 is None else r1
+    out = np.zeros(wq.size // n, np.float32)
+    lib().f_matmul_q8r(_p(out), _p(_c(xq, np.uint8)), _p(_c(xs, np.float32)), _p(wq), _p(_c(ws, np.float32)),
+                       _p(_c(wc, np.int32)), n, r0, r1)
+    return out
+
+
+def fast_matmul_q8r_tile(xq, xs, wq, ws, wc, n, count, r0=0, r1=None):
+    """fast.c's vectorised matmul_q8r_tile: xq (count, n) uint8, xs (count, n/32); returns (count, rows)."""
+    wq = _c(wq, np.int8).reshape(-1)
+    rows = wq.size // n
+    r1 = rows if r1 is None else r1
+    frame = n + 4 * (n // 32)
+    buf = np.zeros((count, frame), np.uint8)
+    buf[:, :n] = np.asarray(xq, np.uint8).reshape(count, n)
+    buf[:, n:] = np.asarray(xs, np.float32).reshape(count, n // 32).view(np.uint8)
+    out = np.zeros((count, rows), np.float32)
+    lib().f_matmul_q8r_tile(_p(out), _p(buf), buf.ctypes.data + n, _p(wq), _p(_c(ws, np.float32)),
+                            _p(_c(wc, np.int32)), n, r0, r1, count, 4 * rows, frame)
+    return out
+
+
+def time_fast_q8r(xq, xs, wq, ws, wc, n, rows, threads, count=0, frame=0):
+    """Seconds one call of fast.c's matmul_q8r (count 0: xq (n), xs (n/32)) or matmul_q8r_tile (count tokens a frame
+    apart in xq, their scales in xs at the same frame) takes over all rows on `threads` host threads."""
+    out = np.zeros(max(count, 1) * rows, np.float32)
+    return lib().f_time_q8r(_p(out), _p(xq), _p(xs), _p(wq), _p(ws), _p(wc), n, rows, count, 4 * rows, frame,
+                            threads)
 
 
 def add_columns(y, rows, a):

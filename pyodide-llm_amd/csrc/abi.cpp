@@ -555,6 +555,74 @@ int32_t parse_jobs(const double *jobs, int32_t count, int32_t stride, std::vecto
   return HQ_OK;
 }
 
+// ready() of `tokens` tokens of one input into xq / xs (frame bytes apart) as a job of `kind` takes them: quantize_x
+// at the kind's bias, then interleave for ternary and binary, sums_x for llama.cpp's blocks (jobs.ts:376-395,
+// 421-424)
+int32_t ready_acts(hq::Kind k, char *xq, char *xs, const char *x, int32_t n, int32_t tokens, int64_t frame,
+                   int64_t x_stride, hipStream_t s) {
+  const int32_t bias = relaxed(k) ? 64 : 0;
+  if (int32_t st = hip_status(hq::launch_quantize_x(xq, xs, x, n, bias, tokens, frame, x_stride, s), "quantize_x"))
+    return st;
+  if (ternary(k))
+    if (int32_t st = hip_status(hq::launch_interleave(xq, xs, n, tokens, frame, s), "interleave")) return st;
+  if (hq::blocks_kind(k))
+    if (int32_t st = hip_status(hq::launch_sums_x(xs, xq, n, tokens, frame, s), "sums_x")) return st;
+  return HQ_OK;
+}
+
+// matmulsAlike (src/runtime/forward/engine.ts:398-407): a kind at a time, the input readied as that kind's jobs take
+// it, then those jobs run as hq_phase runs them.  staging NULL: into the jobs' own a / b (a pair several jobs share
+// readied once); else into staging (every job's a / b replaced by it, its tokens `frame` bytes apart), kind after
+// kind in stream order.
+int32_t matmuls_alike(const void *x, int32_t x_stride, std::vector<hq::Job> by_kind[kKinds], char *staging,
+                      int64_t staging_bytes, hipStream_t s, const char *who) {
+  // one input: every job of one n and one token count
+  int32_t n = -1, tokens = -1;
+  for (int kind = 0; kind < kKinds; kind++)
+    for (const hq::Job &j : by_kind[kind]) {
+      if (n < 0) n = j.n, tokens = j.count;
+      if (j.n != n || j.count != tokens)
+        return fail(HQ_ERR_ARGUMENT, "%s: the jobs take one input (n %d and %d tokens, and %d, %d)", who, n, tokens,
+                    j.n, j.count);
+      // the readied activations of a token are one frame apart, bytes and scales alike (the reference's S)
+      if (!staging && tokens > 1 && j.frame != j.sframe)
+        return fail(HQ_ERR_ARGUMENT, "%s: a job's a and b advance by %lld and %lld bytes a token (one frame)", who,
+                    (long long)j.frame, (long long)j.sframe);
+    }
+  if (n < 0 || tokens == 0) return HQ_OK;
+  if (!x) return fail(HQ_ERR_NULL, "%s: x is NULL", who);
+  if (!aligned(x, 16) || (tokens > 1 && (x_stride < 0 || x_stride % 16)))
+    return fail(HQ_ERR_ALIGNMENT, "%s: x or x_stride not 16-byte aligned", who);
+  // the staging's token frame: n bytes, then the largest scale area a kind reads (llama.cpp's blocks: n/8 of
+  // scales, n/8 of sums of 16, n/4 of sums of 8), each from a 256-byte boundary
+  const int64_t qbytes = ((int64_t)n + 255) & ~(int64_t)255, frame = qbytes + (((int64_t)n / 2 + 255) & ~(int64_t)255);
+  if (staging && (int64_t)tokens * frame > staging_bytes)
+    return fail(HQ_ERR_ARGUMENT, "%s: %d tokens of %d activations take %lld bytes of staging (at most %lld)", who,
+                tokens, n, (long long)(tokens * frame), (long long)staging_bytes);
+  if (int32_t st = ensure_device()) return st;
+  for (int kind = 0; kind < kKinds; kind++) {
+    auto &list = by_kind[kind];
+    if (list.empty()) continue;
+    const hq::Kind k = (hq::Kind)kind;
+    if (staging) {
+      if (int32_t st = ready_acts(k, staging, staging + qbytes, (const char *)x, n, tokens, frame, x_stride, s))
+        return st;
+      for (hq::Job &j : list) j.xq = staging, j.xs = staging + qbytes, j.frame = frame, j.sframe = frame;
+    } else {
+      for (size_t i = 0; i < list.size(); i++) {
+        const hq::Job &j = list[i];
+        bool seen = false;
+        for (size_t e = 0; e < i && !seen; e++) seen = list[e].xq == j.xq && list[e].xs == j.xs && list[e].frame == j.frame;
+        if (seen) continue;
+        if (int32_t st = ready_acts(k, (char *)j.xq, (char *)j.xs, (const char *)x, n, tokens, j.frame, x_stride, s))
+          return st;
+      }
+    }
+    if (int32_t st = run_jobs(k, list, s)) return st;
+  }
+  return HQ_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -577,68 +645,7 @@ int32_t hq_matmuls(const void *x, int32_t x_stride, const double *jobs, int32_t 
   g_error = HQ_OK;
   std::vector<hq::Job> by_kind[kKinds];
   if (int32_t st = parse_jobs(jobs, count, stride, by_kind, "hq_matmuls")) return st;
-  if (count == 0) return HQ_OK;
-  // one input: every job of one n and one token count
-  int32_t n = -1, tokens = -1;
-  for (auto &list : by_kind)
-    for (const hq::Job &j : list) {
-      if (n < 0) n = j.n, tokens = j.count;
-      if (j.n != n || j.count != tokens)
-        return fail(HQ_ERR_ARGUMENT, "hq_matmuls: the jobs take one input (n %d and %d tokens, and %d, %d)", n,
-                    tokens, j.n, j.count);
-    }
-  if (tokens == 0) return HQ_OK;
-  if (!x) return fail(HQ_ERR_NULL, "hq_matmuls: x is NULL");
-  if (!aligned(x, 16) || (tokens > 1 && (x_stride < 0 || x_stride % 16)))
-    return fail(HQ_ERR_ALIGNMENT, "hq_matmuls: x or x_stride not 16-byte aligned");
-  if (int32_t st = ensure_device()) return st;
-  const hipStream_t s = stream_of(stream);
-  for (int kind = 0; kind < kKinds; kind++) {
-    auto &list = by_kind[kind];
-    if (list.empty()) continue;
-    const hq::Kind k = (hq::Kind)kind;
-    if (relaxed(k) && tokens <= hq::kGemvMaxTokens) {
-      // quantize_x in every block of the products (tokens split where their activations do not fit the LDS)
-      const int32_t per = (int64_t)tokens * (n + n / 8) <= 65536 ? tokens : 1;
-      for (int32_t t0 = 0; t0 < tokens; t0 += per)
-        for (int w = 0; w < 2; w++) {
-          std::vector<hq::Job> part;
-          for (const hq::Job &j : list)
-            if ((j.wc != nullptr) == (w == 1)) {
-              hq::Job q = j;
-              q.count = per;
-              q.out = j.out + t0 * j.os;
-              part.push_back(q);
-            }
-          for (size_t i = 0; i < part.size(); i += hq::kMaxJobs) {
-            const int32_t m = (int32_t)(part.size() - i < (size_t)hq::kMaxJobs ? part.size() - i : hq::kMaxJobs);
-            const int32_t st = hip_status(
-                hq::launch_gemv_fused(k, &part[i], m, (const char *)x + (int64_t)t0 * x_stride, x_stride, s),
-                kind_name(k));
-            if (st) return st;
-          }
-        }
-      continue;
-    }
-    // the others: ready() into each job's xq / xs (jobs.ts:376-379, 421-424), then the phase
-    for (const hq::Job &j : list) {
-      const int32_t bias = relaxed(k) ? 64 : 0;
-      if (int32_t st = hip_status(hq::launch_quantize_x((char *)j.xq, (char *)j.xs, (const char *)x, n, bias, tokens,
-                                                        j.frame, x_stride, s),
-                                  "quantize_x"))
-        return st;
-      if (ternary(k)) {
-        if (int32_t st = hip_status(hq::launch_interleave((char *)j.xq, (char *)j.xs, n, tokens, j.frame, s), "interleave"))
-          return st;
-      }
-      if (hq::blocks_kind(k)) {  // and the sums of each 16 and 8 (jobs.ts:385-395)
-        if (int32_t st = hip_status(hq::launch_sums_x((char *)j.xs, (const char *)j.xq, n, tokens, j.frame, s), "sums_x"))
-          return st;
-      }
-    }
-    if (int32_t st = run_jobs(k, list, s)) return st;
-  }
-  return HQ_OK;
+  return matmuls_alike(x, x_stride, by_kind, nullptr, 0, stream_of(stream), "hq_matmuls");
 }
 
 // ---- the ceilings ---------------------------------------------------------------------------------------------

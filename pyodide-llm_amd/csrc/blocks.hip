@@ -262,10 +262,7 @@ HQ_DEV void sb_load_block(BlockBytes<BYTES> &B, const SbBatch &b, int unit, int 
 
 constexpr int kSbLongRow = 32;
 // the most a launch stages of a token's activations (n + n/2 bytes: n up to 32768)
-#ifndef HQ_SB_STAGE_MAX
-#define HQ_SB_STAGE_MAX (48 * 1024)
-#endif
-constexpr size_t kSbStageMax = HQ_SB_STAGE_MAX;
+constexpr size_t kSbStageMax = 48 * 1024;
 constexpr int sb_lanes(int blocks) { return blocks >= kSbLongRow ? 64 : 16; }
 
 template <int TY> constexpr int lds_table_bytes() {
@@ -475,9 +472,6 @@ typedef float v16f_t __attribute__((ext_vector_type(16)));
 
 constexpr int SBT_R = 32;            // a block's rows
 constexpr int SBT_PITCH = 256 + 16;  // an LDS row of a block's 256 bytes (16 more: 16-byte reads of rows apart)
-#ifndef HQ_SB_TILE_NT
-#define HQ_SB_TILE_NT 0  // 0: the widest of 128, 64, 32 tokens a block that gives enough blocks
-#endif
 
 template <int TY> constexpr bool tile_signed() { return has_signs<TY>(); }
 template <int TY> constexpr bool tile_split() { return TY == IQ2_XS || TY == IQ2_S || TY == IQ1_M; }
@@ -848,9 +842,8 @@ template <int TY>
 hipError_t launch_tile_type(const Job &j, hipStream_t s) {
   const int nrt = (j.r1 - j.r0 + SBT_R - 1) / SBT_R;
   const int64_t want = 2 * (int64_t)cu_count();
-  int nt = HQ_SB_TILE_NT;
-  if (nt == 0) nt = tile_wide<TY>() && (int64_t)nrt * ((j.count + 127) / 128) >= want ? 128
-                  : (int64_t)nrt * ((j.count + 63) / 64) >= want ? 64 : 32;
+  const int nt = tile_wide<TY>() && (int64_t)nrt * ((j.count + 127) / 128) >= want ? 128
+               : (int64_t)nrt * ((j.count + 63) / 64) >= want ? 64 : 32;
   if constexpr (tile_wide<TY>())
     if (nt == 128) return launch_tile_nt<TY, 128>(j, nrt, s);
   return nt == 64 ? launch_tile_nt<TY, 64>(j, nrt, s) : launch_tile_nt<TY, 32>(j, nrt, s);

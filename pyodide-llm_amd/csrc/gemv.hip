@@ -33,50 +33,35 @@ struct GemvBatch {
   Job job[kMaxJobs];
   int32_t block0[kMaxJobs + 1];  // the first block of each job
   int32_t njobs;
-  int32_t bias;          // FUSED: the activations' bias (quantize_x's)
-  const char *x;         // FUSED: token t's n float32 activations at x + t x_stride, shared by every job
-  int64_t x_stride;
 };
 
-// where a kernel's activations come from: the caller's xq / xs in global memory (read through the L1), a copy of
-// them the block makes in LDS, or the block's own quantize_x of the float32 activations into LDS (one launch a
-// phase, as the reference's matmulsAlike quantizes once and runs the phase, src/runtime/forward/engine.ts:398-407)
-enum Src { GLOBAL = 0, STAGED = 1, FUSED = 2 };
+// where a kernel's activations come from: the caller's xq / xs in global memory (read through the L1), or a copy
+// of them the block makes in LDS
+enum Src { GLOBAL = 0, STAGED = 1 };
 
 // the LDS a block needs for T tokens of n activations (bytes, then float32 scales)
 HQ_HOST_DEV constexpr int64_t act_lds_bytes(int T, int n) { return (int64_t)T * (n + 4 * (n / 32)); }
 
-// STAGED / FUSED: fill the block's LDS with the activations of T tokens: bytes of token t at lq + t n, scales at
+// STAGED: fill the block's LDS with the activations of T tokens: bytes of token t at lq + t n, scales at
 // ls + t (n / 32).  Every thread takes groups of 32 in turn; the block synchronizes after.
-template <int T, int SRC>
-HQ_DEV void fill_acts(const GemvBatch &b, const Job &J, char *lq, float *ls) {
+template <int T>
+HQ_DEV void fill_acts(const Job &J, char *lq, float *ls) {
   const int n = J.n, ng = n >> 5;
   for (int idx = threadIdx.x; idx < T * ng; idx += blockDim.x) {
     const int t = idx / ng, g = idx - t * ng;
-    uint32_t q[8];
-    float sc;
-    if (SRC == FUSED) {
-      quantize_group((const float *)(b.x + t * b.x_stride) + g * GS, b.bias, q, sc);
-    } else {
-      const uint4 a = *(const uint4 *)(J.xq + t * J.frame + g * GS), c = *(const uint4 *)(J.xq + t * J.frame + g * GS + 16);
-      q[0] = a.x; q[1] = a.y; q[2] = a.z; q[3] = a.w; q[4] = c.x; q[5] = c.y; q[6] = c.z; q[7] = c.w;
-      sc = ((const float *)(J.xs + t * J.sframe))[g];
-    }
+    const char *src = J.xq + t * J.frame + g * GS;
     uint4 *dst = (uint4 *)(lq + t * n + g * GS);
-    dst[0] = make_uint4(q[0], q[1], q[2], q[3]);
-    dst[1] = make_uint4(q[4], q[5], q[6], q[7]);
-    ls[t * ng + g] = sc;
+    dst[0] = *(const uint4 *)src;
+    dst[1] = *(const uint4 *)(src + 16);
+    ls[t * ng + g] = ((const float *)(J.xs + t * J.sframe))[g];
   }
   __syncthreads();
 }
 
 constexpr int kRowsPerBlock = 16;
 // the relaxed kinds' blocks: kRelaxedRows rows of 16 lanes (fewer rows a block: more blocks, a finer balance of the
-// last ones over the CUs)
-#ifndef HQ_GEMV_ROWS
-#define HQ_GEMV_ROWS 8
-#endif
-constexpr int kRelaxedRows = HQ_GEMV_ROWS;
+// last ones over the CUs; 8 measured faster than 16 at the 8B decode)
+constexpr int kRelaxedRows = 8;
 HQ_HOST_DEV constexpr int rows_per_block(Kind kind) { return kind == Q8R || kind == Q6R ? kRelaxedRows : kRowsPerBlock; }
 
 HQ_DEV int job_of(const GemvBatch &b, int blk) {
@@ -88,20 +73,7 @@ HQ_DEV int job_of(const GemvBatch &b, int blk) {
 HQ_DEV uint4 ld16(const char *p) { return *(const uint4 *)p; }
 HQ_DEV uint2 ld8(const char *p) { return *(const uint2 *)p; }
 
-// the weights are read once a launch: loads that do not keep them in the caches (HQ_GEMV_NT) leave the caches to
-// the activations
-#ifndef HQ_GEMV_NT
-#define HQ_GEMV_NT 0
-#endif
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-HQ_DEV uint4 ldw16(const char *p) {
-#if HQ_GEMV_NT
-  const u32x4 v = __builtin_nontemporal_load((const u32x4 *)p);
-  return make_uint4(v.x, v.y, v.z, v.w);
-#else
-  return *(const uint4 *)p;
-#endif
-}
+HQ_DEV uint4 ldw16(const char *p) { return *(const uint4 *)p; }
 
 // the 32 weight bytes of group g of a row, as eight dwords of int8 (int6 groups widened, kernels/six.ts)
 template <int PACK>
@@ -148,10 +120,7 @@ struct ActSource {
 
 template <int PACK, int T, bool WC, int SRC>
 struct RelaxedChunk {
-#ifndef HQ_GEMV_U
-#define HQ_GEMV_U 4
-#endif
-  static constexpr int U = T == 1 ? HQ_GEMV_U : (T == 2 ? 2 : 1);
+  static constexpr int U = T == 1 ? 4 : (T == 2 ? 2 : 1);
   uint32_t w[U][8];
   uint32_t x[U][T][8];
   float ws[U], xs[U][T];
@@ -228,10 +197,10 @@ struct RelaxedChunk {
   }
 };
 
-// the kRelaxedRows rows of tile `tile` (the batch's jobs' row ranges cut into tiles in order).  fill: first make the
-// block's LDS copy of the activations (STAGED, FUSED), while the first weights are in flight
+// the kRelaxedRows rows of tile `tile` (the batch's jobs' row ranges cut into tiles in order).  STAGED: first make
+// the block's LDS copy of the activations, while the first weights are in flight
 template <int PACK, int T, bool WC, int SRC>
-HQ_DEV void relaxed_tile(const GemvBatch &batch, int tile, char *lds, bool fill) {
+HQ_DEV void relaxed_tile(const GemvBatch &batch, int tile, char *lds) {
   const int jb = job_of(batch, tile);
   const Job &J = batch.job[jb];
   const int lane = threadIdx.x & 15;
@@ -261,9 +230,9 @@ HQ_DEV void relaxed_tile(const GemvBatch &batch, int tile, char *lds, bool fill)
   constexpr int U = Chunk::U;
   const int steps = (ng4 + 15) >> 4;
   Chunk a, b;
-  if (fill) {
+  if (SRC == STAGED) {
     if (steps > 0) a.load_w(wrow, srow, crow, 0, lane, ng4);  // the first weights in flight during the staging
-    fill_acts<T, SRC>(batch, J, lds, (float *)(lds + T * J.n));
+    fill_acts<T>(J, lds, (float *)(lds + T * J.n));
     if (steps > 0) a.load_x(A, 0, lane, ng4);
   } else if (steps > 0) {
     a.load(wrow, srow, crow, A, 0, lane, ng4);
@@ -311,19 +280,11 @@ HQ_DEV void relaxed_tile(const GemvBatch &batch, int tile, char *lds, bool fill)
   }
 }
 
-// GLOBAL / STAGED: a tile a block.  FUSED: the block quantizes the activations once (they are every job's) and then
-// takes tiles blockIdx.x, + gridDim.x, ... (the grid is a few blocks a CU): one quantize_x a block, not a tile
+// a tile a block
 template <int PACK, int T, bool WC, int SRC>
 __global__ __launch_bounds__(16 * kRelaxedRows) void gemv_relaxed(GemvBatch batch) {
   extern __shared__ __align__(16) char lds[];
-  if (SRC == FUSED) {
-    const int tiles = batch.block0[batch.njobs];
-    relaxed_tile<PACK, T, WC, SRC>(batch, blockIdx.x, lds, true);
-    for (int tile = blockIdx.x + gridDim.x; tile < tiles; tile += gridDim.x)
-      relaxed_tile<PACK, T, WC, SRC>(batch, tile, lds, false);
-  } else {
-    relaxed_tile<PACK, T, WC, SRC>(batch, blockIdx.x, lds, SRC == STAGED);
-  }
+  relaxed_tile<PACK, T, WC, SRC>(batch, blockIdx.x, lds);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -441,10 +402,7 @@ __global__ __launch_bounds__(256) void gemv_plain(GemvBatch batch) {
 // copies the activations of its T tokens into LDS once (STAGE), so that only the codes stream from memory, U steps
 // at a time with the next U steps' loads in flight.  In LDS a group's 128 bytes take 144 (16 bytes of padding), so
 // that the 16 lanes of a row, which read the same 16 bytes of 16 consecutive groups, hit 16 different bank quads.
-#ifndef HQ_TERNARY_STEPS
-#define HQ_TERNARY_STEPS 1
-#endif
-constexpr int kTernarySteps = HQ_TERNARY_STEPS;  // steps a chunk
+constexpr int kTernarySteps = 1;  // steps a chunk (two chunks of loads in flight)
 constexpr int kTernaryPitch = 144;  // LDS bytes a group of 128 activations
 
 HQ_HOST_DEV constexpr int ternary_token_bytes(int n) { return (n >> 7) * kTernaryPitch + n / 4; }
@@ -556,10 +514,7 @@ struct TernaryChunk {
   }
 };
 
-#ifndef HQ_TERN_THREADS
-#define HQ_TERN_THREADS 256
-#endif
-constexpr int kTernThreads = HQ_TERN_THREADS;  // a block's threads: kTernThreads / L rows
+constexpr int kTernThreads = 256;  // a block's threads: kTernThreads / L rows
 // rows of L lanes (16: 16 rows a block; 32 for long rows: twice the waves on the same rows)
 template <int T, bool STAGE, int L, bool BIN>
 __global__ __launch_bounds__(kTernThreads) void gemv_ternary(GemvBatch batch) {
@@ -637,31 +592,18 @@ __global__ __launch_bounds__(kTernThreads) void gemv_ternary(GemvBatch batch) {
 }
 
 // the LDS a ternary block stages for T tokens of n activations (beyond: read through the L1)
-#ifndef HQ_TERNARY_STAGE_MAX
-#define HQ_TERNARY_STAGE_MAX (64 * 1024)
-#endif
-constexpr size_t kTernaryStageMax = HQ_TERNARY_STAGE_MAX;
-// lanes a row of ternary weights: 32 for rows of at least kTernaryLongRow weights
-#ifndef HQ_TERNARY_LONG
-#define HQ_TERNARY_LONG 8192
-#endif
-#ifndef HQ_TERNARY_L8
-#define HQ_TERNARY_L8 1
-#endif
+constexpr size_t kTernaryStageMax = 64 * 1024;
+// lanes a row of ternary weights: 32 for rows of at least kTernaryLongRow weights, 8 for rows of an odd number of
+// 8-group steps (no lanes idle in the last step), else 16
+constexpr int kTernaryLongRow = 8192;
 HQ_HOST_DEV constexpr int ternary_lanes(int n) {
-  return n >= HQ_TERNARY_LONG ? 32
-       : (HQ_TERNARY_L8 && (n >> 7) % 16 != 0 && (n >> 7) % 8 == 0) ? 8 : 16;
+  return n >= kTernaryLongRow ? 32 : ((n >> 7) % 16 != 0 && (n >> 7) % 8 == 0) ? 8 : 16;
 }
 HQ_HOST_DEV constexpr size_t ternary_stage_bytes(int T, int n) { return (size_t)T * ternary_token_bytes(n); }
 
-// FUSED: blocks a CU (each quantizes the activations once and takes tiles in turn)
-#ifndef HQ_FUSED_BLOCKS_PER_CU
-#define HQ_FUSED_BLOCKS_PER_CU 6
-#endif
 template <int PACK, int T, int SRC>
 hipError_t launch_relaxed(const GemvBatch &b, int tiles, bool wc, size_t lds, hipStream_t s) {
-  const int cap = HQ_FUSED_BLOCKS_PER_CU * cu_count();
-  dim3 grid(SRC == FUSED && tiles > cap ? cap : tiles), block(16 * kRelaxedRows);
+  dim3 grid(tiles), block(16 * kRelaxedRows);
   if (wc) hipLaunchKernelGGL((gemv_relaxed<PACK, T, true, SRC>), grid, block, lds, s, b);
   else hipLaunchKernelGGL((gemv_relaxed<PACK, T, false, SRC>), grid, block, lds, s, b);
   return hipGetLastError();
@@ -698,11 +640,9 @@ hipError_t launch_t(Kind kind, const GemvBatch &b, int blocks, bool wc, int src,
   case Q8R:
   case Q6R:
     if (kind == Q8R) {
-      if (src == FUSED) return launch_relaxed<8, T, FUSED>(b, blocks, wc, lds, s);
       if (src == STAGED) return launch_relaxed<8, T, STAGED>(b, blocks, wc, lds, s);
       return launch_relaxed<8, T, GLOBAL>(b, blocks, wc, 0, s);
     }
-    if (src == FUSED) return launch_relaxed<6, T, FUSED>(b, blocks, wc, lds, s);
     if (src == STAGED) return launch_relaxed<6, T, STAGED>(b, blocks, wc, lds, s);
     return launch_relaxed<6, T, GLOBAL>(b, blocks, wc, 0, s);
   case Q8: hipLaunchKernelGGL((gemv_plain<8, T>), grid, block, 0, s, b); break;
@@ -718,19 +658,14 @@ hipError_t launch_t(Kind kind, const GemvBatch &b, int blocks, bool wc, int src,
 
 }  // namespace
 
-// the largest activations (bytes and scales of all tokens) a block copies into LDS (STAGED) rather than reading
-// them through the L1: more would leave too few 8-row blocks a CU (4 tokens of the 8B down projection, 64.5 KB,
-// measured 4 % slower a decode step staged than read through the caches)
-#ifndef HQ_GEMV_STAGE_MAX_MULTI
-#define HQ_GEMV_STAGE_MAX_MULTI (32 * 1024)
-#endif
-#ifndef HQ_GEMV_STAGE_MAX
-#define HQ_GEMV_STAGE_MAX 0
-#endif
+// the largest activations (bytes and scales of all tokens) a block of 2..4 tokens copies into LDS (STAGED) rather
+// than reading them through the L1: more would leave too few 8-row blocks a CU (4 tokens of the 8B down
+// projection, 64.5 KB, measured 4 % slower a decode step staged than read through the caches).  One token is read
+// through the caches (measured 9 % faster than staged).
+constexpr size_t kGemvStageMax = 32 * 1024;
 
 namespace {
-hipError_t launch_batch(Kind kind, const Job *jobs, int32_t njobs, const char *x, int64_t x_stride, int32_t bias,
-                        hipStream_t s) {
+hipError_t launch_batch(Kind kind, const Job *jobs, int32_t njobs, hipStream_t s) {
   if (njobs < 1 || njobs > kMaxJobs) return hipErrorInvalidValue;
   GemvBatch b{};
   int blocks = 0, nmax = 0;
@@ -743,17 +678,12 @@ hipError_t launch_batch(Kind kind, const Job *jobs, int32_t njobs, const char *x
   }
   b.block0[njobs] = blocks;
   b.njobs = njobs;
-  b.x = x;
-  b.x_stride = x_stride;
-  b.bias = bias;
   if (blocks == 0) return hipSuccess;
   const bool wc = jobs[0].wc != nullptr;
   const int T = jobs[0].count;
   const size_t lds = (size_t)act_lds_bytes(T, nmax);
-  // staged in LDS for 2..4 tokens (each row's lanes read every token's activations: measured 4 % faster at M = 4),
-  // read through the caches for one (measured 9 % faster)
-  const size_t stage_max = T == 1 ? (size_t)HQ_GEMV_STAGE_MAX : (size_t)HQ_GEMV_STAGE_MAX_MULTI;
-  int src = x ? FUSED : (lds <= stage_max ? STAGED : GLOBAL);
+  // staged in LDS for 2..4 tokens (each row's lanes read every token's activations: measured 4 % faster at M = 4)
+  const int src = T > 1 && lds <= kGemvStageMax ? STAGED : GLOBAL;
   switch (T) {
   case 1: return launch_t<1>(kind, b, blocks, wc, src, lds, s);
   case 2: return launch_t<2>(kind, b, blocks, wc, src, lds, s);
@@ -766,14 +696,7 @@ hipError_t launch_batch(Kind kind, const Job *jobs, int32_t njobs, const char *x
 
 // jobs: one kind, one token count (1..4), one wc-ness (all with corrections or all without)
 hipError_t launch_gemv(Kind kind, const Job *jobs, int32_t njobs, hipStream_t s) {
-  return launch_batch(kind, jobs, njobs, nullptr, 0, 0, s);
-}
-
-// the same, the activations quantized by each block from token t's n float32 at x + t x_stride (relaxed kinds)
-hipError_t launch_gemv_fused(Kind kind, const Job *jobs, int32_t njobs, const char *x, int64_t x_stride,
-                             hipStream_t s) {
-  if (kind != Q8R && kind != Q6R) return hipErrorNotSupported;
-  return launch_batch(kind, jobs, njobs, x, x_stride, 64, s);
+  return launch_batch(kind, jobs, njobs, s);
 }
 
 }  // namespace hq

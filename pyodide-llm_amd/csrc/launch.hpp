@@ -60,10 +60,6 @@ inline int cu_count() {
 // GEMV-shaped products (every job of one kind and one token count, 1..4; up to kMaxJobs jobs a launch)
 constexpr int kMaxJobs = 8;
 hipError_t launch_gemv(Kind kind, const Job *jobs, int32_t njobs, hipStream_t s);
-// the relaxed kinds with quantize_x fused: each block quantizes token t's n float32 activations at x + t x_stride
-// (bias 64) into LDS itself; the jobs' xq / xs are not read
-hipError_t launch_gemv_fused(Kind kind, const Job *jobs, int32_t njobs, const char *x, int64_t x_stride,
-                             hipStream_t s);
 
 // llama.cpp's blocks: the tables from the codebooks row; a token's sums of 16 and 8 after its scales (count tokens,
 // frame apart); a row as float32; the products (jobs of the sb kinds, 1..4 tokens, up to kMaxJobs a launch); the

@@ -166,3 +166,18 @@ def test_job_path_keeps_tile_offsets_in_32_bits(pkg):
     assert L.hq_job_path(sbr, n, 64, 1 << 24, 4096) == 0  # the blocks' tile: frames under 16 MiB
     assert L.hq_job_path(sbr, n, 64, (1 << 24) - 16, 4096) == 1
     assert L.hq_job_path(3, n, 64, frame, frame) == -1  # attention is not a kind run here
+
+
+def test_matmuls_refuses_two_frames(pkg):
+    """hq_matmuls readies each token's bytes and scales one frame apart (the reference's S): a job whose a and b
+    advance by different strides is refused on the host, as are jobs of two inputs."""
+    from pyodide_llm_amd import jobs
+    L = pkg.library()
+    two = jobs.job("matmul_q8", 16, 16, 4096, 16, 16, 0, 64, rows=4, count=2, os=16, as_=256, bs=512)
+    assert jobs.matmuls(L, 16, 256, [two]) == pkg.HQ_ERR_ARGUMENT
+    assert "one frame" in L.hq_last_error_message().decode()
+    a = jobs.job("matmul_q8r", 16, 16, 4096, 16, 16, 16, 64, rows=4)
+    b = jobs.job("matmul_q8r", 16, 16, 4096, 16, 16, 16, 128, rows=4)
+    assert jobs.matmuls(L, 16, 256, [a, b]) == pkg.HQ_ERR_ARGUMENT
+    assert "one input" in L.hq_last_error_message().decode()
+    L.hq_clear_error()

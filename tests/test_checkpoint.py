@@ -20,65 +20,78 @@ def ck(pkg):
 def test_published_sizes_of_stories15m(ck):
     """src/models/built.ts:26, 45 (and tests/models-check.ts:183): karpathy/tinyllamas' stories15M is 60816028
     bytes as float32 and 17101468 as the reference's int8"""
-    rows = ck.tensor_rows(STORIES15M)
-    assert ck.file_size(rows, "float32") == 60816028
-    assert ck.file_size(rows, "int8") == 17101468
-    assert ck.checkpoint_dtype(STORIES15M, 60816028) == "float32"
-    assert ck.checkpoint_dtype(STORIES15M, 17101468) == "int8"
+    shape = ck.read_header(STORIES15M)
+    assert ck.file_bytes(shape, "float32") == 60816028
+    assert ck.file_bytes(shape, "int8") == 17101468
+    assert ck.storage_of(shape, 60816028) == "float32"
+    assert ck.storage_of(shape, 17101468) == "int8"
 
 
 def test_sizes_follow_the_layout(ck):
     """tests/test_checkpoint_dtype.py:32-36's case, and checkpoint.py:160-167's closed forms: with M values in the
     matrices and V in the vectors a file is 1.125 M + 4 V (int8, groups of 32), 0.875 M + 4 V (int6), 0.265625 M + 4 V
     (ternary), 0.140625 M + 4 V (binary), besides the header"""
-    header = (64, 172, 3, 8, 2, -300, 128)
-    floats = sum(int(np.prod(r.shape)) for r in ck.tensor_rows(header))
-    assert ck.checkpoint_dtype(header, 28 + 4 * floats) == "float32"
-    assert ck.checkpoint_dtype(list(header), 28 + 2 * floats) == "float16"
-    header = (128, 384, 2, 4, 4, -512, 64)
-    rows = ck.tensor_rows(header)
-    M = sum(int(np.prod(r.shape)) for r in rows if r.role != ck.VECTOR and r.role != ck.TABLE)
-    V = sum(int(np.prod(r.shape)) for r in rows if r.role == ck.VECTOR)
+    shape = ck.read_header((64, 172, 3, 8, 2, -300, 128))
+    floats = sum(int(np.prod(dims)) for _, _, dims in ck.llama_tensors(shape))
+    assert ck.storage_of(shape, 28 + 4 * floats) == "float32"
+    assert ck.storage_of(ck.read_header([64, 172, 3, 8, 2, -300, 128]), 28 + 2 * floats) == "float16"
+    shape = ck.read_header((128, 384, 2, 4, 4, -512, 64))
+    tensors = ck.llama_tensors(shape)
+    M = sum(int(np.prod(dims)) for _, what, dims in tensors if what == ck.MATRIX)
+    V = sum(int(np.prod(dims)) for _, what, dims in tensors if what == ck.NORM)
     for dtype, per in (("int8", 1.125), ("int6", 0.875), ("ternary", 0.265625), ("binary", 0.140625)):
-        size = ck.file_size(rows, dtype)
+        size = ck.file_bytes(shape, dtype)
         assert size == 28 + per * M + 4 * V, dtype
-        assert ck.checkpoint_dtype(header, size) == dtype
+        assert ck.storage_of(shape, size) == dtype
+
+
+def test_packed_storages_need_whole_groups_and_aligned_ends(ck):
+    """a packed storage holds only rows of whole groups (int6: 32, ternary and binary: 128), and tensors whose bytes
+    end on 4 (dtypes.py:81-85: an odd number of float16 scales would leave the next tensor on 2)"""
+    assert ck.file_bytes(ck.read_header((96, 256, 1, 4, 4, 256, 16)), "ternary") is None  # rows of 96
+    assert ck.file_bytes(ck.read_header((96, 256, 1, 4, 4, 256, 16)), "int6") is not None
+    # dim 128, vocab 129: the embedding has 129 float16 scales (258 bytes): not on 4
+    assert ck.file_bytes(ck.read_header((128, 256, 1, 4, 4, 129, 16)), "binary") is None
+    assert ck.file_bytes(ck.read_header((128, 256, 1, 4, 4, 130, 16)), "binary") is not None
+    assert ck.file_bytes(ck.read_header((40, 64, 1, 4, 4, 10, 16)), "int8") is not None  # groups of 8
 
 
 @pytest.mark.parametrize("size", [0, 27, 1000, 123456789])
 def test_a_file_of_another_size_is_refused(ck, size):
-    with pytest.raises(ValueError, match="not a llama2.c checkpoint"):
-        ck.checkpoint_dtype(STORIES15M, size)
+    with pytest.raises(ValueError, match="refused: a file of"):
+        ck.storage_of(ck.read_header(STORIES15M), size)
 
 
-@pytest.mark.parametrize("header", [(0, 0, 0, 0, 0, 0, 0), (32, 64, 2, 5, 5, 100, 16), (32, 64, 2, 4, 3, 100, 16),
-                                    (-32, 64, 2, 4, 4, 100, 16), (1885434739, 1, 1, 1, 1, 1, 1)])
-def test_a_header_that_makes_no_sense_is_refused(ck, header):
-    """tests/test_checkpoint_dtype.py:74-78's headers"""
-    with pytest.raises(ValueError, match="not a llama2.c checkpoint"):
-        ck.checkpoint_dtype(header, 1 << 20)
+@pytest.mark.parametrize("header, field", [((0, 0, 0, 0, 0, 0, 0), "dim"), ((32, 64, 2, 5, 5, 100, 16), "heads"),
+                                           ((32, 64, 2, 4, 3, 100, 16), "kv_heads"), ((-32, 64, 2, 4, 4, 100, 16), "dim"),
+                                           ((1885434739, 1, 1, 1, 1, 1, 1), "dim"),
+                                           ((32, 64, 4096, 4, 4, 100, 16), "layers")])
+def test_a_header_that_makes_no_sense_is_refused(ck, header, field):
+    """tests/test_checkpoint_dtype.py:74-78's headers, each refused by the field that is wrong"""
+    with pytest.raises(ValueError, match=f"refused: header (field )?{field} ="):
+        ck.read_header(header)
 
 
 def test_int8_groups_follow_the_row(ck):
     """packing.py:32-37: 32, or the largest power of two below it that divides the row"""
-    assert [ck.group32(n) for n in (288, 768, 48, 40, 36, 7)] == [32, 32, 16, 8, 4, 1]
+    assert [ck.int8_group(n) for n in (288, 768, 48, 40, 36, 7)] == [32, 32, 16, 8, 4, 1]
 
 
 @pytest.mark.parametrize("dtype", ["float32", "float16", "int8", "int6", "ternary", "binary"])
 @pytest.mark.parametrize("shared", [True, False])
-def test_places_match_an_independent_writer(ck, dtype, shared):
+def test_spans_match_an_independent_writer(ck, dtype, shared):
     header = (128, 384, 2, 4, 2, 256 if shared else -256, 32)
     data, where = checkpoints.write(header, dtype, np.random.default_rng(1))
-    rows = ck.tensor_rows(header)
-    assert ck.file_size(rows, dtype) == len(data)
-    assert ck.checkpoint_dtype(header, len(data)) == dtype
-    places = {p.row.name: p for p in ck.placed(rows, dtype) if p.kind}
-    assert set(places) == set(where)
+    shape = ck.read_header(header)
+    assert ck.file_bytes(shape, dtype) == len(data)
+    assert ck.storage_of(shape, len(data)) == dtype
+    table = {s.name: s for s in ck.spans(shape, dtype)}
+    assert set(table) == set(where)
     for name, (offset, scales, size) in where.items():
-        p = places[name]
-        assert (p.offset, p.size) == (offset, size), name
+        s = table[name]
+        assert (s.at, s.size) == (offset, size), name
         if scales is not None:
-            assert p.scales == scales, name
+            assert s.scales == scales, name
 
 
 def test_outlier_channels(ck):

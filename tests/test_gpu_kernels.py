@@ -690,7 +690,7 @@ def test_phase_matches_single_calls(pkg, k, arena, oracle):
         assert same_bits(arena.get(addr, F, want.size), want)
 
 
-# ---- hq_matmuls: quantize_x in the products' launch (relaxed kinds), ready() + phase for the others ----------
+# ---- hq_matmuls: ready() into the jobs' a / b, then the phase ------------------------------------------------
 @pytest.mark.parametrize("tokens", [1, 2, 3, 4, 7])
 @pytest.mark.parametrize("n", [288, 4096, 17408])
 def test_matmuls_relaxed(pkg, arena, oracle, tokens, n):
@@ -712,7 +712,7 @@ def test_matmuls_relaxed(pkg, arena, oracle, tokens, n):
         ws = (np.abs(rng.standard_normal(rows * ng)) * 0.02 / 127).astype(F)
         os_ = 4 * rows
         out = arena.alloc(os_ * tokens, fill=np.full(rows * tokens, -7, F))
-        scratch = arena.alloc(tokens * 2 * n)  # where ready() would put xq / xs (unused when fused)
+        scratch = arena.alloc(tokens * 2 * n)  # where ready() puts xq / xs
         wca = 0 if kind == "matmul_q8r_derived" else arena.put(wc)
         name = "matmul_q6r" if six else "matmul_q8r"
         table.append(jobs.job(name, out, scratch, scratch + n, arena.put(wbytes), arena.put(ws), wca, n, rows=rows,
@@ -721,23 +721,26 @@ def test_matmuls_relaxed(pkg, arena, oracle, tokens, n):
             q, s = oracle.quantize_x(x[t], 64)
             full = (oracle.matmul_q6r if six else oracle.matmul_q8r)(q, s, wbytes, ws, wc, n)
             wants.append((out + t * os_, full, f"{kind} token {t}"))
+            wants.append((scratch + t * 2 * n, q.view(np.int8), f"{kind} xq of token {t}"))
+            wants.append((scratch + t * 2 * n + n, s, f"{kind} xs of token {t}"))
     L = pkg.library()
     assert jobs.matmuls(L, ax, 4 * n, table) == 0, L.hq_last_error_message()
     for addr, want, what in wants:
-        got = arena.get(addr, F, want.size)
+        got = arena.get(addr, want.dtype, want.size)
         assert same_bits(got, want), f"{what}: {first_difference(got, want)}"
 
 
 @pytest.mark.parametrize("tokens", [1, 3])
 def test_matmuls_relaxed_many_tiles(pkg, arena, oracle, tokens):
-    """more 8-row tiles than the fused launch has blocks (a few a CU): every block quantizes once and then takes
-    several tiles, across the boundary of two jobs, with the groups past the fours (n = 320: 10 groups)"""
+    """jobs of tens of thousands of rows (thousands of 8-row tiles) sharing one pair of a / b, across the boundary
+    of two jobs of a launch, with the groups past the fours (n = 320: 10 groups)"""
     from pyodide_llm_amd import jobs
     rng = np.random.default_rng(900 + tokens)
     n = 320
     ng = n // 32
     x = rng.standard_normal((tokens, n)).astype(F)
     ax = arena.put(x)
+    scratch = arena.alloc(tokens * 2 * n)  # every job's a / b
     table, wants = [], []
     for name, rows, derived in (("matmul_q8r", 30011, False), ("matmul_q8r", 9000, False),
                                 ("matmul_q8r", 25003, True), ("matmul_q6r", 14000, False)):
@@ -751,7 +754,6 @@ def test_matmuls_relaxed_many_tiles(pkg, arena, oracle, tokens):
         ws = (np.abs(rng.standard_normal(rows * ng)) * 0.02 / 127).astype(F)
         os_ = 4 * rows
         out = arena.alloc(os_ * tokens, fill=np.full(rows * tokens, -7, F))
-        scratch = arena.alloc(tokens * 2 * n)
         table.append(jobs.job(name, out, scratch, scratch + n, arena.put(wbytes), arena.put(ws),
                               0 if derived else arena.put(wc), n, rows=rows, count=tokens, os=os_, as_=2 * n,
                               bs=2 * n))

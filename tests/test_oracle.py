@@ -739,3 +739,38 @@ def test_matmul_sbr_order_and_integers(oracle, sb_setup, name):
     for tk, (q, area) in enumerate(toks):
         want = oracle.matmul_sbr(q, area, w, tab, n, t)
         assert np.array_equal(out[tk * (rows + 1):tk * (rows + 1) + rows].view(np.uint32), want.view(np.uint32))
+
+
+# ---- the CPU baseline's vectorised kernel (fast.c) gives the oracle's numbers -----------------------------------
+@pytest.mark.parametrize("ng", [1, 3, 4, 7, 13, 128, 448])
+def test_fast_q8r_is_the_oracle(oracle, ng):
+    """fast.c's AVX2 matmul_q8r (bench.py's CPU baseline) against oracle.c's scalar one, to the bit: random groups
+    and the extremes of the relaxed form's pairs (activation 127 by weight -128, twice, in every pair: 2^15 - 256,
+    no saturation of the 16-bit pair sums), rows past the quads, the groups past the fours"""
+    rng = np.random.default_rng(ng)
+    n, rows = 32 * ng, 11
+    w = rng.integers(-128, 128, rows * n).astype(np.int8)
+    w[:n] = -128
+    xq, xs = oracle.quantize_x(rng.standard_normal(n).astype(F), 64)
+    xq[: min(n, 64)] = 127
+    ws = (np.abs(rng.standard_normal(rows * ng)) * 0.02 / 127).astype(F)
+    wc = oracle.int8_sums(w)
+    want = oracle.matmul_q8r(xq, xs, w, ws, wc, n)
+    got = oracle.fast_matmul_q8r(xq, xs, w, ws, wc, n)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("count, rows", [(1, 4), (4, 8), (6, 13), (9, 3)])
+def test_fast_q8r_tile_is_the_oracle(oracle, count, rows):
+    """the tile's 4 x 4 quads, the rows and tokens past them: every (row, token) the oracle's matmul_q8r"""
+    rng = np.random.default_rng(100 * count + rows)
+    ng = 13
+    n = 32 * ng
+    w = rng.integers(-128, 128, rows * n).astype(np.int8)
+    ws = (np.abs(rng.standard_normal(rows * ng)) * 0.02 / 127).astype(F)
+    wc = oracle.int8_sums(w)
+    qs = [oracle.quantize_x(rng.standard_normal(n).astype(F), 64) for _ in range(count)]
+    got = oracle.fast_matmul_q8r_tile(np.stack([q for q, _ in qs]), np.stack([s for _, s in qs]), w, ws, wc, n, count)
+    for t, (q, s) in enumerate(qs):
+        want = oracle.matmul_q8r(q, s, w, ws, wc, n)
+        assert np.array_equal(got[t].view(np.uint32), want.view(np.uint32)), t
