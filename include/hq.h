@@ -236,6 +236,17 @@ int32_t hq_phase(const double *jobs, int32_t count, int32_t stride, void *stream
  * give, and a / b hold the readied activations after the call. */
 int32_t hq_matmuls(const void *x, int32_t x_stride, const double *jobs, int32_t count, int32_t stride, void *stream);
 
+/* hq_matmuls without the caller's staging, for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops, harnesses that forbid hipMalloc); it has no counterpart in the reference.  The same jobs
+ * and outputs, but the jobs' a, b, as and bs are not read: the input is readied into a staging area the library
+ * holds on each device (a static device array of 4 MiB, looked up by hq_init or by the first call on a device), a
+ * token's activations round_up(n, 256) + round_up(n / 2, 256) bytes apart.  Refused (HQ_ERR_ARGUMENT) when the
+ * tokens do not fit: count x that frame must be at most 4 MiB (n = 4096: 682 tokens).  No device memory is
+ * allocated or freed.  Every call on one device shares that device's staging: calls that overlap on one device
+ * (other streams, other threads) race; calls in one stream follow each other. */
+int32_t hq_matmuls_static(const void *x, int32_t x_stride, const double *jobs, int32_t count, int32_t stride,
+                          void *stream);
+
 /* Which kernels take a job of `kind` (hq_phase's numbers), row length n and `count` tokens whose activations are
  * frame bytes apart and their scales sframe: 1 the matrix-core tile (16 tokens or more, and every offset within a
  * tile of 64 tokens, 128 for llama.cpp's blocks, and of 128 rows below 4 GiB), 0 the token kernel (4 tokens a

@@ -78,6 +78,35 @@ int32_t ensure_device() {
 
 bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
+// hq_matmuls_static's staging of the readied activations: a device array of the library's own, one copy on each
+// device (the runtime makes it when it loads the library's code there; it lives until the process ends).  In host
+// code `scratch` names a host-side stand-in: its device address is looked up once a device (hipGetSymbolAddress,
+// with that device current) and only that address reaches a kernel.
+constexpr int64_t kStagingBytes = (int64_t)4 << 20;
+static __device__ __align__(256) char scratch[kStagingBytes];
+std::atomic<char *> g_scratch[64];
+
+int32_t scratch_of(char **out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(HQ_ERR_DEVICE, "no HIP device: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= 64) return fail(HQ_ERR_DEVICE, "device %d out of range", dev);
+  char *p = g_scratch[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_init_mutex);
+    p = g_scratch[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      void *at = nullptr;
+      e = hipGetSymbolAddress(&at, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !at) return fail(HQ_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+      p = (char *)at;
+      g_scratch[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return HQ_OK;
+}
+
 hipStream_t stream_of(void *s) { return (hipStream_t)s; }
 
 constexpr int kKinds = 15;  // kinds are numbered by their place in WORK: the last one run here is matmul_b1 (14)
@@ -287,7 +316,9 @@ int32_t hq_job_path(int32_t kind, int32_t n, int32_t count, int64_t frame, int64
 
 int32_t hq_init(void) {
   g_error = HQ_OK;
-  return ensure_device();
+  if (int32_t st = ensure_device()) return st;
+  char *staging = nullptr;  // hq_matmuls_static's staging on this device, looked up now (outside any capture)
+  return scratch_of(&staging);
 }
 
 int32_t hq_set_stream(void *stream) {
@@ -516,8 +547,15 @@ int32_t hq_binary_x_ex(void *out, void *xs, const void *x, int32_t n, void *bad,
 namespace {
 
 // [kind, out, a, b, a4, a5, a6, a7, a8, rows, count, os, as, bs] (src/runtime/jobs.ts:46, 207-333) -> a Job
+// the frame of a token's readied activations in a staging area: n bytes, then the largest scale area a kind reads
+// (llama.cpp's blocks: n/8 of scales, n/8 of sums of 16, n/4 of sums of 8), each from a 256-byte boundary
+int64_t staging_bytes_of(int32_t n) { return ((int64_t)n + 255) & ~(int64_t)255; }
+int64_t staging_frame(int32_t n) { return staging_bytes_of(n) + (((int64_t)n / 2 + 255) & ~(int64_t)255); }
+
+// staging (not NULL): every job's a / b are the staging's (its tokens staging_frame(n) apart) and the table's a, b,
+// as and bs are not read
 int32_t parse_jobs(const double *jobs, int32_t count, int32_t stride, std::vector<hq::Job> by_kind[kKinds],
-                   const char *who) {
+                   const char *who, const char *staging = nullptr) {
   if (count < 0 || (count > 0 && (!jobs || stride < 14)))
     return fail(HQ_ERR_ARGUMENT, "%s: count %d, stride %d (a job has 14 numbers at least)", who, count, stride);
   for (int32_t i = 0; i < count; i++) {
@@ -548,6 +586,10 @@ int32_t parse_jobs(const double *jobs, int32_t count, int32_t stride, std::vecto
       break;
     case hq::SB: k = hq::SB; j.type = (int32_t)e[6]; break;
     default: return fail(HQ_ERR_KIND, "%s: job %d is of kind %d, which this library does not run", who, i, kind);
+    }
+    if (staging) {
+      j.xq = staging, j.xs = staging + staging_bytes_of(j.n > 0 ? j.n : 0);
+      j.frame = j.sframe = staging_frame(j.n > 0 ? j.n : 0);
     }
     if (int32_t st = check_job(k, j, hq::binary_kind(k) ? 2 : 3)) return st;
     by_kind[kind].push_back(j);
@@ -593,9 +635,7 @@ int32_t matmuls_alike(const void *x, int32_t x_stride, std::vector<hq::Job> by_k
   if (!x) return fail(HQ_ERR_NULL, "%s: x is NULL", who);
   if (!aligned(x, 16) || (tokens > 1 && (x_stride < 0 || x_stride % 16)))
     return fail(HQ_ERR_ALIGNMENT, "%s: x or x_stride not 16-byte aligned", who);
-  // the staging's token frame: n bytes, then the largest scale area a kind reads (llama.cpp's blocks: n/8 of
-  // scales, n/8 of sums of 16, n/4 of sums of 8), each from a 256-byte boundary
-  const int64_t qbytes = ((int64_t)n + 255) & ~(int64_t)255, frame = qbytes + (((int64_t)n / 2 + 255) & ~(int64_t)255);
+  const int64_t qbytes = staging_bytes_of(n), frame = staging_frame(n);
   if (staging && (int64_t)tokens * frame > staging_bytes)
     return fail(HQ_ERR_ARGUMENT, "%s: %d tokens of %d activations take %lld bytes of staging (at most %lld)", who,
                 tokens, n, (long long)(tokens * frame), (long long)staging_bytes);
@@ -646,6 +686,24 @@ int32_t hq_matmuls(const void *x, int32_t x_stride, const double *jobs, int32_t 
   std::vector<hq::Job> by_kind[kKinds];
   if (int32_t st = parse_jobs(jobs, count, stride, by_kind, "hq_matmuls")) return st;
   return matmuls_alike(x, x_stride, by_kind, nullptr, 0, stream_of(stream), "hq_matmuls");
+}
+
+int32_t hq_matmuls_static(const void *x, int32_t x_stride, const double *jobs, int32_t count, int32_t stride,
+                          void *stream) {
+  g_error = HQ_OK;
+  std::vector<hq::Job> by_kind[kKinds];
+  // parsed against a stand-in (the staging's device address is looked up below, after the host checks)
+  char *const stand_in = (char *)(uintptr_t)4096;
+  if (int32_t st = parse_jobs(jobs, count, stride, by_kind, "hq_matmuls_static", stand_in)) return st;
+  for (auto &list : by_kind)
+    for (const hq::Job &j : list)
+      if ((int64_t)j.count * staging_frame(j.n) > kStagingBytes)
+        return fail(HQ_ERR_ARGUMENT, "hq_matmuls_static: %d tokens of %d activations take %lld bytes of staging (at "
+                    "most %lld)", j.count, j.n, (long long)(j.count * staging_frame(j.n)), (long long)kStagingBytes);
+  if (count == 0) return HQ_OK;
+  char *staging = nullptr;
+  if (int32_t st = scratch_of(&staging)) return st;
+  return matmuls_alike(x, x_stride, by_kind, staging, kStagingBytes, stream_of(stream), "hq_matmuls_static");
 }
 
 // ---- the ceilings ---------------------------------------------------------------------------------------------

@@ -181,3 +181,16 @@ def test_matmuls_refuses_two_frames(pkg):
     assert jobs.matmuls(L, 16, 256, [a, b]) == pkg.HQ_ERR_ARGUMENT
     assert "one input" in L.hq_last_error_message().decode()
     L.hq_clear_error()
+
+
+def test_matmuls_static_refuses_more_than_its_staging(pkg):
+    """hq_matmuls_static stages a token's activations round_up(n, 256) + round_up(n / 2, 256) bytes apart in 4 MiB:
+    more tokens are refused on the host, before any device is touched"""
+    from pyodide_llm_amd import jobs
+    L = pkg.library()
+    n = 4096
+    fits = (4 << 20) // (4096 + 2048)
+    job = jobs.job("matmul_q8r", 4096, 0, 0, 4096, 4096, 0, n, rows=8, count=fits + 1, os=32)
+    assert L.hq_matmuls_static(4096, 4 * n, jobs.table([job]), 1, jobs.JOB, None) == pkg.HQ_ERR_ARGUMENT
+    assert "staging" in L.hq_last_error_message().decode()
+    L.hq_clear_error()
