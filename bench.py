@@ -751,15 +751,16 @@ def profile(torch, pkg, args):
     """--profile WHAT: WHAT's launches alone, issued directly (no graph) `steps` times after `warmup` untimed ones,
     for rocprofv3's counters (a counter pass serialises the dispatches):
       gemm     config 3's prefill, M = 2048 through one layer's 7 matrices, corrections derived (gemm_relaxed)
+      gemm_wc  the same with the caller's corrections (int8_sums')
       gemv     one decode step's products at M = 1 (129 hq_phase launches of gemv_relaxed<8,1,...>)
       gemv_m4  the same at M = 4 (gemv_relaxed<8,4,...>)
     Prints one JSON line naming what ran."""
     from pyodide_llm_amd import jobs
     lib = pkg.library()
-    if args.profile == "gemm":
+    if args.profile in ("gemm", "gemm_wc"):
         run, launches, _ = gemm_workload(torch, pkg)
         for _ in range(args.warmup + args.steps):
-            run(False)
+            run(args.profile == "gemm_wc")
     else:
         layers, head, phases = build_decode(torch, jobs, lib)
         if args.profile == "gemv":
@@ -795,7 +796,7 @@ def main():
     ap.add_argument("--configs", action="store_true",
                     help="also measure binary weights at config 4's shapes, llama.cpp's blocks and the outlier "
                          "channels")
-    ap.add_argument("--profile", choices=("gemm", "gemv", "gemv_m4"),
+    ap.add_argument("--profile", choices=("gemm", "gemm_wc", "gemv", "gemv_m4"),
                     help="only run one workload's launches, for rocprofv3's counters")
     ap.add_argument("--calibrate", action="store_true",
                     help="only run kernels of known traffic (for scaling rocprofv3's FETCH_SIZE / WRITE_SIZE)")

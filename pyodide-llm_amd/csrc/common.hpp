@@ -68,17 +68,11 @@ HQ_DEV int32_t trunc_sat(float v) {
   return (int32_t)v;
 }
 
-// kernels/kernel/quantize.ts:124-151 for one group of 32 float32 values at p (16-byte aligned): its 32 bytes (eight
-// dwords, values 4i..4i+3 in dword i) and its scale.  groupMax (quantize.ts:10-19): lane j's maximum of |values 4i + j|
-// with a NaN kept (a non-negative float's bits order as the float does, and every NaN's bits are above +inf's), then
-// lanes 1..3 compared with lane 0's in order, where a NaN is passed over.
-HQ_DEV void quantize_group(const float *p, int32_t bias, uint32_t q[8], float &scale) {
-  float v[32];
-#pragma unroll
-  for (int i = 0; i < 8; i++) {
-    const float4 f = ((const float4 *)p)[i];
-    v[4 * i] = f.x; v[4 * i + 1] = f.y; v[4 * i + 2] = f.z; v[4 * i + 3] = f.w;
-  }
+// kernels/kernel/quantize.ts:124-151 for one group of 32 float32 values v: its 32 bytes (eight dwords, values
+// 4i..4i+3 in dword i) and its scale.  groupMax (quantize.ts:10-19): lane j's maximum of |values 4i + j| with a NaN
+// kept (a non-negative float's bits order as the float does, and every NaN's bits are above +inf's), then lanes 1..3
+// compared with lane 0's in order, where a NaN is passed over.
+HQ_DEV void quantize_values(const float v[32], int32_t bias, uint32_t q[8], float &scale) {
   uint32_t m[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
   for (int i = 0; i < 8; i++)
@@ -104,6 +98,17 @@ HQ_DEV void quantize_group(const float *p, int32_t bias, uint32_t q[8], float &s
     }
     q[i] = d;
   }
+}
+
+// the same for the group at p (16-byte aligned)
+HQ_DEV void quantize_group(const float *p, int32_t bias, uint32_t q[8], float &scale) {
+  float v[32];
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const float4 f = ((const float4 *)p)[i];
+    v[4 * i] = f.x; v[4 * i + 1] = f.y; v[4 * i + 2] = f.z; v[4 * i + 3] = f.w;
+  }
+  quantize_values(v, bias, q, scale);
 }
 
 // v_perm_b32: byte i of the result is byte sel.i of {hi:lo} (0..3 from lo, 4..7 from hi)

@@ -275,11 +275,18 @@ struct Relaxed {
       } else if (p < P) {
         const int q = p - NWP - 8, kind = q / SPK, i = q % SPK;
         const bool tokens = kind == NSK - 1;
-        char *dst = tokens ? (char *)&S.xs[16 * i][0] : (kind == 0 || !WC) ? (char *)&S.ws[16 * i][0]
-                                                                           : (char *)&S.wc[16 * i][0];
-        const __amdgpu_buffer_rsrc_t r = tokens ? rxs : (kind == 0 || !WC) ? rws : rwc;
-        if (WIDE) dma16(r, dst, off[k], s * QG * 4);
-        else dma4(r, dst, off[k], s * QG * 4);
+        // a branch for each resource: a resource chosen by a select is a per-lane value to the compiler, which then
+        // loops over its lanes (v_readfirstlane) around every load (measured 28 % of the launch with wc)
+        if (tokens) {
+          if (WIDE) dma16(rxs, &S.xs[16 * i][0], off[k], s * QG * 4);
+          else dma4(rxs, &S.xs[16 * i][0], off[k], s * QG * 4);
+        } else if (kind == 0 || !WC) {
+          if (WIDE) dma16(rws, &S.ws[16 * i][0], off[k], s * QG * 4);
+          else dma4(rws, &S.ws[16 * i][0], off[k], s * QG * 4);
+        } else {
+          if (WIDE) dma16(rwc, &S.wc[16 * i][0], off[k], s * QG * 4);
+          else dma4(rwc, &S.wc[16 * i][0], off[k], s * QG * 4);
+        }
       }
     }
   }
