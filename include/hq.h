@@ -97,6 +97,15 @@ void matmul_b1r_tile(void *xout, const void *xq, const void *xs, const void *wq,
  * returns 1 where a value is not plus or minus its group's largest (or the call failed: hq_last_error), else 0.
  * It waits for the library's stream to know. */
 int32_t binary_x(void *out, void *xs, const void *x, int32_t n);
+/* kernels/kernel/quantize.ts:161-182: n float32 values at x (device; groups of 32) -> out (24 bytes a group: the six
+ * bits v of each value, v = round(value / scale) in -32..31 with scale = the group's largest |value| / 31, packed as
+ * kernels/six.ts reads them) and xs (scale / 4, float32, a group) */
+void quantize6_x(void *out, void *xs, const void *x, int32_t n);
+/* kernels/kernel/quantize.ts:197-225: n float32 values at x (device; groups of 128) -> out (n/4 bytes: the code
+ * sign + 1 of value j at bits 2 (j & 3) of byte j >> 2) and xs (the largest |value| of every group, float32);
+ * returns 1 where a value is neither 0 nor plus or minus its group's largest (or the call failed: hq_last_error),
+ * else 0.  It waits for the library's stream to know. */
+int32_t ternary_x(void *out, void *xs, const void *x, int32_t n);
 
 /* llama.cpp's blocks of 256 weights (kernels/blocks/: Q2_K 10, Q4_K 12, IQ2_XXS 16, IQ2_XS 17, IQ3_XXS 18, IQ1_S 19,
  * IQ3_S 21, IQ2_S 22, IQ4_XS 23, IQ1_M 29; a row is whole blocks, n a multiple of 256; w 2-byte aligned).
@@ -187,6 +196,9 @@ int32_t hq_matmul_b1r_tile_ex(void *xout, const void *xq, const void *xs, const 
 /* binary_x on a stream, without waiting: `bad` (device, 4-byte aligned; may be NULL) is set to 1 where a value is
  * refused and left as it was otherwise, so the caller clears it first */
 int32_t hq_binary_x_ex(void *out, void *xs, const void *x, int32_t n, void *bad, void *stream);
+/* quantize6_x on a stream; ternary_x on a stream, without waiting (`bad` as hq_binary_x_ex's) */
+int32_t hq_quantize6_x_ex(void *out, void *xs, const void *x, int32_t n, void *stream);
+int32_t hq_ternary_x_ex(void *out, void *xs, const void *x, int32_t n, void *bad, void *stream);
 int32_t hq_sb_tables_ex(void *area, const void *codebooks, void *stream);
 int32_t hq_matmul_sbr_ex(void *xout, const void *xq, const void *xs, const void *w, const void *tab, int32_t n,
                          int32_t r0, int32_t r1, int32_t type, void *stream);

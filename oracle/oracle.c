@@ -360,6 +360,68 @@ int32_t o_binary_x(uint8_t *out, float *xs, const float *x, int32_t n) {
   return bad;
 }
 
+/* ---- the converters' packers: kernels/kernel/quantize.ts:153-225 ---------------------------------------------- */
+
+/* quantize6_x (quantize.ts:161-182): per group of 32, scale = groupMax / 31 (groupMax as quantize_x's), xs =
+ * scale / 4 (a multiply by 0.25), v = clamp(trunc_sat(nearest(value * (1 / scale))), -32, 31) (six(), 158-160), and
+ * the six bits of v packed into 24 bytes: byte j (j < 16) the low nibbles of values j and j + 16, byte 16 + k
+ * (k < 8) the top two bits of values k, k + 8, k + 16, k + 24 at bits 0, 2, 4, 6 (the shuffle at 177-179). */
+void o_quantize6_x(uint8_t *out, float *xs, const float *x, int32_t n) {
+  for (int32_t g = 0; g < n; g += GS) {
+    float m[4];
+    for (int j = 0; j < 4; j++) {
+      float v = fabsf(x[g + j]);
+      for (int i = 1; i < 8; i++) v = wasm_max(v, fabsf(x[g + 4 * i + j]));
+      m[j] = v;
+    }
+    float amax = m[0];
+    if (m[1] > amax) amax = m[1];
+    if (m[2] > amax) amax = m[2];
+    if (m[3] > amax) amax = m[3];
+    const float scale = amax / 31.0f;
+    xs[g / GS] = scale * 0.25f;
+    const float inv = scale > 0 ? 1.0f / scale : 0.0f;
+    uint8_t six[GS];
+    for (int j = 0; j < GS; j++) {
+      int32_t v = trunc_sat(rintf(x[g + j] * inv));
+      if (v > 31) v = 31;
+      if (v < -32) v = -32;
+      six[j] = (uint8_t)((uint32_t)v & 63u);
+    }
+    uint8_t *at = out + (g / GS) * 24;
+    for (int j = 0; j < 16; j++) at[j] = (uint8_t)((six[j] & 15) | ((six[j + 16] & 15) << 4));
+    for (int k = 0; k < 8; k++)
+      at[16 + k] = (uint8_t)((six[k] >> 4) | ((six[k + 8] >> 4) << 2) | ((six[k + 16] >> 4) << 4) | ((six[k + 24] >> 4) << 6));
+  }
+}
+
+/* ternary_x (quantize.ts:197-225): per group of 128, the scale is groupLargest's (186-191: lane j's f32x4.max of
+ * |values 4i + j|, then max(max(l0, l1), max(l2, l3)), NaN kept), the code of a value 1 + (v > 0) - (v < 0) (a NaN
+ * gets 1) at bits 2 (j & 3) of byte j >> 2; the result is 1 where a value is neither 0 nor of the scale's size */
+int32_t o_ternary_x(uint8_t *out, float *xs, const float *x, int32_t n) {
+  int32_t bad = 0;
+  for (int32_t g = 0; g < n; g += 128) {
+    const float *p = x + g;
+    float lane[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = 0; i < 32; i++)
+      for (int j = 0; j < 4; j++) lane[j] = wasm_max(lane[j], fabsf(p[4 * i + j]));
+    const float scale = wasm_max(wasm_max(lane[0], lane[1]), wasm_max(lane[2], lane[3]));
+    xs[g >> 7] = scale;
+    uint8_t *to = out + (g >> 2);
+    for (int b = 0; b < 32; b++) {
+      uint32_t byte = 0;
+      for (int q = 0; q < 4; q++) {
+        const float v = p[4 * b + q];
+        const uint32_t code = 1u + (v > 0.0f ? 1u : 0u) - (v < 0.0f ? 1u : 0u);
+        byte |= code << (2 * q);
+        if (!(fabsf(v) == scale || v == 0.0f)) bad = 1;
+      }
+      to[b] = (uint8_t)byte;
+    }
+  }
+  return bad;
+}
+
 /* ---- CPU baseline: phase()-style row chunks over host threads ------------------------------------------------ */
 typedef struct {
   int32_t kind;

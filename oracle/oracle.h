@@ -66,6 +66,11 @@ void o_matmul_b1r_tile(void *xout, const void *xq, const void *xs, const uint8_t
  * where value 64h + 4c + p is not below 0) and the largest |value| of every group; 1 where a value is not plus or
  * minus its group's largest, else 0 */
 int32_t o_binary_x(uint8_t *out, float *xs, const float *x, int32_t n);
+/* kernels/kernel/quantize.ts:161-182 (quantize6_x): groups of 32 -> 24 bytes and a scale / 4 each */
+void o_quantize6_x(uint8_t *out, float *xs, const float *x, int32_t n);
+/* kernels/kernel/quantize.ts:197-225 (ternary_x): groups of 128 -> 32 bytes of codes and the largest |value|; 1 where
+ * a value is not ternary */
+int32_t o_ternary_x(uint8_t *out, float *xs, const float *x, int32_t n);
 
 /* llama.cpp's blocks of 256 weights (kernels/blocks/types.ts: Q2_K 10, Q4_K 12, IQ2_XXS 16, IQ2_XS 17, IQ3_XXS 18,
  * IQ1_S 19, IQ3_S 21, IQ2_S 22, IQ4_XS 23, IQ1_M 29): the bytes of a block of `type` (types.ts:103-106), 0 for

@@ -58,6 +58,8 @@ def lib():
             fn.argtypes, fn.restype = argtypes, None
         L.o_half.argtypes, L.o_half.restype = [ctypes.c_uint16], ctypes.c_float
         L.o_binary_x.argtypes, L.o_binary_x.restype = [p, p, p, i32], i32
+        L.o_quantize6_x.argtypes, L.o_quantize6_x.restype = [p, p, p, i32], None
+        L.o_ternary_x.argtypes, L.o_ternary_x.restype = [p, p, p, i32], i32
         L.o_sb_bytes.argtypes, L.o_sb_bytes.restype = [i32], i32
         L.o_sb_tables.argtypes, L.o_sb_tables.restype = [p, p], i32
         L.o_time_gemv.argtypes = [i32, p, p, p, p, p, p, i32, i32, i32, i32]
@@ -189,6 +191,26 @@ def binary_x(x):
     n = x.size
     out, xs = np.zeros(n // 8, np.uint8), np.zeros(n // 128, np.float32)
     bad = lib().o_binary_x(_p(out), _p(xs), _p(x), n)
+    return out, xs, bad
+
+
+def quantize6_x(x):
+    """kernels/kernel/quantize.ts:161-182: float32 x (groups of 32) -> (uint8 24 bytes a group, float32 scale / 4 a
+    group)."""
+    x = _c(x, np.float32)
+    n = x.size
+    out, xs = np.zeros(n // 32 * 24, np.uint8), np.zeros(n // 32, np.float32)
+    lib().o_quantize6_x(_p(out), _p(xs), _p(x), n)
+    return out, xs
+
+
+def ternary_x(x):
+    """kernels/kernel/quantize.ts:197-225: float32 x (groups of 128) -> (uint8 codes (n/4), float32 scales (n/128),
+    the refusal flag)."""
+    x = _c(x, np.float32)
+    n = x.size
+    out, xs = np.zeros(n // 4, np.uint8), np.zeros(n // 128, np.float32)
+    bad = lib().o_ternary_x(_p(out), _p(xs), _p(x), n)
     return out, xs, bad
 
 

@@ -52,6 +52,8 @@ REFERENCE_SIGNATURES = {
     "matmul_b1": [p, p, p, p, p, i32, i32, i32, i32],
     "matmul_b1r_tile": [p, p, p, p, p, i32, i32, i32, i32, i32, i32, i32],
     "binary_x": [p, p, p, i32],
+    "quantize6_x": [p, p, p, i32],
+    "ternary_x": [p, p, p, i32],
     "sb_tables": [p, p],
     "sums_x": [p, p, i32],
     "matmul_sbr": [p, p, p, p, p, i32, i32, i32, i32],
@@ -63,7 +65,7 @@ REFERENCE_SIGNATURES = {
     "add_columns": [p, p, p, i32, i32],
 }
 # the reference kernels that return a value (the others return nothing)
-REFERENCE_RESTYPES = {"binary_x": i32, "sb_tables": i32}
+REFERENCE_RESTYPES = {"binary_x": i32, "ternary_x": i32, "sb_tables": i32}
 
 # the library's own (include/hq.h, second block): name -> (argtypes, restype)
 OWN_SIGNATURES = {
@@ -89,6 +91,8 @@ OWN_SIGNATURES = {
     "hq_matmul_b1r_ex": ([p, p, p, p, p, i32, i32, i32, i32, p], i32),
     "hq_matmul_b1r_tile_ex": ([p, p, p, p, p, i32, i32, i32, i32, i32, i32, i32, p], i32),
     "hq_binary_x_ex": ([p, p, p, i32, p, p], i32),
+    "hq_quantize6_x_ex": ([p, p, p, i32, p], i32),
+    "hq_ternary_x_ex": ([p, p, p, i32, p, p], i32),
     "hq_sb_tables_ex": ([p, p, p], i32),
     "hq_matmul_sbr_ex": ([p, p, p, p, p, i32, i32, i32, i32, p], i32),
     "hq_matmul_sbr_tile_ex": ([p, p, p, p, p, i32, i32, i32, i32, i32, i32, i32, p], i32),

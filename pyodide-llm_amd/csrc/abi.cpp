@@ -528,6 +528,30 @@ int32_t hq_take_channels_ex(void *picked, void *x, const int32_t *channels, int3
 }
 
 // ---- binary weights from float32 (kernels/kernel/quantize.ts:232-247) -------------------------------------------
+int32_t hq_quantize6_x_ex(void *out, void *xs, const void *x, int32_t n, void *stream) {
+  g_error = HQ_OK;
+  if (n < 0 || n % 32) return fail(HQ_ERR_ARGUMENT, "quantize6_x: n = %d is not a multiple of 32", n);
+  if (n == 0) return HQ_OK;
+  if (!out || !xs || !x) return fail(HQ_ERR_NULL, "quantize6_x: a NULL pointer");
+  if (!aligned(x, 4) || !aligned(xs, 4)) return fail(HQ_ERR_ALIGNMENT, "quantize6_x: x or xs not 4-byte aligned");
+  if (int32_t st = ensure_device()) return st;
+  return hip_status(hq::launch_quantize6_x((uint8_t *)out, (float *)xs, (const float *)x, n / 32, stream_of(stream)),
+                    "quantize6_x");
+}
+
+int32_t hq_ternary_x_ex(void *out, void *xs, const void *x, int32_t n, void *bad, void *stream) {
+  g_error = HQ_OK;
+  if (n < 0 || n % 128) return fail(HQ_ERR_ARGUMENT, "ternary_x: n = %d is not a multiple of 128", n);
+  if (n == 0) return HQ_OK;
+  if (!out || !xs || !x) return fail(HQ_ERR_NULL, "ternary_x: a NULL pointer");
+  if (!aligned(x, 16) || !aligned(xs, 4) || (bad && !aligned(bad, 4)))
+    return fail(HQ_ERR_ALIGNMENT, "ternary_x: x not 16-, xs or bad not 4-byte aligned");
+  if (int32_t st = ensure_device()) return st;
+  return hip_status(hq::launch_ternary_x((uint8_t *)out, (float *)xs, (const float *)x, n / 128, (int32_t *)bad,
+                                         stream_of(stream)),
+                    "ternary_x");
+}
+
 int32_t hq_binary_x_ex(void *out, void *xs, const void *x, int32_t n, void *bad, void *stream) {
   g_error = HQ_OK;
   if (n < 0 || n % 128) return fail(HQ_ERR_ARGUMENT, "binary_x: n = %d is not a multiple of 128", n);
@@ -819,25 +843,34 @@ void sb_row(void *out, const void *w, const void *tab, int32_t n, int32_t type) 
 void add_columns(void *y, const void *rows, const void *a, int32_t count, int32_t n) {
   hq_add_columns_ex(y, rows, a, count, n, g_stream.load());
 }
-// the reference's binary_x returns its refusal: this one waits for the library's stream to give it (a word of
-// device memory the library keeps for it, one a device); 1 also when the call fails (hq_last_error says why)
-int32_t binary_x(void *out, void *xs, const void *x, int32_t n) {
+// the reference's binary_x and ternary_x return their refusal: these wait for the library's stream to give it (a
+// word of device memory the library keeps for them, one a device, cleared before each call); 1 also when the call
+// fails (hq_last_error says why)
+static int32_t refusal_of(const char *who, int32_t (*run)(void *, void *, const void *, int32_t, void *, void *), void *out,
+                   void *xs, const void *x, int32_t n) {
   static std::mutex lock;
   static int32_t *word[64];
   std::lock_guard<std::mutex> hold(lock);
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
-    fail(HQ_ERR_DEVICE, "binary_x: no device");
+    fail(HQ_ERR_DEVICE, "%s: no device", who);
     return 1;
   }
   if (!word[dev] && hip_status(hipMalloc((void **)&word[dev], 4), "hipMalloc")) return 1;
   const hipStream_t s = stream_of(g_stream.load());
   if (hip_status(hipMemsetAsync(word[dev], 0, 4, s), "hipMemsetAsync")) return 1;
-  if (hq_binary_x_ex(out, xs, x, n, word[dev], s)) return 1;
+  if (run(out, xs, x, n, word[dev], s)) return 1;
   int32_t bad = 1;
   if (hip_status(hipMemcpyAsync(&bad, word[dev], 4, hipMemcpyDeviceToHost, s), "hipMemcpyAsync")) return 1;
   if (hip_status(hipStreamSynchronize(s), "hipStreamSynchronize")) return 1;
   return bad;
 }
+int32_t binary_x(void *out, void *xs, const void *x, int32_t n) {
+  return refusal_of("binary_x", hq_binary_x_ex, out, xs, x, n);
+}
+int32_t ternary_x(void *out, void *xs, const void *x, int32_t n) {
+  return refusal_of("ternary_x", hq_ternary_x_ex, out, xs, x, n);
+}
+void quantize6_x(void *out, void *xs, const void *x, int32_t n) { hq_quantize6_x_ex(out, xs, x, n, g_stream.load()); }
 
 }  // extern "C"

@@ -42,6 +42,10 @@ hipError_t launch_six_sums(int32_t *out, const char *w, int32_t groups, hipStrea
 // binary weights from float32: groups of 128 -> 16 bytes and the largest |value| each; *bad = 1 (bad: NULL or a word
 // the caller cleared) where a value is not plus or minus its group's largest
 hipError_t launch_binary_x(uint8_t *out, float *xs, const float *x, int32_t groups, int32_t *bad, hipStream_t s);
+// int6 weights from float32: groups of 32 -> 24 bytes and the scale / 4 each; ternary weights: groups of 128 -> 32
+// bytes of codes and the largest |value|, *bad = 1 (bad: NULL or a word the caller cleared) where one is not ternary
+hipError_t launch_quantize6_x(uint8_t *out, float *xs, const float *x, int32_t groups, hipStream_t s);
+hipError_t launch_ternary_x(uint8_t *out, float *xs, const float *x, int32_t groups, int32_t *bad, hipStream_t s);
 
 // the current device's compute units (256 on an MI355X; 256 when the query fails), for grids of blocks that take
 // work in turn

@@ -1,6 +1,7 @@
 // quantize.hip — the activations' preparation and the weights' corrections:
 //   quantize_x (kernels/kernel/quantize.ts:124-151), interleave (kernels/kernel/matmul.ts:107-146),
-//   int8_sums (matmul.ts:50-58), six_sums (matmul.ts:38-46), binary_x (quantize.ts:184-247: a converter's, at load).
+//   int8_sums (matmul.ts:50-58), six_sums (matmul.ts:38-46), and the converters' packers quantize6_x, ternary_x,
+//   binary_x (quantize.ts:153-247: used at load).
 // Byte-for-byte the reference's outputs; small, latency-bound kernels (a token's activations are a few KB).
 #include "common.hpp"
 #include "launch.hpp"
@@ -166,6 +167,87 @@ __global__ __launch_bounds__(256) void binary_x_kernel(uint8_t *out, float *xs, 
 hipError_t launch_binary_x(uint8_t *out, float *xs, const float *x, int32_t groups, int32_t *bad, hipStream_t s) {
   if (groups <= 0) return hipSuccess;
   hipLaunchKernelGGL(binary_x_kernel, dim3((groups + 15) / 16), dim3(256), 0, s, out, xs, x, groups, bad);
+  return hipGetLastError();
+}
+
+// quantize6_x (quantize.ts:161-182): one group of 32 values a half-wave, lane j its value j; groupMax as
+// quantize_x's; v = clamp(trunc_sat(nearest(value / scale)), -32, 31) (six(), 158-160), its six bits packed as
+// six.ts reads them: byte j < 16 the low nibbles of values j and j + 16, byte 16 + k the top two bits of values k,
+// k + 8, k + 16, k + 24 at bits 0, 2, 4, 6; the scale stored / 4
+__global__ __launch_bounds__(256) void quantize6_kernel(uint8_t *out, float *xs, const float *x, int32_t groups) {
+  const int64_t gi = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
+  const int j = threadIdx.x & 31;
+  const bool live = gi < groups;
+  const int64_t g = live ? gi : 0;
+  const float v = x[g * GS + j];
+  float m = fabsf(v);
+  m = wasm_max_abs(m, from_lane_plus<4>(m));
+  m = wasm_max_abs(m, from_lane_plus<8>(m));
+  m = wasm_max_abs(m, __shfl_xor(m, 16, 64));
+  const float m0 = quad_lane<0>(m), m1 = quad_lane<1>(m), m2 = quad_lane<2>(m), m3 = quad_lane<3>(m);
+  float amax = m0;
+  if (m1 > amax) amax = m1;
+  if (m2 > amax) amax = m2;
+  if (m3 > amax) amax = m3;
+  const float scale = fdiv(amax, 31.0f);
+  const float inv = scale > 0.0f ? fdiv(1.0f, scale) : 0.0f;
+  int32_t q = trunc_sat(rintf(fmul(v, inv)));
+  q = q > 31 ? 31 : (q < -32 ? -32 : q);
+  const uint32_t six = (uint32_t)q & 63u;
+  // every lane reads what its byte needs from the lanes of its group (lanes j + 8, j + 16, j + 24 of the half-wave)
+  const int base = threadIdx.x & ~31;
+  const uint32_t s8 = (uint32_t)__shfl((int)six, base + ((j + 8) & 31), 64);
+  const uint32_t s16 = (uint32_t)__shfl((int)six, base + ((j + 16) & 31), 64);
+  const uint32_t s24 = (uint32_t)__shfl((int)six, base + ((j + 24) & 31), 64);
+  if (live) {
+    uint8_t *at = out + g * 24;
+    if (j < 16) at[j] = (uint8_t)((six & 15u) | ((s16 & 15u) << 4));
+    if (j < 8) at[16 + j] = (uint8_t)((six >> 4) | ((s8 >> 4) << 2) | ((s16 >> 4) << 4) | ((s24 >> 4) << 6));
+    if (j == 0) xs[g] = fmul(scale, 0.25f);
+  }
+}
+
+hipError_t launch_quantize6_x(uint8_t *out, float *xs, const float *x, int32_t groups, hipStream_t s) {
+  if (groups <= 0) return hipSuccess;
+  hipLaunchKernelGGL(quantize6_kernel, dim3((groups + 7) / 8), dim3(256), 0, s, out, xs, x, groups);
+  return hipGetLastError();
+}
+
+// ternary_x (quantize.ts:197-225): a group of 128 values a half-wave, lane c its byte c (values 4c..4c+3).  The
+// scale is groupLargest's (the largest |value|, NaN where there is one: the largest bits, as binary_x takes it); a
+// value's code 1 + (v > 0) - (v < 0) at bits 2 (its place in the four); *bad = 1 where a value is neither 0 nor of
+// the scale's size (a NaN never is).
+__global__ __launch_bounds__(256) void ternary_x_kernel(uint8_t *out, float *xs, const float *x, int32_t groups,
+                                                        int32_t *bad) {
+  const int64_t gi = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
+  const int c = threadIdx.x & 31;
+  const bool live = gi < groups;
+  const int64_t g = live ? gi : 0;
+  const float4 f = ((const float4 *)(x + g * 128))[c];
+  const float v[4] = {f.x, f.y, f.z, f.w};
+  uint32_t m = 0;
+#pragma unroll
+  for (int i = 0; i < 4; i++) m = max(m, __float_as_uint(v[i]) & 0x7fffffffu);
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, o, 32));
+  const float scale = __uint_as_float(m);
+  uint32_t byte = 0;
+  bool refused = false;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    byte |= (1u + (v[i] > 0.0f ? 1u : 0u) - (v[i] < 0.0f ? 1u : 0u)) << (2 * i);
+    refused |= !(fabsf(v[i]) == scale || v[i] == 0.0f);
+  }
+  if (live) {
+    out[g * 32 + c] = (uint8_t)byte;
+    if (c == 0) xs[g] = scale;
+    if (refused && bad) *bad = 1;
+  }
+}
+
+hipError_t launch_ternary_x(uint8_t *out, float *xs, const float *x, int32_t groups, int32_t *bad, hipStream_t s) {
+  if (groups <= 0) return hipSuccess;
+  hipLaunchKernelGGL(ternary_x_kernel, dim3((groups + 7) / 8), dim3(256), 0, s, out, xs, x, groups, bad);
   return hipGetLastError();
 }
 

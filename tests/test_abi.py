@@ -36,6 +36,7 @@ def test_reference_names_and_arities(pkg):
     reference = {"quantize_x": 5, "int8_sums": 3, "six_sums": 3, "interleave": 3, "matmul_q8r": 9, "matmul_q8": 8,
                  "matmul_q8r_tile": 12, "matmul_q6r": 9, "matmul_q6": 8, "matmul_t2r": 9, "matmul_t2": 9,
                  "matmul_t2r_tile": 12, "matmul_b1r": 9, "matmul_b1": 9, "matmul_b1r_tile": 12, "binary_x": 4,
+                 "quantize6_x": 4, "ternary_x": 4,
                  "sb_tables": 2, "sums_x": 3, "matmul_sbr": 9, "matmul_sb": 9, "matmul_sbr_tile": 12,
                  "matmul_sbw_tile": 13, "signed_dots": 3, "sb_row": 5, "add_columns": 5}
     for name, arity in reference.items():
@@ -60,6 +61,10 @@ def test_version(pkg):
     (lambda L: L.hq_matmul_b1r_tile_ex(16, 16, 16, 16, 16, 128, 0, 1, 2, 4, 8, 2, None), 2, "frame"),
     (lambda L: L.hq_binary_x_ex(16, 16, 16, 100, None, None), 1, "multiple of 128"),
     (lambda L: L.hq_binary_x_ex(16, 16, 8, 128, None, None), 2, "aligned"),
+    (lambda L: L.hq_quantize6_x_ex(16, 16, 16, 48, None), 1, "multiple of 32"),
+    (lambda L: L.hq_quantize6_x_ex(16, 18, 16, 32, None), 2, "aligned"),
+    (lambda L: L.hq_ternary_x_ex(16, 16, 16, 100, None, None), 1, "multiple of 128"),
+    (lambda L: L.hq_ternary_x_ex(16, 16, 8, 128, None, None), 2, "aligned"),
     (lambda L: L.hq_matmul_sbr_ex(16, 16, 16, 16, 16, 256, 0, 1, 11, None), 1, "type 11"),
     (lambda L: L.hq_matmul_sbr_ex(16, 16, 16, 16, 16, 384, 0, 1, 12, None), 1, "multiple of 256"),
     (lambda L: L.hq_matmul_sbr_ex(16, 16, 16, 17, 16, 256, 0, 1, 12, None), 2, "w not 2-byte"),

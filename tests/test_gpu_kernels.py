@@ -637,6 +637,73 @@ def test_binary_x(pkg, k, arena, oracle):
         assert arena.get(word, np.int32, 1)[0] == want_bad, case
 
 
+def test_quantize6_x(pkg, k, arena, oracle):
+    """kernels/kernel/quantize.ts:161-182 on the GPU: the oracle's 24 bytes and scale / 4 of every group (random groups
+    of every magnitude, a group of zeros, ties to even, a subnormal scale, a NaN passed over and one that makes the
+    scale NaN), through the drop-in name and the _ex form"""
+    rng = np.random.default_rng(1611)
+    L = pkg.library()
+    for groups in (1, 7, 999):
+        x = (rng.standard_normal((groups, 32)) * np.exp(rng.uniform(-20, 20, (groups, 1)))).astype(F)
+        if groups > 7:
+            x[3] = 0.0
+            x[5] = np.arange(32, dtype=F) - F(15.5)
+            x[5, 31] = 31.0
+            x[6, 0] = 1e-38
+            x[7, 1] = np.nan  # lane 1 of groupMax: passed over
+            x[8, 0] = np.nan  # lane 0: the scale is NaN
+        x = x.reshape(-1)
+        want_out, want_xs = oracle.quantize6_x(x)
+        xa = arena.put(x)
+        for form in ("drop-in", "ex"):
+            out = arena.alloc(groups * 24, fill=np.full(groups * 24, 0xAA, np.uint8))
+            xs = arena.alloc(4 * groups, fill=np.full(groups, -7, F))
+            if form == "drop-in":
+                k.quantize6_x(out, xs, xa, x.size)
+            else:
+                assert L.hq_quantize6_x_ex(out, xs, xa, x.size, None) == 0, L.hq_last_error_message()
+            assert np.array_equal(arena.get(out, np.uint8, groups * 24), want_out), (groups, form)
+            got_xs = arena.get(xs, F, groups)
+            assert np.array_equal(np.isnan(got_xs), np.isnan(want_xs))
+            assert same_bits(np.nan_to_num(got_xs), np.nan_to_num(want_xs)), (groups, form)
+
+
+def test_ternary_x(pkg, k, arena, oracle):
+    """kernels/kernel/quantize.ts:197-225 on the GPU: the oracle's codes and scales (tests/ternary-check.ts:252-258's
+    groups: scales of every size, zeros, -0), and its refusals (ternary-check.ts:276-283's places), through the
+    drop-in's return value and the _ex form's device word"""
+    import test_oracle
+    rng = np.random.default_rng(2300)
+    L = pkg.library()
+    cases = [(None, None), (0, 0.5), (127, 1.0000001), (128 + 63, 2), (128 * 39 + 127, np.nan), (128 * 7 + 5, -0.999999),
+             (128 * 9 + 33, 0.5), (128 * 9 + 38, 0.5), (128 * 9 + 43, 0.5), (128 * 9 + 46, 0.5)]
+    for at, spoil in cases:
+        x = test_oracle.ternary_case(rng)
+        if at is not None:
+            g = at >> 7
+            x[g * 128:(g + 1) * 128] = np.where(np.arange(128) % 2 == 1, 3.0, -3.0)
+            x[at] = F(spoil * 3)
+        want_out, want_xs, want_bad = oracle.ternary_x(x)
+        xa = arena.put(x)
+        out = arena.alloc(x.size // 4, fill=np.full(x.size // 4, 0xAA, np.uint8))
+        xs = arena.alloc(4 * (x.size // 128), fill=np.full(x.size // 128, -7, F))
+        assert k.ternary_x(out, xs, xa, x.size) == want_bad, (at, spoil)
+        assert np.array_equal(arena.get(out, np.uint8, x.size // 4), want_out), (at, spoil)
+        got_xs = arena.get(xs, F, x.size // 128)
+        assert np.array_equal(np.isnan(got_xs), np.isnan(want_xs))
+        assert same_bits(np.nan_to_num(got_xs), np.nan_to_num(want_xs)), (at, spoil)
+        word = arena.alloc(4, fill=np.zeros(1, np.int32))
+        assert L.hq_ternary_x_ex(out, xs, xa, x.size, word, None) == 0
+        assert arena.get(word, np.int32, 1)[0] == want_bad, (at, spoil)
+    # a long row: 17408 values (136 groups), the 27B down projection's
+    x = (rng.integers(-1, 2, 17408) * np.repeat(rng.uniform(0.01, 1, 136), 128)).astype(F)
+    want_out, want_xs, want_bad = oracle.ternary_x(x)
+    out, xs = arena.alloc(x.size // 4), arena.alloc(4 * 136)
+    assert k.ternary_x(out, xs, arena.put(x), x.size) == want_bad == 0
+    assert np.array_equal(arena.get(out, np.uint8, x.size // 4), want_out)
+    assert same_bits(arena.get(xs, F, 136), want_xs)
+
+
 # ---- the order-revealing inputs of test_oracle.py, on the GPU ------------------------------------------------
 @pytest.mark.parametrize("ds, es, want", [
     ([1, 1, 0, 0, -1, 0, 0, 0, 0, 0, 0, 0], [24, 0, 0, 0, 24, 0, 0, 0, 0, 0, 0, 0], 1.0),

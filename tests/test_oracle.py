@@ -774,3 +774,104 @@ def test_fast_q8r_tile_is_the_oracle(oracle, count, rows):
     for t, (q, s) in enumerate(qs):
         want = oracle.matmul_q8r(q, s, w, ws, wc, n)
         assert np.array_equal(got[t].view(np.uint32), want.view(np.uint32)), t
+
+
+# ---- the converters' packers: quantize6_x and ternary_x (kernels/kernel/quantize.ts:153-225) ----------------------
+def numpy_quantize6(x):
+    """src/python/engine/packing.py:73-80 (quantize6, the converter's NumPy form the reference's smoke test holds the
+    kernel to, tests/smoke.ts:800-811), with pack6 (tests/streams.py): 24 bytes and scale / 4 a group"""
+    groups = np.asarray(x, np.float32).reshape(-1, 32)
+    scales = (np.abs(groups).max(axis=1) / np.float32(31.0)).astype(np.float32)
+    inverse = np.divide(np.float32(1.0), scales, out=np.zeros_like(scales), where=scales > 0)
+    six = np.clip(np.rint(groups * inverse[:, None]), -32, 31).astype(np.int8)
+    return pack6((six * 4).astype(np.int8)), scales / np.float32(4)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_quantize6_x_is_the_converters_quantize6(oracle, seed):
+    """random groups of every magnitude, a group of zeros, and smoke.ts:802-804's ties (halves that round to even
+    with a scale of exactly 1), against packing.py's NumPy quantize6 + pack6 to the byte"""
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((24, 32)) * np.exp(rng.uniform(-20, 20, (24, 1)))).astype(F)
+    x[3] = 0.0
+    x[5] = np.arange(32, dtype=F) - F(15.5)
+    x[5, 31] = 31.0
+    x[6] = -x[5]
+    x[7, 0] = 1e-38  # a subnormal scale
+    got_bytes, got_scales = oracle.quantize6_x(x.reshape(-1))
+    want_bytes, want_scales = numpy_quantize6(x)
+    assert np.array_equal(got_bytes, want_bytes)
+    assert np.array_equal(got_scales.view(np.uint32), want_scales.view(np.uint32))
+    assert not got_bytes[3 * 24:4 * 24].any() and got_scales[3] == 0
+    # the ties: value j - 15.5 over scale 1 rounds to the even neighbour (np.rint), so the six bits of -15.5 are -16
+    values = oracle.six_unpack(got_bytes[5 * 24:6 * 24]).astype(np.int32) // 4
+    assert values.tolist() == np.rint(x[5]).astype(np.int32).tolist() and got_scales[5] == 0.25
+
+
+def test_quantize6_x_round_trip_and_nan(oracle):
+    """six_unpack (kernels/six.ts, pinned separately) of quantize6_x's bytes gives 4 v; v times 4 xs is the value to
+    half a scale; a NaN in lane 1..3 of groupMax is passed over (the scale is lane 0's or the others'), one in lane 0
+    makes the scale NaN and every code 0 (trunc_sat of NaN)"""
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((16, 32)).astype(F)
+    b, s = oracle.quantize6_x(x.reshape(-1))
+    v = oracle.six_unpack(b).astype(np.float64).reshape(16, 32)  # 4 v
+    assert np.all(np.abs(v * s[:, None].astype(np.float64) - x) <= 2 * s[:, None] * (1 + 1e-6))
+    y = np.ones((2, 32), F)
+    y[0, 1] = np.nan  # lane 1 of the first four: passed over
+    y[1, 0] = np.nan  # lane 0: the scale is NaN
+    b, s = oracle.quantize6_x(y.reshape(-1))
+    assert s[0] == F(1.0 / 31.0) * F(0.25) and np.isnan(s[1])
+    assert oracle.six_unpack(b[24:]).tolist() == [0] * 32
+
+
+def numpy_ternary(x):
+    """src/python/engine/packing.py:117-130 (ternary, without its float16 check): the sign + 1 of each value packed
+    four to a byte (tests/streams.py), the largest |value| of each group of 128, and whether every value is its sign
+    times that"""
+    groups = np.asarray(x, np.float32).reshape(-1, 128)
+    scales = np.abs(groups).max(axis=1)
+    signs = np.sign(groups)
+    codes = (np.nan_to_num(signs) + 1).astype(np.uint8)  # (a NaN is refused below; its code is not compared)
+    return pack_ternary(codes.reshape(-1)), scales, int(not np.array_equal(signs * scales[:, None], groups))
+
+
+def ternary_case(rng):
+    """tests/ternary-check.ts:252-258: 40 groups, scales of every size, a group of zeros, one of -0 alone"""
+    x = np.zeros((40, 128), F)
+    for g in range(40):
+        d = 0.0 if g == 3 else F([1, 0.0078125, 3.0000002, 1e-30, 65504, 1.5e-5][g % 6] * (1 + rng.integers(0, 7)))
+        x[g] = -0.0 if g == 5 else (rng.integers(0, 3, 128) - 1) * F(d)
+    return x.reshape(-1)
+
+
+def test_ternary_x_is_the_converters_ternary(oracle):
+    rng = np.random.default_rng(6)
+    x = ternary_case(rng)
+    got = oracle.ternary_x(x)
+    want = numpy_ternary(x)
+    assert got[2] == 0 and want[2] == 0
+    assert np.array_equal(got[0], want[0]) and np.array_equal(got[1], want[1])
+    assert (got[0][5 * 32:6 * 32] == 0x55).all()  # -0: code 1 (neither above nor below 0)
+
+
+@pytest.mark.parametrize("at, spoil", [(0, 0.5), (127, 1.0000001), (128 + 63, 2), (128 * 39 + 127, np.nan),
+                                       (128 * 7 + 5, -0.999999), (128 * 9 + 33, 0.5), (128 * 9 + 38, 0.5),
+                                       (128 * 9 + 43, 0.5), (128 * 9 + 46, 0.5)])
+def test_ternary_x_refusals(oracle, at, spoil):
+    """tests/ternary-check.ts:276-283: one value of one place that is not ternary (half the scale, a little more
+    than it, twice it, not a number; in each of the four vectors of sixteen values) is refused; the codes and scales
+    are still written"""
+    rng = np.random.default_rng(7)
+    x = ternary_case(rng)
+    g = at >> 7
+    x[g * 128:(g + 1) * 128] = np.where(np.arange(128) % 2 == 1, 3.0, -3.0)
+    x[at] = F(spoil * 3)
+    got = oracle.ternary_x(x)
+    assert got[2] == 1
+    assert numpy_ternary(x)[2] == 1
+    if not np.isnan(spoil):
+        want = numpy_ternary(x)
+        assert np.array_equal(got[0], want[0]) and np.array_equal(got[1], want[1])
+    else:
+        assert np.isnan(got[1][g])
