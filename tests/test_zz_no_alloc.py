@@ -97,3 +97,40 @@ def test_static_staging_refuses_what_does_not_fit(pkg):
     assert L.hq_matmuls_static(4096, 4 * n, jobs.table([job]), 1, jobs.JOB, None) == pkg.HQ_ERR_ARGUMENT
     assert "staging" in L.hq_last_error_message().decode()
     L.hq_clear_error()
+
+
+def test_static_staging_under_graph_capture(pkg, arena, oracle):
+    """the callers it is for: hq_matmuls_static captured into a HIP graph (no allocation, no memset in it), replayed
+    three times with new inputs written eagerly between the replays, each replay's outputs checked against an eager
+    hq_matmuls of the same inputs"""
+    import torch
+    from pyodide_llm_amd import jobs
+    L = pkg.library()
+    assert L.hq_init() == 0
+    rng = np.random.default_rng(78)
+    n, tokens, rows = 1024, 2, 96
+    arena.reset()
+    ax, specs = phase_of(arena, oracle, rng, n, tokens, rows)
+    os_ = 4 * rows
+    outs = [arena.alloc(os_ * tokens) for _ in specs]
+    table = jobs.table([jobs.job(kind, o, 0, 0, wq, ws, wc, n, rows=rows, count=tokens, os=os_)
+                        for (kind, wq, ws, wc), o in zip(specs, outs)])
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        h = stream.cuda_stream
+        assert L.hq_matmuls_static(ax, 4 * n, table, len(specs), jobs.JOB, h) == 0, L.hq_last_error_message()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            L.hq_matmuls_static(ax, 4 * n, table, len(specs), jobs.JOB, h)
+    assert L.hq_last_error() == 0, L.hq_last_error_message()
+    for replay in range(3):
+        x = rng.standard_normal((tokens, n)).astype(F) * (replay + 1)
+        arena.write(ax, x)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = [arena.get(o, F, rows * tokens) for o in outs]
+        want, _ = run_both(pkg, arena, ax, specs, n, tokens, rows)
+        for (kind, _, _, wc), w_, g_ in zip(specs, want, got):
+            assert same_bits(g_, w_), f"replay {replay} {kind} wc {bool(wc)}: {first_difference(g_, w_)}"
