@@ -258,6 +258,12 @@ def measure_decode_m4(torch, pkg, args, phases):
             "gemv_avg_launch_us": round(1e6 * gemv / launches, 3), "gemv_GBps": round(step_bytes / gemv / 1e9, 1)}
 
 
+def _graph_time_median(torch, launch, reps, rounds=3):
+    """the median of `rounds` measurements of _graph_time (one alone can be off by tens of per cent while the clocks
+    settle)"""
+    return sorted(_graph_time(torch, launch, reps) for _ in range(rounds))[rounds // 2]
+
+
 def _graph_time(torch, launch, reps):
     """seconds a replay of a graph of launch()'s launches takes, over `reps` replays between HIP events"""
     stream = torch.cuda.Stream()
@@ -345,7 +351,7 @@ def measure_configs(torch, pkg, args, extras):
         def launch(h):
             for t, nj in tables:
                 lib.hq_phase(t, nj, 16, h)
-        sec = _graph_time(torch, launch, reps)
+        sec = _graph_time_median(torch, launch, reps)
         pkg.check(lib.hq_last_error())
         out[label] = {"GBps": round(total / sec / 1e9, 1), "us_per_launch": round(1e6 * sec / len(tables), 2),
                       "launches": len(tables), "bytes": total}
@@ -384,7 +390,7 @@ def measure_configs(torch, pkg, args, extras):
         def launch(h):
             for c in calls:
                 c(h)
-        sec = _graph_time(torch, launch, reps)
+        sec = _graph_time_median(torch, launch, reps)
         pkg.check(lib.hq_last_error())
         out[label] = {"TOPS": round(ops / sec / 1e12, 1), "frac": round(ops / sec / 1e12 / INT8_PEAK_TOPS, 4),
                       "ms": round(1e3 * sec, 3)}
