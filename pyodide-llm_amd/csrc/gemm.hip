@@ -31,23 +31,21 @@
 // (half a 32x32x1_2b) + 16 (half a correction MFMA) of the matrix core: ~185 cycles for 65536 operations, about a
 // third of the int8 peak (0.83 POPS at 2.3 GHz) — the bound this kernel is measured against.
 //
-// Tiles.  A block computes a 128-row x 64-token tile.  int8 / int6: 8 waves, two a SIMD; the waves of pair p (waves
-// 4 p .. 4 p + 3) take rows 64 p .. + 63 and chain w % 4, four 32 x 32 sub-tiles each (two row slices x two token
-// halves: the weights' operand read once for two MFMAs, the tokens' for two slices); a launch of few tiles takes
-// 64-row tiles of one pair (4 waves, two blocks a CU) instead.  Ternary: 16 waves; wave w takes rows 32 (w / 4) .. + 31
+// Tiles.  int8 / int6: a block (4 waves, two blocks a CU) computes a 64-row x 64-token tile; wave w is chain w, four
+// 32 x 32 sub-tiles (two row slices x two token halves: the weights' operand read once for two MFMAs, the tokens' for
+// two slices).  Ternary: a block of 16 waves computes a 128-row x 64-token tile; wave w takes rows 32 (w / 4) .. + 31
 // and chain w % 4, both 32-token halves.
 //
 // Pipeline (int8 / int6).  A wave issues each sub-tile's MFMAs one sub-tile ahead of its epilogue, so the matrix core
-// works on the next sub-tile while the VALU folds this one, and a stage's last epilogue runs beside the first MFMAs
-// of the next stage.  Its operands for stage s + 1 are read from LDS in the middle of stage s, right after the
-// block's barrier that makes stage s + 1's loads everyone's.  The operands go from HBM / L2 straight into LDS with
+// works on the next sub-tile while the VALU folds this one.  The operands go from HBM / L2 straight into LDS with
 // buffer-to-LDS loads into a ring of 4 stage buffers (a stage: 4 groups of int8 / int6, 2 groups of 128 of ternary):
-// at the barrier for stage s + 1 the loads of stage s + 4 go into the buffer stage s's operands were read from.  Every
-// wave issues the same number of loads a stage (some into a scratch area of LDS), so one s_waitcnt vmcnt count says
-// "my loads of stage s + 1 have landed".  A load past the tile's last row or token, or past the last group, reads
-// zeros (buffer bounds; such results are never stored).  The 16-byte chunks of a row are stored XOR-swizzled so that
-// the MFMA operand reads (32 rows or tokens, one chunk each) spread over the LDS banks, and tiles are ordered so that
-// the blocks one XCD runs at a time share rows and tokens in that XCD's L2.
+// at the barrier for stage s, which says that stage s's loads have landed and that every wave has read stage s - 1's
+// operands, a wave reads its operands of stage s and issues its loads of stage s + 3 into stage s - 1's buffer.  A
+// wave issues the same loads every stage, so one s_waitcnt vmcnt count says "my loads of stage s have landed".  A load
+// past the tile's last row or token, or past the last group, reads zeros (buffer bounds; such results are never
+// stored).  The 16-byte chunks of a row are stored XOR-swizzled so that the MFMA operand reads (32 rows or tokens, one
+// chunk each) spread over the LDS banks, and tiles are ordered so that the blocks one XCD runs at a time share rows
+// and tokens in that XCD's L2.
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -86,8 +84,9 @@ HQ_DEV v32f zero32f() {
 // Direct loads into LDS: lane l's `size` bytes land at dst + size * l (dst the same in the whole wave; 2-byte loads
 // land zero-extended in 4-byte slots).  The stage buffers are distinct __shared__ objects, so the compiler can tell
 // that a load into one buffer does not write the one being read, and waits for these loads only where the stage
-// barriers say so.
-#define HQ_LDS(p) ((__attribute__((address_space(3))) void *)(p))
+// barriers say so.  A generic address of LDS is the LDS offset in its low 32 bits: taken that way, not by an
+// address-space cast (which tests for the null pointer), M0 is a constant for every load into a stage buffer.
+#define HQ_LDS(p) ((__attribute__((address_space(3))) void *)(uintptr_t)(uint32_t)(uintptr_t)(p))
 HQ_DEV void dma16(__amdgpu_buffer_rsrc_t r, void *dst, uint32_t vo, uint32_t so) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, HQ_LDS(dst), 16, vo, so, 0, 0);
 }
@@ -208,9 +207,11 @@ HQ_DEV v4i six_half(const char *p, int kh) {
 
 // A block's loads of a stage, as 1 KB pieces (256 B for the narrow scale loads) dealt to the four waves in turn:
 // the weights' pieces (8 of int8, 6 of int6), the activations' (8), then the scales' (wide: the rows', the
-// corrections' with wc, the tokens'; narrow: 4 of each).  Wave w issues pieces w, w + 4, ..., so its loads a stage
-// are count(w); no load is issued that is not needed.
-template <int PACK, bool WC, bool WIDE>
+// corrections' with wc, the tokens'; narrow: 4 of each).  Wave W issues pieces W, W + 4, ..., so its loads a stage
+// are count(W); no load is issued that is not needed.  W is a template argument (the kernel runs one copy of its
+// main loop a wave), so a wave's loads are straight-line code: chosen at run time, every stage took a tree of
+// scalar branches per piece (measured 4-6 % of the launch).
+template <int PACK, bool WC, bool WIDE, int W>
 struct Relaxed {
   static constexpr int GB = PACK == 8 ? 32 : 24;    // bytes of a group of weights
   static constexpr int NWP = PACK == 8 ? 8 : 6;     // the weights' pieces
@@ -218,12 +219,13 @@ struct Relaxed {
   static constexpr int SPK = WIDE ? 1 : 4;          // pieces of each
   static constexpr int P = NWP + 8 + NSK * SPK;     // pieces a stage
   static constexpr int PW = (P + 3) / 4;            // the most pieces of a wave
-  static HQ_DEV int count(int w) { return P / 4 + (w < P % 4 ? 1 : 0); }
+  static constexpr int count = P / 4 + (W < P % 4 ? 1 : 0);  // this wave's
+  static constexpr int wave = W;
   __amdgpu_buffer_rsrc_t rw, rx, rws, rwc, rxs;
   uint32_t off[PW];
-  int wave;
 
-  HQ_DEV Relaxed(const Job &J, int row0, int tok0, int M, int w) : wave(w) {
+  HQ_DEV Relaxed(const Job &J, int row0, int tok0, int M) {
+    constexpr int w = W;
     const int lane = threadIdx.x & 63, ng = J.n >> 5;
     const int64_t rb = (int64_t)ng * GB;
     rw = resource(J.wq + row0 * rb, (J.r1 - row0) * rb);
@@ -294,11 +296,9 @@ struct Relaxed {
 
 // stage s's loads have landed everywhere: this wave's own, with those of the two stages after it still in flight,
 // then the block's barrier
-template <int PACK, bool WC, bool WIDE>
-HQ_DEV void q_ready(int wave) {
-  using L = Relaxed<PACK, WC, WIDE>;
-  if (wave < L::P % 4) stage_ready<2 * (L::P / 4 + 1)>();
-  else stage_ready<2 * (L::P / 4)>();
+template <int PACK, bool WC, bool WIDE, int W>
+HQ_DEV void q_ready() {
+  stage_ready<2 * Relaxed<PACK, WC, WIDE, W>::count>();
 }
 
 // a wave's operands of one group gi of a stage: the activations of both token halves, the weights of both row slices
@@ -448,18 +448,18 @@ HQ_DEV void fold(float a[16], const v16i &c, const v32f &sc, int h) {
   for (int r = 0; r < 16; r++) a[r] = fadd(a[r], fmul((float)c[r], sc[16 * h + r]));
 }
 
-// Stage s of a wave's chain (group 4 s + chain): the stage's loads landed everywhere (the block's barrier), the
+// Stage s of wave W's chain (group 4 s + W): the stage's loads landed everywhere (the block's barrier), the
 // wave's operands read from `cur`, its loads of stage s + 3 issued into `dma` (the buffer stage s - 1's operands came
 // from, which every wave has read by this barrier), then the four sub-tiles (slice, half) = (0, 0), (0, 1), (1, 0),
 // (1, 1), each sub-tile's MFMAs issued before the previous one's fold so that the matrix core and the VALU take
 // turns without waiting for each other.  Every wave has issued its loads of stages up to s + 2 at the barrier (a
 // stage past the job's last group loads zeros, and its buffer is never read), so "stage s landed" is always "at most
 // two stages of this wave's loads in flight".
-template <int PACK, bool WC, bool WIDE>
-HQ_DEV void q_stage(Relaxed<PACK, WC, WIDE> &L, const StageQ &cur, StageQ &dma, int s, float acc[4][16], int chain,
+template <int PACK, bool WC, bool WIDE, int W>
+HQ_DEV void q_stage(Relaxed<PACK, WC, WIDE, W> &L, const StageQ &cur, StageQ &dma, int s, float acc[4][16],
                     int lane) {
-  q_ready<PACK, WC, WIDE>(L.wave);
-  const OpsQ op = read_ops<PACK, WC, WIDE>(cur, chain, lane);
+  q_ready<PACK, WC, WIDE, W>();
+  const OpsQ op = read_ops<PACK, WC, WIDE>(cur, W, lane);
   L.load(dma, s + AHEAD);
   const v16i cin0 = corrections<WC>(op, 0);
   const v32f S0 = scales(op, 0);
@@ -496,6 +496,27 @@ HQ_DEV void add_chains4(float acc[4][16], float *p0, float *p1, int chain, int l
   }
 }
 
+// wave W's stages of the tile (chain W): its loads, and every stage in order
+template <int PACK, bool WC, bool WIDE, int W>
+HQ_DEV void q_chain(const Job &J, int row0, int tok0, int M, int stages, StageQ &b0, StageQ &b1, StageQ &b2,
+                    StageQ &b3, float acc[4][16], int lane) {
+  Relaxed<PACK, WC, WIDE, W> L(J, row0, tok0, M);
+  // stages 0..2 first (whatever the job has: a stage past its groups loads zeros); stage s's operands come from
+  // buffer s % 4 and its loads of stage s + 3 go into buffer (s - 1) % 4
+  L.load(b0, 0);
+  L.load(b1, 1);
+  L.load(b2, 2);
+  for (int s = 0; s < stages; s += RING) {
+    q_stage<PACK, WC, WIDE, W>(L, b0, b3, s, acc, lane);
+    if (s + 1 >= stages) break;
+    q_stage<PACK, WC, WIDE, W>(L, b1, b0, s + 1, acc, lane);
+    if (s + 2 >= stages) break;
+    q_stage<PACK, WC, WIDE, W>(L, b2, b1, s + 2, acc, lane);
+    if (s + 3 >= stages) break;
+    q_stage<PACK, WC, WIDE, W>(L, b3, b2, s + 3, acc, lane);
+  }
+}
+
 template <int PACK, bool WC, bool WIDE>
 __global__ __launch_bounds__(QT, 2) void gemm_relaxed(Job J) {
   __shared__ StageQ b0, b1, b2, b3;
@@ -513,21 +534,12 @@ __global__ __launch_bounds__(QT, 2) void gemm_relaxed(Job J) {
 #pragma unroll
     for (int r = 0; r < 16; r++) acc[i][r] = 0.0f;
 
-  Relaxed<PACK, WC, WIDE> L(J, row0, tok0, M, chain);
   const int stages = ng4 / QG;  // whole stages of the four chains; the groups past them (ng % 4) are one more stage
-  // stages 0..2 first (whatever the job has: a stage past its groups loads zeros); stage s's operands come from
-  // buffer s % 4 and its loads of stage s + 3 go into buffer (s - 1) % 4
-  L.load(b0, 0);
-  L.load(b1, 1);
-  L.load(b2, 2);
-  for (int s = 0; s < stages; s += RING) {
-    q_stage<PACK, WC, WIDE>(L, b0, b3, s, acc, chain, lane);
-    if (s + 1 >= stages) break;
-    q_stage<PACK, WC, WIDE>(L, b1, b0, s + 1, acc, chain, lane);
-    if (s + 2 >= stages) break;
-    q_stage<PACK, WC, WIDE>(L, b2, b1, s + 2, acc, chain, lane);
-    if (s + 3 >= stages) break;
-    q_stage<PACK, WC, WIDE>(L, b3, b2, s + 3, acc, chain, lane);
+  switch (chain) {
+  case 0: q_chain<PACK, WC, WIDE, 0>(J, row0, tok0, M, stages, b0, b1, b2, b3, acc, lane); break;
+  case 1: q_chain<PACK, WC, WIDE, 1>(J, row0, tok0, M, stages, b0, b1, b2, b3, acc, lane); break;
+  case 2: q_chain<PACK, WC, WIDE, 2>(J, row0, tok0, M, stages, b0, b1, b2, b3, acc, lane); break;
+  default: q_chain<PACK, WC, WIDE, 3>(J, row0, tok0, M, stages, b0, b1, b2, b3, acc, lane); break;
   }
   stage_ready<0>();  // every load has landed (the tail's too) and every wave is done with the stages
   auto ring = [&](int i) -> StageQ & { return i == 0 ? b0 : i == 1 ? b1 : i == 2 ? b2 : b3; };
