@@ -664,11 +664,6 @@ HQ_DEV v4i plane_pair(uint32_t w0, uint32_t w1) {
   return b;
 }
 
-// 8 bytes at byte o (a multiple of 8) of a token's 256 stage bytes
-HQ_DEV uint2 t_acts8(const StageT &S, int tok, int o) {
-  return *(const uint2 *)(S.x + tok * 256 + (((o >> 4) ^ (tok & 15)) << 4) + (o & 8));
-}
-
 // binary's planes 2 kh, 2 kh + 1 of block h (bits 4 h + 2 kh and + 1 of every byte, doubled: kernels/binary.ts:19-22)
 HQ_DEV v4i bit_pair(uint32_t w0, uint32_t w1, int b) {
   v4i r;
@@ -680,46 +675,87 @@ HQ_DEV v4i bit_pair(uint32_t w0, uint32_t w1, int b) {
 }
 
 // part k of group gi of the stage for the lane's slice, both token halves: f(f(whole * xs) * d) into the part's
-// chain (relaxed/signs.ts:31)
+// chain (relaxed/signs.ts:31).  The stage's operands are read by blocks of ds_reads with one wait each: read as C++
+// loads, each would first wait for every buffer-to-LDS load in flight, the next stages' included (the compiler cannot
+// tell that those write other stage buffers), and no stage's loads would overlap the stages before it.
 template <bool BIN>
 HQ_DEV void t_group(float acc0[16], float acc1[16], const StageT &S, int gi, int k, int slice, int lane) {
   const int h = k >> 1, s = k & 1, kh = lane >> 5, row = 32 * slice + (lane & 31);
-  // B: the row's codes of planes 2 kh, 2 kh + 1, bytes c = 8 s .. + 7 of block h (ternary: chunk 2 gi + h, half s;
-  // binary: group gi's 16 bytes, half s, bits 4 h + 2 kh ..)
-  v4i B;
-  if (BIN) {
-    const uint2 wv = *(const uint2 *)(S.w + row * 32 + ((gi ^ bswz(row)) << 4) + 8 * s);
-    B = bit_pair(wv.x, wv.y, 4 * h + 2 * kh);
-  } else {
-    const int j = 2 * gi + h;
-    const uint2 wv = *(const uint2 *)(S.w + row * 64 + ((j ^ tswz(row)) << 4) + 8 * s);
-    B = kh == 0 ? plane_pair<0>(wv.x, wv.y) : plane_pair<2>(wv.x, wv.y);
-  }
-  const float d = half_to_float(S.d[gi][row]);
   const int o = 128 * gi + 64 * h + 8 * s + 32 * kh;
+  // the row's codes (ternary: chunk 2 gi + h, half s; binary: group gi's 16 bytes, half s), its scale, the tokens'
+  // activations (8 bytes at o and o + 16 of token 32 half + lane % 32), the sums and scales of tokens
+  // 32 half + 4 kh + 8 q: byte offsets in the stage buffer, added to its address, which is made opaque to the compiler
+  // so that it adds them here rather than keeping every stage buffer's addresses in registers
+  uint32_t base = lds_addr(&S);
+  asm volatile("" : "+s"(base));
+  const uint32_t aw = base + (BIN ? (uint32_t)(offsetof(StageT, w) + row * 32 + ((gi ^ bswz(row)) << 4) + 8 * s)
+                                  : (uint32_t)(offsetof(StageT, w) + row * 64 + (((2 * gi + h) ^ tswz(row)) << 4) + 8 * s));
+  const uint32_t ad = base + (uint32_t)(offsetof(StageT, d) + (gi * BR + row) * 4);
+  uint32_t aa[2][2];
 #pragma unroll
   for (int half = 0; half < 2; half++) {
     const int tok = 32 * half + (lane & 31);
-    const uint2 a0 = t_acts8(S, tok, o), a1 = t_acts8(S, tok, o + 16);
-    v4i A;
-    A[0] = (int32_t)a0.x; A[1] = (int32_t)a0.y; A[2] = (int32_t)a1.x; A[3] = (int32_t)a1.y;
-    const int tbase = 32 * half + 4 * kh;
-    v16i C;
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-      const int4 c4 = *(const int4 *)&S.sums[4 * gi + k][tbase + 8 * q];
-      C[4 * q] = c4.x; C[4 * q + 1] = c4.y; C[4 * q + 2] = c4.z; C[4 * q + 3] = c4.w;
-    }
-    C = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, C, 0, 0, 0);
-    float *acc = half ? acc1 : acc0;
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-      const float4 x4 = *(const float4 *)&S.xs[4 * gi + k][tbase + 8 * q];
-      const float xv[4] = {x4.x, x4.y, x4.z, x4.w};
-#pragma unroll
-      for (int e = 0; e < 4; e++) acc[4 * q + e] = fadd(acc[4 * q + e], fmul(fmul((float)C[4 * q + e], xv[e]), d));
+    for (int i = 0; i < 2; i++) {
+      const int oi = o + 16 * i;
+      aa[half][i] = base + (uint32_t)(offsetof(StageT, x) + tok * 256 + (((oi >> 4) ^ (tok & 15)) << 4) + (oi & 8));
     }
   }
+  const uint32_t asum = base + (uint32_t)(offsetof(StageT, sums) + ((4 * gi + k) * BT + 4 * kh) * 4);
+  const uint32_t axs = base + (uint32_t)(offsetof(StageT, xs) + ((4 * gi + k) * BT + 4 * kh) * 4);
+  // the codes, the scale, token half 0's activations and sums
+  uint2 wv, a0, a1;
+  uint32_t dh;
+  v4i c[4];
+  asm volatile(
+      "ds_read_b64 %0, %8\n\tds_read_b32 %1, %9\n\tds_read_b64 %2, %10\n\tds_read_b64 %3, %11\n\t"
+      "ds_read_b128 %4, %12\n\tds_read_b128 %5, %12 offset:32\n\tds_read_b128 %6, %12 offset:64\n\t"
+      "ds_read_b128 %7, %12 offset:96\n\ts_waitcnt lgkmcnt(0)"
+      : "=&v"(wv), "=&v"(dh), "=&v"(a0), "=&v"(a1), "=&v"(c[0]), "=&v"(c[1]), "=&v"(c[2]), "=&v"(c[3])
+      : "v"(aw), "v"(ad), "v"(aa[0][0]), "v"(aa[0][1]), "v"(asum)
+      : "memory");
+  // B: the row's codes of planes 2 kh, 2 kh + 1 (binary: bits 4 h + 2 kh ..)
+  v4i B;
+  if (BIN) B = bit_pair(wv.x, wv.y, 4 * h + 2 * kh);
+  else B = kh == 0 ? plane_pair<0>(wv.x, wv.y) : plane_pair<2>(wv.x, wv.y);
+  const float d = half_to_float(dh);
+  const auto product = [&](const uint2 &p0, const uint2 &p1, const v4i cq[4]) {
+    v4i A;
+    A[0] = (int32_t)p0.x; A[1] = (int32_t)p0.y; A[2] = (int32_t)p1.x; A[3] = (int32_t)p1.y;
+    v16i cin;
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) cin[4 * q + e] = cq[q][e];
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, cin, 0, 0, 0);
+  };
+  const v16i C0 = product(a0, a1, c);
+  // token half 1's activations and sums, half 0's scales
+  v4f x[4];
+  asm volatile(
+      "ds_read_b64 %0, %10\n\tds_read_b64 %1, %11\n\t"
+      "ds_read_b128 %2, %12 offset:128\n\tds_read_b128 %3, %12 offset:160\n\tds_read_b128 %4, %12 offset:192\n\t"
+      "ds_read_b128 %5, %12 offset:224\n\tds_read_b128 %6, %13\n\tds_read_b128 %7, %13 offset:32\n\t"
+      "ds_read_b128 %8, %13 offset:64\n\tds_read_b128 %9, %13 offset:96\n\ts_waitcnt lgkmcnt(0)"
+      : "=&v"(a0), "=&v"(a1), "=&v"(c[0]), "=&v"(c[1]), "=&v"(c[2]), "=&v"(c[3]), "=&v"(x[0]), "=&v"(x[1]),
+        "=&v"(x[2]), "=&v"(x[3])
+      : "v"(aa[1][0]), "v"(aa[1][1]), "v"(asum), "v"(axs)
+      : "memory");
+  const v16i C1 = product(a0, a1, c);
+#pragma unroll
+  for (int q = 0; q < 4; q++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) acc0[4 * q + e] = fadd(acc0[4 * q + e], fmul(fmul((float)C0[4 * q + e], x[q][e]), d));
+  asm volatile(
+      "ds_read_b128 %0, %4 offset:128\n\tds_read_b128 %1, %4 offset:160\n\tds_read_b128 %2, %4 offset:192\n\t"
+      "ds_read_b128 %3, %4 offset:224\n\ts_waitcnt lgkmcnt(0)"
+      : "=&v"(x[0]), "=&v"(x[1]), "=&v"(x[2]), "=&v"(x[3])
+      : "v"(axs)
+      : "memory");
+#pragma unroll
+  for (int q = 0; q < 4; q++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) acc1[4 * q + e] = fadd(acc1[4 * q + e], fmul(fmul((float)C1[4 * q + e], x[q][e]), d));
 }
 
 template <bool BIN>
