@@ -168,14 +168,16 @@ HQ_DEV void add_chains(float acc0[16], float acc1[16], float *p0, float *p1, int
 // slice: its register r (r + 16) is the same (token, row) of the first (second) token half.
 // ---------------------------------------------------------------------------------------------------------------
 constexpr int QG = 4;   // groups a stage
-constexpr int QR = 64;  // rows of a block's tile: 4 waves, one chain each, two row slices x two token halves a wave
-constexpr int QT = 256; // threads a block
+constexpr int QT = 256; // threads a block: 4 waves, one chain each
 
+// A stage of a tile of R rows (64: two row slices x two token halves a wave; 32: one slice x two halves, for launches
+// of few tiles).  The rows' scales have room for 64 rows whatever R is: a wide scale load fills 64.
+template <int R>
 struct alignas(16) StageQ {
-  char w[QR * 128];    // int8: 64 rows x 4 groups x 32 bytes, chunks swizzled; int6: 64 rows x 4 x 24 bytes
+  char w[R * 128];     // int8: R rows x 4 groups x 32 bytes, chunks swizzled; int6: R rows x 4 x 24 bytes
   char x[BT * 128];    // 64 tokens x 4 groups x 32 bytes, chunks swizzled
-  float ws[QR][QG];    // the rows' scales of the stage's groups
-  int32_t wc[QR][QG];  // the rows' corrections (with the caller's wc)
+  float ws[64][QG];    // the rows' scales of the stage's groups
+  int32_t wc[64][QG];  // the rows' corrections (with the caller's wc)
   float xs[BT][QG];    // the tokens' scales
 };
 
@@ -206,18 +208,20 @@ HQ_DEV v4i six_half(const char *p, int kh) {
 }
 
 // A block's loads of a stage, as 1 KB pieces (256 B for the narrow scale loads) dealt to the four waves in turn:
-// the weights' pieces (8 of int8, 6 of int6), the activations' (8), then the scales' (wide: the rows', the
-// corrections' with wc, the tokens'; narrow: 4 of each).  Wave W issues pieces W, W + 4, ..., so its loads a stage
+// the weights' pieces (8 of int8, 6 of int6 a 64-row tile; half as many for 32 rows), the activations' (8), then the
+// scales' (wide: the rows', the corrections' with wc, the tokens'; narrow: R / 16 of the rows' kinds, 4 of the
+// tokens').  Wave W issues pieces W, W + 4, ..., so its loads a stage
 // are count(W); no load is issued that is not needed.  W is a template argument (the kernel runs one copy of its
 // main loop a wave), so a wave's loads are straight-line code: chosen at run time, every stage took a tree of
 // scalar branches per piece (measured 4-6 % of the launch).
-template <int PACK, bool WC, bool WIDE, int W>
+template <int PACK, bool WC, bool WIDE, int W, int R>
 struct Relaxed {
-  static constexpr int GB = PACK == 8 ? 32 : 24;    // bytes of a group of weights
-  static constexpr int NWP = PACK == 8 ? 8 : 6;     // the weights' pieces
-  static constexpr int NSK = WC ? 3 : 2;            // kinds of scale pieces: ws, (wc), xs
-  static constexpr int SPK = WIDE ? 1 : 4;          // pieces of each
-  static constexpr int P = NWP + 8 + NSK * SPK;     // pieces a stage
+  static constexpr int GB = PACK == 8 ? 32 : 24;           // bytes of a group of weights
+  static constexpr int NWP = (PACK == 8 ? 8 : 6) * R / 64;  // the weights' pieces
+  static constexpr int NRK = WC ? 2 : 1;                   // kinds of the rows' scale pieces: ws, (wc)
+  static constexpr int SPR = WIDE ? 1 : R / 16;            // pieces of each
+  static constexpr int SPT = WIDE ? 1 : 4;                 // pieces of the tokens' scales
+  static constexpr int P = NWP + 8 + NRK * SPR + SPT;      // pieces a stage
   static constexpr int PW = (P + 3) / 4;            // the most pieces of a wave
   static constexpr int count = P / 4 + (W < P % 4 ? 1 : 0);  // this wave's
   static constexpr int wave = W;
@@ -252,8 +256,9 @@ struct Relaxed {
         const int c = p - NWP, tok = 8 * c + (lane >> 3), ch = (lane & 7) ^ swz(tok);
         o = (uint32_t)(tok * J.frame + (ch >> 1) * 32 + (ch & 1) * 16);
       } else if (p < P) {
-        const int q = p - NWP - 8, kind = q / SPK, i = q % SPK;  // kind 0 ws, 1 wc (or xs without wc), 2 xs
-        const bool tokens = kind == NSK - 1;
+        const int q = p - NWP - 8;  // ws pieces, then wc's, then xs's
+        const bool tokens = q >= NRK * SPR;
+        const int i = tokens ? q - NRK * SPR : q % SPR;
         if (WIDE) {  // lane l: row (or token) l, its 16 bytes
           o = tokens ? (uint32_t)(lane * J.sframe) : (uint32_t)(lane * ng * 4);
         } else {     // lane l: row 16 i + l / 4, group (l % 4) ^ gswz(row)
@@ -266,7 +271,7 @@ struct Relaxed {
   }
 
   // wave w's loads of stage s (groups 4 s .. 4 s + 3) into S
-  HQ_DEV void load(StageQ &S, int s) {
+  HQ_DEV void load(StageQ<R> &S, int s) {
 #pragma unroll
     for (int k = 0; k < PW; k++) {
       const int p = wave + 4 * k;
@@ -275,14 +280,15 @@ struct Relaxed {
       } else if (p < NWP + 8) {
         dma16(rx, S.x + (p - NWP) * 1024, off[k], s * QG * 32);
       } else if (p < P) {
-        const int q = p - NWP - 8, kind = q / SPK, i = q % SPK;
-        const bool tokens = kind == NSK - 1;
+        const int q = p - NWP - 8;
+        const bool tokens = q >= NRK * SPR;
+        const int i = tokens ? q - NRK * SPR : q % SPR;
         // a branch for each resource: a resource chosen by a select is a per-lane value to the compiler, which then
         // loops over its lanes (v_readfirstlane) around every load (measured 28 % of the launch with wc)
         if (tokens) {
           if (WIDE) dma16(rxs, &S.xs[16 * i][0], off[k], s * QG * 4);
           else dma4(rxs, &S.xs[16 * i][0], off[k], s * QG * 4);
-        } else if (kind == 0 || !WC) {
+        } else if (q < SPR) {
           if (WIDE) dma16(rws, &S.ws[16 * i][0], off[k], s * QG * 4);
           else dma4(rws, &S.ws[16 * i][0], off[k], s * QG * 4);
         } else {
@@ -296,9 +302,9 @@ struct Relaxed {
 
 // stage s's loads have landed everywhere: this wave's own, with those of the two stages after it still in flight,
 // then the block's barrier
-template <int PACK, bool WC, bool WIDE, int W>
+template <int PACK, bool WC, bool WIDE, int W, int R>
 HQ_DEV void q_ready() {
-  stage_ready<2 * Relaxed<PACK, WC, WIDE, W>::count>();
+  stage_ready<2 * Relaxed<PACK, WC, WIDE, W, R>::count>();
 }
 
 // a wave's operands of one group gi of a stage: the activations of both token halves, the weights of both row slices
@@ -374,9 +380,9 @@ HQ_DEV v4i six_regs(const uint2 p[3], int kh) {
   return v;
 }
 
-// a wave's operands of group gi of stage S (ds_ops' reads)
-template <int PACK, bool WC, bool WIDE>
-HQ_DEV OpsQ read_ops(const StageQ &S, int gi, int lane) {
+// a wave's operands of group gi of stage S (ds_ops' reads; a 32-row tile's second slice reads the first's again)
+template <int PACK, bool WC, bool WIDE, int R>
+HQ_DEV OpsQ read_ops(const StageQ<R> &S, int gi, int lane) {
   OpsQ o;
   uint2 six[2][3];
   const int kh = lane >> 5, l32 = lane & 31;
@@ -388,7 +394,7 @@ HQ_DEV OpsQ read_ops(const StageQ &S, int gi, int lane) {
   }
 #pragma unroll
   for (int sp = 0; sp < 2; sp++) {
-    const int row = 32 * sp + l32;
+    const int row = (R == 64 ? 32 * sp : 0) + l32;
     aw[sp] = PACK == 8 ? lds_addr(S.w + row * 128 + ((2 * gi + kh) ^ swz(row)) * 16) : lds_addr(S.w + row * 96 + gi * 24);
     aws[sp] = lds_addr(&S.ws[row][sslot<WIDE>(row, gi)]);
     awc[sp] = lds_addr(&S.wc[row][sslot<WIDE>(row, gi)]);
@@ -396,14 +402,14 @@ HQ_DEV OpsQ read_ops(const StageQ &S, int gi, int lane) {
   ds_ops<PACK, WC>(o, six, ax, aw, lds_addr(&S.xs[lane][sslot<WIDE>(lane, gi)]), aws, awc);
   if (PACK == 6) {
     o.W[0] = six_regs(six[0], kh);
-    o.W[1] = six_regs(six[1], kh);
+    if (R == 64) o.W[1] = six_regs(six[1], kh);
   }
   return o;
 }
 
 // the same from C++ loads (outside the main loop, where no load into LDS is in flight)
-template <int PACK, bool WC, bool WIDE>
-HQ_DEV OpsQ read_ops_plain(const StageQ &S, int gi, int lane) {
+template <int PACK, bool WC, bool WIDE, int R>
+HQ_DEV OpsQ read_ops_plain(const StageQ<R> &S, int gi, int lane) {
   OpsQ o;
   const int kh = lane >> 5, l32 = lane & 31;
 #pragma unroll
@@ -412,7 +418,7 @@ HQ_DEV OpsQ read_ops_plain(const StageQ &S, int gi, int lane) {
     o.X[h] = *(const v4i *)(S.x + t * 128 + ((2 * gi + kh) ^ swz(t)) * 16);
   }
 #pragma unroll
-  for (int sp = 0; sp < 2; sp++) {
+  for (int sp = 0; sp < R / 32; sp++) {
     const int row = 32 * sp + l32;
     if (PACK == 8) o.W[sp] = *(const v4i *)(S.w + row * 128 + ((2 * gi + kh) ^ swz(row)) * 16);
     else o.W[sp] = six_half(S.w + row * 96 + gi * 24, kh);
@@ -451,20 +457,25 @@ HQ_DEV void fold(float a[16], const v16i &c, const v32f &sc, int h) {
 // Stage s of wave W's chain (group 4 s + W): the stage's loads landed everywhere (the block's barrier), the
 // wave's operands read from `cur`, its loads of stage s + 3 issued into `dma` (the buffer stage s - 1's operands came
 // from, which every wave has read by this barrier), then the four sub-tiles (slice, half) = (0, 0), (0, 1), (1, 0),
-// (1, 1), each sub-tile's MFMAs issued before the previous one's fold so that the matrix core and the VALU take
+// (1, 1) (a 32-row tile: the first two), each sub-tile's MFMAs issued before the previous one's fold so that the matrix core and the VALU take
 // turns without waiting for each other.  Every wave has issued its loads of stages up to s + 2 at the barrier (a
 // stage past the job's last group loads zeros, and its buffer is never read), so "stage s landed" is always "at most
 // two stages of this wave's loads in flight".
-template <int PACK, bool WC, bool WIDE, int W>
-HQ_DEV void q_stage(Relaxed<PACK, WC, WIDE, W> &L, const StageQ &cur, StageQ &dma, int s, float acc[4][16],
+template <int PACK, bool WC, bool WIDE, int W, int R>
+HQ_DEV void q_stage(Relaxed<PACK, WC, WIDE, W, R> &L, const StageQ<R> &cur, StageQ<R> &dma, int s, float acc[4][16],
                     int lane) {
-  q_ready<PACK, WC, WIDE, W>();
-  const OpsQ op = read_ops<PACK, WC, WIDE>(cur, W, lane);
+  q_ready<PACK, WC, WIDE, W, R>();
+  const OpsQ op = read_ops<PACK, WC, WIDE, R>(cur, W, lane);
   L.load(dma, s + AHEAD);
   const v16i cin0 = corrections<WC>(op, 0);
   const v32f S0 = scales(op, 0);
   const v16i C0 = integers(op, 0, 0, cin0);
   const v16i C1 = integers(op, 0, 1, cin0);
+  if (R == 32) {
+    fold(acc[0], C0, S0, 0);
+    fold(acc[1], C1, S0, 1);
+    return;
+  }
   const v16i cin1 = corrections<WC>(op, 1);
   fold(acc[0], C0, S0, 0);
   const v32f S1 = scales(op, 1);
@@ -478,14 +489,15 @@ HQ_DEV void q_stage(Relaxed<PACK, WC, WIDE, W> &L, const StageQ &cur, StageQ &dm
 // the 4 chains of the tile added in LDS, ((a0 + a1) + a2) + a3, for its four sub-tiles: wave k adds its sums to
 // what waves 0..k-1 left (the values of a lane are the same (row, token)s in the four waves); the sums end in chain
 // 3's wave.  p0 (sub-tiles 0, 1) and p1 (2, 3): 32 x 64 floats each that nothing else uses, value v of a lane at
-// [v][lane] (consecutive lanes, consecutive banks)
+// [v][lane] (consecutive lanes, consecutive banks).  NS: the sub-tiles, 4 (64-row tiles) or 2 (32 rows)
+template <int NS>
 HQ_DEV void add_chains4(float acc[4][16], float *p0, float *p1, int chain, int lane) {
   float *q[2] = {p0 + lane, p1 + lane};
   for (int k = 0; k < 4; k++) {
     __syncthreads();
     if (chain == k) {
 #pragma unroll
-      for (int i = 0; i < 4; i++)
+      for (int i = 0; i < NS; i++)
 #pragma unroll
         for (int r = 0; r < 16; r++) {
           float *m = q[i >> 1] + (16 * (i & 1) + r) * 64;
@@ -497,34 +509,34 @@ HQ_DEV void add_chains4(float acc[4][16], float *p0, float *p1, int chain, int l
 }
 
 // wave W's stages of the tile (chain W): its loads, and every stage in order
-template <int PACK, bool WC, bool WIDE, int W>
-HQ_DEV void q_chain(const Job &J, int row0, int tok0, int M, int stages, StageQ &b0, StageQ &b1, StageQ &b2,
-                    StageQ &b3, float acc[4][16], int lane) {
-  Relaxed<PACK, WC, WIDE, W> L(J, row0, tok0, M);
+template <int PACK, bool WC, bool WIDE, int W, int R>
+HQ_DEV void q_chain(const Job &J, int row0, int tok0, int M, int stages, StageQ<R> &b0, StageQ<R> &b1,
+                    StageQ<R> &b2, StageQ<R> &b3, float acc[4][16], int lane) {
+  Relaxed<PACK, WC, WIDE, W, R> L(J, row0, tok0, M);
   // stages 0..2 first (whatever the job has: a stage past its groups loads zeros); stage s's operands come from
   // buffer s % 4 and its loads of stage s + 3 go into buffer (s - 1) % 4
   L.load(b0, 0);
   L.load(b1, 1);
   L.load(b2, 2);
   for (int s = 0; s < stages; s += RING) {
-    q_stage<PACK, WC, WIDE, W>(L, b0, b3, s, acc, lane);
+    q_stage<PACK, WC, WIDE, W, R>(L, b0, b3, s, acc, lane);
     if (s + 1 >= stages) break;
-    q_stage<PACK, WC, WIDE, W>(L, b1, b0, s + 1, acc, lane);
+    q_stage<PACK, WC, WIDE, W, R>(L, b1, b0, s + 1, acc, lane);
     if (s + 2 >= stages) break;
-    q_stage<PACK, WC, WIDE, W>(L, b2, b1, s + 2, acc, lane);
+    q_stage<PACK, WC, WIDE, W, R>(L, b2, b1, s + 2, acc, lane);
     if (s + 3 >= stages) break;
-    q_stage<PACK, WC, WIDE, W>(L, b3, b2, s + 3, acc, lane);
+    q_stage<PACK, WC, WIDE, W, R>(L, b3, b2, s + 3, acc, lane);
   }
 }
 
-template <int PACK, bool WC, bool WIDE>
+template <int PACK, bool WC, bool WIDE, int R>
 __global__ __launch_bounds__(QT, 2) void gemm_relaxed(Job J) {
-  __shared__ StageQ b0, b1, b2, b3;
+  __shared__ StageQ<R> b0, b1, b2, b3;
   const int M = J.count;
   const int ng = J.n >> 5, ng4 = ng & ~3;
   int rb, tb;
-  tile_of(blockIdx.x, gridDim.x, (J.r1 - J.r0 + QR - 1) / QR, rb, tb);
-  const int row0 = J.r0 + rb * QR, tok0 = tb * BT;
+  tile_of(blockIdx.x, gridDim.x, (J.r1 - J.r0 + R - 1) / R, rb, tb);
+  const int row0 = J.r0 + rb * R, tok0 = tb * BT;
   const int lane = threadIdx.x & 63;
   const int chain = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 
@@ -536,21 +548,21 @@ __global__ __launch_bounds__(QT, 2) void gemm_relaxed(Job J) {
 
   const int stages = ng4 / QG;  // whole stages of the four chains; the groups past them (ng % 4) are one more stage
   switch (chain) {
-  case 0: q_chain<PACK, WC, WIDE, 0>(J, row0, tok0, M, stages, b0, b1, b2, b3, acc, lane); break;
-  case 1: q_chain<PACK, WC, WIDE, 1>(J, row0, tok0, M, stages, b0, b1, b2, b3, acc, lane); break;
-  case 2: q_chain<PACK, WC, WIDE, 2>(J, row0, tok0, M, stages, b0, b1, b2, b3, acc, lane); break;
-  default: q_chain<PACK, WC, WIDE, 3>(J, row0, tok0, M, stages, b0, b1, b2, b3, acc, lane); break;
+  case 0: q_chain<PACK, WC, WIDE, 0, R>(J, row0, tok0, M, stages, b0, b1, b2, b3, acc, lane); break;
+  case 1: q_chain<PACK, WC, WIDE, 1, R>(J, row0, tok0, M, stages, b0, b1, b2, b3, acc, lane); break;
+  case 2: q_chain<PACK, WC, WIDE, 2, R>(J, row0, tok0, M, stages, b0, b1, b2, b3, acc, lane); break;
+  default: q_chain<PACK, WC, WIDE, 3, R>(J, row0, tok0, M, stages, b0, b1, b2, b3, acc, lane); break;
   }
   stage_ready<0>();  // every load has landed (the tail's too) and every wave is done with the stages
-  auto ring = [&](int i) -> StageQ & { return i == 0 ? b0 : i == 1 ? b1 : i == 2 ? b2 : b3; };
-  add_chains4(acc, (float *)&ring((stages + 1) % RING), (float *)&ring((stages + 2) % RING), chain, lane);
+  auto ring = [&](int i) -> StageQ<R> & { return i == 0 ? b0 : i == 1 ? b1 : i == 2 ? b2 : b3; };
+  add_chains4<R / 16>(acc, (float *)&ring((stages + 1) % RING), (float *)&ring((stages + 2) % RING), chain, lane);
   if (chain == 3) {
     // the groups past the fours, one at a time, after the four chains' sum (relaxed/int8.ts:40-47)
-    const StageQ &T = ring(stages % RING);
+    const StageQ<R> &T = ring(stages % RING);
     for (int gi = 0; gi < ng - ng4; gi++) {
-      const OpsQ o = read_ops_plain<PACK, WC, WIDE>(T, gi, lane);
+      const OpsQ o = read_ops_plain<PACK, WC, WIDE, R>(T, gi, lane);
 #pragma unroll
-      for (int sp = 0; sp < 2; sp++) {
+      for (int sp = 0; sp < R / 32; sp++) {
         const v16i cin = corrections<WC>(o, sp);
         const v32f sc = scales(o, sp);
 #pragma unroll
@@ -558,7 +570,7 @@ __global__ __launch_bounds__(QT, 2) void gemm_relaxed(Job J) {
       }
     }
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < R / 16; i++) {
       const int row = row0 + 32 * (i >> 1) + (lane & 31);
       if (row < J.r1) {
         const int tbase = tok0 + 32 * (i & 1) + 4 * (lane >> 5);
@@ -825,13 +837,25 @@ bool wide_scales(const Job &j) {
          (j.count <= 1 || j.sframe % 16 == 0);
 }
 
-template <int PACK>
-void launch_relaxed(const Job &job, dim3 grid, hipStream_t s) {
+template <int PACK, int R>
+void launch_relaxed(const Job &job, int token_tiles, hipStream_t s) {
+  const dim3 grid(((job.r1 - job.r0 + R - 1) / R) * token_tiles);
   const bool wc = job.wc != nullptr, wide = wide_scales(job);
-  if (wc && wide) hipLaunchKernelGGL((gemm_relaxed<PACK, true, true>), grid, dim3(QT), 0, s, job);
-  else if (wc) hipLaunchKernelGGL((gemm_relaxed<PACK, true, false>), grid, dim3(QT), 0, s, job);
-  else if (wide) hipLaunchKernelGGL((gemm_relaxed<PACK, false, true>), grid, dim3(QT), 0, s, job);
-  else hipLaunchKernelGGL((gemm_relaxed<PACK, false, false>), grid, dim3(QT), 0, s, job);
+  if (wc && wide) hipLaunchKernelGGL((gemm_relaxed<PACK, true, true, R>), grid, dim3(QT), 0, s, job);
+  else if (wc) hipLaunchKernelGGL((gemm_relaxed<PACK, true, false, R>), grid, dim3(QT), 0, s, job);
+  else if (wide) hipLaunchKernelGGL((gemm_relaxed<PACK, false, true, R>), grid, dim3(QT), 0, s, job);
+  else hipLaunchKernelGGL((gemm_relaxed<PACK, false, false, R>), grid, dim3(QT), 0, s, job);
+}
+
+// 32-row tiles where they take fewer rounds of the CUs' block slots (two a CU) than 64-row tiles, counting a round of
+// 32-row tiles as kTile32 of one of 64-row tiles (measured over launches of many rounds: 383 against 474 TOPS, so a
+// 32-row tile costs 0.62 of a 64-row one; the 8B prefill's shapes all keep 64-row tiles)
+constexpr double kTile32 = 0.62;
+bool short_tiles(int rows, int token_tiles) {
+  const int64_t slots = 2 * (int64_t)cu_count();
+  const int64_t t64 = (int64_t)((rows + 63) / 64) * token_tiles, t32 = (int64_t)((rows + 31) / 32) * token_tiles;
+  const int64_t r64 = (t64 + slots - 1) / slots, r32 = (t32 + slots - 1) / slots;
+  return kTile32 * (double)r32 < (double)r64;
 }
 
 }  // namespace
@@ -843,8 +867,14 @@ hipError_t launch_gemm(Kind kind, const Job &job, hipStream_t s) {
   if (rows <= 0 || job.count <= 0) return hipSuccess;
   const int token_tiles = (job.count + BT - 1) / BT;
   switch (kind) {
-  case Q8R: launch_relaxed<8>(job, dim3(((rows + QR - 1) / QR) * token_tiles), s); break;
-  case Q6R: launch_relaxed<6>(job, dim3(((rows + QR - 1) / QR) * token_tiles), s); break;
+  case Q8R:
+    if (short_tiles(rows, token_tiles)) launch_relaxed<8, 32>(job, token_tiles, s);
+    else launch_relaxed<8, 64>(job, token_tiles, s);
+    break;
+  case Q6R:
+    if (short_tiles(rows, token_tiles)) launch_relaxed<6, 32>(job, token_tiles, s);
+    else launch_relaxed<6, 64>(job, token_tiles, s);
+    break;
   case T2R:
   case T2: hipLaunchKernelGGL(gemm_ternary<false>, dim3(((rows + BR - 1) / BR) * token_tiles), dim3(NT), 0, s, job); break;
   case B1R:

@@ -374,15 +374,35 @@ def test_q6r_many_tokens(pkg, arena, oracle, count, ng):
             assert same_bits(got[t], want), f"wc {form} token {t}: {first_difference(got[t], want)}"
 
 
+def tile_rows(rows, token_tiles, cus):
+    """the rows of the prompt kernel's tile for a launch (gemm.hip's short_tiles: 32-row tiles where their rounds of
+    the 2 x CU block slots, each 0.62 of a 64-row round, are fewer)"""
+    slots = 2 * cus
+    t64, t32 = -(-rows // 64) * token_tiles, -(-rows // 32) * token_tiles
+    return 32 if 0.62 * -(-t32 // slots) < -(-t64 // slots) else 64
+
+
 @pytest.mark.parametrize("packing", ["int8", "int6"])
 @pytest.mark.parametrize("ng", [13, 16])
-def test_relaxed_prompt_many_tiles(pkg, arena, oracle, packing, ng):
-    """A prompt over many of the matrix cores' 64-row x 64-token tiles: 301 rows cut at 5 and 299 (tiles starting
-    off a multiple of 64, a ragged last tile), 131 tokens (a ragged third token tile), the corrections given, moved
-    and derived, the scales loaded four bytes a lane (13 groups: also groups past the last four) and sixteen (16)."""
+@pytest.mark.parametrize("height", [32, 64])
+def test_relaxed_prompt_many_tiles(pkg, arena, oracle, packing, ng, height):
+    """A prompt over many of the matrix cores' tiles, of both heights (32 rows: a launch of few tiles, 301 rows cut at
+    5 and 299; 64 rows: enough row tiles to fill the block slots, cut at 5 and 21 short of the end): tiles starting
+    off a multiple of the height, a ragged last tile, 131 tokens (a ragged third token tile), the corrections given,
+    moved and derived, the scales loaded four bytes a lane (13 groups: also groups past the last four) and sixteen
+    (16)."""
+    import torch
     from pyodide_llm_amd import jobs
-    rng = np.random.default_rng(4242 + ng + (100 if packing == "int6" else 0))
-    rows, count, r0, r1 = 301, 131, 5, 299
+    rng = np.random.default_rng(4242 + ng + (100 if packing == "int6" else 0) + height)
+    count, r0 = 131, 5
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    if height == 32:
+        rows, r1 = 301, 299
+    else:  # 64-row tiles a little fewer than the block slots: one round of them, two of 32-row tiles
+        rows = 64 * ((2 * cus) // 3 - 1) + 26
+        r1 = rows - 21
+    # int8 goes through the drop-in tile (a launch of rows r0..r1), int6 through a phase (rows 0..r1)
+    assert tile_rows(r1 - r0 if packing == "int8" else r1, 3, cus) == height
     n = 32 * ng
     frame = ((n + 4 * ng + 15) // 16) * 16
     if packing == "int8":
