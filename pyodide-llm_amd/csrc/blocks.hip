@@ -261,8 +261,13 @@ HQ_DEV void sb_load_block(BlockBytes<BYTES> &B, const SbBatch &b, int unit, int 
 }
 
 constexpr int kSbLongRow = 32;
-// the most a launch stages of a token's activations (n + n/2 bytes: n up to 32768)
-constexpr size_t kSbStageMax = 48 * 1024;
+// A staged block of 256 activations takes kSbPitch bytes of LDS: the 16 lanes of a row read the same 16 bytes of 16
+// consecutive blocks, which 256 bytes apart would all fall in one bank (a 16-way conflict on every read); 16 bytes of
+// padding put them in 16 different bank quads.  The scales and sums follow the blocks.
+constexpr int kSbPitch = 272;
+constexpr size_t sb_stage_bytes(int n) { return (size_t)(n >> 8) * kSbPitch + n / 2; }
+// the most a launch stages of a token's activations (n up to 32768)
+constexpr size_t kSbStageMax = 52 * 1024;
 constexpr int sb_lanes(int blocks) { return blocks >= kSbLongRow ? 64 : 16; }
 
 template <int TY> constexpr int lds_table_bytes() {
@@ -290,11 +295,11 @@ __global__ __launch_bounds__(256) void gemv_sb(SbBatch batch) {
   }
   if (STAGE) {
     const Job &J0 = batch.job[0];
-    const int per = J0.n + J0.n / 2;
+    const int per = J0.n + J0.n / 2, acts = (J0.n >> 8) * kSbPitch;
     for (int i = threadIdx.x; i < per / 16; i += 256) {
       const int o = 16 * i;
-      const char *from = o < J0.n ? J0.xq + o : J0.xs + (o - J0.n);
-      *(uint4 *)(staged + o) = *(const uint4 *)from;
+      if (o < J0.n) *(uint4 *)(staged + (o >> 8) * kSbPitch + (o & 255)) = *(const uint4 *)(J0.xq + o);
+      else *(uint4 *)(staged + acts + (o - J0.n)) = *(const uint4 *)(J0.xs + (o - J0.n));
     }
   }
   uint32_t iq4[4] = {0u, 0u, 0u, 0u};
@@ -337,7 +342,7 @@ __global__ __launch_bounds__(256) void gemv_sb(SbBatch batch) {
 #pragma unroll
     for (int t = 0; t < T; t++) {
       xq[t] = STAGE ? (const int8_t *)staged : (const int8_t *)(J.xq + t * J.frame);
-      xs[t] = STAGE ? (const float *)(staged + J.n) : (const float *)(J.xs + t * J.sframe);
+      xs[t] = STAGE ? (const float *)(staged + (J.n >> 8) * kSbPitch) : (const float *)(J.xs + t * J.sframe);
       s16[t] = (const int16_t *)(xs[t] + (J.n >> 5));
       s8[t] = s16[t] + (J.n >> 4);
     }
@@ -358,7 +363,7 @@ __global__ __launch_bounds__(256) void gemv_sb(SbBatch batch) {
       for (int j = 0; j < 4; j++) signed_part[j] = c.mag[j] & c.neg[j];
 #pragma unroll
       for (int t = 0; t < T; t++) {
-        const uint4 av = *(const uint4 *)(xq[t] + 256 * bl + 16 * h);
+        const uint4 av = *(const uint4 *)(xq[t] + (STAGE ? kSbPitch : 256) * bl + 16 * h);
         const int32_t a[4] = {(int32_t)av.x, (int32_t)av.y, (int32_t)av.z, (int32_t)av.w};
         int32_t d = 0;
 #pragma unroll
@@ -1034,14 +1039,12 @@ hipError_t launch_sb(const Job *jobs, int32_t njobs, hipStream_t s) {
   b.njobs = njobs;
   if (units == 0) return hipSuccess;
   const int T = jobs[0].count;
-  // one token's activations, the same for every job: staged in LDS (n + n/2 bytes) when they fit, for the types
-  // that read no grid (Q2_K, Q4_K, IQ4_XS: measured faster; the grids' gathers and the activations' reads would
-  // share the LDS)
-  const int ty = jobs[0].type;
-  bool same = T == 1 && (ty == Q2_K || ty == Q4_K || ty == IQ4_XS);
+  // one token's activations, the same for every job: staged in LDS (sb_stage_bytes) when they fit (every type:
+  // with the padded pitch, 20-51 % faster than reading them through the L1 for the types that gather from a grid)
+  bool same = T == 1;
   for (int j = 1; j < njobs; j++)
     same = same && jobs[j].xq == jobs[0].xq && jobs[j].xs == jobs[0].xs && jobs[j].n == jobs[0].n;
-  const size_t stage_bytes = (size_t)jobs[0].n + jobs[0].n / 2;
+  const size_t stage_bytes = sb_stage_bytes(jobs[0].n);
   const size_t lds = same && stage_bytes <= kSbStageMax ? stage_bytes : 0;
   switch (jobs[0].type) {
   case Q2_K: return launch_type<Q2_K>(b, T, L, lds, s);
