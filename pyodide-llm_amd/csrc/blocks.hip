@@ -222,7 +222,7 @@ HQ_DEV float block_fm(const BB &B) {
 // the products (matmul_sbr == matmul_sb): rows of L lanes (16, 4 rows a wave; 64 for rows of 32 blocks or more,
 // a row a wave), a block of 256 weights a lane a step.
 // The blocks of a launch are persistent: each copies its type's grid and sign table (at most 17 KB) into LDS once,
-// and its waves take groups of 4 rows in turn.
+// and its waves take units (a wave's 64 / L rows) in turn.
 // ---------------------------------------------------------------------------------------------------------------
 struct SbBatch {
   Job job[kMaxJobs];
@@ -261,11 +261,17 @@ HQ_DEV void sb_load_block(BlockBytes<BYTES> &B, const SbBatch &b, int unit, int 
 }
 
 constexpr int kSbLongRow = 32;
-// A staged block of 256 activations takes kSbPitch bytes of LDS: the 16 lanes of a row read the same 16 bytes of 16
-// consecutive blocks, which 256 bytes apart would all fall in one bank (a 16-way conflict on every read); 16 bytes of
-// padding put them in 16 different bank quads.  The scales and sums follow the blocks.
-constexpr int kSbPitch = 272;
-constexpr size_t sb_stage_bytes(int n) { return (size_t)(n >> 8) * kSbPitch + n / 2; }
+// The staged activations: the 16 lanes of a row read the same bytes of 16 consecutive blocks, which 256 bytes apart
+// would all fall in one bank (a 16-way conflict on every read).  A block's 256 bytes take kSbPitch (16 bytes of
+// padding: 16 different bank quads), the scales and sums following all the blocks; or, for the types that read the
+// sums of 16 or 8 too (the K types, IQ1), a block's activations, 8 scales, 16 sums of 16 and 32 sums of 8 together
+// in kSbPitchSums bytes (their reads as far apart: Q4_K 7 % faster, IQ1_S 4 %, the others' 1-2 % slower)
+constexpr int kSbPitch = 272, kSbPitchSums = 400;
+template <int TY> constexpr bool stages_sums() { return has_minimums<TY>() || is_iq1<TY>(); }
+constexpr bool stages_sums(int ty) { return ty == Q2_K || ty == Q4_K || ty == IQ1_S || ty == IQ1_M; }
+constexpr size_t sb_stage_bytes(int ty, int n) {
+  return stages_sums(ty) ? (size_t)(n >> 8) * kSbPitchSums : (size_t)(n >> 8) * kSbPitch + n / 2;
+}
 // the most a launch stages of a token's activations (n up to 32768)
 constexpr size_t kSbStageMax = 52 * 1024;
 constexpr int sb_lanes(int blocks) { return blocks >= kSbLongRow ? 64 : 16; }
@@ -277,29 +283,41 @@ template <int TY> constexpr int lds_table_bytes() {
 
 // STAGE (one token, and every job of the launch the same activations): the block copies the token's n bytes and
 // its n/2 bytes of scales and sums into LDS first, so a step's activations are LDS reads, which the next step's block
-// loads in flight do not hold up (a vector memory load waits for every one issued before it)
+// loads in flight do not hold up (a vector memory load waits for every one issued before it).  kSbWaves waves a
+// block: the fewer the blocks a CU, the fewer copies of the tables and the activations its LDS is filled with
+// (16 against 4: 3-10 % faster for every type)
+constexpr int kSbWaves = 16;
 template <int TY, int T, int L, bool STAGE>
-__global__ __launch_bounds__(256) void gemv_sb(SbBatch batch) {
+__global__ __launch_bounds__(64 * kSbWaves) void gemv_sb(SbBatch batch) {
   constexpr int R = 64 / L;  // rows a wave
   constexpr int BYTES = sb_block_bytes(TY);
   constexpr int GRID = grid_bytes<TY>();
-  __shared__ FoldL<T, L> fold[4];
+  __shared__ FoldL<T, L> fold[kSbWaves];
   __shared__ __align__(16) uint8_t table[lds_table_bytes<TY>()];
   extern __shared__ __align__(16) char staged[];
   const uint8_t *tab = (const uint8_t *)batch.job[0].ws;  // every job of a launch has the same tables' area
   {
     const uint4 *from = (const uint4 *)(tab + grid_at<TY>());
-    for (int i = threadIdx.x; i < GRID / 16; i += 256) ((uint4 *)table)[i] = from[i];
+    for (int i = threadIdx.x; i < GRID / 16; i += 64 * kSbWaves) ((uint4 *)table)[i] = from[i];
     if (reads_signs<TY>())
-      for (int i = threadIdx.x; i < 1024 / 16; i += 256) ((uint4 *)(table + GRID))[i] = ((const uint4 *)(tab + T_SIGNS))[i];
+      for (int i = threadIdx.x; i < 1024 / 16; i += 64 * kSbWaves)
+        ((uint4 *)(table + GRID))[i] = ((const uint4 *)(tab + T_SIGNS))[i];
   }
   if (STAGE) {
     const Job &J0 = batch.job[0];
-    const int per = J0.n + J0.n / 2, acts = (J0.n >> 8) * kSbPitch;
-    for (int i = threadIdx.x; i < per / 16; i += 256) {
-      const int o = 16 * i;
-      if (o < J0.n) *(uint4 *)(staged + (o >> 8) * kSbPitch + (o & 255)) = *(const uint4 *)(J0.xq + o);
-      else *(uint4 *)(staged + acts + (o - J0.n)) = *(const uint4 *)(J0.xs + (o - J0.n));
+    const int per = J0.n + J0.n / 2, acts = (J0.n >> 8) * kSbPitch, n8 = J0.n >> 3;
+    for (int i = threadIdx.x; i < per / 16; i += 64 * kSbWaves) {
+      const int o = 16 * i, r = o - J0.n;
+      int at;
+      if (stages_sums<TY>()) {  // block b's activations, scales, sums of 16, sums of 8 at b kSbPitchSums + 0, 256, 288, 320
+        if (o < J0.n) at = (o >> 8) * kSbPitchSums + (o & 255);
+        else if (r < n8) at = (r >> 5) * kSbPitchSums + 256 + (r & 31);
+        else if (r < 2 * n8) at = ((r - n8) >> 5) * kSbPitchSums + 288 + ((r - n8) & 31);
+        else at = ((r - 2 * n8) >> 6) * kSbPitchSums + 320 + ((r - 2 * n8) & 63);
+      } else {
+        at = o < J0.n ? (o >> 8) * kSbPitch + (o & 255) : acts + r;
+      }
+      *(uint4 *)(staged + at) = *(const uint4 *)(o < J0.n ? J0.xq + o : J0.xs + r);
     }
   }
   uint32_t iq4[4] = {0u, 0u, 0u, 0u};
@@ -312,8 +330,8 @@ __global__ __launch_bounds__(256) void gemv_sb(SbBatch batch) {
   // the wave's number as a scalar: its units, jobs and buffers are then the wave's own (scalar registers)
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), slot = (threadIdx.x & 63) / L;
   FoldL<T, L> &f = fold[wave];
-  const int units = batch.unit0[batch.njobs], stride = gridDim.x * 4;
-  int unit = blockIdx.x * 4 + wave, it = 0, count = 0;
+  const int units = batch.unit0[batch.njobs], stride = gridDim.x * kSbWaves;
+  int unit = blockIdx.x * kSbWaves + wave, it = 0, count = 0;
   if (unit >= units) return;  // (no barrier follows)
   // a wave's steps one after the other (a step: a unit's rows, a block a lane), the next step's blocks loaded before
   // this one is decoded; past the wave's last step it loads this step's blocks again, so every step issues the same
@@ -342,13 +360,17 @@ __global__ __launch_bounds__(256) void gemv_sb(SbBatch batch) {
 #pragma unroll
     for (int t = 0; t < T; t++) {
       xq[t] = STAGE ? (const int8_t *)staged : (const int8_t *)(J.xq + t * J.frame);
-      xs[t] = STAGE ? (const float *)(staged + (J.n >> 8) * kSbPitch) : (const float *)(J.xs + t * J.sframe);
+      xs[t] = STAGE && !stages_sums<TY>() ? (const float *)(staged + (J.n >> 8) * kSbPitch)
+                                          : (const float *)(J.xs + t * J.sframe);
       s16[t] = (const int16_t *)(xs[t] + (J.n >> 5));
       s8[t] = s16[t] + (J.n >> 4);
     }
     const int b = it * L + lane;
     const bool valid = b < blocks;
     const int bl = valid ? b : 0;
+    // the staged copy of block bl's activations, and of its scales and sums (stages_sums)
+    constexpr int PITCH = STAGE ? (stages_sums<TY>() ? kSbPitchSums : kSbPitch) : 256;
+    const char *sblk = staged + PITCH * bl;
     int32_t G[T][8], Mi[T][8];
 #pragma unroll
     for (int t = 0; t < T; t++)
@@ -363,7 +385,7 @@ __global__ __launch_bounds__(256) void gemv_sb(SbBatch batch) {
       for (int j = 0; j < 4; j++) signed_part[j] = c.mag[j] & c.neg[j];
 #pragma unroll
       for (int t = 0; t < T; t++) {
-        const uint4 av = *(const uint4 *)(xq[t] + (STAGE ? kSbPitch : 256) * bl + 16 * h);
+        const uint4 av = *(const uint4 *)((const char *)xq[t] + PITCH * bl + 16 * h);
         const int32_t a[4] = {(int32_t)av.x, (int32_t)av.y, (int32_t)av.z, (int32_t)av.w};
         int32_t d = 0;
 #pragma unroll
@@ -375,17 +397,20 @@ __global__ __launch_bounds__(256) void gemv_sb(SbBatch batch) {
           d -= 2 * e;
         }
         if (is_iq1<TY>()) {  // 8 dot(code, a) - (7 + 2 down) sum of each 8 (token.ts:93-99, 117-127)
-          const int32_t e0 = s8[t][32 * bl + 2 * h], e1 = s8[t][32 * bl + 2 * h + 1];
+          const int16_t *s8b = STAGE ? (const int16_t *)(sblk + 320) : s8[t] + 32 * bl;
+          const int32_t e0 = s8b[2 * h], e1 = s8b[2 * h + 1];
           d = 8 * d - (7 + 2 * (int32_t)c.down0) * e0 - (7 + 2 * (int32_t)c.down1) * e1;
         }
         G[t][h >> 1] += c.S * d;
-        if (has_minimums<TY>()) Mi[t][h >> 1] += c.M * (int32_t)s16[t][16 * bl + h];
+        if (has_minimums<TY>())
+          Mi[t][h >> 1] += c.M * (int32_t)(STAGE ? (const int16_t *)(sblk + 288) : s16[t] + 16 * bl)[h];
       }
     }
     const float F = block_f<TY>(B), Fm = block_fm<TY>(B);
 #pragma unroll
     for (int t = 0; t < T; t++) {
-      const float4 x0 = *(const float4 *)(xs[t] + 8 * bl), x1 = *(const float4 *)(xs[t] + 8 * bl + 4);
+      const float *xsb = STAGE && stages_sums<TY>() ? (const float *)(sblk + 256) : xs[t] + 8 * bl;
+      const float4 x0 = *(const float4 *)xsb, x1 = *(const float4 *)(xsb + 4);
       const float sl[4] = {x0.x, x0.y, x0.z, x0.w}, sh[4] = {x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
       for (int k = 0; k < 4; k++) {
@@ -418,7 +443,7 @@ __global__ __launch_bounds__(256) void gemv_sb(SbBatch batch) {
   }
 }
 
-// a launch's blocks: as many as stay resident together (at most the waves' groups of rows over 4); lds: the staged
+// a launch's blocks: as many as stay resident together (at most the units over kSbWaves); lds: the staged
 // activations' bytes (0: none)
 template <int TY, int T, int L, bool STAGE>
 hipError_t launch_tt(const SbBatch &b, size_t lds, hipStream_t s) {
@@ -428,13 +453,13 @@ hipError_t launch_tt(const SbBatch &b, size_t lds, hipStream_t s) {
   const int slot = (int)(lds / 4096) < 16 ? (int)(lds / 4096) : 15;
   if (per_cu[dev][slot] == 0) {
     int k = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&k, gemv_sb<TY, T, L, STAGE>, 256, 4096 * (slot + 1)) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&k, gemv_sb<TY, T, L, STAGE>, 64 * kSbWaves, 4096 * (slot + 1)) !=
             hipSuccess || k < 1)
       k = 1;
     per_cu[dev][slot] = k;
   }
-  const int want = (b.unit0[b.njobs] + 3) / 4, cap = per_cu[dev][slot] * cu_count();
-  hipLaunchKernelGGL((gemv_sb<TY, T, L, STAGE>), dim3(want < cap ? want : cap), dim3(256), lds, s, b);
+  const int want = (b.unit0[b.njobs] + kSbWaves - 1) / kSbWaves, cap = per_cu[dev][slot] * cu_count();
+  hipLaunchKernelGGL((gemv_sb<TY, T, L, STAGE>), dim3(want < cap ? want : cap), dim3(64 * kSbWaves), lds, s, b);
   return hipGetLastError();
 }
 
@@ -1044,7 +1069,7 @@ hipError_t launch_sb(const Job *jobs, int32_t njobs, hipStream_t s) {
   bool same = T == 1;
   for (int j = 1; j < njobs; j++)
     same = same && jobs[j].xq == jobs[0].xq && jobs[j].xs == jobs[0].xs && jobs[j].n == jobs[0].n;
-  const size_t stage_bytes = sb_stage_bytes(jobs[0].n);
+  const size_t stage_bytes = sb_stage_bytes(jobs[0].type, jobs[0].n);
   const size_t lds = same && stage_bytes <= kSbStageMax ? stage_bytes : 0;
   switch (jobs[0].type) {
   case Q2_K: return launch_type<Q2_K>(b, T, L, lds, s);
