@@ -509,6 +509,44 @@ HQ_DEV void add_chains4(float acc[4][16], float *p0, float *p1, int chain, int l
 }
 
 // wave W's stages of the tile (chain W): its loads, and every stage in order
+// A 64-row tile without groups past the fours: the chains' sums ((a0 + a1) + a2) + a3 made by the four waves at once,
+// each storing a quarter of the tile.  In two halves (sub-tiles 0, 1, then 2, 3) every wave writes the half's 32
+// values of a lane as 8 float4s ([quad][lane], wave w's at p[w / 2] + 8 KB (w % 2)), and after the barrier wave q adds
+// the quads 2 q and 2 q + 1 of the four waves in chain order and stores them.
+HQ_DEV void finish_tile(const float acc[4][16], float *p0, float *p1, int chain, int lane, const Job &J, int row0,
+                        int tok0) {
+  float *const part[4] = {p0, p0 + 2048, p1, p1 + 2048};
+#pragma unroll
+  for (int half = 0; half < 2; half++) {
+    __syncthreads();
+#pragma unroll
+    for (int vq = 0; vq < 8; vq++) {
+      const float *a = acc[2 * half + (vq >> 2)] + 4 * (vq & 3);
+      *(float4 *)(part[chain] + (vq * 64 + lane) * 4) = make_float4(a[0], a[1], a[2], a[3]);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+      const int vq = 2 * chain + k;
+      float4 c[4];
+#pragma unroll
+      for (int w = 0; w < 4; w++) c[w] = *(const float4 *)(part[w] + (vq * 64 + lane) * 4);
+      const float v[4] = {fadd(fadd(fadd(c[0].x, c[1].x), c[2].x), c[3].x), fadd(fadd(fadd(c[0].y, c[1].y), c[2].y), c[3].y),
+                          fadd(fadd(fadd(c[0].z, c[1].z), c[2].z), c[3].z), fadd(fadd(fadd(c[0].w, c[1].w), c[2].w), c[3].w)};
+      // value 4 (vq % 4) + e of sub-tile i = 2 half + vq / 4: row 32 (i / 2) + lane % 32, token 32 (i % 2) + 4 (lane / 32)
+      // + 8 (vq % 4) + e
+      const int i = 2 * half + (vq >> 2);
+      const int row = row0 + 32 * (i >> 1) + (lane & 31);
+      if (row < J.r1) {
+        const int tbase = tok0 + 32 * (i & 1) + 4 * (lane >> 5) + 8 * (vq & 3);
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+          if (tbase + e < J.count) ((float *)(J.out + (tbase + e) * J.os))[row] = v[e];
+      }
+    }
+  }
+}
+
 template <int PACK, bool WC, bool WIDE, int W, int R>
 HQ_DEV void q_chain(const Job &J, int row0, int tok0, int M, int stages, StageQ<R> &b0, StageQ<R> &b1,
                     StageQ<R> &b2, StageQ<R> &b3, float acc[4][16], int lane) {
@@ -555,6 +593,10 @@ __global__ __launch_bounds__(QT, 2) void gemm_relaxed(Job J) {
   }
   stage_ready<0>();  // every load has landed (the tail's too) and every wave is done with the stages
   auto ring = [&](int i) -> StageQ<R> & { return i == 0 ? b0 : i == 1 ? b1 : i == 2 ? b2 : b3; };
+  if (R == 64 && ng == ng4) {  // (measured against the chain-at-a-time add below: 1-3 % of a launch)
+    finish_tile(acc, (float *)&ring((stages + 1) % RING), (float *)&ring((stages + 2) % RING), chain, lane, J, row0, tok0);
+    return;
+  }
   add_chains4<R / 16>(acc, (float *)&ring((stages + 1) % RING), (float *)&ring((stages + 2) % RING), chain, lane);
   if (chain == 3) {
     // the groups past the fours, one at a time, after the four chains' sum (relaxed/int8.ts:40-47)
