@@ -508,14 +508,18 @@ HQ_DEV void add_chains4(float acc[4][16], float *p0, float *p1, int chain, int l
   }
 }
 
-// wave W's stages of the tile (chain W): its loads, and every stage in order
-// A 64-row tile without groups past the fours: the chains' sums ((a0 + a1) + a2) + a3 made by the four waves at once,
-// each storing a quarter of the tile.  In two halves (sub-tiles 0, 1, then 2, 3) every wave writes the half's 32
-// values of a lane as 8 float4s ([quad][lane], wave w's at p[w / 2] + 8 KB (w % 2)), and after the barrier wave q adds
-// the quads 2 q and 2 q + 1 of the four waves in chain order and stores them.
-HQ_DEV void finish_tile(const float acc[4][16], float *p0, float *p1, int chain, int lane, const Job &J, int row0,
-                        int tok0) {
+// A 64-row tile's end: the chains' sums ((a0 + a1) + a2) + a3 made by the four waves at once, each storing a quarter
+// of the tile.  In two halves (sub-tiles 0, 1, then 2, 3) every wave writes the half's 32 values of a lane as 8
+// float4s ([quad][lane], wave w's at p[w / 2] + 8 KB (w % 2)), and after the barrier wave q adds the quads 2 q and
+// 2 q + 1 of the four waves in chain order, then the terms of the groups past the fours one at a time (from the tail
+// stage T: each wave makes them for its own sub-tile of the half, the integer and scale MFMAs of its slice and token
+// half), and stores them.  (Measured against a chain-at-a-time add through four barriers with one wave storing the
+// tile: 1-3 % of a launch.)
+template <int PACK, bool WC, bool WIDE>
+HQ_DEV void finish_tile(const float acc[4][16], float *p0, float *p1, const StageQ<64> &T, int tail, int chain,
+                        int lane, const Job &J, int row0, int tok0) {
   float *const part[4] = {p0, p0 + 2048, p1, p1 + 2048};
+  const int th = chain >> 1, r0 = 8 * (chain & 1);  // this wave's sub-tile of a half (its token half), its values
 #pragma unroll
   for (int half = 0; half < 2; half++) {
     __syncthreads();
@@ -525,20 +529,36 @@ HQ_DEV void finish_tile(const float acc[4][16], float *p0, float *p1, int chain,
       *(float4 *)(part[chain] + (vq * 64 + lane) * 4) = make_float4(a[0], a[1], a[2], a[3]);
     }
     __syncthreads();
+    // the groups past the fours: f(f(C) * f(ws * xs)) of values r0 .. r0 + 7 of sub-tile (slice half, token half th)
+    float tt[QG - 1][8];
+#pragma unroll
+    for (int gi = 0; gi < QG - 1; gi++) {
+      if (gi >= tail) break;
+      const OpsQ o = read_ops_plain<PACK, WC, WIDE, 64>(T, gi, lane);
+      const v16i C = integers(o, half, th, corrections<WC>(o, half));
+      const v32f sc = scales(o, half);
+#pragma unroll
+      for (int m = 0; m < 8; m++) tt[gi][m] = fmul((float)C[r0 + m], sc[16 * th + r0 + m]);
+    }
 #pragma unroll
     for (int k = 0; k < 2; k++) {
       const int vq = 2 * chain + k;
       float4 c[4];
 #pragma unroll
       for (int w = 0; w < 4; w++) c[w] = *(const float4 *)(part[w] + (vq * 64 + lane) * 4);
-      const float v[4] = {fadd(fadd(fadd(c[0].x, c[1].x), c[2].x), c[3].x), fadd(fadd(fadd(c[0].y, c[1].y), c[2].y), c[3].y),
-                          fadd(fadd(fadd(c[0].z, c[1].z), c[2].z), c[3].z), fadd(fadd(fadd(c[0].w, c[1].w), c[2].w), c[3].w)};
-      // value 4 (vq % 4) + e of sub-tile i = 2 half + vq / 4: row 32 (i / 2) + lane % 32, token 32 (i % 2) + 4 (lane / 32)
-      // + 8 (vq % 4) + e
-      const int i = 2 * half + (vq >> 2);
-      const int row = row0 + 32 * (i >> 1) + (lane & 31);
+      float v[4] = {fadd(fadd(fadd(c[0].x, c[1].x), c[2].x), c[3].x), fadd(fadd(fadd(c[0].y, c[1].y), c[2].y), c[3].y),
+                    fadd(fadd(fadd(c[0].z, c[1].z), c[2].z), c[3].z), fadd(fadd(fadd(c[0].w, c[1].w), c[2].w), c[3].w)};
+#pragma unroll
+      for (int gi = 0; gi < QG - 1; gi++) {
+        if (gi >= tail) break;
+#pragma unroll
+        for (int e = 0; e < 4; e++) v[e] = fadd(v[e], tt[gi][4 * k + e]);
+      }
+      // value r = r0 + 4 k + e of sub-tile 2 half + th: row 32 half + lane % 32, token 32 th + 8 (r / 4) + 4 (lane / 32)
+      // + e
+      const int row = row0 + 32 * half + (lane & 31);
       if (row < J.r1) {
-        const int tbase = tok0 + 32 * (i & 1) + 4 * (lane >> 5) + 8 * (vq & 3);
+        const int tbase = tok0 + 32 * th + 2 * r0 + 8 * k + 4 * (lane >> 5);
 #pragma unroll
         for (int e = 0; e < 4; e++)
           if (tbase + e < J.count) ((float *)(J.out + (tbase + e) * J.os))[row] = v[e];
@@ -547,61 +567,27 @@ HQ_DEV void finish_tile(const float acc[4][16], float *p0, float *p1, int chain,
   }
 }
 
-template <int PACK, bool WC, bool WIDE, int W, int R>
-HQ_DEV void q_chain(const Job &J, int row0, int tok0, int M, int stages, StageQ<R> &b0, StageQ<R> &b1,
-                    StageQ<R> &b2, StageQ<R> &b3, float acc[4][16], int lane) {
-  Relaxed<PACK, WC, WIDE, W, R> L(J, row0, tok0, M);
-  // stages 0..2 first (whatever the job has: a stage past its groups loads zeros); stage s's operands come from
-  // buffer s % 4 and its loads of stage s + 3 go into buffer (s - 1) % 4
-  L.load(b0, 0);
-  L.load(b1, 1);
-  L.load(b2, 2);
-  for (int s = 0; s < stages; s += RING) {
-    q_stage<PACK, WC, WIDE, W, R>(L, b0, b3, s, acc, lane);
-    if (s + 1 >= stages) break;
-    q_stage<PACK, WC, WIDE, W, R>(L, b1, b0, s + 1, acc, lane);
-    if (s + 2 >= stages) break;
-    q_stage<PACK, WC, WIDE, W, R>(L, b2, b1, s + 2, acc, lane);
-    if (s + 3 >= stages) break;
-    q_stage<PACK, WC, WIDE, W, R>(L, b3, b2, s + 3, acc, lane);
-  }
-}
-
+// the tile's end in wave `chain` (every load landed, the chains added, the groups past the fours, the stores); in the
+// wave's own copy of the main loop's function, so that its accumulators pass to it where they are
 template <int PACK, bool WC, bool WIDE, int R>
-__global__ __launch_bounds__(QT, 2) void gemm_relaxed(Job J) {
-  __shared__ StageQ<R> b0, b1, b2, b3;
-  const int M = J.count;
+HQ_DEV void q_end(const Job &J, int row0, int tok0, int M, int stages, StageQ<R> &b0, StageQ<R> &b1, StageQ<R> &b2,
+                  StageQ<R> &b3, float acc[4][16], int chain, int lane) {
   const int ng = J.n >> 5, ng4 = ng & ~3;
-  int rb, tb;
-  tile_of(blockIdx.x, gridDim.x, (J.r1 - J.r0 + R - 1) / R, rb, tb);
-  const int row0 = J.r0 + rb * R, tok0 = tb * BT;
-  const int lane = threadIdx.x & 63;
-  const int chain = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-
-  float acc[4][16];
-#pragma unroll
-  for (int i = 0; i < 4; i++)
-#pragma unroll
-    for (int r = 0; r < 16; r++) acc[i][r] = 0.0f;
-
-  const int stages = ng4 / QG;  // whole stages of the four chains; the groups past them (ng % 4) are one more stage
-  switch (chain) {
-  case 0: q_chain<PACK, WC, WIDE, 0, R>(J, row0, tok0, M, stages, b0, b1, b2, b3, acc, lane); break;
-  case 1: q_chain<PACK, WC, WIDE, 1, R>(J, row0, tok0, M, stages, b0, b1, b2, b3, acc, lane); break;
-  case 2: q_chain<PACK, WC, WIDE, 2, R>(J, row0, tok0, M, stages, b0, b1, b2, b3, acc, lane); break;
-  default: q_chain<PACK, WC, WIDE, 3, R>(J, row0, tok0, M, stages, b0, b1, b2, b3, acc, lane); break;
-  }
   stage_ready<0>();  // every load has landed (the tail's too) and every wave is done with the stages
   auto ring = [&](int i) -> StageQ<R> & { return i == 0 ? b0 : i == 1 ? b1 : i == 2 ? b2 : b3; };
-  if (R == 64 && ng == ng4) {  // (measured against the chain-at-a-time add below: 1-3 % of a launch)
-    finish_tile(acc, (float *)&ring((stages + 1) % RING), (float *)&ring((stages + 2) % RING), chain, lane, J, row0, tok0);
+  if constexpr (R == 64) {
+    finish_tile<PACK, WC, WIDE>(acc, (float *)&ring((stages + 1) % RING), (float *)&ring((stages + 2) % RING),
+                                ring(stages % RING), ng - ng4, chain, lane, J, row0, tok0);
     return;
   }
+  // a 32-row tile: the chains added one after the other through LDS, chain 3 storing the tile
   add_chains4<R / 16>(acc, (float *)&ring((stages + 1) % RING), (float *)&ring((stages + 2) % RING), chain, lane);
   if (chain == 3) {
     // the groups past the fours, one at a time, after the four chains' sum (relaxed/int8.ts:40-47)
     const StageQ<R> &T = ring(stages % RING);
-    for (int gi = 0; gi < ng - ng4; gi++) {
+#pragma unroll
+    for (int gi = 0; gi < QG - 1; gi++) {
+      if (gi >= ng - ng4) break;
       const OpsQ o = read_ops_plain<PACK, WC, WIDE, R>(T, gi, lane);
 #pragma unroll
       for (int sp = 0; sp < R / 32; sp++) {
@@ -625,6 +611,53 @@ __global__ __launch_bounds__(QT, 2) void gemm_relaxed(Job J) {
           }
       }
     }
+  }
+}
+
+// wave W's stages of the tile (chain W): its loads, every stage in order, then the tile's end
+template <int PACK, bool WC, bool WIDE, int W, int R>
+HQ_DEV void q_chain(const Job &J, int row0, int tok0, int M, int stages, StageQ<R> &b0, StageQ<R> &b1,
+                    StageQ<R> &b2, StageQ<R> &b3, float acc[4][16], int lane) {
+  Relaxed<PACK, WC, WIDE, W, R> L(J, row0, tok0, M);
+  // stages 0..2 first (whatever the job has: a stage past its groups loads zeros); stage s's operands come from
+  // buffer s % 4 and its loads of stage s + 3 go into buffer (s - 1) % 4
+  L.load(b0, 0);
+  L.load(b1, 1);
+  L.load(b2, 2);
+  for (int s = 0; s < stages; s += RING) {
+    q_stage<PACK, WC, WIDE, W, R>(L, b0, b3, s, acc, lane);
+    if (s + 1 >= stages) break;
+    q_stage<PACK, WC, WIDE, W, R>(L, b1, b0, s + 1, acc, lane);
+    if (s + 2 >= stages) break;
+    q_stage<PACK, WC, WIDE, W, R>(L, b2, b1, s + 2, acc, lane);
+    if (s + 3 >= stages) break;
+    q_stage<PACK, WC, WIDE, W, R>(L, b3, b2, s + 3, acc, lane);
+  }
+  q_end<PACK, WC, WIDE, R>(J, row0, tok0, M, stages, b0, b1, b2, b3, acc, W, lane);
+}
+
+template <int PACK, bool WC, bool WIDE, int R>
+__global__ __launch_bounds__(QT, 2) void gemm_relaxed(Job J) {
+  __shared__ StageQ<R> b0, b1, b2, b3;
+  const int M = J.count;
+  int rb, tb;
+  tile_of(blockIdx.x, gridDim.x, (J.r1 - J.r0 + R - 1) / R, rb, tb);
+  const int row0 = J.r0 + rb * R, tok0 = tb * BT;
+  const int lane = threadIdx.x & 63;
+  const int chain = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+
+  float acc[4][16];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[i][r] = 0.0f;
+
+  const int stages = (J.n >> 5) / QG;  // whole stages of the four chains; the groups past them are one more stage
+  switch (chain) {
+  case 0: q_chain<PACK, WC, WIDE, 0, R>(J, row0, tok0, M, stages, b0, b1, b2, b3, acc, lane); break;
+  case 1: q_chain<PACK, WC, WIDE, 1, R>(J, row0, tok0, M, stages, b0, b1, b2, b3, acc, lane); break;
+  case 2: q_chain<PACK, WC, WIDE, 2, R>(J, row0, tok0, M, stages, b0, b1, b2, b3, acc, lane); break;
+  default: q_chain<PACK, WC, WIDE, 3, R>(J, row0, tok0, M, stages, b0, b1, b2, b3, acc, lane); break;
   }
 }
 
