@@ -283,12 +283,14 @@ template <int TY> constexpr int lds_table_bytes() {
 
 // STAGE (one token, and every job of the launch the same activations): the block copies the token's n bytes and
 // its n/2 bytes of scales and sums into LDS first, so a step's activations are LDS reads, which the next step's block
-// loads in flight do not hold up (a vector memory load waits for every one issued before it).  kSbWaves waves a
+// loads in flight do not hold up (a vector memory load waits for every one issued before it).  sb_waves<T>() waves a
 // block: the fewer the blocks a CU, the fewer copies of the tables and the activations its LDS is filled with
-// (16 against 4: 3-10 % faster for every type)
-constexpr int kSbWaves = 16;
+// (one token: 16 against 4, 3-10 % faster for every type); 2..4 tokens keep 4 (their registers: 16 waves a block
+// leave a wave 128)
+template <int T> constexpr int sb_waves() { return T == 1 ? 16 : 4; }
 template <int TY, int T, int L, bool STAGE>
-__global__ __launch_bounds__(64 * kSbWaves) void gemv_sb(SbBatch batch) {
+__global__ __launch_bounds__(64 * sb_waves<T>()) void gemv_sb(SbBatch batch) {
+  constexpr int kSbWaves = sb_waves<T>();
   constexpr int R = 64 / L;  // rows a wave
   constexpr int BYTES = sb_block_bytes(TY);
   constexpr int GRID = grid_bytes<TY>();
@@ -443,7 +445,7 @@ __global__ __launch_bounds__(64 * kSbWaves) void gemv_sb(SbBatch batch) {
   }
 }
 
-// a launch's blocks: as many as stay resident together (at most the units over kSbWaves); lds: the staged
+// a launch's blocks: as many as stay resident together (at most the units over the waves a block); lds: the staged
 // activations' bytes (0: none)
 template <int TY, int T, int L, bool STAGE>
 hipError_t launch_tt(const SbBatch &b, size_t lds, hipStream_t s) {
@@ -453,13 +455,14 @@ hipError_t launch_tt(const SbBatch &b, size_t lds, hipStream_t s) {
   const int slot = (int)(lds / 4096) < 16 ? (int)(lds / 4096) : 15;
   if (per_cu[dev][slot] == 0) {
     int k = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&k, gemv_sb<TY, T, L, STAGE>, 64 * kSbWaves, 4096 * (slot + 1)) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&k, gemv_sb<TY, T, L, STAGE>, 64 * sb_waves<T>(), 4096 * (slot + 1)) !=
             hipSuccess || k < 1)
       k = 1;
     per_cu[dev][slot] = k;
   }
-  const int want = (b.unit0[b.njobs] + kSbWaves - 1) / kSbWaves, cap = per_cu[dev][slot] * cu_count();
-  hipLaunchKernelGGL((gemv_sb<TY, T, L, STAGE>), dim3(want < cap ? want : cap), dim3(64 * kSbWaves), lds, s, b);
+  constexpr int W = sb_waves<T>();
+  const int want = (b.unit0[b.njobs] + W - 1) / W, cap = per_cu[dev][slot] * cu_count();
+  hipLaunchKernelGGL((gemv_sb<TY, T, L, STAGE>), dim3(want < cap ? want : cap), dim3(64 * W), lds, s, b);
   return hipGetLastError();
 }
 
