@@ -3,11 +3,13 @@
     python pyodide-llm_amd/build.py [--jobs N]
 
 Every source is compiled again on every call.  Flags: -ffp-contract=off (every float operation written in the
-kernels is one IEEE operation, as the reference's are), denormals kept, and packed FP32 instructions off.
+kernels is one IEEE operation, as the reference's are), denormals kept, and packed FP32 instructions off.  The build
+fails if a kernel spills registers to scratch memory (the compiler's resource-usage remarks say so).
 """
 import argparse
 import concurrent.futures
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -32,15 +34,45 @@ FLAGS = [
 ]
 
 
+REMARK = re.compile(r"remark: +(Function Name|ScratchSize \[bytes/lane\]|VGPRs Spill|SGPRs Spill): (\S+)")
+
+
+def _spills(stderr):
+    """the kernels the resource-usage remarks report spilling or using scratch memory"""
+    bad, name = [], None
+    for m in REMARK.finditer(stderr):
+        if m.group(1) == "Function Name":
+            name = m.group(2)
+        elif int(m.group(2)) > 0 and (not bad or bad[-1] != name):
+            bad.append(name)
+    return bad
+
+
 def _compile(src):
     obj = os.path.join(OBJ, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC, *FLAGS, *EXTRA.get(src, []), "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [HIPCC, *FLAGS, *EXTRA.get(src, []), "-Rpass-analysis=kernel-resource-usage", "-x", "hip", "-c",
+           os.path.join(CSRC, src), "-o", obj]
     run = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass does not know the packed-fp32 feature and says so: harmless
     noise = "is not a recognized feature for this target"
-    err = "\n".join(line for line in run.stderr.splitlines() if noise not in line)
+    lines = run.stderr.splitlines()
+    # the remarks (and the source lines and carets they quote) are read, not shown
+    keep, skip = [], 0
+    for line in lines:
+        if "[-Rpass-analysis=kernel-resource-usage]" in line:
+            skip = 2 if "Function Name" in line else 0
+            continue
+        if skip:
+            skip -= 1
+            continue
+        if noise not in line:
+            keep.append(line)
+    err = "\n".join(keep)
     if run.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{err}")
+    bad = _spills(run.stderr)
+    if bad:
+        raise RuntimeError(f"{src}: kernels spill registers to scratch memory: {', '.join(bad)}")
     if err.strip():
         print(err, file=sys.stderr)
     return obj
