@@ -33,14 +33,16 @@
 //
 // Tiles.  int8 / int6: a block (4 waves, two blocks a CU) computes a 64-row x 64-token tile; wave w is chain w, four
 // 32 x 32 sub-tiles (two row slices x two token halves: the weights' operand read once for two MFMAs, the tokens' for
-// two slices).  Ternary: a block of 16 waves computes a 128-row x 64-token tile; wave w takes rows 32 (w / 4) .. + 31
+// two slices).  Launches whose 64-row tiles would leave block slots idle take 32-row tiles (one slice, ~150 VGPRs,
+// a ring of 3 stage buffers: three blocks a CU).  Ternary: a block of 16 waves computes a 128-row x 64-token tile; wave w takes rows 32 (w / 4) .. + 31
 // and chain w % 4, both 32-token halves.
 //
 // Pipeline (int8 / int6).  A wave issues each sub-tile's MFMAs one sub-tile ahead of its epilogue, so the matrix core
 // works on the next sub-tile while the VALU folds this one.  The operands go from HBM / L2 straight into LDS with
-// buffer-to-LDS loads into a ring of 4 stage buffers (a stage: 4 groups of int8 / int6, 2 groups of 128 of ternary):
-// at the barrier for stage s, which says that stage s's loads have landed and that every wave has read stage s - 1's
-// operands, a wave reads its operands of stage s and issues its loads of stage s + 3 into stage s - 1's buffer.  A
+// buffer-to-LDS loads into a ring of 4 stage buffers (3 for 32-row tiles; a stage: 4 groups of int8 / int6, 2 groups
+// of 128 of ternary): at the barrier for stage s, which says that stage s's loads have landed and that every wave has
+// read stage s - 1's operands, a wave reads its operands of stage s and issues its loads of stage s + 3 (s + 2) into
+// stage s - 1's buffer.  A
 // wave issues the same loads every stage, so one s_waitcnt vmcnt count says "my loads of stage s have landed".  A load
 // past the tile's last row or token, or past the last group, reads zeros (buffer bounds; such results are never
 // stored).  The 16-byte chunks of a row are stored XOR-swizzled so that the MFMA operand reads (32 rows or tokens, one
@@ -62,6 +64,10 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 constexpr int BR = 128, BT = 64;  // block tile: rows x tokens
 constexpr int RING = 4;           // stage buffers
 constexpr int AHEAD = RING - 1;   // stages loaded beyond the one computed
+// the int8 / int6 tiles' rings: 4 buffers for 64-row tiles (76 KB, two blocks a CU), 3 for 32-row tiles (45 KB,
+// three blocks a CU: more waves a SIMD against one stage less in flight, measured 2-4 % faster than 4 buffers and two
+// blocks)
+template <int R> constexpr int ring_of() { return R == 32 ? 3 : 4; }
 
 HQ_DEV v16i zero16i() {
   v16i z;
@@ -300,11 +306,11 @@ struct Relaxed {
   }
 };
 
-// stage s's loads have landed everywhere: this wave's own, with those of the two stages after it still in flight,
-// then the block's barrier
+// stage s's loads have landed everywhere: this wave's own, with those of the stages after it still in flight (two
+// with a ring of 4 buffers, one with 3), then the block's barrier
 template <int PACK, bool WC, bool WIDE, int W, int R>
 HQ_DEV void q_ready() {
-  stage_ready<2 * Relaxed<PACK, WC, WIDE, W, R>::count>();
+  stage_ready<(ring_of<R>() - 2) * Relaxed<PACK, WC, WIDE, W, R>::count>();
 }
 
 // a wave's operands of one group gi of a stage: the activations of both token halves, the weights of both row slices
@@ -466,7 +472,7 @@ HQ_DEV void q_stage(Relaxed<PACK, WC, WIDE, W, R> &L, const StageQ<R> &cur, Stag
                     int lane) {
   q_ready<PACK, WC, WIDE, W, R>();
   const OpsQ op = read_ops<PACK, WC, WIDE, R>(cur, W, lane);
-  L.load(dma, s + AHEAD);
+  L.load(dma, s + ring_of<R>() - 1);
   const v16i cin0 = corrections<WC>(op, 0);
   const v32f S0 = scales(op, 0);
   const v16i C0 = integers(op, 0, 0, cin0);
@@ -575,6 +581,7 @@ HQ_DEV void q_end(const Job &J, int row0, int tok0, int M, int stages, StageQ<R>
   const int ng = J.n >> 5, ng4 = ng & ~3;
   stage_ready<0>();  // every load has landed (the tail's too) and every wave is done with the stages
   auto ring = [&](int i) -> StageQ<R> & { return i == 0 ? b0 : i == 1 ? b1 : i == 2 ? b2 : b3; };
+  constexpr int RING = ring_of<R>();
   if constexpr (R == 64) {
     finish_tile<PACK, WC, WIDE>(acc, (float *)&ring((stages + 1) % RING), (float *)&ring((stages + 2) % RING),
                                 ring(stages % RING), ng - ng4, chain, lane, J, row0, tok0);
@@ -619,10 +626,21 @@ template <int PACK, bool WC, bool WIDE, int W, int R>
 HQ_DEV void q_chain(const Job &J, int row0, int tok0, int M, int stages, StageQ<R> &b0, StageQ<R> &b1,
                     StageQ<R> &b2, StageQ<R> &b3, float acc[4][16], int lane) {
   Relaxed<PACK, WC, WIDE, W, R> L(J, row0, tok0, M);
-  // stages 0..2 first (whatever the job has: a stage past its groups loads zeros); stage s's operands come from
-  // buffer s % 4 and its loads of stage s + 3 go into buffer (s - 1) % 4
+  // stages 0..2 first (0..1 with 3 buffers; whatever the job has: a stage past its groups loads zeros); stage s's
+  // operands come from buffer s % 4 (s % 3) and its loads of stage s + 3 (s + 2) go into buffer s - 1's
   L.load(b0, 0);
   L.load(b1, 1);
+  if constexpr (ring_of<R>() == 3) {
+    for (int s = 0; s < stages; s += 3) {
+      q_stage<PACK, WC, WIDE, W, R>(L, b0, b2, s, acc, lane);
+      if (s + 1 >= stages) break;
+      q_stage<PACK, WC, WIDE, W, R>(L, b1, b0, s + 1, acc, lane);
+      if (s + 2 >= stages) break;
+      q_stage<PACK, WC, WIDE, W, R>(L, b2, b1, s + 2, acc, lane);
+    }
+    q_end<PACK, WC, WIDE, R>(J, row0, tok0, M, stages, b0, b1, b2, b2, acc, W, lane);
+    return;
+  }
   L.load(b2, 2);
   for (int s = 0; s < stages; s += RING) {
     q_stage<PACK, WC, WIDE, W, R>(L, b0, b3, s, acc, lane);
@@ -637,8 +655,10 @@ HQ_DEV void q_chain(const Job &J, int row0, int tok0, int M, int stages, StageQ<
 }
 
 template <int PACK, bool WC, bool WIDE, int R>
-__global__ __launch_bounds__(QT, 2) void gemm_relaxed(Job J) {
-  __shared__ StageQ<R> b0, b1, b2, b3;
+__global__ __launch_bounds__(QT, ring_of<R>() == 3 ? 3 : 2) void gemm_relaxed(Job J) {
+  __shared__ StageQ<R> b0, b1, b2;
+  __shared__ StageQ<R> b3x[1];  // not allocated for a ring of 3 (never used then)
+  StageQ<R> &b3 = ring_of<R>() == 3 ? b2 : b3x[0];
   const int M = J.count;
   int rb, tb;
   tile_of(blockIdx.x, gridDim.x, (J.r1 - J.r0 + R - 1) / R, rb, tb);
@@ -922,15 +942,17 @@ void launch_relaxed(const Job &job, int token_tiles, hipStream_t s) {
   else hipLaunchKernelGGL((gemm_relaxed<PACK, false, false, R>), grid, dim3(QT), 0, s, job);
 }
 
-// 32-row tiles where they take fewer rounds of the CUs' block slots (two a CU) than 64-row tiles, counting a round of
-// 32-row tiles as kTile32 of one of 64-row tiles (measured over launches of many rounds: 383 against 474 TOPS, so a
-// 32-row tile costs 0.62 of a 64-row one; the 8B prefill's shapes all keep 64-row tiles)
-constexpr double kTile32 = 0.62;
+// 32-row tiles (three blocks a CU) where they cost less than 64-row tiles (two a CU): a launch costs its tiles over
+// the CUs' block slots in rounds (at least one, however few its tiles), a round of 32-row tiles kTile32 of one of
+// 64-row tiles (measured over launches of many rounds: 426 against 508 TOPS at 14336 x 2 x 4096, M = 2048, so a
+// round of 3 x 32-row tiles a CU costs 0.89 of one of 2 x 64-row tiles).  Against nine prompt shapes measured both
+// ways (the 8B layer at M = 2048, Llama-3.2-1B at 512, the 27B projections at 256) it picks the faster height each
+// time: 64 for the 8B shapes, the 1B gate/up and the 27B gate/up, 32 for the other 1B shapes and the 27B down.
+constexpr double kTile32 = 0.89;
 bool short_tiles(int rows, int token_tiles) {
-  const int64_t slots = 2 * (int64_t)cu_count();
-  const int64_t t64 = (int64_t)((rows + 63) / 64) * token_tiles, t32 = (int64_t)((rows + 31) / 32) * token_tiles;
-  const int64_t r64 = (t64 + slots - 1) / slots, r32 = (t32 + slots - 1) / slots;
-  return kTile32 * (double)r32 < (double)r64;
+  const double cus = (double)cu_count();
+  const double t64 = (double)((rows + 63) / 64) * token_tiles, t32 = (double)((rows + 31) / 32) * token_tiles;
+  return kTile32 * fmax(1.0, t32 / (3 * cus)) < fmax(1.0, t64 / (2 * cus));
 }
 
 }  // namespace

@@ -376,10 +376,10 @@ def test_q6r_many_tokens(pkg, arena, oracle, count, ng):
 
 def tile_rows(rows, token_tiles, cus):
     """the rows of the prompt kernel's tile for a launch (gemm.hip's short_tiles: 32-row tiles where their rounds of
-    the 2 x CU block slots, each 0.62 of a 64-row round, are fewer)"""
-    slots = 2 * cus
+    the 3 x CU block slots, each 0.89 of a round of 64-row tiles over 2 x CU, at least one round either way, cost
+    less)"""
     t64, t32 = -(-rows // 64) * token_tiles, -(-rows // 32) * token_tiles
-    return 32 if 0.62 * -(-t32 // slots) < -(-t64 // slots) else 64
+    return 32 if 0.89 * max(1.0, t32 / (3 * cus)) < max(1.0, t64 / (2 * cus)) else 64
 
 
 @pytest.mark.parametrize("packing", ["int8", "int6"])
