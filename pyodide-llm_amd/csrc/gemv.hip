@@ -102,7 +102,10 @@ HQ_DEV void load_acts(const char *xq, int g, uint32_t x[8]) {
 // Memory-level parallelism: a lane's steps are taken U at a time (a chunk: its weights and scales, and from global
 // memory its activations, loaded into registers together), and the next chunk's loads are issued before the current
 // chunk is computed, so a wave keeps two chunks of loads in flight.  The compiler cannot unroll the step loop itself
-// (the DPP moves are convergent), so the two chunk buffers alternate by hand.
+// (the DPP moves are convergent), so the two chunk buffers alternate by hand.  With 2..4 tokens staged in LDS (LATE)
+// a chunk holds only the weights of 2 steps and the fold reads each step's activations from LDS as it goes, so
+// the registers that 4 tokens' activations would take hold more weights in flight (one step a chunk with the
+// activations in it: 8 % slower at M = 4; 4 or 8 steps a chunk: slower still).
 template <int T, int SRC>
 struct ActSource {
   const char *xq[T];
@@ -120,10 +123,12 @@ struct ActSource {
 
 template <int PACK, int T, bool WC, int SRC>
 struct RelaxedChunk {
-  static constexpr int U = T == 1 ? 4 : (T == 2 ? 2 : 1);
+  static constexpr bool LATE = T > 1 && SRC == STAGED;
+  static constexpr int U = T == 1 ? 4 : (LATE || T == 2 ? 2 : 1);
+  static constexpr int UX = LATE ? 1 : U;  // steps of activations a chunk holds (none read when LATE)
   uint32_t w[U][8];
-  uint32_t x[U][T][8];
-  float ws[U], xs[U][T];
+  uint32_t x[UX][T][8];
+  float ws[U], xs[UX][T];
   int32_t wc[U];
 
   // steps it0 .. it0 + U - 1 of this lane (its group 16 it + lane of each; a lane past the row's fours reads group
@@ -140,6 +145,7 @@ struct RelaxedChunk {
   }
   // ... and the activations of the same groups (from global memory or the block's LDS)
   HQ_DEV void load_x(const ActSource<T, SRC> &A, int it0, int lane, int ng4) {
+    if (LATE) return;
 #pragma unroll
     for (int u = 0; u < U; u++) {
       const int g = (it0 + u) * 16 + lane;
@@ -161,21 +167,32 @@ struct RelaxedChunk {
       load_group<PACK>(wrow, gl, w[u]);
       ws[u] = srow[gl];
       if (WC) wc[u] = crow[gl];
+      if (!LATE) {
 #pragma unroll
-      for (int t = 0; t < T; t++) {
-        A.get(t, gl, x[u][t]);
-        xs[u][t] = A.scale(t, gl);
+        for (int t = 0; t < T; t++) {
+          A.get(t, gl, x[u][t]);
+          xs[u][t] = A.scale(t, gl);
+        }
       }
     }
   }
 
   // the chunk's terms, folded into the lanes' sums: lane k takes groups 16 it + k, + 4, + 8, + 12 in order
   // (relaxed/int8.ts:26-39)
-  HQ_DEV void fold(float acc[T], int it0, int lane, int ng4) const {
+  HQ_DEV void fold(float acc[T], int it0, int lane, int ng4, const ActSource<T, SRC> &A) const {
 #pragma unroll
     for (int u = 0; u < U; u++) {
       const int g = (it0 + u) * 16 + lane;
       const bool valid = g < ng4;
+      uint32_t xl[T][8];  // LATE: the step's activations, read here
+      float xsl[T];
+      if (LATE) {
+#pragma unroll
+        for (int t = 0; t < T; t++) {
+          A.get(t, valid ? g : 0, xl[t]);
+          xsl[t] = A.scale(t, valid ? g : 0);
+        }
+      }
       int32_t wsum = 0;
       if (!WC) {
 #pragma unroll
@@ -185,8 +202,8 @@ struct RelaxedChunk {
       for (int t = 0; t < T; t++) {
         int32_t d = WC ? wc[u] : -64 * wsum;
 #pragma unroll
-        for (int i = 0; i < 8; i++) d = sdot4((int32_t)w[u][i], (int32_t)x[u][t][i], d);
-        const float p = fmul((float)d, fmul(ws[u], xs[u][t]));
+        for (int i = 0; i < 8; i++) d = sdot4((int32_t)w[u][i], (int32_t)(LATE ? xl[t][i] : x[LATE ? 0 : u][t][i]), d);
+        const float p = fmul((float)d, fmul(ws[u], LATE ? xsl[t] : xs[LATE ? 0 : u][t]));
         const float q = valid ? p : 0.0f;  // +0 leaves a lane as it is: a lane is never -0
         float a = fadd(acc[t], q);
         a = fadd(a, from_lane_plus<4>(q));
@@ -237,12 +254,32 @@ HQ_DEV void relaxed_tile(const GemvBatch &batch, int tile, char *lds) {
   } else if (steps > 0) {
     a.load(wrow, srow, crow, A, 0, lane, ng4);
   }
-  for (int it = 0; it < steps; it += 2 * U) {
-    if (it + U < steps) b.load(wrow, srow, crow, A, it + U, lane, ng4);
-    a.fold(acc, it, lane, ng4);
-    if (it + U < steps) {
-      if (it + 2 * U < steps) a.load(wrow, srow, crow, A, it + 2 * U, lane, ng4);
-      b.fold(acc, it + U, lane, ng4);
+  if (T == 1) {
+    for (int it = 0; it < steps; it += 2 * U) {
+      if (it + U < steps) b.load(wrow, srow, crow, A, it + U, lane, ng4);
+      a.fold(acc, it, lane, ng4, A);
+      if (it + U < steps) {
+        if (it + 2 * U < steps) a.load(wrow, srow, crow, A, it + 2 * U, lane, ng4);
+        b.fold(acc, it + U, lane, ng4, A);
+      }
+    }
+  } else {
+    // each fold in the block of the loads issued before it, so that its wait counts only the chunk it folds: where
+    // paths with and without those loads met, the fold also waited for the next chunk's first loads (one chunk in
+    // flight instead of two; a chunk of M = 1 is 24 loads, so only one of them, and it keeps the loop above)
+    for (int it = 0; steps > 0; it += 2 * U) {
+      if (it + U >= steps) {
+        a.fold(acc, it, lane, ng4, A);
+        break;
+      }
+      b.load(wrow, srow, crow, A, it + U, lane, ng4);
+      a.fold(acc, it, lane, ng4, A);
+      if (it + 2 * U >= steps) {
+        b.fold(acc, it + U, lane, ng4, A);
+        break;
+      }
+      a.load(wrow, srow, crow, A, it + 2 * U, lane, ng4);
+      b.fold(acc, it + U, lane, ng4, A);
     }
   }
   // lane 0: ((l0 + l1) + l2) + l3 (math.ts:7-9), then the groups past the fours one at a time (int8.ts:40-47)
