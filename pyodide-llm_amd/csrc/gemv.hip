@@ -389,21 +389,32 @@ __global__ __launch_bounds__(256) void gemv_plain(GemvBatch batch) {
 #pragma unroll
   for (int t = 0; t < T; t++) acc[t] = 0.0f;
   const int steps = (ng + 15) >> 4;
-  for (int it = 0; it < steps; ++it) {
-    const int g = it * 16 + lane;
-    const bool valid = g < ng;
-    const int gl = valid ? g : 0;
-    uint32_t w[8], wp[8];
-    load_group<PACK>(wrow, gl, w);
-    parts_of(w, wp);
-    const float ws = srow[gl];
+  // a step's loads (group 16 it + lane of the row, and of every token's activations; past the row's groups, group 0
+  // again), issued a step ahead of its use on every path, so that using a step waits for its own loads alone
+  struct Step {
+    uint32_t w[8], x[T][8];
+    float ws, xs[T];
+  };
+  const auto load = [&](Step &p, int it) {
+    const int g = it * 16 + lane, gl = g < ng ? g : 0;
+    load_group<PACK>(wrow, gl, p.w);
+    p.ws = srow[gl];
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+      load_acts(J.xq + t * J.frame, gl, p.x[t]);
+      p.xs[t] = ((const float *)(J.xs + t * J.sframe))[gl];
+    }
+  };
+  const auto step = [&](const Step &p, int it) {
+    const bool valid = it * 16 + lane < ng;
+    uint32_t wp[8];
+    parts_of(p.w, wp);
     const int buf = it & 1;
 #pragma unroll
     for (int t = 0; t < T; t++) {
-      uint32_t x[8], xp[8];
-      load_acts(J.xq + t * J.frame, gl, x);
-      parts_of(x, xp);
-      const float s = fmul(ws, ((const float *)(J.xs + t * J.sframe))[gl]);
+      uint32_t xp[8];
+      parts_of(p.x[t], xp);
+      const float s = fmul(p.ws, p.xs[t]);
 #pragma unroll
       for (int k = 0; k < 4; k++) {
         const int32_t d = sdot4((int32_t)wp[2 * k + 1], (int32_t)xp[2 * k + 1], sdot4((int32_t)wp[2 * k], (int32_t)xp[2 * k], 0));
@@ -411,6 +422,15 @@ __global__ __launch_bounds__(256) void gemv_plain(GemvBatch batch) {
       }
     }
     fold_step<T>(f, buf, slot, lane, acc);
+  };
+  Step a, b;
+  if (steps > 0) load(a, 0);
+  for (int it = 0; it < steps; it += 2) {
+    load(b, it + 1);
+    step(a, it);
+    if (it + 1 >= steps) break;  // uniform
+    load(a, it + 2);
+    step(b, it + 1);
   }
   // lanes 0..3 hold the four parts' sums: ((l0 + l1) + l2) + l3 in lane 0
   float sum[T];
