@@ -42,6 +42,10 @@ template <int S>
 HQ_DEV float from_lane_plus(float v) {
   return __int_as_float(from_lane_plus<S>(__float_as_int(v)));
 }
+// lanes 0..15 (32..47) get lanes 16..31's (48..63's) values: v_permlane16_swap's second result, of v with itself
+HQ_DEV float upper_row(float v) {
+  return __uint_as_float(__builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false)[1]);
+}
 // lane l gets lane (l ^ 1)'s value (quad_perm [1, 0, 3, 2])
 HQ_DEV int32_t swap_pair(int32_t v) { return dpp<0xB1>(v); }
 // every lane of a quad gets that quad's lane Q (quad_perm [Q, Q, Q, Q])

@@ -6,15 +6,17 @@
 //   matmul_b1r / matmul_b1    (relaxed/signs.ts:123-125, kernel/matmul.ts:222-224: the ternary kernels on binary
 //                              weights, kernels/binary.ts; ternary's numbers for the same signs)
 //
-// Layout: a row is 16 lanes (ternary: 8, 16 or 32 by the row's length), a wave 4 rows; a block is 2 waves (8 rows)
-// for the relaxed kinds, 4 waves for the others.  Lane l of a row of L lanes takes the groups L i + l (i = 0, 1,
-// ...): a group's bytes (32 int8, 24 int6 or 32 ternary) are one lane's, so its integer sum is exact in that lane
-// (v_dot4_i32_i8) and the row's 16 lanes read 512 (384) contiguous bytes a step.
+// Layout: a row is 16 lanes (relaxed: 16 or 32 by the launch's shape; ternary: 8, 16 or 32 by the row's length), a
+// wave 4 rows (2 of 32 lanes); a block is 2 waves (8 rows, or 4 of 32 lanes) for the relaxed kinds, 4 waves for the
+// others.  Lane l of a row of L lanes takes the groups L i + l (i = 0, 1, ...): a group's bytes (32 int8, 24 int6 or
+// 32 ternary) are one lane's, so its integer sum is exact in that lane (v_dot4_i32_i8) and a row's lanes read
+// 32 L (24 L) contiguous bytes a step.
 //
 // The float32 order is the reference's, so every output is its number to the bit:
 //   relaxed int8 / int6: lane k (k = 0..3) of the reference's accumulator adds the groups 4 j + k in order.  Those
-//     are lanes k, k + 4, k + 8, k + 12 of a step here: lane k adds them in that order with DPP moves (no LDS),
-//     then lane 0 adds the four lanes ((l0 + l1) + l2) + l3 and the groups past the last four one at a time.
+//     are lanes k, k + 4, k + 8, k + 12 of a step here (of a 32-lane row's step, then k + 16, ..., k + 28): lane k
+//     adds them in that order with DPP moves (no LDS; the upper 16 lanes brought down by v_permlane16_swap), then
+//     lane 0 adds the four lanes ((l0 + l1) + l2) + l3 and the groups past the last four one at a time.
 //   plain int8 / int6 and ternary: the reference's lane k adds part k of EVERY group in order (matmul_q8: the
 //     products 2k, 2k+1, 2k+8, 2k+9 of each half; ternary: the k-th 32 of each 128).  A step's 16 groups x 4 parts
 //     are written to LDS and lane k of the row adds its part of the 16 groups in order.
@@ -59,10 +61,20 @@ HQ_DEV void fill_acts(const Job &J, char *lq, float *ls) {
 }
 
 constexpr int kRowsPerBlock = 16;
-// the relaxed kinds' blocks: kRelaxedRows rows of 16 lanes (fewer rows a block: more blocks, a finer balance of the
-// last ones over the CUs; 8 measured faster than 16 at the 8B decode)
-constexpr int kRelaxedRows = 8;
-HQ_HOST_DEV constexpr int rows_per_block(Kind kind) { return kind == Q8R || kind == Q6R ? kRelaxedRows : kRowsPerBlock; }
+// the relaxed kinds' blocks: 128 threads, 8 rows of 16 lanes or 4 of 32 (fewer rows a block: more blocks, a finer
+// balance of the last ones over the CUs; 8 rows of 16 measured faster than 16 rows at the 8B decode)
+constexpr int kRelaxedThreads = 128;
+// Lanes a relaxed row: 32 lanes give a launch twice the waves, each lane half the steps.  Measured phase by phase
+// streaming from HBM (configs 1-4's decode shapes, int8 and int6, 16 against 32 lanes): one int8 token, 32 lanes are
+// faster where a row is 4096 or 8192 bytes (8B q/k/v 7.7 -> 7.1 us, o 6.2 -> 5.8, gate+up 25.3 -> 23.5, lm-head 97 ->
+// 94; 1B down 6.8 -> 6.3) and slower at 1024, 2048, 5120 and 14336 (LFM2's lm-head 18.1 -> 25.7, 8B down 14.0 ->
+// 14.6); int6 shows no consistent gain (16 lanes); 2..4 tokens gain on rows past 8192 (four tokens' 8B down 19.8 ->
+// 18.8 us, int6 30.4 -> 20.7) and lose below (gate+up 29.6 -> 31.9).
+constexpr int kRelaxedLongRow = 8192;
+HQ_HOST_DEV constexpr int relaxed_lanes(Kind kind, int T, int n) {
+  if (T > 1) return n > kRelaxedLongRow ? 32 : 16;
+  return kind == Q8R && n % 4096 == 0 && n <= kRelaxedLongRow ? 32 : 16;
+}
 
 HQ_DEV int job_of(const GemvBatch &b, int blk) {
   int j = 0;
@@ -121,7 +133,7 @@ struct ActSource {
   HQ_DEV float scale(int t, int g) const { return SRC == GLOBAL ? ((const float *)xs[t])[g] : ls[t * ng + g]; }
 };
 
-template <int PACK, int T, bool WC, int SRC>
+template <int PACK, int T, bool WC, int SRC, int RL>
 struct RelaxedChunk {
   static constexpr bool LATE = T > 1 && SRC == STAGED;
   static constexpr int U = T == 1 ? 4 : (LATE || T == 2 ? 2 : 1);
@@ -131,12 +143,12 @@ struct RelaxedChunk {
   float ws[U], xs[UX][T];
   int32_t wc[U];
 
-  // steps it0 .. it0 + U - 1 of this lane (its group 16 it + lane of each; a lane past the row's fours reads group
+  // steps it0 .. it0 + U - 1 of this lane (its group RL it + lane of each; a lane past the row's fours reads group
   // 0 again, whose term it drops): the weights, their scales and corrections
   HQ_DEV void load_w(const char *wrow, const float *srow, const int32_t *crow, int it0, int lane, int ng4) {
 #pragma unroll
     for (int u = 0; u < U; u++) {
-      const int g = (it0 + u) * 16 + lane;
+      const int g = (it0 + u) * RL + lane;
       const int gl = g < ng4 ? g : 0;
       load_group<PACK>(wrow, gl, w[u]);
       ws[u] = srow[gl];
@@ -148,7 +160,7 @@ struct RelaxedChunk {
     if (LATE) return;
 #pragma unroll
     for (int u = 0; u < U; u++) {
-      const int g = (it0 + u) * 16 + lane;
+      const int g = (it0 + u) * RL + lane;
       const int gl = g < ng4 ? g : 0;
 #pragma unroll
       for (int t = 0; t < T; t++) {
@@ -162,7 +174,7 @@ struct RelaxedChunk {
                    int lane, int ng4) {
 #pragma unroll
     for (int u = 0; u < U; u++) {
-      const int g = (it0 + u) * 16 + lane;
+      const int g = (it0 + u) * RL + lane;
       const int gl = g < ng4 ? g : 0;
       load_group<PACK>(wrow, gl, w[u]);
       ws[u] = srow[gl];
@@ -177,12 +189,12 @@ struct RelaxedChunk {
     }
   }
 
-  // the chunk's terms, folded into the lanes' sums: lane k takes groups 16 it + k, + 4, + 8, + 12 in order
-  // (relaxed/int8.ts:26-39)
+  // the chunk's terms, folded into the lanes' sums: lane k takes groups RL it + k, + 4, + 8, ... in order
+  // (relaxed/int8.ts:26-39); a 32-lane row's second 16 groups come to lanes 0..15 by v_permlane16_swap
   HQ_DEV void fold(float acc[T], int it0, int lane, int ng4, const ActSource<T, SRC> &A) const {
 #pragma unroll
     for (int u = 0; u < U; u++) {
-      const int g = (it0 + u) * 16 + lane;
+      const int g = (it0 + u) * RL + lane;
       const bool valid = g < ng4;
       uint32_t xl[T][8];  // LATE: the step's activations, read here
       float xsl[T];
@@ -208,20 +220,28 @@ struct RelaxedChunk {
         float a = fadd(acc[t], q);
         a = fadd(a, from_lane_plus<4>(q));
         a = fadd(a, from_lane_plus<8>(q));
-        acc[t] = fadd(a, from_lane_plus<12>(q));
+        a = fadd(a, from_lane_plus<12>(q));
+        if (RL == 32) {
+          const float qh = upper_row(q);
+          a = fadd(a, qh);
+          a = fadd(a, from_lane_plus<4>(qh));
+          a = fadd(a, from_lane_plus<8>(qh));
+          a = fadd(a, from_lane_plus<12>(qh));
+        }
+        acc[t] = a;
       }
     }
   }
 };
 
-// the kRelaxedRows rows of tile `tile` (the batch's jobs' row ranges cut into tiles in order).  STAGED: first make
-// the block's LDS copy of the activations, while the first weights are in flight
-template <int PACK, int T, bool WC, int SRC>
+// the kRelaxedThreads / RL rows of tile `tile` (the batch's jobs' row ranges cut into tiles in order).  STAGED: first
+// make the block's LDS copy of the activations, while the first weights are in flight
+template <int PACK, int T, bool WC, int SRC, int RL>
 HQ_DEV void relaxed_tile(const GemvBatch &batch, int tile, char *lds) {
   const int jb = job_of(batch, tile);
   const Job &J = batch.job[jb];
-  const int lane = threadIdx.x & 15;
-  const int row_u = J.r0 + (tile - batch.block0[jb]) * kRelaxedRows + (threadIdx.x >> 4);
+  const int lane = threadIdx.x & (RL - 1);
+  const int row_u = J.r0 + (tile - batch.block0[jb]) * (kRelaxedThreads / RL) + (int)(threadIdx.x / RL);
   const bool live = row_u < J.r1;
   const int row = live ? row_u : J.r1 - 1;
   const int ng = J.n >> 5, ng4 = ng & ~3;
@@ -243,9 +263,9 @@ HQ_DEV void relaxed_tile(const GemvBatch &batch, int tile, char *lds) {
   float acc[T];
 #pragma unroll
   for (int t = 0; t < T; t++) acc[t] = 0.0f;
-  using Chunk = RelaxedChunk<PACK, T, WC, SRC>;
+  using Chunk = RelaxedChunk<PACK, T, WC, SRC, RL>;
   constexpr int U = Chunk::U;
-  const int steps = (ng4 + 15) >> 4;
+  const int steps = (ng4 + RL - 1) / RL;
   Chunk a, b;
   if (SRC == STAGED) {
     if (steps > 0) a.load_w(wrow, srow, crow, 0, lane, ng4);  // the first weights in flight during the staging
@@ -318,10 +338,10 @@ HQ_DEV void relaxed_tile(const GemvBatch &batch, int tile, char *lds) {
 }
 
 // a tile a block
-template <int PACK, int T, bool WC, int SRC>
-__global__ __launch_bounds__(16 * kRelaxedRows) void gemv_relaxed(GemvBatch batch) {
+template <int PACK, int T, bool WC, int SRC, int RL>
+__global__ __launch_bounds__(kRelaxedThreads) void gemv_relaxed(GemvBatch batch) {
   extern __shared__ __align__(16) char lds[];
-  relaxed_tile<PACK, T, WC, SRC>(batch, blockIdx.x, lds);
+  relaxed_tile<PACK, T, WC, SRC, RL>(batch, blockIdx.x, lds);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -659,10 +679,15 @@ HQ_HOST_DEV constexpr int ternary_lanes(int n) {
 HQ_HOST_DEV constexpr size_t ternary_stage_bytes(int T, int n) { return (size_t)T * ternary_token_bytes(n); }
 
 template <int PACK, int T, int SRC>
-hipError_t launch_relaxed(const GemvBatch &b, int tiles, bool wc, size_t lds, hipStream_t s) {
-  dim3 grid(tiles), block(16 * kRelaxedRows);
-  if (wc) hipLaunchKernelGGL((gemv_relaxed<PACK, T, true, SRC>), grid, block, lds, s, b);
-  else hipLaunchKernelGGL((gemv_relaxed<PACK, T, false, SRC>), grid, block, lds, s, b);
+hipError_t launch_relaxed(const GemvBatch &b, int tiles, bool wc, int lanes, size_t lds, hipStream_t s) {
+  dim3 grid(tiles), block(kRelaxedThreads);
+  if (lanes == 32) {
+    if (wc) hipLaunchKernelGGL((gemv_relaxed<PACK, T, true, SRC, 32>), grid, block, lds, s, b);
+    else hipLaunchKernelGGL((gemv_relaxed<PACK, T, false, SRC, 32>), grid, block, lds, s, b);
+  } else {
+    if (wc) hipLaunchKernelGGL((gemv_relaxed<PACK, T, true, SRC, 16>), grid, block, lds, s, b);
+    else hipLaunchKernelGGL((gemv_relaxed<PACK, T, false, SRC, 16>), grid, block, lds, s, b);
+  }
   return hipGetLastError();
 }
 
@@ -691,17 +716,18 @@ hipError_t launch_signs(const GemvBatch &b, int blocks, hipStream_t s) {
 }
 
 template <int T>
-hipError_t launch_t(Kind kind, const GemvBatch &b, int blocks, bool wc, int src, size_t lds, hipStream_t s) {
+hipError_t launch_t(Kind kind, const GemvBatch &b, int blocks, bool wc, int src, int lanes, size_t lds,
+                    hipStream_t s) {
   dim3 grid(blocks), block(256);
   switch (kind) {
   case Q8R:
   case Q6R:
     if (kind == Q8R) {
-      if (src == STAGED) return launch_relaxed<8, T, STAGED>(b, blocks, wc, lds, s);
-      return launch_relaxed<8, T, GLOBAL>(b, blocks, wc, 0, s);
+      if (src == STAGED) return launch_relaxed<8, T, STAGED>(b, blocks, wc, lanes, lds, s);
+      return launch_relaxed<8, T, GLOBAL>(b, blocks, wc, lanes, 0, s);
     }
-    if (src == STAGED) return launch_relaxed<6, T, STAGED>(b, blocks, wc, lds, s);
-    return launch_relaxed<6, T, GLOBAL>(b, blocks, wc, 0, s);
+    if (src == STAGED) return launch_relaxed<6, T, STAGED>(b, blocks, wc, lanes, lds, s);
+    return launch_relaxed<6, T, GLOBAL>(b, blocks, wc, lanes, 0, s);
   case Q8: hipLaunchKernelGGL((gemv_plain<8, T>), grid, block, 0, s, b); break;
   case Q6: hipLaunchKernelGGL((gemv_plain<6, T>), grid, block, 0, s, b); break;
   case T2R:
@@ -727,7 +753,12 @@ hipError_t launch_batch(Kind kind, const Job *jobs, int32_t njobs, hipStream_t s
   GemvBatch b{};
   int blocks = 0, nmax = 0;
   for (int j = 0; j < njobs; j++) nmax = jobs[j].n > nmax ? jobs[j].n : nmax;
-  const int rpb = signs_kind(kind) ? kTernThreads / ternary_lanes(nmax) : rows_per_block(kind);
+  const int T = jobs[0].count;
+  const bool relaxed = kind == Q8R || kind == Q6R;
+  const int lanes = relaxed ? relaxed_lanes(kind, T, nmax) : 16;
+  const int rpb = signs_kind(kind) ? kTernThreads / ternary_lanes(nmax)
+                  : relaxed          ? kRelaxedThreads / lanes
+                                     : kRowsPerBlock;
   for (int j = 0; j < njobs; j++) {
     b.job[j] = jobs[j];
     b.block0[j] = blocks;
@@ -737,15 +768,14 @@ hipError_t launch_batch(Kind kind, const Job *jobs, int32_t njobs, hipStream_t s
   b.njobs = njobs;
   if (blocks == 0) return hipSuccess;
   const bool wc = jobs[0].wc != nullptr;
-  const int T = jobs[0].count;
   const size_t lds = (size_t)act_lds_bytes(T, nmax);
   // staged in LDS for 2..4 tokens (each row's lanes read every token's activations: measured 4 % faster at M = 4)
   const int src = T > 1 && lds <= kGemvStageMax ? STAGED : GLOBAL;
   switch (T) {
-  case 1: return launch_t<1>(kind, b, blocks, wc, src, lds, s);
-  case 2: return launch_t<2>(kind, b, blocks, wc, src, lds, s);
-  case 3: return launch_t<3>(kind, b, blocks, wc, src, lds, s);
-  case 4: return launch_t<4>(kind, b, blocks, wc, src, lds, s);
+  case 1: return launch_t<1>(kind, b, blocks, wc, src, lanes, lds, s);
+  case 2: return launch_t<2>(kind, b, blocks, wc, src, lanes, lds, s);
+  case 3: return launch_t<3>(kind, b, blocks, wc, src, lanes, lds, s);
+  case 4: return launch_t<4>(kind, b, blocks, wc, src, lanes, lds, s);
   default: return hipErrorInvalidValue;
   }
 }
