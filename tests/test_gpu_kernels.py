@@ -319,6 +319,50 @@ def test_relaxed_tokens_long_rows(pkg, k, arena, oracle, count, packing):
                                                 f"{first_difference(got[t], want)}"
 
 
+@pytest.mark.parametrize("count,ng,packing", [(1, 128, "int8"), (1, 256, "int8"), (2, 259, "int8"), (3, 259, "int8"),
+                                               (4, 259, "int8"), (2, 259, "int6"), (3, 259, "int6")])
+def test_relaxed_wide_rows(pkg, k, arena, oracle, count, ng, packing):
+    """The launches whose relaxed rows are 32 lanes (one int8 token on rows of 4096 or 8192 values; 2..4 tokens on
+    rows past 8192 — 2 and 3 tokens of 8288 values staged in LDS, 4 read through the caches, with 3 groups past the
+    fours): rows cut inside the 4-row blocks at both ends, the corrections given, derived and moved"""
+    from pyodide_llm_amd import jobs
+    rng = np.random.default_rng(71 + count + ng)
+    rows = 37
+    n = 32 * ng
+    frame = ((n + 4 * ng + 15) // 16) * 16
+    if packing == "int8":
+        w = rng.integers(-128, 128, rows * n).astype(np.int8)
+        wbytes, sums = w, oracle.int8_sums(w)
+    else:
+        wbytes = pack6((4 * rng.integers(-32, 32, rows * n)).astype(np.int8))
+        sums = oracle.six_sums(wbytes)
+    ws = (rng.random(rows * ng) * 1e-3).astype(F)
+    moved = sums.copy()
+    moved[rng.integers(0, rows * ng, 3)] += np.array([1, -5000, 77], np.int32)
+    q = tile_inputs(oracle, rng, n, count, frame, rows)
+    wq, wsa, xq = arena.put(wbytes, align=256), arena.put(ws), arena.put(q)
+    kind = "matmul_q8r" if packing == "int8" else "matmul_q6r"
+    product = oracle.matmul_q8r if packing == "int8" else oracle.matmul_q6r
+    for form, corrections in (("sums", sums), ("derived", None), ("moved", moved)):
+        wca = 0 if corrections is None else arena.put(corrections)
+        for r0, r1 in ([(0, rows), (3, 34)] if packing == "int8" else [(0, rows), (0, 34)]):
+            out = arena.alloc(4 * rows * count, fill=np.full(rows * count, -7, F))
+            if packing == "int8":
+                k.matmul_q8r_tile(out, xq, xq + n, wq, wsa, wca, n, r0, r1, count, 4 * rows, frame)
+            else:
+                job = jobs.job(kind, out, xq, xq + n, wq, wsa, wca, n, rows=r1, count=count, os=4 * rows, as_=frame,
+                               bs=frame)
+                assert jobs.phase(pkg.library(), [job]) == 0, pkg.library().hq_last_error_message()
+            got = arena.get(out, F, rows * count).reshape(count, rows)
+            for t in range(count):
+                full = product(q[t, :n], q[t, n:n + 4 * ng].view(F), wbytes, ws,
+                               sums if corrections is None else corrections, n)
+                want = np.full(rows, F(-7), F)
+                want[r0:r1] = full[r0:r1]
+                assert same_bits(got[t], want), f"{packing} count {count} ng {ng} rows {r0}..{r1} token {t} " \
+                                                f"wc {form}: {first_difference(got[t], want)}"
+
+
 def test_relaxed_bytes_past_seven_bits(k, arena):
     """Activation bytes 128..255 lie outside the reference's domain (its relaxed dot is machine-dependent there):
     libhq takes every byte as a signed int8, so the token kernel and the prompt tile still agree to the bit."""
