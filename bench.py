@@ -250,8 +250,8 @@ def measure_decode_m4(torch, pkg, args, phases):
     lib = pkg.library()
     step, products, step_bytes, launches, keep = build_decode_m4(torch, pkg, phases)
     reps = max(3, args.steps // 2)
-    sec = _graph_time(torch, step, reps)
-    gemv = _graph_time(torch, products, reps)
+    sec = _graph_time_median(torch, step, reps)
+    gemv = _graph_time_median(torch, products, reps)
     pkg.check(lib.hq_last_error())
     return {"M": 4, "ms_per_step": round(1e3 * sec, 4), "GBps": round(step_bytes / sec / 1e9, 1),
             "tokens_per_s": round(4 / sec, 1), "step_bytes": step_bytes,

@@ -62,8 +62,10 @@ HQ_DEV void fill_acts(const Job &J, char *lq, float *ls) {
 
 constexpr int kRowsPerBlock = 16;
 // the relaxed kinds' blocks: 128 threads, 8 rows of 16 lanes or 4 of 32 (fewer rows a block: more blocks, a finer
-// balance of the last ones over the CUs; 8 rows of 16 measured faster than 16 rows at the 8B decode)
+// balance of the last ones over the CUs; 8 rows of 16 measured faster than 16 rows at the 8B decode); 2..4 tokens
+// staged in LDS take 256 (one staged copy for twice the rows: M = 4's staged phases 5 % faster, 512 no better)
 constexpr int kRelaxedThreads = 128;
+HQ_HOST_DEV constexpr int relaxed_threads(int T, bool staged) { return T > 1 && staged ? 256 : kRelaxedThreads; }
 // Lanes a relaxed row: 32 lanes give a launch twice the waves, each lane half the steps.  Measured phase by phase
 // streaming from HBM (configs 1-4's decode shapes, int8 and int6, 16 against 32 lanes): one int8 token, 32 lanes are
 // faster where a row is 4096 or 8192 bytes (8B q/k/v 7.7 -> 7.1 us, o 6.2 -> 5.8, gate+up 25.3 -> 23.5, lm-head 97 ->
@@ -234,14 +236,15 @@ struct RelaxedChunk {
   }
 };
 
-// the kRelaxedThreads / RL rows of tile `tile` (the batch's jobs' row ranges cut into tiles in order).  STAGED: first
+// the relaxed_threads / RL rows of tile `tile` (the batch's jobs' row ranges cut into tiles in order).  STAGED: first
 // make the block's LDS copy of the activations, while the first weights are in flight
 template <int PACK, int T, bool WC, int SRC, int RL>
 HQ_DEV void relaxed_tile(const GemvBatch &batch, int tile, char *lds) {
   const int jb = job_of(batch, tile);
   const Job &J = batch.job[jb];
   const int lane = threadIdx.x & (RL - 1);
-  const int row_u = J.r0 + (tile - batch.block0[jb]) * (kRelaxedThreads / RL) + (int)(threadIdx.x / RL);
+  constexpr int rows = relaxed_threads(T, SRC == STAGED) / RL;
+  const int row_u = J.r0 + (tile - batch.block0[jb]) * rows + (int)(threadIdx.x / RL);
   const bool live = row_u < J.r1;
   const int row = live ? row_u : J.r1 - 1;
   const int ng = J.n >> 5, ng4 = ng & ~3;
@@ -339,7 +342,7 @@ HQ_DEV void relaxed_tile(const GemvBatch &batch, int tile, char *lds) {
 
 // a tile a block
 template <int PACK, int T, bool WC, int SRC, int RL>
-__global__ __launch_bounds__(kRelaxedThreads) void gemv_relaxed(GemvBatch batch) {
+__global__ __launch_bounds__(relaxed_threads(T, SRC == STAGED)) void gemv_relaxed(GemvBatch batch) {
   extern __shared__ __align__(16) char lds[];
   relaxed_tile<PACK, T, WC, SRC, RL>(batch, blockIdx.x, lds);
 }
@@ -680,7 +683,7 @@ HQ_HOST_DEV constexpr size_t ternary_stage_bytes(int T, int n) { return (size_t)
 
 template <int PACK, int T, int SRC>
 hipError_t launch_relaxed(const GemvBatch &b, int tiles, bool wc, int lanes, size_t lds, hipStream_t s) {
-  dim3 grid(tiles), block(kRelaxedThreads);
+  dim3 grid(tiles), block(relaxed_threads(T, SRC == STAGED));
   if (lanes == 32) {
     if (wc) hipLaunchKernelGGL((gemv_relaxed<PACK, T, true, SRC, 32>), grid, block, lds, s, b);
     else hipLaunchKernelGGL((gemv_relaxed<PACK, T, false, SRC, 32>), grid, block, lds, s, b);
@@ -742,7 +745,7 @@ hipError_t launch_t(Kind kind, const GemvBatch &b, int blocks, bool wc, int src,
 }  // namespace
 
 // the largest activations (bytes and scales of all tokens) a block of 2..4 tokens copies into LDS (STAGED) rather
-// than reading them through the L1: more would leave too few 8-row blocks a CU (4 tokens of the 8B down
+// than reading them through the L1: more would leave too few blocks a CU (4 tokens of the 8B down
 // projection, 64.5 KB, measured 4 % slower a decode step staged than read through the caches).  One token is read
 // through the caches (measured 9 % faster than staged).
 constexpr size_t kGemvStageMax = 32 * 1024;
@@ -756,8 +759,11 @@ hipError_t launch_batch(Kind kind, const Job *jobs, int32_t njobs, hipStream_t s
   const int T = jobs[0].count;
   const bool relaxed = kind == Q8R || kind == Q6R;
   const int lanes = relaxed ? relaxed_lanes(kind, T, nmax) : 16;
+  const size_t lds = (size_t)act_lds_bytes(T, nmax);
+  // staged in LDS for 2..4 tokens (each row's lanes read every token's activations: measured 4 % faster at M = 4)
+  const int src = T > 1 && lds <= kGemvStageMax ? STAGED : GLOBAL;
   const int rpb = signs_kind(kind) ? kTernThreads / ternary_lanes(nmax)
-                  : relaxed          ? kRelaxedThreads / lanes
+                  : relaxed          ? relaxed_threads(T, src == STAGED) / lanes
                                      : kRowsPerBlock;
   for (int j = 0; j < njobs; j++) {
     b.job[j] = jobs[j];
@@ -768,9 +774,6 @@ hipError_t launch_batch(Kind kind, const Job *jobs, int32_t njobs, hipStream_t s
   b.njobs = njobs;
   if (blocks == 0) return hipSuccess;
   const bool wc = jobs[0].wc != nullptr;
-  const size_t lds = (size_t)act_lds_bytes(T, nmax);
-  // staged in LDS for 2..4 tokens (each row's lanes read every token's activations: measured 4 % faster at M = 4)
-  const int src = T > 1 && lds <= kGemvStageMax ? STAGED : GLOBAL;
   switch (T) {
   case 1: return launch_t<1>(kind, b, blocks, wc, src, lanes, lds, s);
   case 2: return launch_t<2>(kind, b, blocks, wc, src, lanes, lds, s);
