@@ -745,10 +745,11 @@ hipError_t launch_t(Kind kind, const GemvBatch &b, int blocks, bool wc, int src,
 }  // namespace
 
 // the largest activations (bytes and scales of all tokens) a block of 2..4 tokens copies into LDS (STAGED) rather
-// than reading them through the L1: more would leave too few blocks a CU (4 tokens of the 8B down
-// projection, 64.5 KB, measured 4 % slower a decode step staged than read through the caches).  One token is read
-// through the caches (measured 9 % faster than staged).
-constexpr size_t kGemvStageMax = 32 * 1024;
+// than reading them through the L1: two blocks a CU.  Four tokens of the 8B down projection (64.5 KB) staged make the
+// decode step 2.37 -> 2.29 ms: in a step the activations were just written by quantize_x, and read through the caches
+// every wave fetches them anew (with activations left warm by earlier launches the staged form is 2 % slower).  One
+// token is read through the caches (measured 9 % faster than staged).
+constexpr size_t kGemvStageMax = 80 * 1024;
 
 namespace {
 hipError_t launch_batch(Kind kind, const Job *jobs, int32_t njobs, hipStream_t s) {

@@ -275,15 +275,17 @@ def test_q8r_tile(k, arena, oracle, count, ng):
 
 @pytest.mark.parametrize("count", [2, 3, 4])
 @pytest.mark.parametrize("packing", ["int8", "int6"])
-def test_relaxed_tokens_long_rows(pkg, k, arena, oracle, count, packing):
-    """2..4 tokens of rows so long that their activations are read through the caches rather than staged in LDS
-    (17408 values: more than 32 KB for two tokens), rows cut, the corrections given, derived and moved"""
+@pytest.mark.parametrize("ng", [544, 1152])
+def test_relaxed_tokens_long_rows(pkg, k, arena, oracle, count, packing, ng):
+    """2..4 tokens of long rows: 17408 values, whose activations (39-78 KB) are staged in LDS, and 36864, whose
+    activations (more than 80 KB for two tokens) are read through the caches; rows cut, the corrections given,
+    derived and moved"""
     from pyodide_llm_amd import jobs
-    rng = np.random.default_rng(31 + count)
-    rows, ng = 37, 544
+    rng = np.random.default_rng(31 + count + ng)
+    rows = 37
     n = 32 * ng
     frame = ((n + 4 * ng + 15) // 16) * 16
-    assert count * (n + 4 * ng) > 32 * 1024
+    assert (count * (n + 4 * ng) > 80 * 1024) == (ng == 1152)
     if packing == "int8":
         w = rng.integers(-128, 128, rows * n).astype(np.int8)
         wbytes, sums = w, oracle.int8_sums(w)
