@@ -687,77 +687,95 @@ __global__ __launch_bounds__(QT, ring_of<R>() == 3 ? 3 : 2) void gemm_relaxed(Jo
 // 8 (r / 4) + 4 (l / 32) + r % 4 of its half.  Part k of a group of 128 (block h = k / 2, bytes c = 8 (k % 2) .. + 7
 // of it) as 32 K values in the order plane-major: K half kh of a lane is planes 2 kh, 2 kh + 1, eight c's each, for
 // the codes and for interleave()'s activation bytes 64 h + 16 p + 8 (k % 2) .. + 7 alike.
+// A tile is R rows (128, or 96 for launches whose 128-row tiles would end in a part-empty round) x 64 tokens, a block
+// of R / 32 slices x 4 parts = 4 R / 32 waves, one block a CU.
 // ---------------------------------------------------------------------------------------------------------------
-constexpr int TG = 2;       // groups of 128 a stage
-constexpr int NT = 1024;    // threads a block: 16 waves, 4 slices of 32 rows x 4 parts
-constexpr int TLOADS = 3;   // loads a wave a stage
+constexpr int TG = 2;  // groups of 128 a stage
 
+template <int R>
 struct alignas(16) StageT {
-  char w[BR * 64];           // 128 rows x 2 groups x 32 code bytes; 16-byte chunk j of row r at j ^ tswz(r)
+  char w[R * 64];            // R rows x 2 groups x 32 code bytes; 16-byte chunk j of row r at j ^ tswz(r) (binary: R
+                             // rows x 2 x 16, group j of row r at j ^ bswz(r))
   char x[BT * 256];          // 64 tokens x 2 groups x 128 activation bytes; chunk c of token t at c ^ (t & 15)
   float xs[TG * 4][BT];      // the tokens' scales of each (group, part)
   int32_t sums[TG * 4][BT];  // and their sums
-  uint32_t d[TG][BR];        // the rows' float16 group scales, one a word
+  uint32_t d[TG][128];       // the rows' float16 group scales, one a word (96-row tiles: rows 96..127 loaded, unread)
 };
 
 HQ_DEV int tswz(int r) { return (r >> 2) & 3; }
 // binary: a row's two 16-byte groups of a stage, swapped on every other 8 rows
 HQ_DEV int bswz(int r) { return (r >> 3) & 1; }
 
-// a block's loads of ternary (binary: BIN) stages: wave w's three loads a stage and their offsets
-template <bool BIN>
+// A block's loads of a stage, as pieces dealt to the waves in turn (wave w takes pieces w, w + NW, ...): 16 pieces of
+// the activations (tokens 4 p .. + 3, 1 KB each), the codes (16 rows a piece; binary 32), the tokens' scales and sums
+// of each (group, part) (256 bytes each), the rows' scales (64 rows a piece, 2 bytes a row).  Every wave issues PW
+// loads a stage (a load past the pieces reads 1 KB into a junk area), so one wait count serves every wave.
+template <bool BIN, int R>
 struct Ternary {
+  static constexpr int NW = 4 * (R / 32);                   // waves
+  static constexpr int NC = BIN ? R / 32 : R / 16;          // code pieces
+  static constexpr int ND = (R + 63) / 64;                  // row-scale pieces a group
+  static constexpr int P = 16 + NC + 16 + TG * ND;          // pieces a stage
+  static constexpr int PW = (P + NW - 1) / NW;              // loads a wave a stage
   __amdgpu_buffer_rsrc_t rw, rx, rxs, rws;
-  uint32_t oa, ob, oc;
+  uint32_t off[PW];
   int wave;
   char *junk;
 
   HQ_DEV Ternary(const Job &J, int row0, int tok0, int M, int w, char *junk_area) : wave(w), junk(junk_area) {
     const int lane = threadIdx.x & 63, groups = J.n >> 7;
-    const int nsc = 4 * (J.n >> 5);  // the bytes of a token's scales: its sums follow them
-    constexpr int GB = BIN ? 16 : 32;  // bytes of a group's codes
+    const int nsc = 4 * (J.n >> 5);
+    constexpr int GB = BIN ? 16 : 32;
     rw = resource(J.wq + (int64_t)row0 * groups * GB, (int64_t)(J.r1 - row0) * groups * GB);
     rws = resource(J.ws + (int64_t)row0 * groups * 2, (int64_t)(J.r1 - row0) * groups * 2);
     rx = resource(J.xq + tok0 * J.frame, (M - 1 - tok0) * J.frame + J.n);
     rxs = resource(J.xs + tok0 * J.sframe, (M - 1 - tok0) * J.sframe + 2 * nsc);
-    // load a: the activations, tokens 4 w .. + 3, lane l token 4 w + l / 16, slot l % 16 holding chunk
-    // (l % 16) ^ (token & 15) of the stage's 256 bytes
-    {
-      const int tok = 4 * w + (lane >> 4), c = (lane & 15) ^ (tok & 15);
-      oa = (uint32_t)(tok * J.frame + c * 16);
-    }
-    // load b: waves 0..7 the codes (rows 16 w .. + 15, lane l row 16 w + l / 4, slot l % 4 holding chunk
-    // (l % 4) ^ tswz(row) of the row's 64 bytes; binary: waves 0..3, rows 32 w .. + 31, lane l row 32 w + l / 2,
-    // slot l % 2 holding group (l % 2) ^ bswz(row) of the row's 32 bytes, waves 4..7 into the scratch area); waves
-    // 8..15 the tokens' scales of (group, part) w - 8
-    if (w < 8 && BIN) {
-      const int row = 32 * (w & 3) + (lane >> 1), j = (lane & 1) ^ bswz(row);
-      ob = (uint32_t)(row * groups * 16 + j * 16);
-    } else if (w < 8) {
-      const int row = 16 * w + (lane >> 2), j = (lane & 3) ^ tswz(row);
-      ob = (uint32_t)(row * groups * 32 + (j >> 1) * 32 + (j & 1) * 16);
-    } else {
-      ob = (uint32_t)(lane * J.sframe + (w - 8) * 4);
-    }
-    // load c: waves 0..7 the sums of (group, part) w; waves 8..11 the float16 scales (group (w - 8) / 2, rows
-    // 64 ((w - 8) % 2) + l)
-    if (w < 8) {
-      oc = (uint32_t)(lane * J.sframe + nsc + w * 4);
-    } else {
-      const int i = w - 8;
-      oc = (uint32_t)(((64 * (i & 1) + lane) * groups + (i >> 1)) * 2);
+#pragma unroll
+    for (int k = 0; k < PW; k++) {
+      const int p = w + NW * k;
+      uint32_t o = 0;
+      if (p < 16) {
+        const int tok = 4 * p + (lane >> 4), c = (lane & 15) ^ (tok & 15);
+        o = (uint32_t)(tok * J.frame + c * 16);
+      } else if (p < 16 + NC) {
+        const int q = p - 16;
+        if (BIN) {
+          const int row = 32 * q + (lane >> 1), j = (lane & 1) ^ bswz(row);
+          o = (uint32_t)(row * groups * 16 + j * 16);
+        } else {
+          const int row = 16 * q + (lane >> 2), j = (lane & 3) ^ tswz(row);
+          o = (uint32_t)(row * groups * 32 + (j >> 1) * 32 + (j & 1) * 16);
+        }
+      } else if (p < 24 + NC) {
+        o = (uint32_t)(lane * J.sframe + (p - 16 - NC) * 4);
+      } else if (p < 32 + NC) {
+        o = (uint32_t)(lane * J.sframe + nsc + (p - 24 - NC) * 4);
+      } else if (p < P) {
+        const int q = p - 32 - NC, g = q / ND, i = q % ND;
+        o = (uint32_t)(((64 * i + lane) * groups + g) * 2);
+      }
+      off[k] = o;
     }
   }
 
-  HQ_DEV void load(StageT &S, int s) {
-    const int w = wave;
-    dma16(rx, S.x + w * 1024, oa, s * TG * 128);
-    if (w < 8 && (!BIN || w < 4)) dma16(rw, S.w + w * 1024, ob, s * TG * (BIN ? 16 : 32));
-    else if (w < 8) dma16(rxs, junk, 0, 0);
-    else dma4(rxs, &S.xs[w - 8][0], ob, s * TG * 16);
-    if (w < 8) dma4(rxs, &S.sums[w][0], oc, s * TG * 16);
-    else if (w < 12) dma2(rws, &S.d[(w - 8) >> 1][64 * ((w - 8) & 1)], oc, s * TG * 2);
-    else dma4(rxs, junk, 0, 0);
+  // (the stage buffer's address made opaque, so that the compiler forms each load's LDS destination here instead of
+  // holding every buffer's destinations in scalar registers across the main loop)
+  HQ_DEV void load(StageT<R> &S, int s) {
+    uint32_t base = lds_addr(&S);
+    asm volatile("" : "+s"(base));
+    const auto at = [&](size_t o) { return (void *)(uintptr_t)(base + (uint32_t)o); };
+#pragma unroll
+    for (int k = 0; k < PW; k++) {
+      const int p = wave + NW * k;
+      if (p < 16) dma16(rx, at(offsetof(StageT<R>, x) + p * 1024), off[k], s * TG * 128);
+      else if (p < 16 + NC) dma16(rw, at(offsetof(StageT<R>, w) + (p - 16) * 1024), off[k], s * TG * (BIN ? 16 : 32));
+      else if (p < 24 + NC) dma4(rxs, at(offsetof(StageT<R>, xs) + (p - 16 - NC) * 4 * BT), off[k], s * TG * 16);
+      else if (p < 32 + NC) dma4(rxs, at(offsetof(StageT<R>, sums) + (p - 24 - NC) * 4 * BT), off[k], s * TG * 16);
+      else if (p < P) {
+        const int q = p - 32 - NC;
+        dma2(rws, at(offsetof(StageT<R>, d) + ((q / ND) * 128 + 64 * (q % ND)) * 4), off[k], s * TG * 2);
+      } else dma16(rxs, junk, 0, 0);
+    }
   }
 };
 
@@ -784,20 +802,18 @@ HQ_DEV v4i bit_pair(uint32_t w0, uint32_t w1, int b) {
 // part k of group gi of the stage for the lane's slice, both token halves: f(f(whole * xs) * d) into the part's
 // chain (relaxed/signs.ts:31).  The stage's operands are read by blocks of ds_reads with one wait each: read as C++
 // loads, each would first wait for every buffer-to-LDS load in flight, the next stages' included (the compiler cannot
-// tell that those write other stage buffers), and no stage's loads would overlap the stages before it.
-template <bool BIN>
-HQ_DEV void t_group(float acc0[16], float acc1[16], const StageT &S, int gi, int k, int slice, int lane) {
+// tell that those write other stage buffers), and no stage's loads would overlap the stages before it.  The codes'
+// address and the others are byte offsets added to the stage buffer's address, made opaque to the compiler so that it
+// adds them here rather than keeping every stage buffer's addresses in registers.
+template <bool BIN, int R>
+HQ_DEV void t_group(float acc0[16], float acc1[16], const StageT<R> &S, int gi, int k, int slice, int lane) {
   const int h = k >> 1, s = k & 1, kh = lane >> 5, row = 32 * slice + (lane & 31);
   const int o = 128 * gi + 64 * h + 8 * s + 32 * kh;
-  // the row's codes (ternary: chunk 2 gi + h, half s; binary: group gi's 16 bytes, half s), its scale, the tokens'
-  // activations (8 bytes at o and o + 16 of token 32 half + lane % 32), the sums and scales of tokens
-  // 32 half + 4 kh + 8 q: byte offsets in the stage buffer, added to its address, which is made opaque to the compiler
-  // so that it adds them here rather than keeping every stage buffer's addresses in registers
   uint32_t base = lds_addr(&S);
   asm volatile("" : "+s"(base));
-  const uint32_t aw = base + (BIN ? (uint32_t)(offsetof(StageT, w) + row * 32 + ((gi ^ bswz(row)) << 4) + 8 * s)
-                                  : (uint32_t)(offsetof(StageT, w) + row * 64 + (((2 * gi + h) ^ tswz(row)) << 4) + 8 * s));
-  const uint32_t ad = base + (uint32_t)(offsetof(StageT, d) + (gi * BR + row) * 4);
+  const uint32_t aw = base + (BIN ? (uint32_t)(offsetof(StageT<R>, w) + row * 32 + ((gi ^ bswz(row)) << 4) + 8 * s)
+                                  : (uint32_t)(offsetof(StageT<R>, w) + row * 64 + (((2 * gi + h) ^ tswz(row)) << 4) + 8 * s));
+  const uint32_t ad = base + (uint32_t)(offsetof(StageT<R>, d) + (gi * 128 + row) * 4);
   uint32_t aa[2][2];
 #pragma unroll
   for (int half = 0; half < 2; half++) {
@@ -805,12 +821,11 @@ HQ_DEV void t_group(float acc0[16], float acc1[16], const StageT &S, int gi, int
 #pragma unroll
     for (int i = 0; i < 2; i++) {
       const int oi = o + 16 * i;
-      aa[half][i] = base + (uint32_t)(offsetof(StageT, x) + tok * 256 + (((oi >> 4) ^ (tok & 15)) << 4) + (oi & 8));
+      aa[half][i] = base + (uint32_t)(offsetof(StageT<R>, x) + tok * 256 + (((oi >> 4) ^ (tok & 15)) << 4) + (oi & 8));
     }
   }
-  const uint32_t asum = base + (uint32_t)(offsetof(StageT, sums) + ((4 * gi + k) * BT + 4 * kh) * 4);
-  const uint32_t axs = base + (uint32_t)(offsetof(StageT, xs) + ((4 * gi + k) * BT + 4 * kh) * 4);
-  // the codes, the scale, token half 0's activations and sums
+  const uint32_t asum = base + (uint32_t)(offsetof(StageT<R>, sums) + ((4 * gi + k) * BT + 4 * kh) * 4);
+  const uint32_t axs = base + (uint32_t)(offsetof(StageT<R>, xs) + ((4 * gi + k) * BT + 4 * kh) * 4);
   uint2 wv, a0, a1;
   uint32_t dh;
   v4i c[4];
@@ -821,7 +836,6 @@ HQ_DEV void t_group(float acc0[16], float acc1[16], const StageT &S, int gi, int
       : "=&v"(wv), "=&v"(dh), "=&v"(a0), "=&v"(a1), "=&v"(c[0]), "=&v"(c[1]), "=&v"(c[2]), "=&v"(c[3])
       : "v"(aw), "v"(ad), "v"(aa[0][0]), "v"(aa[0][1]), "v"(asum)
       : "memory");
-  // B: the row's codes of planes 2 kh, 2 kh + 1 (binary: bits 4 h + 2 kh ..)
   v4i B;
   if (BIN) B = bit_pair(wv.x, wv.y, 4 * h + 2 * kh);
   else B = kh == 0 ? plane_pair<0>(wv.x, wv.y) : plane_pair<2>(wv.x, wv.y);
@@ -837,7 +851,6 @@ HQ_DEV void t_group(float acc0[16], float acc1[16], const StageT &S, int gi, int
     return __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, cin, 0, 0, 0);
   };
   const v16i C0 = product(a0, a1, c);
-  // token half 1's activations and sums, half 0's scales
   v4f x[4];
   asm volatile(
       "ds_read_b64 %0, %10\n\tds_read_b64 %1, %11\n\t"
@@ -865,44 +878,44 @@ HQ_DEV void t_group(float acc0[16], float acc1[16], const StageT &S, int gi, int
     for (int e = 0; e < 4; e++) acc1[4 * q + e] = fadd(acc1[4 * q + e], fmul(fmul((float)C1[4 * q + e], x[q][e]), d));
 }
 
-template <bool BIN>
-HQ_DEV void t_step(Ternary<BIN> &L, const StageT &cur, StageT &next, int s, int stages, int groups, float acc0[16],
-                   float acc1[16], int slice, int part, int lane) {
+// stage s of the tile: its loads landed everywhere (two stages after it still in flight), the loads of stage s + 3
+// issued into the buffer stage s - 1 was read from, then part `part` of groups 2 s and 2 s + 1 (relaxed/signs.ts:28-31)
+template <bool BIN, int R>
+HQ_DEV void t_step(Ternary<BIN, R> &L, const StageT<R> &cur, StageT<R> &next, int s, int stages, int groups,
+                    float acc0[16], float acc1[16], int slice, int part, int lane) {
   if (s >= stages) return;
-  wait_for<TLOADS>(s, stages, AHEAD - 1);
+  wait_for<Ternary<BIN, R>::PW>(s, stages, AHEAD - 1);
   if (s + AHEAD < stages) L.load(next, s + AHEAD);
-  // part `part` of groups 2 s and 2 s + 1 (relaxed/signs.ts:28-31)
-  t_group<BIN>(acc0, acc1, cur, 0, part, slice, lane);
-  if (TG * s + 1 < groups) t_group<BIN>(acc0, acc1, cur, 1, part, slice, lane);
+  t_group<BIN, R>(acc0, acc1, cur, 0, part, slice, lane);
+  if (TG * s + 1 < groups) t_group<BIN, R>(acc0, acc1, cur, 1, part, slice, lane);
 }
 
-template <bool BIN>
-__global__ __launch_bounds__(NT) void gemm_ternary(Job J) {
-  __shared__ StageT b0, b1, b2, b3;
+// the tile's stages, the four parts' chains added in order ((p0 + p1) + p2) + p3 (math.ts:7-9), part 3's waves storing
+template <bool BIN, int R>
+__global__ __launch_bounds__(64 * 4 * (R / 32)) void gemm_ternary(Job J) {
+  __shared__ StageT<R> b0, b1, b2, b3;
   __shared__ __attribute__((aligned(16))) char junk[1024];
   const int M = J.count;
   const int groups = J.n >> 7;
   int rb, tb;
-  tile_of(blockIdx.x, gridDim.x, (J.r1 - J.r0 + BR - 1) / BR, rb, tb);
-  const int row0 = J.r0 + rb * BR, tok0 = tb * BT;
+  tile_of(blockIdx.x, gridDim.x, (J.r1 - J.r0 + R - 1) / R, rb, tb);
+  const int row0 = J.r0 + rb * R, tok0 = tb * BT;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int slice = wave >> 2, part = wave & 3;
-
   float acc0[16], acc1[16];
 #pragma unroll
   for (int r = 0; r < 16; r++) acc0[r] = acc1[r] = 0.0f;
-
-  Ternary<BIN> L(J, row0, tok0, M, wave, junk);
+  Ternary<BIN, R> L(J, row0, tok0, M, wave, junk);
   const int stages = (groups + TG - 1) / TG;
   if (stages > 0) L.load(b0, 0);
   if (stages > 1) L.load(b1, 1);
   if (stages > 2) L.load(b2, 2);
   for (int s = 0; s < stages; s += RING) {
-    t_step<BIN>(L, b0, b3, s, stages, groups, acc0, acc1, slice, part, lane);
-    t_step<BIN>(L, b1, b0, s + 1, stages, groups, acc0, acc1, slice, part, lane);
-    t_step<BIN>(L, b2, b1, s + 2, stages, groups, acc0, acc1, slice, part, lane);
-    t_step<BIN>(L, b3, b2, s + 3, stages, groups, acc0, acc1, slice, part, lane);
+    t_step<BIN, R>(L, b0, b3, s, stages, groups, acc0, acc1, slice, part, lane);
+    t_step<BIN, R>(L, b1, b0, s + 1, stages, groups, acc0, acc1, slice, part, lane);
+    t_step<BIN, R>(L, b2, b1, s + 2, stages, groups, acc0, acc1, slice, part, lane);
+    t_step<BIN, R>(L, b3, b2, s + 3, stages, groups, acc0, acc1, slice, part, lane);
   }
   stage_ready<0>();
   add_chains(acc0, acc1, (float *)&b0, (float *)&b1, slice, part, lane);
@@ -925,11 +938,29 @@ __global__ __launch_bounds__(NT) void gemm_ternary(Job J) {
   }
 }
 
+// The ternary tile's rows for a launch: 96 where that costs less, a launch costing its rounds of tiles over the CUs (one
+// block a CU) times the tile's rows times its cost a row (a 96-row tile of 12 waves does 1.155 times the 128-row
+// tile's time a row, measured over launches of many rounds: 348 against 402 TOPS).  27B at M = 256: gate/up 544
+// tiles of 128 rows (3 rounds, the last an eighth full) against 728 of 96 (3 rounds), 276 -> 331 TOPS; down 160 of
+// 128 (96 CUs idle) against 216 of 96, 276 -> 329; at M = 1024 both keep 128 rows.
+int ternary_rows(int rows, int token_tiles) {
+  const int64_t cus = cu_count();
+  const int64_t r128 = ((int64_t)((rows + 127) / 128) * token_tiles + cus - 1) / cus;
+  const int64_t r96 = ((int64_t)((rows + 95) / 96) * token_tiles + cus - 1) / cus;
+  return 96.0 * 1.155 * (double)r96 < 128.0 * (double)r128 ? 96 : 128;
+}
+
 // int8 / int6: the wide scale loads where a stage's four scales of every row and token are 16-byte aligned runs
 bool wide_scales(const Job &j) {
   const auto a16 = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
   return (j.n >> 5) % 4 == 0 && a16(j.ws) && (j.wc == nullptr || a16(j.wc)) && a16(j.xs) &&
          (j.count <= 1 || j.sframe % 16 == 0);
+}
+
+template <bool BIN, int R>
+void launch_ternary(const Job &job, int token_tiles, hipStream_t s) {
+  const dim3 grid(((job.r1 - job.r0 + R - 1) / R) * token_tiles);
+  hipLaunchKernelGGL((gemm_ternary<BIN, R>), grid, dim3(8 * R), 0, s, job);
 }
 
 template <int PACK, int R>
@@ -973,9 +1004,15 @@ hipError_t launch_gemm(Kind kind, const Job &job, hipStream_t s) {
     else launch_relaxed<6, 64>(job, token_tiles, s);
     break;
   case T2R:
-  case T2: hipLaunchKernelGGL(gemm_ternary<false>, dim3(((rows + BR - 1) / BR) * token_tiles), dim3(NT), 0, s, job); break;
+  case T2:
+    if (ternary_rows(rows, token_tiles) == 96) launch_ternary<false, 96>(job, token_tiles, s);
+    else launch_ternary<false, 128>(job, token_tiles, s);
+    break;
   case B1R:
-  case B1: hipLaunchKernelGGL(gemm_ternary<true>, dim3(((rows + BR - 1) / BR) * token_tiles), dim3(NT), 0, s, job); break;
+  case B1:
+    if (ternary_rows(rows, token_tiles) == 96) launch_ternary<true, 96>(job, token_tiles, s);
+    else launch_ternary<true, 128>(job, token_tiles, s);
+    break;
   default: return hipErrorNotSupported;
   }
   return hipGetLastError();

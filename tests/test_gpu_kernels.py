@@ -586,6 +586,60 @@ def test_t2r_tile(k, arena, oracle, count, groups):
                                             f"{first_difference(got[t], want)}"
 
 
+def ternary_tile_rows(rows, token_tiles, cus):
+    """the rows of the ternary prompt tile for a launch (gemm.hip's ternary_rows: 96 where its rounds of tiles over
+    the CUs, one block a CU, times 96 x 1.155 cost less than the 128-row tiles' rounds times 128)"""
+    r128 = -(-(-(-rows // 128) * token_tiles) // cus)
+    r96 = -(-(-(-rows // 96) * token_tiles) // cus)
+    return 96 if 96 * 1.155 * r96 < 128 * r128 else 128
+
+
+@pytest.mark.parametrize("height", [96, 128])
+@pytest.mark.parametrize("packing", ["ternary", "binary"])
+def test_signs_tile_heights(pkg, k, arena, oracle, height, packing):
+    """The ternary / binary prompt tile at both heights: 96 rows (a launch of few tiles: 301 rows cut at 3 and 299, 131
+    tokens) and 128 (a launch of two full rounds of 128-row tiles, sized from the device's CU count: ~32 row tiles
+    of 1024 tokens, cut at 5 and 21 short of the end); 3 groups of 128, rows cut inside the tiles."""
+    import torch
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    if height == 96:
+        rows, r0, r1, count = 301, 3, 299, 131
+    else:
+        count = 1024
+        rows = 128 * ((2 * cus) // 16) + 26
+        r0, r1 = 5, rows - 21
+    assert ternary_tile_rows(r1 - r0, -(-count // 64), cus) == height
+    groups = 3
+    if packing == "ternary":
+        n, codes, halves, rng = ternary_case(groups, rows=rows, seed=900 + height)
+        wbytes = pack_ternary(codes)
+    else:
+        n, _, wbytes, halves, rng = binary_case(groups, rows=rows, seed=900 + height)
+    wq, wsa = arena.put(wbytes), arena.put(halves)
+    frame = ((n + 8 * (n // 32) + 15) // 16) * 16
+    buf = np.zeros((count, frame), np.uint8)
+    areas = []
+    for t in range(count):
+        xq_b, area = ternary_acts(rng, oracle, n)
+        buf[t, :n] = xq_b.view(np.uint8)
+        buf[t, n:n + area.nbytes] = area.view(np.uint8)
+        areas.append((xq_b, area))
+    xq = arena.put(buf)
+    os_ = 4 * (rows + 5)
+    out = arena.alloc(os_ * count, fill=np.full(os_ * count // 4, -7, F))
+    if packing == "ternary":
+        k.matmul_t2r_tile(out, xq, xq + n, wq, wsa, n, r0, r1, count, os_, frame, 3)
+    else:
+        k.matmul_b1r_tile(out, xq, xq + n, wq, wsa, n, r0, r1, count, os_, frame, 2)
+    got = arena.get(out, F, os_ * count // 4).reshape(count, -1)
+    product = oracle.matmul_t2r if packing == "ternary" else oracle.matmul_b1r
+    for t in range(count):
+        full = product(areas[t][0], areas[t][1], wbytes, halves, n)
+        want = np.full(os_ // 4, F(-7), F)
+        want[r0:r1] = full[r0:r1]
+        assert same_bits(got[t], want), f"{packing} height {height} token {t}: {first_difference(got[t], want)}"
+
+
 # ---- binary: the ternary kernels on one bit a weight ----------------------------------------------------------
 def binary_case(groups, rows=ROWS, seed=634):
     """tests/ternary-check.ts:292-305: signs (row 0 all +1, row 1 all -1), written both ways, the scales of
