@@ -34,8 +34,9 @@
 // Tiles.  int8 / int6: a block (4 waves, two blocks a CU) computes a 64-row x 64-token tile; wave w is chain w, four
 // 32 x 32 sub-tiles (two row slices x two token halves: the weights' operand read once for two MFMAs, the tokens' for
 // two slices).  Launches whose 64-row tiles would leave block slots idle take 32-row tiles (one slice, ~150 VGPRs,
-// a ring of 3 stage buffers: three blocks a CU).  Ternary: a block of 16 waves computes a 128-row x 64-token tile; wave w takes rows 32 (w / 4) .. + 31
-// and chain w % 4, both 32-token halves.
+// a ring of 3 stage buffers: three blocks a CU).  Ternary: a block of 16 waves computes a 128-row x 64-token tile
+// (12 waves and 96 rows for launches whose 128-row tiles would end in a part-empty round); wave w takes rows
+// 32 (w / 4) .. + 31 and chain w % 4, both 32-token halves.
 //
 // Pipeline (int8 / int6).  A wave issues each sub-tile's MFMAs one sub-tile ahead of its epilogue, so the matrix core
 // works on the next sub-tile while the VALU folds this one.  The operands go from HBM / L2 straight into LDS with
