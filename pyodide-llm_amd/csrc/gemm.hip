@@ -462,12 +462,12 @@ HQ_DEV void fold(float a[16], const v16i &c, const v32f &sc, int h) {
 }
 
 // Stage s of wave W's chain (group 4 s + W): the stage's loads landed everywhere (the block's barrier), the
-// wave's operands read from `cur`, its loads of stage s + 3 issued into `dma` (the buffer stage s - 1's operands came
-// from, which every wave has read by this barrier), then the four sub-tiles (slice, half) = (0, 0), (0, 1), (1, 0),
-// (1, 1) (a 32-row tile: the first two), each sub-tile's MFMAs issued before the previous one's fold so that the matrix core and the VALU take
-// turns without waiting for each other.  Every wave has issued its loads of stages up to s + 2 at the barrier (a
-// stage past the job's last group loads zeros, and its buffer is never read), so "stage s landed" is always "at most
-// two stages of this wave's loads in flight".
+// wave's operands read from `cur`, its loads of stage s + 3 (s + 2 with 3 buffers) issued into `dma` (the buffer
+// stage s - 1's operands came from, which every wave has read by this barrier), then the four sub-tiles (slice, half)
+// = (0, 0), (0, 1), (1, 0), (1, 1) (a 32-row tile: the first two), each sub-tile's MFMAs issued before the previous
+// one's fold so that the matrix core and the VALU take turns without waiting for each other.  Every wave has issued
+// its loads of stages up to s + 2 (s + 1) at the barrier (a stage past the job's last group loads zeros, and its
+// buffer is never read), so "stage s landed" is always "at most two stages (one) of this wave's loads in flight".
 template <int PACK, bool WC, bool WIDE, int W, int R>
 HQ_DEV void q_stage(Relaxed<PACK, WC, WIDE, W, R> &L, const StageQ<R> &cur, StageQ<R> &dma, int s, float acc[4][16],
                     int lane) {
@@ -939,8 +939,8 @@ __global__ __launch_bounds__(64 * 4 * (R / 32)) void gemm_ternary(Job J) {
   }
 }
 
-// The ternary tile's rows for a launch: 96 where that costs less, a launch costing its rounds of tiles over the CUs (one
-// block a CU) times the tile's rows times its cost a row (a 96-row tile of 12 waves does 1.155 times the 128-row
+// The ternary tile's rows for a launch: 96 where that costs less, a launch costing its rounds of tiles over the CUs
+// (one block a CU) times the tile's rows times its cost a row (a 96-row tile of 12 waves does 1.155 times the 128-row
 // tile's time a row, measured over launches of many rounds: 348 against 402 TOPS).  27B at M = 256: gate/up 544
 // tiles of 128 rows (3 rounds, the last an eighth full) against 728 of 96 (3 rounds), 276 -> 331 TOPS; down 160 of
 // 128 (96 CUs idle) against 216 of 96, 276 -> 329; at M = 1024 both keep 128 rows.
