@@ -62,7 +62,7 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef float v32f __attribute__((ext_vector_type(32)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-constexpr int BR = 128, BT = 64;  // block tile: rows x tokens
+constexpr int BT = 64;           // a tile's tokens
 constexpr int RING = 4;           // stage buffers
 constexpr int AHEAD = RING - 1;   // stages loaded beyond the one computed
 // the int8 / int6 tiles' rings: 4 buffers for 64-row tiles (76 KB, two blocks a CU), 3 for 32-row tiles (45 KB,
