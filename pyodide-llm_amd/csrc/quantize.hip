@@ -14,12 +14,12 @@ namespace hq {
 __global__ __launch_bounds__(256) void quantize_kernel(char *xq, char *xs, const char *x, int32_t n, int32_t bias,
                                                        int64_t total_groups, int64_t frame, int64_t x_stride) {
   const int32_t ng = n >> 5;
-  const int64_t gi = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
+  const uint32_t gi = blockIdx.x * 8u + (threadIdx.x >> 5);
   const int j = threadIdx.x & 31;
-  const bool live = gi < total_groups;
-  const int64_t gg = live ? gi : 0;
-  const int64_t t = gg / ng;
-  const int32_t g = (int32_t)(gg - t * ng);
+  const bool live = gi < (uint64_t)total_groups;
+  const uint32_t gg = live ? gi : 0;
+  const uint32_t t = total_groups <= ng ? 0u : gg / (uint32_t)ng;
+  const int32_t g = (int32_t)(gg - t * (uint32_t)ng);
   const float v = ((const float *)(x + t * x_stride))[g * GS + j];
 
   float m = fabsf(v);
@@ -47,6 +47,7 @@ __global__ __launch_bounds__(256) void quantize_kernel(char *xq, char *xs, const
 hipError_t launch_quantize_x(char *xq, char *xs, const char *x, int32_t n, int32_t bias, int32_t count,
                              int64_t frame, int64_t x_stride, hipStream_t s) {
   const int64_t groups = (int64_t)count * (n >> 5);
+  if (groups >= (int64_t)1 << 32) return hipErrorInvalidValue;  // the kernel's group index is 32-bit
   const int64_t blocks = (groups + 7) / 8;
   hipLaunchKernelGGL(quantize_kernel, dim3((uint32_t)blocks), dim3(256), 0, s, xq, xs, x, n, bias, groups, frame,
                      x_stride);
