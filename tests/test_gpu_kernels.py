@@ -80,9 +80,10 @@ def test_quantize_x_nan_groups(k, arena, oracle):
     assert got_s[1] == want_s[1]
 
 
-def test_quantize_x_batch(pkg, arena, oracle):
+@pytest.mark.parametrize("n,count,frame", [(1024, 7, 2048), (4608, 3, 5248), (14336, 4, 16128)])
+def test_quantize_x_batch(pkg, arena, oracle, n, count, frame):
+    """tokens of a batch: each token's group index taken apart as token and group (group counts 32, 144, 448)"""
     rng = np.random.default_rng(11)
-    n, count, frame = 1024, 7, 2048
     x = rng.standard_normal((count, n)).astype(F)
     ax = arena.put(x)
     xq = arena.alloc(count * frame)
