@@ -61,8 +61,11 @@ STORAGES = {s.name: s for s in (
     Storage("float32", 32), Storage("float16", 16),
     Storage("int8", 8, 4, int8_group), Storage("int6", 6, 4, lambda length: 32),
     Storage("ternary", 2, 2, lambda length: 128), Storage("binary", 1, 2, lambda length: 128))}
-# the storages tried in turn: a size two of them share is the earlier's (the reference's preference)
-PREFERENCE = ("float32", "float16", "int8", "int6", "ternary", "binary")
+# the storages tried in turn: a size two of them share is the earlier's.  The reference's table of sizes
+# (src/python/engine/checkpoint.py:159-169) takes the unpacked storages in the order float32, float16, int8, a later
+# one taking over a size an earlier one had, then the packed ones only where a size is still free: int8, float16,
+# float32, then int6, ternary, binary.
+PREFERENCE = ("int8", "float16", "float32", "int6", "ternary", "binary")
 QUANTIZED = ("int8", "int6", "ternary", "binary")
 
 

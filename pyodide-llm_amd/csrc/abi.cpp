@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cmath>
 #include <cstdarg>
@@ -639,9 +640,14 @@ int32_t ready_acts(hq::Kind k, char *xq, char *xs, const char *x, int32_t n, int
 // matmulsAlike (src/runtime/forward/engine.ts:398-407): a kind at a time, the input readied as that kind's jobs take
 // it, then those jobs run as hq_phase runs them.  staging NULL: into the jobs' own a / b (a pair several jobs share
 // readied once); else into staging (every job's a / b replaced by it, its tokens `frame` bytes apart), kind after
-// kind in stream order.
+// kind in stream order.  A job of no rows computes nothing and takes no part: check_job passes it without looking
+// at its pointers, so its a / b are never written.
 int32_t matmuls_alike(const void *x, int32_t x_stride, std::vector<hq::Job> by_kind[kKinds], char *staging,
                       int64_t staging_bytes, hipStream_t s, const char *who) {
+  for (int kind = 0; kind < kKinds; kind++) {
+    auto &list = by_kind[kind];
+    list.erase(std::remove_if(list.begin(), list.end(), [](const hq::Job &j) { return j.r1 == j.r0; }), list.end());
+  }
   // one input: every job of one n and one token count
   int32_t n = -1, tokens = -1;
   for (int kind = 0; kind < kKinds; kind++)
@@ -724,7 +730,10 @@ int32_t hq_matmuls_static(const void *x, int32_t x_stride, const double *jobs, i
       if ((int64_t)j.count * staging_frame(j.n) > kStagingBytes)
         return fail(HQ_ERR_ARGUMENT, "hq_matmuls_static: %d tokens of %d activations take %lld bytes of staging (at "
                     "most %lld)", j.count, j.n, (long long)(j.count * staging_frame(j.n)), (long long)kStagingBytes);
-  if (count == 0) return HQ_OK;
+  bool work = false;  // jobs of no rows or no tokens compute nothing: with only those, no device is needed
+  for (auto &list : by_kind)
+    for (const hq::Job &j : list) work = work || (j.r1 > j.r0 && j.count > 0);
+  if (!work) return HQ_OK;
   char *staging = nullptr;
   if (int32_t st = scratch_of(&staging)) return st;
   return matmuls_alike(x, x_stride, by_kind, staging, kStagingBytes, stream_of(stream), "hq_matmuls_static");

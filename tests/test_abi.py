@@ -199,3 +199,14 @@ def test_matmuls_static_refuses_more_than_its_staging(pkg):
     assert L.hq_matmuls_static(4096, 4 * n, jobs.table([job]), 1, jobs.JOB, None) == pkg.HQ_ERR_ARGUMENT
     assert "staging" in L.hq_last_error_message().decode()
     L.hq_clear_error()
+
+
+def test_matmuls_passes_over_jobs_of_no_rows(pkg):
+    """A job of no rows computes nothing, so hq_matmuls neither checks nor readies its a / b (here 0) and takes no
+    part of it in the one-input check: a table of only such jobs succeeds without a device or an input."""
+    from pyodide_llm_amd import jobs
+    L = pkg.library()
+    empty = jobs.job("matmul_q8r", 0, 0, 0, 0, 0, 0, 64, rows=0, count=3, os=0, as_=0, bs=0)
+    other = jobs.job("matmul_t2r", 0, 0, 0, 0, 0, 0, 4096, rows=0, count=1)
+    assert jobs.matmuls(L, 0, 0, [empty, other]) == 0, L.hq_last_error_message()
+    assert L.hq_matmuls_static(0, 0, jobs.table([empty]), 1, jobs.JOB, None) == 0, L.hq_last_error_message()

@@ -45,6 +45,16 @@ def test_sizes_follow_the_layout(ck):
         assert ck.storage_of(shape, size) == dtype
 
 
+def test_a_size_two_storages_share_is_the_references_choice(ck):
+    """Tiny headers can give two storages one size: here float16 and int8 are both 308 bytes.  The reference's size
+    table lets int8 take a size float16 (or float32) had and the packed storages only a free size
+    (src/python/engine/checkpoint.py:159-169): int8 wins."""
+    shape = ck.read_header((4, 4, 1, 1, 1, 1, 3))
+    assert ck.file_bytes(shape, "float16") == ck.file_bytes(shape, "int8") == 308
+    assert ck.storage_of(shape, 308) == "int8"
+    assert ck.storage_of(shape, ck.file_bytes(shape, "float32")) == "float32"
+
+
 def test_packed_storages_need_whole_groups_and_aligned_ends(ck):
     """a packed storage holds only rows of whole groups (int6: 32, ternary and binary: 128), and tensors whose bytes
     end on 4 (dtypes.py:81-85: an odd number of float16 scales would leave the next tensor on 2)"""

@@ -911,6 +911,8 @@ def test_matmuls_relaxed(pkg, arena, oracle, tokens, n):
             wants.append((out + t * os_, full, f"{kind} token {t}"))
             wants.append((scratch + t * 2 * n, q.view(np.int8), f"{kind} xq of token {t}"))
             wants.append((scratch + t * 2 * n + n, s, f"{kind} xs of token {t}"))
+    # a job of no rows whose a / b are 0 (of another n, too): passed over, nothing readied into it
+    table.insert(1, jobs.job("matmul_q8r", 0, 0, 0, 0, 0, 0, 2 * n, rows=0, count=tokens))
     L = pkg.library()
     assert jobs.matmuls(L, ax, 4 * n, table) == 0, L.hq_last_error_message()
     for addr, want, what in wants:

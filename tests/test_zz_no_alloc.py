@@ -1,13 +1,15 @@
 """hq_matmuls_static (the form of hq_matmuls that allocates nothing: the readied activations in the library's own
 static staging, not the jobs' a / b) against hq_matmuls on the same inputs, through the C-ABI, to the bit: two calls
 in a row, the second with a smaller input, every kind of job the staging serves (relaxed int8 with and without the
-caller's corrections, relaxed int6, plain int8, ternary), a prompt through the matrix-core tiles and a decode
-through the token kernels; and the refusal of inputs past the staging's 4 MiB."""
+caller's corrections, relaxed int6, plain int8, ternary, binary, llama.cpp's blocks, whose sums_x fills the staging
+frame's scale area), a prompt through the matrix-core tiles and a decode through the token kernels; and the refusal
+of inputs past the staging's 4 MiB."""
 import numpy as np
 import pytest
 
+import blocks_model as bm
 from gpu_util import Arena, first_difference, same_bits
-from streams import pack6, pack_ternary
+from streams import pack6, pack_binary, pack_ternary
 
 pytestmark = pytest.mark.gpu
 F = np.float32
@@ -25,8 +27,8 @@ def staged_frame(n):
     return -(-n // 256) * 256 + -(-(n // 2) // 256) * 256
 
 
-def phase_of(arena, oracle, rng, n, tokens, rows):
-    """jobs of five kinds over one input: (x on the device, [(job's numbers without outputs)], output sizes)"""
+def phase_of(pkg, arena, oracle, rng, n, tokens, rows):
+    """jobs of eight kinds over one input: (x on the device, [(job's numbers without outputs)], output sizes)"""
     ng = n // 32
     specs = []
     w8 = rng.integers(-128, 128, rows * n).astype(np.int8)
@@ -41,6 +43,15 @@ def phase_of(arena, oracle, rng, n, tokens, rows):
     codes = rng.integers(0, 3, rows * n).astype(np.uint8)
     halves = (np.abs(rng.standard_normal(rows * (n // 128))) * 0.01).astype(np.float16).view(np.uint16)
     specs.append(("matmul_t2r", arena.put(pack_ternary(codes)), arena.put(halves), 0))
+    signs = rng.integers(0, 2, rows * n).astype(np.uint8)
+    specs.append(("matmul_b1r", arena.put(pack_binary(signs, n)), arena.put(halves), 0))
+    # llama.cpp's blocks (IQ3_S: a grid, signs and a scale a 32; Q4_K: the minimums against the sums of 16), their
+    # tables made on the device from a codebooks row
+    tables = arena.alloc(34992)
+    assert pkg.load_kernels().sb_tables(tables, arena.put(bm.codebooks(rng))) == 34992
+    for t in (21, 12):
+        blocks = bm.random_blocks(rng, t, rows * (n // 256))
+        specs.append(("matmul_sbr", arena.put(blocks), tables, t))
     x = rng.standard_normal((tokens, n)).astype(F)
     return arena.put(x), specs
 
@@ -74,10 +85,10 @@ def test_static_staging_is_hq_matmuls(pkg, arena, oracle):
     # a prompt (the matrix-core tiles; the plain kind in slices of four tokens), then a smaller decode
     for n, tokens, rows in ((2048, 20, 200), (1024, 3, 70)):
         arena.reset()
-        ax, specs = phase_of(arena, oracle, rng, n, tokens, rows)
+        ax, specs = phase_of(pkg, arena, oracle, rng, n, tokens, rows)
         want, got = run_both(pkg, arena, ax, specs, n, tokens, rows)
         for (kind, _, _, wc), w, g in zip(specs, want, got):
-            assert same_bits(g, w), f"n {n} tokens {tokens} {kind} wc {bool(wc)}: {first_difference(g, w)}"
+            assert same_bits(g, w), f"n {n} tokens {tokens} {kind} a6 {wc}: {first_difference(g, w)}"
         # and the first job against the oracle, so that the two agreeing is not two wrong numbers
         x = arena.get(ax, F, tokens * n).reshape(tokens, n)
         w8 = arena.get(specs[0][1], np.int8, rows * n)
@@ -110,7 +121,7 @@ def test_static_staging_under_graph_capture(pkg, arena, oracle):
     rng = np.random.default_rng(78)
     n, tokens, rows = 1024, 2, 96
     arena.reset()
-    ax, specs = phase_of(arena, oracle, rng, n, tokens, rows)
+    ax, specs = phase_of(pkg, arena, oracle, rng, n, tokens, rows)
     os_ = 4 * rows
     outs = [arena.alloc(os_ * tokens) for _ in specs]
     table = jobs.table([jobs.job(kind, o, 0, 0, wq, ws, wc, n, rows=rows, count=tokens, os=os_)
