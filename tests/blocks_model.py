@@ -47,8 +47,27 @@ def grids(row):
     return g
 
 
+def ieee_half(bits):
+    """float16 bits -> float32 as NumPy (and the converter, superblocks.py:34-36) widen them: infinities and NaNs kept"""
+    return np.asarray(bits).astype("<u2").view("<f2").astype(F32)
+
+
+def kernel_half(bits):
+    """float16 bits -> float32 as the kernels widen a block's scales (kernels/blocks/row.ts:3-15 through
+    kernels/kernel/halves.ts:20-23): the half sign-extended, shifted left 13, ANDed with 0x8fffffff, as a float32,
+    times 2^112 (one float32 product).  Exact for every finite half; an infinity reads as 65536 and a NaN as a finite
+    number."""
+    b = np.asarray(bits).astype(np.int64) & 0xFFFF
+    extended = (b ^ 0x8000) - 0x8000
+    moved = ((extended << 13) & 0x8FFFFFFF).astype(np.uint32).view(F32)
+    return (moved * F32(2.0 ** 112)).astype(F32)
+
+
+HALF = ieee_half  # how read_ints widens a block's float16 scales (tests set kernel_half to model the kernels)
+
+
 def halves(raw):
-    return np.ascontiguousarray(raw).view("<f2").astype(F32).reshape(-1)
+    return HALF(np.ascontiguousarray(raw).view("<u2").reshape(-1))
 
 
 def u16(raw):
@@ -142,7 +161,7 @@ def read_ints(t, b, g):
     elif t == 29:  # IQ1_M: qs[32] qh[16] 4 words; d the words' top four bits; a nibble of qh a 8 (its top: the shift)
         held = u16(b[:, 48:56].copy()).reshape(N, 4)
         dbits = (held[:, 0] >> 12) | ((held[:, 1] >> 8) & 0xF0) | ((held[:, 2] >> 4) & 0xF00) | (held[:, 3] & 0xF000)
-        d = dbits.astype("<u2").view("<f2").astype(F32)
+        d = HALF(dbits)
         four = np.stack([b[:, 32:48] & 15, b[:, 32:48] >> 4], axis=2).reshape(N, 32).astype(np.int64)
         index = b[:, :32].astype(np.int64) | ((four & 7) << 8)
         grid = g["IQ1S"][index].reshape(N, 32, 8)

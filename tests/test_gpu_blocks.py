@@ -1,6 +1,8 @@
 """llama.cpp's blocks of 256 weights on the GPU (kernels/blocks/): every kernel through the C-ABI, bit for bit against
-the oracle (oracle/oracle.c, pinned in test_oracle.py against a model of the converter's readers), for all ten types,
-with random codebooks and random blocks of sane scales (tests/blocks_model.py)."""
+the oracle (oracle/oracle.c, pinned in test_oracle.py against a model of the converter's readers, and in
+test_blocks_digests.py to the reference's own digests of what its readers read), for all ten types, with random
+codebooks and random blocks of sane scales (tests/blocks_model.py), and the reader on the digests' blocks with
+llama.cpp's codebooks."""
 import numpy as np
 import pytest
 
@@ -88,6 +90,29 @@ def test_sb_row(k, arena, oracle, setup, name, t):
         got = arena.get(out, F, n)
         want = oracle.sb_row(blocks.reshape(-1), tab, n, t)
         assert same_bits(got, want), f"{name} tiny {tiny}: {first_difference(got, want)}"
+
+
+@pytest.mark.parametrize("name,t", TYPES)
+def test_sb_row_on_the_references_digest_blocks(k, arena, oracle, name, t):
+    """the reference's golden vectors (tests/fixtures/superblocks.json "read"; test_blocks_digests.py): the GPU's
+    reader on the digests' 2000 SHAKE-256 blocks with llama.cpp's codebooks (tables made on the device) is the
+    oracle's to the bit, and gives the reference's digest wherever the kernels' and the converter's widening of the
+    float16 scales agree (every block whose scales are finite)"""
+    from test_blocks_digests import BLOCKS, DIGESTS, codebooks, digest, model_floats, shake_blocks
+    row = codebooks()
+    area = put_tables(k, arena, row)
+    blocks = shake_blocks(name)
+    n = 256 * BLOCKS
+    w = arena.alloc(blocks.size + 2) + 2  # 2 bytes into a word
+    arena.write(w, blocks)
+    out = arena.alloc(4 * n)
+    k.sb_row(out, w, area, n, t)
+    got = arena.get(out, F, n)
+    want = oracle.sb_row(blocks.reshape(-1), oracle.sb_tables(row), n, t)
+    assert same_bits(got, want), f"{name}: {first_difference(got, want)}"
+    ieee, kernel = model_floats(name, row, bm.ieee_half), model_floats(name, row, bm.kernel_half)
+    same = (np.nan_to_num(ieee, nan=0.0).view(np.uint32) == kernel.view(np.uint32)).reshape(BLOCKS, 256).all(1)
+    assert digest(np.where(np.repeat(same, 256), got, ieee)) == DIGESTS[name]
 
 
 @pytest.mark.parametrize("name,t", TYPES)
