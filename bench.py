@@ -2,7 +2,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-gemm] [--no-configs] [--configs]
                     [--mode phase|matmuls]
-    python bench.py --profile gemm|gemv|gemv_m4   (one workload's launches alone, for rocprofv3's counters)
+    python bench.py --profile gemm|gemm_wc|gemm_tol|gemv|gemv_m4   (one workload's launches alone, for rocprofv3's counters)
     python bench.py --calibrate     (kernels of known traffic, for scaling rocprofv3's FETCH_SIZE / WRITE_SIZE)
 
 A step is one decode token of the Llama-3-8B-shaped Q8 path: per layer the reference's
@@ -575,14 +575,23 @@ def gemm_workload(torch, pkg):
         pkg.check(lib.hq_quantize_x_batch(buf.data_ptr(), buf.data_ptr() + n, x.data_ptr(), n, 64, M, frame, 4 * n, None))
         acts[n] = (buf, frame)
     outs = [torch.empty(M, r, dtype=torch.float32, device="cuda:0") for r, _ in shapes]
+    # the tolerance form's workspace (the activations widened to float16, the scales regrouped), one for the layer's
+    # calls, which follow each other on the null stream
+    need = max(lib.hq_tol_work_bytes(n, M) for n in (HIDDEN, FFN))
+    work = torch.empty(need + 256, dtype=torch.uint8, device="cuda:0")
+    wptr = (work.data_ptr() + 255) // 256 * 256
 
-    def run(with_wc):
+    def run(with_wc, tol=False):
         for m, o in zip(mats, outs):
             buf, frame = acts[m.n]
-            lib.hq_matmul_q8r_tile_ex(o.data_ptr(), buf.data_ptr(), buf.data_ptr() + m.n, m.w.data_ptr(),
-                                      m.ws.data_ptr(), m.wc.data_ptr() if with_wc else None, m.n, 0, m.rows, M,
-                                      4 * m.rows, frame, None)
-    run.keep = (mats, acts, outs)
+            if tol:
+                lib.hq_matmul_q8r_tile_tol_ex(o.data_ptr(), buf.data_ptr(), buf.data_ptr() + m.n, m.w.data_ptr(),
+                                              m.ws.data_ptr(), m.n, 0, m.rows, M, 4 * m.rows, frame, wptr, need, None)
+            else:
+                lib.hq_matmul_q8r_tile_ex(o.data_ptr(), buf.data_ptr(), buf.data_ptr() + m.n, m.w.data_ptr(),
+                                          m.ws.data_ptr(), m.wc.data_ptr() if with_wc else None, m.n, 0, m.rows, M,
+                                          4 * m.rows, frame, None)
+    run.keep = (mats, acts, outs, work)
     return run, len(shapes), sum(2.0 * M * r * n for r, n in shapes)
 
 
@@ -591,31 +600,44 @@ def measure_gemm(torch, pkg, args):
     median round's rate: one round alone varies by several per cent)"""
     lib = pkg.library()
     run, _, ops = gemm_workload(torch, pkg)
-    times = {False: [], True: []}
-    for with_wc in (False, True):
-        run(with_wc)
+    forms = {"exact": lambda: run(False), "exact_with_wc": lambda: run(True), "tolerance": lambda: run(False, True)}
+    times = {k: [] for k in forms}
+    for f in forms.values():
+        f()
     pkg.check(lib.hq_last_error())
     torch.cuda.synchronize()
+    # the tolerance form's outputs against the bit-exact tile's (the reference's numbers), matrix by matrix
+    mats, _, outs, _ = run.keep
+    run(False)
+    exact = [o.clone() for o in outs]
+    run(False, True)
+    torch.cuda.synchronize()
+    worst = max(float((o - e).abs().max() / e.abs().max()) for o, e in zip(outs, exact))
     reps = max(5, args.steps)
     for _ in range(5):
-        for with_wc in (False, True):
+        for name, f in forms.items():
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
             for _ in range(reps):
-                run(with_wc)
+                f()
             e1.record()
             torch.cuda.synchronize()
-            times[with_wc].append(e0.elapsed_time(e1) * 1e-3 / reps)
+            times[name].append(e0.elapsed_time(e1) * 1e-3 / reps)
     pkg.check(lib.hq_last_error())
     out = {"M": 2048}
-    for with_wc in (False, True):
-        s = sorted(times[with_wc])[2]
+    for name in forms:
+        s = sorted(times[name])[2]
         r = {"tops": round(ops / s / 1e12, 1), "frac": round(ops / s / 1e12 / INT8_PEAK_TOPS, 4),
-             "ms_per_layer": round(s * 1e3, 4), "best_tops": round(ops / min(times[with_wc]) / 1e12, 1)}
-        if with_wc:
+             "ms_per_layer": round(s * 1e3, 4), "best_tops": round(ops / min(times[name]) / 1e12, 1)}
+        if name == "exact":
+            out.update(r)
+        elif name == "exact_with_wc":
             out["with_wc"] = r
         else:
-            out.update(r)
+            r.update({"kernel": "gemm_tol (float16-operand MFMA, one fused multiply-add a group; its activation "
+                                "widening included)",
+                      "max_err_over_max_y": worst, "bound": 1e-5})
+            out["tolerance"] = r
     return out
 
 
@@ -758,15 +780,16 @@ def profile(torch, pkg, args):
     for rocprofv3's counters (a counter pass serialises the dispatches):
       gemm     config 3's prefill, M = 2048 through one layer's 7 matrices, corrections derived (gemm_relaxed)
       gemm_wc  the same with the caller's corrections (int8_sums')
+      gemm_tol the same in the tolerance form (tol_prepare_x / _s, then gemm_tol)
       gemv     one decode step's products at M = 1 (129 hq_phase launches of gemv_relaxed<8,1,...>)
       gemv_m4  the same at M = 4 (gemv_relaxed<8,4,...>)
     Prints one JSON line naming what ran."""
     from pyodide_llm_amd import jobs
     lib = pkg.library()
-    if args.profile in ("gemm", "gemm_wc"):
+    if args.profile in ("gemm", "gemm_wc", "gemm_tol"):
         run, launches, _ = gemm_workload(torch, pkg)
         for _ in range(args.warmup + args.steps):
-            run(args.profile == "gemm_wc")
+            run(args.profile == "gemm_wc", args.profile == "gemm_tol")
     else:
         layers, head, phases = build_decode(torch, jobs, lib)
         if args.profile == "gemv":
@@ -802,7 +825,7 @@ def main():
     ap.add_argument("--configs", action="store_true",
                     help="also measure binary weights at config 4's shapes, llama.cpp's blocks and the outlier "
                          "channels")
-    ap.add_argument("--profile", choices=("gemm", "gemm_wc", "gemv", "gemv_m4"),
+    ap.add_argument("--profile", choices=("gemm", "gemm_wc", "gemm_tol", "gemv", "gemv_m4"),
                     help="only run one workload's launches, for rocprofv3's counters")
     ap.add_argument("--calibrate", action="store_true",
                     help="only run kernels of known traffic (for scaling rocprofv3's FETCH_SIZE / WRITE_SIZE)")

@@ -259,6 +259,22 @@ int32_t hq_matmuls(const void *x, int32_t x_stride, const double *jobs, int32_t 
 int32_t hq_matmuls_static(const void *x, int32_t x_stride, const double *jobs, int32_t count, int32_t stride,
                           void *stream);
 
+/* matmul_q8r_tile's products (src/runtime/forward/engine.ts's prompt blocks; kernels/relaxed/int8.ts:52-166) to the
+ * north star's float32 tolerance instead of to the bit, for prompts on the matrix cores: xout + t os row i (i in
+ * [r0, r1), t < count) = sum over the groups g of f(ws[i][g] xs_t[g]) * d_g, with d_g = sum_k w[i][k] (q_t[k] - 64)
+ * exact (the corrections int8_sums gives, made from the weights: there is no wc argument) and the groups added in an
+ * order of this library's, each term one fused multiply-add.  Every output is within 1e-5 max|y| of the reference's
+ * (max over the matrix's outputs; tests/tile-bench.ts:34-41's LINE), and equal to it where every term and sum is
+ * exact.  Arguments as hq_matmul_q8r_tile_ex's (xq and xs of token t at + t frame; xq, wq 16-byte aligned), plus a
+ * device workspace of at least hq_tol_work_bytes(n, count) bytes, 256-byte aligned, that the call writes (the
+ * activations widened to float16 and the scales regrouped) before its tiles read it: calls that share a workspace
+ * on one stream follow each other, on two streams they race.  Its counterpart in the reference: none (its prompt
+ * tile is the bit-exact matmul_q8r_tile). */
+int64_t hq_tol_work_bytes(int32_t n, int32_t count);
+int32_t hq_matmul_q8r_tile_tol_ex(void *xout, const void *xq, const void *xs, const void *wq, const void *ws,
+                                  int32_t n, int32_t r0, int32_t r1, int32_t count, int32_t os, int32_t frame,
+                                  void *work, int64_t work_bytes, void *stream);
+
 /* Which kernels take a job of `kind` (hq_phase's numbers), row length n and `count` tokens whose activations are
  * frame bytes apart and their scales sframe: 1 the matrix-core tile (16 tokens or more, and every offset within a
  * tile of 64 tokens, 128 for llama.cpp's blocks, and of 128 rows below 4 GiB), 0 the token kernel (4 tokens a

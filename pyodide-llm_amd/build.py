@@ -20,7 +20,7 @@ CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 OBJ = os.path.join(HERE, "_build")
 LIBRARY = os.path.join(HERE, "libhq.so")
-SOURCES = ["quantize.hip", "gemv.hip", "gemm.hip", "blocks.hip", "columns.hip", "ceilings.hip", "abi.cpp"]
+SOURCES = ["quantize.hip", "gemv.hip", "gemm.hip", "gemm_tol.hip", "blocks.hip", "columns.hip", "ceilings.hip", "abi.cpp"]
 # blocks.hip's prompt tile keeps its matrix-core results in ordinary VGPRs (no copies out of AGPRs: it has registers
 # to spare and reads every result on the VALU)
 EXTRA = {"blocks.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}

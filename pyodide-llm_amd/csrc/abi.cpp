@@ -411,6 +411,34 @@ int32_t hq_matmul_q8r_tile_ex(void *xout, const void *xq, const void *xs, const 
                               int32_t frame, void *stream) {
   return matmul(hq::Q8R, xout, xq, xs, wq, ws, wc, n, r0, r1, count, os, frame, 3, stream);
 }
+int64_t hq_tol_work_bytes(int32_t n, int32_t count) {
+  g_error = HQ_OK;
+  if (n <= 0 || n % 32 || count < 0) return fail(HQ_ERR_ARGUMENT, "hq_tol_work_bytes: n = %d, count = %d", n, count), -1;
+  return hq::tol_work_bytes(n, count);
+}
+int32_t hq_matmul_q8r_tile_tol_ex(void *xout, const void *xq, const void *xs, const void *wq, const void *ws,
+                                  int32_t n, int32_t r0, int32_t r1, int32_t count, int32_t os, int32_t frame,
+                                  void *work, int64_t work_bytes, void *stream) {
+  g_error = HQ_OK;
+  const char *name = "hq_matmul_q8r_tile_tol_ex";
+  hq::Job j{(char *)xout, (const char *)xq, (const char *)xs, (const char *)wq, (const char *)ws, nullptr, n, r0, r1,
+            count, os, frame, frame};
+  if (int32_t st = check_job(hq::Q8R, j, 3)) return st;
+  if (j.r1 == j.r0 || j.count == 0) return HQ_OK;
+  if (!aligned(xs, 4) || !aligned(ws, 4)) return fail(HQ_ERR_ALIGNMENT, "%s: xs or ws not 4-byte aligned", name);
+  if (!work) return fail(HQ_ERR_NULL, "%s: work is NULL", name);
+  if (!aligned(work, 256)) return fail(HQ_ERR_ALIGNMENT, "%s: work not 256-byte aligned", name);
+  const int64_t need = hq::tol_work_bytes(n, count);
+  if (work_bytes < need)
+    return fail(HQ_ERR_ARGUMENT, "%s: a workspace of %lld bytes (n = %d, %d tokens need %lld)", name,
+                (long long)work_bytes, n, count, (long long)need);
+  // a tile's loads keep 32-bit offsets from its first row and token: 128 rows of n bytes, 128 tokens of 2 n bytes,
+  // and the scales' n / 32 groups x count words
+  if ((int64_t)n * 256 >= ((int64_t)1 << 32) || (int64_t)(n / 32) * (count + 3) * 4 >= ((int64_t)1 << 32))
+    return fail(HQ_ERR_ARGUMENT, "%s: n = %d with %d tokens is past the tiles' 32-bit offsets", name, n, count);
+  if (int32_t st = ensure_device()) return st;
+  return hip_status(hq::launch_gemm_tol(j, (char *)work, stream_of(stream)), name);
+}
 int32_t hq_matmul_q6r_ex(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, const void *wc,
                          int32_t n, int32_t r0, int32_t r1, void *stream) {
   return matmul(hq::Q6R, xout, xq, xs, wq, ws, wc, n, r0, r1, 1, 0, 0, 3, stream);

@@ -96,6 +96,11 @@ hipError_t launch_take_channels(float *picked, float *x, const Channels &ch, hip
 // matmul_t2r_tile over a prompt.  Returns hipErrorNotSupported for a kind that has none.
 hipError_t launch_gemm(Kind kind, const Job &job, hipStream_t s);
 
+// the relaxed int8 prompt tile to float32 tolerance (gemm_tol.hip): the job's activations widened into `work`
+// (tol_work_bytes(n, count) bytes, 256-byte aligned), then the tiles; job.wc is not read (corrections derived)
+int64_t tol_work_bytes(int32_t n, int32_t count);
+hipError_t launch_gemm_tol(const Job &job, char *work, hipStream_t s);
+
 // the ceilings (ceilings.hip): every byte of [p, p + bytes) read once; `iterations` x 8 MFMAs a wave of `blocks`
 // blocks of 4 waves.  sink: 256 words that are almost never written
 hipError_t launch_ceiling_read(const char *p, int64_t bytes, uint32_t *sink, hipStream_t s);

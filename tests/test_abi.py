@@ -210,3 +210,23 @@ def test_matmuls_passes_over_jobs_of_no_rows(pkg):
     other = jobs.job("matmul_t2r", 0, 0, 0, 0, 0, 0, 4096, rows=0, count=1)
     assert jobs.matmuls(L, 0, 0, [empty, other]) == 0, L.hq_last_error_message()
     assert L.hq_matmuls_static(0, 0, jobs.table([empty]), 1, jobs.JOB, None) == 0, L.hq_last_error_message()
+
+
+def test_tolerance_tile_refusals_on_host(pkg):
+    """hq_matmul_q8r_tile_tol_ex checks its workspace (size, alignment, NULL) and the job before any device work;
+    hq_tol_work_bytes is the float16 activations (2 n a token, to 256 bytes) and the scales (n / 32 groups x the
+    tokens to a multiple of 4, 4 bytes each)"""
+    L = pkg.library()
+    assert L.hq_tol_work_bytes(4096, 2048) == 2 * 4096 * 2048 + 128 * 2048 * 4
+    assert L.hq_tol_work_bytes(288, 37) == ((2 * 288 * 37 + 255) // 256) * 256 + 9 * 40 * 4
+    assert L.hq_tol_work_bytes(100, 4) == -1 and L.hq_last_error() == pkg.HQ_ERR_ARGUMENT
+    n, count, need = 1024, 20, L.hq_tol_work_bytes(1024, 20)
+    args = (4096, 8192, 8192 + n, 65536, 1 << 20, n, 0, 64, count, 256, 2048)
+    assert L.hq_matmul_q8r_tile_tol_ex(*args, 1 << 24, need - 1, None) == pkg.HQ_ERR_ARGUMENT
+    assert "workspace" in L.hq_last_error_message().decode()
+    assert L.hq_matmul_q8r_tile_tol_ex(*args, (1 << 24) + 128, need, None) == pkg.HQ_ERR_ALIGNMENT
+    assert L.hq_matmul_q8r_tile_tol_ex(*args, None, need, None) == pkg.HQ_ERR_NULL
+    assert L.hq_matmul_q8r_tile_tol_ex(4096, 8192, 8192, 65536, 1 << 20, 100, 0, 64, count, 256, 2048,
+                                       1 << 24, need, None) == pkg.HQ_ERR_ARGUMENT
+    assert L.hq_matmul_q8r_tile_tol_ex(None, None, None, None, None, n, 5, 5, count, 256, 2048, None, 0, None) == 0
+    L.hq_clear_error()
