@@ -187,12 +187,26 @@ def measure_decode(torch, pkg, args, phases, matmuls, with_wc, by_phase=True):
         kinds = {}
         if by_phase:  # each kind of phase on its own (a graph of at least 32 launches)
             names = [PHASE_NAMES[i % 4] if i < 4 * LAYERS else "lm_head" for i in range(len(tables))]
+            # the read ceiling on the same bytes: hq_ceiling_read over slices of one launch's bytes of the phase,
+            # taken in turn from a 2 GiB buffer (several times the 256 MB Infinity Cache), a graph of 32 launches
+            big = torch.empty(2 << 30, dtype=torch.uint8, device="cuda:0")
+            sink = torch.zeros(256, dtype=torch.int32, device="cuda:0")
             for name in PHASE_NAMES:
                 mine = [t for t, nm in zip(tables, names) if nm == name]
                 mine = mine * -(-32 // len(mine))
                 s = products(mine)
+                size = int(sum(t[3] for t in mine) / len(mine)) // 16 * 16
+                slices = big.numel() // size
+
+                def reads(h, size=size, slices=slices):
+                    for i in range(32):
+                        lib.hq_ceiling_read(big.data_ptr() + (i % slices) * size, size, sink.data_ptr(), h)
+                ceiling = _graph_time_median(torch, reads, max(5, args.steps)) / 32
                 kinds[name] = {"us": round(1e6 * s / len(mine), 2),
-                               "GBps": round(sum(t[3] for t in mine) / s / 1e9, 1)}
+                               "GBps": round(sum(t[3] for t in mine) / s / 1e9, 1),
+                               "read_ceiling_us": round(1e6 * ceiling, 2),
+                               "of_read_ceiling": round(s / len(mine) / ceiling, 3)}
+            del big
         pkg.check(lib.hq_last_error())
         pkg.check(lib.hq_set_stream(None))
     out["ms_per_step"] = 1e3 * graph_s
@@ -723,7 +737,8 @@ def cpu_baseline(args, gemv_seconds=8.0, tile_seconds=6.0):
 
 def measure_ceilings(torch, pkg):
     """The measured ceilings beside the nominal peaks: hq_ceiling_read over 512 MB buffers taken in turn (2 GB in
-    all, past the 256 MB Infinity Cache; a graph of 16 launches), and hq_ceiling_mfma (registers only, 8 blocks a CU)."""
+    all, past the 256 MB Infinity Cache; a graph of 16 launches), hq_ceiling_mfma (registers only, 8 blocks a CU),
+    and hq_ceiling_epilogue's two forms (the prompt tiles' register work, 2 blocks a CU as the tiles run)."""
     lib = pkg.library()
     sink = torch.zeros(256, dtype=torch.int32, device="cuda:0")
     size = 512 << 20
@@ -742,8 +757,16 @@ def measure_ceilings(torch, pkg):
         pkg.check(lib.hq_ceiling_mfma(blocks, iters, sink.data_ptr(), h))
     mfma_s = _graph_time(torch, mfmas, 3)
     ops = blocks * 4 * iters * 8 * 32768 * 2
+    # the prompt tiles' epilogues on registers, two waves a SIMD (2 blocks a CU)
+    eblocks, eiters = 2 * cus, 4000
+    epilogue = {}
+    for form, name in ((0, "epilogue_exact_TOPS"), (1, "epilogue_tolerance_TOPS")):
+        def work(h, form=form):
+            pkg.check(lib.hq_ceiling_epilogue(form, eblocks, eiters, sink.data_ptr(), h))
+        es = _graph_time_median(torch, work, 3)
+        epilogue[name] = round(eblocks * 4 * eiters * 262144 / es / 1e12, 1)
     return {"read_GBps": round(size / read_s / 1e9, 1), "read_bytes": size,
-            "mfma_int8_TOPS": round(ops / mfma_s / 1e12, 1)}
+            "mfma_int8_TOPS": round(ops / mfma_s / 1e12, 1), **epilogue}
 
 
 def calibrate():

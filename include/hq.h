@@ -289,6 +289,13 @@ int32_t hq_job_path(int32_t kind, int32_t n, int32_t count, int64_t frame, int64
  * written. */
 int32_t hq_ceiling_read(const void *p, int64_t bytes, void *sink, void *stream);
 int32_t hq_ceiling_mfma(int32_t blocks, int32_t iterations, void *sink, void *stream);
+/* The prompt tiles' register work alone (no loads, no LDS), two waves a SIMD: form 0 the bit-exact tile's epilogue
+ * (a correction MFMA, the scales' f32 outer product, the int8 MFMAs, and convert, multiply, add an output), form 1
+ * the tolerance tile's (the weights' float16 widening, the float16 MFMAs, the outer product, a fused multiply-add an
+ * output); `iterations` groups of a wave's four 32 x 32 sub-tiles (262 144 operations) a wave of `blocks` blocks of
+ * 4 waves.
+ * The most a tile of that epilogue can give; no counterpart in the reference. */
+int32_t hq_ceiling_epilogue(int32_t form, int32_t blocks, int32_t iterations, void *sink, void *stream);
 
 #ifdef __cplusplus
 }

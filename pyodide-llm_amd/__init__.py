@@ -111,6 +111,7 @@ OWN_SIGNATURES = {
     "hq_matmul_q8r_tile_tol_ex": ([p, p, p, p, p, i32, i32, i32, i32, i32, i32, p, ctypes.c_int64, p], i32),
     "hq_ceiling_read": ([p, ctypes.c_int64, p, p], i32),
     "hq_ceiling_mfma": ([i32, i32, p, p], i32),
+    "hq_ceiling_epilogue": ([i32, i32, i32, p, p], i32),
 }
 
 _lib = None

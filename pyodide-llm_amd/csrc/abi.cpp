@@ -785,6 +785,16 @@ int32_t hq_ceiling_mfma(int32_t blocks, int32_t iterations, void *sink, void *st
   return hip_status(hq::launch_ceiling_mfma(blocks, iterations, (int32_t *)sink, stream_of(stream)), "ceiling_mfma");
 }
 
+int32_t hq_ceiling_epilogue(int32_t form, int32_t blocks, int32_t iterations, void *sink, void *stream) {
+  g_error = HQ_OK;
+  if (form < 0 || form > 1 || blocks <= 0 || iterations <= 0)
+    return fail(HQ_ERR_ARGUMENT, "hq_ceiling_epilogue: form %d, %d blocks, %d iterations", form, blocks, iterations);
+  if (!sink || !aligned(sink, 4)) return fail(HQ_ERR_NULL, "hq_ceiling_epilogue: sink");
+  if (int32_t st = ensure_device()) return st;
+  return hip_status(hq::launch_ceiling_epilogue(form, blocks, iterations, (int32_t *)sink, stream_of(stream)),
+                    "ceiling_epilogue");
+}
+
 // ---- the drop-in names: the library's stream, errors kept for hq_last_error() ---------------------------------
 void quantize_x(void *xq, void *xs, const void *x, int32_t n, int32_t bias) {
   hq_quantize_x_ex(xq, xs, x, n, bias, g_stream.load());

@@ -105,6 +105,9 @@ hipError_t launch_gemm_tol(const Job &job, char *work, hipStream_t s);
 // blocks of 4 waves.  sink: 256 words that are almost never written
 hipError_t launch_ceiling_read(const char *p, int64_t bytes, uint32_t *sink, hipStream_t s);
 hipError_t launch_ceiling_mfma(int32_t blocks, int32_t iterations, int32_t *sink, hipStream_t s);
+// the prompt tiles' register work (form 0 the bit-exact tile's, 1 the tolerance tile's): `iterations` groups of a
+// wave's four 32 x 32 sub-tiles a wave of `blocks` blocks of 4 waves
+hipError_t launch_ceiling_epilogue(int32_t form, int32_t blocks, int32_t iterations, int32_t *sink, hipStream_t s);
 
 // which path a job of `count` tokens takes
 constexpr int kGemvMaxTokens = 4;
