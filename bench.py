@@ -3,6 +3,7 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-gemm] [--no-configs] [--configs]
                     [--mode phase|matmuls]
     python bench.py --profile gemm|gemm_wc|gemm_tol|gemv|gemv_m4   (one workload's launches alone, for rocprofv3's counters)
+    python bench.py --profile blocks_decode|blocks_prompt [--block-type Q4_K]   (llama.cpp's blocks, the same way)
     python bench.py --calibrate     (kernels of known traffic, for scaling rocprofv3's FETCH_SIZE / WRITE_SIZE)
 
 A step is one decode token of the Llama-3-8B-shaped Q8 path: per layer the reference's
@@ -482,31 +483,31 @@ def measure_outliers(torch, pkg, args, gen):
 BLOCK_SCALES = {10: (80, 82), 12: (0, 2), 16: (0,), 17: (0,), 18: (0,), 19: (0,), 21: (0,), 22: (0,), 23: (0,)}
 
 
-def measure_blocks(torch, pkg, args, gen):
-    """llama.cpp's blocks (job kinds 10-12) at Llama-3-8B's MLP shapes: the token product (M = 1; copies of the
-    weights past the Infinity Cache) in GB/s of algorithmic bytes (the blocks, the activations and the sums of 16
-    or 8 the type reads, the outputs) and prompts of 64 and 512 tokens in TOPS.  Random blocks (random bytes, sane
-    scales), random codebooks."""
-    from pyodide_llm_amd import jobs
-    lib = pkg.library()
-    dev = "cuda:0"
-    reps = max(3, args.steps // 2)
-    out = {}
-    tab = torch.empty(34992, dtype=torch.uint8, device=dev)
-    books = torch.randint(0, 256, (33808,), dtype=torch.uint8, device=dev, generator=gen)
-    pkg.check(lib.hq_sb_tables_ex(tab.data_ptr(), books.data_ptr(), None))
+class BlocksWorkload:
+    """llama.cpp's blocks (job kinds 10-12) at Llama-3-8B's MLP shapes (gate, up [14336, 4096], down [4096, 14336]):
+    random blocks (random bytes, sane scales), random codebooks, activations quantized with their sums."""
+    SHAPES = [(14336, 4096), (14336, 4096), (4096, 14336)]
 
-    def acts(n, count=1):
-        x = torch.randn(count, n, device=dev, generator=gen)
+    def __init__(self, torch, pkg, gen):
+        self.torch, self.pkg, self.gen = torch, pkg, gen
+        self.lib = pkg.library()
+        self.dev = "cuda:0"
+        self.tab = torch.empty(34992, dtype=torch.uint8, device=self.dev)
+        books = torch.randint(0, 256, (33808,), dtype=torch.uint8, device=self.dev, generator=gen)
+        pkg.check(self.lib.hq_sb_tables_ex(self.tab.data_ptr(), books.data_ptr(), None))
+
+    def acts(self, n, count=1):
+        x = self.torch.randn(count, n, device=self.dev, generator=self.gen)
         frame = (n + n // 2 + 15) // 16 * 16
-        buf = torch.empty(count * frame, dtype=torch.uint8, device=dev)
-        pkg.check(lib.hq_quantize_x_batch(buf.data_ptr(), buf.data_ptr() + n, x.data_ptr(), n, 0, count, frame,
-                                          4 * n, None))
-        pkg.check(lib.hq_sums_x_batch(buf.data_ptr() + n, buf.data_ptr(), n, count, frame, None))
+        buf = self.torch.empty(count * frame, dtype=self.torch.uint8, device=self.dev)
+        self.pkg.check(self.lib.hq_quantize_x_batch(buf.data_ptr(), buf.data_ptr() + n, x.data_ptr(), n, 0, count,
+                                                    frame, 4 * n, None))
+        self.pkg.check(self.lib.hq_sums_x_batch(buf.data_ptr() + n, buf.data_ptr(), n, count, frame, None))
         return buf, frame
 
-    def weights(t, size, rows, n):
-        w = torch.randint(0, 256, (rows * (n // 256), size), dtype=torch.uint8, device=dev, generator=gen)
+    def weights(self, t, size, rows, n):
+        w = self.torch.randint(0, 256, (rows * (n // 256), size), dtype=self.torch.uint8, device=self.dev,
+                               generator=self.gen)
         for at in BLOCK_SCALES.get(t, ()):
             w[:, at], w[:, at + 1] = 0x00, 0x20
         if t == 29:  # 0x2000: the nibbles 0, 0, 0, 2 at the tops of the four words
@@ -514,55 +515,84 @@ def measure_blocks(torch, pkg, args, gen):
                 w[:, 49 + 2 * k] = (w[:, 49 + 2 * k] & 0x0F) | (nib << 4)
         return w
 
+    @staticmethod
     def act_bytes(t, n):
         """per token: xq, the scales, and the sums of 16 (the K types) or of 8 (IQ1)"""
         return n + n // 8 + (n // 8 if t in (10, 12) else n // 4 if t in (19, 29) else 0)
 
-    shapes = [(14336, 4096), (14336, 4096), (4096, 14336)]
-    for name, (t, size) in jobs.BLOCK_TYPES.items():
-        per_layer = sum(rows * (n // 256) * size for rows, n in shapes)
+    def decode(self, name):
+        """the token product (M = 1) of `copies` copies of one layer's MLP (together past the Infinity Cache), gate
+        and up in one phase, down in the next (their launches as the forward pass makes them).  Returns launch(h),
+        the launches a call, the copies and the algorithmic bytes a call (the blocks, the activations and sums the
+        type reads, the outputs)."""
+        from pyodide_llm_amd import jobs
+        t, size = jobs.BLOCK_TYPES[name]
+        per_layer = sum(rows * (n // 256) * size for rows, n in self.SHAPES)
         copies = max(2, -(-1_200_000_000 // per_layer))
-        a = {n: acts(n) for _, n in shapes}
+        a = {n: self.acts(n) for _, n in self.SHAPES}
         tables, total, keep = [], 0.0, []
         for _ in range(copies):
             entries = []
-            for rows, n in shapes:
-                w = weights(t, size, rows, n)
-                o = torch.empty(rows, device=dev)
+            for rows, n in self.SHAPES:
+                w = self.weights(t, size, rows, n)
+                o = self.torch.empty(rows, device=self.dev)
                 keep += [w, o]
                 buf, _ = a[n]
                 entries.append(jobs.job("matmul_sbr", o.data_ptr(), buf.data_ptr(), buf.data_ptr() + n, w.data_ptr(),
-                                        tab.data_ptr(), t, n, rows=rows))
-                total += rows * (n // 256) * size + act_bytes(t, n) + 4 * rows
-            # gate and up in one phase, down in the next (their launches as the forward pass makes them)
+                                        self.tab.data_ptr(), t, n, rows=rows))
+                total += rows * (n // 256) * size + self.act_bytes(t, n) + 4 * rows
             tables.append((jobs.table(entries[:2]), 2))
             tables.append((jobs.table(entries[2:]), 1))
+        lib = self.lib
 
-        def launch(h):
+        def launch(h, keep=keep, a=a):
             for tb, nj in tables:
                 lib.hq_phase(tb, nj, 16, h)
+        return launch, len(tables), copies, total
+
+    def prompt(self, name, count):
+        """a prompt of `count` tokens through one layer's MLP (one hq_phase of three jobs: the matrix-core tile).
+        Returns launch(h) and the operations a call."""
+        from pyodide_llm_amd import jobs
+        t, size = jobs.BLOCK_TYPES[name]
+        entries, keep = [], []
+        for rows, n in self.SHAPES:
+            w = self.weights(t, size, rows, n)
+            buf, frame = self.acts(n, count)
+            o = self.torch.empty(count, rows, device=self.dev)
+            keep += [w, buf, o]
+            entries.append(jobs.job("matmul_sbr", o.data_ptr(), buf.data_ptr(), buf.data_ptr() + n, w.data_ptr(),
+                                    self.tab.data_ptr(), t, n, rows=rows, count=count, os=4 * rows, as_=frame,
+                                    bs=frame))
+        tb = jobs.table(entries)
+        lib = self.lib
+
+        def launch(h, keep=keep):
+            lib.hq_phase(tb, len(entries), 16, h)
+        return launch, sum(2.0 * count * rows * n for rows, n in self.SHAPES)
+
+
+def measure_blocks(torch, pkg, args, gen, names=None, prompts=None):
+    """llama.cpp's blocks at Llama-3-8B's MLP shapes: the token product (M = 1) in GB/s of algorithmic bytes and
+    prompts of 64 and 512 tokens in TOPS, every block type (or `names`, prompts of `prompts` tokens)."""
+    from pyodide_llm_amd import jobs
+    lib = pkg.library()
+    reps = max(3, args.steps // 2)
+    out = {}
+    W = BlocksWorkload(torch, pkg, gen)
+    for name in names or jobs.BLOCK_TYPES:
+        launch, _, copies, total = W.decode(name)
         sec = _graph_time(torch, launch, reps)
         pkg.check(lib.hq_last_error())
         out[f"8B MLP {name} M=1 x {copies}"] = {"GBps": round(total / sec / 1e9, 1),
                                                   "us_per_layer": round(1e6 * sec / copies, 2), "bytes": total}
-        del keep, tables
-        # prompts of 64 and 512 tokens through one layer's MLP (the matrix-core tile)
-        for count in getattr(args, "block_prompts", (64, 512)):
-            entries, keep = [], []
-            for rows, n in shapes:
-                w = weights(t, size, rows, n)
-                buf, frame = acts(n, count)
-                o = torch.empty(count, rows, device=dev)
-                keep += [w, buf, o]
-                entries.append(jobs.job("matmul_sbr", o.data_ptr(), buf.data_ptr(), buf.data_ptr() + n,
-                                        w.data_ptr(), tab.data_ptr(), t, n, rows=rows, count=count, os=4 * rows,
-                                        as_=frame, bs=frame))
-            tb = jobs.table(entries)
-            ops = sum(2.0 * count * rows * n for rows, n in shapes)
-            sec = _graph_time(torch, lambda h: lib.hq_phase(tb, len(entries), 16, h), reps)
+        del launch
+        for count in prompts or getattr(args, "block_prompts", (64, 512)):
+            launch, ops = W.prompt(name, count)
+            sec = _graph_time(torch, launch, reps)
             pkg.check(lib.hq_last_error())
             out[f"8B MLP {name} prompt M={count}"] = {"TOPS": round(ops / sec / 1e12, 2), "ms": round(1e3 * sec, 3)}
-            del keep
+            del launch
             torch.cuda.empty_cache()
     return out
 
@@ -806,6 +836,8 @@ def profile(torch, pkg, args):
       gemm_tol the same in the tolerance form (tol_prepare_x / _s, then gemm_tol)
       gemv     one decode step's products at M = 1 (129 hq_phase launches of gemv_relaxed<8,1,...>)
       gemv_m4  the same at M = 4 (gemv_relaxed<8,4,...>)
+      blocks_decode  --block-type's token product at M = 1 through copies of Llama-3-8B's MLP (sb_gemv)
+      blocks_prompt  --block-type's prompt of 512 tokens through one layer's MLP (the matrix-core tile)
     Prints one JSON line naming what ran."""
     from pyodide_llm_amd import jobs
     lib = pkg.library()
@@ -813,6 +845,18 @@ def profile(torch, pkg, args):
         run, launches, _ = gemm_workload(torch, pkg)
         for _ in range(args.warmup + args.steps):
             run(args.profile == "gemm_wc", args.profile == "gemm_tol")
+    elif args.profile in ("blocks_decode", "blocks_prompt"):
+        gen = torch.Generator(device="cuda:0")
+        gen.manual_seed(12)
+        W = BlocksWorkload(torch, pkg, gen)
+        if args.profile == "blocks_decode":
+            launch, launches, _, _ = W.decode(args.block_type)
+        else:
+            launch, _ = W.prompt(args.block_type, 512)
+            launches = 1
+        torch.cuda.synchronize()
+        for _ in range(args.warmup + args.steps):
+            launch(None)
     else:
         layers, head, phases = build_decode(torch, jobs, lib)
         if args.profile == "gemv":
@@ -831,7 +875,10 @@ def profile(torch, pkg, args):
             products(None)
     torch.cuda.synchronize()
     pkg.check(lib.hq_last_error())
-    print(json.dumps({"profile": args.profile, "launches_per_step": launches, "steps": args.warmup + args.steps}))
+    line = {"profile": args.profile, "launches_per_step": launches, "steps": args.warmup + args.steps}
+    if args.profile.startswith("blocks"):
+        line["block_type"] = args.block_type
+    print(json.dumps(line))
 
 
 def main():
@@ -848,8 +895,11 @@ def main():
     ap.add_argument("--configs", action="store_true",
                     help="also measure binary weights at config 4's shapes, llama.cpp's blocks and the outlier "
                          "channels")
-    ap.add_argument("--profile", choices=("gemm", "gemm_wc", "gemm_tol", "gemv", "gemv_m4"),
+    ap.add_argument("--profile", choices=("gemm", "gemm_wc", "gemm_tol", "gemv", "gemv_m4", "blocks_decode",
+                                          "blocks_prompt"),
                     help="only run one workload's launches, for rocprofv3's counters")
+    ap.add_argument("--block-type", default="Q4_K",
+                    help="the llama.cpp block type of --profile blocks_decode / blocks_prompt (a BLOCK_TYPES name)")
     ap.add_argument("--calibrate", action="store_true",
                     help="only run kernels of known traffic (for scaling rocprofv3's FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
@@ -877,6 +927,12 @@ def main():
     torch.cuda.empty_cache()
     gemm = None if args.no_gemm else measure_gemm(torch, pkg, args)
     ceilings = measure_ceilings(torch, pkg)
+    # one llama.cpp block type (Q4_K, the type the reference's GPU path keeps) at the 8B MLP's shapes, decode and a
+    # prompt of 512 tokens (--configs: every type)
+    gen = torch.Generator(device="cuda:0")
+    gen.manual_seed(12)
+    blocks_q4k = measure_blocks(torch, pkg, args, gen, names=("Q4_K",), prompts=(512,))
+    torch.cuda.empty_cache()
     configs = None if args.no_configs else measure_configs(torch, pkg, args, extras=args.configs)
     cpu = None if args.no_cpu else cpu_baseline(args)
     headline = one_call if args.mode == "matmuls" else separate
@@ -897,7 +953,7 @@ def main():
         "cpu_baseline": cpu,
         "detail": {"quantize_then_phase": separate, "quantize_then_phase_with_wc": separate_wc,
                    "hq_matmuls": one_call, "decode_m4": decode_m4,
-                   "prefill_gemm": gemm, "ceilings": ceilings, "configs": configs},
+                   "prefill_gemm": gemm, "ceilings": ceilings, "blocks_q4k": blocks_q4k, "configs": configs},
     }
     print(json.dumps(line))
 
