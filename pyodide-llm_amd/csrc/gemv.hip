@@ -63,9 +63,10 @@ HQ_DEV void fill_acts(const Job &J, char *lq, float *ls) {
 constexpr int kRowsPerBlock = 16;
 // the relaxed kinds' blocks: 128 threads, 8 rows of 16 lanes or 4 of 32 (fewer rows a block: more blocks, a finer
 // balance of the last ones over the CUs; 8 rows of 16 measured faster than 16 rows at the 8B decode); 2..4 tokens
-// staged in LDS take 256 (one staged copy for twice the rows: M = 4's staged phases 5 % faster, 512 no better)
+// staged in LDS take 512 (one staged copy for four times the rows: the 8B decode's products at M = 4 2.02 ms with
+// 256 threads, 1.96 with 512; 1024 threads, whose waves get 128 registers, 2.26)
 constexpr int kRelaxedThreads = 128;
-HQ_HOST_DEV constexpr int relaxed_threads(int T, bool staged) { return T > 1 && staged ? 256 : kRelaxedThreads; }
+HQ_HOST_DEV constexpr int relaxed_threads(int T, bool staged) { return T > 1 && staged ? 512 : kRelaxedThreads; }
 // Lanes a relaxed row: 32 lanes give a launch twice the waves, each lane half the steps.  Measured phase by phase
 // streaming from HBM (configs 1-4's decode shapes, int8 and int6, 16 against 32 lanes): one int8 token, 32 lanes are
 // faster where a row is 4096 or 8192 bytes (8B q/k/v 7.7 -> 7.1 us, o 6.2 -> 5.8, gate+up 25.3 -> 23.5, lm-head 97 ->
