@@ -230,3 +230,16 @@ def test_tolerance_tile_refusals_on_host(pkg):
                                        1 << 24, need, None) == pkg.HQ_ERR_ARGUMENT
     assert L.hq_matmul_q8r_tile_tol_ex(None, None, None, None, None, n, 5, 5, count, 256, 2048, None, 0, None) == 0
     L.hq_clear_error()
+
+
+def test_ceiling_epilogue_refusals_on_host(pkg):
+    """hq_ceiling_epilogue takes form 0 (the bit-exact tile's epilogue) or 1 (the tolerance tile's), a positive grid
+    and iteration count, and an aligned sink, checked before any device work"""
+    L = pkg.library()
+    assert L.hq_ceiling_epilogue(2, 8, 8, 4096, None) == pkg.HQ_ERR_ARGUMENT
+    assert L.hq_ceiling_epilogue(-1, 8, 8, 4096, None) == pkg.HQ_ERR_ARGUMENT
+    assert L.hq_ceiling_epilogue(0, 0, 8, 4096, None) == pkg.HQ_ERR_ARGUMENT
+    assert L.hq_ceiling_epilogue(1, 8, 0, 4096, None) == pkg.HQ_ERR_ARGUMENT
+    assert L.hq_ceiling_epilogue(0, 8, 8, None, None) == pkg.HQ_ERR_NULL
+    assert L.hq_ceiling_epilogue(0, 8, 8, 4098, None) == pkg.HQ_ERR_NULL
+    L.hq_clear_error()

@@ -1014,3 +1014,12 @@ def test_ceiling_mfma_runs(pkg, arena):
     sink = arena.alloc(1024, fill=np.zeros(256, np.int32))
     assert L.hq_ceiling_mfma(4, 3, sink, None) == 0, L.hq_last_error_message()
     assert not arena.get(sink, np.int32, 256).any()
+
+
+@pytest.mark.parametrize("form", [0, 1])
+def test_ceiling_epilogue_runs(pkg, arena, form):
+    """both prompt-tile epilogues on registers (an odd number of groups, blocks of 4 waves) run and store nothing"""
+    L = pkg.library()
+    sink = arena.alloc(1024, fill=np.zeros(256, np.int32))
+    assert L.hq_ceiling_epilogue(form, 8, 7, sink, None) == 0, L.hq_last_error_message()
+    assert not arena.get(sink, np.int32, 256).any()
