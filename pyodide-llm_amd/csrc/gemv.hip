@@ -89,6 +89,13 @@ HQ_DEV uint4 ld16(const char *p) { return *(const uint4 *)p; }
 HQ_DEV uint2 ld8(const char *p) { return *(const uint2 *)p; }
 
 HQ_DEV uint4 ldw16(const char *p) { return *(const uint4 *)p; }
+// a weight load that is not kept in the caches (each weight byte is read once); for whole cache lines only: a line
+// read in halves by two such loads is fetched twice
+HQ_DEV uint4 ldw16_nt(const char *p) {
+  typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+  const u4v q = __builtin_nontemporal_load((const u4v *)p);
+  return make_uint4(q.x, q.y, q.z, q.w);
+}
 
 // the 32 weight bytes of group g of a row, as eight dwords of int8 (int6 groups widened, kernels/six.ts)
 template <int PACK>
@@ -141,10 +148,82 @@ struct RelaxedChunk {
   static constexpr bool LATE = T > 1 && SRC == STAGED;
   static constexpr int U = T == 1 ? 4 : (LATE || T == 2 ? 2 : 1);
   static constexpr int UX = LATE ? 1 : U;  // steps of activations a chunk holds (none read when LATE)
-  uint32_t w[U][8];
+  // One token of int8 (PAIRED): a step's weights are read as whole cache lines by non-temporal loads.  Lane j of a
+  // row takes the 16 bytes at 16 j of the step's first half (group j / 2's half j % 2) and at RL 16 + 16 j of its
+  // second (group RL / 2 + j / 2's), so that each load instruction reads a row's RL 16 contiguous bytes; a group's
+  // integer is its two halves' (lanes 2 i and 2 i + 1) added by a DPP swap.  Half-lines read by two loads would be
+  // fetched twice past the caches.
+  static constexpr bool PAIRED = T == 1 && SRC == GLOBAL && PACK == 8;
+  uint32_t w[U][8];   // PAIRED: w[u][0..3] the first half's 16 bytes, [4..7] the second's
   uint32_t x[UX][T][8];
-  float ws[U], xs[UX][T];
-  int32_t wc[U];
+  float ws[U], xs[UX][T];  // PAIRED: the scales (and wc the correction) of group 2 i's lane's own group: an even
+  int32_t wc[U];           // lane's of the first half, an odd lane's of the second (the pair swaps them by DPP)
+
+  // PAIRED: steps it0 .. it0 + U - 1, weights, activations and scales of the lane's two half-groups (a group past
+  // the row's fours: group 0's bytes, its term dropped)
+  // (wb, sb, cb: the wave's first row's weights, scales and corrections, the same in every lane; rb: the lane's row's
+  // byte offset from wb, gb its offset from sb and cb: every address a scalar base plus a 32-bit offset)
+  HQ_DEV void load_paired(const char *wb, const float *sb, const int32_t *cb, uint32_t rb, uint32_t gb,
+                          const ActSource<T, SRC> &A, int it0, int lane, int ng4) {
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int g0 = (it0 + u) * RL + (lane >> 1), g1 = g0 + RL / 2;
+      const uint32_t h = 16u * (uint32_t)(lane & 1);
+      const uint32_t c0 = (uint32_t)(g0 < ng4 ? g0 : 0), c1 = (uint32_t)(g1 < ng4 ? g1 : 0);
+      const uint4 a = ldw16_nt(wb + (rb + c0 * 32u + h)), b = ldw16_nt(wb + (rb + c1 * 32u + h));
+      w[u][0] = a.x; w[u][1] = a.y; w[u][2] = a.z; w[u][3] = a.w;
+      w[u][4] = b.x; w[u][5] = b.y; w[u][6] = b.z; w[u][7] = b.w;
+      const uint4 xa = ld16(A.xq[0] + (c0 * 32u + h)), xb = ld16(A.xq[0] + (c1 * 32u + h));
+      x[u][0][0] = xa.x; x[u][0][1] = xa.y; x[u][0][2] = xa.z; x[u][0][3] = xa.w;
+      x[u][0][4] = xb.x; x[u][0][5] = xb.y; x[u][0][6] = xb.z; x[u][0][7] = xb.w;
+      const uint32_t own = (lane & 1) ? c1 : c0;
+      ws[u] = *(const float *)((const char *)sb + (gb + own * 4u));
+      xs[u][0] = *(const float *)(A.xs[0] + own * 4u);
+      if (WC) wc[u] = *(const int32_t *)((const char *)cb + (gb + own * 4u));
+    }
+  }
+  // PAIRED: the chunk's terms folded into the chains: chain k of the reference (groups 4 j + k) lives in lane 2 k, and
+  // a step's groups k, k + 4, .. of its first half are lanes 2 k, 2 k + 8 (then 2 k + 16, 2 k + 24 of a 32-lane row,
+  // brought down by v_permlane16_swap), then the same of its second half (relaxed/int8.ts:26-39)
+  HQ_DEV void fold_paired(float acc[T], int it0, int lane, int ng4) const {
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int g0 = (it0 + u) * RL + (lane >> 1), g1 = g0 + RL / 2;
+      // an even lane's scale product of its first group, and (swapped in from the odd lane) of its second
+      const float sown = fmul(ws[u], xs[u][0]);
+      const float sc[2] = {sown, __int_as_float(swap_pair(__float_as_int(sown)))};
+      const int32_t cw[2] = {WC ? wc[u] : 0, WC ? swap_pair(wc[u]) : 0};
+      float q[2];
+#pragma unroll
+      for (int s2 = 0; s2 < 2; s2++) {
+        int32_t d = 0;
+        if (!WC) {
+          int32_t wsum = 0;
+#pragma unroll
+          for (int i = 0; i < 4; i++) wsum = sdot4((int32_t)w[u][4 * s2 + i], 0x01010101, wsum);
+          d = -64 * wsum;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) d = sdot4((int32_t)w[u][4 * s2 + i], (int32_t)x[u][0][4 * s2 + i], d);
+        d += swap_pair(d);  // the group's two halves (wrapping int32 adds, as the reference's i32x4.add)
+        if (WC) d += cw[s2];
+        const float p = fmul((float)d, sc[s2]);  // (an odd lane's terms are never read)
+        q[s2] = (s2 ? g1 : g0) < ng4 ? p : 0.0f;  // +0 leaves a lane as it is: a lane is never -0
+      }
+      float a = acc[0];
+#pragma unroll
+      for (int s2 = 0; s2 < 2; s2++) {
+        a = fadd(a, q[s2]);
+        a = fadd(a, from_lane_plus<8>(q[s2]));
+        if (RL == 32) {
+          const float qh = upper_row(q[s2]);
+          a = fadd(a, qh);
+          a = fadd(a, from_lane_plus<8>(qh));
+        }
+      }
+      acc[0] = a;
+    }
+  }
 
   // steps it0 .. it0 + U - 1 of this lane (its group RL it + lane of each; a lane past the row's fours reads group
   // 0 again, whose term it drops): the weights, their scales and corrections
@@ -253,6 +332,12 @@ HQ_DEV void relaxed_tile(const GemvBatch &batch, int tile, char *lds) {
   const char *wrow = J.wq + (int64_t)row * ng * GB;
   const float *srow = (const float *)J.ws + (int64_t)row * ng;
   const int32_t *crow = WC ? (const int32_t *)J.wc + (int64_t)row * ng : nullptr;
+  // the wave's first row (lane 0's: the rows of a wave ascend, and a clamped row is the job's last) as scalar bases
+  const int row0 = __builtin_amdgcn_readfirstlane(row);
+  const char *wb = J.wq + (int64_t)row0 * ng * GB;
+  const float *sb = (const float *)J.ws + (int64_t)row0 * ng;
+  const int32_t *cb = WC ? (const int32_t *)J.wc + (int64_t)row0 * ng : nullptr;
+  const uint32_t rb = (uint32_t)(row - row0) * (uint32_t)(ng * GB), gb = (uint32_t)(row - row0) * (uint32_t)(ng * 4);
   ActSource<T, SRC> A;
 #pragma unroll
   for (int t = 0; t < T; t++) {
@@ -275,10 +360,21 @@ HQ_DEV void relaxed_tile(const GemvBatch &batch, int tile, char *lds) {
     if (steps > 0) a.load_w(wrow, srow, crow, 0, lane, ng4);  // the first weights in flight during the staging
     fill_acts<T>(J, lds, (float *)(lds + T * J.n));
     if (steps > 0) a.load_x(A, 0, lane, ng4);
+  } else if (Chunk::PAIRED) {
+    if (steps > 0) a.load_paired(wb, sb, cb, rb, gb, A, 0, lane, ng4);
   } else if (steps > 0) {
     a.load(wrow, srow, crow, A, 0, lane, ng4);
   }
-  if (T == 1) {
+  if (Chunk::PAIRED) {
+    for (int it = 0; it < steps; it += 2 * U) {
+      if (it + U < steps) b.load_paired(wb, sb, cb, rb, gb, A, it + U, lane, ng4);
+      a.fold_paired(acc, it, lane, ng4);
+      if (it + U < steps) {
+        if (it + 2 * U < steps) a.load_paired(wb, sb, cb, rb, gb, A, it + 2 * U, lane, ng4);
+        b.fold_paired(acc, it + U, lane, ng4);
+      }
+    }
+  } else if (T == 1) {
     for (int it = 0; it < steps; it += 2 * U) {
       if (it + U < steps) b.load(wrow, srow, crow, A, it + U, lane, ng4);
       a.fold(acc, it, lane, ng4, A);
@@ -306,11 +402,16 @@ HQ_DEV void relaxed_tile(const GemvBatch &batch, int tile, char *lds) {
       b.fold(acc, it + U, lane, ng4, A);
     }
   }
-  // lane 0: ((l0 + l1) + l2) + l3 (math.ts:7-9), then the groups past the fours one at a time (int8.ts:40-47)
+  // lane 0: ((l0 + l1) + l2) + l3 (math.ts:7-9), then the groups past the fours one at a time (int8.ts:40-47); the
+  // paired layout's chains are in lanes 0, 2, 4, 6
   float sum[T];
 #pragma unroll
-  for (int t = 0; t < T; t++)
-    sum[t] = fadd(fadd(fadd(acc[t], from_lane_plus<1>(acc[t])), from_lane_plus<2>(acc[t])), from_lane_plus<3>(acc[t]));
+  for (int t = 0; t < T; t++) {
+    if (Chunk::PAIRED)
+      sum[t] = fadd(fadd(fadd(acc[t], from_lane_plus<2>(acc[t])), from_lane_plus<4>(acc[t])), from_lane_plus<6>(acc[t]));
+    else
+      sum[t] = fadd(fadd(fadd(acc[t], from_lane_plus<1>(acc[t])), from_lane_plus<2>(acc[t])), from_lane_plus<3>(acc[t]));
+  }
   const int tail = ng - ng4;
   if (tail > 0) {
     const int g = ng4 + (lane < tail ? lane : 0);
