@@ -10,13 +10,16 @@
 // wave 4 rows (2 of 32 lanes); a block is 2 waves (8 rows, or 4 of 32 lanes) for the relaxed kinds, 4 waves for the
 // others.  Lane l of a row of L lanes takes the groups L i + l (i = 0, 1, ...): a group's bytes (32 int8, 24 int6 or
 // 32 ternary) are one lane's, so its integer sum is exact in that lane (v_dot4_i32_i8) and a row's lanes read
-// 32 L (24 L) contiguous bytes a step.
+// 32 L (24 L) contiguous bytes a step.  One token of int8 (RelaxedChunk::PAIRED) instead reads each step as whole
+// cache lines with non-temporal loads: a group's two 16-byte halves are in lanes 2 i and 2 i + 1, which add their
+// integers by a DPP swap.
 //
 // The float32 order is the reference's, so every output is its number to the bit:
 //   relaxed int8 / int6: lane k (k = 0..3) of the reference's accumulator adds the groups 4 j + k in order.  Those
 //     are lanes k, k + 4, k + 8, k + 12 of a step here (of a 32-lane row's step, then k + 16, ..., k + 28): lane k
 //     adds them in that order with DPP moves (no LDS; the upper 16 lanes brought down by v_permlane16_swap), then
-//     lane 0 adds the four lanes ((l0 + l1) + l2) + l3 and the groups past the last four one at a time.
+//     lane 0 adds the four lanes ((l0 + l1) + l2) + l3 and the groups past the last four one at a time (one token
+//     of int8: chain k in lane 2 k, the four in lanes 0, 2, 4, 6).
 //   plain int8 / int6 and ternary: the reference's lane k adds part k of EVERY group in order (matmul_q8: the
 //     products 2k, 2k+1, 2k+8, 2k+9 of each half; ternary: the k-th 32 of each 128).  A step's 16 groups x 4 parts
 //     are written to LDS and lane k of the row adds its part of the 16 groups in order.
