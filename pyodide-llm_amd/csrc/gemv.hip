@@ -179,10 +179,11 @@ struct RelaxedChunk {
       const uint4 xa = ld16(A.xq[0] + (c0 * 32u + h)), xb = ld16(A.xq[0] + (c1 * 32u + h));
       x[u][0][0] = xa.x; x[u][0][1] = xa.y; x[u][0][2] = xa.z; x[u][0][3] = xa.w;
       x[u][0][4] = xb.x; x[u][0][5] = xb.y; x[u][0][6] = xb.z; x[u][0][7] = xb.w;
+      // the row's scales and corrections, like its weights, streamed once (a row's 32 lanes read one whole line)
       const uint32_t own = (lane & 1) ? c1 : c0;
-      ws[u] = *(const float *)((const char *)sb + (gb + own * 4u));
+      ws[u] = __builtin_nontemporal_load((const float *)((const char *)sb + (gb + own * 4u)));
       xs[u][0] = *(const float *)(A.xs[0] + own * 4u);
-      if (WC) wc[u] = *(const int32_t *)((const char *)cb + (gb + own * 4u));
+      if (WC) wc[u] = __builtin_nontemporal_load((const int32_t *)((const char *)cb + (gb + own * 4u)));
     }
   }
   // PAIRED: the chunk's terms folded into the chains: chain k of the reference (groups 4 j + k) lives in lane 2 k, and
