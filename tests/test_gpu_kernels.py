@@ -958,6 +958,79 @@ def test_matmuls_relaxed_many_tiles(pkg, arena, oracle, tokens):
         assert same_bits(got, want), f"{what}: {first_difference(got, want)}"
 
 
+@pytest.mark.parametrize("tokens", [1, 2, 4, 6])
+@pytest.mark.parametrize("n", [288, 4096, 14336])
+def test_matmuls_is_quantize_then_phase(pkg, arena, oracle, tokens, n):
+    """hq_matmuls of the relaxed kinds (matmulsAlike: the input readied into the jobs' a / b, then the phase): its
+    outputs and readied a / b against quantize_x then hq_phase on the same inputs, to the bit, over groups whose scale
+    is NaN (lane 0 of groupMax), whose NaN is passed over (lane 1), of infinities, zeros, -0 and subnormals; jobs with
+    and without wc, int8 and int6, two jobs sharing one a / b (readied once), one of 1000 rows; every row against the
+    oracle too (NaN where it has NaN)"""
+    from pyodide_llm_amd import jobs
+    rng = np.random.default_rng(7 * n + tokens)
+    ng = n // 32
+    x = (rng.standard_normal((tokens, n)) * np.exp(rng.uniform(-8, 8, (tokens, ng, 1))).repeat(32, 1).reshape(
+        tokens, n)).astype(F)
+    x[0, 0:32] = 0.0
+    x[0, 33] = -0.0
+    x[0, 64 + 1] = np.nan        # passed over: the group's scale from the other lanes
+    x[0, 96 + 7] = np.inf
+    x[-1, 128:160] = 1e-40       # a subnormal group
+    x[-1, 160] = np.nan          # lane 0 of groupMax: the scale is NaN
+    ax = arena.put(x)
+    L = pkg.library()
+    frame = 2 * n
+    shared = arena.alloc(tokens * frame)
+    specs = []   # (name, rows, wc?, a / b)
+    for name, rows, with_wc, ab in (("matmul_q8r", 70, True, None), ("matmul_q8r", 33, False, None),
+                                    ("matmul_q8r", 1000, True, shared), ("matmul_q8r", 9, True, shared),
+                                    ("matmul_q6r", 50, True, None), ("matmul_q6r", 17, False, None)):
+        six = name == "matmul_q6r"
+        if six:
+            v = (4 * rng.integers(-32, 32, rows * n)).astype(np.int8)
+            wbytes, wc = pack6(v), oracle.six_sums(pack6(v))
+        else:
+            wbytes = rng.integers(-128, 128, rows * n).astype(np.int8)
+            wc = oracle.int8_sums(wbytes)
+        ws = (np.abs(rng.standard_normal(rows * ng)) * 0.02 / 127).astype(F)
+        specs.append((name, rows, six, wbytes, wc, arena.put(wbytes), arena.put(ws), arena.put(wc) if with_wc else 0,
+                      ws, ab))
+    runs = {}
+    for form in ("matmuls", "two launches"):
+        table, outs, abs_ = [], [], []
+        for name, rows, six, wbytes, wc, wa, wsa, wca, ws, ab in specs:
+            out = arena.alloc(4 * rows * tokens, fill=np.full(rows * tokens, -7, F))
+            if ab is None or form == "two launches":
+                ab = arena.alloc(tokens * frame, fill=np.full(tokens * frame, 0xAA, np.uint8))
+            table.append(jobs.job(name, out, ab, ab + n, wa, wsa, wca, n, rows=rows, count=tokens, os=4 * rows,
+                                  as_=frame, bs=frame))
+            outs.append(out)
+            abs_.append(ab)
+        if form == "matmuls":
+            assert jobs.matmuls(L, ax, 4 * n, table) == 0, L.hq_last_error_message()
+        else:
+            for ab in abs_:
+                assert L.hq_quantize_x_batch(ab, ab + n, ax, n, 64, tokens, frame, 4 * n, None) == 0
+            assert jobs.phase(L, table) == 0, L.hq_last_error_message()
+        runs[form] = ([arena.get(o, F, r * tokens) for o, (_, r, *_) in zip(outs, specs)],
+                      [(arena.get(ab, np.uint8, tokens * frame).reshape(tokens, frame)) for ab in abs_])
+    for i, (name, rows, six, wbytes, wc, wa, wsa, wca, ws, _) in enumerate(specs):
+        got, want = runs["matmuls"][0][i], runs["two launches"][0][i]
+        assert np.array_equal(np.isnan(got), np.isnan(want)), name
+        assert same_bits(np.nan_to_num(got), np.nan_to_num(want)), f"{name} {rows}: {first_difference(got, want)}"
+        ga, wa_ = runs["matmuls"][1][i], runs["two launches"][1][i]
+        assert np.array_equal(ga[:, :n], wa_[:, :n]), f"{name} {rows}: readied bytes"
+        gs, ws_ = ga[:, n:n + 4 * ng].copy().view(F), wa_[:, n:n + 4 * ng].copy().view(F)
+        assert np.array_equal(np.isnan(gs), np.isnan(ws_)) and same_bits(np.nan_to_num(gs), np.nan_to_num(ws_))
+        for t in range(tokens):
+            q, sc = oracle.quantize_x(x[t], 64)
+            full = (oracle.matmul_q6r if six else oracle.matmul_q8r)(q, sc, wbytes, ws, wc, n)
+            g = got[t * rows:(t + 1) * rows]
+            assert np.array_equal(np.isnan(g), np.isnan(full)), f"{name} {rows} token {t}"
+            assert same_bits(np.nan_to_num(g), np.nan_to_num(full)), f"{name} {rows} token {t}: " \
+                f"{first_difference(g, full)}"
+
+
 @pytest.mark.parametrize("tokens", [1, 3, 5])
 def test_matmuls_plain_and_ternary(pkg, arena, oracle, tokens):
     from pyodide_llm_amd import jobs
