@@ -282,6 +282,38 @@ def test_phase_and_matmuls_of_blocks(pkg, k, arena, oracle, setup):
         assert same_bits(arena.get(addr, F, want.size), want), what
 
 
+@pytest.mark.parametrize("name,t", [("Q4_K", 12), ("IQ4_XS", 23)])
+@pytest.mark.parametrize("nb", [16, 56])
+def test_matmul_sbr_coalesced_batches(pkg, k, arena, oracle, setup, name, t, nb):
+    """the types whose token steps are read as coalesced 16-byte loads and handed to the lanes through LDS (blocks of
+    144 and 136 bytes, one token staged, every row of the launch starting on 16 bytes): three jobs of one token in
+    one hq_phase (rows not a multiple of a wave's), 16- and 64-lane rows; then the same with one matrix 2 bytes into
+    a word, which takes the whole launch back to a lane's own loads"""
+    from pyodide_llm_amd import jobs
+    row, tab = setup
+    area = put_tables(k, arena, row)
+    rng = np.random.default_rng(4400 + t + nb)
+    n = 256 * nb
+    q, act = token_area(oracle, rng, n)
+    xq, xs = arena.put(q), arena.put(act)
+    L = pkg.library()
+    for shifts in ((0, 0, 0), (0, 2, 0)):
+        table, wants = [], []
+        for rows, shift in zip((37, 50, 9), shifts):
+            wbytes = bm.random_blocks(rng, t, rows * nb).reshape(-1)
+            w = arena.alloc(wbytes.size + 16) + shift
+            arena.write(w, wbytes)
+            out = arena.alloc(4 * (rows + 1), fill=np.full(rows + 1, -7, F))
+            table.append(jobs.job("matmul_sbr", out, xq, xs, w, area, t, n, rows=rows))
+            want = np.full(rows + 1, F(-7), F)
+            want[:rows] = oracle.matmul_sbr(q, act, wbytes, tab, n, t)
+            wants.append((out, want, f"{name} nb {nb} shifts {shifts} rows {rows}"))
+        assert jobs.phase(L, table) == 0, L.hq_last_error_message()
+        for out, want, what in wants:
+            got = arena.get(out, F, want.size)
+            assert same_bits(got, want), f"{what}: {first_difference(got, want)}"
+
+
 def test_signed_dots(k, arena):
     rng = np.random.default_rng(9)
     a = rng.integers(-128, 128, 16).astype(np.int8)
