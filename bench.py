@@ -371,15 +371,25 @@ def measure_configs(torch, pkg, args, extras):
         out[label] = {"GBps": round(total / sec / 1e9, 1), "us_per_launch": round(1e6 * sec / len(tables), 2),
                       "launches": len(tables), "bytes": total}
 
-    def prefill(label, kind, shapes, count):
+    def prefill(label, kind, shapes, count, tol=False):
         ops, calls, keep = 0.0, [], []
+        if tol:  # the tolerance form's workspace, one for the calls, which follow each other on the stream
+            need = max(lib.hq_tol_work_bytes(n, count) for _, n in shapes)
+            work = torch.empty(need + 256, dtype=torch.uint8, device=dev)
+            wptr = (work.data_ptr() + 255) // 256 * 256
+            keep.append(work)
         for rows, n in shapes:
             w, ws = weights(kind, rows, n)
             buf, frame = acts(n, kind, count)
             o = torch.empty(count, rows, device=dev)
             keep += [w, ws, buf, o]
             ops += 2.0 * count * rows * n
-            if kind == "int8":
+            if tol:
+                calls.append(lambda h, w=w, ws=ws, buf=buf, frame=frame, o=o, rows=rows, n=n:
+                             lib.hq_matmul_q8r_tile_tol_ex(o.data_ptr(), buf.data_ptr(), buf.data_ptr() + n,
+                                                           w.data_ptr(), ws.data_ptr(), n, 0, rows, count, 4 * rows,
+                                                           frame, wptr, need, h))
+            elif kind == "int8":
                 wc = torch.empty(rows, n // 32, dtype=torch.int32, device=dev)
                 pkg.check(lib.hq_int8_sums_ex(wc.data_ptr(), w.data_ptr(), rows * n // 32, None))
                 keep.append(wc)
@@ -413,8 +423,9 @@ def measure_configs(torch, pkg, args, extras):
     decode("c0 stories15M q8r M=1 (weights in cache: 221 KB x 64)", "int8", [[(768, 288)]], 64)
     decode("c1 LFM2-350M q8r M=1, 16 layers + lm-head", "int8",
            [[(1536, 1024)], [(1024, 1024)], [(9216, 1024)], [(1024, 4608)]] * 16 + [[(65536, 1024)]], 1)
-    prefill("c2 Llama-3.2-1B prefill M=512, one layer", "int8",
-            [(3072, 2048), (2048, 2048), (8192, 2048), (8192, 2048), (2048, 8192)], 512)
+    c2 = [(3072, 2048), (2048, 2048), (8192, 2048), (8192, 2048), (2048, 8192)]
+    prefill("c2 Llama-3.2-1B prefill M=512, one layer", "int8", c2, 512)
+    prefill("c2 Llama-3.2-1B prefill M=512, one layer, tolerance form", "int8", c2, 512, tol=True)
     for kind in ("ternary", "int6", "binary") if extras else ("ternary", "int6"):
         copies = {"ternary": 8, "int6": 3, "binary": 12}[kind]
         tag = "c4 27B" if kind != "binary" else "27B shapes"

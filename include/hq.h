@@ -274,6 +274,13 @@ int64_t hq_tol_work_bytes(int32_t n, int32_t count);
 int32_t hq_matmul_q8r_tile_tol_ex(void *xout, const void *xq, const void *xs, const void *wq, const void *ws,
                                   int32_t n, int32_t r0, int32_t r1, int32_t count, int32_t os, int32_t frame,
                                   void *work, int64_t work_bytes, void *stream);
+/* The launches hq_matmul_q8r_tile_tol_ex gives its tolerance tile (128 rows x 128 tokens): those of at least `tiles`
+ * tiles; a smaller one takes the bit-exact kernels instead (hq_matmul_q8r_tile_ex's, corrections derived: the
+ * reference's numbers, inside any tolerance), whose smaller tiles fill the GPU where 128 x 128 would leave it idle.
+ * -1 (the default): one round of two blocks a compute unit; 0: every launch takes the tile.  Returns the previous
+ * setting; below -1: HQ_ERR_ARGUMENT, nothing changed.  One setting for the process.  Its counterpart in the
+ * reference: none. */
+int32_t hq_tol_min_tiles(int32_t tiles);
 
 /* Which kernels take a job of `kind` (hq_phase's numbers), row length n and `count` tokens whose activations are
  * frame bytes apart and their scales sframe: 1 the matrix-core tile (16 tokens or more, and every offset within a

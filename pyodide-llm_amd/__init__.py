@@ -108,6 +108,7 @@ OWN_SIGNATURES = {
     "hq_matmuls_static": ([p, i32, ctypes.POINTER(ctypes.c_double), i32, i32, p], i32),
     "hq_job_path": ([i32, i32, i32, ctypes.c_int64, ctypes.c_int64], i32),
     "hq_tol_work_bytes": ([i32, i32], ctypes.c_int64),
+    "hq_tol_min_tiles": ([i32], i32),
     "hq_matmul_q8r_tile_tol_ex": ([p, p, p, p, p, i32, i32, i32, i32, i32, i32, p, ctypes.c_int64, p], i32),
     "hq_ceiling_read": ([p, ctypes.c_int64, p, p], i32),
     "hq_ceiling_mfma": ([i32, i32, p, p], i32),

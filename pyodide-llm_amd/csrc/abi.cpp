@@ -20,6 +20,8 @@ namespace {
 thread_local int32_t g_error = HQ_OK;
 thread_local char g_message[512] = "";
 std::atomic<void *> g_stream{nullptr};
+// hq_tol_min_tiles's setting: -1, one round of two blocks a compute unit
+std::atomic<int32_t> g_tol_min_tiles{-1};
 
 // more tokens than this take the matrix cores (fewer: the token kernel, the weights read once a 4 tokens)
 constexpr int32_t kGemmMinTokens = 16;
@@ -411,6 +413,11 @@ int32_t hq_matmul_q8r_tile_ex(void *xout, const void *xq, const void *xs, const 
                               int32_t frame, void *stream) {
   return matmul(hq::Q8R, xout, xq, xs, wq, ws, wc, n, r0, r1, count, os, frame, 3, stream);
 }
+int32_t hq_tol_min_tiles(int32_t tiles) {
+  g_error = HQ_OK;
+  if (tiles < -1) return fail(HQ_ERR_ARGUMENT, "hq_tol_min_tiles: %d tiles", tiles);
+  return g_tol_min_tiles.exchange(tiles);
+}
 int64_t hq_tol_work_bytes(int32_t n, int32_t count) {
   g_error = HQ_OK;
   if (n <= 0 || n % 32 || count < 0) return fail(HQ_ERR_ARGUMENT, "hq_tol_work_bytes: n = %d, count = %d", n, count), -1;
@@ -437,6 +444,10 @@ int32_t hq_matmul_q8r_tile_tol_ex(void *xout, const void *xq, const void *xs, co
   if ((int64_t)n * 256 >= ((int64_t)1 << 32) || (int64_t)(n / 32) * (count + 3) * 4 >= ((int64_t)1 << 32))
     return fail(HQ_ERR_ARGUMENT, "%s: n = %d with %d tokens is past the tiles' 32-bit offsets", name, n, count);
   if (int32_t st = ensure_device()) return st;
+  // a launch of fewer tiles than the setting asks takes the bit-exact kernels (their numbers are the reference's)
+  const int32_t least = g_tol_min_tiles.load();
+  const int64_t min_tiles = least >= 0 ? least : 2 * (int64_t)hq::cu_count();
+  if (hq::tol_tiles(j.r1 - j.r0, j.count) < min_tiles) return run_jobs(hq::Q8R, {j}, stream_of(stream));
   return hip_status(hq::launch_gemm_tol(j, (char *)work, stream_of(stream)), name);
 }
 int32_t hq_matmul_q6r_ex(void *xout, const void *xq, const void *xs, const void *wq, const void *ws, const void *wc,

@@ -399,6 +399,10 @@ int64_t tol_work_bytes(int32_t n, int32_t count) {
   return ((2 * (int64_t)n * count + 255) & ~(int64_t)255) + 4 * (int64_t)(n >> 5) * cp;
 }
 
+int64_t tol_tiles(int32_t rows, int32_t count) {
+  return ((int64_t)rows + TR - 1) / TR * (((int64_t)count + TT - 1) / TT);
+}
+
 hipError_t launch_gemm_tol(const Job &job, char *work, hipStream_t s) {
   const int rows = job.r1 - job.r0;
   if (rows <= 0 || job.count <= 0) return hipSuccess;
@@ -410,7 +414,7 @@ hipError_t launch_gemm_tol(const Job &job, char *work, hipStream_t s) {
   hipLaunchKernelGGL(tol_prepare, dim3((uint32_t)(xblocks + sblocks)), dim3(256), 0, s, job.xq, job.xs, job.frame,
                      job.sframe, n, count, cp, xblocks, xh, xst);
   TolJob J{job.out, (const char *)xh, (const char *)xst, job.wq, job.ws, n, job.r0, job.r1, count, cp, job.os};
-  const dim3 grid(((rows + TR - 1) / TR) * ((count + TT - 1) / TT));
+  const dim3 grid((uint32_t)tol_tiles(rows, count));
   hipLaunchKernelGGL(gemm_tol, grid, dim3(TW), 0, s, J);
   return hipGetLastError();
 }

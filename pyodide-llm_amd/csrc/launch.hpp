@@ -100,6 +100,8 @@ hipError_t launch_gemm(Kind kind, const Job &job, hipStream_t s);
 // (tol_work_bytes(n, count) bytes, 256-byte aligned), then the tiles; job.wc is not read (corrections derived)
 int64_t tol_work_bytes(int32_t n, int32_t count);
 hipError_t launch_gemm_tol(const Job &job, char *work, hipStream_t s);
+// the tiles launch_gemm_tol gives `rows` rows of `count` tokens
+int64_t tol_tiles(int32_t rows, int32_t count);
 
 // the ceilings (ceilings.hip): every byte of [p, p + bytes) read once; `iterations` x 8 MFMAs a wave of `blocks`
 // blocks of 4 waves.  sink: 256 words that are almost never written

@@ -232,6 +232,22 @@ def test_tolerance_tile_refusals_on_host(pkg):
     L.hq_clear_error()
 
 
+def test_tol_min_tiles_setting(pkg):
+    """hq_tol_min_tiles: -1 by default (a round of two blocks a compute unit), any count of tiles from 0 (every
+    launch takes the tolerance tile), each call returning the setting before it; below -1 refused, nothing changed"""
+    L = pkg.library()
+    before = L.hq_tol_min_tiles(5)
+    try:
+        assert before == -1
+        assert L.hq_tol_min_tiles(0) == 5
+        assert L.hq_tol_min_tiles(-2) == pkg.HQ_ERR_ARGUMENT
+        assert L.hq_last_error() == pkg.HQ_ERR_ARGUMENT
+        L.hq_clear_error()
+        assert L.hq_tol_min_tiles(-1) == 0
+    finally:
+        L.hq_tol_min_tiles(before)
+
+
 def test_ceiling_epilogue_refusals_on_host(pkg):
     """hq_ceiling_epilogue takes form 0 (the bit-exact tile's epilogue) or 1 (the tolerance tile's), a positive grid
     and iteration count, and an aligned sink, checked before any device work"""

@@ -30,9 +30,13 @@ def arena():
 
 
 @pytest.fixture(autouse=True)
-def fresh(arena):
+def fresh(arena, L):
+    """every test here runs the tolerance tile itself, whatever its launch's size (hq_tol_min_tiles 0), unless it
+    says otherwise"""
     arena.reset()
+    before = L.hq_tol_min_tiles(0)
     yield
+    L.hq_tol_min_tiles(before)
 
 
 def frames(q, s, n):
@@ -156,3 +160,30 @@ def test_full_prompt_shapes(pkg, L, arena, oracle, name, rows, n, count):
     wc = oracle.int8_sums(w)
     for t in (0, 1, count // 2, count - 1):
         assert np.array_equal(want[t].view(np.uint32), oracle.matmul_q8r(q[t], s[t], w, ws, wc, n).view(np.uint32))
+
+
+def test_small_launches_take_the_bit_exact_tile(L, arena, oracle):
+    """under the default setting a launch of fewer tolerance tiles than two blocks a compute unit runs the bit-exact
+    kernels: its outputs are hq_matmul_q8r_tile_ex's (corrections derived) to the bit, and the reference's; with
+    every launch given the tile, the same call is within the tolerance"""
+    import torch
+    rng = np.random.default_rng(5150)
+    rows, n, count = 300, 1024, 40  # 3 tiles
+    w = rng.integers(-128, 128, rows * n).astype(np.int8)
+    ws = (np.abs(rng.standard_normal(rows * (n // 32))) * 0.02 / 127).astype(F)
+    q, s = quantized(oracle, rng, count, n)
+    buf, frame = frames(q, s, n)
+    want = reference(oracle, w, ws, q, s, n)
+    assert L.hq_tol_min_tiles(-1) == 0
+    got = run_tol(L, arena, w, ws, buf, frame, n, 0, rows, count, rows)
+    assert np.array_equal(got.view(np.uint32), want.astype(F).view(np.uint32))
+    # the bit-exact tile's own call on the same inputs
+    wq, wsa, xq = arena.put(w), arena.put(ws), arena.put(buf)
+    out = arena.alloc(4 * rows * count, fill=np.full(rows * count, SENTINEL, F))
+    assert L.hq_matmul_q8r_tile_ex(out, xq, xq + n, wq, wsa, None, n, 0, rows, count, 4 * rows, frame, None) == 0
+    exact = arena.get(out, F, rows * count).reshape(count, rows)
+    assert np.array_equal(got.view(np.uint32), exact.view(np.uint32))
+    L.hq_tol_min_tiles(0)
+    forced = run_tol(L, arena, w, ws, buf, frame, n, 0, rows, count, rows)
+    ok, msg = within(forced, want)
+    assert ok, msg
