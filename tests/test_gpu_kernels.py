@@ -878,6 +878,75 @@ def test_phase_matches_single_calls(pkg, k, arena, oracle):
         assert same_bits(arena.get(addr, F, want.size), want)
 
 
+# ---- a phase's jobs as pieces of equal block counts (a job a grid row), or found through block0 ---------------
+@pytest.mark.parametrize("kind, tokens, n, rows", [
+    ("matmul_q8r", 1, 4096, (64, 16, 16)),   # q/k/v-shaped: 16, 4, 4 blocks of 4 rows -> 6 pieces of 4 blocks
+    ("matmul_q8r", 1, 4096, (56, 56)),       # gate / up: 2 pieces
+    ("matmul_q8r", 1, 4096, (64, 17)),       # 16 and 5 blocks: 21 pieces, past 8 -> through block0
+    ("matmul_q8r", 4, 4096, (256, 64, 64)),  # four tokens staged: 8, 2, 2 blocks of 32 rows -> 6 pieces
+    ("matmul_q8r", 4, 4096, (256, 65)),      # 8 and 3 blocks -> 11 pieces -> through block0
+    ("matmul_q8r", 1, 1024, (3, 40, 200)),   # 16-lane rows, 8 a block: 1, 5, 25 blocks -> through block0
+    ("matmul_t2r", 1, 1024, (128, 32, 32)),  # 8-lane rows, 32 a block: 4, 1, 1 blocks -> 6 pieces
+    ("matmul_t2r", 2, 1024, (100, 33)),      # 4 and 2 blocks -> 3 pieces of 2 (the last block of each partial)
+])
+def test_phase_job_pieces(pkg, arena, oracle, kind, tokens, n, rows):
+    """Jobs of one launch whose block counts cut into at most 8 equal pieces run as a job a grid row; others find
+    their job through the first blocks of each.  Either way every row of every job is the reference's number to the
+    bit, for every token, and nothing past a job's rows is written."""
+    from pyodide_llm_amd import jobs
+    rng = np.random.default_rng(sum(rows) + 7 * tokens + n)
+    ternary = kind == "matmul_t2r"
+    if ternary:
+        pairs = [oracle.interleave(rng.integers(-128, 128, n).astype(np.int8),
+                                   (rng.random(n // 32) * 0.05 + 1e-3).astype(F)) for _ in range(tokens)]
+        # a token's bytes, then its area, one frame a token (the tile kinds take one stride for both)
+        frame = sframe = n + 8 * (n // 32)
+        buf = np.zeros(tokens * frame, np.uint8)
+        for t, (b, area) in enumerate(pairs):
+            buf[t * frame:t * frame + n] = b.view(np.uint8)
+            buf[t * frame + n:(t + 1) * frame] = area.view(np.uint8)
+        xq = arena.put(buf)
+        xs = xq + n
+    else:
+        qs = [oracle.quantize_x(rng.standard_normal(n).astype(F), 64) for _ in range(tokens)]
+        frame = sframe = 2 * n
+        buf = np.zeros(tokens * frame, np.uint8)
+        for t, (q, s) in enumerate(qs):
+            buf[t * frame:t * frame + n] = q.view(np.uint8)
+            buf[t * frame + n:t * frame + n + 4 * (n // 32)] = s.view(np.uint8)
+        xq = arena.put(buf)
+        xs = xq + n
+    table, wants = [], []
+    for r in rows:
+        if ternary:
+            codes = rng.integers(0, 3, r * n).astype(np.uint8)
+            w = pack_ternary(codes)
+            ws = np.full(r * (n // 128), 0, np.uint16)
+            ws[:] = np.array(rng.random(r) * 0.02 + 1e-3, np.float16).view(np.uint16).repeat(n // 128)
+            wca = 0
+        else:
+            w = rng.integers(-128, 128, r * n).astype(np.int8)
+            ws = (np.abs(rng.standard_normal(r * (n // 32))) * 0.02 / 127).astype(F)
+            wca = 0
+        out = arena.alloc(4 * (r + 1) * tokens, fill=np.full((r + 1) * tokens, -7, F))
+        table.append(jobs.job(kind, out, xq, xs, arena.put(w), arena.put(ws), wca, n, rows=r, count=tokens,
+                              os=4 * (r + 1), as_=frame, bs=sframe))
+        for t in range(tokens):
+            if ternary:
+                p = pairs[t]
+                full = oracle.matmul_t2r(p[0], p[1], w, ws, n)
+            else:
+                q, s = qs[t]
+                full = oracle.matmul_q8r(q, s, w, ws, oracle.int8_sums(w), n)
+            want = np.append(full, F(-7))
+            wants.append((out + t * 4 * (r + 1), want, f"rows {r} token {t}"))
+    L = pkg.library()
+    assert jobs.phase(L, table) == 0, L.hq_last_error_message()
+    for addr, want, what in wants:
+        got = arena.get(addr, F, want.size)
+        assert same_bits(got, want), f"{kind} {rows} {what}: {first_difference(got, want)}"
+
+
 # ---- hq_matmuls: ready() into the jobs' a / b, then the phase ------------------------------------------------
 @pytest.mark.parametrize("tokens", [1, 2, 3, 4, 7])
 @pytest.mark.parametrize("n", [288, 4096, 17408])
