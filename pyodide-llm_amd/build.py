@@ -23,7 +23,9 @@ LIBRARY = os.path.join(HERE, "libhq.so")
 SOURCES = ["quantize.hip", "gemv.hip", "gemm.hip", "gemm_tol.hip", "blocks.hip", "columns.hip", "ceilings.hip", "abi.cpp"]
 # blocks.hip's prompt tile keeps its matrix-core results in ordinary VGPRs (no copies out of AGPRs: it has registers
 # to spare and reads every result on the VALU)
-EXTRA = {"blocks.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+EXTRA = {"blocks.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+         # the token kernels' scalar arguments (one job's fields) in the waves' scalar registers at launch
+         "gemv.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"]}
 
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 FLAGS = [

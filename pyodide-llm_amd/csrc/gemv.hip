@@ -342,8 +342,7 @@ struct RelaxedChunk {
 // the relaxed_threads / RL rows of tile `blk` of job `jb` (its row range cut into tiles in order).  STAGED: first
 // make the block's LDS copy of the activations, while the first weights are in flight
 template <int PACK, int T, bool WC, int SRC, int RL>
-HQ_DEV void relaxed_tile(const GemvBatch &batch, int jb, int blk, char *lds) {
-  const Job &J = batch.job[jb];
+HQ_DEV void relaxed_tile(const Job &J, int blk, char *lds) {
   const int lane = threadIdx.x & (RL - 1);
   constexpr int rows = relaxed_threads(T, SRC == STAGED) / RL;
   const int row_u = J.r0 + blk * rows + (int)(threadIdx.x / RL);
@@ -465,12 +464,22 @@ HQ_DEV void relaxed_tile(const GemvBatch &batch, int jb, int blk, char *lds) {
 }
 
 // a tile a block
-template <int PACK, int T, bool WC, int SRC, int RL, bool BY>
-__global__ __launch_bounds__(relaxed_threads(T, SRC == STAGED)) void gemv_relaxed(GemvBatch batch) {
+// ONE (one job, one token): the job is the first arguments, which the command processor puts in the waves' scalar
+// registers before they start (gemv.hip is built with kernel-argument preloading: the 13 dwords up to r1 fit the 14
+// user registers left): no scalar load before the first weight loads (wc: one, where WC); the batch is not read
+template <int PACK, int T, bool WC, int SRC, int RL, bool BY, bool ONE>
+__global__ __launch_bounds__(relaxed_threads(T, SRC == STAGED)) void gemv_relaxed(
+    char *out, const char *xq, const char *xs, const char *wq, const char *ws, int32_t n, int32_t r0, int32_t r1,
+    const char *wc, GemvBatch batch) {
   extern __shared__ __align__(16) char lds[];
+  if (ONE) {
+    const Job J{out, xq, xs, wq, ws, wc, n, r0, r1, 1, 0, 0, 0, 0};
+    relaxed_tile<PACK, T, WC, SRC, RL>(J, (int)blockIdx.x, lds);
+    return;
+  }
   int jb, blk;
   block_job<BY>(batch, jb, blk);
-  relaxed_tile<PACK, T, WC, SRC, RL>(batch, jb, blk, lds);
+  relaxed_tile<PACK, T, WC, SRC, RL>(batch.job[jb], blk, lds);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -808,21 +817,27 @@ HQ_HOST_DEV constexpr int ternary_lanes(int n) {
 }
 HQ_HOST_DEV constexpr size_t ternary_stage_bytes(int T, int n) { return (size_t)T * ternary_token_bytes(n); }
 
-template <int PACK, int T, int SRC, bool BY>
+template <int PACK, int T, int SRC, bool BY, bool ONE>
 void launch_relaxed_by(const GemvBatch &b, dim3 grid, bool wc, int lanes, size_t lds, hipStream_t s) {
   const dim3 block(relaxed_threads(T, SRC == STAGED));
+  const Job &J = b.job[0];
   if (lanes == 32) {
-    if (wc) hipLaunchKernelGGL((gemv_relaxed<PACK, T, true, SRC, 32, BY>), grid, block, lds, s, b);
-    else hipLaunchKernelGGL((gemv_relaxed<PACK, T, false, SRC, 32, BY>), grid, block, lds, s, b);
+    if (wc) hipLaunchKernelGGL((gemv_relaxed<PACK, T, true, SRC, 32, BY, ONE>), grid, block, lds, s, J.out, J.xq, J.xs,
+                               J.wq, J.ws, J.n, J.r0, J.r1, J.wc, b);
+    else hipLaunchKernelGGL((gemv_relaxed<PACK, T, false, SRC, 32, BY, ONE>), grid, block, lds, s, J.out, J.xq, J.xs,
+                            J.wq, J.ws, J.n, J.r0, J.r1, J.wc, b);
   } else {
-    if (wc) hipLaunchKernelGGL((gemv_relaxed<PACK, T, true, SRC, 16, BY>), grid, block, lds, s, b);
-    else hipLaunchKernelGGL((gemv_relaxed<PACK, T, false, SRC, 16, BY>), grid, block, lds, s, b);
+    if (wc) hipLaunchKernelGGL((gemv_relaxed<PACK, T, true, SRC, 16, BY, ONE>), grid, block, lds, s, J.out, J.xq, J.xs,
+                               J.wq, J.ws, J.n, J.r0, J.r1, J.wc, b);
+    else hipLaunchKernelGGL((gemv_relaxed<PACK, T, false, SRC, 16, BY, ONE>), grid, block, lds, s, J.out, J.xq, J.xs,
+                            J.wq, J.ws, J.n, J.r0, J.r1, J.wc, b);
   }
 }
 template <int PACK, int T, int SRC>
 hipError_t launch_relaxed(const GemvBatch &b, dim3 grid, bool by, bool wc, int lanes, size_t lds, hipStream_t s) {
-  if (by) launch_relaxed_by<PACK, T, SRC, true>(b, grid, wc, lanes, lds, s);
-  else launch_relaxed_by<PACK, T, SRC, false>(b, grid, wc, lanes, lds, s);
+  if (T == 1 && by && b.njobs == 1) launch_relaxed_by<PACK, T, SRC, true, T == 1>(b, grid, wc, lanes, lds, s);
+  else if (by) launch_relaxed_by<PACK, T, SRC, true, false>(b, grid, wc, lanes, lds, s);
+  else launch_relaxed_by<PACK, T, SRC, false, false>(b, grid, wc, lanes, lds, s);
   return hipGetLastError();
 }
 
