@@ -43,6 +43,13 @@ struct GemvBatch {
   int32_t njobs;
 };
 
+// how a batch is launched: by (a job a grid row) with pieces of `rows` rows; lead_r1 the end of the rows of the job
+// whose pieces come first
+struct Pieces {
+  bool by;
+  int32_t rows, lead_r1, lead_pieces;  // lead_pieces: how many of the pieces are that job's
+};
+
 // where a kernel's activations come from: the caller's xq / xs in global memory (read through the L1), or a copy
 // of them the block makes in LDS
 enum Src { GLOBAL = 0, STAGED = 1 };
@@ -464,18 +471,23 @@ HQ_DEV void relaxed_tile(const Job &J, int blk, char *lds) {
 }
 
 // a tile a block
-// ONE (one job, one token): the job is the first arguments, which the command processor puts in the waves' scalar
-// registers before they start (gemv.hip is built with kernel-argument preloading: the 13 dwords up to r1 fit the 14
-// user registers left): no scalar load before the first weight loads (wc: one, where WC); the batch is not read
-template <int PACK, int T, bool WC, int SRC, int RL, bool BY, bool ONE>
+// PRE (one token, a job a grid row): the batch's first job is also the first arguments, which the command processor
+// puts in the waves' scalar registers before they start (gemv.hip is built with kernel-argument preloading: the 14
+// dwords up to pr fill the user registers left), so the blocks of its pieces (rows r0 + pr y .. of grid row y) make
+// no scalar load before their first weight loads (wc: one, where WC); the other jobs' pieces read theirs.  PRE 2:
+// every piece is the first job's (no other path in the kernel: measured 0.05 us a launch shorter than PRE 1)
+template <int PACK, int T, bool WC, int SRC, int RL, bool BY, int PRE>
 __global__ __launch_bounds__(relaxed_threads(T, SRC == STAGED)) void gemv_relaxed(
     char *out, const char *xq, const char *xs, const char *wq, const char *ws, int32_t n, int32_t r0, int32_t r1,
-    const char *wc, GemvBatch batch) {
+    int32_t pr, const char *wc, GemvBatch batch) {
   extern __shared__ __align__(16) char lds[];
-  if (ONE) {
-    const Job J{out, xq, xs, wq, ws, wc, n, r0, r1, 1, 0, 0, 0, 0};
-    relaxed_tile<PACK, T, WC, SRC, RL>(J, (int)blockIdx.x, lds);
-    return;
+  if (PRE) {
+    const int a = r0 + (int)blockIdx.y * pr;
+    if (PRE == 2 || a < r1) {
+      const Job J{out, xq, xs, wq, ws, wc, n, a, min(a + pr, r1), 1, 0, 0, 0, 0};
+      relaxed_tile<PACK, T, WC, SRC, RL>(J, (int)blockIdx.x, lds);
+      return;
+    }
   }
   int jb, blk;
   block_job<BY>(batch, jb, blk);
@@ -817,27 +829,35 @@ HQ_HOST_DEV constexpr int ternary_lanes(int n) {
 }
 HQ_HOST_DEV constexpr size_t ternary_stage_bytes(int T, int n) { return (size_t)T * ternary_token_bytes(n); }
 
-template <int PACK, int T, int SRC, bool BY, bool ONE>
-void launch_relaxed_by(const GemvBatch &b, dim3 grid, bool wc, int lanes, size_t lds, hipStream_t s) {
+// lead_r1, pr: the end of the rows of the job whose pieces come first (b.job[0] is its first piece), and the rows a
+// piece (the arguments PRE reads)
+template <int PACK, int T, int SRC, bool BY, int PRE>
+void launch_relaxed_by(const GemvBatch &b, dim3 grid, int32_t lead_r1, int32_t pr, bool wc, int lanes, size_t lds,
+                       hipStream_t s) {
   const dim3 block(relaxed_threads(T, SRC == STAGED));
   const Job &J = b.job[0];
   if (lanes == 32) {
-    if (wc) hipLaunchKernelGGL((gemv_relaxed<PACK, T, true, SRC, 32, BY, ONE>), grid, block, lds, s, J.out, J.xq, J.xs,
-                               J.wq, J.ws, J.n, J.r0, J.r1, J.wc, b);
-    else hipLaunchKernelGGL((gemv_relaxed<PACK, T, false, SRC, 32, BY, ONE>), grid, block, lds, s, J.out, J.xq, J.xs,
-                            J.wq, J.ws, J.n, J.r0, J.r1, J.wc, b);
+    if (wc) hipLaunchKernelGGL((gemv_relaxed<PACK, T, true, SRC, 32, BY, PRE>), grid, block, lds, s, J.out, J.xq, J.xs,
+                               J.wq, J.ws, J.n, J.r0, lead_r1, pr, J.wc, b);
+    else hipLaunchKernelGGL((gemv_relaxed<PACK, T, false, SRC, 32, BY, PRE>), grid, block, lds, s, J.out, J.xq, J.xs,
+                            J.wq, J.ws, J.n, J.r0, lead_r1, pr, J.wc, b);
   } else {
-    if (wc) hipLaunchKernelGGL((gemv_relaxed<PACK, T, true, SRC, 16, BY, ONE>), grid, block, lds, s, J.out, J.xq, J.xs,
-                               J.wq, J.ws, J.n, J.r0, J.r1, J.wc, b);
-    else hipLaunchKernelGGL((gemv_relaxed<PACK, T, false, SRC, 16, BY, ONE>), grid, block, lds, s, J.out, J.xq, J.xs,
-                            J.wq, J.ws, J.n, J.r0, J.r1, J.wc, b);
+    if (wc) hipLaunchKernelGGL((gemv_relaxed<PACK, T, true, SRC, 16, BY, PRE>), grid, block, lds, s, J.out, J.xq, J.xs,
+                               J.wq, J.ws, J.n, J.r0, lead_r1, pr, J.wc, b);
+    else hipLaunchKernelGGL((gemv_relaxed<PACK, T, false, SRC, 16, BY, PRE>), grid, block, lds, s, J.out, J.xq, J.xs,
+                            J.wq, J.ws, J.n, J.r0, lead_r1, pr, J.wc, b);
   }
 }
 template <int PACK, int T, int SRC>
-hipError_t launch_relaxed(const GemvBatch &b, dim3 grid, bool by, bool wc, int lanes, size_t lds, hipStream_t s) {
-  if (T == 1 && by && b.njobs == 1) launch_relaxed_by<PACK, T, SRC, true, T == 1>(b, grid, wc, lanes, lds, s);
-  else if (by) launch_relaxed_by<PACK, T, SRC, true, false>(b, grid, wc, lanes, lds, s);
-  else launch_relaxed_by<PACK, T, SRC, false, false>(b, grid, wc, lanes, lds, s);
+hipError_t launch_relaxed(const GemvBatch &b, dim3 grid, const Pieces &p, bool wc, int lanes, size_t lds,
+                          hipStream_t s) {
+  // (T == 1 in the template arguments: the PRE kernels of 2..4 tokens are never made)
+  if (T == 1 && p.by && p.lead_pieces == b.njobs)
+    launch_relaxed_by<PACK, T, SRC, true, T == 1 ? 2 : 0>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
+  else if (T == 1 && p.by)
+    launch_relaxed_by<PACK, T, SRC, true, T == 1 ? 1 : 0>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
+  else if (p.by) launch_relaxed_by<PACK, T, SRC, true, 0>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
+  else launch_relaxed_by<PACK, T, SRC, false, 0>(b, grid, 0, 0, wc, lanes, lds, s);
   return hipGetLastError();
 }
 
@@ -870,20 +890,21 @@ hipError_t launch_signs(const GemvBatch &b, dim3 grid, bool by, hipStream_t s) {
   return hipGetLastError();
 }
 
-// grid: (blocks) with the jobs found through block0, or (blocks a piece, pieces) when `by`
+// grid: (blocks) with the jobs found through block0, or (blocks a piece, pieces) when p.by
 template <int T>
-hipError_t launch_t(Kind kind, const GemvBatch &b, dim3 grid, bool by, bool wc, int src, int lanes, size_t lds,
-                    hipStream_t s) {
+hipError_t launch_t(Kind kind, const GemvBatch &b, dim3 grid, const Pieces &p, bool wc, int src, int lanes,
+                    size_t lds, hipStream_t s) {
+  const bool by = p.by;
   const dim3 block(256);
   switch (kind) {
   case Q8R:
   case Q6R:
     if (kind == Q8R) {
-      if (src == STAGED) return launch_relaxed<8, T, STAGED>(b, grid, by, wc, lanes, lds, s);
-      return launch_relaxed<8, T, GLOBAL>(b, grid, by, wc, lanes, 0, s);
+      if (src == STAGED) return launch_relaxed<8, T, STAGED>(b, grid, p, wc, lanes, lds, s);
+      return launch_relaxed<8, T, GLOBAL>(b, grid, p, wc, lanes, 0, s);
     }
-    if (src == STAGED) return launch_relaxed<6, T, STAGED>(b, grid, by, wc, lanes, lds, s);
-    return launch_relaxed<6, T, GLOBAL>(b, grid, by, wc, lanes, 0, s);
+    if (src == STAGED) return launch_relaxed<6, T, STAGED>(b, grid, p, wc, lanes, lds, s);
+    return launch_relaxed<6, T, GLOBAL>(b, grid, p, wc, lanes, 0, s);
   case Q8: hipLaunchKernelGGL((gemv_plain<8, T>), grid, block, 0, s, b); break;
   case Q6: hipLaunchKernelGGL((gemv_plain<6, T>), grid, block, 0, s, b); break;
   case T2R:
@@ -933,15 +954,17 @@ hipError_t launch_batch(Kind kind, const Job *jobs, int32_t njobs, hipStream_t s
   // greatest common divisor of the jobs' block counts) make at most kMaxJobs pieces: a block's job is then blockIdx.y,
   // and its fields are read in the kernel's first round of scalar loads instead of a round after the block0 it is
   // found by (measured on the 8B decode: the o and down projections' launches 0.14-0.2 us shorter with one job).
-  bool by = false;
+  Pieces pc{false, 0, 0, 0};
   if (relaxed || signs_kind(kind)) {
     int g = 0;
     for (int j = 0; j < njobs; j++) g = std::gcd(g, b.block0[j + 1] - b.block0[j]);
     if (blocks / g <= kMaxJobs) {
       GemvBatch p{};
-      int pieces = 0;
+      int pieces = 0, lead = -1;
       for (int j = 0; j < njobs; j++)
         for (int r = jobs[j].r0; r < jobs[j].r1; r += g * rpb) {
+          if (pieces == 0) lead = j, pc.lead_r1 = jobs[j].r1;
+          if (j == lead) ++pc.lead_pieces;
           p.job[pieces] = jobs[j];
           p.job[pieces].r0 = r;
           p.job[pieces].r1 = std::min(r + g * rpb, jobs[j].r1);
@@ -952,15 +975,16 @@ hipError_t launch_batch(Kind kind, const Job *jobs, int32_t njobs, hipStream_t s
       p.njobs = pieces;
       b = p;
       grid = dim3(g, pieces);
-      by = true;
+      pc.by = true;
+      pc.rows = g * rpb;
     }
   }
   const bool wc = jobs[0].wc != nullptr;
   switch (T) {
-  case 1: return launch_t<1>(kind, b, grid, by, wc, src, lanes, lds, s);
-  case 2: return launch_t<2>(kind, b, grid, by, wc, src, lanes, lds, s);
-  case 3: return launch_t<3>(kind, b, grid, by, wc, src, lanes, lds, s);
-  case 4: return launch_t<4>(kind, b, grid, by, wc, src, lanes, lds, s);
+  case 1: return launch_t<1>(kind, b, grid, pc, wc, src, lanes, lds, s);
+  case 2: return launch_t<2>(kind, b, grid, pc, wc, src, lanes, lds, s);
+  case 3: return launch_t<3>(kind, b, grid, pc, wc, src, lanes, lds, s);
+  case 4: return launch_t<4>(kind, b, grid, pc, wc, src, lanes, lds, s);
   default: return hipErrorInvalidValue;
   }
 }

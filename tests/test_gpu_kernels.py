@@ -947,6 +947,31 @@ def test_phase_job_pieces(pkg, arena, oracle, kind, tokens, n, rows):
         assert same_bits(got, want), f"{kind} {rows} {what}: {first_difference(got, want)}"
 
 
+@pytest.mark.parametrize("cuts", [(0, 32, 64), (0, 8, 64), (16, 48, 64), (0, 0, 40, 64)])
+def test_phase_jobs_of_one_matrix(pkg, arena, oracle, cuts):
+    """Jobs that are row ranges of one matrix (the same weights and outputs; a range of no rows first, too): cut
+    into pieces, every range is the reference's numbers and the rows outside every range are left as they were."""
+    from pyodide_llm_amd import jobs
+    rng = np.random.default_rng(len(cuts) + sum(cuts))
+    n, rows = 4096, 64
+    q, s = oracle.quantize_x(rng.standard_normal(n).astype(F), 64)
+    buf = np.concatenate([q.view(np.uint8), s.view(np.uint8)])
+    xq = arena.put(buf)
+    w = rng.integers(-128, 128, rows * n).astype(np.int8)
+    ws = (np.abs(rng.standard_normal(rows * (n // 32))) * 0.02 / 127).astype(F)
+    wq, wsa = arena.put(w), arena.put(ws)
+    out = arena.alloc(4 * (rows + 1), fill=np.full(rows + 1, -7, F))
+    table = [jobs.job("matmul_q8r", out + 4 * a, xq, xq + n, wq + a * n, wsa + 4 * a * (n // 32), 0, n, rows=b - a)
+             for a, b in zip(cuts, cuts[1:])]
+    L = pkg.library()
+    assert jobs.phase(L, table) == 0, L.hq_last_error_message()
+    full = oracle.matmul_q8r(q, s, w, ws, oracle.int8_sums(w), n)
+    want = np.full(rows + 1, F(-7), F)
+    want[cuts[0]:cuts[-1]] = full[cuts[0]:cuts[-1]]
+    got = arena.get(out, F, rows + 1)
+    assert same_bits(got, want), f"cuts {cuts}: {first_difference(got, want)}"
+
+
 # ---- hq_matmuls: ready() into the jobs' a / b, then the phase ------------------------------------------------
 @pytest.mark.parametrize("tokens", [1, 2, 3, 4, 7])
 @pytest.mark.parametrize("n", [288, 4096, 17408])
