@@ -25,7 +25,9 @@ SOURCES = ["quantize.hip", "gemv.hip", "gemm.hip", "gemm_tol.hip", "blocks.hip",
 # to spare and reads every result on the VALU)
 EXTRA = {"blocks.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
          # the token kernels' scalar arguments (one job's fields) in the waves' scalar registers at launch
-         "gemv.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"]}
+         "gemv.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"],
+         # quantize_x's arguments likewise (14 dwords): it runs before every phase of a decode step
+         "quantize.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"]}
 
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 FLAGS = [
