@@ -743,13 +743,8 @@ struct TernaryChunk {
 
 constexpr int kTernThreads = 256;  // a block's threads: kTernThreads / L rows
 // rows of L lanes (16: 16 rows a block; 32 for long rows: twice the waves on the same rows)
-template <int T, bool STAGE, int L, bool BIN, bool BY>
-__global__ __launch_bounds__(kTernThreads) void gemv_ternary(GemvBatch batch) {
-  extern __shared__ __align__(16) char acts[];
-  __shared__ FoldL<T, L> fold[kTernThreads / 64];
-  int jb, blk;
-  block_job<BY>(batch, jb, blk);
-  const Job &J = batch.job[jb];
+template <int T, bool STAGE, int L, bool BIN>
+HQ_DEV void ternary_rows(const Job &J, int blk, char *acts, FoldL<T, L> *fold) {
   const int lane = threadIdx.x & (L - 1);
   const int wave = threadIdx.x >> 6, slot = (threadIdx.x & 63) / L;
   const int row_u = J.r0 + blk * (kTernThreads / L) + threadIdx.x / L;
@@ -819,6 +814,26 @@ __global__ __launch_bounds__(kTernThreads) void gemv_ternary(GemvBatch batch) {
   }
 }
 
+// PRE (one token, a job a grid row), as gemv_relaxed's: the first job's pieces from the preloaded arguments
+template <int T, bool STAGE, int L, bool BIN, bool BY, int PRE>
+__global__ __launch_bounds__(kTernThreads) void gemv_ternary(char *out, const char *xq, const char *xs, const char *wq,
+                                                             const char *ws, int32_t n, int32_t r0, int32_t r1,
+                                                             int32_t pr, GemvBatch batch) {
+  extern __shared__ __align__(16) char acts[];
+  __shared__ FoldL<T, L> fold[kTernThreads / 64];
+  if (PRE) {
+    const int a = r0 + (int)blockIdx.y * pr;
+    if (PRE == 2 || a < r1) {
+      const Job J{out, xq, xs, wq, ws, nullptr, n, a, min(a + pr, r1), 1, 0, 0, 0, 0};
+      ternary_rows<T, STAGE, L, BIN>(J, (int)blockIdx.x, acts, fold);
+      return;
+    }
+  }
+  int jb, blk;
+  block_job<BY>(batch, jb, blk);
+  ternary_rows<T, STAGE, L, BIN>(batch.job[jb], blk, acts, fold);
+}
+
 // the LDS a ternary block stages for T tokens of n activations (beyond: read through the L1)
 constexpr size_t kTernaryStageMax = 64 * 1024;
 // lanes a row of ternary weights: 32 for rows of at least kTernaryLongRow weights, 8 for rows of an odd number of
@@ -862,8 +877,9 @@ hipError_t launch_relaxed(const GemvBatch &b, dim3 grid, const Pieces &p, bool w
 }
 
 // ternary / binary: rows of ternary_lanes(n) lanes, the activations staged in LDS when they fit
-template <int T, bool BIN, bool BY>
-void launch_signs_by(const GemvBatch &b, dim3 grid, hipStream_t s) {
+template <int T, bool BIN, bool BY, int PRE>
+void launch_signs_by(const GemvBatch &b, dim3 grid, int32_t lead_r1, int32_t pr, hipStream_t s) {
+  const Job &J = b.job[0];
   int nmax = 0;
   for (int j = 0; j < b.njobs; j++) nmax = b.job[j].n > nmax ? b.job[j].n : nmax;
   const size_t bytes = ternary_stage_bytes(T, nmax);
@@ -871,22 +887,38 @@ void launch_signs_by(const GemvBatch &b, dim3 grid, hipStream_t s) {
   const dim3 block(kTernThreads);
   switch (ternary_lanes(nmax)) {
   case 32:
-    if (stage) hipLaunchKernelGGL((gemv_ternary<T, true, 32, BIN, BY>), grid, block, bytes, s, b);
-    else hipLaunchKernelGGL((gemv_ternary<T, false, 32, BIN, BY>), grid, block, 0, s, b);
+    if (stage)
+      hipLaunchKernelGGL((gemv_ternary<T, true, 32, BIN, BY, PRE>), grid, block, bytes, s, J.out, J.xq, J.xs, J.wq, J.ws,
+                         J.n, J.r0, lead_r1, pr, b);
+    else
+      hipLaunchKernelGGL((gemv_ternary<T, false, 32, BIN, BY, PRE>), grid, block, 0, s, J.out, J.xq, J.xs, J.wq, J.ws,
+                         J.n, J.r0, lead_r1, pr, b);
     break;
   case 8:
-    if (stage) hipLaunchKernelGGL((gemv_ternary<T, true, 8, BIN, BY>), grid, block, bytes, s, b);
-    else hipLaunchKernelGGL((gemv_ternary<T, false, 8, BIN, BY>), grid, block, 0, s, b);
+    if (stage)
+      hipLaunchKernelGGL((gemv_ternary<T, true, 8, BIN, BY, PRE>), grid, block, bytes, s, J.out, J.xq, J.xs, J.wq, J.ws,
+                         J.n, J.r0, lead_r1, pr, b);
+    else
+      hipLaunchKernelGGL((gemv_ternary<T, false, 8, BIN, BY, PRE>), grid, block, 0, s, J.out, J.xq, J.xs, J.wq, J.ws,
+                         J.n, J.r0, lead_r1, pr, b);
     break;
   default:
-    if (stage) hipLaunchKernelGGL((gemv_ternary<T, true, 16, BIN, BY>), grid, block, bytes, s, b);
-    else hipLaunchKernelGGL((gemv_ternary<T, false, 16, BIN, BY>), grid, block, 0, s, b);
+    if (stage)
+      hipLaunchKernelGGL((gemv_ternary<T, true, 16, BIN, BY, PRE>), grid, block, bytes, s, J.out, J.xq, J.xs, J.wq, J.ws,
+                         J.n, J.r0, lead_r1, pr, b);
+    else
+      hipLaunchKernelGGL((gemv_ternary<T, false, 16, BIN, BY, PRE>), grid, block, 0, s, J.out, J.xq, J.xs, J.wq, J.ws,
+                         J.n, J.r0, lead_r1, pr, b);
   }
 }
 template <int T, bool BIN>
-hipError_t launch_signs(const GemvBatch &b, dim3 grid, bool by, hipStream_t s) {
-  if (by) launch_signs_by<T, BIN, true>(b, grid, s);
-  else launch_signs_by<T, BIN, false>(b, grid, s);
+hipError_t launch_signs(const GemvBatch &b, dim3 grid, const Pieces &p, hipStream_t s) {
+  if (T == 1 && p.by && p.lead_pieces == b.njobs)
+    launch_signs_by<T, BIN, true, T == 1 ? 2 : 0>(b, grid, p.lead_r1, p.rows, s);
+  else if (T == 1 && p.by)
+    launch_signs_by<T, BIN, true, T == 1 ? 1 : 0>(b, grid, p.lead_r1, p.rows, s);
+  else if (p.by) launch_signs_by<T, BIN, true, 0>(b, grid, p.lead_r1, p.rows, s);
+  else launch_signs_by<T, BIN, false, 0>(b, grid, 0, 0, s);
   return hipGetLastError();
 }
 
@@ -894,7 +926,6 @@ hipError_t launch_signs(const GemvBatch &b, dim3 grid, bool by, hipStream_t s) {
 template <int T>
 hipError_t launch_t(Kind kind, const GemvBatch &b, dim3 grid, const Pieces &p, bool wc, int src, int lanes,
                     size_t lds, hipStream_t s) {
-  const bool by = p.by;
   const dim3 block(256);
   switch (kind) {
   case Q8R:
@@ -908,9 +939,9 @@ hipError_t launch_t(Kind kind, const GemvBatch &b, dim3 grid, const Pieces &p, b
   case Q8: hipLaunchKernelGGL((gemv_plain<8, T>), grid, block, 0, s, b); break;
   case Q6: hipLaunchKernelGGL((gemv_plain<6, T>), grid, block, 0, s, b); break;
   case T2R:
-  case T2: return launch_signs<T, false>(b, grid, by, s);
+  case T2: return launch_signs<T, false>(b, grid, p, s);
   case B1R:
-  case B1: return launch_signs<T, true>(b, grid, by, s);
+  case B1: return launch_signs<T, true>(b, grid, p, s);
   default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
