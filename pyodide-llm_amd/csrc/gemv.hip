@@ -45,7 +45,7 @@ struct GemvBatch {
 
 // how a batch is launched: by (a job a grid row) with pieces of `rows` rows; lead_r1 the end of the rows of the job
 // whose pieces come first
-struct Pieces {
+struct JobPieces {
   bool by;
   int32_t rows, lead_r1, lead_pieces;  // lead_pieces: how many of the pieces are that job's
 };
@@ -864,7 +864,7 @@ void launch_relaxed_by(const GemvBatch &b, dim3 grid, int32_t lead_r1, int32_t p
   }
 }
 template <int PACK, int T, int SRC>
-hipError_t launch_relaxed(const GemvBatch &b, dim3 grid, const Pieces &p, bool wc, int lanes, size_t lds,
+hipError_t launch_relaxed(const GemvBatch &b, dim3 grid, const JobPieces &p, bool wc, int lanes, size_t lds,
                           hipStream_t s) {
   // (T == 1 in the template arguments: the PRE kernels of 2..4 tokens are never made)
   if (T == 1 && p.by && p.lead_pieces == b.njobs)
@@ -912,7 +912,7 @@ void launch_signs_by(const GemvBatch &b, dim3 grid, int32_t lead_r1, int32_t pr,
   }
 }
 template <int T, bool BIN>
-hipError_t launch_signs(const GemvBatch &b, dim3 grid, const Pieces &p, hipStream_t s) {
+hipError_t launch_signs(const GemvBatch &b, dim3 grid, const JobPieces &p, hipStream_t s) {
   if (T == 1 && p.by && p.lead_pieces == b.njobs)
     launch_signs_by<T, BIN, true, T == 1 ? 2 : 0>(b, grid, p.lead_r1, p.rows, s);
   else if (T == 1 && p.by)
@@ -924,7 +924,7 @@ hipError_t launch_signs(const GemvBatch &b, dim3 grid, const Pieces &p, hipStrea
 
 // grid: (blocks) with the jobs found through block0, or (blocks a piece, pieces) when p.by
 template <int T>
-hipError_t launch_t(Kind kind, const GemvBatch &b, dim3 grid, const Pieces &p, bool wc, int src, int lanes,
+hipError_t launch_t(Kind kind, const GemvBatch &b, dim3 grid, const JobPieces &p, bool wc, int src, int lanes,
                     size_t lds, hipStream_t s) {
   const dim3 block(256);
   switch (kind) {
@@ -985,7 +985,7 @@ hipError_t launch_batch(Kind kind, const Job *jobs, int32_t njobs, hipStream_t s
   // greatest common divisor of the jobs' block counts) make at most kMaxJobs pieces: a block's job is then blockIdx.y,
   // and its fields are read in the kernel's first round of scalar loads instead of a round after the block0 it is
   // found by (measured on the 8B decode: the o and down projections' launches 0.14-0.2 us shorter with one job).
-  Pieces pc{false, 0, 0, 0};
+  JobPieces pc{false, 0, 0, 0};
   if (relaxed || signs_kind(kind)) {
     int g = 0;
     for (int j = 0; j < njobs; j++) g = std::gcd(g, b.block0[j + 1] - b.block0[j]);
