@@ -471,20 +471,22 @@ HQ_DEV void relaxed_tile(const Job &J, int blk, char *lds) {
 }
 
 // a tile a block
-// PRE (one token, a job a grid row): the batch's first job is also the first arguments, which the command processor
-// puts in the waves' scalar registers before they start (gemv.hip is built with kernel-argument preloading: the 14
-// dwords up to pr fill the user registers left), so the blocks of its pieces (rows r0 + pr y .. of grid row y) make
-// no scalar load before their first weight loads (wc: one, where WC); the other jobs' pieces read theirs.  PRE 2:
-// every piece is the first job's (no other path in the kernel: measured 0.05 us a launch shorter than PRE 1)
+// PRE (a job a grid row): the batch's first job is also the first arguments, which the command processor puts in the
+// waves' scalar registers before they start (gemv.hip is built with kernel-argument preloading: the 13 dwords up to
+// frame fit the 14 user registers left), so the blocks of its pieces (rows r0 + pr y .. of grid row y) make no scalar
+// load before their first weight and activation loads (out, os and wc, read late, follow as ordinary arguments); the
+// other jobs' pieces read theirs.  PRE 2: every piece is the first job's (no other path in the kernel: measured
+// 0.05 us a launch shorter than PRE 1).  The activations and their scales are `frame` bytes a token apart (the tile
+// kinds' one stride).
 template <int PACK, int T, bool WC, int SRC, int RL, bool BY, int PRE>
 __global__ __launch_bounds__(relaxed_threads(T, SRC == STAGED)) void gemv_relaxed(
-    char *out, const char *xq, const char *xs, const char *wq, const char *ws, int32_t n, int32_t r0, int32_t r1,
-    int32_t pr, const char *wc, GemvBatch batch) {
+    const char *xq, const char *xs, const char *wq, const char *ws, int32_t n, int32_t r0, int32_t r1, int32_t pr,
+    int32_t frame, char *out, int64_t os, const char *wc, GemvBatch batch) {
   extern __shared__ __align__(16) char lds[];
   if (PRE) {
     const int a = r0 + (int)blockIdx.y * pr;
     if (PRE == 2 || a < r1) {
-      const Job J{out, xq, xs, wq, ws, wc, n, a, min(a + pr, r1), 1, 0, 0, 0, 0};
+      const Job J{out, xq, xs, wq, ws, wc, n, a, min(a + pr, r1), T, os, frame, frame, 0};
       relaxed_tile<PACK, T, WC, SRC, RL>(J, (int)blockIdx.x, lds);
       return;
     }
@@ -851,26 +853,29 @@ void launch_relaxed_by(const GemvBatch &b, dim3 grid, int32_t lead_r1, int32_t p
                        hipStream_t s) {
   const dim3 block(relaxed_threads(T, SRC == STAGED));
   const Job &J = b.job[0];
+  const int32_t frame = (int32_t)J.frame;  // (PRE: J.frame == J.sframe, below 2^31)
   if (lanes == 32) {
-    if (wc) hipLaunchKernelGGL((gemv_relaxed<PACK, T, true, SRC, 32, BY, PRE>), grid, block, lds, s, J.out, J.xq, J.xs,
-                               J.wq, J.ws, J.n, J.r0, lead_r1, pr, J.wc, b);
-    else hipLaunchKernelGGL((gemv_relaxed<PACK, T, false, SRC, 32, BY, PRE>), grid, block, lds, s, J.out, J.xq, J.xs,
-                            J.wq, J.ws, J.n, J.r0, lead_r1, pr, J.wc, b);
+    if (wc) hipLaunchKernelGGL((gemv_relaxed<PACK, T, true, SRC, 32, BY, PRE>), grid, block, lds, s, J.xq, J.xs, J.wq,
+                               J.ws, J.n, J.r0, lead_r1, pr, frame, J.out, J.os, J.wc, b);
+    else hipLaunchKernelGGL((gemv_relaxed<PACK, T, false, SRC, 32, BY, PRE>), grid, block, lds, s, J.xq, J.xs, J.wq,
+                            J.ws, J.n, J.r0, lead_r1, pr, frame, J.out, J.os, J.wc, b);
   } else {
-    if (wc) hipLaunchKernelGGL((gemv_relaxed<PACK, T, true, SRC, 16, BY, PRE>), grid, block, lds, s, J.out, J.xq, J.xs,
-                               J.wq, J.ws, J.n, J.r0, lead_r1, pr, J.wc, b);
-    else hipLaunchKernelGGL((gemv_relaxed<PACK, T, false, SRC, 16, BY, PRE>), grid, block, lds, s, J.out, J.xq, J.xs,
-                            J.wq, J.ws, J.n, J.r0, lead_r1, pr, J.wc, b);
+    if (wc) hipLaunchKernelGGL((gemv_relaxed<PACK, T, true, SRC, 16, BY, PRE>), grid, block, lds, s, J.xq, J.xs, J.wq,
+                               J.ws, J.n, J.r0, lead_r1, pr, frame, J.out, J.os, J.wc, b);
+    else hipLaunchKernelGGL((gemv_relaxed<PACK, T, false, SRC, 16, BY, PRE>), grid, block, lds, s, J.xq, J.xs, J.wq,
+                            J.ws, J.n, J.r0, lead_r1, pr, frame, J.out, J.os, J.wc, b);
   }
 }
 template <int PACK, int T, int SRC>
 hipError_t launch_relaxed(const GemvBatch &b, dim3 grid, const JobPieces &p, bool wc, int lanes, size_t lds,
                           hipStream_t s) {
-  // (T == 1 in the template arguments: the PRE kernels of 2..4 tokens are never made)
-  if (T == 1 && p.by && p.lead_pieces == b.njobs)
-    launch_relaxed_by<PACK, T, SRC, true, T == 1 ? 2 : 0>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
-  else if (T == 1 && p.by)
-    launch_relaxed_by<PACK, T, SRC, true, T == 1 ? 1 : 0>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
+  // PRE takes one stride for a token's activations and scales (the tile kinds' frame; one token: none read)
+  const Job &J = b.job[0];
+  const bool pre = p.by && (T == 1 || (J.frame == J.sframe && J.frame >= 0 && J.frame <= INT32_MAX));
+  if (pre && p.lead_pieces == b.njobs)
+    launch_relaxed_by<PACK, T, SRC, true, 2>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
+  else if (pre)
+    launch_relaxed_by<PACK, T, SRC, true, 1>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
   else if (p.by) launch_relaxed_by<PACK, T, SRC, true, 0>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
   else launch_relaxed_by<PACK, T, SRC, false, 0>(b, grid, 0, 0, wc, lanes, lds, s);
   return hipGetLastError();
