@@ -87,9 +87,15 @@ HQ_HOST_DEV constexpr int relaxed_threads(int T, bool staged) { return T > 1 && 
 // 14.6); int6 shows no consistent gain (16 lanes); 2..4 tokens gain on rows past 8192 (four tokens' 8B down 19.8 ->
 // 18.8 us, int6 30.4 -> 20.7) and lose below (gate+up 29.6 -> 31.9).
 constexpr int kRelaxedLongRow = 8192;
+// One token of int8 past 8192 takes 32 lanes where a row is an even number of 32-lane steps, not a multiple of four
+// (10240, 14336, ...), in chunks of 2 steps: none past the row's end (8B down 12.73 -> 12.55 us; with chunks of 4,
+// half a chunk of loads wasted at each row's end, 13.45).
+HQ_HOST_DEV constexpr bool relaxed_pairs_of_steps(Kind kind, int T, int n) {
+  return T == 1 && kind == Q8R && n > kRelaxedLongRow && (n / 1024) % 4 == 2 && n % 1024 == 0;
+}
 HQ_HOST_DEV constexpr int relaxed_lanes(Kind kind, int T, int n) {
   if (T > 1) return n > kRelaxedLongRow ? 32 : 16;
-  return kind == Q8R && n % 4096 == 0 && n <= kRelaxedLongRow ? 32 : 16;
+  return kind == Q8R && ((n % 4096 == 0 && n <= kRelaxedLongRow) || relaxed_pairs_of_steps(kind, T, n)) ? 32 : 16;
 }
 
 // the job of block `blk`: block0's entries past the batch's jobs are INT32_MAX, so that every entry is compared
@@ -172,10 +178,10 @@ struct ActSource {
   HQ_DEV float scale(int t, int g) const { return SRC == GLOBAL ? ((const float *)xs[t])[g] : ls[t * ng + g]; }
 };
 
-template <int PACK, int T, bool WC, int SRC, int RL>
+template <int PACK, int T, bool WC, int SRC, int RL, int U1>
 struct RelaxedChunk {
   static constexpr bool LATE = T > 1 && SRC == STAGED;
-  static constexpr int U = T == 1 ? 4 : (LATE || T == 2 ? 2 : 1);
+  static constexpr int U = T == 1 ? U1 : (LATE || T == 2 ? 2 : 1);  // U1: 4, or 2 (relaxed_pairs_of_steps)
   static constexpr int UX = LATE ? 1 : U;  // steps of activations a chunk holds (none read when LATE)
   // One token of int8 (PAIRED): a step's weights are read as whole cache lines by non-temporal loads.  Lane j of a
   // row takes the 16 bytes at 16 j of the step's first half (group j / 2's half j % 2) and at RL 16 + 16 j of its
@@ -348,7 +354,7 @@ struct RelaxedChunk {
 
 // the relaxed_threads / RL rows of tile `blk` of job `jb` (its row range cut into tiles in order).  STAGED: first
 // make the block's LDS copy of the activations, while the first weights are in flight
-template <int PACK, int T, bool WC, int SRC, int RL>
+template <int PACK, int T, bool WC, int SRC, int RL, int U1>
 HQ_DEV void relaxed_tile(const Job &J, int blk, char *lds) {
   const int lane = threadIdx.x & (RL - 1);
   constexpr int rows = relaxed_threads(T, SRC == STAGED) / RL;
@@ -380,7 +386,7 @@ HQ_DEV void relaxed_tile(const Job &J, int blk, char *lds) {
   float acc[T];
 #pragma unroll
   for (int t = 0; t < T; t++) acc[t] = 0.0f;
-  using Chunk = RelaxedChunk<PACK, T, WC, SRC, RL>;
+  using Chunk = RelaxedChunk<PACK, T, WC, SRC, RL, U1>;
   constexpr int U = Chunk::U;
   const int steps = (ng4 + RL - 1) / RL;
   Chunk a, b;
@@ -478,7 +484,7 @@ HQ_DEV void relaxed_tile(const Job &J, int blk, char *lds) {
 // other jobs' pieces read theirs.  PRE 2: every piece is the first job's (no other path in the kernel: measured
 // 0.05 us a launch shorter than PRE 1).  The activations and their scales are `frame` bytes a token apart (the tile
 // kinds' one stride).
-template <int PACK, int T, bool WC, int SRC, int RL, bool BY, int PRE>
+template <int PACK, int T, bool WC, int SRC, int RL, bool BY, int PRE, int U1>
 __global__ __launch_bounds__(relaxed_threads(T, SRC == STAGED)) void gemv_relaxed(
     const char *xq, const char *xs, const char *wq, const char *ws, int32_t n, int32_t r0, int32_t r1, int32_t pr,
     int32_t frame, char *out, int64_t os, const char *wc, GemvBatch batch) {
@@ -487,13 +493,13 @@ __global__ __launch_bounds__(relaxed_threads(T, SRC == STAGED)) void gemv_relaxe
     const int a = r0 + (int)blockIdx.y * pr;
     if (PRE == 2 || a < r1) {
       const Job J{out, xq, xs, wq, ws, wc, n, a, min(a + pr, r1), T, os, frame, frame, 0};
-      relaxed_tile<PACK, T, WC, SRC, RL>(J, (int)blockIdx.x, lds);
+      relaxed_tile<PACK, T, WC, SRC, RL, U1>(J, (int)blockIdx.x, lds);
       return;
     }
   }
   int jb, blk;
   block_job<BY>(batch, jb, blk);
-  relaxed_tile<PACK, T, WC, SRC, RL>(batch.job[jb], blk, lds);
+  relaxed_tile<PACK, T, WC, SRC, RL, U1>(batch.job[jb], blk, lds);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -848,21 +854,21 @@ HQ_HOST_DEV constexpr size_t ternary_stage_bytes(int T, int n) { return (size_t)
 
 // lead_r1, pr: the end of the rows of the job whose pieces come first (b.job[0] is its first piece), and the rows a
 // piece (the arguments PRE reads)
-template <int PACK, int T, int SRC, bool BY, int PRE>
+template <int PACK, int T, int SRC, bool BY, int PRE, int U1>
 void launch_relaxed_by(const GemvBatch &b, dim3 grid, int32_t lead_r1, int32_t pr, bool wc, int lanes, size_t lds,
                        hipStream_t s) {
   const dim3 block(relaxed_threads(T, SRC == STAGED));
   const Job &J = b.job[0];
   const int32_t frame = (int32_t)J.frame;  // (PRE: J.frame == J.sframe, below 2^31)
   if (lanes == 32) {
-    if (wc) hipLaunchKernelGGL((gemv_relaxed<PACK, T, true, SRC, 32, BY, PRE>), grid, block, lds, s, J.xq, J.xs, J.wq,
+    if (wc) hipLaunchKernelGGL((gemv_relaxed<PACK, T, true, SRC, 32, BY, PRE, U1>), grid, block, lds, s, J.xq, J.xs, J.wq,
                                J.ws, J.n, J.r0, lead_r1, pr, frame, J.out, J.os, J.wc, b);
-    else hipLaunchKernelGGL((gemv_relaxed<PACK, T, false, SRC, 32, BY, PRE>), grid, block, lds, s, J.xq, J.xs, J.wq,
+    else hipLaunchKernelGGL((gemv_relaxed<PACK, T, false, SRC, 32, BY, PRE, U1>), grid, block, lds, s, J.xq, J.xs, J.wq,
                             J.ws, J.n, J.r0, lead_r1, pr, frame, J.out, J.os, J.wc, b);
   } else {
-    if (wc) hipLaunchKernelGGL((gemv_relaxed<PACK, T, true, SRC, 16, BY, PRE>), grid, block, lds, s, J.xq, J.xs, J.wq,
+    if (wc) hipLaunchKernelGGL((gemv_relaxed<PACK, T, true, SRC, 16, BY, PRE, U1>), grid, block, lds, s, J.xq, J.xs, J.wq,
                                J.ws, J.n, J.r0, lead_r1, pr, frame, J.out, J.os, J.wc, b);
-    else hipLaunchKernelGGL((gemv_relaxed<PACK, T, false, SRC, 16, BY, PRE>), grid, block, lds, s, J.xq, J.xs, J.wq,
+    else hipLaunchKernelGGL((gemv_relaxed<PACK, T, false, SRC, 16, BY, PRE, U1>), grid, block, lds, s, J.xq, J.xs, J.wq,
                             J.ws, J.n, J.r0, lead_r1, pr, frame, J.out, J.os, J.wc, b);
   }
 }
@@ -872,12 +878,20 @@ hipError_t launch_relaxed(const GemvBatch &b, dim3 grid, const JobPieces &p, boo
   // PRE takes one stride for a token's activations and scales (the tile kinds' frame; one token: none read)
   const Job &J = b.job[0];
   const bool pre = p.by && (T == 1 || (J.frame == J.sframe && J.frame >= 0 && J.frame <= INT32_MAX));
-  if (pre && p.lead_pieces == b.njobs)
-    launch_relaxed_by<PACK, T, SRC, true, 2>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
+  if (T == 1 && lanes == 32 && relaxed_pairs_of_steps(PACK == 8 ? Q8R : Q6R, T, J.n)) {
+    // (T == 1 ? 2 : 4: the kernels of 2..4 tokens are never made with U1 = 2)
+    if (pre && p.lead_pieces == b.njobs)
+      launch_relaxed_by<PACK, T, SRC, true, 2, T == 1 ? 2 : 4>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
+    else if (pre)
+      launch_relaxed_by<PACK, T, SRC, true, 1, T == 1 ? 2 : 4>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
+    else if (p.by) launch_relaxed_by<PACK, T, SRC, true, 0, T == 1 ? 2 : 4>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
+    else launch_relaxed_by<PACK, T, SRC, false, 0, T == 1 ? 2 : 4>(b, grid, 0, 0, wc, lanes, lds, s);
+  } else if (pre && p.lead_pieces == b.njobs)
+    launch_relaxed_by<PACK, T, SRC, true, 2, 4>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
   else if (pre)
-    launch_relaxed_by<PACK, T, SRC, true, 1>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
-  else if (p.by) launch_relaxed_by<PACK, T, SRC, true, 0>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
-  else launch_relaxed_by<PACK, T, SRC, false, 0>(b, grid, 0, 0, wc, lanes, lds, s);
+    launch_relaxed_by<PACK, T, SRC, true, 1, 4>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
+  else if (p.by) launch_relaxed_by<PACK, T, SRC, true, 0, 4>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
+  else launch_relaxed_by<PACK, T, SRC, false, 0, 4>(b, grid, 0, 0, wc, lanes, lds, s);
   return hipGetLastError();
 }
 

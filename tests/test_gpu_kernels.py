@@ -322,12 +322,14 @@ def test_relaxed_tokens_long_rows(pkg, k, arena, oracle, count, packing, ng):
                                                 f"{first_difference(got[t], want)}"
 
 
-@pytest.mark.parametrize("count,ng,packing", [(1, 128, "int8"), (1, 256, "int8"), (2, 259, "int8"), (3, 259, "int8"),
-                                               (4, 259, "int8"), (2, 259, "int6"), (3, 259, "int6")])
+@pytest.mark.parametrize("count,ng,packing", [(1, 128, "int8"), (1, 256, "int8"), (1, 320, "int8"), (1, 448, "int8"),
+                                               (2, 259, "int8"), (3, 259, "int8"), (4, 259, "int8"), (2, 259, "int6"),
+                                               (3, 259, "int6")])
 def test_relaxed_wide_rows(pkg, k, arena, oracle, count, ng, packing):
-    """The launches whose relaxed rows are 32 lanes (one int8 token on rows of 4096 or 8192 values; 2..4 tokens on
-    rows past 8192 — 2 and 3 tokens of 8288 values staged in LDS, 4 read through the caches, with 3 groups past the
-    fours): rows cut inside the 4-row blocks at both ends, the corrections given, derived and moved"""
+    """The launches whose relaxed rows are 32 lanes (one int8 token on rows of 4096 or 8192 values, and of 10240 or
+    14336 in chunks of two steps; 2..4 tokens on rows past 8192 — 2 and 3 tokens of 8288 values staged in LDS, 4 read
+    through the caches, with 3 groups past the fours): rows cut inside the 4-row blocks at both ends, the corrections
+    given, derived and moved"""
     from pyodide_llm_amd import jobs
     rng = np.random.default_rng(71 + count + ng)
     rows = 37
