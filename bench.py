@@ -958,7 +958,7 @@ def main():
                    "step_bytes": headline["step_bytes"], "parallelism": "1 GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_per_launch(),
-                     "kernel": "gemv_relaxed<8,1,false,0,L> (L = 32 lanes a row; 16 for the down projection)",
+                     "kernel": "gemv_relaxed<8,1,false,0,32,…> (32 lanes a row; chunks of 4 steps, of 2 for the down projection)",
                      "avg_launch_us": round(separate["gemv_avg_launch_us"], 3),
                      "bytes_per_launch": round(separate["gemv_bytes_per_launch"])},
         "cpu_baseline": cpu,
