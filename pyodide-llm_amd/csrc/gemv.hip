@@ -660,9 +660,54 @@ HQ_DEV uint32_t plane_codes(uint32_t w) {
   return codes<P>(w);
 }
 
+// Ternary activations staged in nibbles (NIB: ternary weights, activations in LDS).  A code dword w (bytes c0..c0+3
+// of a block, plane p at bits 2p of each byte) gives two words of eight 4-bit codes with one AND each: w & 0x33333333
+// (nibble 2j: plane 0 of byte c0 + j, nibble 2j + 1: plane 2) and (w >> 2) & 0x33333333 (planes 1 and 3).  The
+// staging writes each activation a = 16 hi + lo (hi = a >> 4 in -8..7, lo = a & 15 in 0..15) into the same nibble
+// places, so that sum(code a) = 16 v_dot8_i32_i4(codes, hi) + v_dot8_u32_u4(codes, lo): the same integer, from two
+// dot instructions and three to take a dword's codes apart instead of four and seven.  A staged block of 64 bytes
+// holds for each dword column j (bytes c0 = 4 j ..) the words {lo of planes 0 / 2, hi of 0 / 2, lo of 1 / 3, hi of
+// 1 / 3}; from the interleaved block's plane dwords P0..P3 of column j:
+HQ_DEV uint4 nibble_column(uint32_t p0, uint32_t p1, uint32_t p2, uint32_t p3) {
+  constexpr uint32_t M = 0x0f0f0f0fu;
+  return make_uint4((p0 & M) | ((p2 << 4) & ~M), ((p0 >> 4) & M) | (p2 & ~M), (p1 & M) | ((p3 << 4) & ~M),
+                    ((p1 >> 4) & M) | (p3 & ~M));
+}
+HQ_DEV int32_t nibble_dot(uint32_t w, const uint4 &a, int32_t lo_in, int32_t &hi) {
+  const uint32_t n02 = w & 0x33333333u, n13 = (w >> 2) & 0x33333333u;
+  uint32_t lo = __builtin_amdgcn_udot8(n02, a.x, (uint32_t)lo_in, false);
+  lo = __builtin_amdgcn_udot8(n13, a.z, lo, false);
+  hi = __builtin_amdgcn_sdot8((int32_t)n02, (int32_t)a.y, hi, false);
+  hi = __builtin_amdgcn_sdot8((int32_t)n13, (int32_t)a.w, hi, false);
+  return (int32_t)lo;
+}
+
 template <int T, bool STAGE, int L, bool BIN>
 HQ_DEV void ternary_step(FoldL<T, L> &f, const TernaryActs<T, STAGE> &A, const uint32_t w[8], float d, int g,
                          bool valid, int buf, int slot, int lane, float acc[T]) {
+  constexpr bool NIB = STAGE && !BIN;
+  if constexpr (NIB) {
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+      const char *xb = A.group(t, g);
+      const float *xs = (const float *)A.area(t);
+      const float4 sc = *(const float4 *)(xs + 4 * g);
+      const int4 su = *(const int4 *)((const int32_t *)(xs + (A.n >> 5)) + 4 * g);
+      const float scale[4] = {sc.x, sc.y, sc.z, sc.w};
+      const int32_t sums[4] = {su.x, su.y, su.z, su.w};
+#pragma unroll
+      for (int k = 0; k < 4; k++) {  // part k: block k / 2, columns 2 (k % 2), + 1 (code dwords 2k, 2k + 1)
+        const uint4 a0 = ld16(xb + 32 * k), a1 = ld16(xb + 32 * k + 16);
+        int32_t hi = 0;
+        int32_t lo = nibble_dot(w[2 * k], a0, sums[k], hi);
+        lo = nibble_dot(w[2 * k + 1], a1, lo, hi);
+        const int32_t dot = (int32_t)((uint32_t)lo + ((uint32_t)hi << 4));  // wrapping, as the dot4 chain adds
+        f.v[buf][slot][t][k][lane] = valid ? fmul(fmul((float)dot, scale[k]), d) : 0.0f;
+      }
+    }
+    fold_step_l<T, L>(f, buf, slot, lane, acc);
+    return;
+  }
 #pragma unroll
   for (int t = 0; t < T; t++) {
     const char *xb = A.group(t, g);
@@ -779,7 +824,36 @@ HQ_DEV void ternary_rows(const Job &J, int blk, char *acts, FoldL<T, L> *fold) {
   // the first codes in flight during the staging: the staged bytes' stores then wait for them too (the memory
   // counter is in order), but the two round trips overlap instead of following one another
   a.load(wrow, srow, 0, lane, groups);
-  if (STAGE) {
+  if (STAGE && !BIN) {
+    // every token's n bytes (a group's 128 in 144) as nibbles (nibble_column: a 64-byte block a thread at a time, two
+    // in flight), then its n/32 scales and n/32 sums, 16 bytes a thread at a time
+    const int per = ternary_token_bytes(J.n), nb = J.n / 64, gb = groups * kTernaryPitch, area = J.n / 64;
+    for (int t = 0; t < T; t++) {
+      for (int base = 0; base < nb; base += 2 * kTernThreads) {
+        uint4 v[2][4];
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+          const int b = base + u * kTernThreads + (int)threadIdx.x;
+          if (b < nb)
+#pragma unroll
+            for (int q = 0; q < 4; q++) v[u][q] = ld16(J.xq + t * J.frame + 64 * b + 16 * q);
+        }
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+          const int b = base + u * kTernThreads + (int)threadIdx.x;
+          if (b < nb) {
+            uint4 *dst = (uint4 *)(acts + t * per + (b >> 1) * kTernaryPitch + 64 * (b & 1));
+            dst[0] = nibble_column(v[u][0].x, v[u][1].x, v[u][2].x, v[u][3].x);
+            dst[1] = nibble_column(v[u][0].y, v[u][1].y, v[u][2].y, v[u][3].y);
+            dst[2] = nibble_column(v[u][0].z, v[u][1].z, v[u][2].z, v[u][3].z);
+            dst[3] = nibble_column(v[u][0].w, v[u][1].w, v[u][2].w, v[u][3].w);
+          }
+        }
+      }
+      for (int c = (int)threadIdx.x; c < area; c += kTernThreads)
+        *(uint4 *)(acts + t * per + gb + 16 * c) = ld16(J.xs + t * J.sframe + 16 * c);
+    }
+  } else if (STAGE) {
     // every token's n bytes (a group's 128 in 144), then its n/32 scales and n/32 sums: 16 bytes a thread at a time,
     // eight loads of a thread in flight before their stores
     const int per = ternary_token_bytes(J.n), chunks = (J.n + J.n / 4) / 16, gb = groups * kTernaryPitch;
