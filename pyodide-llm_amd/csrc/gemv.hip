@@ -794,13 +794,15 @@ struct TernaryChunk {
   }
 };
 
-constexpr int kTernThreads = 256;  // a block's threads: kTernThreads / L rows
+// A ternary block is W waves, 64 W / L rows: 4, or for one token 5 or 6, the count chosen a launch by ternary_waves
+constexpr int kTernMaxWaves = 6;
 // rows of L lanes (16: 16 rows a block; 32 for long rows: twice the waves on the same rows)
-template <int T, bool STAGE, int L, bool BIN>
+template <int T, bool STAGE, int L, bool BIN, int W>
 HQ_DEV void ternary_rows(const Job &J, int blk, char *acts, FoldL<T, L> *fold) {
   const int lane = threadIdx.x & (L - 1);
   const int wave = threadIdx.x >> 6, slot = (threadIdx.x & 63) / L;
-  const int row_u = J.r0 + blk * (kTernThreads / L) + threadIdx.x / L;
+  constexpr int threads = 64 * W;
+  const int row_u = J.r0 + blk * (threads / L) + threadIdx.x / L;
   const bool live = row_u < J.r1;
   const int row = live ? row_u : J.r1 - 1;
   const int groups = J.n >> 7;
@@ -829,18 +831,18 @@ HQ_DEV void ternary_rows(const Job &J, int blk, char *acts, FoldL<T, L> *fold) {
     // in flight), then its n/32 scales and n/32 sums, 16 bytes a thread at a time
     const int per = ternary_token_bytes(J.n), nb = J.n / 64, gb = groups * kTernaryPitch, area = J.n / 64;
     for (int t = 0; t < T; t++) {
-      for (int base = 0; base < nb; base += 2 * kTernThreads) {
+      for (int base = 0; base < nb; base += 2 * threads) {
         uint4 v[2][4];
 #pragma unroll
         for (int u = 0; u < 2; u++) {
-          const int b = base + u * kTernThreads + (int)threadIdx.x;
+          const int b = base + u * threads + (int)threadIdx.x;
           if (b < nb)
 #pragma unroll
             for (int q = 0; q < 4; q++) v[u][q] = ld16(J.xq + t * J.frame + 64 * b + 16 * q);
         }
 #pragma unroll
         for (int u = 0; u < 2; u++) {
-          const int b = base + u * kTernThreads + (int)threadIdx.x;
+          const int b = base + u * threads + (int)threadIdx.x;
           if (b < nb) {
             uint4 *dst = (uint4 *)(acts + t * per + (b >> 1) * kTernaryPitch + 64 * (b & 1));
             dst[0] = nibble_column(v[u][0].x, v[u][1].x, v[u][2].x, v[u][3].x);
@@ -850,7 +852,7 @@ HQ_DEV void ternary_rows(const Job &J, int blk, char *acts, FoldL<T, L> *fold) {
           }
         }
       }
-      for (int c = (int)threadIdx.x; c < area; c += kTernThreads)
+      for (int c = (int)threadIdx.x; c < area; c += threads)
         *(uint4 *)(acts + t * per + gb + 16 * c) = ld16(J.xs + t * J.sframe + 16 * c);
     }
   } else if (STAGE) {
@@ -859,17 +861,17 @@ HQ_DEV void ternary_rows(const Job &J, int blk, char *acts, FoldL<T, L> *fold) {
     const int per = ternary_token_bytes(J.n), chunks = (J.n + J.n / 4) / 16, gb = groups * kTernaryPitch;
     constexpr int K = 8;
     for (int t = 0; t < T; t++)
-      for (int base = 0; base < chunks; base += K * kTernThreads) {
+      for (int base = 0; base < chunks; base += K * threads) {
         uint4 v[K];
 #pragma unroll
         for (int u = 0; u < K; u++) {
-          const int o = 16 * (base + u * kTernThreads + (int)threadIdx.x);
+          const int o = 16 * (base + u * threads + (int)threadIdx.x);
           if (o < J.n) v[u] = ld16(J.xq + t * J.frame + o);
           else if (o < J.n + J.n / 4) v[u] = ld16(J.xs + t * J.sframe + (o - J.n));
         }
 #pragma unroll
         for (int u = 0; u < K; u++) {
-          const int o = 16 * (base + u * kTernThreads + (int)threadIdx.x);
+          const int o = 16 * (base + u * threads + (int)threadIdx.x);
           if (o < J.n) *(uint4 *)(acts + t * per + (o >> 7) * kTernaryPitch + (o & 127)) = v[u];
           else if (o < J.n + J.n / 4) *(uint4 *)(acts + t * per + gb + (o - J.n)) = v[u];
         }
@@ -897,23 +899,23 @@ HQ_DEV void ternary_rows(const Job &J, int blk, char *acts, FoldL<T, L> *fold) {
 }
 
 // PRE (one token, a job a grid row), as gemv_relaxed's: the first job's pieces from the preloaded arguments
-template <int T, bool STAGE, int L, bool BIN, bool BY, int PRE>
-__global__ __launch_bounds__(kTernThreads) void gemv_ternary(char *out, const char *xq, const char *xs, const char *wq,
-                                                             const char *ws, int32_t n, int32_t r0, int32_t r1,
-                                                             int32_t pr, GemvBatch batch) {
+template <int T, bool STAGE, int L, bool BIN, bool BY, int PRE, int W>
+__global__ __launch_bounds__(64 * W) void gemv_ternary(char *out, const char *xq, const char *xs, const char *wq,
+                                                       const char *ws, int32_t n, int32_t r0, int32_t r1, int32_t pr,
+                                                       GemvBatch batch) {
   extern __shared__ __align__(16) char acts[];
-  __shared__ FoldL<T, L> fold[kTernThreads / 64];
+  __shared__ FoldL<T, L> fold[W];
   if (PRE) {
     const int a = r0 + (int)blockIdx.y * pr;
     if (PRE == 2 || a < r1) {
       const Job J{out, xq, xs, wq, ws, nullptr, n, a, min(a + pr, r1), 1, 0, 0, 0, 0};
-      ternary_rows<T, STAGE, L, BIN>(J, (int)blockIdx.x, acts, fold);
+      ternary_rows<T, STAGE, L, BIN, W>(J, (int)blockIdx.x, acts, fold);
       return;
     }
   }
   int jb, blk;
   block_job<BY>(batch, jb, blk);
-  ternary_rows<T, STAGE, L, BIN>(batch.job[jb], blk, acts, fold);
+  ternary_rows<T, STAGE, L, BIN, W>(batch.job[jb], blk, acts, fold);
 }
 
 // the LDS a ternary block stages for T tokens of n activations (beyond: read through the L1)
@@ -970,55 +972,62 @@ hipError_t launch_relaxed(const GemvBatch &b, dim3 grid, const JobPieces &p, boo
 }
 
 // ternary / binary: rows of ternary_lanes(n) lanes, the activations staged in LDS when they fit
-template <int T, bool BIN, bool BY, int PRE>
-void launch_signs_by(const GemvBatch &b, dim3 grid, int32_t lead_r1, int32_t pr, hipStream_t s) {
+template <int T, bool BIN, bool BY, int PRE, int W>
+void launch_signs_w(const GemvBatch &b, dim3 grid, int32_t lead_r1, int32_t pr, hipStream_t s) {
   const Job &J = b.job[0];
   int nmax = 0;
   for (int j = 0; j < b.njobs; j++) nmax = b.job[j].n > nmax ? b.job[j].n : nmax;
   const size_t bytes = ternary_stage_bytes(T, nmax);
   const bool stage = bytes <= kTernaryStageMax;
-  const dim3 block(kTernThreads);
+  const dim3 block(64 * W);
   switch (ternary_lanes(nmax)) {
   case 32:
     if (stage)
-      hipLaunchKernelGGL((gemv_ternary<T, true, 32, BIN, BY, PRE>), grid, block, bytes, s, J.out, J.xq, J.xs, J.wq, J.ws,
+      hipLaunchKernelGGL((gemv_ternary<T, true, 32, BIN, BY, PRE, W>), grid, block, bytes, s, J.out, J.xq, J.xs, J.wq, J.ws,
                          J.n, J.r0, lead_r1, pr, b);
     else
-      hipLaunchKernelGGL((gemv_ternary<T, false, 32, BIN, BY, PRE>), grid, block, 0, s, J.out, J.xq, J.xs, J.wq, J.ws,
+      hipLaunchKernelGGL((gemv_ternary<T, false, 32, BIN, BY, PRE, W>), grid, block, 0, s, J.out, J.xq, J.xs, J.wq, J.ws,
                          J.n, J.r0, lead_r1, pr, b);
     break;
   case 8:
     if (stage)
-      hipLaunchKernelGGL((gemv_ternary<T, true, 8, BIN, BY, PRE>), grid, block, bytes, s, J.out, J.xq, J.xs, J.wq, J.ws,
+      hipLaunchKernelGGL((gemv_ternary<T, true, 8, BIN, BY, PRE, W>), grid, block, bytes, s, J.out, J.xq, J.xs, J.wq, J.ws,
                          J.n, J.r0, lead_r1, pr, b);
     else
-      hipLaunchKernelGGL((gemv_ternary<T, false, 8, BIN, BY, PRE>), grid, block, 0, s, J.out, J.xq, J.xs, J.wq, J.ws,
+      hipLaunchKernelGGL((gemv_ternary<T, false, 8, BIN, BY, PRE, W>), grid, block, 0, s, J.out, J.xq, J.xs, J.wq, J.ws,
                          J.n, J.r0, lead_r1, pr, b);
     break;
   default:
     if (stage)
-      hipLaunchKernelGGL((gemv_ternary<T, true, 16, BIN, BY, PRE>), grid, block, bytes, s, J.out, J.xq, J.xs, J.wq, J.ws,
+      hipLaunchKernelGGL((gemv_ternary<T, true, 16, BIN, BY, PRE, W>), grid, block, bytes, s, J.out, J.xq, J.xs, J.wq, J.ws,
                          J.n, J.r0, lead_r1, pr, b);
     else
-      hipLaunchKernelGGL((gemv_ternary<T, false, 16, BIN, BY, PRE>), grid, block, 0, s, J.out, J.xq, J.xs, J.wq, J.ws,
+      hipLaunchKernelGGL((gemv_ternary<T, false, 16, BIN, BY, PRE, W>), grid, block, 0, s, J.out, J.xq, J.xs, J.wq, J.ws,
                          J.n, J.r0, lead_r1, pr, b);
   }
 }
+// (2..4 tokens: 4 waves; the kernels of 5 and 6 are made for one token only)
+template <int T, bool BIN, bool BY, int PRE>
+void launch_signs_by(const GemvBatch &b, dim3 grid, int threads, int32_t lead_r1, int32_t pr, hipStream_t s) {
+  if (threads == 320) launch_signs_w<T, BIN, BY, PRE, T == 1 ? 5 : 4>(b, grid, lead_r1, pr, s);
+  else if (threads == 384) launch_signs_w<T, BIN, BY, PRE, T == 1 ? 6 : 4>(b, grid, lead_r1, pr, s);
+  else launch_signs_w<T, BIN, BY, PRE, 4>(b, grid, lead_r1, pr, s);
+}
 template <int T, bool BIN>
-hipError_t launch_signs(const GemvBatch &b, dim3 grid, const JobPieces &p, hipStream_t s) {
+hipError_t launch_signs(const GemvBatch &b, dim3 grid, int threads, const JobPieces &p, hipStream_t s) {
   if (T == 1 && p.by && p.lead_pieces == b.njobs)
-    launch_signs_by<T, BIN, true, T == 1 ? 2 : 0>(b, grid, p.lead_r1, p.rows, s);
+    launch_signs_by<T, BIN, true, T == 1 ? 2 : 0>(b, grid, threads, p.lead_r1, p.rows, s);
   else if (T == 1 && p.by)
-    launch_signs_by<T, BIN, true, T == 1 ? 1 : 0>(b, grid, p.lead_r1, p.rows, s);
-  else if (p.by) launch_signs_by<T, BIN, true, 0>(b, grid, p.lead_r1, p.rows, s);
-  else launch_signs_by<T, BIN, false, 0>(b, grid, 0, 0, s);
+    launch_signs_by<T, BIN, true, T == 1 ? 1 : 0>(b, grid, threads, p.lead_r1, p.rows, s);
+  else if (p.by) launch_signs_by<T, BIN, true, 0>(b, grid, threads, p.lead_r1, p.rows, s);
+  else launch_signs_by<T, BIN, false, 0>(b, grid, threads, 0, 0, s);
   return hipGetLastError();
 }
 
 // grid: (blocks) with the jobs found through block0, or (blocks a piece, pieces) when p.by
 template <int T>
 hipError_t launch_t(Kind kind, const GemvBatch &b, dim3 grid, const JobPieces &p, bool wc, int src, int lanes,
-                    size_t lds, hipStream_t s) {
+                    size_t lds, int tern_threads, hipStream_t s) {
   const dim3 block(256);
   switch (kind) {
   case Q8R:
@@ -1032,9 +1041,9 @@ hipError_t launch_t(Kind kind, const GemvBatch &b, dim3 grid, const JobPieces &p
   case Q8: hipLaunchKernelGGL((gemv_plain<8, T>), grid, block, 0, s, b); break;
   case Q6: hipLaunchKernelGGL((gemv_plain<6, T>), grid, block, 0, s, b); break;
   case T2R:
-  case T2: return launch_signs<T, false>(b, grid, p, s);
+  case T2: return launch_signs<T, false>(b, grid, tern_threads, p, s);
   case B1R:
-  case B1: return launch_signs<T, true>(b, grid, p, s);
+  case B1: return launch_signs<T, true>(b, grid, tern_threads, p, s);
   default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -1050,6 +1059,27 @@ hipError_t launch_t(Kind kind, const GemvBatch &b, dim3 grid, const JobPieces &p
 constexpr size_t kGemvStageMax = 80 * 1024;
 
 namespace {
+// A ternary / binary launch's waves a block (one token: 4 to 6; more: 4): the count whose blocks come closest to
+// whole rounds of one block a compute unit (the last round's empty slots the fewest, the fewer waves on a tie).
+// Measured on the 27B shapes, A/B on one box: the down projection's 5120 rows in 5-wave blocks (512 blocks, two
+// rounds) 2.76 -> 2.99 TB/s against 4 waves (640: three rounds, the last a quarter full), gate+up's 2 x 17408 in
+// 6-wave blocks (726, three rounds) 4.0 -> 4.18.
+int ternary_waves(const Job *jobs, int32_t njobs, int lanes) {
+  const int64_t cus = cu_count();
+  int best = 4;
+  double best_fill = 0.0;
+  if (jobs[0].count != 1) return 4;
+  for (int w = 4; w <= kTernMaxWaves; w++) {
+    const int rpb = 64 * w / lanes;
+    int64_t blocks = 0;
+    for (int j = 0; j < njobs; j++) blocks += (jobs[j].r1 - jobs[j].r0 + rpb - 1) / rpb;
+    if (blocks == 0) return 4;
+    const double fill = (double)blocks / (double)(((blocks + cus - 1) / cus) * cus);
+    if (fill > best_fill + 1e-9) best = w, best_fill = fill;
+  }
+  return best;
+}
+
 hipError_t launch_batch(Kind kind, const Job *jobs, int32_t njobs, hipStream_t s) {
   if (njobs < 1 || njobs > kMaxJobs) return hipErrorInvalidValue;
   GemvBatch b{};
@@ -1061,7 +1091,8 @@ hipError_t launch_batch(Kind kind, const Job *jobs, int32_t njobs, hipStream_t s
   const size_t lds = (size_t)act_lds_bytes(T, nmax);
   // staged in LDS for 2..4 tokens (each row's lanes read every token's activations: measured 4 % faster at M = 4)
   const int src = T > 1 && lds <= kGemvStageMax ? STAGED : GLOBAL;
-  const int rpb = signs_kind(kind) ? kTernThreads / ternary_lanes(nmax)
+  const int tern_threads = signs_kind(kind) ? 64 * ternary_waves(jobs, njobs, ternary_lanes(nmax)) : 0;
+  const int rpb = signs_kind(kind) ? tern_threads / ternary_lanes(nmax)
                   : relaxed          ? relaxed_threads(T, src == STAGED) / lanes
                                      : kRowsPerBlock;
   for (int j = 0; j < njobs; j++) {
@@ -1105,10 +1136,10 @@ hipError_t launch_batch(Kind kind, const Job *jobs, int32_t njobs, hipStream_t s
   }
   const bool wc = jobs[0].wc != nullptr;
   switch (T) {
-  case 1: return launch_t<1>(kind, b, grid, pc, wc, src, lanes, lds, s);
-  case 2: return launch_t<2>(kind, b, grid, pc, wc, src, lanes, lds, s);
-  case 3: return launch_t<3>(kind, b, grid, pc, wc, src, lanes, lds, s);
-  case 4: return launch_t<4>(kind, b, grid, pc, wc, src, lanes, lds, s);
+  case 1: return launch_t<1>(kind, b, grid, pc, wc, src, lanes, lds, tern_threads, s);
+  case 2: return launch_t<2>(kind, b, grid, pc, wc, src, lanes, lds, tern_threads, s);
+  case 3: return launch_t<3>(kind, b, grid, pc, wc, src, lanes, lds, tern_threads, s);
+  case 4: return launch_t<4>(kind, b, grid, pc, wc, src, lanes, lds, tern_threads, s);
   default: return hipErrorInvalidValue;
   }
 }
