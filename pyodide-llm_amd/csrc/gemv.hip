@@ -80,6 +80,9 @@ constexpr int kRowsPerBlock = 16;
 // 256 threads, 1.96 with 512; 1024 threads, whose waves get 128 registers, 2.26)
 constexpr int kRelaxedThreads = 128;
 HQ_HOST_DEV constexpr int relaxed_threads(int T, bool staged) { return T > 1 && staged ? 512 : kRelaxedThreads; }
+// One token's launches whose blocks of kRelaxedThreads come short of whole rounds of the compute units take blocks of
+// one wave where those fill them better (relaxed_block_threads)
+constexpr int kOneTokenSmall = 64;
 // Lanes a relaxed row: 32 lanes give a launch twice the waves, each lane half the steps.  Measured phase by phase
 // streaming from HBM (configs 1-4's decode shapes, int8 and int6, 16 against 32 lanes): one int8 token, 32 lanes are
 // faster where a row is 4096 or 8192 bytes (8B q/k/v 7.7 -> 7.1 us, o 6.2 -> 5.8, gate+up 25.3 -> 23.5, lm-head 97 ->
@@ -354,10 +357,10 @@ struct RelaxedChunk {
 
 // the relaxed_threads / RL rows of tile `blk` of job `jb` (its row range cut into tiles in order).  STAGED: first
 // make the block's LDS copy of the activations, while the first weights are in flight
-template <int PACK, int T, bool WC, int SRC, int RL, int U1>
+template <int PACK, int T, bool WC, int SRC, int RL, int U1, int NT>
 HQ_DEV void relaxed_tile(const Job &J, int blk, char *lds) {
   const int lane = threadIdx.x & (RL - 1);
-  constexpr int rows = relaxed_threads(T, SRC == STAGED) / RL;
+  constexpr int rows = NT / RL;
   const int row_u = J.r0 + blk * rows + (int)(threadIdx.x / RL);
   const bool live = row_u < J.r1;
   const int row = live ? row_u : J.r1 - 1;
@@ -484,8 +487,8 @@ HQ_DEV void relaxed_tile(const Job &J, int blk, char *lds) {
 // other jobs' pieces read theirs.  PRE 2: every piece is the first job's (no other path in the kernel: measured
 // 0.05 us a launch shorter than PRE 1).  The activations and their scales are `frame` bytes a token apart (the tile
 // kinds' one stride).
-template <int PACK, int T, bool WC, int SRC, int RL, bool BY, int PRE, int U1>
-__global__ __launch_bounds__(relaxed_threads(T, SRC == STAGED)) void gemv_relaxed(
+template <int PACK, int T, bool WC, int SRC, int RL, bool BY, int PRE, int U1, int NT>
+__global__ __launch_bounds__(NT) void gemv_relaxed(
     const char *xq, const char *xs, const char *wq, const char *ws, int32_t n, int32_t r0, int32_t r1, int32_t pr,
     int32_t frame, char *out, int64_t os, const char *wc, GemvBatch batch) {
   extern __shared__ __align__(16) char lds[];
@@ -493,13 +496,13 @@ __global__ __launch_bounds__(relaxed_threads(T, SRC == STAGED)) void gemv_relaxe
     const int a = r0 + (int)blockIdx.y * pr;
     if (PRE == 2 || a < r1) {
       const Job J{out, xq, xs, wq, ws, wc, n, a, min(a + pr, r1), T, os, frame, frame, 0};
-      relaxed_tile<PACK, T, WC, SRC, RL, U1>(J, (int)blockIdx.x, lds);
+      relaxed_tile<PACK, T, WC, SRC, RL, U1, NT>(J, (int)blockIdx.x, lds);
       return;
     }
   }
   int jb, blk;
   block_job<BY>(batch, jb, blk);
-  relaxed_tile<PACK, T, WC, SRC, RL, U1>(batch.job[jb], blk, lds);
+  relaxed_tile<PACK, T, WC, SRC, RL, U1, NT>(batch.job[jb], blk, lds);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -930,45 +933,55 @@ HQ_HOST_DEV constexpr size_t ternary_stage_bytes(int T, int n) { return (size_t)
 
 // lead_r1, pr: the end of the rows of the job whose pieces come first (b.job[0] is its first piece), and the rows a
 // piece (the arguments PRE reads)
-template <int PACK, int T, int SRC, bool BY, int PRE, int U1>
+template <int PACK, int T, int SRC, bool BY, int PRE, int U1, int NT>
 void launch_relaxed_by(const GemvBatch &b, dim3 grid, int32_t lead_r1, int32_t pr, bool wc, int lanes, size_t lds,
                        hipStream_t s) {
-  const dim3 block(relaxed_threads(T, SRC == STAGED));
+  const dim3 block(NT);
   const Job &J = b.job[0];
   const int32_t frame = (int32_t)J.frame;  // (PRE: J.frame == J.sframe, below 2^31)
   if (lanes == 32) {
-    if (wc) hipLaunchKernelGGL((gemv_relaxed<PACK, T, true, SRC, 32, BY, PRE, U1>), grid, block, lds, s, J.xq, J.xs, J.wq,
+    if (wc) hipLaunchKernelGGL((gemv_relaxed<PACK, T, true, SRC, 32, BY, PRE, U1, NT>), grid, block, lds, s, J.xq, J.xs, J.wq,
                                J.ws, J.n, J.r0, lead_r1, pr, frame, J.out, J.os, J.wc, b);
-    else hipLaunchKernelGGL((gemv_relaxed<PACK, T, false, SRC, 32, BY, PRE, U1>), grid, block, lds, s, J.xq, J.xs, J.wq,
+    else hipLaunchKernelGGL((gemv_relaxed<PACK, T, false, SRC, 32, BY, PRE, U1, NT>), grid, block, lds, s, J.xq, J.xs, J.wq,
                             J.ws, J.n, J.r0, lead_r1, pr, frame, J.out, J.os, J.wc, b);
   } else {
-    if (wc) hipLaunchKernelGGL((gemv_relaxed<PACK, T, true, SRC, 16, BY, PRE, U1>), grid, block, lds, s, J.xq, J.xs, J.wq,
+    if (wc) hipLaunchKernelGGL((gemv_relaxed<PACK, T, true, SRC, 16, BY, PRE, U1, NT>), grid, block, lds, s, J.xq, J.xs, J.wq,
                                J.ws, J.n, J.r0, lead_r1, pr, frame, J.out, J.os, J.wc, b);
-    else hipLaunchKernelGGL((gemv_relaxed<PACK, T, false, SRC, 16, BY, PRE, U1>), grid, block, lds, s, J.xq, J.xs, J.wq,
+    else hipLaunchKernelGGL((gemv_relaxed<PACK, T, false, SRC, 16, BY, PRE, U1, NT>), grid, block, lds, s, J.xq, J.xs, J.wq,
                             J.ws, J.n, J.r0, lead_r1, pr, frame, J.out, J.os, J.wc, b);
   }
 }
-template <int PACK, int T, int SRC>
-hipError_t launch_relaxed(const GemvBatch &b, dim3 grid, const JobPieces &p, bool wc, int lanes, size_t lds,
-                          hipStream_t s) {
+template <int PACK, int T, int SRC, int NT>
+hipError_t launch_relaxed_nt(const GemvBatch &b, dim3 grid, const JobPieces &p, bool wc, int lanes, size_t lds,
+                             hipStream_t s) {
   // PRE takes one stride for a token's activations and scales (the tile kinds' frame; one token: none read)
   const Job &J = b.job[0];
   const bool pre = p.by && (T == 1 || (J.frame == J.sframe && J.frame >= 0 && J.frame <= INT32_MAX));
   if (T == 1 && lanes == 32 && relaxed_pairs_of_steps(PACK == 8 ? Q8R : Q6R, T, J.n)) {
     // (T == 1 ? 2 : 4: the kernels of 2..4 tokens are never made with U1 = 2)
     if (pre && p.lead_pieces == b.njobs)
-      launch_relaxed_by<PACK, T, SRC, true, 2, T == 1 ? 2 : 4>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
+      launch_relaxed_by<PACK, T, SRC, true, 2, T == 1 ? 2 : 4, NT>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
     else if (pre)
-      launch_relaxed_by<PACK, T, SRC, true, 1, T == 1 ? 2 : 4>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
-    else if (p.by) launch_relaxed_by<PACK, T, SRC, true, 0, T == 1 ? 2 : 4>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
-    else launch_relaxed_by<PACK, T, SRC, false, 0, T == 1 ? 2 : 4>(b, grid, 0, 0, wc, lanes, lds, s);
+      launch_relaxed_by<PACK, T, SRC, true, 1, T == 1 ? 2 : 4, NT>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
+    else if (p.by) launch_relaxed_by<PACK, T, SRC, true, 0, T == 1 ? 2 : 4, NT>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
+    else launch_relaxed_by<PACK, T, SRC, false, 0, T == 1 ? 2 : 4, NT>(b, grid, 0, 0, wc, lanes, lds, s);
   } else if (pre && p.lead_pieces == b.njobs)
-    launch_relaxed_by<PACK, T, SRC, true, 2, 4>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
+    launch_relaxed_by<PACK, T, SRC, true, 2, 4, NT>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
   else if (pre)
-    launch_relaxed_by<PACK, T, SRC, true, 1, 4>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
-  else if (p.by) launch_relaxed_by<PACK, T, SRC, true, 0, 4>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
-  else launch_relaxed_by<PACK, T, SRC, false, 0, 4>(b, grid, 0, 0, wc, lanes, lds, s);
+    launch_relaxed_by<PACK, T, SRC, true, 1, 4, NT>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
+  else if (p.by) launch_relaxed_by<PACK, T, SRC, true, 0, 4, NT>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
+  else launch_relaxed_by<PACK, T, SRC, false, 0, 4, NT>(b, grid, 0, 0, wc, lanes, lds, s);
   return hipGetLastError();
+}
+// nt: the block's threads, relaxed_threads' or (one token) kOneTokenSmall
+template <int PACK, int T, int SRC>
+hipError_t launch_relaxed(const GemvBatch &b, dim3 grid, const JobPieces &p, bool wc, int lanes, size_t lds, int nt,
+                          hipStream_t s) {
+  constexpr int big = relaxed_threads(T, SRC == STAGED);
+  // (T == 1 ? kOneTokenSmall : big: the kernels of 2..4 tokens are never made with the small blocks)
+  if (T == 1 && nt == kOneTokenSmall)
+    return launch_relaxed_nt<PACK, T, SRC, T == 1 ? kOneTokenSmall : big>(b, grid, p, wc, lanes, lds, s);
+  return launch_relaxed_nt<PACK, T, SRC, big>(b, grid, p, wc, lanes, lds, s);
 }
 
 // ternary / binary: rows of ternary_lanes(n) lanes, the activations staged in LDS when they fit
@@ -1027,17 +1040,17 @@ hipError_t launch_signs(const GemvBatch &b, dim3 grid, int threads, const JobPie
 // grid: (blocks) with the jobs found through block0, or (blocks a piece, pieces) when p.by
 template <int T>
 hipError_t launch_t(Kind kind, const GemvBatch &b, dim3 grid, const JobPieces &p, bool wc, int src, int lanes,
-                    size_t lds, int tern_threads, hipStream_t s) {
+                    size_t lds, int tern_threads, int relaxed_nt, hipStream_t s) {
   const dim3 block(256);
   switch (kind) {
   case Q8R:
   case Q6R:
     if (kind == Q8R) {
-      if (src == STAGED) return launch_relaxed<8, T, STAGED>(b, grid, p, wc, lanes, lds, s);
-      return launch_relaxed<8, T, GLOBAL>(b, grid, p, wc, lanes, 0, s);
+      if (src == STAGED) return launch_relaxed<8, T, STAGED>(b, grid, p, wc, lanes, lds, relaxed_nt, s);
+      return launch_relaxed<8, T, GLOBAL>(b, grid, p, wc, lanes, 0, relaxed_nt, s);
     }
-    if (src == STAGED) return launch_relaxed<6, T, STAGED>(b, grid, p, wc, lanes, lds, s);
-    return launch_relaxed<6, T, GLOBAL>(b, grid, p, wc, lanes, 0, s);
+    if (src == STAGED) return launch_relaxed<6, T, STAGED>(b, grid, p, wc, lanes, lds, relaxed_nt, s);
+    return launch_relaxed<6, T, GLOBAL>(b, grid, p, wc, lanes, 0, relaxed_nt, s);
   case Q8: hipLaunchKernelGGL((gemv_plain<8, T>), grid, block, 0, s, b); break;
   case Q6: hipLaunchKernelGGL((gemv_plain<6, T>), grid, block, 0, s, b); break;
   case T2R:
@@ -1059,25 +1072,42 @@ hipError_t launch_t(Kind kind, const GemvBatch &b, dim3 grid, const JobPieces &p
 constexpr size_t kGemvStageMax = 80 * 1024;
 
 namespace {
+// the fraction of the last round's block slots a launch of `blocks` fills (rounds of one block a compute unit)
+double round_fill(int64_t blocks) {
+  const int64_t cus = cu_count();
+  return blocks <= 0 ? 1.0 : (double)blocks / (double)(((blocks + cus - 1) / cus) * cus);
+}
+// the blocks of `rpb` rows the jobs take
+int64_t blocks_of(const Job *jobs, int32_t njobs, int rpb) {
+  int64_t n = 0;
+  for (int j = 0; j < njobs; j++) n += (jobs[j].r1 - jobs[j].r0 + rpb - 1) / rpb;
+  return n;
+}
 // A ternary / binary launch's waves a block (one token: 4 to 6; more: 4): the count whose blocks come closest to
 // whole rounds of one block a compute unit (the last round's empty slots the fewest, the fewer waves on a tie).
 // Measured on the 27B shapes, A/B on one box: the down projection's 5120 rows in 5-wave blocks (512 blocks, two
 // rounds) 2.76 -> 2.99 TB/s against 4 waves (640: three rounds, the last a quarter full), gate+up's 2 x 17408 in
 // 6-wave blocks (726, three rounds) 4.0 -> 4.18.
 int ternary_waves(const Job *jobs, int32_t njobs, int lanes) {
-  const int64_t cus = cu_count();
   int best = 4;
   double best_fill = 0.0;
   if (jobs[0].count != 1) return 4;
   for (int w = 4; w <= kTernMaxWaves; w++) {
-    const int rpb = 64 * w / lanes;
-    int64_t blocks = 0;
-    for (int j = 0; j < njobs; j++) blocks += (jobs[j].r1 - jobs[j].r0 + rpb - 1) / rpb;
-    if (blocks == 0) return 4;
-    const double fill = (double)blocks / (double)(((blocks + cus - 1) / cus) * cus);
+    const double fill = round_fill(blocks_of(jobs, njobs, 64 * w / lanes));
     if (fill > best_fill + 1e-9) best = w, best_fill = fill;
   }
   return best;
+}
+
+// A relaxed launch's threads a block: relaxed_threads', or for one token blocks of one wave where those come closer
+// to whole rounds (LFM2-350M's o and down projections, 1024 rows of 16 lanes: 128 blocks of 8 rows fill half the
+// compute units, 256 of 4 all of them).  Measured A/B on one box: config 1's step 1.58 -> 1.65 TB/s, the 27B int6
+// down projection 4.53 -> 4.63; the 8B shapes' launches fill whole rounds either way and keep 128 threads.
+int relaxed_block_threads(const Job *jobs, int32_t njobs, int T, bool staged, int lanes) {
+  const int big = relaxed_threads(T, staged);
+  if (T != 1) return big;
+  const double small = round_fill(blocks_of(jobs, njobs, kOneTokenSmall / lanes));
+  return small > round_fill(blocks_of(jobs, njobs, big / lanes)) + 0.02 ? kOneTokenSmall : big;
 }
 
 hipError_t launch_batch(Kind kind, const Job *jobs, int32_t njobs, hipStream_t s) {
@@ -1092,8 +1122,9 @@ hipError_t launch_batch(Kind kind, const Job *jobs, int32_t njobs, hipStream_t s
   // staged in LDS for 2..4 tokens (each row's lanes read every token's activations: measured 4 % faster at M = 4)
   const int src = T > 1 && lds <= kGemvStageMax ? STAGED : GLOBAL;
   const int tern_threads = signs_kind(kind) ? 64 * ternary_waves(jobs, njobs, ternary_lanes(nmax)) : 0;
+  const int relaxed_nt = relaxed ? relaxed_block_threads(jobs, njobs, T, src == STAGED, lanes) : 0;
   const int rpb = signs_kind(kind) ? tern_threads / ternary_lanes(nmax)
-                  : relaxed          ? relaxed_threads(T, src == STAGED) / lanes
+                  : relaxed          ? relaxed_nt / lanes
                                      : kRowsPerBlock;
   for (int j = 0; j < njobs; j++) {
     b.job[j] = jobs[j];
@@ -1136,10 +1167,10 @@ hipError_t launch_batch(Kind kind, const Job *jobs, int32_t njobs, hipStream_t s
   }
   const bool wc = jobs[0].wc != nullptr;
   switch (T) {
-  case 1: return launch_t<1>(kind, b, grid, pc, wc, src, lanes, lds, tern_threads, s);
-  case 2: return launch_t<2>(kind, b, grid, pc, wc, src, lanes, lds, tern_threads, s);
-  case 3: return launch_t<3>(kind, b, grid, pc, wc, src, lanes, lds, tern_threads, s);
-  case 4: return launch_t<4>(kind, b, grid, pc, wc, src, lanes, lds, tern_threads, s);
+  case 1: return launch_t<1>(kind, b, grid, pc, wc, src, lanes, lds, tern_threads, relaxed_nt, s);
+  case 2: return launch_t<2>(kind, b, grid, pc, wc, src, lanes, lds, tern_threads, relaxed_nt, s);
+  case 3: return launch_t<3>(kind, b, grid, pc, wc, src, lanes, lds, tern_threads, relaxed_nt, s);
+  case 4: return launch_t<4>(kind, b, grid, pc, wc, src, lanes, lds, tern_threads, relaxed_nt, s);
   default: return hipErrorInvalidValue;
   }
 }
