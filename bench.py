@@ -371,8 +371,13 @@ def measure_configs(torch, pkg, args, extras):
         out[label] = {"GBps": round(total / sec / 1e9, 1), "us_per_launch": round(1e6 * sec / len(tables), 2),
                       "launches": len(tables), "bytes": total}
 
-    def prefill(label, kind, shapes, count, tol=False):
+    def prefill(label, kind, shapes, count, tol=False, caller_wc=True):
+        """caller_wc (int8): the reference's own call, the corrections int8_sums made (tensors.ts:126-132); else
+        derived in the tile.  tol: hq_matmul_q8r_tile_tol_ex, whose launches of fewer tiles than two blocks a compute
+        unit take the bit-exact tile with derived corrections (hq_tol_min_tiles' default): which did is reported"""
         ops, calls, keep = 0.0, [], []
+        cus = torch.cuda.get_device_properties(0).multi_processor_count
+        tol_tiles = [((r + 127) // 128) * ((count + 127) // 128) for r, _ in shapes]
         if tol:  # the tolerance form's workspace, one for the calls, which follow each other on the stream
             need = max(lib.hq_tol_work_bytes(n, count) for _, n in shapes)
             work = torch.empty(need + 256, dtype=torch.uint8, device=dev)
@@ -393,10 +398,12 @@ def measure_configs(torch, pkg, args, extras):
                 wc = torch.empty(rows, n // 32, dtype=torch.int32, device=dev)
                 pkg.check(lib.hq_int8_sums_ex(wc.data_ptr(), w.data_ptr(), rows * n // 32, None))
                 keep.append(wc)
+                if not caller_wc:
+                    wc = None
                 calls.append(lambda h, w=w, ws=ws, wc=wc, buf=buf, frame=frame, o=o, rows=rows, n=n:
                              lib.hq_matmul_q8r_tile_ex(o.data_ptr(), buf.data_ptr(), buf.data_ptr() + n, w.data_ptr(),
-                                                       ws.data_ptr(), wc.data_ptr(), n, 0, rows, count, 4 * rows,
-                                                       frame, h))
+                                                       ws.data_ptr(), wc.data_ptr() if wc is not None else None, n, 0,
+                                                       rows, count, 4 * rows, frame, h))
             elif kind == "ternary":
                 calls.append(lambda h, w=w, ws=ws, buf=buf, frame=frame, o=o, rows=rows, n=n:
                              lib.hq_matmul_t2r_tile_ex(o.data_ptr(), buf.data_ptr(), buf.data_ptr() + n, w.data_ptr(),
@@ -419,13 +426,17 @@ def measure_configs(torch, pkg, args, extras):
         pkg.check(lib.hq_last_error())
         out[label] = {"TOPS": round(ops / sec / 1e12, 1), "frac": round(ops / sec / 1e12 / INT8_PEAK_TOPS, 4),
                       "ms": round(1e3 * sec, 3)}
+        if tol:
+            out[label]["launches_on_the_tolerance_tile"] = sum(t >= 2 * cus for t in tol_tiles)
+            out[label]["launches"] = len(shapes)
 
     decode("c0 stories15M q8r M=1 (weights in cache: 221 KB x 64)", "int8", [[(768, 288)]], 64)
     decode("c1 LFM2-350M q8r M=1, 16 layers + lm-head", "int8",
            [[(1536, 1024)], [(1024, 1024)], [(9216, 1024)], [(1024, 4608)]] * 16 + [[(65536, 1024)]], 1)
     c2 = [(3072, 2048), (2048, 2048), (8192, 2048), (8192, 2048), (2048, 8192)]
-    prefill("c2 Llama-3.2-1B prefill M=512, one layer", "int8", c2, 512)
-    prefill("c2 Llama-3.2-1B prefill M=512, one layer, tolerance form", "int8", c2, 512, tol=True)
+    prefill("c2 Llama-3.2-1B prefill M=512, one layer (the caller's wc)", "int8", c2, 512)
+    prefill("c2 Llama-3.2-1B prefill M=512, one layer (corrections derived)", "int8", c2, 512, caller_wc=False)
+    prefill("c2 Llama-3.2-1B prefill M=512, one layer, tolerance entry point", "int8", c2, 512, tol=True)
     for kind in ("ternary", "int6", "binary") if extras else ("ternary", "int6"):
         copies = {"ternary": 8, "int6": 3, "binary": 12}[kind]
         tag = "c4 27B" if kind != "binary" else "27B shapes"
