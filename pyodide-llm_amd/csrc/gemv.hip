@@ -86,9 +86,10 @@ constexpr int kOneTokenSmall = 64;
 // Lanes a relaxed row: 32 lanes give a launch twice the waves, each lane half the steps.  Measured phase by phase
 // streaming from HBM (configs 1-4's decode shapes, int8 and int6, 16 against 32 lanes): one int8 token, 32 lanes are
 // faster where a row is 4096 or 8192 bytes (8B q/k/v 7.7 -> 7.1 us, o 6.2 -> 5.8, gate+up 25.3 -> 23.5, lm-head 97 ->
-// 94; 1B down 6.8 -> 6.3) and slower at 1024, 2048, 5120 and 14336 (LFM2's lm-head 18.1 -> 25.7, 8B down 14.0 ->
-// 14.6); int6 shows no consistent gain (16 lanes); 2..4 tokens gain on rows past 8192 (four tokens' 8B down 19.8 ->
-// 18.8 us, int6 30.4 -> 20.7) and lose below (gate+up 29.6 -> 31.9).
+// 94; 1B down 6.8 -> 6.3) and slower at 1024, 2048 and 5120 (LFM2's lm-head 18.1 -> 25.7), and at 14336 in chunks of
+// four steps (8B down 14.0 -> 14.6; in chunks of two, below, faster); int6 shows no consistent gain (16 lanes); 2..4
+// tokens gain on rows past 8192 (four tokens' 8B down 19.8 -> 18.8 us, int6 30.4 -> 20.7) and lose below (gate+up
+// 29.6 -> 31.9).
 constexpr int kRelaxedLongRow = 8192;
 // One token of int8 past 8192 takes 32 lanes where a row is an even number of 32-lane steps, not a multiple of four
 // (10240, 14336, ...), in chunks of 2 steps: none past the row's end (8B down 12.73 -> 12.55 us; with chunks of 4,
