@@ -299,8 +299,8 @@ def _graph_time(torch, launch, reps):
 
 
 def measure_configs(torch, pkg, args, extras):
-    """The other configs' products on one GPU (BASELINE.json configs[0..2, 4]; with `extras` also config 4's shapes
-    with binary weights, the packing the reference ranks next, llama.cpp's blocks and the classifier's outlier
+    """The other configs' products on one GPU (BASELINE.json configs[0..2, 4], and config 4's shapes with binary
+    weights, the packing the reference ranks next; with `extras` also llama.cpp's blocks and the classifier's outlier
     channels): GB/s of algorithmic bytes for the token products (M = 1; copies of the weights past the Infinity Cache
     where the shapes allow), TOPS for the prompts.  Products only (the activations prepared once), graphs of their
     launches timed with HIP events."""
@@ -437,7 +437,7 @@ def measure_configs(torch, pkg, args, extras):
     prefill("c2 Llama-3.2-1B prefill M=512, one layer (the caller's wc)", "int8", c2, 512)
     prefill("c2 Llama-3.2-1B prefill M=512, one layer (corrections derived)", "int8", c2, 512, caller_wc=False)
     prefill("c2 Llama-3.2-1B prefill M=512, one layer, tolerance entry point", "int8", c2, 512, tol=True)
-    for kind in ("ternary", "int6", "binary") if extras else ("ternary", "int6"):
+    for kind in ("ternary", "int6", "binary"):
         copies = {"ternary": 8, "int6": 3, "binary": 12}[kind]
         tag = "c4 27B" if kind != "binary" else "27B shapes"
         decode(f"{tag} {kind} M=1, gate+up x {copies}", kind, [[(17408, 5120), (17408, 5120)]], copies)
@@ -915,8 +915,7 @@ def main():
                     help="the headline's phases: quantize_x then hq_phase (the reference's ready() + phase()), or "
                          "hq_matmuls (the same in one call, the reference's matmulsAlike)")
     ap.add_argument("--configs", action="store_true",
-                    help="also measure binary weights at config 4's shapes, llama.cpp's blocks and the outlier "
-                         "channels")
+                    help="also measure llama.cpp's blocks (all ten types) and the outlier channels")
     ap.add_argument("--profile", choices=("gemm", "gemm_wc", "gemm_tol", "gemv", "gemv_m4", "blocks_decode",
                                           "blocks_prompt"),
                     help="only run one workload's launches, for rocprofv3's counters")
