@@ -675,6 +675,32 @@ def test_binary_token(k, arena, oracle, groups, name):
             assert same_bits(got, want), f"{name} groups {groups} token {t} rows {r0}..{r1}: {first_difference(got, want)}"
 
 
+@pytest.mark.parametrize("rows", [2560, 3072])
+@pytest.mark.parametrize("packing", ["ternary", "binary"])
+def test_signs_block_waves(k, arena, oracle, rows, packing):
+    """One token's launches whose blocks of 4 waves would end in a part-empty round take 5 waves (2560 rows of 32
+    lanes: 256 blocks of 10 rows) or 6 (3072: 256 of 12): every row the oracle's, rows cut at both ends"""
+    rng = np.random.default_rng(rows + len(packing))
+    n = 8192
+    q, s = oracle.quantize_x(rng.standard_normal(n).astype(F), 0)
+    xq_b, area = oracle.interleave(q.view(np.int8), s)
+    halves = np.repeat((np.abs(rng.standard_normal(rows)) * 0.02 + 1e-3).astype(np.float16), n // 128).view(np.uint16)
+    if packing == "ternary":
+        wbytes = pack_ternary(rng.integers(0, 3, rows * n).astype(np.uint8))
+        full, name, last = oracle.matmul_t2r(xq_b, area, wbytes, halves, n), "matmul_t2r", 3
+    else:
+        wbytes = pack_binary(rng.integers(0, 2, rows * n).astype(np.uint8), n)
+        full, name, last = oracle.matmul_b1r(xq_b, area, wbytes, halves, n), "matmul_b1r", 2
+    wq, wsa, xq, xs = arena.put(wbytes), arena.put(halves), arena.put(xq_b), arena.put(area)
+    for r0, r1 in [(0, rows), (3, rows - 5)]:
+        out = arena.alloc(4 * (rows + 1), fill=np.full(rows + 1, -7, F))
+        getattr(k, name)(out, xq, xs, wq, wsa, n, r0, r1, last)
+        got = arena.get(out, F, rows + 1)
+        want = np.full(rows + 1, F(-7), F)
+        want[r0:r1] = full[r0:r1]
+        assert same_bits(got, want), f"{packing} rows {r0}..{r1}: {first_difference(got, want)}"
+
+
 @pytest.mark.parametrize("count,groups", [(c, g) for c in [1, 2, 3, 4, 5, 7, 8, 9, 16, 17, 64, 65, 100]
                                           for g in [1, 3, 9]] + [(4, 136), (3, 136), (2, 40), (33, 136)])
 def test_b1r_tile(k, arena, oracle, count, groups):
