@@ -135,6 +135,10 @@ HQ_DEV uint4 ldw16_nt(const char *p) {
   const u4v q = __builtin_nontemporal_load((const u4v *)p);
   return make_uint4(q.x, q.y, q.z, q.w);
 }
+// streamed (non-temporal) unless CACHED: a launch's weights small enough to stay in the caches from one step to the
+// next are read through them (relaxed_cached)
+template <bool CACHED> HQ_DEV uint4 ldw16_as(const char *p) { return CACHED ? ldw16(p) : ldw16_nt(p); }
+template <bool CACHED, typename V> HQ_DEV V ld_as(const V *p) { return CACHED ? *p : __builtin_nontemporal_load(p); }
 
 // the 32 weight bytes of group g of a row, as eight dwords of int8 (int6 groups widened, kernels/six.ts)
 template <int PACK>
@@ -182,7 +186,7 @@ struct ActSource {
   HQ_DEV float scale(int t, int g) const { return SRC == GLOBAL ? ((const float *)xs[t])[g] : ls[t * ng + g]; }
 };
 
-template <int PACK, int T, bool WC, int SRC, int RL, int U1>
+template <int PACK, int T, bool WC, int SRC, int RL, int U1, bool CACHED>
 struct RelaxedChunk {
   static constexpr bool LATE = T > 1 && SRC == STAGED;
   static constexpr int U = T == 1 ? U1 : (LATE || T == 2 ? 2 : 1);  // U1: 4, or 2 (relaxed_pairs_of_steps)
@@ -209,7 +213,7 @@ struct RelaxedChunk {
       const int g0 = (it0 + u) * RL + (lane >> 1), g1 = g0 + RL / 2;
       const uint32_t h = 16u * (uint32_t)(lane & 1);
       const uint32_t c0 = (uint32_t)(g0 < ng4 ? g0 : 0), c1 = (uint32_t)(g1 < ng4 ? g1 : 0);
-      const uint4 a = ldw16_nt(wb + (rb + c0 * 32u + h)), b = ldw16_nt(wb + (rb + c1 * 32u + h));
+      const uint4 a = ldw16_as<CACHED>(wb + (rb + c0 * 32u + h)), b = ldw16_as<CACHED>(wb + (rb + c1 * 32u + h));
       w[u][0] = a.x; w[u][1] = a.y; w[u][2] = a.z; w[u][3] = a.w;
       w[u][4] = b.x; w[u][5] = b.y; w[u][6] = b.z; w[u][7] = b.w;
       const uint4 xa = ld16(A.xq[0] + (c0 * 32u + h)), xb = ld16(A.xq[0] + (c1 * 32u + h));
@@ -217,9 +221,9 @@ struct RelaxedChunk {
       x[u][0][4] = xb.x; x[u][0][5] = xb.y; x[u][0][6] = xb.z; x[u][0][7] = xb.w;
       // the row's scales and corrections, like its weights, streamed once (a row's 32 lanes read one whole line)
       const uint32_t own = (lane & 1) ? c1 : c0;
-      ws[u] = __builtin_nontemporal_load((const float *)((const char *)sb + (gb + own * 4u)));
+      ws[u] = ld_as<CACHED>((const float *)((const char *)sb + (gb + own * 4u)));
       xs[u][0] = *(const float *)(A.xs[0] + own * 4u);
-      if (WC) wc[u] = __builtin_nontemporal_load((const int32_t *)((const char *)cb + (gb + own * 4u)));
+      if (WC) wc[u] = ld_as<CACHED>((const int32_t *)((const char *)cb + (gb + own * 4u)));
     }
   }
   // PAIRED: the chunk's terms folded into the chains: chain k of the reference (groups 4 j + k) lives in lane 2 k, and
@@ -358,7 +362,7 @@ struct RelaxedChunk {
 
 // the relaxed_threads / RL rows of tile `blk` of job `jb` (its row range cut into tiles in order).  STAGED: first
 // make the block's LDS copy of the activations, while the first weights are in flight
-template <int PACK, int T, bool WC, int SRC, int RL, int U1, int NT>
+template <int PACK, int T, bool WC, int SRC, int RL, int U1, int NT, bool CACHED>
 HQ_DEV void relaxed_tile(const Job &J, int blk, char *lds) {
   const int lane = threadIdx.x & (RL - 1);
   constexpr int rows = NT / RL;
@@ -390,7 +394,7 @@ HQ_DEV void relaxed_tile(const Job &J, int blk, char *lds) {
   float acc[T];
 #pragma unroll
   for (int t = 0; t < T; t++) acc[t] = 0.0f;
-  using Chunk = RelaxedChunk<PACK, T, WC, SRC, RL, U1>;
+  using Chunk = RelaxedChunk<PACK, T, WC, SRC, RL, U1, CACHED>;
   constexpr int U = Chunk::U;
   const int steps = (ng4 + RL - 1) / RL;
   Chunk a, b;
@@ -488,7 +492,7 @@ HQ_DEV void relaxed_tile(const Job &J, int blk, char *lds) {
 // other jobs' pieces read theirs.  PRE 2: every piece is the first job's (no other path in the kernel: measured
 // 0.05 us a launch shorter than PRE 1).  The activations and their scales are `frame` bytes a token apart (the tile
 // kinds' one stride).
-template <int PACK, int T, bool WC, int SRC, int RL, bool BY, int PRE, int U1, int NT>
+template <int PACK, int T, bool WC, int SRC, int RL, bool BY, int PRE, int U1, int NT, bool CACHED>
 __global__ __launch_bounds__(NT) void gemv_relaxed(
     const char *xq, const char *xs, const char *wq, const char *ws, int32_t n, int32_t r0, int32_t r1, int32_t pr,
     int32_t frame, char *out, int64_t os, const char *wc, GemvBatch batch) {
@@ -497,13 +501,13 @@ __global__ __launch_bounds__(NT) void gemv_relaxed(
     const int a = r0 + (int)blockIdx.y * pr;
     if (PRE == 2 || a < r1) {
       const Job J{out, xq, xs, wq, ws, wc, n, a, min(a + pr, r1), T, os, frame, frame, 0};
-      relaxed_tile<PACK, T, WC, SRC, RL, U1, NT>(J, (int)blockIdx.x, lds);
+      relaxed_tile<PACK, T, WC, SRC, RL, U1, NT, CACHED>(J, (int)blockIdx.x, lds);
       return;
     }
   }
   int jb, blk;
   block_job<BY>(batch, jb, blk);
-  relaxed_tile<PACK, T, WC, SRC, RL, U1, NT>(batch.job[jb], blk, lds);
+  relaxed_tile<PACK, T, WC, SRC, RL, U1, NT, CACHED>(batch.job[jb], blk, lds);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -933,56 +937,70 @@ HQ_HOST_DEV constexpr int ternary_lanes(int n) {
 HQ_HOST_DEV constexpr size_t ternary_stage_bytes(int T, int n) { return (size_t)T * ternary_token_bytes(n); }
 
 // lead_r1, pr: the end of the rows of the job whose pieces come first (b.job[0] is its first piece), and the rows a
-// piece (the arguments PRE reads)
-template <int PACK, int T, int SRC, bool BY, int PRE, int U1, int NT>
+// piece (the arguments PRE reads).  CACHED kernels exist for 16-lane rows only (relaxed_cached's launches).
+template <int PACK, int T, int SRC, bool BY, int PRE, int U1, int NT, bool CACHED>
 void launch_relaxed_by(const GemvBatch &b, dim3 grid, int32_t lead_r1, int32_t pr, bool wc, int lanes, size_t lds,
                        hipStream_t s) {
   const dim3 block(NT);
   const Job &J = b.job[0];
   const int32_t frame = (int32_t)J.frame;  // (PRE: J.frame == J.sframe, below 2^31)
-  if (lanes == 32) {
-    if (wc) hipLaunchKernelGGL((gemv_relaxed<PACK, T, true, SRC, 32, BY, PRE, U1, NT>), grid, block, lds, s, J.xq, J.xs, J.wq,
-                               J.ws, J.n, J.r0, lead_r1, pr, frame, J.out, J.os, J.wc, b);
-    else hipLaunchKernelGGL((gemv_relaxed<PACK, T, false, SRC, 32, BY, PRE, U1, NT>), grid, block, lds, s, J.xq, J.xs, J.wq,
-                            J.ws, J.n, J.r0, lead_r1, pr, frame, J.out, J.os, J.wc, b);
-  } else {
-    if (wc) hipLaunchKernelGGL((gemv_relaxed<PACK, T, true, SRC, 16, BY, PRE, U1, NT>), grid, block, lds, s, J.xq, J.xs, J.wq,
-                               J.ws, J.n, J.r0, lead_r1, pr, frame, J.out, J.os, J.wc, b);
-    else hipLaunchKernelGGL((gemv_relaxed<PACK, T, false, SRC, 16, BY, PRE, U1, NT>), grid, block, lds, s, J.xq, J.xs, J.wq,
-                            J.ws, J.n, J.r0, lead_r1, pr, frame, J.out, J.os, J.wc, b);
+  if constexpr (!CACHED) {
+    if (lanes == 32) {
+      if (wc) hipLaunchKernelGGL((gemv_relaxed<PACK, T, true, SRC, 32, BY, PRE, U1, NT, false>), grid, block, lds, s, J.xq,
+                                 J.xs, J.wq, J.ws, J.n, J.r0, lead_r1, pr, frame, J.out, J.os, J.wc, b);
+      else hipLaunchKernelGGL((gemv_relaxed<PACK, T, false, SRC, 32, BY, PRE, U1, NT, false>), grid, block, lds, s, J.xq,
+                              J.xs, J.wq, J.ws, J.n, J.r0, lead_r1, pr, frame, J.out, J.os, J.wc, b);
+      return;
+    }
   }
+  if (wc) hipLaunchKernelGGL((gemv_relaxed<PACK, T, true, SRC, 16, BY, PRE, U1, NT, CACHED>), grid, block, lds, s, J.xq,
+                             J.xs, J.wq, J.ws, J.n, J.r0, lead_r1, pr, frame, J.out, J.os, J.wc, b);
+  else hipLaunchKernelGGL((gemv_relaxed<PACK, T, false, SRC, 16, BY, PRE, U1, NT, CACHED>), grid, block, lds, s, J.xq,
+                          J.xs, J.wq, J.ws, J.n, J.r0, lead_r1, pr, frame, J.out, J.os, J.wc, b);
 }
-template <int PACK, int T, int SRC, int NT>
+template <int PACK, int T, int SRC, int NT, bool CACHED>
 hipError_t launch_relaxed_nt(const GemvBatch &b, dim3 grid, const JobPieces &p, bool wc, int lanes, size_t lds,
                              hipStream_t s) {
   // PRE takes one stride for a token's activations and scales (the tile kinds' frame; one token: none read)
   const Job &J = b.job[0];
   const bool pre = p.by && (T == 1 || (J.frame == J.sframe && J.frame >= 0 && J.frame <= INT32_MAX));
-  if (T == 1 && lanes == 32 && relaxed_pairs_of_steps(PACK == 8 ? Q8R : Q6R, T, J.n)) {
-    // (T == 1 ? 2 : 4: the kernels of 2..4 tokens are never made with U1 = 2)
-    if (pre && p.lead_pieces == b.njobs)
-      launch_relaxed_by<PACK, T, SRC, true, 2, T == 1 ? 2 : 4, NT>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
-    else if (pre)
-      launch_relaxed_by<PACK, T, SRC, true, 1, T == 1 ? 2 : 4, NT>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
-    else if (p.by) launch_relaxed_by<PACK, T, SRC, true, 0, T == 1 ? 2 : 4, NT>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
-    else launch_relaxed_by<PACK, T, SRC, false, 0, T == 1 ? 2 : 4, NT>(b, grid, 0, 0, wc, lanes, lds, s);
-  } else if (pre && p.lead_pieces == b.njobs)
-    launch_relaxed_by<PACK, T, SRC, true, 2, 4, NT>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
+  if constexpr (!CACHED) {
+    if (T == 1 && lanes == 32 && relaxed_pairs_of_steps(PACK == 8 ? Q8R : Q6R, T, J.n)) {
+      // (T == 1 ? 2 : 4: the kernels of 2..4 tokens are never made with U1 = 2)
+      constexpr int U1 = T == 1 ? 2 : 4;
+      if (pre && p.lead_pieces == b.njobs)
+        launch_relaxed_by<PACK, T, SRC, true, 2, U1, NT, false>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
+      else if (pre)
+        launch_relaxed_by<PACK, T, SRC, true, 1, U1, NT, false>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
+      else if (p.by) launch_relaxed_by<PACK, T, SRC, true, 0, U1, NT, false>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
+      else launch_relaxed_by<PACK, T, SRC, false, 0, U1, NT, false>(b, grid, 0, 0, wc, lanes, lds, s);
+      return hipGetLastError();
+    }
+  }
+  if (pre && p.lead_pieces == b.njobs)
+    launch_relaxed_by<PACK, T, SRC, true, 2, 4, NT, CACHED>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
   else if (pre)
-    launch_relaxed_by<PACK, T, SRC, true, 1, 4, NT>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
-  else if (p.by) launch_relaxed_by<PACK, T, SRC, true, 0, 4, NT>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
-  else launch_relaxed_by<PACK, T, SRC, false, 0, 4, NT>(b, grid, 0, 0, wc, lanes, lds, s);
+    launch_relaxed_by<PACK, T, SRC, true, 1, 4, NT, CACHED>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
+  else if (p.by) launch_relaxed_by<PACK, T, SRC, true, 0, 4, NT, CACHED>(b, grid, p.lead_r1, p.rows, wc, lanes, lds, s);
+  else launch_relaxed_by<PACK, T, SRC, false, 0, 4, NT, CACHED>(b, grid, 0, 0, wc, lanes, lds, s);
   return hipGetLastError();
 }
-// nt: the block's threads, relaxed_threads' or (one token) kOneTokenSmall
+// nt: the block's threads, relaxed_threads' or (one token) kOneTokenSmall; cached: relaxed_cached's choice (one token
+// of int8 on 16-lane rows only: the other forms read their weights one way)
 template <int PACK, int T, int SRC>
 hipError_t launch_relaxed(const GemvBatch &b, dim3 grid, const JobPieces &p, bool wc, int lanes, size_t lds, int nt,
-                          hipStream_t s) {
+                          bool cached, hipStream_t s) {
   constexpr int big = relaxed_threads(T, SRC == STAGED);
+  if constexpr (T == 1 && SRC == GLOBAL && PACK == 8) {  // (RelaxedChunk's PAIRED form)
+    if (cached && lanes == 16) {
+      if (nt == kOneTokenSmall) return launch_relaxed_nt<PACK, T, SRC, kOneTokenSmall, true>(b, grid, p, wc, lanes, lds, s);
+      return launch_relaxed_nt<PACK, T, SRC, big, true>(b, grid, p, wc, lanes, lds, s);
+    }
+  }
   // (T == 1 ? kOneTokenSmall : big: the kernels of 2..4 tokens are never made with the small blocks)
   if (T == 1 && nt == kOneTokenSmall)
-    return launch_relaxed_nt<PACK, T, SRC, T == 1 ? kOneTokenSmall : big>(b, grid, p, wc, lanes, lds, s);
-  return launch_relaxed_nt<PACK, T, SRC, big>(b, grid, p, wc, lanes, lds, s);
+    return launch_relaxed_nt<PACK, T, SRC, T == 1 ? kOneTokenSmall : big, false>(b, grid, p, wc, lanes, lds, s);
+  return launch_relaxed_nt<PACK, T, SRC, big, false>(b, grid, p, wc, lanes, lds, s);
 }
 
 // ternary / binary: rows of ternary_lanes(n) lanes, the activations staged in LDS when they fit
@@ -1041,17 +1059,17 @@ hipError_t launch_signs(const GemvBatch &b, dim3 grid, int threads, const JobPie
 // grid: (blocks) with the jobs found through block0, or (blocks a piece, pieces) when p.by
 template <int T>
 hipError_t launch_t(Kind kind, const GemvBatch &b, dim3 grid, const JobPieces &p, bool wc, int src, int lanes,
-                    size_t lds, int tern_threads, int relaxed_nt, hipStream_t s) {
+                    size_t lds, int tern_threads, int relaxed_nt, bool cached, hipStream_t s) {
   const dim3 block(256);
   switch (kind) {
   case Q8R:
   case Q6R:
     if (kind == Q8R) {
-      if (src == STAGED) return launch_relaxed<8, T, STAGED>(b, grid, p, wc, lanes, lds, relaxed_nt, s);
-      return launch_relaxed<8, T, GLOBAL>(b, grid, p, wc, lanes, 0, relaxed_nt, s);
+      if (src == STAGED) return launch_relaxed<8, T, STAGED>(b, grid, p, wc, lanes, lds, relaxed_nt, cached, s);
+      return launch_relaxed<8, T, GLOBAL>(b, grid, p, wc, lanes, 0, relaxed_nt, cached, s);
     }
-    if (src == STAGED) return launch_relaxed<6, T, STAGED>(b, grid, p, wc, lanes, lds, relaxed_nt, s);
-    return launch_relaxed<6, T, GLOBAL>(b, grid, p, wc, lanes, 0, relaxed_nt, s);
+    if (src == STAGED) return launch_relaxed<6, T, STAGED>(b, grid, p, wc, lanes, lds, relaxed_nt, cached, s);
+    return launch_relaxed<6, T, GLOBAL>(b, grid, p, wc, lanes, 0, relaxed_nt, cached, s);
   case Q8: hipLaunchKernelGGL((gemv_plain<8, T>), grid, block, 0, s, b); break;
   case Q6: hipLaunchKernelGGL((gemv_plain<6, T>), grid, block, 0, s, b); break;
   case T2R:
@@ -1111,6 +1129,18 @@ int relaxed_block_threads(const Job *jobs, int32_t njobs, int T, bool staged, in
   return small > round_fill(blocks_of(jobs, njobs, big / lanes)) + 0.02 ? kOneTokenSmall : big;
 }
 
+// One token's int8 weights are streamed past the caches (non-temporal loads: on the 8B decode step 1.83 -> 1.77 ms)
+// unless the launch's weights come to less than kCachedWeights bytes: a small model's matrices can stay in the caches
+// from one step to the next, which streaming them throws away.  Measured A/B on one box: stories15M's 768 x 288
+// (config 0, 221 KB a launch) 2.43 us a launch streamed against 2.13 cached; LFM2-350M's phases (config 1, 1 MiB and
+// more) 3.53 streamed against 3.64.
+constexpr int64_t kCachedWeights = 1 << 20;
+bool relaxed_cached(Kind kind, const Job *jobs, int32_t njobs) {
+  int64_t bytes = 0;
+  for (int j = 0; j < njobs; j++) bytes += (int64_t)(jobs[j].r1 - jobs[j].r0) * jobs[j].n;
+  return kind == Q8R && jobs[0].count == 1 && bytes < kCachedWeights;
+}
+
 hipError_t launch_batch(Kind kind, const Job *jobs, int32_t njobs, hipStream_t s) {
   if (njobs < 1 || njobs > kMaxJobs) return hipErrorInvalidValue;
   GemvBatch b{};
@@ -1124,6 +1154,7 @@ hipError_t launch_batch(Kind kind, const Job *jobs, int32_t njobs, hipStream_t s
   const int src = T > 1 && lds <= kGemvStageMax ? STAGED : GLOBAL;
   const int tern_threads = signs_kind(kind) ? 64 * ternary_waves(jobs, njobs, ternary_lanes(nmax)) : 0;
   const int relaxed_nt = relaxed ? relaxed_block_threads(jobs, njobs, T, src == STAGED, lanes) : 0;
+  const bool cached = relaxed_cached(kind, jobs, njobs);
   const int rpb = signs_kind(kind) ? tern_threads / ternary_lanes(nmax)
                   : relaxed          ? relaxed_nt / lanes
                                      : kRowsPerBlock;
@@ -1168,10 +1199,10 @@ hipError_t launch_batch(Kind kind, const Job *jobs, int32_t njobs, hipStream_t s
   }
   const bool wc = jobs[0].wc != nullptr;
   switch (T) {
-  case 1: return launch_t<1>(kind, b, grid, pc, wc, src, lanes, lds, tern_threads, relaxed_nt, s);
-  case 2: return launch_t<2>(kind, b, grid, pc, wc, src, lanes, lds, tern_threads, relaxed_nt, s);
-  case 3: return launch_t<3>(kind, b, grid, pc, wc, src, lanes, lds, tern_threads, relaxed_nt, s);
-  case 4: return launch_t<4>(kind, b, grid, pc, wc, src, lanes, lds, tern_threads, relaxed_nt, s);
+  case 1: return launch_t<1>(kind, b, grid, pc, wc, src, lanes, lds, tern_threads, relaxed_nt, cached, s);
+  case 2: return launch_t<2>(kind, b, grid, pc, wc, src, lanes, lds, tern_threads, relaxed_nt, cached, s);
+  case 3: return launch_t<3>(kind, b, grid, pc, wc, src, lanes, lds, tern_threads, relaxed_nt, cached, s);
+  case 4: return launch_t<4>(kind, b, grid, pc, wc, src, lanes, lds, tern_threads, relaxed_nt, cached, s);
   default: return hipErrorInvalidValue;
   }
 }

@@ -368,6 +368,37 @@ def test_relaxed_wide_rows(pkg, k, arena, oracle, count, ng, packing):
                                                 f"wc {form}: {first_difference(got[t], want)}"
 
 
+@pytest.mark.parametrize("rows", [1023, 1024])
+def test_relaxed_cached_and_streamed(pkg, k, arena, oracle, rows):
+    """One int8 token on 16-lane rows reads a launch's weights through the caches below 1 MiB and streams them past
+    the caches from 1 MiB on: 1023 and 1024 rows of 1024 values, one job, then two jobs whose rows add up to the
+    same (the rule counts a launch's bytes), the corrections given and derived, every row against the oracle"""
+    from pyodide_llm_amd import jobs
+    rng = np.random.default_rng(5 + rows)
+    n, ng = 1024, 32
+    frame = ((n + 4 * ng + 15) // 16) * 16
+    w = rng.integers(-128, 128, rows * n).astype(np.int8)
+    sums = oracle.int8_sums(w)
+    ws = (rng.random(rows * ng) * 1e-3).astype(F)
+    q = tile_inputs(oracle, rng, n, 1, frame, rows)
+    want = oracle.matmul_q8r(q[0, :n], q[0, n:n + 4 * ng].view(F), w, ws, sums, n)
+    wq, wsa, xq = arena.put(w, align=256), arena.put(ws), arena.put(q)
+    for form in ("sums", "derived"):
+        wca = arena.put(sums) if form == "sums" else 0
+        out = arena.alloc(4 * rows, fill=np.full(rows, -7, F))
+        k.matmul_q8r(out, xq, xq + n, wq, wsa, wca, n, 0, rows)
+        got = arena.get(out, F, rows)
+        assert same_bits(got, want), f"{rows} rows wc {form}: {first_difference(got, want)}"
+        out = arena.alloc(4 * rows, fill=np.full(rows, -7, F))
+        cut = 300  # the second job: rows cut.. of the same matrix
+        table = [jobs.job("matmul_q8r", out, xq, xq + n, wq, wsa, wca, n, rows=cut),
+                 jobs.job("matmul_q8r", out + 4 * cut, xq, xq + n, wq + cut * n, wsa + 4 * cut * ng,
+                          wca + 4 * cut * ng if wca else 0, n, rows=rows - cut)]
+        assert jobs.phase(pkg.library(), table) == 0, pkg.library().hq_last_error_message()
+        got = arena.get(out, F, rows)
+        assert same_bits(got, want), f"{rows} rows in two jobs wc {form}: {first_difference(got, want)}"
+
+
 def test_relaxed_bytes_past_seven_bits(k, arena):
     """Activation bytes 128..255 lie outside the reference's domain (its relaxed dot is machine-dependent there):
     libhq takes every byte as a signed int8, so the token kernel and the prompt tile still agree to the bit."""
