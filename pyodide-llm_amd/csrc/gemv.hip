@@ -191,11 +191,11 @@ struct RelaxedChunk {
   static constexpr bool LATE = T > 1 && SRC == STAGED;
   static constexpr int U = T == 1 ? U1 : (LATE || T == 2 ? 2 : 1);  // U1: 4, or 2 (relaxed_pairs_of_steps)
   static constexpr int UX = LATE ? 1 : U;  // steps of activations a chunk holds (none read when LATE)
-  // One token of int8 (PAIRED): a step's weights are read as whole cache lines by non-temporal loads.  Lane j of a
-  // row takes the 16 bytes at 16 j of the step's first half (group j / 2's half j % 2) and at RL 16 + 16 j of its
-  // second (group RL / 2 + j / 2's), so that each load instruction reads a row's RL 16 contiguous bytes; a group's
-  // integer is its two halves' (lanes 2 i and 2 i + 1) added by a DPP swap.  Half-lines read by two loads would be
-  // fetched twice past the caches.
+  // One token of int8 (PAIRED): a step's weights are read as whole cache lines by non-temporal loads (ordinary
+  // loads when CACHED).  Lane j of a row takes the 16 bytes at 16 j of the step's first half (group j / 2's half
+  // j % 2) and at RL 16 + 16 j of its second (group RL / 2 + j / 2's), so that each load instruction reads a row's
+  // RL 16 contiguous bytes; a group's integer is its two halves' (lanes 2 i and 2 i + 1) added by a DPP swap.
+  // Half-lines read by two loads would be fetched twice past the caches.
   static constexpr bool PAIRED = T == 1 && SRC == GLOBAL && PACK == 8;
   uint32_t w[U][8];   // PAIRED: w[u][0..3] the first half's 16 bytes, [4..7] the second's
   uint32_t x[UX][T][8];
@@ -219,7 +219,8 @@ struct RelaxedChunk {
       const uint4 xa = ld16(A.xq[0] + (c0 * 32u + h)), xb = ld16(A.xq[0] + (c1 * 32u + h));
       x[u][0][0] = xa.x; x[u][0][1] = xa.y; x[u][0][2] = xa.z; x[u][0][3] = xa.w;
       x[u][0][4] = xb.x; x[u][0][5] = xb.y; x[u][0][6] = xb.z; x[u][0][7] = xb.w;
-      // the row's scales and corrections, like its weights, streamed once (a row's 32 lanes read one whole line)
+      // the row's scales and corrections, like its weights, streamed once (a row's 32 lanes read one whole line;
+      // through the caches when CACHED)
       const uint32_t own = (lane & 1) ? c1 : c0;
       ws[u] = ld_as<CACHED>((const float *)((const char *)sb + (gb + own * 4u)));
       xs[u][0] = *(const float *)(A.xs[0] + own * 4u);
