@@ -368,11 +368,13 @@ def test_relaxed_wide_rows(pkg, k, arena, oracle, count, ng, packing):
                                                 f"wc {form}: {first_difference(got[t], want)}"
 
 
+@pytest.mark.parametrize("cut", [300, 512])
 @pytest.mark.parametrize("rows", [1023, 1024])
-def test_relaxed_cached_and_streamed(pkg, k, arena, oracle, rows):
+def test_relaxed_cached_and_streamed(pkg, k, arena, oracle, rows, cut):
     """One int8 token on 16-lane rows reads a launch's weights through the caches below 1 MiB and streams them past
     the caches from 1 MiB on: 1023 and 1024 rows of 1024 values, one job, then two jobs whose rows add up to the
-    same (the rule counts a launch's bytes), the corrections given and derived, every row against the oracle"""
+    same (the rule counts a launch's bytes; cut at 300 the jobs' blocks are found by search, at 512 they are a grid
+    row each), the corrections given and derived, every row against the oracle"""
     from pyodide_llm_amd import jobs
     rng = np.random.default_rng(5 + rows)
     n, ng = 1024, 32
@@ -390,7 +392,7 @@ def test_relaxed_cached_and_streamed(pkg, k, arena, oracle, rows):
         got = arena.get(out, F, rows)
         assert same_bits(got, want), f"{rows} rows wc {form}: {first_difference(got, want)}"
         out = arena.alloc(4 * rows, fill=np.full(rows, -7, F))
-        cut = 300  # the second job: rows cut.. of the same matrix
+        # the second job: rows cut.. of the same matrix
         table = [jobs.job("matmul_q8r", out, xq, xq + n, wq, wsa, wca, n, rows=cut),
                  jobs.job("matmul_q8r", out + 4 * cut, xq, xq + n, wq + cut * n, wsa + 4 * cut * ng,
                           wca + 4 * cut * ng if wca else 0, n, rows=rows - cut)]
